@@ -1,0 +1,50 @@
+"""Build the gfx950 HIP library in-tree: funasrnet_amd/libfunasr_hip.so.
+
+hipcc cross-compiles for gfx950 without a GPU. Flags: no FMA contraction
+(-ffp-contract=off) because the kernels restate the reference's float order,
+fp32 denormals kept, and packed-fp32 instruction selection disabled.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
+LIBRARY = os.path.join(HERE, "libfunasr_hip.so")
+SOURCES = ["fah_kernels.hip", "fah_api.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+         "-fno-gpu-flush-denormals-to-zero", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-Wall", "-Wno-unused-function"]
+
+
+def _compile(source: str) -> str:
+    obj = os.path.join(OBJ, os.path.splitext(source)[0] + ".o")
+    cmd = [HIPCC, *FLAGS, "-c", os.path.join(SRC, source), "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {source}:\n{r.stderr}")
+    return obj
+
+
+def build() -> str:
+    """Compile every source and link the shared library (always rebuilds)."""
+    os.makedirs(OBJ, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+        objects = list(pool.map(_compile, SOURCES))
+    tmp = LIBRARY + ".tmp"
+    r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objects, "-o", tmp],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    print(build())
+    sys.exit(0)

@@ -1,0 +1,928 @@
+// C ABI (include/funasr_hip.h) over the gfx950 kernels.
+//
+// Ownership follows the reference's seam: host pointers are used only during
+// a call; weights are copied to the device once and immutable afterwards; a
+// context owns one stream and serialises its calls with a mutex.
+#include "../../include/funasr_hip.h"
+#include "fah_internal.h"
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& message) {
+  g_error = message;
+  return code;
+}
+
+struct DeviceError {
+  std::string what;
+};
+
+void check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw DeviceError{std::string(what) + ": " + hipGetErrorString(e)};
+}
+
+struct ArgumentError {
+  std::string what;
+};
+
+void require(bool ok, const std::string& what) {
+  if (!ok) throw ArgumentError{what};
+}
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    return f();
+  } catch (const ArgumentError& e) {
+    return fail(FAH_ERROR_ARGUMENT, e.what);
+  } catch (const DeviceError& e) {
+    return fail(FAH_ERROR_DEVICE, e.what);
+  } catch (const std::bad_alloc&) {
+    return fail(FAH_ERROR_DEVICE, "host allocation failed");
+  }
+}
+
+// Device allocation owned by one object; freed on destruction.
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  DeviceBuffer() = default;
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  DeviceBuffer(DeviceBuffer&& o) noexcept : ptr(o.ptr), bytes(o.bytes) {
+    o.ptr = nullptr;
+    o.bytes = 0;
+  }
+  DeviceBuffer& operator=(DeviceBuffer&& o) noexcept {
+    if (this != &o) {
+      release();
+      ptr = o.ptr;
+      bytes = o.bytes;
+      o.ptr = nullptr;
+      o.bytes = 0;
+    }
+    return *this;
+  }
+  ~DeviceBuffer() { release(); }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+  void allocate(size_t n) {
+    release();
+    if (n == 0) n = 16;
+    check(hipMalloc(&ptr, n), "hipMalloc");
+    bytes = n;
+  }
+  void ensure(size_t n) {
+    if (n > bytes) allocate(n);
+  }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(ptr);
+  }
+};
+
+uint16_t float_to_half_bits(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  uint32_t a = x & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  if (a >= 0x38800000u) return (uint16_t)(sign | ((a + 0xfffu + ((a >> 13) & 1u) - 0x38000000u) >> 13));
+  uint32_t e = a >> 23;
+  if (e < 102) return sign;
+  uint32_t m = (a & 0x7fffffu) | 0x800000u, shift = 126u - e;
+  uint32_t r = m >> shift, rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+  if (rem > half || (rem == half && (r & 1u))) r++;
+  return (uint16_t)(sign | r);
+}
+
+float half_bits_to_float(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu, u;
+  if (e == 0) {
+    float mag = (float)m * (1.0f / 16777216.0f);
+    std::memcpy(&u, &mag, 4);
+    u |= sign;
+  } else if (e == 31) {
+    u = m == 0 ? (sign | 0x7f800000u) : (sign | 0x7fc00000u | (m << 13));
+  } else {
+    u = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// True when every scale survives fp32 -> fp16 -> fp32 bit for bit.
+bool scales_fit_half(const float* s, size_t n) {
+  for (size_t i = 0; i < n; ++i) {
+    float back = half_bits_to_float(float_to_half_bits(s[i]));
+    if (std::memcmp(&back, &s[i], 4) != 0) return false;
+  }
+  return true;
+}
+
+// Rows per workgroup for a Q8 GEMV: at most 4 (row, block) pairs per lane,
+// then shrink until the grid has >= 512 workgroups (floor `min_rows`).
+int pick_group_rows(int rows, int K, int min_rows, bool even) {
+  int B = K / 32;
+  int group = 64;
+  while (group > 1 && group * B > 1024) group /= 2;
+  while (group > min_rows && rows / group < 512) group /= 2;
+  if (even && group < 2) group = 2;
+  return group;
+}
+
+}  // namespace
+
+struct fah_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex gate;
+  bool disposed = false;
+  int64_t minimum_operations = 250000;
+  DeviceBuffer in, out, q, s;
+  std::string name;
+};
+
+struct fah_weight {
+  fah_context* context = nullptr;
+  int rows = 0, cols = 0;
+  bool half_scales = true;
+  DeviceBuffer q, s;
+  int group_rows = 1;
+};
+
+struct DeviceMatrix {
+  DeviceBuffer q, s;
+  int rows = 0, cols = 0, group_rows = 1;
+};
+
+struct fah_decoder {
+  fah_context* context = nullptr;
+  fah_decoder_config cfg{};
+  bool half_scales = true;
+  int q_width = 0, kv_width = 0;
+  std::vector<DeviceMatrix> qkv, wo, gateup, down;
+  std::vector<DeviceBuffer> attn_norm, q_norm, k_norm, ffn_norm;
+  DeviceMatrix embed, lm_head;  // lm_head aliases embed when tied
+  bool tied = true;
+  DeviceBuffer output_norm, rope_cos, rope_sin, kcache, vcache;
+  DeviceBuffer x, qkv_out, qh, scores, attn, a, h, logits, keys, token, position, history, history_count, staging;
+  int lm_groups = 0;
+  int host_position = 0;
+  bool have_logits = false;
+  hipGraphExec_t graph_row = nullptr, graph_logits = nullptr, graph_step = nullptr;
+  int64_t weight_bytes = 0;
+};
+
+namespace {
+
+void upload(DeviceBuffer& dst, const void* src, size_t bytes, hipStream_t s) {
+  dst.allocate(bytes);
+  check(hipMemcpyAsync(dst.ptr, src, bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync H2D");
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+// Upload rows in the given order (row_index[i] = source row of storage row i).
+void upload_matrix(DeviceMatrix& m, const std::vector<const fah_q8_host*>& parts,
+                   const std::vector<std::pair<int, int>>& order, int cols, bool half, hipStream_t s) {
+  int B = cols / 32;
+  size_t rows = order.size();
+  std::vector<int8_t> q(rows * cols);
+  std::vector<uint16_t> hs;
+  std::vector<float> fs;
+  if (half) hs.resize(rows * B); else fs.resize(rows * B);
+  for (size_t i = 0; i < rows; ++i) {
+    const fah_q8_host* p = parts[order[i].first];
+    int r = order[i].second;
+    std::memcpy(&q[i * cols], p->quantized + (size_t)r * cols, cols);
+    for (int b = 0; b < B; ++b) {
+      float v = p->scales[(size_t)r * B + b];
+      if (half) hs[i * B + b] = float_to_half_bits(v); else fs[i * B + b] = v;
+    }
+  }
+  upload(m.q, q.data(), q.size(), s);
+  if (half) upload(m.s, hs.data(), hs.size() * 2, s); else upload(m.s, fs.data(), fs.size() * 4, s);
+  m.rows = (int)rows;
+  m.cols = cols;
+}
+
+void validate_q8(const fah_q8_host* w, int rows, int cols, const char* name) {
+  require(w && w->quantized && w->scales, std::string(name) + ": missing Q8 weight");
+  require(w->rows == rows && w->cols == cols,
+          std::string(name) + ": shape " + std::to_string(w->rows) + "x" + std::to_string(w->cols) + " != " +
+              std::to_string(rows) + "x" + std::to_string(cols));
+}
+
+int64_t matrix_bytes(const DeviceMatrix& m) { return (int64_t)m.q.bytes + (int64_t)m.s.bytes; }
+
+fah::GemvArgs gemv_args(const DeviceMatrix& m) {
+  fah::GemvArgs a{};
+  a.w = m.q.as<int8_t>();
+  a.ws = m.s.ptr;
+  a.rows = m.rows;
+  a.K = m.cols;
+  a.group_rows = m.group_rows;
+  return a;
+}
+
+// One decoder row through every layer (x -> x), then optionally the final
+// norm, lm_head and greedy. Records onto the context stream (captured).
+void enqueue_layers(fah_decoder* d, hipStream_t s) {
+  const fah_decoder_config& c = d->cfg;
+  int* pos = d->position.as<int>();
+  for (int l = 0; l < c.layers; ++l) {
+    fah::GemvArgs g = gemv_args(d->qkv[l]);
+    g.x = d->x.as<float>();
+    g.norm_w = d->attn_norm[l].as<float>();
+    g.eps = c.eps;
+    g.out = d->qkv_out.as<float>();
+    g.out_rows = d->qkv[l].rows;
+    check(fah::launch_gemv(g, d->half_scales, fah::kInputNorm, fah::kOutPlain, 1, s), "qkv gemv");
+
+    size_t kv_layer = (size_t)c.kv_heads * c.capacity * c.head_size;
+    fah::QkArgs qa{};
+    qa.qkv = d->qkv_out.as<float>();
+    qa.q_norm = d->q_norm[l].as<float>();
+    qa.k_norm = d->k_norm[l].as<float>();
+    qa.rope_cos = d->rope_cos.as<float>();
+    qa.rope_sin = d->rope_sin.as<float>();
+    qa.position = pos;
+    qa.q_out = d->qh.as<float>();
+    qa.kcache = d->kcache.as<_Float16>() + kv_layer * l;
+    qa.vcache = d->vcache.as<_Float16>() + kv_layer * l;
+    qa.heads = c.heads;
+    qa.kv_heads = c.kv_heads;
+    qa.head_size = c.head_size;
+    qa.q_width = d->q_width;
+    qa.kv_width = d->kv_width;
+    qa.capacity = c.capacity;
+    qa.eps = c.eps;
+    check(fah::launch_qk_prepare(qa, s), "qk prepare");
+
+    fah::AttnArgs at{};
+    at.q = d->qh.as<float>();
+    at.kcache = qa.kcache;
+    at.vcache = qa.vcache;
+    at.position = pos;
+    at.scores = d->scores.as<float>();
+    at.out = d->attn.as<float>();
+    at.heads = c.heads;
+    at.kv_heads = c.kv_heads;
+    at.head_size = c.head_size;
+    at.capacity = c.capacity;
+    at.divisor = std::sqrt((float)c.head_size);
+    check(fah::launch_attention(at, 16, s), "attention");
+
+    fah::GemvArgs o = gemv_args(d->wo[l]);
+    o.x = d->attn.as<float>();
+    o.out = d->a.as<float>();
+    o.out_rows = c.width;
+    o.resid = d->x.as<float>();
+    check(fah::launch_gemv(o, d->half_scales, fah::kInputFloat, fah::kOutResidual, 1, s), "o gemv");
+
+    fah::GemvArgs gu = gemv_args(d->gateup[l]);
+    gu.x = d->a.as<float>();
+    gu.norm_w = d->ffn_norm[l].as<float>();
+    gu.eps = c.eps;
+    gu.out = d->h.as<float>();
+    gu.out_rows = c.ffn;
+    check(fah::launch_gemv(gu, d->half_scales, fah::kInputNorm, fah::kOutSwiGLU, 1, s), "gate/up gemv");
+
+    fah::GemvArgs dn = gemv_args(d->down[l]);
+    dn.x = d->h.as<float>();
+    dn.out = d->x.as<float>();
+    dn.out_rows = c.width;
+    dn.resid = d->a.as<float>();
+    check(fah::launch_gemv(dn, d->half_scales, fah::kInputFloat, fah::kOutResidual, 1, s), "down gemv");
+  }
+}
+
+const DeviceMatrix& head_matrix(const fah_decoder* d) { return d->tied ? d->embed : d->lm_head; }
+
+void enqueue_head(fah_decoder* d, hipStream_t s) {
+  fah::GemvArgs g = gemv_args(head_matrix(d));
+  g.x = d->x.as<float>();
+  g.norm_w = d->output_norm.as<float>();
+  g.eps = d->cfg.eps;
+  g.out = d->logits.as<float>();
+  g.out_rows = d->cfg.vocab;
+  g.partial_keys = d->keys.as<unsigned long long>();
+  check(fah::launch_gemv(g, d->half_scales, fah::kInputNorm, fah::kOutGreedy, 1, s), "lm_head gemv");
+  check(fah::launch_greedy_reduce(d->keys.as<unsigned long long>(), d->lm_groups, d->logits.as<float>(),
+                                  d->token.as<int>(), s),
+        "greedy");
+}
+
+hipGraphExec_t capture(fah_decoder* d, int kind) {
+  hipStream_t s = d->context->stream;
+  hipGraph_t graph = nullptr;
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  try {
+    if (kind == 2)
+      check(fah::launch_embed(d->embed.q.as<int8_t>(), d->embed.s.ptr, d->half_scales, d->cfg.width, d->cfg.vocab,
+                              d->token.as<int>(), d->x.as<float>(), d->history.as<int>(),
+                              d->history_count.as<int>(), s),
+            "embed");
+    enqueue_layers(d, s);
+    if (kind >= 1) enqueue_head(d, s);
+    check(fah::launch_advance(d->position.as<int>(), 1, s), "advance");
+  } catch (...) {
+    hipGraph_t dead = nullptr;
+    (void)hipStreamEndCapture(s, &dead);
+    if (dead) (void)hipGraphDestroy(dead);
+    throw;
+  }
+  check(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  check(e, "hipGraphInstantiate");
+  return exec;
+}
+
+hipGraphExec_t graph_for(fah_decoder* d, int kind) {
+  hipGraphExec_t* slot = kind == 0 ? &d->graph_row : kind == 1 ? &d->graph_logits : &d->graph_step;
+  if (!*slot) *slot = capture(d, kind);
+  return *slot;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fah_abi_version(void) { return FAH_ABI_VERSION; }
+
+const char* fah_last_error(void) { return g_error.c_str(); }
+
+int fah_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+int fah_context_create(int device, fah_context** out) {
+  if (!out) return fail(FAH_ERROR_ARGUMENT, "out is NULL");
+  return guarded([&] {
+    int n = fah_device_count();
+    require(device >= 0 && device < n, "no HIP device " + std::to_string(device));
+    check(hipSetDevice(device), "hipSetDevice");
+    auto* c = new fah_context();
+    c->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete c;
+      check(e, "hipStreamCreate");
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->name = std::string("HIP ") + prop.gcnArchName;
+    else c->name = "HIP";
+    *out = c;
+    return FAH_OK;
+  });
+}
+
+int fah_context_destroy(fah_context* c) {
+  if (!c) return FAH_OK;
+  {
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->stream) {
+      (void)hipSetDevice(c->device);
+      (void)hipStreamSynchronize(c->stream);
+      (void)hipStreamDestroy(c->stream);
+    }
+    c->disposed = true;
+  }
+  delete c;
+  return FAH_OK;
+}
+
+int fah_context_synchronize(fah_context* c) {
+  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  return guarded([&] {
+    std::lock_guard<std::mutex> lock(c->gate);
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return FAH_OK;
+  });
+}
+
+const char* fah_context_name(const fah_context* c) { return c ? c->name.c_str() : ""; }
+
+int fah_context_set_minimum_operations(fah_context* c, int64_t operations) {
+  if (!c || operations < 0) return fail(FAH_ERROR_ARGUMENT, "invalid minimum operations");
+  c->minimum_operations = operations;
+  return FAH_OK;
+}
+
+void* fah_context_stream(fah_context* c) { return c ? (void*)c->stream : nullptr; }
+
+int fah_weight_q8_upload(fah_context* c, const int8_t* quantized, const float* scales, int rows, int cols,
+                         fah_weight** out) {
+  if (!c || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+  return guarded([&] {
+    require(quantized && scales, "Q8 weight needs quantized bytes and scales");
+    require(rows > 0 && cols > 0 && cols % 32 == 0, "Invalid row-major Q8 dimensions");
+    std::lock_guard<std::mutex> lock(c->gate);
+    check(hipSetDevice(c->device), "hipSetDevice");
+    auto* w = new fah_weight();
+    try {
+      w->context = c;
+      w->rows = rows;
+      w->cols = cols;
+      size_t nb = (size_t)rows * (cols / 32);
+      w->half_scales = scales_fit_half(scales, nb);
+      upload(w->q, quantized, (size_t)rows * cols, c->stream);
+      if (w->half_scales) {
+        std::vector<uint16_t> h(nb);
+        for (size_t i = 0; i < nb; ++i) h[i] = float_to_half_bits(scales[i]);
+        upload(w->s, h.data(), nb * 2, c->stream);
+      } else {
+        upload(w->s, scales, nb * 4, c->stream);
+      }
+      w->group_rows = pick_group_rows(rows, cols, 4, false);
+    } catch (...) {
+      delete w;
+      throw;
+    }
+    *out = w;
+    return FAH_OK;
+  });
+}
+
+int fah_weight_release(fah_weight* w) {
+  if (!w) return FAH_OK;
+  (void)hipSetDevice(w->context->device);
+  delete w;
+  return FAH_OK;
+}
+
+int64_t fah_weight_device_bytes(const fah_weight* w) { return w ? (int64_t)(w->q.bytes + w->s.bytes) : 0; }
+
+static fah::GemvArgs weight_args(const fah_weight* w) {
+  fah::GemvArgs a{};
+  a.w = w->q.as<int8_t>();
+  a.ws = w->s.ptr;
+  a.rows = w->rows;
+  a.K = w->cols;
+  a.group_rows = w->group_rows;
+  return a;
+}
+
+int fah_quantized_linear(fah_context* c, const float* input, int frames, const fah_weight* w, const float* bias,
+                         float* output) {
+  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  if (!w || frames <= 0 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
+  if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return FAH_DECLINED;
+  return guarded([&] {
+    require(input && output, "Q8 GPU projection needs input and output");
+    require(w->context == c, "weight belongs to another context");
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    size_t in_bytes = (size_t)frames * w->cols * 4, out_bytes = (size_t)frames * w->rows * 4;
+    c->in.ensure(in_bytes + (bias ? (size_t)w->rows * 4 : 0));
+    c->out.ensure(out_bytes);
+    check(hipMemcpyAsync(c->in.ptr, input, in_bytes, hipMemcpyHostToDevice, c->stream), "H2D input");
+    float* dbias = nullptr;
+    if (bias) {
+      dbias = reinterpret_cast<float*>(c->in.as<char>() + in_bytes);
+      check(hipMemcpyAsync(dbias, bias, (size_t)w->rows * 4, hipMemcpyHostToDevice, c->stream), "H2D bias");
+    }
+    fah::GemvArgs a = weight_args(w);
+    a.x = c->in.as<float>();
+    a.out = c->out.as<float>();
+    a.out_rows = w->rows;
+    a.bias = dbias;
+    check(fah::launch_gemv(a, w->half_scales, fah::kInputFloat, fah::kOutPlain, frames, c->stream), "gemv");
+    check(hipMemcpyAsync(output, c->out.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return FAH_OK;
+  });
+}
+
+int fah_linear_many(fah_context* c, const float* input, int frames, const fah_weight* const* weights, int count,
+                    float* const* outputs) {
+  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  if (count == 0) return FAH_OK;
+  if (!weights || count < 0 || frames <= 0) return FAH_DECLINED;
+  int cols = weights[0] ? weights[0]->cols : 0;
+  int64_t total_rows = 0;
+  for (int i = 0; i < count; ++i) {
+    if (!weights[i] || weights[i]->cols > fah::gemv_max_k()) return FAH_DECLINED;
+    total_rows += weights[i]->rows;
+  }
+  if ((int64_t)frames * cols * total_rows < c->minimum_operations) return FAH_DECLINED;
+  return guarded([&] {
+    require(input && outputs, "grouped projection needs input and outputs");
+    for (int i = 0; i < count; ++i) {
+      require(weights[i]->cols == cols, "Grouped projection dimensions differ");
+      require(weights[i]->context == c, "weight belongs to another context");
+      require(outputs[i] != nullptr, "grouped projection output is NULL");
+    }
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    size_t n = (size_t)frames * cols;
+    c->in.ensure(n * 4);
+    c->q.ensure(n);
+    c->s.ensure(n / 32 * 4);
+    size_t out_total = 0;
+    for (int i = 0; i < count; ++i) out_total += (size_t)frames * weights[i]->rows;
+    c->out.ensure(out_total * 4);
+    check(hipMemcpyAsync(c->in.ptr, input, n * 4, hipMemcpyHostToDevice, c->stream), "H2D input");
+    check(fah::launch_quantize(c->in.as<float>(), (int64_t)n, c->q.as<int8_t>(), c->s.as<float>(), c->stream),
+          "quantize");
+    size_t at = 0;
+    for (int i = 0; i < count; ++i) {
+      fah::GemvArgs a = weight_args(weights[i]);
+      a.xq = c->q.as<int8_t>();
+      a.xs = c->s.as<float>();
+      a.out = c->out.as<float>() + at;
+      a.out_rows = weights[i]->rows;
+      check(fah::launch_gemv(a, weights[i]->half_scales, fah::kInputQuantized, fah::kOutPlain, frames, c->stream),
+            "gemv");
+      at += (size_t)frames * weights[i]->rows;
+    }
+    at = 0;
+    for (int i = 0; i < count; ++i) {
+      size_t bytes = (size_t)frames * weights[i]->rows * 4;
+      check(hipMemcpyAsync(outputs[i], c->out.as<float>() + at, bytes, hipMemcpyDeviceToHost, c->stream), "D2H");
+      at += (size_t)frames * weights[i]->rows;
+    }
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return FAH_OK;
+  });
+}
+
+int fah_quantize_device(fah_context* c, const float* x, int64_t n, int8_t* q, float* scales) {
+  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  return guarded([&] {
+    require(n >= 0 && n % 32 == 0, "Quantization needs matching complete blocks");
+    require(n == 0 || (x && q && scales), "NULL buffer");
+    std::lock_guard<std::mutex> lock(c->gate);
+    check(hipSetDevice(c->device), "hipSetDevice");
+    check(fah::launch_quantize(x, n, q, scales, c->stream), "quantize");
+    return FAH_OK;
+  });
+}
+
+int fah_q8_gemv_device(fah_context* c, const int8_t* q, const float* scales, int frames, const fah_weight* w,
+                       float* out) {
+  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  if (!w || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
+  return guarded([&] {
+    require(frames > 0 && q && scales && out, "invalid GEMV arguments");
+    std::lock_guard<std::mutex> lock(c->gate);
+    check(hipSetDevice(c->device), "hipSetDevice");
+    fah::GemvArgs a = weight_args(w);
+    a.xq = q;
+    a.xs = scales;
+    a.out = out;
+    a.out_rows = w->rows;
+    check(fah::launch_gemv(a, w->half_scales, fah::kInputQuantized, fah::kOutPlain, frames, c->stream), "gemv");
+    return FAH_OK;
+  });
+}
+
+int fah_q8_block_dots_device(fah_context* c, const int8_t* q, const fah_weight* w, int32_t* dots) {
+  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  return guarded([&] {
+    require(w && q && dots, "invalid block-dot arguments");
+    std::lock_guard<std::mutex> lock(c->gate);
+    check(hipSetDevice(c->device), "hipSetDevice");
+    check(fah::launch_block_dots(q, w->q.as<int8_t>(), w->rows, w->cols, dots, c->stream), "block dots");
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_layer_host* layers,
+                       const fah_q8_host* token_embd, const fah_q8_host* output, const float* output_norm,
+                       fah_decoder** out) {
+  if (!c || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+  return guarded([&] {
+    require(cfg && layers && token_embd && output_norm, "decoder needs config, layers, embeddings and norm");
+    const fah_decoder_config& k = *cfg;
+    require(k.layers > 0 && k.width > 0 && k.heads > 0 && k.kv_heads > 0 && k.vocab > 0 && k.ffn > 0,
+            "invalid decoder dimensions");
+    require(k.heads % k.kv_heads == 0, "Invalid GQA head counts");
+    require(k.head_size == 128, "head_size must be 128");
+    require(k.width % 32 == 0 && k.ffn % 32 == 0, "widths must be multiples of 32");
+    int q_width = k.heads * k.head_size, kv_width = k.kv_heads * k.head_size;
+    int maxk = fah::gemv_max_k();
+    require(k.width <= maxk && k.ffn <= maxk && q_width <= maxk, "projection width exceeds kernel limit");
+    require(k.capacity >= 1 && k.capacity <= 12288, "capacity must be in [1, 12288]");
+    for (int l = 0; l < k.layers; ++l) {
+      const fah_layer_host& L = layers[l];
+      std::string p = "blk." + std::to_string(l) + ".";
+      validate_q8(&L.wq, q_width, k.width, (p + "attn_q").c_str());
+      validate_q8(&L.wk, kv_width, k.width, (p + "attn_k").c_str());
+      validate_q8(&L.wv, kv_width, k.width, (p + "attn_v").c_str());
+      validate_q8(&L.wo, k.width, q_width, (p + "attn_output").c_str());
+      validate_q8(&L.gate, k.ffn, k.width, (p + "ffn_gate").c_str());
+      validate_q8(&L.up, k.ffn, k.width, (p + "ffn_up").c_str());
+      validate_q8(&L.down, k.width, k.ffn, (p + "ffn_down").c_str());
+      require(L.attn_norm && L.q_norm && L.k_norm && L.ffn_norm, p + ": missing norm weights");
+    }
+    validate_q8(token_embd, k.vocab, k.width, "token_embd");
+    if (output) validate_q8(output, k.vocab, k.width, "output");
+
+    std::lock_guard<std::mutex> lock(c->gate);
+    check(hipSetDevice(c->device), "hipSetDevice");
+    auto d = std::make_unique<fah_decoder>();
+    d->context = c;
+    d->cfg = k;
+    d->q_width = q_width;
+    d->kv_width = kv_width;
+    hipStream_t s = c->stream;
+
+    bool half = true;
+    auto fits = [&](const fah_q8_host& w) { return scales_fit_half(w.scales, (size_t)w.rows * (w.cols / 32)); };
+    for (int l = 0; l < k.layers && half; ++l) {
+      const fah_layer_host& L = layers[l];
+      half = fits(L.wq) && fits(L.wk) && fits(L.wv) && fits(L.wo) && fits(L.gate) && fits(L.up) && fits(L.down);
+    }
+    half = half && fits(*token_embd) && (!output || fits(*output));
+    d->half_scales = half;
+
+    d->qkv.resize(k.layers);
+    d->wo.resize(k.layers);
+    d->gateup.resize(k.layers);
+    d->down.resize(k.layers);
+    d->attn_norm.resize(k.layers);
+    d->q_norm.resize(k.layers);
+    d->k_norm.resize(k.layers);
+    d->ffn_norm.resize(k.layers);
+    int qkv_rows = q_width + 2 * kv_width;
+    int qkv_group = pick_group_rows(qkv_rows, k.width, 4, false);
+    int o_group = pick_group_rows(k.width, q_width, 4, false);
+    int gu_group = pick_group_rows(2 * k.ffn, k.width, 4, true);
+    while (gu_group > 2 && (k.ffn % (gu_group / 2) != 0)) gu_group /= 2;
+    int down_group = pick_group_rows(k.width, k.ffn, 4, false);
+    for (int l = 0; l < k.layers; ++l) {
+      const fah_layer_host& L = layers[l];
+      std::vector<std::pair<int, int>> order;
+      for (int r = 0; r < q_width; ++r) order.emplace_back(0, r);
+      for (int r = 0; r < kv_width; ++r) order.emplace_back(1, r);
+      for (int r = 0; r < kv_width; ++r) order.emplace_back(2, r);
+      upload_matrix(d->qkv[l], {&L.wq, &L.wk, &L.wv}, order, k.width, half, s);
+      d->qkv[l].group_rows = qkv_group;
+      order.clear();
+      for (int r = 0; r < k.width; ++r) order.emplace_back(0, r);
+      upload_matrix(d->wo[l], {&L.wo}, order, q_width, half, s);
+      d->wo[l].group_rows = o_group;
+      order.clear();
+      int R = gu_group / 2;
+      for (int t = 0; t < k.ffn / R; ++t) {
+        for (int r = 0; r < R; ++r) order.emplace_back(0, t * R + r);
+        for (int r = 0; r < R; ++r) order.emplace_back(1, t * R + r);
+      }
+      upload_matrix(d->gateup[l], {&L.gate, &L.up}, order, k.width, half, s);
+      d->gateup[l].group_rows = gu_group;
+      order.clear();
+      for (int r = 0; r < k.width; ++r) order.emplace_back(0, r);
+      upload_matrix(d->down[l], {&L.down}, order, k.ffn, half, s);
+      d->down[l].group_rows = down_group;
+      upload(d->attn_norm[l], L.attn_norm, (size_t)k.width * 4, s);
+      upload(d->q_norm[l], L.q_norm, (size_t)k.head_size * 4, s);
+      upload(d->k_norm[l], L.k_norm, (size_t)k.head_size * 4, s);
+      upload(d->ffn_norm[l], L.ffn_norm, (size_t)k.width * 4, s);
+      d->weight_bytes += matrix_bytes(d->qkv[l]) + matrix_bytes(d->wo[l]) + matrix_bytes(d->gateup[l]) +
+                         matrix_bytes(d->down[l]);
+    }
+    {
+      std::vector<std::pair<int, int>> order;
+      for (int r = 0; r < k.vocab; ++r) order.emplace_back(0, r);
+      upload_matrix(d->embed, {token_embd}, order, k.width, half, s);
+      d->embed.group_rows = pick_group_rows(k.vocab, k.width, 4, false);
+      d->tied = output == nullptr;
+      if (!d->tied) {
+        upload_matrix(d->lm_head, {output}, order, k.width, half, s);
+        d->lm_head.group_rows = d->embed.group_rows;
+      }
+    }
+    DeviceMatrix& head = d->tied ? d->embed : d->lm_head;
+    d->weight_bytes += matrix_bytes(head);
+    upload(d->output_norm, output_norm, (size_t)k.width * 4, s);
+
+    // RoPE table with the C runtime's powf/cosf/sinf (QwenDecoder.cs:78-95).
+    int half_hs = k.head_size / 2;
+    std::vector<float> freq(half_hs), cs((size_t)k.capacity * half_hs), sn((size_t)k.capacity * half_hs);
+    for (int i = 0; i < half_hs; ++i) freq[i] = powf(k.rope_base, (-2.0f * (float)i) / (float)k.head_size);
+    for (int t = 0; t < k.capacity; ++t)
+      for (int i = 0; i < half_hs; ++i) {
+        float angle = (float)t * freq[i];
+        cs[(size_t)t * half_hs + i] = cosf(angle);
+        sn[(size_t)t * half_hs + i] = sinf(angle);
+      }
+    upload(d->rope_cos, cs.data(), cs.size() * 4, s);
+    upload(d->rope_sin, sn.data(), sn.size() * 4, s);
+
+    size_t kv_elems = (size_t)k.layers * k.kv_heads * k.capacity * k.head_size;
+    d->kcache.allocate(kv_elems * 2);
+    d->vcache.allocate(kv_elems * 2);
+    check(hipMemsetAsync(d->kcache.ptr, 0, kv_elems * 2, s), "memset kv");
+    check(hipMemsetAsync(d->vcache.ptr, 0, kv_elems * 2, s), "memset kv");
+    d->x.allocate((size_t)k.width * 4);
+    d->qkv_out.allocate((size_t)qkv_rows * 4);
+    d->qh.allocate((size_t)q_width * 4);
+    d->scores.allocate((size_t)k.heads * k.capacity * 4);
+    d->attn.allocate((size_t)q_width * 4);
+    d->a.allocate((size_t)k.width * 4);
+    d->h.allocate((size_t)k.ffn * 4);
+    d->logits.allocate((size_t)k.vocab * 4);
+    d->lm_groups = (k.vocab + head.group_rows - 1) / head.group_rows;
+    d->keys.allocate((size_t)d->lm_groups * 8);
+    d->token.allocate(16);
+    d->position.allocate(16);
+    d->history.allocate((size_t)k.capacity * 4 + 16);
+    d->history_count.allocate(16);
+    check(hipMemsetAsync(d->token.ptr, 0, 16, s), "memset");
+    check(hipMemsetAsync(d->position.ptr, 0, 16, s), "memset");
+    check(hipMemsetAsync(d->history_count.ptr, 0, 16, s), "memset");
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    *out = d.release();
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_destroy(fah_decoder* d) {
+  if (!d) return FAH_OK;
+  std::lock_guard<std::mutex> lock(d->context->gate);
+  (void)hipSetDevice(d->context->device);
+  (void)hipStreamSynchronize(d->context->stream);
+  for (hipGraphExec_t g : {d->graph_row, d->graph_logits, d->graph_step})
+    if (g) (void)hipGraphExecDestroy(g);
+  delete d;
+  return FAH_OK;
+}
+
+int fah_decoder_set_position(fah_decoder* d, int position) {
+  if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
+  return guarded([&] {
+    require(position >= 0 && position <= d->cfg.capacity, "position out of range");
+    std::lock_guard<std::mutex> lock(d->context->gate);
+    check(hipSetDevice(d->context->device), "hipSetDevice");
+    check(hipMemcpyAsync(d->position.ptr, &position, 4, hipMemcpyHostToDevice, d->context->stream), "H2D");
+    check(hipStreamSynchronize(d->context->stream), "sync");
+    d->host_position = position;
+    d->have_logits = false;
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_position(const fah_decoder* d, int* position) {
+  if (!d || !position) return fail(FAH_ERROR_ARGUMENT, "decoder/position is NULL");
+  *position = d->host_position;
+  return FAH_OK;
+}
+
+int fah_decoder_decode(fah_decoder* d, const float* embeddings, int frames, float* logits) {
+  if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
+  return guarded([&] {
+    require(embeddings && frames >= 1 && d->host_position + frames <= d->cfg.capacity,
+            "Decoder context exhausted or invalid embeddings");
+    std::lock_guard<std::mutex> lock(d->context->gate);
+    hipStream_t s = d->context->stream;
+    check(hipSetDevice(d->context->device), "hipSetDevice");
+    size_t row = (size_t)d->cfg.width * 4;
+    d->staging.ensure(row * frames);
+    check(hipMemcpyAsync(d->staging.ptr, embeddings, row * frames, hipMemcpyHostToDevice, s), "H2D embeddings");
+    for (int f = 0; f < frames; ++f) {
+      check(hipMemcpyAsync(d->x.ptr, d->staging.as<char>() + row * f, row, hipMemcpyDeviceToDevice, s), "D2D row");
+      bool last = f == frames - 1;
+      check(hipGraphLaunch(graph_for(d, last && logits ? 1 : 0), s), "hipGraphLaunch");
+    }
+    if (logits)
+      check(hipMemcpyAsync(logits, d->logits.ptr, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, s), "D2H");
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    d->host_position += frames;
+    d->have_logits = logits != nullptr;
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_embed(fah_decoder* d, const int32_t* tokens, int count, float* out) {
+  if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
+  return guarded([&] {
+    require(count >= 0 && (count == 0 || (tokens && out)), "invalid embed arguments");
+    for (int i = 0; i < count; ++i) require(tokens[i] >= 0 && tokens[i] < d->cfg.vocab, "token out of range");
+    std::lock_guard<std::mutex> lock(d->context->gate);
+    hipStream_t s = d->context->stream;
+    check(hipSetDevice(d->context->device), "hipSetDevice");
+    d->staging.ensure((size_t)d->cfg.width * 4 + 16);
+    int* tok = reinterpret_cast<int*>(d->staging.as<char>() + (size_t)d->cfg.width * 4);
+    for (int i = 0; i < count; ++i) {
+      check(hipMemcpyAsync(tok, &tokens[i], 4, hipMemcpyHostToDevice, s), "H2D token");
+      check(fah::launch_embed(d->embed.q.as<int8_t>(), d->embed.s.ptr, d->half_scales, d->cfg.width, d->cfg.vocab,
+                              tok, d->staging.as<float>(), nullptr, nullptr, s),
+            "embed");
+      check(hipMemcpyAsync(out + (size_t)i * d->cfg.width, d->staging.ptr, (size_t)d->cfg.width * 4,
+                           hipMemcpyDeviceToHost, s),
+            "D2H");
+      check(hipStreamSynchronize(s), "sync");
+    }
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_greedy(fah_decoder* d, int32_t* token) {
+  if (!d || !token) return fail(FAH_ERROR_ARGUMENT, "decoder/token is NULL");
+  return guarded([&] {
+    if (!d->have_logits) return fail(FAH_ERROR_STATE, "no logits: decode with logits first");
+    std::lock_guard<std::mutex> lock(d->context->gate);
+    check(hipSetDevice(d->context->device), "hipSetDevice");
+    check(hipMemcpyAsync(token, d->token.ptr, 4, hipMemcpyDeviceToHost, d->context->stream), "D2H token");
+    check(hipStreamSynchronize(d->context->stream), "sync");
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_generate(fah_decoder* d, int steps, int32_t* tokens) {
+  if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
+  return guarded([&] {
+    require(steps >= 0 && (steps == 0 || tokens), "invalid generate arguments");
+    if (!d->have_logits) return fail(FAH_ERROR_STATE, "no logits: decode with logits first");
+    require(d->host_position + steps <= d->cfg.capacity, "Decoder context exhausted");
+    std::lock_guard<std::mutex> lock(d->context->gate);
+    hipStream_t s = d->context->stream;
+    check(hipSetDevice(d->context->device), "hipSetDevice");
+    check(hipMemsetAsync(d->history_count.ptr, 0, 4, s), "reset history");
+    hipGraphExec_t g = graph_for(d, 2);
+    for (int i = 0; i < steps; ++i) check(hipGraphLaunch(g, s), "hipGraphLaunch");
+    if (steps > 0)
+      check(hipMemcpyAsync(tokens, d->history.ptr, (size_t)steps * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    d->host_position += steps;
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_kv_write(fah_decoder* d, int layer, const uint16_t* keys, const uint16_t* values, int positions) {
+  if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
+  return guarded([&] {
+    const fah_decoder_config& k = d->cfg;
+    require(layer >= 0 && layer < k.layers && positions >= 0 && positions <= k.capacity && keys && values,
+            "invalid KV write");
+    std::lock_guard<std::mutex> lock(d->context->gate);
+    hipStream_t s = d->context->stream;
+    check(hipSetDevice(d->context->device), "hipSetDevice");
+    size_t layer_elems = (size_t)k.kv_heads * k.capacity * k.head_size;
+    for (int h = 0; h < k.kv_heads; ++h) {
+      // host [t][h][c] -> device [h][t][c]
+      check(hipMemcpy2DAsync(d->kcache.as<uint16_t>() + layer_elems * layer + (size_t)h * k.capacity * k.head_size,
+                             (size_t)k.head_size * 2, keys + (size_t)h * k.head_size, (size_t)d->kv_width * 2,
+                             (size_t)k.head_size * 2, positions, hipMemcpyHostToDevice, s),
+            "H2D keys");
+      check(hipMemcpy2DAsync(d->vcache.as<uint16_t>() + layer_elems * layer + (size_t)h * k.capacity * k.head_size,
+                             (size_t)k.head_size * 2, values + (size_t)h * k.head_size, (size_t)d->kv_width * 2,
+                             (size_t)k.head_size * 2, positions, hipMemcpyHostToDevice, s),
+            "H2D values");
+    }
+    check(hipStreamSynchronize(s), "sync");
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_kv_read(fah_decoder* d, int layer, uint16_t* keys, uint16_t* values, int positions) {
+  if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
+  return guarded([&] {
+    const fah_decoder_config& k = d->cfg;
+    require(layer >= 0 && layer < k.layers && positions >= 0 && positions <= k.capacity && keys && values,
+            "invalid KV read");
+    std::lock_guard<std::mutex> lock(d->context->gate);
+    hipStream_t s = d->context->stream;
+    check(hipSetDevice(d->context->device), "hipSetDevice");
+    size_t layer_elems = (size_t)k.kv_heads * k.capacity * k.head_size;
+    for (int h = 0; h < k.kv_heads; ++h) {
+      check(hipMemcpy2DAsync(keys + (size_t)h * k.head_size, (size_t)d->kv_width * 2,
+                             d->kcache.as<uint16_t>() + layer_elems * layer + (size_t)h * k.capacity * k.head_size,
+                             (size_t)k.head_size * 2, (size_t)k.head_size * 2, positions, hipMemcpyDeviceToHost, s),
+            "D2H keys");
+      check(hipMemcpy2DAsync(values + (size_t)h * k.head_size, (size_t)d->kv_width * 2,
+                             d->vcache.as<uint16_t>() + layer_elems * layer + (size_t)h * k.capacity * k.head_size,
+                             (size_t)k.head_size * 2, (size_t)k.head_size * 2, positions, hipMemcpyDeviceToHost, s),
+            "D2H values");
+    }
+    check(hipStreamSynchronize(s), "sync");
+    return FAH_OK;
+  });
+}
+
+int64_t fah_decoder_weight_bytes(const fah_decoder* d) { return d ? d->weight_bytes : 0; }
+
+}  // extern "C"

@@ -1,0 +1,337 @@
+"""ctypes binding of the C ABI (include/funasr_hip.h) and a Python mirror of
+the reference's backend seam.
+
+``HipBackend`` has the reference's method names and contracts
+(src/FunAsrNet/IQuantizedComputeBackend.cs:4-14,
+IGroupedComputeBackend.cs:4-13): ``try_quantized_linear`` returns False and
+leaves the output untouched when the library declines, raises ValueError on
+shape mismatch (ArgumentException) and RuntimeError on device failure.
+``HipDecoder`` mirrors QwenDecoder's public surface (Decode, Embed, Greedy,
+Reset, RestorePrefix) over the device-resident decoder.
+
+The library must be built (``funasrnet_amd.build.build()``); there is no CPU
+fallback: a missing library or device is an error.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from .model import DecoderWeights, Q8Tensor
+
+LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfunasr_hip.so")
+
+OK, DECLINED = 0, 1
+ERROR_ARGUMENT, ERROR_DEVICE, ERROR_DISPOSED, ERROR_STATE = -1, -2, -3, -4
+
+_vp = ctypes.c_void_p
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i8p = ctypes.POINTER(ctypes.c_int8)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+
+
+class Q8Host(ctypes.Structure):
+    _fields_ = [("quantized", _i8p), ("scales", _f32p), ("rows", ctypes.c_int), ("cols", ctypes.c_int)]
+
+
+class LayerHost(ctypes.Structure):
+    _fields_ = [(n, Q8Host) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down")] + [
+        ("attn_norm", _f32p), ("q_norm", _f32p), ("k_norm", _f32p), ("ffn_norm", _f32p)]
+
+
+class DecoderConfigC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("width", "heads", "kv_heads", "head_size", "layers", "ffn", "vocab")] + [
+        ("eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("capacity", ctypes.c_int)]
+
+
+# Every symbol of include/funasr_hip.h with its signature.
+SIGNATURES = {
+    "fah_abi_version": (ctypes.c_int, []),
+    "fah_last_error": (ctypes.c_char_p, []),
+    "fah_device_count": (ctypes.c_int, []),
+    "fah_context_create": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_vp)]),
+    "fah_context_destroy": (ctypes.c_int, [_vp]),
+    "fah_context_synchronize": (ctypes.c_int, [_vp]),
+    "fah_context_name": (ctypes.c_char_p, [_vp]),
+    "fah_context_set_minimum_operations": (ctypes.c_int, [_vp, ctypes.c_int64]),
+    "fah_context_stream": (_vp, [_vp]),
+    "fah_weight_q8_upload": (ctypes.c_int, [_vp, _i8p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
+    "fah_weight_release": (ctypes.c_int, [_vp]),
+    "fah_weight_device_bytes": (ctypes.c_int64, [_vp]),
+    "fah_quantized_linear": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, _vp, _f32p, _f32p]),
+    "fah_linear_many": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, ctypes.POINTER(_vp), ctypes.c_int,
+                                       ctypes.POINTER(_f32p)]),
+    "fah_quantize_device": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, _vp, _vp]),
+    "fah_q8_gemv_device": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, _vp, _vp]),
+    "fah_q8_block_dots_device": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
+    "fah_decoder_create": (ctypes.c_int, [_vp, ctypes.POINTER(DecoderConfigC), ctypes.POINTER(LayerHost),
+                                          ctypes.POINTER(Q8Host), ctypes.POINTER(Q8Host), _f32p,
+                                          ctypes.POINTER(_vp)]),
+    "fah_decoder_destroy": (ctypes.c_int, [_vp]),
+    "fah_decoder_set_position": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "fah_decoder_position": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int)]),
+    "fah_decoder_decode": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, _f32p]),
+    "fah_decoder_embed": (ctypes.c_int, [_vp, _i32p, ctypes.c_int, _f32p]),
+    "fah_decoder_greedy": (ctypes.c_int, [_vp, _i32p]),
+    "fah_decoder_generate": (ctypes.c_int, [_vp, ctypes.c_int, _i32p]),
+    "fah_decoder_kv_write": (ctypes.c_int, [_vp, ctypes.c_int, _u16p, _u16p, ctypes.c_int]),
+    "fah_decoder_kv_read": (ctypes.c_int, [_vp, ctypes.c_int, _u16p, _u16p, ctypes.c_int]),
+    "fah_decoder_weight_bytes": (ctypes.c_int64, [_vp]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the in-tree HIP library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBRARY):
+            raise RuntimeError(f"{LIBRARY} is missing: build it with funasrnet_amd.build.build()")
+        lib = ctypes.CDLL(LIBRARY)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def _p(a: np.ndarray, ctype):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def _raise(rc: int):
+    msg = load().fah_last_error().decode()
+    if rc == ERROR_ARGUMENT:
+        raise ValueError(msg)
+    if rc == ERROR_DISPOSED:
+        raise RuntimeError("disposed: " + msg)
+    raise RuntimeError(msg)
+
+
+def _check(rc: int) -> int:
+    if rc < 0:
+        _raise(rc)
+    return rc
+
+
+def device_count() -> int:
+    return load().fah_device_count()
+
+
+class HipWeight:
+    """Device copy of a Q8_0 matrix (Weight.Quantized / Weight.Scales)."""
+
+    def __init__(self, backend: "HipBackend", tensor: Q8Tensor):
+        q = np.ascontiguousarray(tensor.quantized, dtype=np.int8)
+        s = np.ascontiguousarray(tensor.scales, dtype=np.float32)
+        self.rows, self.columns = q.shape
+        self._backend = backend
+        h = _vp()
+        _check(load().fah_weight_q8_upload(backend.handle, _p(q, ctypes.c_int8), _p(s, ctypes.c_float), self.rows,
+                                           self.columns, ctypes.byref(h)))
+        self.handle = h
+
+    @property
+    def device_bytes(self) -> int:
+        return load().fah_weight_device_bytes(self.handle)
+
+    def close(self):
+        if self.handle:
+            load().fah_weight_release(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HipBackend:
+    """IQuantizedComputeBackend + IGroupedComputeBackend over one context."""
+
+    def __init__(self, device: int = 0, minimum_operations: int | None = None):
+        h = _vp()
+        _check(load().fah_context_create(device, ctypes.byref(h)))
+        self.handle = h
+        self._weights = {}
+        if minimum_operations is not None:
+            _check(load().fah_context_set_minimum_operations(h, minimum_operations))
+
+    @property
+    def name(self) -> str:
+        return load().fah_context_name(self.handle).decode()
+
+    @property
+    def stream(self) -> int:
+        return load().fah_context_stream(self.handle) or 0
+
+    def synchronize(self):
+        _check(load().fah_context_synchronize(self.handle))
+
+    def weight(self, tensor: Q8Tensor) -> HipWeight:
+        """Device weight cached by tensor identity (the reference keys its
+        cache on the managed array, VulkanFloatBackend.cs:242-283)."""
+        key = id(tensor)
+        if key not in self._weights:
+            self._weights[key] = (tensor, HipWeight(self, tensor))
+        return self._weights[key][1]
+
+    def try_quantized_linear(self, input: np.ndarray, frames: int, weight: Q8Tensor, bias, output: np.ndarray) -> bool:
+        w = self.weight(weight)
+        x = np.ascontiguousarray(input, dtype=np.float32)
+        if x.size != frames * w.columns or output.size != frames * w.rows:
+            raise ValueError("Q8 GPU projection shape mismatch")
+        out = np.empty(frames * w.rows, dtype=np.float32)
+        b = None if bias is None else _p(np.ascontiguousarray(bias, dtype=np.float32), ctypes.c_float)
+        rc = _check(load().fah_quantized_linear(self.handle, _p(x, ctypes.c_float), frames, w.handle, b,
+                                                _p(out, ctypes.c_float)))
+        if rc == DECLINED:
+            return False
+        output.reshape(-1)[:] = out
+        return True
+
+    def try_linear_many(self, input: np.ndarray, frames: int, weights: list):
+        ws = [self.weight(t) for t in weights]
+        x = np.ascontiguousarray(input, dtype=np.float32)
+        outs = [np.empty(frames * w.rows, dtype=np.float32) for w in ws]
+        handles = (_vp * len(ws))(*[w.handle for w in ws])
+        ptrs = (_f32p * len(ws))(*[_p(o, ctypes.c_float) for o in outs])
+        rc = _check(load().fah_linear_many(self.handle, _p(x, ctypes.c_float), frames, handles, len(ws), ptrs))
+        return None if rc == DECLINED else outs
+
+    # device-pointer entry points (pointers are integers, e.g. torch data_ptr())
+    def quantize_device(self, x_ptr: int, n: int, q_ptr: int, s_ptr: int):
+        _check(load().fah_quantize_device(self.handle, x_ptr, n, q_ptr, s_ptr))
+
+    def gemv_device(self, q_ptr: int, s_ptr: int, frames: int, weight: HipWeight, out_ptr: int) -> int:
+        return _check(load().fah_q8_gemv_device(self.handle, q_ptr, s_ptr, frames, weight.handle, out_ptr))
+
+    def block_dots_device(self, q_ptr: int, weight: HipWeight, dots_ptr: int):
+        _check(load().fah_q8_block_dots_device(self.handle, q_ptr, weight.handle, dots_ptr))
+
+    def close(self):
+        for _, w in self._weights.values():
+            w.close()
+        self._weights.clear()
+        if self.handle:
+            load().fah_context_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HipDecoder:
+    """QwenDecoder (src/FunAsrNet/QwenDecoder.cs) on the device."""
+
+    def __init__(self, backend: HipBackend, weights: DecoderWeights, capacity: int = 2048):
+        c = weights.config
+        keep = []
+
+        def q8(t: Q8Tensor) -> Q8Host:
+            q = np.ascontiguousarray(t.quantized, dtype=np.int8)
+            s = np.ascontiguousarray(t.scales, dtype=np.float32)
+            keep.extend([q, s])
+            return Q8Host(_p(q, ctypes.c_int8), _p(s, ctypes.c_float), t.rows, t.columns)
+
+        def f32(a):
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            keep.append(a)
+            return _p(a, ctypes.c_float)
+
+        layers = (LayerHost * c.layers)()
+        for i, L in enumerate(weights.layers):
+            layers[i] = LayerHost(q8(L.wq), q8(L.wk), q8(L.wv), q8(L.wo), q8(L.gate), q8(L.up), q8(L.down),
+                                  f32(L.attn_norm), f32(L.q_norm), f32(L.k_norm), f32(L.ffn_norm))
+        cfg = DecoderConfigC(c.width, c.heads, c.kv_heads, c.head_size, c.layers, c.ffn, c.vocab, c.eps, c.rope_base,
+                             capacity)
+        embd = q8(weights.token_embd)
+        output = q8(weights.output) if weights.output is not None else None
+        h = _vp()
+        _check(load().fah_decoder_create(backend.handle, ctypes.byref(cfg), layers, ctypes.byref(embd),
+                                         ctypes.byref(output) if output is not None else None,
+                                         f32(weights.output_norm), ctypes.byref(h)))
+        self.handle = h
+        self.config = c
+        self.capacity = capacity
+        self.backend = backend
+
+    def close(self):
+        if self.handle:
+            load().fah_decoder_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def position(self) -> int:
+        v = ctypes.c_int()
+        _check(load().fah_decoder_position(self.handle, ctypes.byref(v)))
+        return v.value
+
+    def reset(self):
+        """QwenDecoder.Reset (QwenDecoder.cs:117)."""
+        self.set_position(0)
+
+    def set_position(self, position: int):
+        """QwenDecoder.RestorePrefix (QwenDecoder.cs:137) for any cached length."""
+        _check(load().fah_decoder_set_position(self.handle, position))
+
+    def decode(self, embeddings: np.ndarray, frames: int, output_logits: bool = True):
+        x = np.ascontiguousarray(embeddings, dtype=np.float32)
+        if x.size != frames * self.config.width:
+            raise ValueError("Decoder context exhausted or invalid embeddings")
+        logits = np.empty(self.config.vocab, dtype=np.float32) if output_logits else None
+        _check(load().fah_decoder_decode(self.handle, _p(x, ctypes.c_float), frames,
+                                         None if logits is None else _p(logits, ctypes.c_float)))
+        return logits
+
+    def embed(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((t.size, self.config.width), dtype=np.float32)
+        _check(load().fah_decoder_embed(self.handle, _p(t, ctypes.c_int32), t.size, _p(out, ctypes.c_float)))
+        return out
+
+    def greedy(self) -> int:
+        v = ctypes.c_int32()
+        _check(load().fah_decoder_greedy(self.handle, ctypes.byref(v)))
+        return v.value
+
+    def generate(self, steps: int) -> np.ndarray:
+        tokens = np.empty(max(steps, 1), dtype=np.int32)
+        _check(load().fah_decoder_generate(self.handle, steps, _p(tokens, ctypes.c_int32)))
+        return tokens[:steps]
+
+    def kv_write(self, layer: int, keys_f16: np.ndarray, values_f16: np.ndarray):
+        k = np.ascontiguousarray(keys_f16, dtype=np.float16).view(np.uint16)
+        v = np.ascontiguousarray(values_f16, dtype=np.float16).view(np.uint16)
+        width = self.config.kv_width
+        positions = k.size // width
+        _check(load().fah_decoder_kv_write(self.handle, layer, _p(k, ctypes.c_uint16), _p(v, ctypes.c_uint16),
+                                           positions))
+
+    def kv_read(self, layer: int, positions: int):
+        width = self.config.kv_width
+        k = np.empty(positions * width, dtype=np.uint16)
+        v = np.empty(positions * width, dtype=np.uint16)
+        _check(load().fah_decoder_kv_read(self.handle, layer, _p(k, ctypes.c_uint16), _p(v, ctypes.c_uint16),
+                                          positions))
+        return k.view(np.float16), v.view(np.float16)
+
+    @property
+    def weight_bytes(self) -> int:
+        return load().fah_decoder_weight_bytes(self.handle)

@@ -1,0 +1,203 @@
+/*
+ * funasr_hip.h -- C ABI of the MI355X (gfx950) Qwen3 Q8_0 decoder library.
+ *
+ * This is the drop-in boundary behind FunAsrNet's FloatBackend seam. A C#
+ * FunAsrNet.Hip assembly binds these symbols with [LibraryImport]; every
+ * entry point names the reference interface it replaces (paths relative to
+ * the FunAsrNet source tree).
+ *
+ * Conventions (from the reference's Try* contract,
+ * src/FunAsrNet/IQuantizedComputeBackend.cs:4-14, IFloatComputeBackend.cs:18):
+ *   FAH_OK (0)        the call completed; outputs are written.
+ *   FAH_DECLINED (1)  unsupported shape or type: outputs are untouched and
+ *                     the caller continues on its CPU path ("return false").
+ *   < 0               error: argument mismatch (ArgumentException), device
+ *                     failure (InvalidOperationException) or use after
+ *                     destroy (ObjectDisposedException); fah_last_error()
+ *                     returns the message for the calling thread.
+ * Host pointers are only read or written during the call. Weights are copied
+ * to the device once at upload and are immutable afterwards. A context owns
+ * one HIP stream; calls on one context are serialised by the library, calls
+ * on different contexts may run concurrently.
+ */
+#ifndef FUNASR_HIP_H
+#define FUNASR_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FAH_OK 0
+#define FAH_DECLINED 1
+#define FAH_ERROR_ARGUMENT (-1)
+#define FAH_ERROR_DEVICE (-2)
+#define FAH_ERROR_DISPOSED (-3)
+#define FAH_ERROR_STATE (-4)
+
+#define FAH_ABI_VERSION 1
+
+typedef struct fah_context fah_context;
+typedef struct fah_weight fah_weight;
+typedef struct fah_decoder fah_decoder;
+
+/* Library ------------------------------------------------------------------ */
+
+/* ABI version of the loaded library (FAH_ABI_VERSION). */
+int fah_abi_version(void);
+
+/* Message of the last failing call on this thread (never NULL). Replaces the
+ * exception text the reference raises (VulkanQuantizedBackend.cs:49-52). */
+const char* fah_last_error(void);
+
+/* Number of visible HIP devices; 0 when none (the C# loader then keeps the
+ * CPU path, as VulkanFloatBackend creation failure does). */
+int fah_device_count(void);
+
+/* Context: one device plus one stream. Replaces the backend object assigned
+ * to FunAsr.FloatBackend (src/FunAsrNet/FunAsr.cs:67-71). */
+int fah_context_create(int device, fah_context** out);
+int fah_context_destroy(fah_context* context);
+int fah_context_synchronize(fah_context* context);
+/* Backend name (IFloatComputeBackend.Name, IFloatComputeBackend.cs:6-9). */
+const char* fah_context_name(const fah_context* context);
+/* Projections below this many multiply-adds (frames*rows*cols) are declined
+ * so the caller's CPU path runs them, as VulkanFloatBackend.MinimumOperations
+ * does (src/FunAsrNet.Vulkan/VulkanFloatBackend.cs:36; default 250000). */
+int fah_context_set_minimum_operations(fah_context* context, int64_t operations);
+/* The context's hipStream_t, for callers that order their own device work
+ * (device-pointer entry points below) with the library's. */
+void* fah_context_stream(fah_context* context);
+
+/* Weights ------------------------------------------------------------------ */
+
+/* Upload a Q8_0 matrix in the reference's post-load layout: `quantized` is
+ * sbyte[rows*cols] row-major, `scales` float[rows*cols/32]
+ * (Weight.Quantized / Weight.Scales, src/FunAsrNet/Gguf.cs:289-307,
+ * Columns = cols = Shape[0], Rows = rows = Shape[1]). Scales are kept as
+ * fp16 on the device when every scale converts exactly (always true for
+ * GGUF Q8_0), otherwise as fp32. cols must be a multiple of 32. */
+int fah_weight_q8_upload(fah_context* context, const int8_t* quantized, const float* scales,
+                         int rows, int cols, fah_weight** out);
+int fah_weight_release(fah_weight* weight);
+/* Device bytes held by the weight (int8 plane plus scale plane). */
+int64_t fah_weight_device_bytes(const fah_weight* weight);
+
+/* Projections (host buffers) ------------------------------------------------ */
+
+/* IQuantizedComputeBackend.TryQuantizedLinear
+ * (src/FunAsrNet/IQuantizedComputeBackend.cs:4-14; reference device version
+ * src/FunAsrNet.Vulkan/VulkanQuantizedBackend.cs:40-133):
+ * output[frames*rows] = bias + Q8 projection of the per-32-block quantised
+ * input[frames*cols], with the reference's exact activation quantisation and
+ * per-row block-ordered fp32 accumulation. bias may be NULL. */
+int fah_quantized_linear(fah_context* context, const float* input, int frames, const fah_weight* weight,
+                         const float* bias, float* output);
+
+/* IGroupedComputeBackend.TryLinearMany
+ * (src/FunAsrNet/IGroupedComputeBackend.cs:4-13; CPU version
+ * src/FunAsrNet/TensorMath.Interleaved.cs:22-46): one shared activation
+ * quantisation, outputs[i][frames*rows_i]. All weights share cols. */
+int fah_linear_many(fah_context* context, const float* input, int frames, const fah_weight* const* weights,
+                    int count, float* const* outputs);
+
+/* Projections on device-resident buffers (pointers from hipMalloc on the
+ * context's device; work is ordered on the context stream) ------------------ */
+
+/* TensorMath.Quantize (src/FunAsrNet/TensorMath.cs:378-412): n % 32 == 0. */
+int fah_quantize_device(fah_context* context, const float* x, int64_t n, int8_t* q, float* scales);
+
+/* Q8_0 x quantised-activation GEMV/GEMM: out[frames*rows] from q[frames*cols],
+ * scales[frames*cols/32] (TensorMath.QuantizedRowsAvx.cs:17-60 order). */
+int fah_q8_gemv_device(fah_context* context, const int8_t* q, const float* scales, int frames,
+                       const fah_weight* weight, float* out);
+
+/* Exact int32 block dots dots[rows*cols/32] of one quantised activation row
+ * against every weight row (the integer part of the projection,
+ * TensorMath.QuantizedRowsAvx.cs:80-87), for bit-exact verification. */
+int fah_q8_block_dots_device(fah_context* context, const int8_t* q, const fah_weight* weight, int32_t* dots);
+
+/* Decoder ------------------------------------------------------------------- */
+
+typedef struct fah_decoder_config {
+    int width;      /* qwen3.embedding_length, 1024 */
+    int heads;      /* qwen3.attention.head_count, 16 */
+    int kv_heads;   /* qwen3.attention.head_count_kv, 8 (heads == 2*kv_heads) */
+    int head_size;  /* qwen3.attention.key_length, 128 */
+    int layers;     /* qwen3.block_count, 28 */
+    int ffn;        /* ffn_gate rows, 3072 */
+    int vocab;      /* token_embd rows, 151936 */
+    float eps;      /* qwen3.attention.layer_norm_rms_epsilon, 1e-6 */
+    float rope_base;/* qwen3.rope.freq_base, 1e6 */
+    int capacity;   /* maximum positions (QwenDecoder ctor `capacity`, default 2048) */
+} fah_decoder_config;
+
+typedef struct fah_q8_host {
+    const int8_t* quantized; /* [rows*cols] */
+    const float* scales;     /* [rows*cols/32] */
+    int rows, cols;
+} fah_q8_host;
+
+typedef struct fah_layer_host {
+    fah_q8_host wq, wk, wv, wo, gate, up, down;
+    const float* attn_norm; /* [width] */
+    const float* q_norm;    /* [head_size] */
+    const float* k_norm;    /* [head_size] */
+    const float* ffn_norm;  /* [width] */
+} fah_layer_host;
+
+/* Device-resident QwenDecoder (src/FunAsrNet/QwenDecoder.cs:46-112): copies
+ * every weight, builds the RoPE table with the C runtime's powf/cosf/sinf as
+ * the reference does (QwenDecoder.cs:78-95), allocates the F16 KV cache for
+ * `capacity` positions. `output` NULL means the lm_head is tied to
+ * token_embd (QwenDecoder.cs:267). There is no reference counterpart for a
+ * step-level seam: the C# side probes an optional IDecoderStepBackend at the
+ * top of QwenDecoder.Decode, like IAttentionComputeBackend (TensorMath.cs:619). */
+int fah_decoder_create(fah_context* context, const fah_decoder_config* config, const fah_layer_host* layers,
+                       const fah_q8_host* token_embd, const fah_q8_host* output, const float* output_norm,
+                       fah_decoder** out);
+int fah_decoder_destroy(fah_decoder* decoder);
+
+/* QwenDecoder.Reset (QwenDecoder.cs:117) and RestorePrefix (:137): set the
+ * decode position; cached K/V rows below it stay valid. */
+int fah_decoder_set_position(fah_decoder* decoder, int position);
+int fah_decoder_position(const fah_decoder* decoder, int* position);
+
+/* QwenDecoder.Decode (QwenDecoder.cs:161-271): run `frames` embedding rows
+ * (host, [frames*width]) through the decoder at the current position,
+ * append their K/V, advance the position, and write the last row's logits
+ * (host, [vocab]) when `logits` is not NULL. Throws (returns <0) when
+ * position + frames exceeds capacity, as the reference does (:163-166). */
+int fah_decoder_decode(fah_decoder* decoder, const float* embeddings, int frames, float* logits);
+
+/* QwenDecoder.Embed (QwenDecoder.cs:143-152) for host tokens -> host rows. */
+int fah_decoder_embed(fah_decoder* decoder, const int32_t* tokens, int count, float* out);
+
+/* QwenDecoder.Greedy (QwenDecoder.cs:278-326) of the logits produced by the
+ * last decode, computed on the device. */
+int fah_decoder_greedy(fah_decoder* decoder, int32_t* token);
+
+/* The FunAsr.Transcribe loop (src/FunAsrNet/FunAsr.cs:167-178) without the
+ * tokenizer's end check: `steps` times Greedy -> Embed -> Decode(1), entirely
+ * on the device (token feedback stays in device memory; one captured HIP
+ * graph per step). The first token is the greedy choice of the logits of the
+ * preceding decode. tokens[steps] receives the chosen tokens. */
+int fah_decoder_generate(fah_decoder* decoder, int steps, int32_t* tokens);
+
+/* Overwrite cached K/V rows [0, positions) of one layer from fp16 bit
+ * patterns laid out [positions][kv_heads*head_size] (long-context stress
+ * inputs; no reference counterpart). */
+int fah_decoder_kv_write(fah_decoder* decoder, int layer, const uint16_t* keys, const uint16_t* values,
+                         int positions);
+/* Read cached K/V rows [0, positions) of one layer as fp16 bits. */
+int fah_decoder_kv_read(fah_decoder* decoder, int layer, uint16_t* keys, uint16_t* values, int positions);
+
+/* Device bytes of the weights streamed per decoded token (all projections
+ * plus the lm_head, Q8_0 int8 and scale planes as stored). */
+int64_t fah_decoder_weight_bytes(const fah_decoder* decoder);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,157 @@
+"""GPU parity of the Q8_0 path through the C ABI: activation quantisation and
+int32 block dots bit-exact, projections bit-exact against the oracle."""
+import os
+
+import numpy as np
+import pytest
+
+from tests.golden.make_golden import q8_kat_case
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+# Decoder projection shapes (K -> N) of Qwen3-0.6B.
+SHAPES = [(1024, 2048), (1024, 1024), (2048, 1024), (1024, 3072), (3072, 1024), (1024, 151936)]
+
+
+@pytest.fixture(scope="module")
+def backend():
+    from funasrnet_amd.hip import HipBackend
+    b = HipBackend(0, minimum_operations=0)
+    yield b
+    b.close()
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible HIP device"
+    return torch
+
+
+def _weights(rng, rows, cols):
+    from funasrnet_amd.model import Q8Tensor
+    q = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
+    s = (np.abs(rng.standard_normal(rows * cols // 32, dtype=np.float32)) * np.float32(0.02 / 127)).astype(np.float16)
+    return Q8Tensor("w", q, s.astype(np.float32).reshape(rows, -1))
+
+
+def test_quantize_golden_bit_exact(backend, torch_cuda):
+    torch = torch_cuda
+    g = np.load(os.path.join(GOLDEN, "quantize_kat.npz"))
+    x = torch.from_numpy(g["input"]).cuda()
+    q = torch.empty(x.numel(), dtype=torch.int8, device="cuda")
+    s = torch.empty(x.numel() // 32, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    backend.quantize_device(x.data_ptr(), x.numel(), q.data_ptr(), s.data_ptr())
+    backend.synchronize()
+    qh, sh = q.cpu().numpy(), s.cpu().numpy()
+    assert np.array_equal(qh, g["q"])
+    nan = np.isnan(g["scales"])
+    assert np.array_equal(np.isnan(sh), nan)
+    assert np.array_equal(sh[~nan].view(np.uint32), g["scales"][~nan].view(np.uint32))
+
+
+def test_quantize_random_bit_exact(backend, torch_cuda, oracle_lib):
+    torch = torch_cuda
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(1 << 16), rng.standard_normal(1 << 14) * 10.0 ** rng.integers(-38, 38, 1 << 14)])
+    x = x.astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    q = torch.empty(x.size, dtype=torch.int8, device="cuda")
+    s = torch.empty(x.size // 32, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    backend.quantize_device(xd.data_ptr(), x.size, q.data_ptr(), s.data_ptr())
+    backend.synchronize()
+    q0, s0 = oracle_lib.quantize(x)
+    assert np.array_equal(q.cpu().numpy(), q0)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s0.view(np.uint32))
+
+
+@pytest.mark.parametrize("cols,rows", SHAPES)
+def test_block_dots_bit_exact(backend, torch_cuda, oracle_lib, cols, rows):
+    torch = torch_cuda
+    rng = np.random.default_rng(cols + rows)
+    w = _weights(rng, rows, cols)
+    w.quantized[0, :32] = -128  # the kernels must accept -128 weights
+    hw = backend.weight(w)
+    x = rng.standard_normal(cols).astype(np.float32)
+    xq, xs = oracle_lib.quantize(x)
+    q = torch.from_numpy(xq).cuda()
+    dots = torch.empty(rows * cols // 32, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    backend.block_dots_device(q.data_ptr(), hw, dots.data_ptr())
+    backend.synchronize()
+    assert np.array_equal(dots.cpu().numpy().reshape(rows, -1), oracle_lib.block_dots(xq, w.quantized))
+
+
+@pytest.mark.parametrize("cols,rows", SHAPES)
+def test_gemv_bit_exact(backend, torch_cuda, oracle_lib, cols, rows):
+    torch = torch_cuda
+    rng = np.random.default_rng(cols * 7 + rows)
+    w = _weights(rng, rows, cols)
+    hw = backend.weight(w)
+    x = rng.standard_normal(cols).astype(np.float32)
+    xq, xs = oracle_lib.quantize(x)
+    q, s = torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda()
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    assert backend.gemv_device(q.data_ptr(), s.data_ptr(), 1, hw, out.data_ptr()) == 0
+    backend.synchronize()
+    expected = oracle_lib.gemv_quantized(xq, xs, w.quantized, w.scales)[0]
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), expected.view(np.uint32))
+
+
+@pytest.mark.parametrize("frames", [1, 3, 17])
+@pytest.mark.parametrize("width", [32, 96, 1024])
+@pytest.mark.parametrize("rows", [1, 3, 19, 32])
+def test_quantized_linear_reference_kat(backend, frames, width, rows):
+    """QuantizedAvxChecks.cs:17-50 through TryQuantizedLinear, bit-exact to
+    the committed golden outputs (fp32 scale plane: 0.013/-0.007 are not fp16)."""
+    from funasrnet_amd.model import Q8Tensor
+    values, w, ws, bias, _ = q8_kat_case(frames, width, rows)
+    golden = np.load(os.path.join(GOLDEN, "q8_kat.npz"))[f"{frames}x{width}x{rows}"]
+    out = np.full(frames * rows, 123.0, dtype=np.float32)
+    assert backend.try_quantized_linear(values, frames, Q8Tensor("kat", w, ws), bias, out)
+    assert np.array_equal(out.reshape(frames, rows).view(np.uint32), golden.view(np.uint32))
+
+
+def test_linear_many_equals_independent(backend, oracle_lib):
+    """QuantizedGroupAvxChecks.cs:17-85: grouped outputs bit-identical to
+    separate projections and to the oracle, signed/zero scales, -128 weights."""
+    from funasrnet_amd.model import Q8Tensor
+    rng = np.random.default_rng(512031)
+    for frames in (1, 2, 5, 17):
+        for width in (32, 96, 1024):
+            x = rng.standard_normal(frames * width).astype(np.float32)
+            tensors = []
+            for rows in (1, 3, 17, 32, 65):
+                q = np.where(np.arange(rows * width).reshape(rows, width) % 5 == 0, -128,
+                             rng.integers(-127, 128, (rows, width))).astype(np.int8)
+                s = np.array([0.0, -0.007, 0.013, 0.125], dtype=np.float32)[np.arange(rows * width // 32) % 4]
+                tensors.append(Q8Tensor(f"g{rows}", q, s.reshape(rows, -1)))
+            outs = backend.try_linear_many(x, frames, tensors)
+            assert outs is not None
+            for t, o in zip(tensors, outs):
+                single = np.empty(frames * t.rows, dtype=np.float32)
+                assert backend.try_quantized_linear(x, frames, t, None, single)
+                expected = oracle_lib.linear(x, t.quantized, t.scales).ravel()
+                assert np.array_equal(o.view(np.uint32), single.view(np.uint32))
+                assert np.array_equal(o.view(np.uint32), expected.view(np.uint32))
+
+
+def test_declines_small_and_leaves_output_untouched():
+    """IQuantizedComputeBackend contract: a declined call returns false and
+    the output keeps its contents (MinimumOperations, VulkanFloatBackend.cs:36)."""
+    from funasrnet_amd.hip import HipBackend
+    from funasrnet_amd.model import Q8Tensor
+    b = HipBackend(0)  # default minimum of 250000 multiply-adds
+    try:
+        w = Q8Tensor("tiny", np.ones((3, 32), dtype=np.int8), np.ones((3, 1), dtype=np.float32))
+        out = np.full(3, 123.0, dtype=np.float32)
+        assert not b.try_quantized_linear(np.ones(32, dtype=np.float32), 1, w, None, out)
+        assert np.all(out == 123.0)
+        with pytest.raises(ValueError):
+            b.try_quantized_linear(np.ones(31, dtype=np.float32), 1, w, None, out)
+    finally:
+        b.close()
