@@ -23,10 +23,9 @@ def backend():
 
 
 @pytest.fixture(scope="module")
-def torch_cuda():
-    import torch
-    assert torch.cuda.is_available(), "GPU tests need a visible HIP device"
-    return torch
+def dev():
+    from funasrnet_amd import device
+    return device
 
 
 def _weights(rng, rows, cols):
@@ -36,70 +35,63 @@ def _weights(rng, rows, cols):
     return Q8Tensor("w", q, s.astype(np.float32).reshape(rows, -1))
 
 
-def test_quantize_golden_bit_exact(backend, torch_cuda):
-    torch = torch_cuda
+def test_quantize_golden_bit_exact(backend, dev):
     g = np.load(os.path.join(GOLDEN, "quantize_kat.npz"))
-    x = torch.from_numpy(g["input"]).cuda()
-    q = torch.empty(x.numel(), dtype=torch.int8, device="cuda")
-    s = torch.empty(x.numel() // 32, dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    backend.quantize_device(x.data_ptr(), x.numel(), q.data_ptr(), s.data_ptr())
+    n = g["input"].size
+    x = dev.DeviceArray.from_numpy(g["input"])
+    q = dev.DeviceArray(n, np.int8)
+    s = dev.DeviceArray(n // 32, np.float32)
+    backend.quantize_device(x.ptr, n, q.ptr, s.ptr)
     backend.synchronize()
-    qh, sh = q.cpu().numpy(), s.cpu().numpy()
+    qh, sh = q.numpy(), s.numpy()
     assert np.array_equal(qh, g["q"])
     nan = np.isnan(g["scales"])
     assert np.array_equal(np.isnan(sh), nan)
     assert np.array_equal(sh[~nan].view(np.uint32), g["scales"][~nan].view(np.uint32))
 
 
-def test_quantize_random_bit_exact(backend, torch_cuda, oracle_lib):
-    torch = torch_cuda
+def test_quantize_random_bit_exact(backend, dev, oracle_lib):
     rng = np.random.default_rng(1)
     x = np.concatenate([rng.standard_normal(1 << 16), rng.standard_normal(1 << 14) * 10.0 ** rng.integers(-38, 38, 1 << 14)])
     x = x.astype(np.float32)
-    xd = torch.from_numpy(x).cuda()
-    q = torch.empty(x.size, dtype=torch.int8, device="cuda")
-    s = torch.empty(x.size // 32, dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    backend.quantize_device(xd.data_ptr(), x.size, q.data_ptr(), s.data_ptr())
+    xd = dev.DeviceArray.from_numpy(x)
+    q = dev.DeviceArray(x.size, np.int8)
+    s = dev.DeviceArray(x.size // 32, np.float32)
+    backend.quantize_device(xd.ptr, x.size, q.ptr, s.ptr)
     backend.synchronize()
     q0, s0 = oracle_lib.quantize(x)
-    assert np.array_equal(q.cpu().numpy(), q0)
-    assert np.array_equal(s.cpu().numpy().view(np.uint32), s0.view(np.uint32))
+    assert np.array_equal(q.numpy(), q0)
+    assert np.array_equal(s.numpy().view(np.uint32), s0.view(np.uint32))
 
 
 @pytest.mark.parametrize("cols,rows", SHAPES)
-def test_block_dots_bit_exact(backend, torch_cuda, oracle_lib, cols, rows):
-    torch = torch_cuda
+def test_block_dots_bit_exact(backend, dev, oracle_lib, cols, rows):
     rng = np.random.default_rng(cols + rows)
     w = _weights(rng, rows, cols)
     w.quantized[0, :32] = -128  # the kernels must accept -128 weights
     hw = backend.weight(w)
     x = rng.standard_normal(cols).astype(np.float32)
     xq, xs = oracle_lib.quantize(x)
-    q = torch.from_numpy(xq).cuda()
-    dots = torch.empty(rows * cols // 32, dtype=torch.int32, device="cuda")
-    torch.cuda.synchronize()
-    backend.block_dots_device(q.data_ptr(), hw, dots.data_ptr())
+    q = dev.DeviceArray.from_numpy(xq)
+    dots = dev.DeviceArray(rows * cols // 32, np.int32)
+    backend.block_dots_device(q.ptr, hw, dots.ptr)
     backend.synchronize()
-    assert np.array_equal(dots.cpu().numpy().reshape(rows, -1), oracle_lib.block_dots(xq, w.quantized))
+    assert np.array_equal(dots.numpy().reshape(rows, -1), oracle_lib.block_dots(xq, w.quantized))
 
 
 @pytest.mark.parametrize("cols,rows", SHAPES)
-def test_gemv_bit_exact(backend, torch_cuda, oracle_lib, cols, rows):
-    torch = torch_cuda
+def test_gemv_bit_exact(backend, dev, oracle_lib, cols, rows):
     rng = np.random.default_rng(cols * 7 + rows)
     w = _weights(rng, rows, cols)
     hw = backend.weight(w)
     x = rng.standard_normal(cols).astype(np.float32)
     xq, xs = oracle_lib.quantize(x)
-    q, s = torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda()
-    out = torch.empty(rows, dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    assert backend.gemv_device(q.data_ptr(), s.data_ptr(), 1, hw, out.data_ptr()) == 0
+    q, s = dev.DeviceArray.from_numpy(xq), dev.DeviceArray.from_numpy(xs)
+    out = dev.DeviceArray(rows, np.float32)
+    assert backend.gemv_device(q.ptr, s.ptr, 1, hw, out.ptr) == 0
     backend.synchronize()
     expected = oracle_lib.gemv_quantized(xq, xs, w.quantized, w.scales)[0]
-    assert np.array_equal(out.cpu().numpy().view(np.uint32), expected.view(np.uint32))
+    assert np.array_equal(out.numpy().view(np.uint32), expected.view(np.uint32))
 
 
 @pytest.mark.parametrize("frames", [1, 3, 17])
