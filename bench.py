@@ -1,0 +1,181 @@
+"""Benchmark: Qwen3-0.6B Q8_0 batch-1 greedy decode on one MI355X.
+
+Workload (the decode configuration the metric is quoted on): the synthetic
+Qwen3-0.6B-shaped decoder (28 layers, hidden 1024, 16/8 heads x 128,
+FFN 3072, vocab 151936 tied, Q8_0 int8 U{-127..127}, fp16 scales
+|N(0,0.02)|/127, seed 0), a 150-row N(0,1) embedding prefix, then greedy
+decode steps with the F16 KV cache. A step is one decoded token: the whole
+decoder on the device (embedding of the previous greedy token, 28 layers,
+final norm, tied lm_head, argmax), one captured HIP graph per step.
+
+Printed: one JSON line with decode tok/s, the Q8_0 GEMV roofline (lm_head
+shape 1024->151936, HIP events on the context stream, four rotated weight
+copies so every launch streams from HBM), and the CPU oracle timed on this
+host as the baseline.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+PREFIX = 150
+
+
+def gemv_roofline(backend, weights, repeats: int = 40):
+    """Average duration of the Q8_0 GEMV kernel at the lm_head shape."""
+    from funasrnet_amd import device
+    from funasrnet_amd.model import Q8Tensor
+
+    lm = weights.lm_head
+    copies = [backend.weight(Q8Tensor(f"lm{i}", lm.quantized, lm.scales)) for i in range(4)]
+    rows, cols = lm.rows, lm.columns
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(cols).astype(np.float32)
+    xd = device.DeviceArray.from_numpy(x)
+    q = device.DeviceArray(cols, np.int8)
+    s = device.DeviceArray(cols // 32, np.float32)
+    out = device.DeviceArray(rows, np.float32)
+    backend.quantize_device(xd.ptr, cols, q.ptr, s.ptr)
+    for i in range(8):
+        backend.gemv_device(q.ptr, s.ptr, 1, copies[i % 4], out.ptr)
+    backend.synchronize()
+    start, end = device.Event(), device.Event()
+    start.record(backend.stream)
+    for i in range(repeats):
+        backend.gemv_device(q.ptr, s.ptr, 1, copies[i % 4], out.ptr)
+    end.record(backend.stream)
+    end.synchronize()
+    avg_us = start.elapsed_ms(end) * 1000.0 / repeats
+    algorithmic = rows * cols * 34 // 32 + cols + 4 * (cols // 32) + 4 * rows
+    device_bytes = copies[0].device_bytes
+    for c in copies:
+        c.close()
+    return {
+        "kernel": "q8_gemv_kernel (Q8_0 GEMV, 1024->151936)",
+        "avg_us": avg_us,
+        "algorithmic_bytes": algorithmic,
+        "device_bytes": device_bytes,
+        "achieved_gbs": algorithmic / (avg_us * 1e-6) / 1e9,
+    }
+
+
+def cpu_baseline(weights, prefix, tokens: int, threads: int):
+    """The oracle (C restatement of the reference x64 path) on this host."""
+    import oracle
+
+    used = oracle.set_threads(threads)
+    dec = oracle.Decoder(weights, capacity=PREFIX + tokens + 8)
+    try:
+        logits = dec.decode(prefix, prefix.shape[0])
+        t0 = time.perf_counter()
+        for _ in range(tokens):
+            t = oracle.greedy(logits)
+            logits = dec.decode(dec.embed([t]), 1)
+        seconds = time.perf_counter() - t0
+    finally:
+        dec.close()
+    return tokens / seconds, used, seconds
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cpu-tokens", type=int, default=64)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
+              f"(requested --gpus {args.gpus}); see DESIGN.md for how sessions would shard.", file=sys.stderr)
+        return 2
+    if PREFIX + max(args.steps, args.warmup) + 1 > 2048:
+        print("steps + prefix exceed the decoder capacity (2048)", file=sys.stderr)
+        return 2
+
+    from funasrnet_amd import device, model
+    from funasrnet_amd.hip import HipBackend, HipDecoder
+
+    cfg = model.QWEN3_0_6B
+    weights = model.synthetic(cfg, seed=0)
+    prefix = np.random.default_rng(0).standard_normal((PREFIX, cfg.width)).astype(np.float32)
+
+    backend = HipBackend(0)
+    dec = HipDecoder(backend, weights, capacity=2048)
+    # Warm-up pass: prefill, then `warmup` untimed decode steps.
+    dec.decode(prefix, PREFIX)
+    warm_tokens = dec.generate(args.warmup) if args.warmup else np.array([], dtype=np.int32)
+    # Timed pass from the same state: reset, prefill (untimed), K timed steps.
+    dec.reset()
+    dec.decode(prefix, PREFIX)
+    device.synchronize()
+    start, end = device.Event(), device.Event()
+    t0 = time.perf_counter()
+    start.record(backend.stream)
+    tokens = dec.generate(args.steps)
+    end.record(backend.stream)
+    end.synchronize()
+    wall = time.perf_counter() - t0
+    device.synchronize()
+    gpu_ms = start.elapsed_ms(end)
+    seconds = max(gpu_ms / 1000.0, 1e-9)
+    tok_s = args.steps / seconds
+    deterministic = bool(np.array_equal(tokens[: len(warm_tokens)], warm_tokens))
+
+    weight_bytes = cfg.weight_bytes_per_token()
+    kv_bytes = sum(114688 * (PREFIX + i + 1) for i in range(args.steps)) / max(args.steps, 1)
+    step_bytes = weight_bytes + kv_bytes + 4 * (cfg.width * (2 * cfg.layers + 1) + 2 * cfg.head_size * cfg.layers)
+    step_gbs = step_bytes * tok_s / 1e9
+
+    roof = gemv_roofline(backend, weights)
+    dec.close()
+    backend.close()
+
+    baseline = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        cpu_tok_s, used, cpu_seconds = cpu_baseline(weights, prefix, args.cpu_tokens, threads)
+        baseline = {"value": round(cpu_tok_s, 3), "unit": "tok/s", "cores": used, "kind": "port",
+                    "sample": f"oracle (C restatement of the reference x64 Q8_0 path), same weights and prefix, "
+                              f"{args.cpu_tokens} greedy decode steps after the 150-row prefill, "
+                              f"{cpu_seconds:.1f} s, {used} OpenMP threads"}
+
+    line = {
+        "metric": "decode tok/s Qwen3-0.6B Q8_0 bs=1; Q8_0 GEMV achieved HBM GB/s vs peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 dot / fp32 accumulate (Q8_0)",
+        "data": "synthetic random-init weights (seed 0) and N(0,1) prefix",
+        "config": {"workload": "qwen3-0.6b q8_0 greedy decode, batch 1, 150-row prefix, F16 KV",
+                   "global_batch": 1, "prefix": PREFIX, "decode_steps": args.steps, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(roof["achieved_gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(roof["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": roof["kernel"], "avg_us": round(roof["avg_us"], 3),
+                     "algorithmic_bytes_per_launch": roof["algorithmic_bytes"]},
+        "decode_step": {"bytes_per_token": int(step_bytes), "achieved_gbs": round(step_gbs, 1),
+                        "frac_of_hbm_peak": round(step_gbs / HBM_PEAK_GBS, 4), "wall_s": round(wall, 4),
+                        "deterministic_vs_warmup": deterministic},
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -328,20 +328,15 @@ void enqueue_head(fah_decoder* d, hipStream_t s) {
         "greedy");
 }
 
+void enqueue_kind(fah_decoder* d, int kind, hipStream_t s);
+
 hipGraphExec_t capture(fah_decoder* d, int kind) {
   hipStream_t s = d->context->stream;
   hipGraph_t graph = nullptr;
   check(hipStreamSynchronize(s), "hipStreamSynchronize");
   check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
   try {
-    if (kind == 2)
-      check(fah::launch_embed(d->embed.q.as<int8_t>(), d->embed.s.ptr, d->half_scales, d->cfg.width, d->cfg.vocab,
-                              d->token.as<int>(), d->x.as<float>(), d->history.as<int>(),
-                              d->history_count.as<int>(), s),
-            "embed");
-    enqueue_layers(d, s);
-    if (kind >= 1) enqueue_head(d, s);
-    check(fah::launch_advance(d->position.as<int>(), 1, s), "advance");
+    enqueue_kind(d, kind, s);
   } catch (...) {
     hipGraph_t dead = nullptr;
     (void)hipStreamEndCapture(s, &dead);
@@ -356,10 +351,37 @@ hipGraphExec_t capture(fah_decoder* d, int kind) {
   return exec;
 }
 
-hipGraphExec_t graph_for(fah_decoder* d, int kind) {
+// Enqueue one decoder row: kind 0 = layers only, 1 = layers + lm_head +
+// greedy, 2 = embedding of the device token + layers + lm_head + greedy.
+void enqueue_kind(fah_decoder* d, int kind, hipStream_t s) {
+  if (kind == 2)
+    check(fah::launch_embed(d->embed.q.as<int8_t>(), d->embed.s.ptr, d->half_scales, d->cfg.width, d->cfg.vocab,
+                            d->token.as<int>(), d->x.as<float>(), d->history.as<int>(),
+                            d->history_count.as<int>(), s),
+          "embed");
+  enqueue_layers(d, s);
+  if (kind >= 1) enqueue_head(d, s);
+  check(fah::launch_advance(d->position.as<int>(), 1, s), "advance");
+}
+
+// FAH_GRAPHS=0 launches the kernels directly instead of replaying captured
+// graphs (profilers that do not follow stream capture).
+bool use_graphs() {
+  static const bool on = [] {
+    const char* v = std::getenv("FAH_GRAPHS");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
+void run_kind(fah_decoder* d, int kind, hipStream_t s) {
+  if (!use_graphs()) {
+    enqueue_kind(d, kind, s);
+    return;
+  }
   hipGraphExec_t* slot = kind == 0 ? &d->graph_row : kind == 1 ? &d->graph_logits : &d->graph_step;
   if (!*slot) *slot = capture(d, kind);
-  return *slot;
+  check(hipGraphLaunch(*slot, s), "hipGraphLaunch");
 }
 
 }  // namespace
@@ -621,11 +643,13 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
             "invalid decoder dimensions");
     require(k.heads % k.kv_heads == 0, "Invalid GQA head counts");
     require(k.head_size == 128, "head_size must be 128");
+    require(k.heads == 2 * k.kv_heads, "the paired GQA path needs heads == 2 * kv_heads");
     require(k.width % 32 == 0 && k.ffn % 32 == 0, "widths must be multiples of 32");
     int q_width = k.heads * k.head_size, kv_width = k.kv_heads * k.head_size;
     int maxk = fah::gemv_max_k();
     require(k.width <= maxk && k.ffn <= maxk && q_width <= maxk, "projection width exceeds kernel limit");
-    require(k.capacity >= 1 && k.capacity <= 12288, "capacity must be in [1, 12288]");
+    require(k.capacity >= 1 && fah::attention_slices(k.capacity, k.head_size) != 0,
+            "capacity exceeds the attention kernel's LDS budget");
     for (int l = 0; l < k.layers; ++l) {
       const fah_layer_host& L = layers[l];
       std::string p = "blk." + std::to_string(l) + ".";
@@ -643,6 +667,7 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
 
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
+    check(fah::prepare_attention(k.capacity, k.head_size), "attention LDS budget");
     auto d = std::make_unique<fah_decoder>();
     d->context = c;
     d->cfg = k;
@@ -805,7 +830,7 @@ int fah_decoder_decode(fah_decoder* d, const float* embeddings, int frames, floa
     for (int f = 0; f < frames; ++f) {
       check(hipMemcpyAsync(d->x.ptr, d->staging.as<char>() + row * f, row, hipMemcpyDeviceToDevice, s), "D2D row");
       bool last = f == frames - 1;
-      check(hipGraphLaunch(graph_for(d, last && logits ? 1 : 0), s), "hipGraphLaunch");
+      run_kind(d, last && logits ? 1 : 0, s);
     }
     if (logits)
       check(hipMemcpyAsync(logits, d->logits.ptr, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, s), "D2H");
@@ -862,8 +887,7 @@ int fah_decoder_generate(fah_decoder* d, int steps, int32_t* tokens) {
     hipStream_t s = d->context->stream;
     check(hipSetDevice(d->context->device), "hipSetDevice");
     check(hipMemsetAsync(d->history_count.ptr, 0, 4, s), "reset history");
-    hipGraphExec_t g = graph_for(d, 2);
-    for (int i = 0; i < steps; ++i) check(hipGraphLaunch(g, s), "hipGraphLaunch");
+    for (int i = 0; i < steps; ++i) run_kind(d, 2, s);
     if (steps > 0)
       check(hipMemcpyAsync(tokens, d->history.ptr, (size_t)steps * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
     check(hipStreamSynchronize(s), "hipStreamSynchronize");

@@ -60,6 +60,8 @@ hipError_t launch_greedy_reduce(const unsigned long long* keys, int count, const
 hipError_t launch_embed(const int8_t* q, const void* scales, bool half_scales, int K, int vocab, const int* token,
                         float* x, int* history, int* history_count, hipStream_t s);
 hipError_t launch_qk_prepare(const QkArgs& a, hipStream_t s);
+int attention_slices(int capacity, int head_size);
+hipError_t prepare_attention(int capacity, int head_size);
 hipError_t launch_attention(const AttnArgs& a, int score_groups, hipStream_t s);
 hipError_t launch_advance(int* position, int frames, hipStream_t s);
 hipError_t launch_quantize(const float* x, int64_t n, int8_t* q, float* scales, hipStream_t s);

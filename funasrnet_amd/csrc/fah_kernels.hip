@@ -27,16 +27,25 @@ struct ScaleFloat {
   static __device__ __forceinline__ float get(type v) { return v; }
 };
 
+// Workgroup barrier that orders LDS only. __syncthreads() also fences global
+// memory, which makes the compiler wait for every outstanding global load
+// (vmcnt(0)) before the barrier -- that would drain the weight stream the
+// GEMV issues ahead of its activation prologue.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Block-wide sum of one double per thread (256 threads, 4 waves).
 __device__ __forceinline__ double block_sum_double(double v, double* scratch) {
   v = wave_sum_double(v);
   int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   if (lane == 0) scratch[wave] = v;
-  __syncthreads();
+  lds_barrier();
   double total = 0.0;
   int waves = (blockDim.x + kWave - 1) / kWave;
   for (int i = 0; i < waves; ++i) total += scratch[i];
-  __syncthreads();
   return total;
 }
 
@@ -49,54 +58,71 @@ __device__ __forceinline__ float rms_inverse(double sum_sq, int width, float eps
   return fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
 }
 
-// Quantise K fp32 values staged in LDS (fx) into xq/xs (LDS); one thread per
-// 32-value block.
-__device__ __forceinline__ void quantize_lds(const float* fx, int K, int8_t* xq, float* xs) {
-  int blocks = K >> 5;
-  for (int b = threadIdx.x; b < blocks; b += blockDim.x) {
-    const float* v = fx + b * 32;
-    uint32_t m = 0;
+// Quantise four consecutive values held by this lane; the 32-value block is
+// spread over 8 consecutive lanes (shuffle max of the absolute bit patterns).
+// Returns the four int8 codes packed little-endian; *scale gets the block's d.
+__device__ __forceinline__ int quantize4(float v0, float v1, float v2, float v3, float* scale) {
+  uint32_t m = f2u(v0) & 0x7fffffffu;
+  uint32_t t = f2u(v1) & 0x7fffffffu;
+  m = t > m ? t : m;
+  t = f2u(v2) & 0x7fffffffu;
+  m = t > m ? t : m;
+  t = f2u(v3) & 0x7fffffffu;
+  m = t > m ? t : m;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      uint32_t a = f2u(v[i]) & 0x7fffffffu;
-      m = a > m ? a : m;
-    }
-    float inverse;
-    xs[b] = block_scale(m, &inverse);
-    int words[8];
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-      uint32_t packed = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) packed |= (uint32_t)(uint8_t)quantize_value(v[w * 4 + k], inverse) << (8 * k);
-      words[w] = (int)packed;
-    }
-    int4* dst = reinterpret_cast<int4*>(xq + b * 32);
-    dst[0] = make_int4(words[0], words[1], words[2], words[3]);
-    dst[1] = make_int4(words[4], words[5], words[6], words[7]);
+  for (int s = 1; s < 8; s <<= 1) {
+    uint32_t o = __shfl_xor(m, s, 8);
+    m = o > m ? o : m;
   }
+  float inverse;
+  *scale = block_scale(m, &inverse);
+  uint32_t packed = (uint32_t)(uint8_t)quantize_value(v0, inverse) | ((uint32_t)(uint8_t)quantize_value(v1, inverse) << 8) |
+                    ((uint32_t)(uint8_t)quantize_value(v2, inverse) << 16) |
+                    ((uint32_t)(uint8_t)quantize_value(v3, inverse) << 24);
+  return (int)packed;
 }
+
+constexpr int kMaxChunks = kMaxK / (4 * kThreads);  // K = chunks * 1024: 4 values per lane per chunk
 
 template <typename Scale, int IN, int OUT, int PAIRS>
 __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(GemvArgs a) {
-  __shared__ int4 xq_words[kMaxK / 16];
+  __shared__ int xq_s[kMaxK / 4];
   __shared__ float xs_s[kMaxK / 32];
-  __shared__ float fx_s[kMaxK];
-  __shared__ float prod_s[kThreads * PAIRS + 64];
-  __shared__ float sums_s[kThreads];
+  __shared__ float prod_s[kThreads * PAIRS];  // [block][row]
+  __shared__ float sums_s[64];
   __shared__ double red_s[kThreads / kWave];
-  __shared__ unsigned long long key_s[kThreads / kWave];
-  int8_t* xq_s = reinterpret_cast<int8_t*>(xq_words);
 
   const int tid = threadIdx.x;
   const int K = a.K, B = K >> 5;
   const int frame = blockIdx.y;
-  const int row0 = blockIdx.x * a.group_rows;
-  const int nrows = min(a.group_rows, a.rows - row0);
+  const int R = a.group_rows;
+  const int row0 = blockIdx.x * R;
+  const int nrows = min(R, a.rows - row0);
   const int npairs = nrows * B;
-  const int stride = B + 1;
 
-  // 1. Weight stream for this group: issued first, consumed after the prologue.
+  // 1. Activation, norm-weight and residual loads first: waiting for them
+  //    later does not wait for the weight stream issued after them.
+  float4 xv[kMaxChunks];
+  float4 nw[kMaxChunks];
+  int xw[kMaxChunks];
+  float xsv = 0.0f, rv = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) {
+    int e = c * 4 * kThreads + 4 * tid;
+    if (e < K) {
+      if (IN == kInputQuantized) {
+        xw[c] = *reinterpret_cast<const int*>(a.xq + (size_t)frame * K + e);
+      } else {
+        xv[c] = *reinterpret_cast<const float4*>(a.x + (size_t)frame * K + e);
+        if (IN == kInputNorm) nw[c] = *reinterpret_cast<const float4*>(a.norm_w + e);
+      }
+    }
+  }
+  if (IN == kInputQuantized && tid < B) xsv = a.xs[(size_t)frame * B + tid];
+  if (OUT == kOutResidual && tid < nrows) rv = a.resid[(size_t)frame * a.out_rows + row0 + tid];
+  if (OUT == kOutPlain && a.bias && tid < nrows) rv = a.bias[row0 + tid];
+
+  // 2. Weight stream for this group: one lane per (row, block) pair.
   int4 wv[PAIRS][2];
   typename Scale::type sv[PAIRS];
   const int8_t* wbase = a.w + (size_t)row0 * K;
@@ -112,37 +138,55 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(GemvArgs a) {
     }
   }
 
-  // 2. Activation prologue into LDS.
+  // 3. Activation prologue into LDS.
   if (IN == kInputQuantized) {
-    const int4* src = reinterpret_cast<const int4*>(a.xq + (size_t)frame * K);
-    for (int i = tid; i < K / 16; i += kThreads) xq_words[i] = src[i];
-    for (int i = tid; i < B; i += kThreads) xs_s[i] = a.xs[(size_t)frame * B + i];
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+      int e = c * 4 * kThreads + 4 * tid;
+      if (e < K) xq_s[e >> 2] = xw[c];
+    }
+    if (tid < B) xs_s[tid] = xsv;
   } else {
-    const float* x = a.x + (size_t)frame * K;
-    double sq = 0.0;
-    for (int i = tid; i < K; i += kThreads) {
-      float v = x[i];
-      fx_s[i] = v;
-      if (IN == kInputNorm) sq += (double)v * (double)v;
-    }
+    float inverse = 1.0f;
     if (IN == kInputNorm) {
-      double total = block_sum_double(sq, red_s);
-      float inverse = rms_inverse(total, K, a.eps);
-      for (int i = tid; i < K; i += kThreads) fx_s[i] = fmul(fmul(fx_s[i], inverse), a.norm_w[i]);
+      double sq = 0.0;
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) {
+        int e = c * 4 * kThreads + 4 * tid;
+        if (e < K) {
+          sq += (double)xv[c].x * (double)xv[c].x + (double)xv[c].y * (double)xv[c].y;
+          sq += (double)xv[c].z * (double)xv[c].z + (double)xv[c].w * (double)xv[c].w;
+        }
+      }
+      inverse = rms_inverse(block_sum_double(sq, red_s), K, a.eps);
     }
-    __syncthreads();
-    quantize_lds(fx_s, K, xq_s, xs_s);
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+      int e = c * 4 * kThreads + 4 * tid;
+      if (e < K) {
+        float4 v = xv[c];
+        if (IN == kInputNorm) {
+          v.x = fmul(fmul(v.x, inverse), nw[c].x);
+          v.y = fmul(fmul(v.y, inverse), nw[c].y);
+          v.z = fmul(fmul(v.z, inverse), nw[c].z);
+          v.w = fmul(fmul(v.w, inverse), nw[c].w);
+        }
+        float d;
+        xq_s[e >> 2] = quantize4(v.x, v.y, v.z, v.w, &d);
+        if ((tid & 7) == 0) xs_s[e >> 5] = d;
+      }
+    }
   }
-  __syncthreads();
+  lds_barrier();
 
-  // 3. Exact block dots and scaled products.
+  // 4. Exact block dots and scaled products, stored block-major.
 #pragma unroll
   for (int i = 0; i < PAIRS; ++i) {
     int j = tid + i * kThreads;
     if (j < npairs) {
       int r = j / B, b = j - r * B;
-      const int4* xv = reinterpret_cast<const int4*>(xq_s + b * 32);
-      int4 x0 = xv[0], x1 = xv[1];
+      const int4* xp = reinterpret_cast<const int4*>(xq_s + b * 8);
+      int4 x0 = xp[0], x1 = xp[1];
       int dot = 0;
       dot = __builtin_amdgcn_sdot4(wv[i][0].x, x0.x, dot, false);
       dot = __builtin_amdgcn_sdot4(wv[i][0].y, x0.y, dot, false);
@@ -152,30 +196,40 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(GemvArgs a) {
       dot = __builtin_amdgcn_sdot4(wv[i][1].y, x1.y, dot, false);
       dot = __builtin_amdgcn_sdot4(wv[i][1].z, x1.z, dot, false);
       dot = __builtin_amdgcn_sdot4(wv[i][1].w, x1.w, dot, false);
-      prod_s[r * stride + b] = fmul(fmul((float)dot, Scale::get(sv[i])), xs_s[b]);
+      prod_s[b * R + r] = fmul(fmul((float)dot, Scale::get(sv[i])), xs_s[b]);
     }
   }
-  __syncthreads();
+  lds_barrier();
 
-  // 4. Ordered block sum, one lane per row.
+  // 5. Ordered block sum from 0f, one lane per row (rows live in wave 0).
+  if (tid >= kWave) return;
   float sum = 0.0f;
   if (tid < nrows) {
-    const float* pr = prod_s + tid * stride;
-    for (int b = 0; b < B; ++b) sum = fadd(sum, pr[b]);
+    int b = 0;
+    for (; b + 8 <= B; b += 8) {
+      float p[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) p[k] = prod_s[(b + k) * R + tid];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sum = fadd(sum, p[k]);
+    }
+    for (; b < B; ++b) sum = fadd(sum, prod_s[b * R + tid]);
   }
 
-  // 5. Epilogue.
+  // 6. Epilogue.
   float* out = a.out + (size_t)frame * a.out_rows;
   if (OUT == kOutPlain) {
-    if (tid < nrows) out[row0 + tid] = a.bias ? fadd(a.bias[row0 + tid], sum) : sum;
+    if (tid < nrows) out[row0 + tid] = a.bias ? fadd(rv, sum) : sum;
   } else if (OUT == kOutResidual) {
-    if (tid < nrows) out[row0 + tid] = fadd(sum, a.resid[(size_t)frame * a.out_rows + row0 + tid]);
+    if (tid < nrows) out[row0 + tid] = fadd(sum, rv);
   } else if (OUT == kOutSwiGLU) {
-    // Rows of a group: group_rows/2 gate rows, then the matching up rows
+    // Rows of a group: R/2 gate rows, then the matching up rows
     // (src/FunAsrNet/TensorMath.Elementwise.cs:167-196: g / (1 + exp(-g)) * up).
     if (tid < nrows) sums_s[tid] = sum;
-    __syncthreads();
-    int half = a.group_rows >> 1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    int half = R >> 1;
     if (tid < half) {
       float g = sums_s[tid], u = sums_s[half + tid];
       float silu = fdiv(g, fadd(1.0f, exp_ref(-g)));
@@ -187,14 +241,12 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(GemvArgs a) {
       out[row0 + tid] = sum;
       key = greedy_key(sum, (uint32_t)(row0 + tid));
     }
-    key = wave_max_u64(key);
-    if (tid % kWave == 0) key_s[tid / kWave] = key;
-    __syncthreads();
-    if (tid == 0) {
-      unsigned long long best = key_s[0];
-      for (int w = 1; w < kThreads / kWave; ++w) best = key_s[w] > best ? key_s[w] : best;
-      a.partial_keys[(size_t)frame * gridDim.x + blockIdx.x] = best;
+    // Rows are lanes [0, nrows) of wave 0; the other lanes contribute 0.
+    for (int m = 32; m >= 1; m >>= 1) {
+      unsigned long long o = __shfl_xor(key, m, kWave);
+      key = o > key ? o : key;
     }
+    if (tid == 0) a.partial_keys[(size_t)frame * gridDim.x + blockIdx.x] = key;
   }
 }
 
@@ -306,66 +358,105 @@ __global__ __launch_bounds__(kThreads) void attn_scores_kernel(AttnArgs a) {
   }
 }
 
-// Softmax (TensorMath.SoftmaxAvx.cs:11-58) and the value sum of one query
-// head: out[c] = sum over t of v[t][c] * p[t], in time order from 0f
-// (TensorMath.AttentionAvx.cs:173-224). One thread per channel.
-__global__ __launch_bounds__(128) void attn_values_kernel(AttnArgs a) {
-  extern __shared__ float p_s[];
-  __shared__ float max_s[2];
-  __shared__ double lane_s[8];
-  __shared__ float inv_s;
-  const int head = blockIdx.x, kh = head / (a.heads / a.kv_heads);
-  const int hs = a.head_size;
+// NaN-propagating maximum (Math.Max semantics for the softmax shift).
+__device__ __forceinline__ float nan_max(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return b > a ? b : a;
+}
+
+// Softmax (TensorMath.SoftmaxAvx.cs:11-58) of both query heads of one KV
+// head, then the value sums out[c] = sum over t of v[t][c] * p[t] in time
+// order from 0f (TensorMath.AttentionAvx.cs:173-224). Workgroup
+// (kv head, channel slice of 128/S): the V slice of every position is staged
+// in LDS with all loads issued first, so HBM latency is paid once and
+// overlaps the softmax; one thread then owns one (head, channel) chain.
+// Dynamic LDS: n * 2C bytes of V (fp16) + 2 * n floats of probabilities.
+__global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int slices) {
+  extern __shared__ float dyn_s[];
+  __shared__ float max_s[kThreads / kWave];
+  __shared__ double lane_s[2][8];
+  __shared__ float inv_s[2];
+  const int kh = blockIdx.x / slices, part = blockIdx.x % slices;
+  const int hs = a.head_size, C = hs / slices, c0 = part * C;
   const int n = *a.position + 1;
   const int tid = threadIdx.x;
+  const int group = a.heads / a.kv_heads;
+  float* p_s = dyn_s;                                                     // [2][n]
+  _Float16* v_s = reinterpret_cast<_Float16*>(dyn_s + ((2 * n + 3) & ~3));  // [n][C], 16-byte aligned
+
+  // 1. V slice into LDS: C/8 16-byte pieces per position, batches of 16 per thread.
+  const int pieces = C / 8, total = n * pieces;
+  const _Float16* vbase = a.vcache + (size_t)kh * a.capacity * hs + c0;
+  for (int base = 0; base < total; base += kThreads * 8) {
+    // Branch-free loads (indices clamped in range) keep the batch in registers.
+    int4 reg[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int j = min(base + i * kThreads + tid, total - 1);
+      int t = j / pieces, q = j - t * pieces;
+      reg[i] = *reinterpret_cast<const int4*>(vbase + (size_t)t * hs + q * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int j = base + i * kThreads + tid;
+      if (j < total) *reinterpret_cast<int4*>(v_s + (size_t)j * 8) = reg[i];
+    }
+  }
+
+  // 2. Softmax of the two query heads: threads [0,128) head 0, [128,256) head 1.
+  const int hh = tid >> 7, lt = tid & 127;
+  const int head = kh * group + hh;
   const float* scores = a.scores + (size_t)head * a.capacity;
   float m = -__builtin_inff();
-  for (int t = tid; t < n; t += blockDim.x) {
+  for (int t = lt; t < n; t += 128) {
     float v = scores[t];
-    p_s[t] = v;
-    m = (v != v || m != m) ? (v != v ? v : m) : (v > m ? v : m);
+    p_s[hh * n + t] = v;
+    m = nan_max(m, v);
   }
-  for (int s = 32; s >= 1; s >>= 1) {
-    float o = __shfl_xor(m, s, kWave);
-    m = (o != o || m != m) ? (o != o ? o : m) : (o > m ? o : m);
-  }
-  if (tid % kWave == 0) max_s[tid / kWave] = m;
+  for (int s = 32; s >= 1; s >>= 1) m = nan_max(m, __shfl_xor(m, s, kWave));
+  if ((tid & (kWave - 1)) == 0) max_s[tid / kWave] = m;
   __syncthreads();
-  float mx = max_s[0], m1 = max_s[1];
-  mx = (m1 != m1 || mx != mx) ? (m1 != m1 ? m1 : mx) : (m1 > mx ? m1 : mx);
-  for (int t = tid; t < n; t += blockDim.x) p_s[t] = exp_ref(fadd(p_s[t], -mx));
+  const float mx = nan_max(max_s[hh * 2], max_s[hh * 2 + 1]);
+  for (int t = lt; t < n; t += 128) p_s[hh * n + t] = exp_ref(fadd(p_s[hh * n + t], -mx));
   __syncthreads();
   const int full = n & ~7;
-  if (tid < 8) {
+  if (lt < 8) {
     double l = 0.0;
-    for (int t = tid; t < full; t += 8) l = l + (double)p_s[t];
-    lane_s[tid] = l;
+    for (int t = lt; t < full; t += 8) l = l + (double)p_s[hh * n + t];
+    lane_s[hh][lt] = l;
   }
   __syncthreads();
-  if (tid == 0) {
-    double sum = ((lane_s[0] + lane_s[4]) + (lane_s[1] + lane_s[5])) + ((lane_s[2] + lane_s[6]) + (lane_s[3] + lane_s[7]));
-    for (int t = full; t < n; ++t) sum = sum + (double)p_s[t];
-    inv_s = (float)(1.0 / sum);
+  if (lt == 0) {
+    const double* L = lane_s[hh];
+    double sum = ((L[0] + L[4]) + (L[1] + L[5])) + ((L[2] + L[6]) + (L[3] + L[7]));
+    for (int t = full; t < n; ++t) sum = sum + (double)p_s[hh * n + t];
+    inv_s[hh] = (float)(1.0 / sum);
   }
   __syncthreads();
-  const float inverse = inv_s;
-  for (int t = tid; t < n; t += blockDim.x) p_s[t] = fmul(p_s[t], inverse);
+  const float inverse = inv_s[hh];
+  for (int t = lt; t < n; t += 128) p_s[hh * n + t] = fmul(p_s[hh * n + t], inverse);
   __syncthreads();
-  const _Float16* v = a.vcache + (size_t)kh * a.capacity * hs + tid;
-  float acc = 0.0f;
-  int t = 0;
-  for (; t + 4 <= n; t += 4) {
-    float v0 = from_half(v[(size_t)(t + 0) * hs]);
-    float v1 = from_half(v[(size_t)(t + 1) * hs]);
-    float v2 = from_half(v[(size_t)(t + 2) * hs]);
-    float v3 = from_half(v[(size_t)(t + 3) * hs]);
-    acc = fadd(acc, fmul(v0, p_s[t + 0]));
-    acc = fadd(acc, fmul(v1, p_s[t + 1]));
-    acc = fadd(acc, fmul(v2, p_s[t + 2]));
-    acc = fadd(acc, fmul(v3, p_s[t + 3]));
+
+  // 3. Time-ordered value chains, one per (head, channel) of this slice.
+  if (tid < 2 * C) {
+    const int ch = tid / C == 0 ? tid : tid - C;
+    const int h2 = tid / C;
+    const float* p = p_s + h2 * n;
+    const _Float16* v = v_s + ch;
+    float acc = 0.0f;
+    int t = 0;
+    for (; t + 4 <= n; t += 4) {
+      float v0 = from_half(v[(t + 0) * C]), v1 = from_half(v[(t + 1) * C]);
+      float v2 = from_half(v[(t + 2) * C]), v3 = from_half(v[(t + 3) * C]);
+      acc = fadd(acc, fmul(v0, p[t + 0]));
+      acc = fadd(acc, fmul(v1, p[t + 1]));
+      acc = fadd(acc, fmul(v2, p[t + 2]));
+      acc = fadd(acc, fmul(v3, p[t + 3]));
+    }
+    for (; t < n; ++t) acc = fadd(acc, fmul(from_half(v[t * C]), p[t]));
+    a.out[(size_t)(kh * group + h2) * hs + c0 + ch] = acc;
   }
-  for (; t < n; ++t) acc = fadd(acc, fmul(from_half(v[(size_t)t * hs]), p_s[t]));
-  a.out[head * hs + tid] = acc;
 }
 
 __global__ void advance_kernel(int* position, int frames) {
@@ -461,6 +552,7 @@ int gemv_pairs_per_thread(int group_rows, int K) {
 
 hipError_t launch_gemv(const GemvArgs& a, bool half_scales, int in, int out, int frames, hipStream_t s) {
   if (a.K % 32 != 0 || a.K > kMaxK || a.group_rows < 1 || a.group_rows > 64 || a.rows < 1) return hipErrorInvalidValue;
+  if (a.group_rows * (a.K / 32) > 4 * kThreads) return hipErrorInvalidValue;
   if (out == kOutSwiGLU && (a.group_rows % 2 != 0 || a.rows % a.group_rows != 0)) return hipErrorInvalidValue;
   int ppt = gemv_pairs_per_thread(a.group_rows, a.K);
   if (ppt < 1 || ppt > 4) return hipErrorInvalidValue;
@@ -489,12 +581,33 @@ hipError_t launch_qk_prepare(const QkArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+int attention_slices(int capacity, int head_size) {
+  // LDS per workgroup: n * (2 * head_size / S + 8) bytes must fit 160 KB.
+  for (int slices = 4; slices <= 16; slices *= 2)
+    if ((size_t)capacity * (2 * head_size / slices + 8) + 1024 <= 160 * 1024) return slices;
+  return 0;
+}
+
+size_t attention_lds_bytes(int capacity, int head_size) {
+  int slices = attention_slices(capacity, head_size);
+  return slices ? (size_t)capacity * (2 * head_size / slices + 8) + 16 : 0;
+}
+
+hipError_t prepare_attention(int capacity, int head_size) {
+  size_t bytes = attention_lds_bytes(capacity, head_size);
+  if (!bytes) return hipErrorInvalidValue;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(attn_values_kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
 hipError_t launch_attention(const AttnArgs& a, int score_groups, hipStream_t s) {
-  if (a.head_size != 128) return hipErrorInvalidValue;
+  if (a.head_size != 128 || a.heads != 2 * a.kv_heads) return hipErrorInvalidValue;
+  int slices = attention_slices(a.capacity, a.head_size);
+  if (!slices) return hipErrorInvalidValue;
   attn_scores_kernel<<<dim3(a.heads, score_groups), kThreads, 0, s>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  attn_values_kernel<<<a.heads, 128, sizeof(float) * a.capacity, s>>>(a);
+  attn_values_kernel<<<a.kv_heads * slices, kThreads, attention_lds_bytes(a.capacity, a.head_size), s>>>(a, slices);
   return hipGetLastError();
 }
 
