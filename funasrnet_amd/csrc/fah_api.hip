@@ -187,6 +187,12 @@ struct fah_decoder {
   bool have_logits = false;
   hipGraphExec_t graph_row = nullptr, graph_logits = nullptr, graph_step = nullptr;
   int64_t weight_bytes = 0;
+  // Persistent single-launch step (one workgroup per CU), when the shape has
+  // an instantiation and the device has the CUs for it.
+  bool persistent = false;
+  int blocks = 0;
+  DeviceBuffer layer_table, tx, tqkv, tatt, ta, th, tkeys, epoch, error, timeline;
+  fah::PersistentArgs pargs{};
 };
 
 namespace {
@@ -351,6 +357,18 @@ hipGraphExec_t capture(fah_decoder* d, int kind) {
   return exec;
 }
 
+// The persistent kernel reports a missed exchange (bounded wait expired)
+// through its error word instead of hanging; surface it and clear it.
+void check_step_error(fah_decoder* d) {
+  if (!d->persistent) return;
+  unsigned e = 0;
+  check(hipMemcpy(&e, d->error.ptr, 4, hipMemcpyDeviceToHost), "D2H error word");
+  if (e) {
+    (void)hipMemset(d->error.ptr, 0, 4);
+    throw DeviceError{"persistent decode step: an exchange timed out (workgroups not co-resident?)"};
+  }
+}
+
 // Enqueue one decoder row: kind 0 = layers only, 1 = layers + lm_head +
 // greedy, 2 = embedding of the device token + layers + lm_head + greedy.
 void enqueue_kind(fah_decoder* d, int kind, hipStream_t s) {
@@ -375,6 +393,12 @@ bool use_graphs() {
 }
 
 void run_kind(fah_decoder* d, int kind, hipStream_t s) {
+  if (d->persistent) {
+    fah::PersistentArgs a = d->pargs;
+    a.mode = kind;
+    check(fah::launch_decode_step(a, d->blocks, s), "persistent decode step");
+    return;
+  }
   if (!use_graphs()) {
     enqueue_kind(d, kind, s);
     return;
@@ -695,8 +719,25 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
     int qkv_rows = q_width + 2 * kv_width;
     int qkv_group = pick_group_rows(qkv_rows, k.width, 4, false);
     int o_group = pick_group_rows(k.width, q_width, 4, false);
+    // Persistent path: one workgroup per CU, 256 workgroups.
+    int cus = 0;
+    {
+      hipDeviceProp_t prop;
+      if (hipGetDeviceProperties(&prop, c->device) == hipSuccess) cus = prop.multiProcessorCount;
+    }
+    const char* env = std::getenv("FAH_PERSISTENT");
+    const int nb = 256;
+    d->persistent = !(env && env[0] == '0') && half && cus >= nb &&
+                    fah::persistent_shape_supported(k.width, k.heads, k.kv_heads, k.head_size, k.ffn, nb) &&
+                    k.capacity <= fah::persistent_max_capacity() &&
+                    fah::persistent_blocks_per_cu(k.width) >= 1;
+    d->blocks = nb;
+    // Gate/up storage tiles: R gate rows then the matching R up rows. The
+    // persistent kernel gives each projection workgroup (all but the
+    // attention ones) an even share of the ffn rows, as one tile each.
     int gu_group = pick_group_rows(2 * k.ffn, k.width, 4, true);
     while (gu_group > 2 && (k.ffn % (gu_group / 2) != 0)) gu_group /= 2;
+    const int ng = nb - k.heads;
     int down_group = pick_group_rows(k.width, k.ffn, 4, false);
     for (int l = 0; l < k.layers; ++l) {
       const fah_layer_host& L = layers[l];
@@ -711,10 +752,19 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
       upload_matrix(d->wo[l], {&L.wo}, order, q_width, half, s);
       d->wo[l].group_rows = o_group;
       order.clear();
-      int R = gu_group / 2;
-      for (int t = 0; t < k.ffn / R; ++t) {
-        for (int r = 0; r < R; ++r) order.emplace_back(0, t * R + r);
-        for (int r = 0; r < R; ++r) order.emplace_back(1, t * R + r);
+      if (d->persistent) {
+        const int base = k.ffn / ng, extra = k.ffn % ng;
+        for (int g = 0; g < ng; ++g) {
+          const int r0 = g * base + std::min(g, extra), count = base + (g < extra ? 1 : 0);
+          for (int r = 0; r < count; ++r) order.emplace_back(0, r0 + r);
+          for (int r = 0; r < count; ++r) order.emplace_back(1, r0 + r);
+        }
+      } else {
+        int R = gu_group / 2;
+        for (int t = 0; t < k.ffn / R; ++t) {
+          for (int r = 0; r < R; ++r) order.emplace_back(0, t * R + r);
+          for (int r = 0; r < R; ++r) order.emplace_back(1, t * R + r);
+        }
       }
       upload_matrix(d->gateup[l], {&L.gate, &L.up}, order, k.width, half, s);
       d->gateup[l].group_rows = gu_group;
@@ -779,6 +829,89 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
     check(hipMemsetAsync(d->token.ptr, 0, 16, s), "memset");
     check(hipMemsetAsync(d->position.ptr, 0, 16, s), "memset");
     check(hipMemsetAsync(d->history_count.ptr, 0, 16, s), "memset");
+    if (d->persistent) {
+      std::vector<fah::PersistentLayer> table(k.layers);
+      for (int l = 0; l < k.layers; ++l) {
+        fah::PersistentLayer& t = table[l];
+        t.wqkv = d->qkv[l].q.as<int8_t>();
+        t.sqkv = d->qkv[l].s.as<_Float16>();
+        t.wo = d->wo[l].q.as<int8_t>();
+        t.so = d->wo[l].s.as<_Float16>();
+        t.wgu = d->gateup[l].q.as<int8_t>();
+        t.sgu = d->gateup[l].s.as<_Float16>();
+        t.wd = d->down[l].q.as<int8_t>();
+        t.sd = d->down[l].s.as<_Float16>();
+        t.attn_norm = d->attn_norm[l].as<float>();
+        t.q_norm = d->q_norm[l].as<float>();
+        t.k_norm = d->k_norm[l].as<float>();
+        t.ffn_norm = d->ffn_norm[l].as<float>();
+      }
+      upload(d->layer_table, table.data(), table.size() * sizeof(fah::PersistentLayer), s);
+      auto tagged = [&](DeviceBuffer& b, size_t words) {
+        b.allocate(words * 8);
+        check(hipMemsetAsync(b.ptr, 0, words * 8, s), "memset tagged");
+      };
+      tagged(d->tx, k.width);
+      tagged(d->tqkv, qkv_rows);
+      tagged(d->tatt, q_width);
+      tagged(d->ta, k.width);
+      tagged(d->th, k.ffn);
+      tagged(d->tkeys, 2 * nb);
+      d->epoch.allocate(16);
+      d->error.allocate(16);
+      unsigned one = 1;
+      check(hipMemcpyAsync(d->epoch.ptr, &one, 4, hipMemcpyHostToDevice, s), "epoch");
+      check(hipMemsetAsync(d->error.ptr, 0, 16, s), "memset error");
+      fah::PersistentArgs& a = d->pargs;
+      a.layer_table = d->layer_table.as<fah::PersistentLayer>();
+      a.layers = k.layers;
+      a.embed_q = d->embed.q.as<int8_t>();
+      a.embed_s = d->embed.s.as<_Float16>();
+      a.head_q = head.q.as<int8_t>();
+      a.head_s = head.s.as<_Float16>();
+      a.output_norm = d->output_norm.as<float>();
+      a.rope_cos = d->rope_cos.as<float>();
+      a.rope_sin = d->rope_sin.as<float>();
+      a.kcache = d->kcache.as<_Float16>();
+      a.vcache = d->vcache.as<_Float16>();
+      a.width = k.width;
+      a.heads = k.heads;
+      a.kv_heads = k.kv_heads;
+      a.head_size = k.head_size;
+      a.ffn = k.ffn;
+      a.vocab = k.vocab;
+      a.capacity = k.capacity;
+      a.q_width = q_width;
+      a.kv_width = kv_width;
+      a.eps = k.eps;
+      a.divisor = std::sqrt((float)k.head_size);
+      a.rq = qkv_rows / nb;
+      a.ro = k.width / nb;
+      a.rgu = k.ffn / nb;
+      a.rd = k.width / nb;
+      a.head_chunks = (k.vocab + 31) / 32;
+      a.npre = fah::persistent_max_positions();
+      a.tx = d->tx.as<unsigned long long>();
+      a.tqkv = d->tqkv.as<unsigned long long>();
+      a.tatt = d->tatt.as<unsigned long long>();
+      a.ta = d->ta.as<unsigned long long>();
+      a.th = d->th.as<unsigned long long>();
+      a.tkeys = d->tkeys.as<unsigned long long>();
+      a.x_in = d->x.as<float>();
+      a.position = d->position.as<int>();
+      a.token = d->token.as<int>();
+      a.history = d->history.as<int>();
+      a.history_count = d->history_count.as<int>();
+      a.epoch = d->epoch.as<unsigned>();
+      a.error = d->error.as<unsigned>();
+      a.logits = d->logits.as<float>();
+      const char* tl = std::getenv("FAH_TIMELINE");
+      if (tl && tl[0] == '1') {
+        d->timeline.allocate((size_t)nb * fah::kTimelineEvents * 8);
+        check(hipMemsetAsync(d->timeline.ptr, 0, (size_t)nb * fah::kTimelineEvents * 8, s), "memset timeline");
+        a.timeline = d->timeline.as<unsigned long long>();
+      }
+    }
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
     *out = d.release();
     return FAH_OK;
@@ -835,6 +968,7 @@ int fah_decoder_decode(fah_decoder* d, const float* embeddings, int frames, floa
     if (logits)
       check(hipMemcpyAsync(logits, d->logits.ptr, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, s), "D2H");
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    check_step_error(d);
     d->host_position += frames;
     d->have_logits = logits != nullptr;
     return FAH_OK;
@@ -891,6 +1025,7 @@ int fah_decoder_generate(fah_decoder* d, int steps, int32_t* tokens) {
     if (steps > 0)
       check(hipMemcpyAsync(tokens, d->history.ptr, (size_t)steps * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    check_step_error(d);
     d->host_position += steps;
     return FAH_OK;
   });
@@ -948,5 +1083,46 @@ int fah_decoder_kv_read(fah_decoder* d, int layer, uint16_t* keys, uint16_t* val
 }
 
 int64_t fah_decoder_weight_bytes(const fah_decoder* d) { return d ? d->weight_bytes : 0; }
+
+int fah_decoder_persistent(const fah_decoder* d) { return d && d->persistent ? 1 : 0; }
+
+int fah_decoder_timeline(fah_decoder* d, uint64_t* ticks, int count) {
+  if (!d || !ticks) return fail(FAH_ERROR_ARGUMENT, "decoder/ticks is NULL");
+  if (!d->timeline.ptr) return FAH_DECLINED;
+  return guarded([&] {
+    require(count >= 0 && count <= d->blocks * fah::kTimelineEvents, "invalid timeline size");
+    std::lock_guard<std::mutex> lock(d->context->gate);
+    check(hipSetDevice(d->context->device), "hipSetDevice");
+    check(hipStreamSynchronize(d->context->stream), "sync");
+    check(hipMemcpy(ticks, d->timeline.ptr, (size_t)count * 8, hipMemcpyDeviceToHost), "D2H timeline");
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_trace(fah_decoder* d, int which, float* out, int count) {
+  if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
+  return guarded([&] {
+    const fah_decoder_config& k = d->cfg;
+    const int sizes[5] = {k.width, d->q_width + 2 * d->kv_width, d->q_width, k.width, k.ffn};
+    require(which >= 0 && which < 5 && out && count >= 0 && count <= sizes[which], "invalid trace request");
+    std::lock_guard<std::mutex> lock(d->context->gate);
+    check(hipSetDevice(d->context->device), "hipSetDevice");
+    hipStream_t s = d->context->stream;
+    check(hipStreamSynchronize(s), "sync");
+    if (d->persistent) {
+      DeviceBuffer* tagged[5] = {&d->tx, &d->tqkv, &d->tatt, &d->ta, &d->th};
+      std::vector<unsigned long long> words(count);
+      check(hipMemcpy(words.data(), tagged[which]->ptr, (size_t)count * 8, hipMemcpyDeviceToHost), "D2H trace");
+      for (int i = 0; i < count; ++i) {
+        uint32_t bits = (uint32_t)words[i];
+        std::memcpy(&out[i], &bits, 4);
+      }
+    } else {
+      DeviceBuffer* plain[5] = {&d->x, &d->qkv_out, &d->attn, &d->a, &d->h};
+      check(hipMemcpy(out, plain[which]->ptr, (size_t)count * 4, hipMemcpyDeviceToHost), "D2H trace");
+    }
+    return FAH_OK;
+  });
+}
 
 }  // extern "C"

@@ -52,6 +52,61 @@ struct AttnArgs {
   float divisor;           // sqrtf(head_size)
 };
 
+struct PersistentLayer {
+  const int8_t* wqkv;
+  const _Float16* sqkv;
+  const int8_t* wo;
+  const _Float16* so;
+  const int8_t* wgu;   // tiles of rgu gate rows then rgu up rows
+  const _Float16* sgu;
+  const int8_t* wd;
+  const _Float16* sd;
+  const float* attn_norm;
+  const float* q_norm;
+  const float* k_norm;
+  const float* ffn_norm;
+};
+
+struct PersistentArgs {
+  const PersistentLayer* layer_table;  // device array [layers]
+  int layers;
+  const int8_t* embed_q;
+  const _Float16* embed_s;
+  const int8_t* head_q;
+  const _Float16* head_s;
+  const float* output_norm;
+  const float* rope_cos;
+  const float* rope_sin;
+  _Float16* kcache;  // [layers][kv_heads][capacity][head_size]
+  _Float16* vcache;
+  int width, heads, kv_heads, head_size, ffn, vocab, capacity;
+  int q_width, kv_width;
+  float eps, divisor;
+  int rq, ro, rgu, rd;  // rows per workgroup: qkv, o, gate (and up), down
+  int head_chunks;      // lm_head chunks of 32 rows
+  int npre;             // K/V positions staged in LDS
+  unsigned long long *tx, *tqkv, *tatt, *ta, *th, *tkeys;  // tagged exchange words
+  const float* x_in;    // modes 0/1: the input row
+  int mode;             // 0 layers, 1 layers + lm_head + greedy, 2 embed token + 1
+  int* position;
+  int* token;
+  int* history;
+  int* history_count;
+  unsigned* epoch;
+  unsigned* error;
+  float* logits;
+  unsigned long long* timeline;  // optional [2][kTimelineEvents] s_memrealtime stamps
+};
+
+constexpr int kTimelineEvents = 480;
+
+bool persistent_shape_supported(int width, int heads, int kv_heads, int head_size, int ffn, int blocks);
+hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s);
+int persistent_max_positions();
+int persistent_max_capacity();
+int persistent_threads();
+int persistent_blocks_per_cu(int width);
+
 int gemv_max_k();
 int gemv_pairs_per_thread(int group_rows, int K);
 hipError_t launch_gemv(const GemvArgs& a, bool half_scales, int in, int out, int frames, hipStream_t s);

@@ -1,0 +1,915 @@
+// Persistent decode step: the whole Qwen3 decoder row (28 layers + lm_head +
+// greedy) in one launch of one workgroup per CU.
+//
+// Every workgroup owns a fixed slice of rows of every projection. A layer is
+// five phases -- qkv, attention, o, gate/up, down -- separated by all-to-all
+// exchanges of the activation vector through global memory. Each value is
+// published as a 64-bit word (generation << 32 | float bits) with one
+// relaxed device-scope store, so a consumer sees value and readiness in the
+// same load and a phase boundary costs one memory round trip.
+//
+// Roles inside a workgroup (4 waves):
+//  * wave 0 is the memory wave: it gathers the next phase's input and, in
+//    the same batch of direct global->LDS loads, the small per-layer
+//    constants (norm weights, RoPE row) and the K/V rows of earlier
+//    positions for the next attention. Its waits drain only its own loads.
+//  * waves 1-3 are the compute waves: they hold the weight slices of the
+//    next two phases in registers (issued a phase ahead, a fixed number of
+//    loads per phase so that every wait counts exactly the loads it needs),
+//    and issue no other global load in the steady state.
+// The arithmetic of every phase is the one of the multi-kernel path
+// (bit-identical GEMV order, exact softmax and time-ordered value sums).
+//
+// Every wait is bounded: a missing generation sets the error word and the
+// workgroup leaves, so a broken launch ends instead of hanging.
+#include "fah_device.h"
+#include "fah_internal.h"
+
+namespace fah {
+namespace {
+
+constexpr int kPT = 256;                 // threads per workgroup (4 waves: 512 VGPRs each)
+constexpr int kComp = kPT - kWave;       // compute threads (waves 1..3)
+constexpr int kSlotPairs = 4;            // (row, block) pairs per compute lane per phase
+constexpr int kActFloats = 4096;         // largest phase input (ffn <= 4096)
+constexpr int kTagWords = kActFloats * 3 / 4;  // gathered words held in LDS
+constexpr int kProdFloats = 1024;        // (row, block) products of one phase
+constexpr int kKvBytes = 121 * 1024;     // K/V staging: 512 B per position
+constexpr int kProbOffset = 4 * 128;     // attention probabilities after q/k/v in the tag area
+constexpr long kSpinLimit = 1L << 21;    // bounded polls per gather (~1-2 s)
+using u64 = unsigned long long;
+using lds_ptr = __attribute__((address_space(3))) void*;
+
+__device__ __forceinline__ void lds_barrier_p() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ void tag_store(u64* p, uint32_t gen, float v) {
+  __hip_atomic_store(p, ((u64)gen << 32) | (u64)f2u(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void tag_store_bits(u64* p, uint32_t gen, uint32_t bits) {
+  __hip_atomic_store(p, ((u64)gen << 32) | (u64)bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned error_load(const unsigned* e) {
+  return __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Phase timeline (100 MHz s_memrealtime) of every workgroup, when the
+// caller asked for one.
+__device__ __forceinline__ void stamp(unsigned long long* timeline, int slot, int event) {
+  if (timeline && event < kTimelineEvents) timeline[slot * kTimelineEvents + event] = __builtin_amdgcn_s_memrealtime();
+}
+
+// Wave-level direct global->LDS copy of `bytes` (a multiple of 16): lane i of
+// instruction c moves bytes [1024c + 16i, +16).
+__device__ __forceinline__ void dma(const void* src, void* lds, int bytes) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int c = 0; c < bytes; c += 1024)
+    if (c + 16 * lane < bytes)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(src) + c + 16 * lane,
+                                       (lds_ptr)(reinterpret_cast<char*>(lds) + c), 16, 0, 0);
+}
+
+// K/V rows [t0, t1) of one kv head into kv: position t at byte 512(t - t0),
+// K 256 B then V 256 B; one instruction moves two positions (lanes: K t,
+// V t, K t+1, V t+1). The 16-byte pieces of a K row are stored XOR-swizzled
+// by (t & 15), so that 16 lanes reading piece i of 16 consecutive rows hit
+// 16 different bank groups; V rows stay in order (read one row at a time).
+__device__ __forceinline__ void dma_kv(const _Float16* kb, const _Float16* vb, int t0, int t1, char* kv, int first = 0,
+                                       int stride = 1) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int m = first; t0 + 2 * m < t1; m += stride) {
+    const int t = t0 + 2 * m + (lane >> 5);
+    if (t < t1) {
+      const bool v = (lane >> 4) & 1;
+      const int piece = v ? (lane & 15) : ((lane & 15) ^ (t & 15));
+      const _Float16* src = (v ? vb : kb) + (size_t)t * 128 + piece * 8;
+      __builtin_amdgcn_global_load_lds(src, (lds_ptr)(kv + (size_t)m * 1024), 16, 0, 0);
+    }
+  }
+}
+
+struct NoPre {
+  __device__ void operator()() const {}
+};
+
+// Wave 0 gathers tagged words into the LDS staging area `tag` (one u64 per
+// value; consumers read the low 32 bits). Ranges are multiples of 128 words
+// (chunks); each chunk is one direct global->LDS load of 16 bytes per lane.
+// `pre` issues the plain constant copies once, before the first poll, so
+// they share its wait. Chunks whose tags do not all carry `gen` are issued
+// again until every chunk is current. Returns false after a timeout or when
+// another workgroup reported an error.
+template <class Pre>
+__device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int o1, const u64* s2, int n2, int o2,
+                       uint32_t gen, u64* tag, unsigned* error, Pre pre) {
+  const int lane = threadIdx.x;
+  pre();
+  const int c0 = n0 >> 7, c01 = c0 + (n1 >> 7), total = c01 + (n2 >> 7);
+  u64 pending = total >= 64 ? ~0ull : ((1ull << total) - 1ull);
+  auto locate = [&](int k, const u64*& src, int& off) {
+    if (k < c0) {
+      src = s0 + (k << 7);
+      off = o0 + (k << 7);
+    } else if (k < c01) {
+      src = s1 + ((k - c0) << 7);
+      off = o1 + ((k - c0) << 7);
+    } else {
+      src = s2 + ((k - c01) << 7);
+      off = o2 + ((k - c01) << 7);
+    }
+  };
+  long spin = 0;
+  // Poll one chunk (the last) until it is current before reading them all:
+  // consumers that arrive early then cost one 1 KB load per round trip
+  // instead of the whole vector.
+  {
+    const u64* src;
+    int off;
+    locate(total - 1, src, off);
+    for (;; ++spin) {
+      __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(tag + off), 16, 0, 16);
+      __builtin_amdgcn_s_waitcnt(0);
+      const uint4 t = *reinterpret_cast<const uint4*>(tag + off + 2 * lane);
+      if (__all(t.y == gen && t.w == gen)) break;
+      if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
+        if (lane == 0) __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // Drained here so that no store is pending where the waves rejoin.
+        __builtin_amdgcn_s_waitcnt(0);
+        return false;
+      }
+    }
+    pending &= ~(1ull << (total - 1));
+  }
+  for (;; ++spin) {
+    if (!pending) return true;
+    for (u64 m = pending; m; m &= m - 1) {
+      const u64* src;
+      int off;
+      locate(__builtin_ctzll(m), src, off);
+      // aux 16 = sc1: device-coherent read, as relaxed agent-scope atomic loads use.
+      __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(tag + off), 16, 0, 16);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    for (u64 m = pending; m; m &= m - 1) {
+      const int k = __builtin_ctzll(m);
+      const u64* src;
+      int off;
+      locate(k, src, off);
+      const uint4 t = *reinterpret_cast<const uint4*>(tag + off + 2 * lane);
+      if (__all(t.y == gen && t.w == gen)) pending &= ~(1ull << k);
+    }
+    if (!pending) return true;
+    if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
+      if (lane == 0) __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // Drained here so that no store is pending where the waves rejoin.
+      __builtin_amdgcn_s_waitcnt(0);
+      return false;
+    }
+  }
+}
+
+template <class Pre>
+__device__ __forceinline__ bool gather1(const u64* src, int count, uint32_t gen, u64* tag, unsigned* error, Pre pre) {
+  return gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, gen, tag, error, pre);
+}
+
+__device__ __forceinline__ float tag_value(const u64* tag, int i) { return u2f((uint32_t)tag[i]); }
+
+// A compute lane's share of one weight slice: P (row, block) pairs, each 32
+// int8 weights and the block's F16 scale.
+template <int P>
+struct Slot {
+  int4 w[P][2];
+  _Float16 s[P];
+};
+
+// Load this compute lane's pairs j = ct + kComp*i (i < ceil(NP/kComp)) of a
+// slice of `valid` pairs. Lanes past the end re-read the last pair, so every
+// lane issues the same, compile-time number of loads per slice.
+template <int NP, int P>
+__device__ __forceinline__ void load_slot(Slot<P>& sl, const int8_t* w, const _Float16* s, int ct, int valid) {
+  constexpr int kI = (NP + kComp - 1) / kComp;
+  static_assert(kI <= P, "slot capacity");
+#pragma unroll
+  for (int i = 0; i < kI; ++i) {
+    int j = ct + i * kComp;
+    j = j < valid ? j : valid - 1;
+    const int4* p = reinterpret_cast<const int4*>(w + (size_t)j * 32);
+    sl.w[i][0] = p[0];
+    sl.w[i][1] = p[1];
+    sl.s[i] = s[j];
+  }
+}
+
+__device__ __forceinline__ int dot32(const int4& w0, const int4& w1, const int* xq) {
+  const int4* xp = reinterpret_cast<const int4*>(xq);
+  int4 x0 = xp[0], x1 = xp[1];
+  int d = 0;
+  d = __builtin_amdgcn_sdot4(w0.x, x0.x, d, false);
+  d = __builtin_amdgcn_sdot4(w0.y, x0.y, d, false);
+  d = __builtin_amdgcn_sdot4(w0.z, x0.z, d, false);
+  d = __builtin_amdgcn_sdot4(w0.w, x0.w, d, false);
+  d = __builtin_amdgcn_sdot4(w1.x, x1.x, d, false);
+  d = __builtin_amdgcn_sdot4(w1.y, x1.y, d, false);
+  d = __builtin_amdgcn_sdot4(w1.z, x1.z, d, false);
+  d = __builtin_amdgcn_sdot4(w1.w, x1.w, d, false);
+  return d;
+}
+
+// Scaled block products of a slot into prod[b * R + r] (pairs j < valid;
+// pair j is row j / B, block j % B of the slice).
+template <int NP, int B, int P>
+__device__ __forceinline__ void slot_products(const Slot<P>& sl, int ct, const int* xq, const float* xs, float* prod,
+                                              int R, int valid) {
+  constexpr int kI = (NP + kComp - 1) / kComp;
+#pragma unroll
+  for (int i = 0; i < kI; ++i) {
+    const int j = ct + i * kComp;
+    if (j < valid) {
+      const int r = j / B, b = j - r * B;
+      const int d = dot32(sl.w[i][0], sl.w[i][1], xq + b * 8);
+      prod[b * R + r] = fmul(fmul((float)d, (float)sl.s[i]), xs[b]);
+    }
+  }
+}
+
+// Rows [r0, r0 + count) of R rows split as evenly as possible over NG
+// workgroups (the first R % NG take one more).
+struct Rows {
+  int r0, count;
+};
+template <int R, int NG>
+__device__ __forceinline__ Rows split_rows(int g) {
+  constexpr int base = R / NG, extra = R % NG;
+  return {g * base + (g < extra ? g : extra), base + (g < extra ? 1 : 0)};
+}
+
+// Ordered block sum from 0f for row r (TensorMath.QuantizedRowsAvx.cs:27-58).
+__device__ __forceinline__ float ordered_sum(const float* prod, int B, int R, int r) {
+  float sum = 0.0f;
+  int b = 0;
+  for (; b + 8 <= B; b += 8) {
+    float p[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) p[k] = prod[(b + k) * R + r];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sum = fadd(sum, p[k]);
+  }
+  for (; b < B; ++b) sum = fadd(sum, prod[b * R + r]);
+  return sum;
+}
+
+// Block-wide double sum (all threads of the workgroup).
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+  v = wave_sum_double(v);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+  lds_barrier_p();
+  double t = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPT / kWave; ++i) t += red[i];
+  lds_barrier_p();
+  return t;
+}
+
+__device__ __forceinline__ float4 tag_float4(const u64* tag, int e) {
+  const uint4 a = *reinterpret_cast<const uint4*>(tag + e);
+  const uint4 b = *reinterpret_cast<const uint4*>(tag + e + 2);
+  return make_float4(u2f(a.x), u2f(a.z), u2f(b.x), u2f(b.z));
+}
+
+// RMSNorm (optional, weights in LDS) + activation quantisation of act[0, K)
+// into xq/xs, all threads. Same arithmetic as the multi-kernel GEMV prologue.
+__device__ __forceinline__ void quantize_input(const u64* act, int K, const float* norm_w, float eps, bool norm,
+                                               int* xq, float* xs, double* red) {
+  float inverse = 1.0f;
+  if (norm) {
+    double sq = 0.0;
+    for (int e = 4 * threadIdx.x; e < K; e += 4 * kPT) {
+      float4 v = tag_float4(act, e);
+      sq += (double)v.x * (double)v.x + (double)v.y * (double)v.y;
+      sq += (double)v.z * (double)v.z + (double)v.w * (double)v.w;
+    }
+    double total = block_sum_d(sq, red);
+    float mean = (float)(total / (double)K);
+    inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
+  }
+  for (int e = 4 * threadIdx.x; e < K; e += 4 * kPT) {
+    float4 v = tag_float4(act, e);
+    if (norm) {
+      float4 w = *reinterpret_cast<const float4*>(norm_w + e);
+      v.x = fmul(fmul(v.x, inverse), w.x);
+      v.y = fmul(fmul(v.y, inverse), w.y);
+      v.z = fmul(fmul(v.z, inverse), w.z);
+      v.w = fmul(fmul(v.w, inverse), w.w);
+    }
+    uint32_t m = f2u(v.x) & 0x7fffffffu, t;
+    t = f2u(v.y) & 0x7fffffffu; m = t > m ? t : m;
+    t = f2u(v.z) & 0x7fffffffu; m = t > m ? t : m;
+    t = f2u(v.w) & 0x7fffffffu; m = t > m ? t : m;
+#pragma unroll
+    for (int s = 1; s < 8; s <<= 1) {
+      uint32_t o = __shfl_xor(m, s, 8);
+      m = o > m ? o : m;
+    }
+    float inv;
+    float d = block_scale(m, &inv);
+    xq[e >> 2] = (int)((uint32_t)(uint8_t)quantize_value(v.x, inv) | ((uint32_t)(uint8_t)quantize_value(v.y, inv) << 8) |
+                       ((uint32_t)(uint8_t)quantize_value(v.z, inv) << 16) |
+                       ((uint32_t)(uint8_t)quantize_value(v.w, inv) << 24));
+    if ((threadIdx.x & 7) == 0) xs[e >> 5] = d;
+  }
+}
+
+// One 16-byte piece of a K row (8 F16 channels 8i..8i+7) into the eight
+// channel-strided accumulators: acc[j] += q[8i+j] * k[8i+j].
+__device__ __forceinline__ void score8(float* acc, const uint4& kk, const float* q) {
+  const float4 q0 = *reinterpret_cast<const float4*>(q);
+  const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
+  const uint32_t w[4] = {kk.x, kk.y, kk.z, kk.w};
+  float k[8];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    k[2 * m] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu)));
+    k[2 * m + 1] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16)));
+  }
+  acc[0] = fadd(acc[0], fmul(q0.x, k[0]));
+  acc[1] = fadd(acc[1], fmul(q0.y, k[1]));
+  acc[2] = fadd(acc[2], fmul(q0.z, k[2]));
+  acc[3] = fadd(acc[3], fmul(q0.w, k[3]));
+  acc[4] = fadd(acc[4], fmul(q1.x, k[4]));
+  acc[5] = fadd(acc[5], fmul(q1.y, k[5]));
+  acc[6] = fadd(acc[6], fmul(q1.z, k[6]));
+  acc[7] = fadd(acc[7], fmul(q1.w, k[7]));
+}
+
+__device__ __forceinline__ float nan_max_p(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return b > a ? b : a;
+}
+
+}  // namespace
+
+// Shape-specialised: W hidden width, HQ/HKV query/kv heads (head size 128),
+// FF feed-forward width, NBK workgroups. Workgroups [0, HQ) run attention,
+// one query head each; the other NBK - HQ run the projections, each on an
+// even share of the rows of every matrix. All of them run the lm_head.
+template <int W, int HQ, int HKV, int FF, int NBK>
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_step_kernel(PersistentArgs a) {
+  constexpr int HS = 128, QW = HQ * HS, KVW = HKV * HS, QKVR = QW + 2 * KVW;
+  constexpr int B1 = W / 32, Bq = QW / 32, Bf = FF / 32;
+  constexpr int NB = NBK, NG = NBK - HQ;
+  // Largest per-workgroup slices (rows) and their (row, block) pairs.
+  constexpr int RQ = (QKVR + NG - 1) / NG, RO = (W + NG - 1) / NG, RGU = (FF + NG - 1) / NG;
+  constexpr int NPQ = RQ * B1, NPO = RO * Bq, NPG = 2 * RGU * B1, NPD = RO * Bf;
+  constexpr int PA = (NPQ > NPG ? NPQ : NPG) / kComp + 1;  // slot A: qkv, gate/up
+  constexpr int PB = (NPO > NPD ? NPO : NPD) / kComp + 1;  // slot B: o, down
+  constexpr int NPH = kSlotPairs * kComp, HR = NPH / B1;  // lm_head: pairs and rows per chunk
+  static_assert(RQ <= 64 && 2 * RGU <= 64 && RO <= 64 && HR <= 64 && HR * B1 == NPH, "row lanes");
+  static_assert(PA <= 5 && PB <= 4, "slot registers");
+  static_assert(FF <= kActFloats && QW <= kActFloats && W <= 1024 && NPQ <= kProdFloats && NPG <= kProdFloats &&
+                    NPO <= kProdFloats && NPD <= kProdFloats,
+                "LDS sizing");
+  static_assert(W % kPT == 0 && 2 * NPH * 4 <= kKvBytes, "layer-0 input and lm_head product buffers");
+  static_assert(HQ < NB && HQ == 2 * HKV, "paired heads, one attention workgroup per query head");
+  __shared__ __attribute__((aligned(16))) u64 tag_s[kTagWords];  // gathered inputs (low 32 bits)
+  __shared__ __attribute__((aligned(16))) float norm_s[1024];   // norm weights; attention: q/k norm, cos, sin
+  __shared__ __attribute__((aligned(16))) int xq_s[kActFloats / 4];
+  __shared__ float xs_s[kActFloats / 32];
+  __shared__ float prod_s[kProdFloats];
+  __shared__ float row_s[2][64];  // residual rows: [0] x, [1] a
+  __shared__ double red_s[kPT / kWave];
+  __shared__ int flag_s;
+  __shared__ __attribute__((aligned(16))) float cur_s[3][128];  // attention: q, k, v of the current position
+  __shared__ float tmax_s[kPT / kWave];
+  __shared__ double lane_s[8];
+  __shared__ float inv_s;
+  __shared__ __attribute__((aligned(16))) char kv_s[kKvBytes];  // [t][K 128 | V 128] fp16; lm_head products
+
+  const int w = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int ct = tid - kWave;  // compute-lane index (negative in wave 0)
+  const int L = a.layers;
+  const int pos = *a.position;
+  const uint32_t gen0 = *a.epoch * (uint32_t)(5 * L + 2) + 1u;
+  const int chunks = (a.vocab + HR - 1) / HR;
+  auto gen = [&](int l, int p) { return gen0 + (uint32_t)(5 * l + p); };
+  // The layer table is written before the launch and only read here: the
+  // constant address space turns its reads into scalar loads, which do not
+  // queue behind the vector loads of the weight slices.
+  const __attribute__((address_space(4))) PersistentLayer* LT =
+      (const __attribute__((address_space(4))) PersistentLayer*)a.layer_table;
+
+  // Phase timeline of every workgroup: wave 0 keeps the time its last gather
+  // completed and writes it, with the time the phase output was stored, just
+  // before its next gather (whose wait drains both stores).
+  unsigned long long* tl = a.timeline ? a.timeline + (size_t)w * kTimelineEvents : nullptr;
+  u64 t_in = __builtin_amdgcn_s_memrealtime();
+  u64 t_sub[3] = {0, 0, 0};  // sub-phase times, written with the next stamps
+  auto sub = [&](int i) { t_sub[i] = __builtin_amdgcn_s_memrealtime(); };
+  auto stamps = [&](int in_event, int out_event, int sub_event = -1, int nsub = 0) {
+    if (tl && lane == 0) {
+      tl[in_event] = t_in;
+      tl[out_event] = __builtin_amdgcn_s_memrealtime();
+      for (int i = 0; i < nsub; ++i) tl[sub_event + i] = t_sub[i];
+    }
+  };
+
+  if (w < HQ) {
+    // ======================= attention workgroup ================================
+    constexpr int group = HQ / HKV;
+    const int kh = w / group;
+    const int n = pos + 1;
+    const int npre = min(pos, a.npre);
+    // Positions past the K/V stage go to the free end of the gather area
+    // (after the probabilities).
+    const int ovf_at = (kProbOffset * 8 + 4 * n + 15) & ~15;
+    const int nlds = min(pos, npre + max(0, (kTagWords * 8 - ovf_at) / 512));
+    char* ovf_s = reinterpret_cast<char*>(tag_s) + ovf_at;
+    float* p_s = reinterpret_cast<float*>(tag_s + kProbOffset);  // attention probabilities after q/k/v
+    const size_t kv_layer = (size_t)HKV * a.capacity * HS;
+    const size_t kv_head = (size_t)kh * a.capacity * HS;
+    auto kbase = [&](int l) { return a.kcache + kv_layer * l + kv_head; };
+    auto vbase = [&](int l) { return a.vcache + kv_layer * l + kv_head; };
+    // Every wave stages its share of layer l's K/V rows (earlier positions)
+    // and waits for them; readers are behind the next barrier.
+    auto stage_kv = [&](int l) {
+      dma_kv(kbase(l), vbase(l), 0, npre, kv_s, wave, kPT / kWave);
+      dma_kv(kbase(l), vbase(l), npre, nlds, ovf_s, wave, kPT / kWave);
+      __builtin_amdgcn_s_waitcnt(0);
+    };
+    if (a.mode == 2 && w == 0 && tid == 0) {
+      int token = *a.token;
+      if (token < 0 || token >= a.vocab) token = 0;
+      const int hcount = *a.history_count;
+      a.history[hcount] = token;
+      *a.history_count = hcount + 1;
+    }
+    stage_kv(0);
+
+    for (int l = 0; l < L; ++l) {
+      const auto& Ly = LT[l];
+      const int e = 16 * l + 1;  // timeline events of this layer
+      if (wave == 0) {
+        const int qo = w * HS, ko = QW + kh * HS, vo = QW + KVW + kh * HS;
+        const bool ok =
+            gather(a.tqkv + qo, HS, 0, a.tqkv + ko, HS, HS, a.tqkv + vo, HS, 2 * HS, gen(l, 1), tag_s, a.error, [&] {
+              dma(Ly.q_norm, norm_s, HS * 4);
+              dma(Ly.k_norm, norm_s + HS, HS * 4);
+              dma(a.rope_cos + (size_t)pos * (HS / 2), norm_s + 2 * HS, HS * 2);
+              dma(a.rope_sin + (size_t)pos * (HS / 2), norm_s + 2 * HS + HS / 2, HS * 2);
+            });
+        t_in = __builtin_amdgcn_s_memrealtime();
+        flag_s = ok ? 1 : 0;
+      }
+      lds_barrier_p();
+      if (!flag_s) return;
+
+      // Norm + rope of q (threads 0-127) and k (128-255); v rounded to F16.
+      {
+        const int part = tid >> 7, c = tid & 127;
+        float v = tag_value(tag_s, part * HS + c);
+        double sq = wave_sum_double((double)v * (double)v);
+        if (lane == 0) red_s[wave] = sq;
+        lds_barrier_p();
+        float mean = (float)((red_s[2 * part] + red_s[2 * part + 1]) / (double)HS);
+        float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, a.eps)));
+        cur_s[part][c] = fmul(fmul(v, inverse), norm_s[part * HS + c]);
+        if (tid < HS) cur_s[2][tid] = from_half(to_half(tag_value(tag_s, 2 * HS + tid)));
+      }
+      lds_barrier_p();
+      float rot = 0.0f;
+      {
+        const int part = tid >> 7, c = tid & 127, half = HS >> 1;
+        const float* cosine = norm_s + 2 * HS;
+        const float* sine = norm_s + 2 * HS + half;
+        if (c < half) rot = fadd(fmul(cur_s[part][c], cosine[c]), -fmul(cur_s[part][c + half], sine[c]));
+        else rot = fadd(fmul(cur_s[part][c - half], sine[c - half]), fmul(cur_s[part][c], cosine[c - half]));
+      }
+      lds_barrier_p();
+      // This position's K row, F16 and swizzled like the staged rows.
+      char* kcur = reinterpret_cast<char*>(norm_s + 512);
+      if (tid < 128) {
+        cur_s[0][tid] = rot;
+      } else {
+        const int c = tid - 128;
+        const _Float16 k16 = to_half(rot);
+        cur_s[1][c] = from_half(k16);
+        reinterpret_cast<_Float16*>(kcur + (((c >> 3) ^ (pos & 15)) << 4))[c & 7] = k16;
+      }
+      lds_barrier_p();
+      sub(0);
+
+      // Scores, one position per lane: eight accumulators over channels
+      // j, j+8, ..., then the pairwise tree (AttentionAvx.cs:74-160).
+      for (int t = tid; t < n; t += kPT) {
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (t < nlds || t == pos) {
+          const char* row = t == pos ? kcur : (t < npre ? kv_s + (size_t)t * 512 : ovf_s + (size_t)(t - npre) * 512);
+          const int x = (t & 15) << 4;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const uint4 kk = *reinterpret_cast<const uint4*>(row + ((i << 4) ^ x));
+            score8(acc, kk, &cur_s[0][8 * i]);
+          }
+        } else {
+          const uint4* g = reinterpret_cast<const uint4*>(kbase(l) + (size_t)t * HS);
+#pragma unroll
+          for (int i0 = 0; i0 < 16; i0 += 4) {
+            uint4 kk[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kk[i] = g[i0 + i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) score8(acc, kk[i], &cur_s[0][8 * (i0 + i)]);
+          }
+        }
+        const float s = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])),
+                             fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
+        p_s[t] = fdiv(s, a.divisor);
+      }
+      lds_barrier_p();
+      sub(1);
+      // Softmax (TensorMath.SoftmaxAvx.cs:11-58).
+      float m = -__builtin_inff();
+      for (int t = tid; t < n; t += kPT) m = nan_max_p(m, p_s[t]);
+      for (int s = 32; s >= 1; s >>= 1) m = nan_max_p(m, __shfl_xor(m, s, kWave));
+      if (lane == 0) tmax_s[wave] = m;
+      lds_barrier_p();
+      float mx = tmax_s[0];
+#pragma unroll
+      for (int i = 1; i < kPT / kWave; ++i) mx = nan_max_p(mx, tmax_s[i]);
+      for (int t = tid; t < n; t += kPT) p_s[t] = exp_ref(fadd(p_s[t], -mx));
+      lds_barrier_p();
+      const int full = n & ~7;
+      if (tid < 8) {
+        // Lane j: p[j] + p[j+8] + ... in order, in double.
+        double acc = 0.0;
+        int t = tid;
+        for (; t + 56 < full; t += 64) {
+          float v[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) v[k] = p_s[t + 8 * k];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) acc = acc + (double)v[k];
+        }
+        for (; t < full; t += 8) acc = acc + (double)p_s[t];
+        lane_s[tid] = acc;
+      }
+      lds_barrier_p();
+      if (tid == 0) {
+        double sum = ((lane_s[0] + lane_s[4]) + (lane_s[1] + lane_s[5])) + ((lane_s[2] + lane_s[6]) + (lane_s[3] + lane_s[7]));
+        for (int t = full; t < n; ++t) sum = sum + (double)p_s[t];
+        inv_s = (float)(1.0 / sum);
+      }
+      lds_barrier_p();
+      const float inverse = inv_s;
+      for (int t = tid; t < n; t += kPT) p_s[t] = fmul(p_s[t], inverse);
+      lds_barrier_p();
+      sub(2);
+      // Time-ordered value sums, one lane per channel (AttentionAvx.cs:173-224);
+      // blocks of 16 positions load their values before the chain uses them.
+      if (tid < HS) {
+        const int c = tid;
+        float acc = 0.0f;
+        auto chain16 = [&](const char* vrow, int t) {  // vrow: V row of position t, this channel
+          // Two positions per register (low half t+2k, high half t+2k+1), all
+          // sixteen loads issued before the chain consumes them.
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          h2 v[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            v[k].x = *reinterpret_cast<const _Float16*>(vrow + 1024 * k);
+            v[k].y = *reinterpret_cast<const _Float16*>(vrow + 1024 * k + 512);
+          }
+          float p[16];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float4 q = *reinterpret_cast<const float4*>(p_s + t + 4 * k);
+            p[4 * k] = q.x;
+            p[4 * k + 1] = q.y;
+            p[4 * k + 2] = q.z;
+            p[4 * k + 3] = q.w;
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            acc = fadd(acc, fmul(from_half(v[k].x), p[2 * k]));
+            acc = fadd(acc, fmul(from_half(v[k].y), p[2 * k + 1]));
+          }
+        };
+        // V of position t: kv_s + 512 t (t < npre), ovf_s + 512 (t - npre) after.
+        auto vrow = [&](int t) {
+          return (t < npre ? kv_s + (size_t)t * 512 : ovf_s + (size_t)(t - npre) * 512) + 256 + 2 * c;
+        };
+        auto step = [&](int t) { acc = fadd(acc, fmul(from_half(*reinterpret_cast<const _Float16*>(vrow(t))), p_s[t])); };
+        int t = 0;
+        for (; t + 16 <= npre; t += 16) chain16(vrow(t), t);
+        for (; t < npre; ++t) step(t);
+        for (; t < nlds && (t & 3) != 0; ++t) step(t);
+        for (; t + 16 <= nlds; t += 16) chain16(vrow(t), t);
+        for (; t < nlds; ++t) step(t);
+        const _Float16* vglob = vbase(l) + c;
+        for (; t + 8 <= pos; t += 8) {
+          float x[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) x[k] = from_half(vglob[(size_t)(t + k) * HS]);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) acc = fadd(acc, fmul(x[k], p_s[t + k]));
+        }
+        for (; t < pos; ++t) acc = fadd(acc, fmul(from_half(vglob[(size_t)t * HS]), p_s[t]));
+        acc = fadd(acc, fmul(cur_s[2][c], p_s[pos]));
+        cur_s[0][c] = acc;
+      }
+      lds_barrier_p();
+      if (wave == 0) {
+        tag_store(a.tatt + w * HS + lane, gen(l, 2), cur_s[0][lane]);
+        tag_store(a.tatt + w * HS + kWave + lane, gen(l, 2), cur_s[0][kWave + lane]);
+        if (w % group == 0) {
+          // The first query head of the pair writes this position's K/V row
+          // (four channels per lane).
+          const int c = 4 * (lane & 31);
+          const float* src = lane < 32 ? cur_s[1] : cur_s[2];
+          _Float16* dst = (lane < 32 ? kbase(l) : vbase(l)) + (size_t)pos * HS + c;
+          typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+          half4 h = {to_half(src[c]), to_half(src[c + 1]), to_half(src[c + 2]), to_half(src[c + 3])};
+          *reinterpret_cast<half4*>(dst) = h;
+        }
+        stamps(e + 3, e + 7, e + 4, 3);
+      }
+      // Stage the next layer's K/V while the projections run.
+      if (l + 1 < L) stage_kv(l + 1);
+    }
+    // lm_head input: the last layer's output with output_norm.
+    if (wave == 0) {
+      const bool ok = gather1(a.tx, W, gen(L - 1, 5), tag_s, a.error, [&] { dma(a.output_norm, norm_s, W * 4); });
+      flag_s = ok ? 1 : 0;
+    }
+    lds_barrier_p();
+    if (!flag_s) return;
+  } else {
+    // ======================= projection workgroup ===============================
+    const int g = w - HQ;
+    const Rows rq = split_rows<QKVR, NG>(g), ro = split_rows<W, NG>(g), rf = split_rows<FF, NG>(g);
+    Slot<PA> sa;
+    Slot<PB> sb;
+    // Layer-0 input: a host row or the embedding of the device token
+    // (QwenDecoder.Embed, Gguf.cs:340-344). Its loads go first so that they
+    // do not wait behind the weight slices.
+    constexpr int XI = W / kPT;
+    int8_t eq[XI];
+    _Float16 es[XI];
+    float xr[XI];
+    if (a.mode == 2) {
+      int token = *a.token;
+      if (token < 0 || token >= a.vocab) token = 0;
+#pragma unroll
+      for (int k = 0; k < XI; ++k) {
+        const size_t at = (size_t)token * W + tid + k * kPT;
+        eq[k] = a.embed_q[at];
+        es[k] = a.embed_s[at / 32];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < XI; ++k) xr[k] = a.x_in[tid + k * kPT];
+    }
+    if (wave > 0) {
+      load_slot<NPQ>(sa, LT[0].wqkv + (size_t)rq.r0 * W, LT[0].sqkv + (size_t)rq.r0 * B1, ct, rq.count * B1);
+      // Keep the two slices in issue order: the waits count on it.
+      __builtin_amdgcn_sched_barrier(0);
+      load_slot<NPO>(sb, LT[0].wo + (size_t)ro.r0 * QW, LT[0].so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
+    } else {
+      dma(LT[0].attn_norm, norm_s, W * 4);
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+#pragma unroll
+    for (int k = 0; k < XI; ++k)
+      tag_s[tid + k * kPT] = (u64)f2u(a.mode == 2 ? fmul((float)eq[k], (float)es[k]) : xr[k]);
+    lds_barrier_p();
+
+    // Each phase: all threads quantise the gathered input, waves 1-3 form the
+    // block products of their slice, then wave 0 sums the rows in order,
+    // publishes them and gathers the next phase's input while waves 1-3 load
+    // the slice of the phase after next.
+    for (int l = 0; l < L; ++l) {
+      const auto& Ly = LT[l];
+      const auto& Nx = LT[l + 1 < L ? l + 1 : l];  // the last layer re-reads its own slices
+      const int e = 16 * l + 1;
+      // ---- P1: attn_norm + qkv ----------------------------------------------
+      if (tid < ro.count) row_s[0][tid] = tag_value(tag_s, ro.r0 + tid);
+      quantize_input(tag_s, W, norm_s, a.eps, true, xq_s, xs_s, red_s);
+      lds_barrier_p();
+      sub(0);
+      if (wave > 0) slot_products<NPQ, B1>(sa, ct, xq_s, xs_s, prod_s, rq.count, rq.count * B1);
+      lds_barrier_p();
+      sub(1);
+      if (wave == 0) {
+        if (lane < rq.count) tag_store(a.tqkv + rq.r0 + lane, gen(l, 1), ordered_sum(prod_s, B1, rq.count, lane));
+        stamps(e + 0, e + 2, e + 1, 1);
+        if (tl && lane == 0) tl[e + 4] = t_sub[1];
+        const bool ok = gather1(a.tatt, QW, gen(l, 2), tag_s, a.error, NoPre{});
+        t_in = __builtin_amdgcn_s_memrealtime();
+        flag_s = ok ? 1 : 0;
+      } else {
+        load_slot<NPG>(sa, Ly.wgu + (size_t)2 * rf.r0 * W, Ly.sgu + (size_t)2 * rf.r0 * B1, ct, 2 * rf.count * B1);
+      }
+      lds_barrier_p();
+      if (!flag_s) return;
+
+      // ---- P3: o projection + residual -------------------------------------
+      quantize_input(tag_s, QW, nullptr, 0.0f, false, xq_s, xs_s, red_s);
+      lds_barrier_p();
+      if (wave > 0) slot_products<NPO, Bq>(sb, ct, xq_s, xs_s, prod_s, ro.count, ro.count * Bq);
+      lds_barrier_p();
+      if (wave == 0) {
+        if (lane < ro.count) {
+          const float v = fadd(ordered_sum(prod_s, Bq, ro.count, lane), row_s[0][lane]);
+          row_s[1][lane] = v;
+          tag_store(a.ta + ro.r0 + lane, gen(l, 3), v);
+        }
+        stamps(e + 8, e + 9);
+        const bool ok = gather1(a.ta, W, gen(l, 3), tag_s, a.error, [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
+        t_in = __builtin_amdgcn_s_memrealtime();
+        flag_s = ok ? 1 : 0;
+      } else {
+        load_slot<NPD>(sb, Ly.wd + (size_t)ro.r0 * FF, Ly.sd + (size_t)ro.r0 * Bf, ct, ro.count * Bf);
+      }
+      lds_barrier_p();
+      if (!flag_s) return;
+
+      // ---- P4: ffn_norm + gate/up + SwiGLU -----------------------------------
+      quantize_input(tag_s, W, norm_s, a.eps, true, xq_s, xs_s, red_s);
+      lds_barrier_p();
+      sub(0);
+      if (wave > 0) slot_products<NPG, B1>(sa, ct, xq_s, xs_s, prod_s, 2 * rf.count, 2 * rf.count * B1);
+      lds_barrier_p();
+      if (wave == 0) {
+        // Lanes [0, n) sum the gate rows, [n, 2n) the matching up rows.
+        const int nr = rf.count;
+        const float gs = lane < 2 * nr ? ordered_sum(prod_s, B1, 2 * nr, lane) : 0.0f;
+        const float u = __shfl(gs, lane + nr, kWave);
+        if (lane < nr) {
+          const float silu = fdiv(gs, fadd(1.0f, exp_ref(-gs)));
+          tag_store(a.th + rf.r0 + lane, gen(l, 4), fmul(silu, u));
+        }
+        stamps(e + 10, e + 12, e + 11, 1);
+        const bool ok = gather1(a.th, FF, gen(l, 4), tag_s, a.error, NoPre{});
+        t_in = __builtin_amdgcn_s_memrealtime();
+        flag_s = ok ? 1 : 0;
+      } else {
+        load_slot<NPQ>(sa, Nx.wqkv + (size_t)rq.r0 * W, Nx.sqkv + (size_t)rq.r0 * B1, ct, rq.count * B1);
+      }
+      lds_barrier_p();
+      if (!flag_s) return;
+
+      // ---- P5: down projection + residual ------------------------------------
+      quantize_input(tag_s, FF, nullptr, 0.0f, false, xq_s, xs_s, red_s);
+      lds_barrier_p();
+      sub(0);
+      if (wave > 0) slot_products<NPD, Bf>(sb, ct, xq_s, xs_s, prod_s, ro.count, ro.count * Bf);
+      lds_barrier_p();
+      sub(1);
+      if (wave == 0) {
+        if (lane < ro.count) {
+          const float v = fadd(ordered_sum(prod_s, Bf, ro.count, lane), row_s[1][lane]);
+          tag_store(a.tx + ro.r0 + lane, gen(l, 5), v);
+        }
+        stamps(e + 13, e + 15, e + 14, 1);
+        if (tl && lane == 0) tl[e + 5] = t_sub[1];
+        // Next layer's input with its attn_norm, or the lm_head input with output_norm.
+        const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
+        const bool ok = gather1(a.tx, W, gen(l, 5), tag_s, a.error, [&] { dma(next_norm, norm_s, W * 4); });
+        t_in = __builtin_amdgcn_s_memrealtime();
+        flag_s = ok ? 1 : 0;
+      } else {
+        load_slot<NPO>(sb, Nx.wo + (size_t)ro.r0 * QW, Nx.so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
+      }
+      lds_barrier_p();
+      if (!flag_s) return;
+    }
+  }
+
+  if (a.mode == 0) {
+    if (w == 0 && tid == 0) {
+      *a.position = pos + 1;
+      *a.epoch = *a.epoch + 1;
+    }
+    return;
+  }
+
+  // ---- output_norm + tied lm_head + greedy (every workgroup) -----------------
+  // Chunks of HR rows, round-robin over workgroups, three in flight per
+  // compute lane; wave 0 sums chunk c (logits staged in LDS) while waves 1-3
+  // form chunk c+1.
+  Slot<kSlotPairs> ha, hb, hc;
+  auto load_head = [&](Slot<kSlotPairs>& sl, int c) {
+    const int cc = c < chunks ? c : chunks - 1;  // clamped chunks are never summed
+    const int row0 = cc * HR;
+    load_slot<NPH>(sl, a.head_q + (size_t)row0 * W, a.head_s + (size_t)row0 * B1, ct, min(HR, a.vocab - row0) * B1);
+  };
+  if (wave > 0) {
+    load_head(ha, w);
+    load_head(hb, w + NB);
+    load_head(hc, w + 2 * NB);
+  }
+  quantize_input(tag_s, W, norm_s, a.eps, true, xq_s, xs_s, red_s);
+  lds_barrier_p();
+  float* hprod = reinterpret_cast<float*>(kv_s);  // two buffers of NPH products
+  float* hlog = hprod + 2 * NPH;                  // this workgroup's logits, chunk by chunk
+  u64 best = 0ull;
+  bool nan_first = false;
+  int parity = 0, k = 0;
+  auto head_chunk = [&](const Slot<kSlotPairs>& sl, int c) {
+    float* pr = hprod + parity * NPH;
+    const int row0 = c * HR;
+    const int rows = c < chunks ? min(HR, a.vocab - row0) : 0;
+    if (wave > 0) slot_products<NPH, B1>(sl, ct, xq_s, xs_s, pr, HR, rows * B1);
+    lds_barrier_p();
+    if (tid < rows) {
+      const float v = ordered_sum(pr, B1, HR, tid);
+      hlog[k * HR + tid] = v;
+      const u64 key = greedy_key(v, (uint32_t)(row0 + tid));
+      best = key > best ? key : best;
+      if (row0 + tid == 0 && v != v) nan_first = true;  // NaN first logit: Greedy returns 0
+    }
+    parity ^= 1;
+    ++k;
+  };
+  for (int c = w; c < chunks; c += 3 * NB) {
+    head_chunk(ha, c);
+    if (wave > 0) load_head(ha, c + 3 * NB);
+    head_chunk(hb, c + NB);
+    if (wave > 0) load_head(hb, c + 4 * NB);
+    head_chunk(hc, c + 2 * NB);
+    if (wave > 0) load_head(hc, c + 5 * NB);
+  }
+  if (wave != 0) return;
+  // Wave 0 alone from here: logits out, then this workgroup's best key.
+  for (int i = 0; i < k; ++i) {
+    const int row0 = (w + i * NB) * HR;
+    for (int r = lane; r < HR; r += kWave)
+      if (row0 + r < a.vocab) a.logits[row0 + r] = hlog[i * HR + r];
+  }
+  best = wave_max_u64(best);
+  if (tl && lane == 0) tl[16 * L + 1] = __builtin_amdgcn_s_memrealtime();
+  if (lane == 0) {
+    if (w == 0 && nan_first) best = ~0ull;  // forces token 0 below
+    tag_store_bits(a.tkeys + 2 * w, gen(L, 1), (uint32_t)(best >> 32));
+    tag_store_bits(a.tkeys + 2 * w + 1, gen(L, 1), (uint32_t)best);
+  }
+  if (w != 0) return;
+  if (!gather1(a.tkeys, 2 * NB, gen(L, 1), tag_s, a.error, NoPre{}) || lane != 0) return;
+  u64 b = 0ull;
+  bool first_nan = false;
+  for (int i = 0; i < NB; ++i) {
+    const u64 key = ((u64)(uint32_t)tag_s[2 * i] << 32) | (uint32_t)tag_s[2 * i + 1];
+    if (key == ~0ull) first_nan = true;
+    else b = key > b ? key : b;
+  }
+  *a.token = (first_nan || b == 0ull) ? 0 : (int)greedy_index(b);
+  if (tl) tl[16 * L + 2] = __builtin_amdgcn_s_memrealtime();
+  *a.position = pos + 1;
+  *a.epoch = *a.epoch + 1;
+}
+
+// Shapes with a persistent instantiation: Qwen3-0.6B and the reduced
+// Qwen3-shaped decoder used by the quick parity runs.
+bool persistent_shape_supported(int width, int heads, int kv_heads, int head_size, int ffn, int blocks) {
+  if (head_size != 128 || blocks != 256) return false;
+  return (width == 1024 && heads == 16 && kv_heads == 8 && ffn == 3072) ||
+         (width == 512 && heads == 4 && kv_heads == 2 && ffn == 1024);
+}
+
+// Attention probabilities of every position live in the gather area after
+// the q/k/v words.
+int persistent_max_capacity() { return (kTagWords - kProbOffset) * 2; }
+
+hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s) {
+  if (!persistent_shape_supported(a.width, a.heads, a.kv_heads, a.head_size, a.ffn, blocks)) return hipErrorInvalidValue;
+  if (a.capacity > persistent_max_capacity()) return hipErrorInvalidValue;
+  // lm_head: two product buffers and this workgroup's logits share the K/V stage.
+  const int rows = kSlotPairs * kComp / (a.width / 32);
+  const int per_wg = ((a.vocab + rows - 1) / rows + 3 * blocks - 1) / (3 * blocks) * 3;
+  if ((2 * kSlotPairs * kComp + per_wg * rows) * 4 > kKvBytes) return hipErrorInvalidValue;
+  if (a.width == 1024)
+    decode_step_kernel<1024, 16, 8, 3072, 256><<<blocks, kPT, 0, s>>>(a);
+  else
+    decode_step_kernel<512, 4, 2, 1024, 256><<<blocks, kPT, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+int persistent_max_positions() { return kKvBytes / 512; }
+
+int persistent_threads() { return kPT; }
+
+// Workgroups of the persistent kernel that fit on one CU at once.
+int persistent_blocks_per_cu(int width) {
+  int blocks = 0;
+  hipError_t e = width == 1024
+                     ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_step_kernel<1024, 16, 8, 3072, 256>, kPT, 0)
+                     : hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_step_kernel<512, 4, 2, 1024, 256>, kPT, 0);
+  return e == hipSuccess ? blocks : 0;
+}
+
+}  // namespace fah

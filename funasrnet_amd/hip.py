@@ -80,6 +80,9 @@ SIGNATURES = {
     "fah_decoder_kv_write": (ctypes.c_int, [_vp, ctypes.c_int, _u16p, _u16p, ctypes.c_int]),
     "fah_decoder_kv_read": (ctypes.c_int, [_vp, ctypes.c_int, _u16p, _u16p, ctypes.c_int]),
     "fah_decoder_weight_bytes": (ctypes.c_int64, [_vp]),
+    "fah_decoder_persistent": (ctypes.c_int, [_vp]),
+    "fah_decoder_trace": (ctypes.c_int, [_vp, ctypes.c_int, _f32p, ctypes.c_int]),
+    "fah_decoder_timeline": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int]),
 }
 
 _lib = None
@@ -335,3 +338,23 @@ class HipDecoder:
     @property
     def weight_bytes(self) -> int:
         return load().fah_decoder_weight_bytes(self.handle)
+
+    TRACE = {"x": 0, "qkv": 1, "attn": 2, "a": 3, "h": 4}
+
+    def trace(self, name: str) -> np.ndarray:
+        """Last-layer activation snapshot (QwenDecoder.Trace analogue)."""
+        c = self.config
+        size = {"x": c.width, "qkv": c.q_width + 2 * c.kv_width, "attn": c.q_width, "a": c.width, "h": c.ffn}[name]
+        out = np.empty(size, dtype=np.float32)
+        _check(load().fah_decoder_trace(self.handle, self.TRACE[name], _p(out, ctypes.c_float), size))
+        return out
+
+    def timeline(self):
+        """[workgroups, 480] device-clock stamps of the last persistent step, or None."""
+        out = np.zeros(256 * 480, dtype=np.uint64)
+        rc = _check(load().fah_decoder_timeline(self.handle, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), out.size))
+        return None if rc == DECLINED else out.reshape(256, 480)
+
+    @property
+    def persistent(self) -> bool:
+        return bool(load().fah_decoder_persistent(self.handle))

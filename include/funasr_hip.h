@@ -193,6 +193,28 @@ int fah_decoder_kv_write(fah_decoder* decoder, int layer, const uint16_t* keys, 
 /* Read cached K/V rows [0, positions) of one layer as fp16 bits. */
 int fah_decoder_kv_read(fah_decoder* decoder, int layer, uint16_t* keys, uint16_t* values, int positions);
 
+/* Copy the newest value of an intermediate activation of the last decoded
+ * row (the reference's Trace snapshots, QwenDecoder.cs:248-251, 269):
+ * which = 0 layer output x [width], 1 raw q|k|v projections [q+2kv],
+ * 2 attention output [heads*head_size], 3 post-attention residual a
+ * [width], 4 SwiGLU output [ffn]; values are those of the last layer. */
+int fah_decoder_trace(fah_decoder* decoder, int which, float* out, int count);
+
+/* Phase timestamps (100 MHz device clock) of the last persistent step:
+ * one row of 480 stamps per workgroup (256 rows): [1+16l .. 16+16l] the
+ * phase boundaries of layer l
+ * (input gathered, input quantised, output stored, attention sub-steps),
+ * [1+16L] lm_head done, [2+16L] greedy token written. Only
+ * recorded when FAH_TIMELINE=1 at creation (FAH_DECLINED otherwise); the
+ * rocprof-style per-op timing of the reference's LinearMeasured callback
+ * (src/FunAsrNet/TensorMath.cs:37-40) for a single-launch step. */
+int fah_decoder_timeline(fah_decoder* decoder, uint64_t* ticks, int count);
+
+/* 1 when decode steps run as one persistent launch (one workgroup per CU,
+ * phases exchanged through device memory), 0 for the per-kernel graph path.
+ * FAH_PERSISTENT=0 in the environment at creation forces the latter. */
+int fah_decoder_persistent(const fah_decoder* decoder);
+
 /* Device bytes of the weights streamed per decoded token (all projections
  * plus the lm_head, Q8_0 int8 and scale planes as stored). */
 int64_t fah_decoder_weight_bytes(const fah_decoder* decoder);
