@@ -21,7 +21,10 @@ import numpy as np
 
 from .model import DecoderWeights, Q8Tensor
 
-LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfunasr_hip.so")
+# The in-tree build; FUNASRNET_HIP_LIBRARY names another copy (absolute path),
+# as the C# loader's resolver does.
+LIBRARY = os.environ.get("FUNASRNET_HIP_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                                   "libfunasr_hip.so")
 
 OK, DECLINED = 0, 1
 ERROR_ARGUMENT, ERROR_DEVICE, ERROR_DISPOSED, ERROR_STATE = -1, -2, -3, -4

@@ -180,8 +180,9 @@ int fah_decoder_greedy(fah_decoder* decoder, int32_t* token);
 
 /* The FunAsr.Transcribe loop (src/FunAsrNet/FunAsr.cs:167-178) without the
  * tokenizer's end check: `steps` times Greedy -> Embed -> Decode(1), entirely
- * on the device (token feedback stays in device memory; one captured HIP
- * graph per step). The first token is the greedy choice of the logits of the
+ * on the device (token feedback stays in device memory; one persistent
+ * launch per step, or one captured HIP graph per step on the multi-kernel
+ * path). The first token is the greedy choice of the logits of the
  * preceding decode. tokens[steps] receives the chosen tokens. */
 int fah_decoder_generate(fah_decoder* decoder, int steps, int32_t* tokens);
 
