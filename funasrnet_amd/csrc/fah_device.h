@@ -67,14 +67,13 @@ __device__ __forceinline__ float from_half(_Float16 h) { return (float)h; }
 // float->int conversion (NaN -> 0). The amax is the integer maximum of the
 // absolute bit patterns (NaN above infinity), as the AVX path takes it.
 __device__ __forceinline__ int8_t quantize_value(float x, float inverse) {
-  float v = fmul(x, inverse);
-  if (v != v) return 0;
-  float t = __builtin_truncf(v);
-  float frac = __builtin_fabsf(fadd(v, -t));
-  float r = t;
-  if (frac >= 0.5f) r = fadd(t, v < 0.0f ? -1.0f : 1.0f);
+  // Branch-free: selects instead of divergent returns.
+  const float v = fmul(x, inverse);
+  const float t = __builtin_truncf(v);
+  const float frac = __builtin_fabsf(fadd(v, -t));
+  float r = frac >= 0.5f ? fadd(t, v < 0.0f ? -1.0f : 1.0f) : t;
   r = __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
-  return (int8_t)(int)r;
+  return v != v ? (int8_t)0 : (int8_t)(int)r;
 }
 
 __device__ __forceinline__ float block_scale(uint32_t max_abs_bits, float* inverse) {
@@ -83,10 +82,46 @@ __device__ __forceinline__ float block_scale(uint32_t max_abs_bits, float* inver
   return d;
 }
 
-// Wave-wide reductions (64 lanes) via DPP-free xor shuffles.
+// Cross-lane moves within rows of 16 lanes (DPP): quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror (lane i <- 7-i of its 8) and row_mirror
+// (lane i <- 15-i). All 64 lanes must be active.
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int Ctrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, Ctrl, 0xF, 0xF, false);
+}
+template <int Ctrl>
+__device__ __forceinline__ double dpp_double(double v) {
+  const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+  const uint32_t lo = dpp_u32<Ctrl>((uint32_t)u), hi = dpp_u32<Ctrl>((uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+__device__ __forceinline__ double readlane_double(double v, int lane) {
+  const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// Maximum over each aligned group of 8 lanes, in all 8 lanes.
+__device__ __forceinline__ uint32_t max8_u32(uint32_t m) {
+  uint32_t o = dpp_u32<kDppQuadXor1>(m);
+  m = o > m ? o : m;
+  o = dpp_u32<kDppQuadXor2>(m);
+  m = o > m ? o : m;
+  o = dpp_u32<kDppHalfMirror>(m);
+  return o > m ? o : m;
+}
+
+// Wave-wide double sum (64 lanes, all active), the same value in every lane:
+// pairwise within rows of 16 by DPP, then the four row sums.
 __device__ __forceinline__ double wave_sum_double(double v) {
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+  v += dpp_double<kDppQuadXor1>(v);
+  v += dpp_double<kDppQuadXor2>(v);
+  v += dpp_double<kDppHalfMirror>(v);
+  v += dpp_double<kDppMirror>(v);
+  return (readlane_double(v, 0) + readlane_double(v, 16)) + (readlane_double(v, 32) + readlane_double(v, 48));
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   for (int m = 32; m >= 1; m >>= 1) {

@@ -219,11 +219,13 @@ __device__ __forceinline__ int dot32(const int4& w0, const int4& w1, const int* 
   return d;
 }
 
-// Scaled block products of a slot into prod[b * R + r] (pairs j < valid;
-// pair j is row j / B, block j % B of the slice).
+// Scaled block products of a slot into prod[r * (B + 4) + b] (pairs
+// j < valid; pair j is row j / B, block j % B of the slice). Rows are padded
+// by four floats so that the lanes summing different rows read different
+// LDS banks.
 template <int NP, int B, int P>
 __device__ __forceinline__ void slot_products(const Slot<P>& sl, int ct, const int* xq, const float* xs, float* prod,
-                                              int R, int valid) {
+                                              int valid) {
   constexpr int kI = (NP + kComp - 1) / kComp;
 #pragma unroll
   for (int i = 0; i < kI; ++i) {
@@ -231,7 +233,7 @@ __device__ __forceinline__ void slot_products(const Slot<P>& sl, int ct, const i
     if (j < valid) {
       const int r = j / B, b = j - r * B;
       const int d = dot32(sl.w[i][0], sl.w[i][1], xq + b * 8);
-      prod[b * R + r] = fmul(fmul((float)d, (float)sl.s[i]), xs[b]);
+      prod[r * (B + 4) + b] = fmul(fmul((float)d, (float)sl.s[i]), xs[b]);
     }
   }
 }
@@ -247,18 +249,26 @@ __device__ __forceinline__ Rows split_rows(int g) {
   return {g * base + (g < extra ? g : extra), base + (g < extra ? 1 : 0)};
 }
 
-// Ordered block sum from 0f for row r (TensorMath.QuantizedRowsAvx.cs:27-58).
-__device__ __forceinline__ float ordered_sum(const float* prod, int B, int R, int r) {
+// Ordered block sum from 0f of one row of products (row r of the layout
+// above, 16-byte aligned) (TensorMath.QuantizedRowsAvx.cs:27-58).
+template <int B>
+__device__ __forceinline__ float ordered_sum(const float* prod, int r) {
+  static_assert(B % 16 == 0, "whole float4 batches");
+  const float* row = prod + r * (B + 4);
   float sum = 0.0f;
-  int b = 0;
-  for (; b + 8 <= B; b += 8) {
-    float p[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) p[k] = prod[(b + k) * R + r];
+  for (int b = 0; b < B; b += 16) {
+    float4 q[4];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) sum = fadd(sum, p[k]);
+    for (int k = 0; k < 4; ++k) q[k] = *reinterpret_cast<const float4*>(row + b + 4 * k);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      sum = fadd(sum, q[k].x);
+      sum = fadd(sum, q[k].y);
+      sum = fadd(sum, q[k].z);
+      sum = fadd(sum, q[k].w);
+    }
   }
-  for (; b < B; ++b) sum = fadd(sum, prod[b * R + r]);
   return sum;
 }
 
@@ -282,44 +292,59 @@ __device__ __forceinline__ float4 tag_float4(const u64* tag, int e) {
 
 // RMSNorm (optional, weights in LDS) + activation quantisation of act[0, K)
 // into xq/xs, all threads. Same arithmetic as the multi-kernel GEMV prologue.
-__device__ __forceinline__ void quantize_input(const u64* act, int K, const float* norm_w, float eps, bool norm,
-                                               int* xq, float* xs, double* red) {
-  float inverse = 1.0f;
-  if (norm) {
-    double sq = 0.0;
-    for (int e = 4 * threadIdx.x; e < K; e += 4 * kPT) {
-      float4 v = tag_float4(act, e);
-      sq += (double)v.x * (double)v.x + (double)v.y * (double)v.y;
-      sq += (double)v.z * (double)v.z + (double)v.w * (double)v.w;
-    }
-    double total = block_sum_d(sq, red);
-    float mean = (float)(total / (double)K);
-    inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
-  }
-  for (int e = 4 * threadIdx.x; e < K; e += 4 * kPT) {
-    float4 v = tag_float4(act, e);
-    if (norm) {
-      float4 w = *reinterpret_cast<const float4*>(norm_w + e);
-      v.x = fmul(fmul(v.x, inverse), w.x);
-      v.y = fmul(fmul(v.y, inverse), w.y);
-      v.z = fmul(fmul(v.z, inverse), w.z);
-      v.w = fmul(fmul(v.w, inverse), w.w);
-    }
-    uint32_t m = f2u(v.x) & 0x7fffffffu, t;
-    t = f2u(v.y) & 0x7fffffffu; m = t > m ? t : m;
-    t = f2u(v.z) & 0x7fffffffu; m = t > m ? t : m;
-    t = f2u(v.w) & 0x7fffffffu; m = t > m ? t : m;
+// Thread i takes values 4i + 4*kPT*g; a wave covers 256 consecutive values,
+// so with K a multiple of 256 every wave is either whole or idle in a group,
+// and eight consecutive threads hold one 32-value block.
+template <int K, bool NORM>
+__device__ __forceinline__ void quantize_input(const u64* act, const float* norm_w, float eps, int* xq, float* xs,
+                                               double* red) {
+  static_assert(K % (4 * kWave) == 0, "whole waves per group");
+  constexpr int G = (K + 4 * kPT - 1) / (4 * kPT);
+  float4 v[G];
 #pragma unroll
-    for (int s = 1; s < 8; s <<= 1) {
-      uint32_t o = __shfl_xor(m, s, 8);
-      m = o > m ? o : m;
+  for (int g = 0; g < G; ++g) {
+    const int e = 4 * threadIdx.x + 4 * kPT * g;
+    v[g] = e < K ? tag_float4(act, e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  if (NORM) {
+    double sq = 0.0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      sq += (double)v[g].x * (double)v[g].x + (double)v[g].y * (double)v[g].y;
+      sq += (double)v[g].z * (double)v[g].z + (double)v[g].w * (double)v[g].w;
     }
-    float inv;
-    float d = block_scale(m, &inv);
-    xq[e >> 2] = (int)((uint32_t)(uint8_t)quantize_value(v.x, inv) | ((uint32_t)(uint8_t)quantize_value(v.y, inv) << 8) |
-                       ((uint32_t)(uint8_t)quantize_value(v.z, inv) << 16) |
-                       ((uint32_t)(uint8_t)quantize_value(v.w, inv) << 24));
-    if ((threadIdx.x & 7) == 0) xs[e >> 5] = d;
+    const double total = block_sum_d(sq, red);
+    const float mean = (float)(total / (double)K);
+    const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int e = 4 * threadIdx.x + 4 * kPT * g;
+      if (e < K) {
+        const float4 w = *reinterpret_cast<const float4*>(norm_w + e);
+        v[g].x = fmul(fmul(v[g].x, inverse), w.x);
+        v[g].y = fmul(fmul(v[g].y, inverse), w.y);
+        v[g].z = fmul(fmul(v[g].z, inverse), w.z);
+        v[g].w = fmul(fmul(v[g].w, inverse), w.w);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int e = 4 * threadIdx.x + 4 * kPT * g;
+    if (e < K) {  // wave-uniform
+      uint32_t m = f2u(v[g].x) & 0x7fffffffu, t;
+      t = f2u(v[g].y) & 0x7fffffffu; m = t > m ? t : m;
+      t = f2u(v[g].z) & 0x7fffffffu; m = t > m ? t : m;
+      t = f2u(v[g].w) & 0x7fffffffu; m = t > m ? t : m;
+      m = max8_u32(m);
+      float inv;
+      const float d = block_scale(m, &inv);
+      xq[e >> 2] = (int)((uint32_t)(uint8_t)quantize_value(v[g].x, inv) |
+                         ((uint32_t)(uint8_t)quantize_value(v[g].y, inv) << 8) |
+                         ((uint32_t)(uint8_t)quantize_value(v[g].z, inv) << 16) |
+                         ((uint32_t)(uint8_t)quantize_value(v[g].w, inv) << 24));
+      if ((threadIdx.x & 7) == 0) xs[e >> 5] = d;
+    }
   }
 }
 
@@ -370,8 +395,8 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   constexpr int NPH = kSlotPairs * kComp, HR = NPH / B1;  // lm_head: pairs and rows per chunk
   static_assert(RQ <= 64 && 2 * RGU <= 64 && RO <= 64 && HR <= 64 && HR * B1 == NPH, "row lanes");
   static_assert(PA <= 5 && PB <= 4, "slot registers");
-  static_assert(FF <= kActFloats && QW <= kActFloats && W <= 1024 && NPQ <= kProdFloats && NPG <= kProdFloats &&
-                    NPO <= kProdFloats && NPD <= kProdFloats,
+  static_assert(FF <= kActFloats && QW <= kActFloats && W <= 1024 && RQ * (B1 + 4) <= kProdFloats &&
+                    2 * RGU * (B1 + 4) <= kProdFloats && RO * (Bq + 4) <= kProdFloats && RO * (Bf + 4) <= kProdFloats,
                 "LDS sizing");
   static_assert(W % kPT == 0 && 2 * NPH * 4 <= kKvBytes, "layer-0 input and lm_head product buffers");
   static_assert(HQ < NB && HQ == 2 * HKV, "paired heads, one attention workgroup per query head");
@@ -698,14 +723,14 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       const int e = 16 * l + 1;
       // ---- P1: attn_norm + qkv ----------------------------------------------
       if (tid < ro.count) row_s[0][tid] = tag_value(tag_s, ro.r0 + tid);
-      quantize_input(tag_s, W, norm_s, a.eps, true, xq_s, xs_s, red_s);
+      quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
       lds_barrier_p();
       sub(0);
-      if (wave > 0) slot_products<NPQ, B1>(sa, ct, xq_s, xs_s, prod_s, rq.count, rq.count * B1);
+      if (wave > 0) slot_products<NPQ, B1>(sa, ct, xq_s, xs_s, prod_s, rq.count * B1);
       lds_barrier_p();
       sub(1);
       if (wave == 0) {
-        if (lane < rq.count) tag_store(a.tqkv + rq.r0 + lane, gen(l, 1), ordered_sum(prod_s, B1, rq.count, lane));
+        if (lane < rq.count) tag_store(a.tqkv + rq.r0 + lane, gen(l, 1), ordered_sum<B1>(prod_s, lane));
         stamps(e + 0, e + 2, e + 1, 1);
         if (tl && lane == 0) tl[e + 4] = t_sub[1];
         const bool ok = gather1(a.tatt, QW, gen(l, 2), tag_s, a.error, NoPre{});
@@ -718,13 +743,13 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       if (!flag_s) return;
 
       // ---- P3: o projection + residual -------------------------------------
-      quantize_input(tag_s, QW, nullptr, 0.0f, false, xq_s, xs_s, red_s);
+      quantize_input<QW, false>(tag_s, nullptr, 0.0f, xq_s, xs_s, red_s);
       lds_barrier_p();
-      if (wave > 0) slot_products<NPO, Bq>(sb, ct, xq_s, xs_s, prod_s, ro.count, ro.count * Bq);
+      if (wave > 0) slot_products<NPO, Bq>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bq);
       lds_barrier_p();
       if (wave == 0) {
         if (lane < ro.count) {
-          const float v = fadd(ordered_sum(prod_s, Bq, ro.count, lane), row_s[0][lane]);
+          const float v = fadd(ordered_sum<Bq>(prod_s, lane), row_s[0][lane]);
           row_s[1][lane] = v;
           tag_store(a.ta + ro.r0 + lane, gen(l, 3), v);
         }
@@ -739,15 +764,15 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       if (!flag_s) return;
 
       // ---- P4: ffn_norm + gate/up + SwiGLU -----------------------------------
-      quantize_input(tag_s, W, norm_s, a.eps, true, xq_s, xs_s, red_s);
+      quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
       lds_barrier_p();
       sub(0);
-      if (wave > 0) slot_products<NPG, B1>(sa, ct, xq_s, xs_s, prod_s, 2 * rf.count, 2 * rf.count * B1);
+      if (wave > 0) slot_products<NPG, B1>(sa, ct, xq_s, xs_s, prod_s, 2 * rf.count * B1);
       lds_barrier_p();
       if (wave == 0) {
         // Lanes [0, n) sum the gate rows, [n, 2n) the matching up rows.
         const int nr = rf.count;
-        const float gs = lane < 2 * nr ? ordered_sum(prod_s, B1, 2 * nr, lane) : 0.0f;
+        const float gs = lane < 2 * nr ? ordered_sum<B1>(prod_s, lane) : 0.0f;
         const float u = __shfl(gs, lane + nr, kWave);
         if (lane < nr) {
           const float silu = fdiv(gs, fadd(1.0f, exp_ref(-gs)));
@@ -764,15 +789,15 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       if (!flag_s) return;
 
       // ---- P5: down projection + residual ------------------------------------
-      quantize_input(tag_s, FF, nullptr, 0.0f, false, xq_s, xs_s, red_s);
+      quantize_input<FF, false>(tag_s, nullptr, 0.0f, xq_s, xs_s, red_s);
       lds_barrier_p();
       sub(0);
-      if (wave > 0) slot_products<NPD, Bf>(sb, ct, xq_s, xs_s, prod_s, ro.count, ro.count * Bf);
+      if (wave > 0) slot_products<NPD, Bf>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bf);
       lds_barrier_p();
       sub(1);
       if (wave == 0) {
         if (lane < ro.count) {
-          const float v = fadd(ordered_sum(prod_s, Bf, ro.count, lane), row_s[1][lane]);
+          const float v = fadd(ordered_sum<Bf>(prod_s, lane), row_s[1][lane]);
           tag_store(a.tx + ro.r0 + lane, gen(l, 5), v);
         }
         stamps(e + 13, e + 15, e + 14, 1);
@@ -813,21 +838,22 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     load_head(hb, w + NB);
     load_head(hc, w + 2 * NB);
   }
-  quantize_input(tag_s, W, norm_s, a.eps, true, xq_s, xs_s, red_s);
+  quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
   lds_barrier_p();
-  float* hprod = reinterpret_cast<float*>(kv_s);  // two buffers of NPH products
-  float* hlog = hprod + 2 * NPH;                  // this workgroup's logits, chunk by chunk
+  constexpr int HP = HR * (B1 + 4);                 // one chunk's padded products
+  float* hprod = reinterpret_cast<float*>(kv_s);  // two buffers of HP products
+  float* hlog = hprod + 2 * HP;                   // this workgroup's logits, chunk by chunk
   u64 best = 0ull;
   bool nan_first = false;
   int parity = 0, k = 0;
   auto head_chunk = [&](const Slot<kSlotPairs>& sl, int c) {
-    float* pr = hprod + parity * NPH;
+    float* pr = hprod + parity * HP;
     const int row0 = c * HR;
     const int rows = c < chunks ? min(HR, a.vocab - row0) : 0;
-    if (wave > 0) slot_products<NPH, B1>(sl, ct, xq_s, xs_s, pr, HR, rows * B1);
+    if (wave > 0) slot_products<NPH, B1>(sl, ct, xq_s, xs_s, pr, rows * B1);
     lds_barrier_p();
     if (tid < rows) {
-      const float v = ordered_sum(pr, B1, HR, tid);
+      const float v = ordered_sum<B1>(pr, tid);
       hlog[k * HR + tid] = v;
       const u64 key = greedy_key(v, (uint32_t)(row0 + tid));
       best = key > best ? key : best;
@@ -891,7 +917,7 @@ hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s
   // lm_head: two product buffers and this workgroup's logits share the K/V stage.
   const int rows = kSlotPairs * kComp / (a.width / 32);
   const int per_wg = ((a.vocab + rows - 1) / rows + 3 * blocks - 1) / (3 * blocks) * 3;
-  if ((2 * kSlotPairs * kComp + per_wg * rows) * 4 > kKvBytes) return hipErrorInvalidValue;
+  if ((2 * rows * (a.width / 32 + 4) + per_wg * rows) * 4 > kKvBytes) return hipErrorInvalidValue;
   if (a.width == 1024)
     decode_step_kernel<1024, 16, 8, 3072, 256><<<blocks, kPT, 0, s>>>(a);
   else
