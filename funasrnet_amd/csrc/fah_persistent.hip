@@ -37,6 +37,7 @@ constexpr int kProdFloats = 1024;        // (row, block) products of one phase
 constexpr int kKvBytes = 121 * 1024;     // K/V staging: 512 B per position
 constexpr int kProbOffset = 4 * 128;     // attention probabilities after q/k/v in the tag area
 constexpr long kSpinLimit = 1L << 21;    // bounded polls per gather (~1-2 s)
+constexpr int kSentinelChunks = 0;       // gathers above this many 1 KB chunks poll a sentinel first
 using u64 = unsigned long long;
 using lds_ptr = __attribute__((address_space(3))) void*;
 
@@ -122,10 +123,11 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
     }
   };
   long spin = 0;
-  // Poll one chunk (the last) until it is current before reading them all:
-  // consumers that arrive early then cost one 1 KB load per round trip
-  // instead of the whole vector.
-  {
+  // Large vectors: poll one chunk (the last) until it is current before
+  // reading them all, so that consumers that arrive early cost one 1 KB load
+  // per round trip instead of the whole vector. Small ones are polled whole
+  // (one round trip less once the data is there).
+  if (total > kSentinelChunks) {
     const u64* src;
     int off;
     locate(total - 1, src, off);
@@ -376,6 +378,19 @@ __device__ __forceinline__ float nan_max_p(float a, float b) {
   return b > a ? b : a;
 }
 
+// nan_max_p over the 64 lanes of a wave (all active), in every lane.
+__device__ __forceinline__ float wave_max_nan(float m) {
+  m = nan_max_p(m, u2f(dpp_u32<kDppQuadXor1>(f2u(m))));
+  m = nan_max_p(m, u2f(dpp_u32<kDppQuadXor2>(f2u(m))));
+  m = nan_max_p(m, u2f(dpp_u32<kDppHalfMirror>(f2u(m))));
+  m = nan_max_p(m, u2f(dpp_u32<kDppMirror>(f2u(m))));
+  const float r0 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 0));
+  const float r1 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 16));
+  const float r2 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 32));
+  const float r3 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 48));
+  return nan_max_p(nan_max_p(r0, r1), nan_max_p(r2, r3));
+}
+
 }  // namespace
 
 // Shape-specialised: W hidden width, HQ/HKV query/kv heads (head size 128),
@@ -560,7 +575,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       // Softmax (TensorMath.SoftmaxAvx.cs:11-58).
       float m = -__builtin_inff();
       for (int t = tid; t < n; t += kPT) m = nan_max_p(m, p_s[t]);
-      for (int s = 32; s >= 1; s >>= 1) m = nan_max_p(m, __shfl_xor(m, s, kWave));
+      m = wave_max_nan(m);
       if (lane == 0) tmax_s[wave] = m;
       lds_barrier_p();
       float mx = tmax_s[0];
@@ -628,7 +643,8 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         auto vrow = [&](int t) {
           return (t < npre ? kv_s + (size_t)t * 512 : ovf_s + (size_t)(t - npre) * 512) + 256 + 2 * c;
         };
-        auto step = [&](int t) { acc = fadd(acc, fmul(from_half(*reinterpret_cast<const _Float16*>(vrow(t))), p_s[t])); };
+        auto prob = [&](int t) { return p_s[t]; };
+        auto step = [&](int t) { acc = fadd(acc, fmul(from_half(*reinterpret_cast<const _Float16*>(vrow(t))), prob(t))); };
         int t = 0;
         for (; t + 16 <= npre; t += 16) chain16(vrow(t), t);
         for (; t < npre; ++t) step(t);
@@ -641,10 +657,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
           for (int k = 0; k < 8; ++k) x[k] = from_half(vglob[(size_t)(t + k) * HS]);
 #pragma unroll
-          for (int k = 0; k < 8; ++k) acc = fadd(acc, fmul(x[k], p_s[t + k]));
+          for (int k = 0; k < 8; ++k) acc = fadd(acc, fmul(x[k], prob(t + k)));
         }
-        for (; t < pos; ++t) acc = fadd(acc, fmul(from_half(vglob[(size_t)t * HS]), p_s[t]));
-        acc = fadd(acc, fmul(cur_s[2][c], p_s[pos]));
+        for (; t < pos; ++t) acc = fadd(acc, fmul(from_half(vglob[(size_t)t * HS]), prob(t)));
+        acc = fadd(acc, fmul(cur_s[2][c], prob(pos)));
         cur_s[0][c] = acc;
       }
       lds_barrier_p();
