@@ -193,6 +193,10 @@ struct fah_decoder {
   int blocks = 0;
   DeviceBuffer layer_table, tx, tqkv, tatt, ta, th, tkeys, epoch, error, timeline;
   fah::PersistentArgs pargs{};
+  // Prefill (decode of many rows at once): row buffers grown on demand, and
+  // the gate/up storage tiles (base rows, the first `extra` tiles one more).
+  DeviceBuffer pf_x, pf_a, pf_qkv, pf_q, pf_attn, pf_h, pf_xq, pf_xs;
+  int gu_base = 1, gu_extra = 0;
 };
 
 namespace {
@@ -335,6 +339,113 @@ void enqueue_head(fah_decoder* d, hipStream_t s) {
 }
 
 void enqueue_kind(fah_decoder* d, int kind, hipStream_t s);
+
+// Rows per prefill pass: the GEMMs see all of them at once.
+constexpr int kPrefillChunk = 1024;
+
+// QwenDecoder.Decode for frames > 1 (QwenDecoder.cs:161-271): every layer
+// runs over all rows of a chunk -- norm + quantise per row, MFMA Q8_0 GEMMs
+// with the per-row block order, QK-norm/RoPE/KV write per row, causal
+// attention per (head, row) -- then the last row's final norm, lm_head and
+// greedy when logits are wanted. `x` is the device copy of the rows.
+void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_t s) {
+  const fah_decoder_config& c = d->cfg;
+  const int qkv_rows = d->q_width + 2 * d->kv_width;
+  const int widest = std::max(std::max(c.width, d->q_width), c.ffn);
+  const size_t kv_layer = (size_t)c.kv_heads * c.capacity * c.head_size;
+  for (int done = 0; done < frames; done += kPrefillChunk) {
+    const int T = std::min(kPrefillChunk, frames - done);
+    d->pf_x.ensure((size_t)T * c.width * 4);
+    d->pf_a.ensure((size_t)T * c.width * 4);
+    d->pf_qkv.ensure((size_t)T * qkv_rows * 4);
+    d->pf_q.ensure((size_t)T * d->q_width * 4);
+    d->pf_attn.ensure((size_t)T * d->q_width * 4);
+    d->pf_h.ensure((size_t)T * c.ffn * 4);
+    d->pf_xq.ensure((size_t)T * widest);
+    d->pf_xs.ensure((size_t)T * widest / 32 * 4);
+    check(hipMemcpyAsync(d->pf_x.ptr, x + (size_t)done * c.width, (size_t)T * c.width * 4, hipMemcpyDeviceToDevice, s),
+          "D2D prefill rows");
+    int8_t* xq = d->pf_xq.as<int8_t>();
+    float* xs = d->pf_xs.as<float>();
+    auto gemm = [&](const DeviceMatrix& m, int rows, float* out, int stride, const float* resid, int mode) {
+      fah::GemmArgs g{};
+      g.w = m.q.as<int8_t>();
+      g.ws = m.s.ptr;
+      g.rows = rows;
+      g.K = m.cols;
+      g.xq = xq;
+      g.xs = xs;
+      g.frames = T;
+      g.out = out;
+      g.out_stride = stride;
+      g.resid = resid;
+      g.split_base = d->gu_base;
+      g.split_extra = d->gu_extra;
+      check(fah::launch_gemm(g, d->half_scales, mode, s), "prefill gemm");
+    };
+    for (int l = 0; l < c.layers; ++l) {
+      check(fah::launch_norm_quantize_rows(d->pf_x.as<float>(), T, c.width, d->attn_norm[l].as<float>(), c.eps, xq, xs,
+                                           s),
+            "prefill attn_norm");
+      gemm(d->qkv[l], qkv_rows, d->pf_qkv.as<float>(), qkv_rows, nullptr, fah::kGemmPlain);
+      fah::QkArgs qa{};
+      qa.qkv = d->pf_qkv.as<float>();
+      qa.q_norm = d->q_norm[l].as<float>();
+      qa.k_norm = d->k_norm[l].as<float>();
+      qa.rope_cos = d->rope_cos.as<float>();
+      qa.rope_sin = d->rope_sin.as<float>();
+      qa.position = d->position.as<int>();
+      qa.q_out = d->pf_q.as<float>();
+      qa.kcache = d->kcache.as<_Float16>() + kv_layer * l;
+      qa.vcache = d->vcache.as<_Float16>() + kv_layer * l;
+      qa.heads = c.heads;
+      qa.kv_heads = c.kv_heads;
+      qa.head_size = c.head_size;
+      qa.q_width = d->q_width;
+      qa.kv_width = d->kv_width;
+      qa.capacity = c.capacity;
+      qa.eps = c.eps;
+      qa.frames = T;
+      check(fah::launch_qk_prepare(qa, s), "prefill qk prepare");
+      fah::PrefillAttnArgs pa{};
+      pa.q = d->pf_q.as<float>();
+      pa.kcache = qa.kcache;
+      pa.vcache = qa.vcache;
+      pa.out = d->pf_attn.as<float>();
+      pa.frames = T;
+      pa.position = d->host_position + done;
+      pa.heads = c.heads;
+      pa.kv_heads = c.kv_heads;
+      pa.head_size = c.head_size;
+      pa.capacity = c.capacity;
+      pa.divisor = std::sqrt((float)c.head_size);
+      check(fah::launch_attn_prefill(pa, s), "prefill attention");
+      check(fah::launch_norm_quantize_rows(d->pf_attn.as<float>(), T, d->q_width, nullptr, 0.0f, xq, xs, s),
+            "prefill quantise attention");
+      gemm(d->wo[l], c.width, d->pf_a.as<float>(), c.width, d->pf_x.as<float>(), fah::kGemmResidual);
+      check(fah::launch_norm_quantize_rows(d->pf_a.as<float>(), T, c.width, d->ffn_norm[l].as<float>(), c.eps, xq, xs,
+                                           s),
+            "prefill ffn_norm");
+      gemm(d->gateup[l], c.ffn, d->pf_h.as<float>(), c.ffn, nullptr, fah::kGemmSwiGLU);
+      check(fah::launch_norm_quantize_rows(d->pf_h.as<float>(), T, c.ffn, nullptr, 0.0f, xq, xs, s),
+            "prefill quantise ffn");
+      gemm(d->down[l], c.width, d->pf_x.as<float>(), c.width, d->pf_a.as<float>(), fah::kGemmResidual);
+    }
+    check(fah::launch_advance(d->position.as<int>(), T, s), "advance");
+    if (logits && done + T == frames) {
+      check(hipMemcpyAsync(d->x.ptr, d->pf_x.as<float>() + (size_t)(T - 1) * c.width, (size_t)c.width * 4,
+                           hipMemcpyDeviceToDevice, s),
+            "D2D last row");
+      enqueue_head(d, s);
+    }
+  }
+}
+
+// Row-by-row decode below this many frames (and with FAH_PREFILL=0).
+bool use_prefill(int frames) {
+  const char* env = std::getenv("FAH_PREFILL");
+  return frames >= 4 && !(env && env[0] == '0');
+}
 
 hipGraphExec_t capture(fah_decoder* d, int kind) {
   hipStream_t s = d->context->stream;
@@ -519,6 +630,26 @@ int fah_weight_release(fah_weight* w) {
 
 int64_t fah_weight_device_bytes(const fah_weight* w) { return w ? (int64_t)(w->q.bytes + w->s.bytes) : 0; }
 
+// Many rows at once go through the MFMA GEMM (same per-row block order).
+constexpr int kGemmMinFrames = 4;
+bool gemm_fits(const fah_weight* w, int frames) { return frames >= kGemmMinFrames && w->cols <= 3072; }
+
+void launch_weight_gemm(const fah_weight* w, const int8_t* xq, const float* xs, int frames, float* out,
+                        const float* bias, hipStream_t s) {
+  fah::GemmArgs g{};
+  g.w = w->q.as<int8_t>();
+  g.ws = w->s.ptr;
+  g.rows = w->rows;
+  g.K = w->cols;
+  g.xq = xq;
+  g.xs = xs;
+  g.frames = frames;
+  g.out = out;
+  g.out_stride = w->rows;
+  g.bias = bias;
+  check(fah::launch_gemm(g, w->half_scales, fah::kGemmPlain, s), "gemm");
+}
+
 static fah::GemvArgs weight_args(const fah_weight* w) {
   fah::GemvArgs a{};
   a.w = w->q.as<int8_t>();
@@ -549,12 +680,21 @@ int fah_quantized_linear(fah_context* c, const float* input, int frames, const f
       dbias = reinterpret_cast<float*>(c->in.as<char>() + in_bytes);
       check(hipMemcpyAsync(dbias, bias, (size_t)w->rows * 4, hipMemcpyHostToDevice, c->stream), "H2D bias");
     }
-    fah::GemvArgs a = weight_args(w);
-    a.x = c->in.as<float>();
-    a.out = c->out.as<float>();
-    a.out_rows = w->rows;
-    a.bias = dbias;
-    check(fah::launch_gemv(a, w->half_scales, fah::kInputFloat, fah::kOutPlain, frames, c->stream), "gemv");
+    if (gemm_fits(w, frames)) {
+      size_t n = (size_t)frames * w->cols;
+      c->q.ensure(n);
+      c->s.ensure(n / 32 * 4);
+      check(fah::launch_quantize(c->in.as<float>(), (int64_t)n, c->q.as<int8_t>(), c->s.as<float>(), c->stream),
+            "quantize");
+      launch_weight_gemm(w, c->q.as<int8_t>(), c->s.as<float>(), frames, c->out.as<float>(), dbias, c->stream);
+    } else {
+      fah::GemvArgs a = weight_args(w);
+      a.x = c->in.as<float>();
+      a.out = c->out.as<float>();
+      a.out_rows = w->rows;
+      a.bias = dbias;
+      check(fah::launch_gemv(a, w->half_scales, fah::kInputFloat, fah::kOutPlain, frames, c->stream), "gemv");
+    }
     check(hipMemcpyAsync(output, c->out.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return FAH_OK;
@@ -595,13 +735,18 @@ int fah_linear_many(fah_context* c, const float* input, int frames, const fah_we
           "quantize");
     size_t at = 0;
     for (int i = 0; i < count; ++i) {
-      fah::GemvArgs a = weight_args(weights[i]);
-      a.xq = c->q.as<int8_t>();
-      a.xs = c->s.as<float>();
-      a.out = c->out.as<float>() + at;
-      a.out_rows = weights[i]->rows;
-      check(fah::launch_gemv(a, weights[i]->half_scales, fah::kInputQuantized, fah::kOutPlain, frames, c->stream),
-            "gemv");
+      if (gemm_fits(weights[i], frames)) {
+        launch_weight_gemm(weights[i], c->q.as<int8_t>(), c->s.as<float>(), frames, c->out.as<float>() + at, nullptr,
+                           c->stream);
+      } else {
+        fah::GemvArgs a = weight_args(weights[i]);
+        a.xq = c->q.as<int8_t>();
+        a.xs = c->s.as<float>();
+        a.out = c->out.as<float>() + at;
+        a.out_rows = weights[i]->rows;
+        check(fah::launch_gemv(a, weights[i]->half_scales, fah::kInputQuantized, fah::kOutPlain, frames, c->stream),
+              "gemv");
+      }
       at += (size_t)frames * weights[i]->rows;
     }
     at = 0;
@@ -635,12 +780,16 @@ int fah_q8_gemv_device(fah_context* c, const int8_t* q, const float* scales, int
     require(frames > 0 && q && scales && out, "invalid GEMV arguments");
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
-    fah::GemvArgs a = weight_args(w);
-    a.xq = q;
-    a.xs = scales;
-    a.out = out;
-    a.out_rows = w->rows;
-    check(fah::launch_gemv(a, w->half_scales, fah::kInputQuantized, fah::kOutPlain, frames, c->stream), "gemv");
+    if (gemm_fits(w, frames)) {
+      launch_weight_gemm(w, q, scales, frames, out, nullptr, c->stream);
+    } else {
+      fah::GemvArgs a = weight_args(w);
+      a.xq = q;
+      a.xs = scales;
+      a.out = out;
+      a.out_rows = w->rows;
+      check(fah::launch_gemv(a, w->half_scales, fah::kInputQuantized, fah::kOutPlain, frames, c->stream), "gemv");
+    }
     return FAH_OK;
   });
 }
@@ -738,6 +887,8 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
     int gu_group = pick_group_rows(2 * k.ffn, k.width, 4, true);
     while (gu_group > 2 && (k.ffn % (gu_group / 2) != 0)) gu_group /= 2;
     const int ng = nb - k.heads;
+    d->gu_base = d->persistent ? k.ffn / ng : gu_group / 2;
+    d->gu_extra = d->persistent ? k.ffn % ng : 0;
     int down_group = pick_group_rows(k.width, k.ffn, 4, false);
     for (int l = 0; l < k.layers; ++l) {
       const fah_layer_host& L = layers[l];
@@ -960,10 +1111,14 @@ int fah_decoder_decode(fah_decoder* d, const float* embeddings, int frames, floa
     size_t row = (size_t)d->cfg.width * 4;
     d->staging.ensure(row * frames);
     check(hipMemcpyAsync(d->staging.ptr, embeddings, row * frames, hipMemcpyHostToDevice, s), "H2D embeddings");
-    for (int f = 0; f < frames; ++f) {
-      check(hipMemcpyAsync(d->x.ptr, d->staging.as<char>() + row * f, row, hipMemcpyDeviceToDevice, s), "D2D row");
-      bool last = f == frames - 1;
-      run_kind(d, last && logits ? 1 : 0, s);
+    if (use_prefill(frames)) {
+      prefill(d, d->staging.as<float>(), frames, logits != nullptr, s);
+    } else {
+      for (int f = 0; f < frames; ++f) {
+        check(hipMemcpyAsync(d->x.ptr, d->staging.as<char>() + row * f, row, hipMemcpyDeviceToDevice, s), "D2D row");
+        bool last = f == frames - 1;
+        run_kind(d, last && logits ? 1 : 0, s);
+      }
     }
     if (logits)
       check(hipMemcpyAsync(logits, d->logits.ptr, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, s), "D2H");

@@ -152,4 +152,103 @@ __device__ __forceinline__ uint32_t greedy_index(unsigned long long key) {
   return 0xffffffffu - (uint32_t)(key & 0xffffffffull);
 }
 
+
+// ---- shared by the decode, persistent and prefill kernels ----------------
+
+// Workgroup barrier that orders LDS only. __syncthreads() also fences global
+// memory, which makes the compiler wait for every outstanding global load
+// (vmcnt(0)) before the barrier -- that would drain the weight stream the
+// GEMV issues ahead of its activation prologue.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Block-wide sum of one double per thread (256 threads, 4 waves).
+__device__ __forceinline__ double block_sum_double(double v, double* scratch) {
+  v = wave_sum_double(v);
+  int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (lane == 0) scratch[wave] = v;
+  lds_barrier();
+  double total = 0.0;
+  int waves = (blockDim.x + kWave - 1) / kWave;
+  for (int i = 0; i < waves; ++i) total += scratch[i];
+  return total;
+}
+
+// RMSNorm inverse of src/FunAsrNet/TensorMath.Elementwise.cs:58-78 (rms):
+// 1f / sqrtf((float)(sum_sq / width) + eps). The double sum is a tree here;
+// the reference's sequential lane order only changes double rounding, which
+// reaches the float result with probability ~1e-7 per row.
+__device__ __forceinline__ float rms_inverse(double sum_sq, int width, float eps) {
+  float mean = (float)(sum_sq / (double)width);
+  return fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
+}
+
+// Quantise four consecutive values held by this lane; the 32-value block is
+// spread over 8 consecutive lanes (shuffle max of the absolute bit patterns).
+// Returns the four int8 codes packed little-endian; *scale gets the block's d.
+__device__ __forceinline__ int quantize4(float v0, float v1, float v2, float v3, float* scale) {
+  uint32_t m = f2u(v0) & 0x7fffffffu;
+  uint32_t t = f2u(v1) & 0x7fffffffu;
+  m = t > m ? t : m;
+  t = f2u(v2) & 0x7fffffffu;
+  m = t > m ? t : m;
+  t = f2u(v3) & 0x7fffffffu;
+  m = t > m ? t : m;
+#pragma unroll
+  for (int s = 1; s < 8; s <<= 1) {
+    uint32_t o = __shfl_xor(m, s, 8);
+    m = o > m ? o : m;
+  }
+  float inverse;
+  *scale = block_scale(m, &inverse);
+  uint32_t packed = (uint32_t)(uint8_t)quantize_value(v0, inverse) | ((uint32_t)(uint8_t)quantize_value(v1, inverse) << 8) |
+                    ((uint32_t)(uint8_t)quantize_value(v2, inverse) << 16) |
+                    ((uint32_t)(uint8_t)quantize_value(v3, inverse) << 24);
+  return (int)packed;
+}
+
+// One 16-byte piece of a K row (8 F16 channels 8i..8i+7) into the eight
+// channel-strided accumulators: acc[j] += q[8i+j] * k[8i+j].
+__device__ __forceinline__ void score8(float* acc, const uint4& kk, const float* q) {
+  const float4 q0 = *reinterpret_cast<const float4*>(q);
+  const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
+  const uint32_t w[4] = {kk.x, kk.y, kk.z, kk.w};
+  float k[8];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    k[2 * m] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu)));
+    k[2 * m + 1] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16)));
+  }
+  acc[0] = fadd(acc[0], fmul(q0.x, k[0]));
+  acc[1] = fadd(acc[1], fmul(q0.y, k[1]));
+  acc[2] = fadd(acc[2], fmul(q0.z, k[2]));
+  acc[3] = fadd(acc[3], fmul(q0.w, k[3]));
+  acc[4] = fadd(acc[4], fmul(q1.x, k[4]));
+  acc[5] = fadd(acc[5], fmul(q1.y, k[5]));
+  acc[6] = fadd(acc[6], fmul(q1.z, k[6]));
+  acc[7] = fadd(acc[7], fmul(q1.w, k[7]));
+}
+
+__device__ __forceinline__ float nan_max_p(float a, float b) {
+  if (a != a) return a;
+  if (b != b) return b;
+  return b > a ? b : a;
+}
+
+// nan_max_p over the 64 lanes of a wave (all active), in every lane.
+__device__ __forceinline__ float wave_max_nan(float m) {
+  m = nan_max_p(m, u2f(dpp_u32<kDppQuadXor1>(f2u(m))));
+  m = nan_max_p(m, u2f(dpp_u32<kDppQuadXor2>(f2u(m))));
+  m = nan_max_p(m, u2f(dpp_u32<kDppHalfMirror>(f2u(m))));
+  m = nan_max_p(m, u2f(dpp_u32<kDppMirror>(f2u(m))));
+  const float r0 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 0));
+  const float r1 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 16));
+  const float r2 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 32));
+  const float r3 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 48));
+  return nan_max_p(nan_max_p(r0, r1), nan_max_p(r2, r3));
+}
+
 }  // namespace fah

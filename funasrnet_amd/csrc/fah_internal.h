@@ -39,6 +39,7 @@ struct QkArgs {
   _Float16* vcache;
   int heads, kv_heads, head_size, q_width, kv_width, capacity;
   float eps;
+  int frames;             // rows (0 or 1: decode); row t sits at position + t
 };
 
 struct AttnArgs {
@@ -99,6 +100,38 @@ struct PersistentArgs {
 };
 
 constexpr int kTimelineEvents = 480;
+
+// Prefill (many frames): Q8_0 GEMM with the reference's per-row block order.
+struct GemmArgs {
+  const int8_t* w;      // storage rows [*][K] int8
+  const void* ws;       // storage scales [*][K/32] (fp16 or fp32)
+  int rows;             // logical output rows (SwiGLU: ffn)
+  int K;
+  const int8_t* xq;     // [frames][K]
+  const float* xs;      // [frames][K/32]
+  int frames;
+  float* out;           // [frames][out_stride]
+  int out_stride;
+  const float* resid;   // [frames][out_stride] (residual epilogue; may equal out)
+  const float* bias;    // [rows] or null (plain epilogue)
+  int split_base, split_extra;  // SwiGLU storage: tiles of base(+1) gate rows then the same up rows
+};
+enum GemmOut { kGemmPlain = 0, kGemmResidual = 1, kGemmSwiGLU = 2 };
+
+struct PrefillAttnArgs {
+  const float* q;          // [frames][heads*head_size], normalised and rotated
+  const _Float16* kcache;  // [kv_heads][capacity][head_size] (this layer)
+  const _Float16* vcache;
+  float* out;              // [frames][heads*head_size]
+  int frames, position;    // query row t sits at position + t
+  int heads, kv_heads, head_size, capacity;
+  float divisor;
+};
+
+hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t s);
+hipError_t launch_norm_quantize_rows(const float* x, int frames, int K, const float* norm_w, float eps, int8_t* xq,
+                                     float* xs, hipStream_t s);
+hipError_t launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t s);
 
 bool persistent_shape_supported(int width, int heads, int kv_heads, int head_size, int ffn, int blocks);
 hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s);

@@ -27,61 +27,6 @@ struct ScaleFloat {
   static __device__ __forceinline__ float get(type v) { return v; }
 };
 
-// Workgroup barrier that orders LDS only. __syncthreads() also fences global
-// memory, which makes the compiler wait for every outstanding global load
-// (vmcnt(0)) before the barrier -- that would drain the weight stream the
-// GEMV issues ahead of its activation prologue.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// Block-wide sum of one double per thread (256 threads, 4 waves).
-__device__ __forceinline__ double block_sum_double(double v, double* scratch) {
-  v = wave_sum_double(v);
-  int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  if (lane == 0) scratch[wave] = v;
-  lds_barrier();
-  double total = 0.0;
-  int waves = (blockDim.x + kWave - 1) / kWave;
-  for (int i = 0; i < waves; ++i) total += scratch[i];
-  return total;
-}
-
-// RMSNorm inverse of src/FunAsrNet/TensorMath.Elementwise.cs:58-78 (rms):
-// 1f / sqrtf((float)(sum_sq / width) + eps). The double sum is a tree here;
-// the reference's sequential lane order only changes double rounding, which
-// reaches the float result with probability ~1e-7 per row.
-__device__ __forceinline__ float rms_inverse(double sum_sq, int width, float eps) {
-  float mean = (float)(sum_sq / (double)width);
-  return fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
-}
-
-// Quantise four consecutive values held by this lane; the 32-value block is
-// spread over 8 consecutive lanes (shuffle max of the absolute bit patterns).
-// Returns the four int8 codes packed little-endian; *scale gets the block's d.
-__device__ __forceinline__ int quantize4(float v0, float v1, float v2, float v3, float* scale) {
-  uint32_t m = f2u(v0) & 0x7fffffffu;
-  uint32_t t = f2u(v1) & 0x7fffffffu;
-  m = t > m ? t : m;
-  t = f2u(v2) & 0x7fffffffu;
-  m = t > m ? t : m;
-  t = f2u(v3) & 0x7fffffffu;
-  m = t > m ? t : m;
-#pragma unroll
-  for (int s = 1; s < 8; s <<= 1) {
-    uint32_t o = __shfl_xor(m, s, 8);
-    m = o > m ? o : m;
-  }
-  float inverse;
-  *scale = block_scale(m, &inverse);
-  uint32_t packed = (uint32_t)(uint8_t)quantize_value(v0, inverse) | ((uint32_t)(uint8_t)quantize_value(v1, inverse) << 8) |
-                    ((uint32_t)(uint8_t)quantize_value(v2, inverse) << 16) |
-                    ((uint32_t)(uint8_t)quantize_value(v3, inverse) << 24);
-  return (int)packed;
-}
-
 constexpr int kMaxChunks = kMaxK / (4 * kThreads);  // K = chunks * 1024: 4 values per lane per chunk
 
 template <typename Scale, int IN, int OUT, int PAIRS>
@@ -296,11 +241,13 @@ __global__ __launch_bounds__(128) void qk_prepare_kernel(QkArgs a) {
   __shared__ double red_s[2];
   __shared__ float y_s[128];
   const int c = threadIdx.x;
-  const int pos = *a.position;
+  const int frame = blockIdx.y;
+  const int pos = *a.position + frame;
   const int hs = a.head_size, half = hs >> 1;
   const bool is_q = blockIdx.x < a.heads;
   const int head = is_q ? blockIdx.x : blockIdx.x - a.heads;
-  const float* src = is_q ? a.qkv + head * hs : a.qkv + a.q_width + head * hs;
+  const float* qkv = a.qkv + (size_t)frame * (a.q_width + 2 * a.kv_width);
+  const float* src = is_q ? qkv + head * hs : qkv + a.q_width + head * hs;
   const float* w = is_q ? a.q_norm : a.k_norm;
   float v = src[c];
   double sq = wave_sum_double((double)v * (double)v);
@@ -320,11 +267,11 @@ __global__ __launch_bounds__(128) void qk_prepare_kernel(QkArgs a) {
     r = fadd(fmul(x0, sine[c - half]), fmul(x1, cosine[c - half]));
   }
   if (is_q) {
-    a.q_out[head * hs + c] = r;
+    a.q_out[(size_t)frame * a.q_width + head * hs + c] = r;
   } else {
     size_t row = ((size_t)head * a.capacity + pos) * hs + c;
     a.kcache[row] = to_half(r);
-    a.vcache[row] = to_half(a.qkv[a.q_width + a.kv_width + head * hs + c]);
+    a.vcache[row] = to_half(qkv[a.q_width + a.kv_width + head * hs + c]);
   }
 }
 
@@ -577,7 +524,7 @@ hipError_t launch_embed(const int8_t* q, const void* scales, bool half_scales, i
 
 hipError_t launch_qk_prepare(const QkArgs& a, hipStream_t s) {
   if (a.head_size != 128) return hipErrorInvalidValue;
-  qk_prepare_kernel<<<a.heads + a.kv_heads, 128, 0, s>>>(a);
+  qk_prepare_kernel<<<dim3(a.heads + a.kv_heads, a.frames > 1 ? a.frames : 1), 128, 0, s>>>(a);
   return hipGetLastError();
 }
 

@@ -350,47 +350,6 @@ __device__ __forceinline__ void quantize_input(const u64* act, const float* norm
   }
 }
 
-// One 16-byte piece of a K row (8 F16 channels 8i..8i+7) into the eight
-// channel-strided accumulators: acc[j] += q[8i+j] * k[8i+j].
-__device__ __forceinline__ void score8(float* acc, const uint4& kk, const float* q) {
-  const float4 q0 = *reinterpret_cast<const float4*>(q);
-  const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
-  const uint32_t w[4] = {kk.x, kk.y, kk.z, kk.w};
-  float k[8];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    k[2 * m] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu)));
-    k[2 * m + 1] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16)));
-  }
-  acc[0] = fadd(acc[0], fmul(q0.x, k[0]));
-  acc[1] = fadd(acc[1], fmul(q0.y, k[1]));
-  acc[2] = fadd(acc[2], fmul(q0.z, k[2]));
-  acc[3] = fadd(acc[3], fmul(q0.w, k[3]));
-  acc[4] = fadd(acc[4], fmul(q1.x, k[4]));
-  acc[5] = fadd(acc[5], fmul(q1.y, k[5]));
-  acc[6] = fadd(acc[6], fmul(q1.z, k[6]));
-  acc[7] = fadd(acc[7], fmul(q1.w, k[7]));
-}
-
-__device__ __forceinline__ float nan_max_p(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  return b > a ? b : a;
-}
-
-// nan_max_p over the 64 lanes of a wave (all active), in every lane.
-__device__ __forceinline__ float wave_max_nan(float m) {
-  m = nan_max_p(m, u2f(dpp_u32<kDppQuadXor1>(f2u(m))));
-  m = nan_max_p(m, u2f(dpp_u32<kDppQuadXor2>(f2u(m))));
-  m = nan_max_p(m, u2f(dpp_u32<kDppHalfMirror>(f2u(m))));
-  m = nan_max_p(m, u2f(dpp_u32<kDppMirror>(f2u(m))));
-  const float r0 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 0));
-  const float r1 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 16));
-  const float r2 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 32));
-  const float r3 = u2f((uint32_t)__builtin_amdgcn_readlane((int)f2u(m), 48));
-  return nan_max_p(nan_max_p(r0, r1), nan_max_p(r2, r3));
-}
-
 }  // namespace
 
 // Shape-specialised: W hidden width, HQ/HKV query/kv heads (head size 128),

@@ -1,0 +1,340 @@
+// Prefill kernels: QwenDecoder.Decode with frames > 1
+// (src/FunAsrNet/QwenDecoder.cs:161-271; grouped Q8 over frames,
+// TensorMath.QuantizedGroupAvx.cs:156-199 / QuantizedVnni.cs:77-126, whose
+// float order equals the single-frame one).
+//
+// q8_gemm_kernel: out[t][r] = sum over blocks b, in order, from 0f, of
+// ((float)dot_b * w_scale[r][b]) * x_scale[t][b]. The exact int32 32-term
+// block dots come from one v_mfma_i32_32x32x32_i8 per block with a zero
+// accumulator (a 32-row x 32-frame tile per wave); the fp32 steps then run
+// on the accumulator registers in block order, so the result is the one of
+// the reference's per-row loop for every frame. A workgroup (4 waves) owns a
+// 64-row x 64-frame tile; its row and frame scales are staged in LDS as fp32.
+//
+// Accumulator layout of v_mfma_i32_32x32x32_i8 (checked on gfx950): lane l,
+// register j holds C[m][n] with n = l % 32 and m = 8*(j/4) + 4*(l/32) + j%4;
+// the A (B) operand of lane l is 16 bytes of row (column) l % 32, lanes l and
+// l + 32 holding the two halves of the 32-byte block.
+#include "fah_device.h"
+#include "fah_internal.h"
+
+namespace fah {
+namespace {
+
+constexpr int kGT = 256;  // threads per GEMM workgroup
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+struct ScaleF16 {
+  using type = _Float16;
+  static __device__ __forceinline__ float get(type v) { return (float)v; }
+};
+struct ScaleF32 {
+  using type = float;
+  static __device__ __forceinline__ float get(type v) { return v; }
+};
+
+// Storage row of logical gate (kind 0) or up (kind 1) row r when the rows are
+// stored as tiles of count gate rows followed by the same count up rows; the
+// first `extra` tiles hold base + 1 rows, the others base.
+__device__ __forceinline__ int gate_up_row(int r, int kind, int base, int extra) {
+  const int big = extra * (base + 1);
+  int r0, count;
+  if (r < big) {
+    r0 = r / (base + 1) * (base + 1);
+    count = base + 1;
+  } else {
+    r0 = big + (r - big) / base * base;
+    count = base;
+  }
+  return 2 * r0 + kind * count + (r - r0);
+}
+
+template <class Scale, int OUT>
+__global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) float gemm_s[];
+  constexpr bool kSwiGLU = OUT == kGemmSwiGLU;
+  const int B = g.K >> 5;
+  float* ws_s = gemm_s;           // [B][64] tile-row scales
+  float* xs_s = gemm_s + 64 * B;  // [B][64] frame scales
+  float* up_s = gemm_s + 128 * B; // SwiGLU: [64 frames][32 rows] up sums
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int rw = wave & 1, fw = wave >> 1;
+  const int row0 = blockIdx.x * (kSwiGLU ? 32 : 64);  // logical rows
+  const int f0 = blockIdx.y * 64;
+  // Tile row tr (0..63) -> storage row, or -1 past the end. SwiGLU tiles
+  // hold 32 gate rows (tr < 32) and the matching 32 up rows.
+  auto storage_row = [&](int tr) -> int {
+    if (kSwiGLU) {
+      const int r = row0 + (tr & 31);
+      return r < g.rows ? gate_up_row(r, tr >> 5, g.split_base, g.split_extra) : -1;
+    }
+    const int r = row0 + tr;
+    return r < g.rows ? r : -1;
+  };
+  const typename Scale::type* ws = reinterpret_cast<const typename Scale::type*>(g.ws);
+  for (int i = tid; i < 64 * B; i += kGT) {
+    const int b = i >> 6, t = i & 63;
+    const int sr = storage_row(t);
+    ws_s[i] = sr >= 0 ? Scale::get(ws[(size_t)sr * B + b]) : 0.0f;
+    xs_s[i] = f0 + t < g.frames ? g.xs[(size_t)(f0 + t) * B + b] : 0.0f;
+  }
+  lds_barrier();
+
+  const int ml = lane & 31, half = lane >> 5;
+  const int sr = storage_row(32 * rw + ml);
+  const int frame = f0 + 32 * fw + ml;
+  const int8_t* ap = sr >= 0 ? g.w + (size_t)sr * g.K + 16 * half : nullptr;
+  const int8_t* bp = frame < g.frames ? g.xq + (size_t)frame * g.K + 16 * half : nullptr;
+  const v4i zero4 = {0, 0, 0, 0};
+  const v16i zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  float acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+
+  // Operands of four blocks are loaded one group ahead of their use.
+  auto load4 = [&](v4i* av, v4i* bv, int b0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int b = b0 + k;
+      av[k] = (ap && b < B) ? *reinterpret_cast<const v4i*>(ap + (size_t)b * 32) : zero4;
+      bv[k] = (bp && b < B) ? *reinterpret_cast<const v4i*>(bp + (size_t)b * 32) : zero4;
+    }
+  };
+  v4i a_cur[4], b_cur[4];
+  load4(a_cur, b_cur, 0);
+  for (int b0 = 0; b0 < B; b0 += 4) {
+    v4i a_nx[4], b_nx[4];
+    load4(a_nx, b_nx, b0 + 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int b = b0 + k;
+      if (b < B) {
+        const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_cur[k], b_cur[k], zero16, 0, 0, 0);
+        const float xsv = xs_s[b * 64 + 32 * fw + ml];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 w4 = *reinterpret_cast<const float4*>(ws_s + b * 64 + 32 * rw + 8 * q + 4 * half);
+          acc[4 * q + 0] = fadd(acc[4 * q + 0], fmul(fmul((float)c[4 * q + 0], w4.x), xsv));
+          acc[4 * q + 1] = fadd(acc[4 * q + 1], fmul(fmul((float)c[4 * q + 1], w4.y), xsv));
+          acc[4 * q + 2] = fadd(acc[4 * q + 2], fmul(fmul((float)c[4 * q + 2], w4.z), xsv));
+          acc[4 * q + 3] = fadd(acc[4 * q + 3], fmul(fmul((float)c[4 * q + 3], w4.w), xsv));
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      a_cur[k] = a_nx[k];
+      b_cur[k] = b_nx[k];
+    }
+  }
+
+  if (!kSwiGLU) {
+    if (frame < g.frames) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = row0 + 32 * rw + 8 * (j >> 2) + 4 * half + (j & 3);
+        if (r < g.rows) {
+          float v = acc[j];
+          float* o = g.out + (size_t)frame * g.out_stride + r;
+          if (OUT == kGemmResidual) v = fadd(v, g.resid[(size_t)frame * g.out_stride + r]);
+          if (OUT == kGemmPlain && g.bias) v = fadd(g.bias[r], v);
+          *o = v;
+        }
+      }
+    }
+  } else {
+    // SwiGLU (Elementwise.cs:167-196): gate waves meet their up rows in LDS.
+    if (rw == 1) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) up_s[(32 * fw + ml) * 32 + 8 * (j >> 2) + 4 * half + (j & 3)] = acc[j];
+    }
+    lds_barrier();
+    if (rw == 0 && frame < g.frames) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int m = 8 * (j >> 2) + 4 * half + (j & 3);
+        const int r = row0 + m;
+        if (r < g.rows) {
+          const float gv = acc[j], u = up_s[(32 * fw + ml) * 32 + m];
+          const float silu = fdiv(gv, fadd(1.0f, exp_ref(-gv)));
+          g.out[(size_t)frame * g.out_stride + r] = fmul(silu, u);
+        }
+      }
+    }
+  }
+}
+
+// RMSNorm (when norm_w is set) and activation quantisation of one row per
+// workgroup: the GEMV prologue's arithmetic (TensorMath.Elementwise.cs:26-100,
+// TensorMath.cs:378-412), four values per thread per 1024-value chunk.
+__global__ __launch_bounds__(256) void norm_quantize_rows_kernel(const float* x, int K, const float* norm_w, float eps,
+                                                                 int8_t* xq, float* xs) {
+  __shared__ double red_s[4];
+  constexpr int kChunks = 4;  // K <= 4096
+  const int frame = blockIdx.x, tid = threadIdx.x;
+  const float* row = x + (size_t)frame * K;
+  float4 v[kChunks];
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e = c * 1024 + 4 * tid;
+    v[c] = e < K ? *reinterpret_cast<const float4*>(row + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  if (norm_w) {
+    double sq = 0.0;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      sq += (double)v[c].x * (double)v[c].x + (double)v[c].y * (double)v[c].y;
+      sq += (double)v[c].z * (double)v[c].z + (double)v[c].w * (double)v[c].w;
+    }
+    const float inverse = rms_inverse(block_sum_double(sq, red_s), K, eps);
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const int e = c * 1024 + 4 * tid;
+      if (e < K) {
+        const float4 w = *reinterpret_cast<const float4*>(norm_w + e);
+        v[c].x = fmul(fmul(v[c].x, inverse), w.x);
+        v[c].y = fmul(fmul(v[c].y, inverse), w.y);
+        v[c].z = fmul(fmul(v[c].z, inverse), w.z);
+        v[c].w = fmul(fmul(v[c].w, inverse), w.w);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e = c * 1024 + 4 * tid;
+    if (e < K) {
+      float d;
+      const int packed = quantize4(v[c].x, v[c].y, v[c].z, v[c].w, &d);
+      *reinterpret_cast<int*>(xq + (size_t)frame * K + e) = packed;
+      if ((tid & 7) == 0) xs[(size_t)frame * (K >> 5) + (e >> 5)] = d;
+    }
+  }
+}
+
+// Causal attention of one query head for one frame (row t at position
+// p + t sees positions [0, p + t]): scores one position per lane (eight
+// channel-strided accumulators and their pairwise tree), exact softmax with
+// a double denominator, time-ordered value sums one lane per channel --
+// the decode arithmetic (AttentionAvx.cs:74-224, SoftmaxAvx.cs:11-58) applied
+// per row, as the oracle restates the prefill path (QwenDecoder.cs:206-224).
+__global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float attn_s[];  // probabilities [n]
+  __shared__ __attribute__((aligned(16))) float q_s[128];
+  __shared__ float tmax_s[4];
+  __shared__ double lane_s[8];
+  __shared__ float inv_s;
+  const int head = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hs = 128, kh = head / (a.heads / a.kv_heads);
+  const int pos = a.position + t, n = pos + 1;
+  const float* q = a.q + ((size_t)t * a.heads + head) * hs;
+  const _Float16* kc = a.kcache + (size_t)kh * a.capacity * hs;
+  const _Float16* vc = a.vcache + (size_t)kh * a.capacity * hs;
+  float* p_s = attn_s;
+  if (tid < hs) q_s[tid] = q[tid];
+  lds_barrier();
+
+  for (int s = tid; s < n; s += 256) {
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)s * hs);
+#pragma unroll
+    for (int i0 = 0; i0 < 16; i0 += 4) {
+      uint4 kk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kk[i] = row[i0 + i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) score8(acc, kk[i], q_s + 8 * (i0 + i));
+    }
+    const float sc = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
+    p_s[s] = fdiv(sc, a.divisor);
+  }
+  lds_barrier();
+  float m = -__builtin_inff();
+  for (int s = tid; s < n; s += 256) m = nan_max_p(m, p_s[s]);
+  m = wave_max_nan(m);
+  if (lane == 0) tmax_s[wave] = m;
+  lds_barrier();
+  const float mx = nan_max_p(nan_max_p(tmax_s[0], tmax_s[1]), nan_max_p(tmax_s[2], tmax_s[3]));
+  for (int s = tid; s < n; s += 256) p_s[s] = exp_ref(fadd(p_s[s], -mx));
+  lds_barrier();
+  const int full = n & ~7;
+  if (tid < 8) {
+    double acc = 0.0;
+    int s = tid;
+    for (; s + 56 < full; s += 64) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = p_s[s + 8 * k];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc = acc + (double)v[k];
+    }
+    for (; s < full; s += 8) acc = acc + (double)p_s[s];
+    lane_s[tid] = acc;
+  }
+  lds_barrier();
+  if (tid == 0) {
+    double sum = ((lane_s[0] + lane_s[4]) + (lane_s[1] + lane_s[5])) + ((lane_s[2] + lane_s[6]) + (lane_s[3] + lane_s[7]));
+    for (int s = full; s < n; ++s) sum = sum + (double)p_s[s];
+    inv_s = (float)(1.0 / sum);
+  }
+  lds_barrier();
+  const float inverse = inv_s;
+  for (int s = tid; s < n; s += 256) p_s[s] = fmul(p_s[s], inverse);
+  lds_barrier();
+  if (tid < hs) {
+    const _Float16* v = vc + tid;
+    float acc = 0.0f;
+    int s = 0;
+    for (; s + 16 <= n; s += 16) {
+      float x[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = from_half(v[(size_t)(s + k) * hs]);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc = fadd(acc, fmul(x[k], p_s[s + k]));
+    }
+    for (; s < n; ++s) acc = fadd(acc, fmul(from_half(v[(size_t)s * hs]), p_s[s]));
+    a.out[((size_t)t * a.heads + head) * hs + tid] = acc;
+  }
+}
+
+template <class Scale>
+hipError_t launch_gemm_scaled(const GemmArgs& g, int out, hipStream_t s) {
+  const int B = g.K / 32;
+  const int rows_per_wg = out == kGemmSwiGLU ? 32 : 64;
+  dim3 grid((g.rows + rows_per_wg - 1) / rows_per_wg, (g.frames + 63) / 64);
+  const size_t lds = (size_t)128 * B * 4 + (out == kGemmSwiGLU ? 64 * 32 * 4 : 0);
+  switch (out) {
+    case kGemmPlain: q8_gemm_kernel<Scale, kGemmPlain><<<grid, kGT, lds, s>>>(g); break;
+    case kGemmResidual: q8_gemm_kernel<Scale, kGemmResidual><<<grid, kGT, lds, s>>>(g); break;
+    case kGemmSwiGLU: q8_gemm_kernel<Scale, kGemmSwiGLU><<<grid, kGT, lds, s>>>(g); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t s) {
+  // The row and frame scales of the whole K range live in LDS (512 B per
+  // block): K <= 3072 keeps the tile, with the SwiGLU exchange, under 64 KiB.
+  if (g.K % 32 != 0 || g.K > 3072 || g.rows < 1 || g.frames < 1) return hipErrorInvalidValue;
+  if (out == kGemmSwiGLU && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
+  return half_scales ? launch_gemm_scaled<ScaleF16>(g, out, s) : launch_gemm_scaled<ScaleF32>(g, out, s);
+}
+
+hipError_t launch_norm_quantize_rows(const float* x, int frames, int K, const float* norm_w, float eps, int8_t* xq,
+                                     float* xs, hipStream_t s) {
+  if (K % 32 != 0 || K > 4096 || frames < 1) return hipErrorInvalidValue;
+  norm_quantize_rows_kernel<<<frames, 256, 0, s>>>(x, K, norm_w, eps, xq, xs);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t s) {
+  if (a.head_size != 128 || a.frames < 1 || a.heads % a.kv_heads != 0) return hipErrorInvalidValue;
+  const int n = a.position + a.frames;
+  if (n > a.capacity || (size_t)n * 4 > 60 * 1024) return hipErrorInvalidValue;
+  attn_prefill_kernel<<<dim3(a.heads, a.frames), 256, (size_t)n * 4, s>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace fah
