@@ -72,6 +72,121 @@ def gemv_roofline(backend, weights, repeats: int = 40):
     }
 
 
+GEMV_SHAPES = [(1024, 2048), (1024, 1024), (2048, 1024), (1024, 3072), (3072, 1024), (1024, 151936)]
+MFMA_PEAK_INT8_OPS = 5.0e15
+
+
+def gemv_sweep(backend, rotate_bytes: int = 512 << 20):
+    """Q8_0 GEMV at the decoder's projection shapes (K -> N), each launch on
+    a different copy of the weight, rotating through at least `rotate_bytes`
+    so that launches stream from HBM rather than the 256 MB MALL."""
+    from funasrnet_amd import device
+    from funasrnet_amd.model import Q8Tensor
+
+    rng = np.random.default_rng(3)
+    results = []
+    for K, N in GEMV_SHAPES:
+        q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+        sc = (np.abs(rng.standard_normal((N, K // 32))) * 0.02 / 127).astype(np.float16).astype(np.float32)
+        tensor = Q8Tensor("sweep", q, sc)
+        algorithmic = N * K * 34 // 32 + K + 4 * (K // 32) + 4 * N
+        copies = [backend.weight(tensor) for _ in range(max(2, -(-rotate_bytes // algorithmic)))]
+        x = rng.standard_normal(K).astype(np.float32)
+        xd = device.DeviceArray.from_numpy(x)
+        xq = device.DeviceArray(K, np.int8)
+        xs = device.DeviceArray(K // 32, np.float32)
+        out = device.DeviceArray(N, np.float32)
+        backend.quantize_device(xd.ptr, K, xq.ptr, xs.ptr)
+        for c in copies:
+            backend.gemv_device(xq.ptr, xs.ptr, 1, c, out.ptr)
+        backend.synchronize()
+        start, end = device.Event(), device.Event()
+        start.record(backend.stream)
+        for c in copies:
+            backend.gemv_device(xq.ptr, xs.ptr, 1, c, out.ptr)
+        end.record(backend.stream)
+        end.synchronize()
+        avg_us = start.elapsed_ms(end) * 1000.0 / len(copies)
+        gbs = algorithmic / (avg_us * 1e-6) / 1e9
+        results.append({"shape": f"{K}->{N}", "avg_us": round(avg_us, 3), "algorithmic_bytes": algorithmic,
+                        "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": len(copies)})
+        for c in copies:
+            c.close()
+        for arr in (xd, xq, xs, out):
+            arr.free()
+    return results
+
+
+def prefill_ttft(backend, weights, rows_list=(375, 750)):
+    """Time to first token: one decode call on `rows` N(0,1) rows from
+    position 0 (the MFMA GEMM prefill) plus the greedy pick, wall clock, best
+    of three. The call copies the rows in (rows x 4 KiB) and the logits out
+    (0.6 MB) over PCIe; both are inside the time."""
+    from funasrnet_amd import device
+    from funasrnet_amd.hip import HipDecoder
+
+    cfg = weights.config
+    qw, kvw = cfg.heads * cfg.head_size, cfg.kv_heads * cfg.head_size
+    per_row = 2 * cfg.layers * (cfg.width * (qw + 2 * kvw) + qw * cfg.width + 3 * cfg.width * cfg.ffn)
+    dec = HipDecoder(backend, weights, capacity=max(rows_list) + 8)
+    out = []
+    try:
+        for rows in rows_list:
+            x = np.random.default_rng(rows).standard_normal((rows, cfg.width)).astype(np.float32)
+            dec.reset()
+            dec.decode(x, rows)
+            best = None
+            for _ in range(3):
+                dec.reset()
+                device.synchronize()
+                t0 = time.perf_counter()
+                dec.decode(x, rows)
+                dec.greedy()
+                ms = (time.perf_counter() - t0) * 1e3
+                best = ms if best is None else min(best, ms)
+            ops = per_row * rows + 2 * cfg.vocab * cfg.width
+            out.append({"rows": rows, "ttft_ms": round(best, 3), "int8_ops": int(ops),
+                        "achieved_tops": round(ops / (best * 1e-3) / 1e12, 2),
+                        "frac_of_int8_mfma_peak": round(ops / (best * 1e-3) / MFMA_PEAK_INT8_OPS, 5)})
+    finally:
+        dec.close()
+    return out
+
+
+def long_kv(backend, weights, positions: int = 4096, steps: int = 64):
+    """Decode with a long cache: K/V rows [0, positions) pre-filled with
+    fp16(N(0,1)) in every layer, one row decoded at `positions`, then `steps`
+    timed greedy steps. Algorithmic bytes per token include the K/V reads."""
+    from funasrnet_amd import device
+    from funasrnet_amd.hip import HipDecoder
+
+    cfg = weights.config
+    dec = HipDecoder(backend, weights, capacity=positions + steps + 64)
+    try:
+        rng = np.random.default_rng(4)
+        width = cfg.kv_heads * cfg.head_size
+        for layer in range(cfg.layers):
+            k = rng.standard_normal((positions, width)).astype(np.float16)
+            v = rng.standard_normal((positions, width)).astype(np.float16)
+            dec.kv_write(layer, k, v)
+        dec.set_position(positions)
+        dec.decode(rng.standard_normal((1, cfg.width)).astype(np.float32), 1)
+        device.synchronize()
+        start, end = device.Event(), device.Event()
+        start.record(backend.stream)
+        dec.generate(steps)
+        end.record(backend.stream)
+        end.synchronize()
+        ms = start.elapsed_ms(end) / steps
+        kv = sum(114688 * (positions + 1 + i + 1) for i in range(steps)) / steps
+        step_bytes = cfg.weight_bytes_per_token() + kv
+        gbs = step_bytes / (ms * 1e-3) / 1e9
+        return {"positions": positions, "steps": steps, "ms_per_step": round(ms, 4), "tok_s": round(1000.0 / ms, 2),
+                "bytes_per_token": int(step_bytes), "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    finally:
+        dec.close()
+
+
 def cpu_baseline(weights, prefix, tokens: int, threads: int, seconds_target: float):
     """The oracle (C restatement of the reference x64 path) on this host.
 
@@ -111,6 +226,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-tokens", type=int, default=128, help="decode steps per CPU pass")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU sample length")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the GEMV sweep, prefill and long-cache measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
@@ -157,6 +274,11 @@ def main() -> int:
 
     gemv = gemv_roofline(backend, weights)
     dec.close()
+    extra = {}
+    if not args.no_extra:
+        extra["gemv_sweep"] = gemv_sweep(backend)
+        extra["prefill"] = prefill_ttft(backend, weights)
+        extra["long_kv"] = long_kv(backend, weights)
     backend.close()
 
     baseline = None
@@ -211,6 +333,7 @@ def main() -> int:
         "decode_step": {"wall_s": round(wall, 4), "deterministic_vs_warmup": deterministic},
         "cpu_baseline": baseline,
     }
+    line.update(extra)
     print(json.dumps(line))
     return 0
 

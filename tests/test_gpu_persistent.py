@@ -82,3 +82,58 @@ def test_persistent_against_oracle_tokens(backend, oracle_lib):
     finally:
         fast.close()
         ref.close()
+
+
+@pytest.mark.parametrize("shape", ["small", "qwen3"])
+def test_long_cache_matches_graph_path(backend, oracle_lib, shape):
+    """A cache pre-filled with 4096 F16 N(0,1) rows in every layer: the
+    persistent kernel (staged rows, spill area and global rows) and the
+    per-kernel path (16 channel slices at this capacity) give identical
+    logits bits, K/V rows and tokens; the small shape matches the oracle."""
+    cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
+    w = model.synthetic(cfg, seed=12)
+    positions, capacity, steps = 4096, 4224, 8
+    rng = np.random.default_rng(13)
+    kv = [(rng.standard_normal((positions, cfg.kv_width)).astype(np.float16),
+           rng.standard_normal((positions, cfg.kv_width)).astype(np.float16)) for _ in range(cfg.layers)]
+    x = rng.standard_normal((1, cfg.width)).astype(np.float32)
+    fast = _decoder(backend, w, True, capacity)
+    slow = _decoder(backend, w, False, capacity)
+    try:
+        assert fast.persistent and not slow.persistent
+        for d in (fast, slow):
+            for layer, (k, v) in enumerate(kv):
+                d.kv_write(layer, k, v)
+            d.set_position(positions)
+        print(f"long cache {shape} positions={positions}", flush=True)
+        lf = fast.decode(x, 1)
+        ls = slow.decode(x, 1)
+        assert np.array_equal(lf.view(np.uint32), ls.view(np.uint32))
+        tf = fast.generate(steps)
+        ts = slow.generate(steps)
+        assert tf.tolist() == ts.tolist()
+        for layer in (0, cfg.layers - 1):
+            kf, vf = fast.kv_read(layer, positions + 1 + steps)
+            ks, vs = slow.kv_read(layer, positions + 1 + steps)
+            assert np.array_equal(kf.view(np.uint16), ks.view(np.uint16))
+            assert np.array_equal(vf.view(np.uint16), vs.view(np.uint16))
+            assert np.array_equal(kf[:positions * cfg.kv_width].view(np.uint16), kv[layer][0].view(np.uint16).ravel())
+        if shape == "small":
+            ref = oracle_lib.Decoder(w, capacity=capacity)
+            try:
+                for layer, (k, v) in enumerate(kv):
+                    ref.set_kv(layer, k.astype(np.float32), v.astype(np.float32))
+                ref.set_position(positions)
+                lr = ref.decode(x, 1)
+                assert np.abs(lf.astype(np.float64) - lr).max() <= 1e-2
+                expected = []
+                for _ in range(steps):
+                    t = oracle_lib.greedy(lr)
+                    expected.append(t)
+                    lr = ref.decode(ref.embed([t]), 1)
+                assert tf.tolist() == expected
+            finally:
+                ref.close()
+    finally:
+        fast.close()
+        slow.close()
