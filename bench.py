@@ -187,6 +187,42 @@ def long_kv(backend, weights, positions: int = 4096, steps: int = 64):
         dec.close()
 
 
+def sessions_decode(backend, weights, count: int = 16, steps: int = 128, prefix: int = 150, warmup: int = 4):
+    """Lock-step decode of `count` sessions over one weight set: 150-row
+    N(0,1) prefixes (seeds 1..count), `warmup` lock-step steps (the first
+    call captures the step), then `steps` timed steps (wall clock around one
+    call). Algorithmic bytes per step: the weights once plus every session's
+    K/V rows."""
+    from funasrnet_amd.hip import HipDecoder
+
+    cfg = weights.config
+    capacity = prefix + warmup + steps + 8
+    parent = HipDecoder(backend, weights, capacity=capacity)
+    sessions = [parent] + [parent.session() for _ in range(count - 1)]
+    try:
+        for seed, d in enumerate(sessions, 1):
+            x = np.random.default_rng(seed).standard_normal((prefix, cfg.width)).astype(np.float32)
+            d.decode(x, prefix)
+        HipDecoder.generate_sessions(sessions, warmup)
+        t0 = time.perf_counter()
+        toks = HipDecoder.generate_sessions(sessions, steps)
+        wall = time.perf_counter() - t0
+        ms = wall * 1e3 / steps
+        start = prefix + warmup
+        kv = count * sum(114688 * (start + i + 1) for i in range(steps)) / steps
+        step_bytes = cfg.weight_bytes_per_token() + kv
+        gbs = step_bytes / (ms * 1e-3) / 1e9
+        distinct = len({tuple(t) for t in toks.tolist()})
+        return {"sessions": count, "steps": steps, "ms_per_step": round(ms, 4),
+                "tok_s": round(count * 1000.0 / ms, 1), "bytes_per_step": int(step_bytes),
+                "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "distinct_token_rows": distinct}
+    finally:
+        for d in sessions[1:]:
+            d.close()
+        parent.close()
+
+
 def cpu_baseline(weights, prefix, tokens: int, threads: int, seconds_target: float):
     """The oracle (C restatement of the reference x64 path) on this host.
 
@@ -227,7 +263,7 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=128, help="decode steps per CPU pass")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU sample length")
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the GEMV sweep, prefill and long-cache measurements")
+                    help="skip the GEMV sweep, prefill, long-cache and sessions measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
@@ -279,6 +315,7 @@ def main() -> int:
         extra["gemv_sweep"] = gemv_sweep(backend)
         extra["prefill"] = prefill_ttft(backend, weights)
         extra["long_kv"] = long_kv(backend, weights)
+        extra["sessions"] = sessions_decode(backend, weights)
     backend.close()
 
     baseline = None

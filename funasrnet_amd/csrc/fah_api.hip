@@ -6,6 +6,7 @@
 #include "../../include/funasr_hip.h"
 #include "fah_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -146,6 +147,22 @@ int pick_group_rows(int rows, int K, int min_rows, bool even) {
   return group;
 }
 
+// Row buffers and the captured step of one lock-step batch of sessions. The
+// context keeps the last one while its sessions live, so repeated calls on
+// the same sessions replay the same graph.
+struct SessionBatch {
+  std::vector<fah_decoder*> members;
+  int max_positions = 0;
+  DeviceBuffer table, x, a, qkv, q, h, xq, xs, logits;
+  hipGraphExec_t graph = nullptr;
+  SessionBatch() = default;
+  SessionBatch(const SessionBatch&) = delete;
+  SessionBatch& operator=(const SessionBatch&) = delete;
+  ~SessionBatch() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+  }
+};
+
 }  // namespace
 
 struct fah_context {
@@ -156,6 +173,7 @@ struct fah_context {
   int64_t minimum_operations = 250000;
   DeviceBuffer in, out, q, s;
   std::string name;
+  std::unique_ptr<SessionBatch> batch;  // last lock-step batch (its sessions alive)
 };
 
 struct fah_weight {
@@ -171,32 +189,42 @@ struct DeviceMatrix {
   int rows = 0, cols = 0, group_rows = 1;
 };
 
-struct fah_decoder {
-  fah_context* context = nullptr;
-  fah_decoder_config cfg{};
+// Device weights of one decoder, shared by every session created from it.
+struct DecoderWeights {
   bool half_scales = true;
-  int q_width = 0, kv_width = 0;
   std::vector<DeviceMatrix> qkv, wo, gateup, down;
   std::vector<DeviceBuffer> attn_norm, q_norm, k_norm, ffn_norm;
   DeviceMatrix embed, lm_head;  // lm_head aliases embed when tied
   bool tied = true;
-  DeviceBuffer output_norm, rope_cos, rope_sin, kcache, vcache;
+  DeviceBuffer output_norm;
+  int64_t weight_bytes = 0;
+  // Persistent kernel's per-layer pointer table (when the layout is the
+  // persistent one) and the gate/up storage tiles: base rows, the first
+  // `extra` tiles one more.
+  bool persistent_layout = false;
+  DeviceBuffer layer_table;
+  int gu_base = 1, gu_extra = 0;
+};
+
+struct fah_decoder {
+  fah_context* context = nullptr;
+  fah_decoder_config cfg{};
+  int q_width = 0, kv_width = 0;
+  std::shared_ptr<DecoderWeights> wt;
+  DeviceBuffer rope_cos, rope_sin, kcache, vcache;
   DeviceBuffer x, qkv_out, qh, scores, attn, a, h, logits, keys, token, position, history, history_count, staging;
   int lm_groups = 0;
   int host_position = 0;
   bool have_logits = false;
   hipGraphExec_t graph_row = nullptr, graph_logits = nullptr, graph_step = nullptr;
-  int64_t weight_bytes = 0;
   // Persistent single-launch step (one workgroup per CU), when the shape has
   // an instantiation and the device has the CUs for it.
   bool persistent = false;
   int blocks = 0;
-  DeviceBuffer layer_table, tx, tqkv, tatt, ta, th, tkeys, epoch, error, timeline;
+  DeviceBuffer tx, tqkv, tatt, ta, th, tkeys, epoch, error, timeline;
   fah::PersistentArgs pargs{};
-  // Prefill (decode of many rows at once): row buffers grown on demand, and
-  // the gate/up storage tiles (base rows, the first `extra` tiles one more).
-  DeviceBuffer pf_x, pf_a, pf_qkv, pf_q, pf_attn, pf_h, pf_xq, pf_xs;
-  int gu_base = 1, gu_extra = 0;
+  // Prefill (decode of many rows at once): row buffers grown on demand.
+  DeviceBuffer pf_x, pf_a, pf_qkv, pf_q, pf_h, pf_xq, pf_xs;
 };
 
 namespace {
@@ -256,19 +284,19 @@ void enqueue_layers(fah_decoder* d, hipStream_t s) {
   const fah_decoder_config& c = d->cfg;
   int* pos = d->position.as<int>();
   for (int l = 0; l < c.layers; ++l) {
-    fah::GemvArgs g = gemv_args(d->qkv[l]);
+    fah::GemvArgs g = gemv_args(d->wt->qkv[l]);
     g.x = d->x.as<float>();
-    g.norm_w = d->attn_norm[l].as<float>();
+    g.norm_w = d->wt->attn_norm[l].as<float>();
     g.eps = c.eps;
     g.out = d->qkv_out.as<float>();
-    g.out_rows = d->qkv[l].rows;
-    check(fah::launch_gemv(g, d->half_scales, fah::kInputNorm, fah::kOutPlain, 1, s), "qkv gemv");
+    g.out_rows = d->wt->qkv[l].rows;
+    check(fah::launch_gemv(g, d->wt->half_scales, fah::kInputNorm, fah::kOutPlain, 1, s), "qkv gemv");
 
     size_t kv_layer = (size_t)c.kv_heads * c.capacity * c.head_size;
     fah::QkArgs qa{};
     qa.qkv = d->qkv_out.as<float>();
-    qa.q_norm = d->q_norm[l].as<float>();
-    qa.k_norm = d->k_norm[l].as<float>();
+    qa.q_norm = d->wt->q_norm[l].as<float>();
+    qa.k_norm = d->wt->k_norm[l].as<float>();
     qa.rope_cos = d->rope_cos.as<float>();
     qa.rope_sin = d->rope_sin.as<float>();
     qa.position = pos;
@@ -298,44 +326,156 @@ void enqueue_layers(fah_decoder* d, hipStream_t s) {
     at.divisor = std::sqrt((float)c.head_size);
     check(fah::launch_attention(at, 16, s), "attention");
 
-    fah::GemvArgs o = gemv_args(d->wo[l]);
+    fah::GemvArgs o = gemv_args(d->wt->wo[l]);
     o.x = d->attn.as<float>();
     o.out = d->a.as<float>();
     o.out_rows = c.width;
     o.resid = d->x.as<float>();
-    check(fah::launch_gemv(o, d->half_scales, fah::kInputFloat, fah::kOutResidual, 1, s), "o gemv");
+    check(fah::launch_gemv(o, d->wt->half_scales, fah::kInputFloat, fah::kOutResidual, 1, s), "o gemv");
 
-    fah::GemvArgs gu = gemv_args(d->gateup[l]);
+    fah::GemvArgs gu = gemv_args(d->wt->gateup[l]);
     gu.x = d->a.as<float>();
-    gu.norm_w = d->ffn_norm[l].as<float>();
+    gu.norm_w = d->wt->ffn_norm[l].as<float>();
     gu.eps = c.eps;
     gu.out = d->h.as<float>();
     gu.out_rows = c.ffn;
-    check(fah::launch_gemv(gu, d->half_scales, fah::kInputNorm, fah::kOutSwiGLU, 1, s), "gate/up gemv");
+    check(fah::launch_gemv(gu, d->wt->half_scales, fah::kInputNorm, fah::kOutSwiGLU, 1, s), "gate/up gemv");
 
-    fah::GemvArgs dn = gemv_args(d->down[l]);
+    fah::GemvArgs dn = gemv_args(d->wt->down[l]);
     dn.x = d->h.as<float>();
     dn.out = d->x.as<float>();
     dn.out_rows = c.width;
     dn.resid = d->a.as<float>();
-    check(fah::launch_gemv(dn, d->half_scales, fah::kInputFloat, fah::kOutResidual, 1, s), "down gemv");
+    check(fah::launch_gemv(dn, d->wt->half_scales, fah::kInputFloat, fah::kOutResidual, 1, s), "down gemv");
   }
 }
 
-const DeviceMatrix& head_matrix(const fah_decoder* d) { return d->tied ? d->embed : d->lm_head; }
+const DeviceMatrix& head_matrix(const fah_decoder* d) { return d->wt->tied ? d->wt->embed : d->wt->lm_head; }
 
 void enqueue_head(fah_decoder* d, hipStream_t s) {
   fah::GemvArgs g = gemv_args(head_matrix(d));
   g.x = d->x.as<float>();
-  g.norm_w = d->output_norm.as<float>();
+  g.norm_w = d->wt->output_norm.as<float>();
   g.eps = d->cfg.eps;
   g.out = d->logits.as<float>();
   g.out_rows = d->cfg.vocab;
   g.partial_keys = d->keys.as<unsigned long long>();
-  check(fah::launch_gemv(g, d->half_scales, fah::kInputNorm, fah::kOutGreedy, 1, s), "lm_head gemv");
+  check(fah::launch_gemv(g, d->wt->half_scales, fah::kInputNorm, fah::kOutGreedy, 1, s), "lm_head gemv");
   check(fah::launch_greedy_reduce(d->keys.as<unsigned long long>(), d->lm_groups, d->logits.as<float>(),
                                   d->token.as<int>(), s),
         "greedy");
+}
+
+// Per-decoder state over shared weights: RoPE tables for this capacity, the
+// F16 KV cache, row buffers, token/position/history words and, on the
+// persistent path, the tagged exchange buffers and the kernel's arguments.
+void init_state(fah_decoder* d, hipStream_t s) {
+  const fah_decoder_config& k = d->cfg;
+  const int q_width = d->q_width, kv_width = d->kv_width, qkv_rows = q_width + 2 * kv_width;
+  const int nb = 256;
+  d->blocks = nb;
+  const DeviceMatrix& head = head_matrix(d);
+  // RoPE table with the C runtime's powf/cosf/sinf (QwenDecoder.cs:78-95).
+  int half_hs = k.head_size / 2;
+  std::vector<float> freq(half_hs), cs((size_t)k.capacity * half_hs), sn((size_t)k.capacity * half_hs);
+  for (int i = 0; i < half_hs; ++i) freq[i] = powf(k.rope_base, (-2.0f * (float)i) / (float)k.head_size);
+  for (int t = 0; t < k.capacity; ++t)
+    for (int i = 0; i < half_hs; ++i) {
+      float angle = (float)t * freq[i];
+      cs[(size_t)t * half_hs + i] = cosf(angle);
+      sn[(size_t)t * half_hs + i] = sinf(angle);
+    }
+  upload(d->rope_cos, cs.data(), cs.size() * 4, s);
+  upload(d->rope_sin, sn.data(), sn.size() * 4, s);
+
+  size_t kv_elems = (size_t)k.layers * k.kv_heads * k.capacity * k.head_size;
+  d->kcache.allocate(kv_elems * 2);
+  d->vcache.allocate(kv_elems * 2);
+  check(hipMemsetAsync(d->kcache.ptr, 0, kv_elems * 2, s), "memset kv");
+  check(hipMemsetAsync(d->vcache.ptr, 0, kv_elems * 2, s), "memset kv");
+  d->x.allocate((size_t)k.width * 4);
+  d->qkv_out.allocate((size_t)qkv_rows * 4);
+  d->qh.allocate((size_t)q_width * 4);
+  d->scores.allocate((size_t)k.heads * k.capacity * 4);
+  d->attn.allocate((size_t)q_width * 4);
+  d->a.allocate((size_t)k.width * 4);
+  d->h.allocate((size_t)k.ffn * 4);
+  d->logits.allocate((size_t)k.vocab * 4);
+  d->lm_groups = (k.vocab + head.group_rows - 1) / head.group_rows;
+  d->keys.allocate((size_t)d->lm_groups * 8);
+  d->token.allocate(16);
+  d->position.allocate(16);
+  d->history.allocate((size_t)k.capacity * 4 + 16);
+  d->history_count.allocate(16);
+  check(hipMemsetAsync(d->token.ptr, 0, 16, s), "memset");
+  check(hipMemsetAsync(d->position.ptr, 0, 16, s), "memset");
+  check(hipMemsetAsync(d->history_count.ptr, 0, 16, s), "memset");
+  if (d->persistent) {
+    auto tagged = [&](DeviceBuffer& b, size_t words) {
+      b.allocate(words * 8);
+      check(hipMemsetAsync(b.ptr, 0, words * 8, s), "memset tagged");
+    };
+    tagged(d->tx, k.width);
+    tagged(d->tqkv, qkv_rows);
+    tagged(d->tatt, q_width);
+    tagged(d->ta, k.width);
+    tagged(d->th, k.ffn);
+    tagged(d->tkeys, 2 * nb);
+    d->epoch.allocate(16);
+    d->error.allocate(16);
+    unsigned one = 1;
+    check(hipMemcpyAsync(d->epoch.ptr, &one, 4, hipMemcpyHostToDevice, s), "epoch");
+    check(hipMemsetAsync(d->error.ptr, 0, 16, s), "memset error");
+    fah::PersistentArgs& a = d->pargs;
+    a.layer_table = d->wt->layer_table.as<fah::PersistentLayer>();
+    a.layers = k.layers;
+    a.embed_q = d->wt->embed.q.as<int8_t>();
+    a.embed_s = d->wt->embed.s.as<_Float16>();
+    a.head_q = head.q.as<int8_t>();
+    a.head_s = head.s.as<_Float16>();
+    a.output_norm = d->wt->output_norm.as<float>();
+    a.rope_cos = d->rope_cos.as<float>();
+    a.rope_sin = d->rope_sin.as<float>();
+    a.kcache = d->kcache.as<_Float16>();
+    a.vcache = d->vcache.as<_Float16>();
+    a.width = k.width;
+    a.heads = k.heads;
+    a.kv_heads = k.kv_heads;
+    a.head_size = k.head_size;
+    a.ffn = k.ffn;
+    a.vocab = k.vocab;
+    a.capacity = k.capacity;
+    a.q_width = q_width;
+    a.kv_width = kv_width;
+    a.eps = k.eps;
+    a.divisor = std::sqrt((float)k.head_size);
+    a.rq = qkv_rows / nb;
+    a.ro = k.width / nb;
+    a.rgu = k.ffn / nb;
+    a.rd = k.width / nb;
+    a.head_chunks = (k.vocab + 31) / 32;
+    a.npre = fah::persistent_max_positions();
+    a.tx = d->tx.as<unsigned long long>();
+    a.tqkv = d->tqkv.as<unsigned long long>();
+    a.tatt = d->tatt.as<unsigned long long>();
+    a.ta = d->ta.as<unsigned long long>();
+    a.th = d->th.as<unsigned long long>();
+    a.tkeys = d->tkeys.as<unsigned long long>();
+    a.x_in = d->x.as<float>();
+    a.position = d->position.as<int>();
+    a.token = d->token.as<int>();
+    a.history = d->history.as<int>();
+    a.history_count = d->history_count.as<int>();
+    a.epoch = d->epoch.as<unsigned>();
+    a.error = d->error.as<unsigned>();
+    a.logits = d->logits.as<float>();
+    const char* tl = std::getenv("FAH_TIMELINE");
+    if (tl && tl[0] == '1') {
+      d->timeline.allocate((size_t)nb * fah::kTimelineEvents * 8);
+      check(hipMemsetAsync(d->timeline.ptr, 0, (size_t)nb * fah::kTimelineEvents * 8, s), "memset timeline");
+      a.timeline = d->timeline.as<unsigned long long>();
+    }
+  }
 }
 
 void enqueue_kind(fah_decoder* d, int kind, hipStream_t s);
@@ -359,7 +499,6 @@ void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_
     d->pf_a.ensure((size_t)T * c.width * 4);
     d->pf_qkv.ensure((size_t)T * qkv_rows * 4);
     d->pf_q.ensure((size_t)T * d->q_width * 4);
-    d->pf_attn.ensure((size_t)T * d->q_width * 4);
     d->pf_h.ensure((size_t)T * c.ffn * 4);
     d->pf_xq.ensure((size_t)T * widest);
     d->pf_xs.ensure((size_t)T * widest / 32 * 4);
@@ -379,19 +518,19 @@ void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_
       g.out = out;
       g.out_stride = stride;
       g.resid = resid;
-      g.split_base = d->gu_base;
-      g.split_extra = d->gu_extra;
-      check(fah::launch_gemm(g, d->half_scales, mode, s), "prefill gemm");
+      g.split_base = d->wt->gu_base;
+      g.split_extra = d->wt->gu_extra;
+      check(fah::launch_gemm(g, d->wt->half_scales, mode, s), "prefill gemm");
     };
     for (int l = 0; l < c.layers; ++l) {
-      check(fah::launch_norm_quantize_rows(d->pf_x.as<float>(), T, c.width, d->attn_norm[l].as<float>(), c.eps, xq, xs,
+      check(fah::launch_norm_quantize_rows(d->pf_x.as<float>(), T, c.width, d->wt->attn_norm[l].as<float>(), c.eps, xq, xs,
                                            s),
             "prefill attn_norm");
-      gemm(d->qkv[l], qkv_rows, d->pf_qkv.as<float>(), qkv_rows, nullptr, fah::kGemmPlain);
+      gemm(d->wt->qkv[l], qkv_rows, d->pf_qkv.as<float>(), qkv_rows, nullptr, fah::kGemmPlain);
       fah::QkArgs qa{};
       qa.qkv = d->pf_qkv.as<float>();
-      qa.q_norm = d->q_norm[l].as<float>();
-      qa.k_norm = d->k_norm[l].as<float>();
+      qa.q_norm = d->wt->q_norm[l].as<float>();
+      qa.k_norm = d->wt->k_norm[l].as<float>();
       qa.rope_cos = d->rope_cos.as<float>();
       qa.rope_sin = d->rope_sin.as<float>();
       qa.position = d->position.as<int>();
@@ -411,7 +550,8 @@ void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_
       pa.q = d->pf_q.as<float>();
       pa.kcache = qa.kcache;
       pa.vcache = qa.vcache;
-      pa.out = d->pf_attn.as<float>();
+      pa.xq = xq;  // quantised for the o projection inside the kernel
+      pa.xs = xs;
       pa.frames = T;
       pa.position = d->host_position + done;
       pa.heads = c.heads;
@@ -420,16 +560,14 @@ void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_
       pa.capacity = c.capacity;
       pa.divisor = std::sqrt((float)c.head_size);
       check(fah::launch_attn_prefill(pa, s), "prefill attention");
-      check(fah::launch_norm_quantize_rows(d->pf_attn.as<float>(), T, d->q_width, nullptr, 0.0f, xq, xs, s),
-            "prefill quantise attention");
-      gemm(d->wo[l], c.width, d->pf_a.as<float>(), c.width, d->pf_x.as<float>(), fah::kGemmResidual);
-      check(fah::launch_norm_quantize_rows(d->pf_a.as<float>(), T, c.width, d->ffn_norm[l].as<float>(), c.eps, xq, xs,
+      gemm(d->wt->wo[l], c.width, d->pf_a.as<float>(), c.width, d->pf_x.as<float>(), fah::kGemmResidual);
+      check(fah::launch_norm_quantize_rows(d->pf_a.as<float>(), T, c.width, d->wt->ffn_norm[l].as<float>(), c.eps, xq, xs,
                                            s),
             "prefill ffn_norm");
-      gemm(d->gateup[l], c.ffn, d->pf_h.as<float>(), c.ffn, nullptr, fah::kGemmSwiGLU);
+      gemm(d->wt->gateup[l], c.ffn, d->pf_h.as<float>(), c.ffn, nullptr, fah::kGemmSwiGLU);
       check(fah::launch_norm_quantize_rows(d->pf_h.as<float>(), T, c.ffn, nullptr, 0.0f, xq, xs, s),
             "prefill quantise ffn");
-      gemm(d->down[l], c.width, d->pf_x.as<float>(), c.width, d->pf_a.as<float>(), fah::kGemmResidual);
+      gemm(d->wt->down[l], c.width, d->pf_x.as<float>(), c.width, d->pf_a.as<float>(), fah::kGemmResidual);
     }
     check(fah::launch_advance(d->position.as<int>(), T, s), "advance");
     if (logits && done + T == frames) {
@@ -484,7 +622,7 @@ void check_step_error(fah_decoder* d) {
 // greedy, 2 = embedding of the device token + layers + lm_head + greedy.
 void enqueue_kind(fah_decoder* d, int kind, hipStream_t s) {
   if (kind == 2)
-    check(fah::launch_embed(d->embed.q.as<int8_t>(), d->embed.s.ptr, d->half_scales, d->cfg.width, d->cfg.vocab,
+    check(fah::launch_embed(d->wt->embed.q.as<int8_t>(), d->wt->embed.s.ptr, d->wt->half_scales, d->cfg.width, d->cfg.vocab,
                             d->token.as<int>(), d->x.as<float>(), d->history.as<int>(),
                             d->history_count.as<int>(), s),
           "embed");
@@ -517,6 +655,91 @@ void run_kind(fah_decoder* d, int kind, hipStream_t s) {
   hipGraphExec_t* slot = kind == 0 ? &d->graph_row : kind == 1 ? &d->graph_logits : &d->graph_step;
   if (!*slot) *slot = capture(d, kind);
   check(hipGraphLaunch(*slot, s), "hipGraphLaunch");
+}
+
+// ---- lock-step sessions ---------------------------------------------------
+
+// Upper bound on sessions in one lock-step batch, and on their positions
+// (the batched attention keeps a row's probabilities in 60 KiB of LDS).
+constexpr int kMaxSessions = 256;
+constexpr int kSessionPositions = 15360;
+
+// One greedy step of every session at once: the embeddings of their tokens,
+// the layers over all rows (MFMA Q8_0 GEMMs with the per-row block order;
+// per-session QK-norm, RoPE, KV write and attention), the final norm,
+// lm_head and a greedy pick per row. Each row's arithmetic is the
+// single-session step's, so each session's tokens are its own.
+void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s) {
+  const fah_decoder_config& c = d->cfg;
+  const DecoderWeights& w = *d->wt;
+  const int S = (int)b.members.size();
+  const int qkv_rows = d->q_width + 2 * d->kv_width;
+  const fah::SessionRef* table = b.table.as<fah::SessionRef>();
+  int8_t* xq = b.xq.as<int8_t>();
+  float* xs = b.xs.as<float>();
+  auto gemm = [&](const DeviceMatrix& m, int rows, float* out, const float* resid, int mode) {
+    fah::GemmArgs g{};
+    g.w = m.q.as<int8_t>();
+    g.ws = m.s.ptr;
+    g.rows = rows;
+    g.K = m.cols;
+    g.xq = xq;
+    g.xs = xs;
+    g.frames = S;
+    g.out = out;
+    g.out_stride = rows;
+    g.resid = resid;
+    g.split_base = w.gu_base;
+    g.split_extra = w.gu_extra;
+    check(fah::launch_gemm(g, w.half_scales, mode, s), "session gemm");
+  };
+  auto norm_quantize = [&](const float* x, int K, const DeviceBuffer* norm) {
+    check(fah::launch_norm_quantize_rows(x, S, K, norm ? norm->as<float>() : nullptr, norm ? c.eps : 0.0f, xq, xs, s),
+          "session norm/quantise");
+  };
+  check(fah::launch_session_embed(w.embed.q.as<int8_t>(), w.embed.s.ptr, w.half_scales, c.width, c.vocab, table, S,
+                                  b.x.as<float>(), s),
+        "session embed");
+  for (int l = 0; l < c.layers; ++l) {
+    norm_quantize(b.x.as<float>(), c.width, &w.attn_norm[l]);
+    gemm(w.qkv[l], qkv_rows, b.qkv.as<float>(), nullptr, fah::kGemmPlain);
+    fah::QkArgs qa{};
+    qa.qkv = b.qkv.as<float>();
+    qa.q_norm = w.q_norm[l].as<float>();
+    qa.k_norm = w.k_norm[l].as<float>();
+    qa.q_out = b.q.as<float>();
+    qa.heads = c.heads;
+    qa.kv_heads = c.kv_heads;
+    qa.head_size = c.head_size;
+    qa.q_width = d->q_width;
+    qa.kv_width = d->kv_width;
+    qa.eps = c.eps;
+    qa.frames = S;
+    qa.sessions = table;
+    qa.layer = l;
+    check(fah::launch_qk_prepare(qa, s), "session qk prepare");
+    fah::PrefillAttnArgs pa{};
+    pa.q = b.q.as<float>();
+    pa.xq = xq;
+    pa.xs = xs;
+    pa.frames = S;
+    pa.heads = c.heads;
+    pa.kv_heads = c.kv_heads;
+    pa.head_size = c.head_size;
+    pa.divisor = std::sqrt((float)c.head_size);
+    pa.sessions = table;
+    pa.layer = l;
+    pa.max_positions = b.max_positions;
+    check(fah::launch_attn_prefill(pa, s), "session attention");
+    gemm(w.wo[l], c.width, b.a.as<float>(), b.x.as<float>(), fah::kGemmResidual);
+    norm_quantize(b.a.as<float>(), c.width, &w.ffn_norm[l]);
+    gemm(w.gateup[l], c.ffn, b.h.as<float>(), nullptr, fah::kGemmSwiGLU);
+    norm_quantize(b.h.as<float>(), c.ffn, nullptr);
+    gemm(w.down[l], c.width, b.x.as<float>(), b.a.as<float>(), fah::kGemmResidual);
+  }
+  norm_quantize(b.x.as<float>(), c.width, &w.output_norm);
+  gemm(head_matrix(d), c.vocab, b.logits.as<float>(), nullptr, fah::kGemmPlain);
+  check(fah::launch_session_greedy(b.logits.as<float>(), c.vocab, table, S, s), "session greedy");
 }
 
 }  // namespace
@@ -561,6 +784,7 @@ int fah_context_destroy(fah_context* c) {
     if (c->stream) {
       (void)hipSetDevice(c->device);
       (void)hipStreamSynchronize(c->stream);
+      c->batch.reset();
       (void)hipStreamDestroy(c->stream);
     }
     c->disposed = true;
@@ -846,6 +1070,7 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
     d->cfg = k;
     d->q_width = q_width;
     d->kv_width = kv_width;
+    d->wt = std::make_shared<DecoderWeights>();
     hipStream_t s = c->stream;
 
     bool half = true;
@@ -855,16 +1080,16 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
       half = fits(L.wq) && fits(L.wk) && fits(L.wv) && fits(L.wo) && fits(L.gate) && fits(L.up) && fits(L.down);
     }
     half = half && fits(*token_embd) && (!output || fits(*output));
-    d->half_scales = half;
+    d->wt->half_scales = half;
 
-    d->qkv.resize(k.layers);
-    d->wo.resize(k.layers);
-    d->gateup.resize(k.layers);
-    d->down.resize(k.layers);
-    d->attn_norm.resize(k.layers);
-    d->q_norm.resize(k.layers);
-    d->k_norm.resize(k.layers);
-    d->ffn_norm.resize(k.layers);
+    d->wt->qkv.resize(k.layers);
+    d->wt->wo.resize(k.layers);
+    d->wt->gateup.resize(k.layers);
+    d->wt->down.resize(k.layers);
+    d->wt->attn_norm.resize(k.layers);
+    d->wt->q_norm.resize(k.layers);
+    d->wt->k_norm.resize(k.layers);
+    d->wt->ffn_norm.resize(k.layers);
     int qkv_rows = q_width + 2 * kv_width;
     int qkv_group = pick_group_rows(qkv_rows, k.width, 4, false);
     int o_group = pick_group_rows(k.width, q_width, 4, false);
@@ -880,15 +1105,15 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
                     fah::persistent_shape_supported(k.width, k.heads, k.kv_heads, k.head_size, k.ffn, nb) &&
                     k.capacity <= fah::persistent_max_capacity() &&
                     fah::persistent_blocks_per_cu(k.width) >= 1;
-    d->blocks = nb;
+    d->wt->persistent_layout = d->persistent;
     // Gate/up storage tiles: R gate rows then the matching R up rows. The
     // persistent kernel gives each projection workgroup (all but the
     // attention ones) an even share of the ffn rows, as one tile each.
     int gu_group = pick_group_rows(2 * k.ffn, k.width, 4, true);
     while (gu_group > 2 && (k.ffn % (gu_group / 2) != 0)) gu_group /= 2;
     const int ng = nb - k.heads;
-    d->gu_base = d->persistent ? k.ffn / ng : gu_group / 2;
-    d->gu_extra = d->persistent ? k.ffn % ng : 0;
+    d->wt->gu_base = d->persistent ? k.ffn / ng : gu_group / 2;
+    d->wt->gu_extra = d->persistent ? k.ffn % ng : 0;
     int down_group = pick_group_rows(k.width, k.ffn, 4, false);
     for (int l = 0; l < k.layers; ++l) {
       const fah_layer_host& L = layers[l];
@@ -896,12 +1121,12 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
       for (int r = 0; r < q_width; ++r) order.emplace_back(0, r);
       for (int r = 0; r < kv_width; ++r) order.emplace_back(1, r);
       for (int r = 0; r < kv_width; ++r) order.emplace_back(2, r);
-      upload_matrix(d->qkv[l], {&L.wq, &L.wk, &L.wv}, order, k.width, half, s);
-      d->qkv[l].group_rows = qkv_group;
+      upload_matrix(d->wt->qkv[l], {&L.wq, &L.wk, &L.wv}, order, k.width, half, s);
+      d->wt->qkv[l].group_rows = qkv_group;
       order.clear();
       for (int r = 0; r < k.width; ++r) order.emplace_back(0, r);
-      upload_matrix(d->wo[l], {&L.wo}, order, q_width, half, s);
-      d->wo[l].group_rows = o_group;
+      upload_matrix(d->wt->wo[l], {&L.wo}, order, q_width, half, s);
+      d->wt->wo[l].group_rows = o_group;
       order.clear();
       if (d->persistent) {
         const int base = k.ffn / ng, extra = k.ffn % ng;
@@ -917,152 +1142,54 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
           for (int r = 0; r < R; ++r) order.emplace_back(1, t * R + r);
         }
       }
-      upload_matrix(d->gateup[l], {&L.gate, &L.up}, order, k.width, half, s);
-      d->gateup[l].group_rows = gu_group;
+      upload_matrix(d->wt->gateup[l], {&L.gate, &L.up}, order, k.width, half, s);
+      d->wt->gateup[l].group_rows = gu_group;
       order.clear();
       for (int r = 0; r < k.width; ++r) order.emplace_back(0, r);
-      upload_matrix(d->down[l], {&L.down}, order, k.ffn, half, s);
-      d->down[l].group_rows = down_group;
-      upload(d->attn_norm[l], L.attn_norm, (size_t)k.width * 4, s);
-      upload(d->q_norm[l], L.q_norm, (size_t)k.head_size * 4, s);
-      upload(d->k_norm[l], L.k_norm, (size_t)k.head_size * 4, s);
-      upload(d->ffn_norm[l], L.ffn_norm, (size_t)k.width * 4, s);
-      d->weight_bytes += matrix_bytes(d->qkv[l]) + matrix_bytes(d->wo[l]) + matrix_bytes(d->gateup[l]) +
-                         matrix_bytes(d->down[l]);
+      upload_matrix(d->wt->down[l], {&L.down}, order, k.ffn, half, s);
+      d->wt->down[l].group_rows = down_group;
+      upload(d->wt->attn_norm[l], L.attn_norm, (size_t)k.width * 4, s);
+      upload(d->wt->q_norm[l], L.q_norm, (size_t)k.head_size * 4, s);
+      upload(d->wt->k_norm[l], L.k_norm, (size_t)k.head_size * 4, s);
+      upload(d->wt->ffn_norm[l], L.ffn_norm, (size_t)k.width * 4, s);
+      d->wt->weight_bytes += matrix_bytes(d->wt->qkv[l]) + matrix_bytes(d->wt->wo[l]) + matrix_bytes(d->wt->gateup[l]) +
+                         matrix_bytes(d->wt->down[l]);
     }
     {
       std::vector<std::pair<int, int>> order;
       for (int r = 0; r < k.vocab; ++r) order.emplace_back(0, r);
-      upload_matrix(d->embed, {token_embd}, order, k.width, half, s);
-      d->embed.group_rows = pick_group_rows(k.vocab, k.width, 4, false);
-      d->tied = output == nullptr;
-      if (!d->tied) {
-        upload_matrix(d->lm_head, {output}, order, k.width, half, s);
-        d->lm_head.group_rows = d->embed.group_rows;
+      upload_matrix(d->wt->embed, {token_embd}, order, k.width, half, s);
+      d->wt->embed.group_rows = pick_group_rows(k.vocab, k.width, 4, false);
+      d->wt->tied = output == nullptr;
+      if (!d->wt->tied) {
+        upload_matrix(d->wt->lm_head, {output}, order, k.width, half, s);
+        d->wt->lm_head.group_rows = d->wt->embed.group_rows;
       }
     }
-    DeviceMatrix& head = d->tied ? d->embed : d->lm_head;
-    d->weight_bytes += matrix_bytes(head);
-    upload(d->output_norm, output_norm, (size_t)k.width * 4, s);
+    DeviceMatrix& head = d->wt->tied ? d->wt->embed : d->wt->lm_head;
+    d->wt->weight_bytes += matrix_bytes(head);
+    upload(d->wt->output_norm, output_norm, (size_t)k.width * 4, s);
 
-    // RoPE table with the C runtime's powf/cosf/sinf (QwenDecoder.cs:78-95).
-    int half_hs = k.head_size / 2;
-    std::vector<float> freq(half_hs), cs((size_t)k.capacity * half_hs), sn((size_t)k.capacity * half_hs);
-    for (int i = 0; i < half_hs; ++i) freq[i] = powf(k.rope_base, (-2.0f * (float)i) / (float)k.head_size);
-    for (int t = 0; t < k.capacity; ++t)
-      for (int i = 0; i < half_hs; ++i) {
-        float angle = (float)t * freq[i];
-        cs[(size_t)t * half_hs + i] = cosf(angle);
-        sn[(size_t)t * half_hs + i] = sinf(angle);
-      }
-    upload(d->rope_cos, cs.data(), cs.size() * 4, s);
-    upload(d->rope_sin, sn.data(), sn.size() * 4, s);
-
-    size_t kv_elems = (size_t)k.layers * k.kv_heads * k.capacity * k.head_size;
-    d->kcache.allocate(kv_elems * 2);
-    d->vcache.allocate(kv_elems * 2);
-    check(hipMemsetAsync(d->kcache.ptr, 0, kv_elems * 2, s), "memset kv");
-    check(hipMemsetAsync(d->vcache.ptr, 0, kv_elems * 2, s), "memset kv");
-    d->x.allocate((size_t)k.width * 4);
-    d->qkv_out.allocate((size_t)qkv_rows * 4);
-    d->qh.allocate((size_t)q_width * 4);
-    d->scores.allocate((size_t)k.heads * k.capacity * 4);
-    d->attn.allocate((size_t)q_width * 4);
-    d->a.allocate((size_t)k.width * 4);
-    d->h.allocate((size_t)k.ffn * 4);
-    d->logits.allocate((size_t)k.vocab * 4);
-    d->lm_groups = (k.vocab + head.group_rows - 1) / head.group_rows;
-    d->keys.allocate((size_t)d->lm_groups * 8);
-    d->token.allocate(16);
-    d->position.allocate(16);
-    d->history.allocate((size_t)k.capacity * 4 + 16);
-    d->history_count.allocate(16);
-    check(hipMemsetAsync(d->token.ptr, 0, 16, s), "memset");
-    check(hipMemsetAsync(d->position.ptr, 0, 16, s), "memset");
-    check(hipMemsetAsync(d->history_count.ptr, 0, 16, s), "memset");
     if (d->persistent) {
       std::vector<fah::PersistentLayer> table(k.layers);
       for (int l = 0; l < k.layers; ++l) {
         fah::PersistentLayer& t = table[l];
-        t.wqkv = d->qkv[l].q.as<int8_t>();
-        t.sqkv = d->qkv[l].s.as<_Float16>();
-        t.wo = d->wo[l].q.as<int8_t>();
-        t.so = d->wo[l].s.as<_Float16>();
-        t.wgu = d->gateup[l].q.as<int8_t>();
-        t.sgu = d->gateup[l].s.as<_Float16>();
-        t.wd = d->down[l].q.as<int8_t>();
-        t.sd = d->down[l].s.as<_Float16>();
-        t.attn_norm = d->attn_norm[l].as<float>();
-        t.q_norm = d->q_norm[l].as<float>();
-        t.k_norm = d->k_norm[l].as<float>();
-        t.ffn_norm = d->ffn_norm[l].as<float>();
+        t.wqkv = d->wt->qkv[l].q.as<int8_t>();
+        t.sqkv = d->wt->qkv[l].s.as<_Float16>();
+        t.wo = d->wt->wo[l].q.as<int8_t>();
+        t.so = d->wt->wo[l].s.as<_Float16>();
+        t.wgu = d->wt->gateup[l].q.as<int8_t>();
+        t.sgu = d->wt->gateup[l].s.as<_Float16>();
+        t.wd = d->wt->down[l].q.as<int8_t>();
+        t.sd = d->wt->down[l].s.as<_Float16>();
+        t.attn_norm = d->wt->attn_norm[l].as<float>();
+        t.q_norm = d->wt->q_norm[l].as<float>();
+        t.k_norm = d->wt->k_norm[l].as<float>();
+        t.ffn_norm = d->wt->ffn_norm[l].as<float>();
       }
-      upload(d->layer_table, table.data(), table.size() * sizeof(fah::PersistentLayer), s);
-      auto tagged = [&](DeviceBuffer& b, size_t words) {
-        b.allocate(words * 8);
-        check(hipMemsetAsync(b.ptr, 0, words * 8, s), "memset tagged");
-      };
-      tagged(d->tx, k.width);
-      tagged(d->tqkv, qkv_rows);
-      tagged(d->tatt, q_width);
-      tagged(d->ta, k.width);
-      tagged(d->th, k.ffn);
-      tagged(d->tkeys, 2 * nb);
-      d->epoch.allocate(16);
-      d->error.allocate(16);
-      unsigned one = 1;
-      check(hipMemcpyAsync(d->epoch.ptr, &one, 4, hipMemcpyHostToDevice, s), "epoch");
-      check(hipMemsetAsync(d->error.ptr, 0, 16, s), "memset error");
-      fah::PersistentArgs& a = d->pargs;
-      a.layer_table = d->layer_table.as<fah::PersistentLayer>();
-      a.layers = k.layers;
-      a.embed_q = d->embed.q.as<int8_t>();
-      a.embed_s = d->embed.s.as<_Float16>();
-      a.head_q = head.q.as<int8_t>();
-      a.head_s = head.s.as<_Float16>();
-      a.output_norm = d->output_norm.as<float>();
-      a.rope_cos = d->rope_cos.as<float>();
-      a.rope_sin = d->rope_sin.as<float>();
-      a.kcache = d->kcache.as<_Float16>();
-      a.vcache = d->vcache.as<_Float16>();
-      a.width = k.width;
-      a.heads = k.heads;
-      a.kv_heads = k.kv_heads;
-      a.head_size = k.head_size;
-      a.ffn = k.ffn;
-      a.vocab = k.vocab;
-      a.capacity = k.capacity;
-      a.q_width = q_width;
-      a.kv_width = kv_width;
-      a.eps = k.eps;
-      a.divisor = std::sqrt((float)k.head_size);
-      a.rq = qkv_rows / nb;
-      a.ro = k.width / nb;
-      a.rgu = k.ffn / nb;
-      a.rd = k.width / nb;
-      a.head_chunks = (k.vocab + 31) / 32;
-      a.npre = fah::persistent_max_positions();
-      a.tx = d->tx.as<unsigned long long>();
-      a.tqkv = d->tqkv.as<unsigned long long>();
-      a.tatt = d->tatt.as<unsigned long long>();
-      a.ta = d->ta.as<unsigned long long>();
-      a.th = d->th.as<unsigned long long>();
-      a.tkeys = d->tkeys.as<unsigned long long>();
-      a.x_in = d->x.as<float>();
-      a.position = d->position.as<int>();
-      a.token = d->token.as<int>();
-      a.history = d->history.as<int>();
-      a.history_count = d->history_count.as<int>();
-      a.epoch = d->epoch.as<unsigned>();
-      a.error = d->error.as<unsigned>();
-      a.logits = d->logits.as<float>();
-      const char* tl = std::getenv("FAH_TIMELINE");
-      if (tl && tl[0] == '1') {
-        d->timeline.allocate((size_t)nb * fah::kTimelineEvents * 8);
-        check(hipMemsetAsync(d->timeline.ptr, 0, (size_t)nb * fah::kTimelineEvents * 8, s), "memset timeline");
-        a.timeline = d->timeline.as<unsigned long long>();
-      }
+      upload(d->wt->layer_table, table.data(), table.size() * sizeof(fah::PersistentLayer), s);
     }
+    init_state(d.get(), s);
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
     *out = d.release();
     return FAH_OK;
@@ -1074,6 +1201,8 @@ int fah_decoder_destroy(fah_decoder* d) {
   std::lock_guard<std::mutex> lock(d->context->gate);
   (void)hipSetDevice(d->context->device);
   (void)hipStreamSynchronize(d->context->stream);
+  auto& batch = d->context->batch;
+  if (batch && std::find(batch->members.begin(), batch->members.end(), d) != batch->members.end()) batch.reset();
   for (hipGraphExec_t g : {d->graph_row, d->graph_logits, d->graph_step})
     if (g) (void)hipGraphExecDestroy(g);
   delete d;
@@ -1142,7 +1271,7 @@ int fah_decoder_embed(fah_decoder* d, const int32_t* tokens, int count, float* o
     int* tok = reinterpret_cast<int*>(d->staging.as<char>() + (size_t)d->cfg.width * 4);
     for (int i = 0; i < count; ++i) {
       check(hipMemcpyAsync(tok, &tokens[i], 4, hipMemcpyHostToDevice, s), "H2D token");
-      check(fah::launch_embed(d->embed.q.as<int8_t>(), d->embed.s.ptr, d->half_scales, d->cfg.width, d->cfg.vocab,
+      check(fah::launch_embed(d->wt->embed.q.as<int8_t>(), d->wt->embed.s.ptr, d->wt->half_scales, d->cfg.width, d->cfg.vocab,
                               tok, d->staging.as<float>(), nullptr, nullptr, s),
             "embed");
       check(hipMemcpyAsync(out + (size_t)i * d->cfg.width, d->staging.ptr, (size_t)d->cfg.width * 4,
@@ -1182,6 +1311,132 @@ int fah_decoder_generate(fah_decoder* d, int steps, int32_t* tokens) {
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
     check_step_error(d);
     d->host_position += steps;
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** out) {
+  if (!parent || !out) return fail(FAH_ERROR_ARGUMENT, "parent/session is NULL");
+  return guarded([&] {
+    require(capacity >= 1, "capacity must be positive");
+    fah_context* c = parent->context;
+    auto d = std::make_unique<fah_decoder>();
+    d->context = c;
+    d->cfg = parent->cfg;
+    d->cfg.capacity = capacity;
+    d->q_width = parent->q_width;
+    d->kv_width = parent->kv_width;
+    d->wt = parent->wt;
+    if (d->wt->persistent_layout) {
+      require(capacity <= fah::persistent_max_capacity(),
+              "session capacity exceeds the persistent decode step's limit of " +
+                  std::to_string(fah::persistent_max_capacity()) + " positions");
+      d->persistent = true;
+    } else {
+      require(fah::attention_slices(capacity, d->cfg.head_size) != 0,
+              "capacity exceeds the attention kernel's LDS budget");
+    }
+    std::lock_guard<std::mutex> lock(c->gate);
+    check(hipSetDevice(c->device), "hipSetDevice");
+    if (!d->persistent) check(fah::prepare_attention(capacity, d->cfg.head_size), "attention LDS budget");
+    init_state(d.get(), c->stream);
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    *out = d.release();
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int steps, int32_t* tokens) {
+  if (!sessions || count < 1) return fail(FAH_ERROR_ARGUMENT, "no sessions");
+  return guarded([&] {
+    require(count <= kMaxSessions, "at most " + std::to_string(kMaxSessions) + " sessions per batch");
+    require(steps >= 0 && (steps == 0 || tokens), "invalid generate arguments");
+    const fah_decoder* d0 = sessions[0];
+    require(d0 != nullptr, "session is NULL");
+    // The batched attention keeps one row's probabilities in LDS: positions
+    // up to kSessionPositions; the captured step is sized for that bound (or
+    // the largest capacity, if smaller) so it serves every later call.
+    int bound = 0;
+    for (int i = 0; i < count; ++i) {
+      const fah_decoder* d = sessions[i];
+      require(d != nullptr, "session is NULL");
+      require(d->wt == d0->wt && d->context == d0->context, "sessions must share one decoder's weights");
+      for (int j = 0; j < i; ++j) require(sessions[j] != d, "a session appears twice");
+      if (!d->have_logits)
+        return fail(FAH_ERROR_STATE, "session " + std::to_string(i) + " has no logits: decode with logits first");
+      require(d->host_position + steps <= d->cfg.capacity, "Decoder context exhausted");
+      require(d->host_position + steps <= kSessionPositions,
+              "lock-step sessions are limited to " + std::to_string(kSessionPositions) + " positions");
+      bound = std::max(bound, std::min(d->cfg.capacity, kSessionPositions));
+    }
+    if (steps == 0) return FAH_OK;
+    fah_context* c = d0->context;
+    std::lock_guard<std::mutex> lock(c->gate);
+    hipStream_t s = c->stream;
+    check(hipSetDevice(c->device), "hipSetDevice");
+    std::vector<fah_decoder*> members(sessions, sessions + count);
+    if (!c->batch || c->batch->members != members || c->batch->max_positions != bound) {
+      c->batch.reset();
+      auto b = std::make_unique<SessionBatch>();
+      b->members = members;
+      b->max_positions = bound;
+      const fah_decoder_config& k = d0->cfg;
+      const int widest = std::max(std::max(k.width, d0->q_width), k.ffn);
+      std::vector<fah::SessionRef> table(count);
+      for (int i = 0; i < count; ++i) {
+        fah_decoder* d = sessions[i];
+        fah::SessionRef& r = table[i];
+        r.kcache = d->kcache.as<_Float16>();
+        r.vcache = d->vcache.as<_Float16>();
+        r.rope_cos = d->rope_cos.as<float>();
+        r.rope_sin = d->rope_sin.as<float>();
+        r.position = d->position.as<int>();
+        r.token = d->token.as<int>();
+        r.history = d->history.as<int>();
+        r.history_count = d->history_count.as<int>();
+        r.capacity = d->cfg.capacity;
+      }
+      upload(b->table, table.data(), table.size() * sizeof(fah::SessionRef), s);
+      b->x.allocate((size_t)count * k.width * 4);
+      b->a.allocate((size_t)count * k.width * 4);
+      b->qkv.allocate((size_t)count * (d0->q_width + 2 * d0->kv_width) * 4);
+      b->q.allocate((size_t)count * d0->q_width * 4);
+      b->h.allocate((size_t)count * k.ffn * 4);
+      b->xq.allocate((size_t)count * widest);
+      b->xs.allocate((size_t)count * (widest / 32) * 4);
+      b->logits.allocate((size_t)count * k.vocab * 4);
+      if (use_graphs()) {
+        hipGraph_t graph = nullptr;
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        try {
+          enqueue_sessions_step(d0, *b, s);
+        } catch (...) {
+          hipGraph_t dead = nullptr;
+          (void)hipStreamEndCapture(s, &dead);
+          if (dead) (void)hipGraphDestroy(dead);
+          throw;
+        }
+        check(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
+        hipError_t e = hipGraphInstantiate(&b->graph, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        check(e, "hipGraphInstantiate");
+      }
+      c->batch = std::move(b);
+    }
+    SessionBatch& b = *c->batch;
+    for (int i = 0; i < count; ++i)
+      check(hipMemsetAsync(sessions[i]->history_count.ptr, 0, 4, s), "reset history");
+    for (int i = 0; i < steps; ++i) {
+      if (b.graph) check(hipGraphLaunch(b.graph, s), "hipGraphLaunch");
+      else enqueue_sessions_step(d0, b, s);
+    }
+    for (int i = 0; i < count; ++i)
+      check(hipMemcpyAsync(tokens + (size_t)i * steps, sessions[i]->history.ptr, (size_t)steps * 4,
+                           hipMemcpyDeviceToHost, s),
+            "D2H tokens");
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    for (int i = 0; i < count; ++i) sessions[i]->host_position += steps;
     return FAH_OK;
   });
 }
@@ -1237,7 +1492,7 @@ int fah_decoder_kv_read(fah_decoder* d, int layer, uint16_t* keys, uint16_t* val
   });
 }
 
-int64_t fah_decoder_weight_bytes(const fah_decoder* d) { return d ? d->weight_bytes : 0; }
+int64_t fah_decoder_weight_bytes(const fah_decoder* d) { return d ? d->wt->weight_bytes : 0; }
 
 int fah_decoder_persistent(const fah_decoder* d) { return d && d->persistent ? 1 : 0; }
 

@@ -27,6 +27,21 @@ struct GemvArgs {
   unsigned long long* partial_keys;  // [frames][groups] (kOutGreedy)
 };
 
+// One decoder session of a lock-step batch: row f of a batched step reads and
+// writes session f's cache, position and token.
+struct SessionRef {
+  _Float16* kcache;        // [layers][kv_heads][capacity][head_size]
+  _Float16* vcache;
+  const float* rope_cos;   // [capacity][head_size/2]
+  const float* rope_sin;
+  int* position;
+  int* token;
+  int* history;
+  int* history_count;
+  int capacity;
+  int reserved;
+};
+
 struct QkArgs {
   const float* qkv;    // [q_width + 2*kv_width] raw projections
   const float* q_norm; // [head_size]
@@ -40,6 +55,10 @@ struct QkArgs {
   int heads, kv_heads, head_size, q_width, kv_width, capacity;
   float eps;
   int frames;             // rows (0 or 1: decode); row t sits at position + t
+  // Batched sessions (when set): row t is session t's next position; its
+  // cache, RoPE tables and capacity replace the fields above for layer `layer`.
+  const SessionRef* sessions;
+  int layer;
 };
 
 struct AttnArgs {
@@ -122,16 +141,28 @@ struct PrefillAttnArgs {
   const float* q;          // [frames][heads*head_size], normalised and rotated
   const _Float16* kcache;  // [kv_heads][capacity][head_size] (this layer)
   const _Float16* vcache;
-  float* out;              // [frames][heads*head_size]
+  float* out;              // [frames][heads*head_size], or null with xq set
   int frames, position;    // query row t sits at position + t
   int heads, kv_heads, head_size, capacity;
   float divisor;
+  // Optional Q8_0 quantisation of the output rows ([frames][heads*head_size]
+  // codes, [frames][heads*head_size/32] scales), block by block.
+  int8_t* xq;
+  float* xs;
+  // Batched sessions (when set): row t attends over session t's cache for
+  // layer `layer` at its position; max_positions bounds position + 1.
+  const SessionRef* sessions;
+  int layer, max_positions;
 };
 
 hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t s);
 hipError_t launch_norm_quantize_rows(const float* x, int frames, int K, const float* norm_w, float eps, int8_t* xq,
                                      float* xs, hipStream_t s);
 hipError_t launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t s);
+hipError_t launch_session_embed(const int8_t* q, const void* scales, bool half_scales, int K, int vocab,
+                                const SessionRef* sessions, int count, float* x, hipStream_t s);
+hipError_t launch_session_greedy(const float* logits, int vocab, const SessionRef* sessions, int count,
+                                 hipStream_t s);
 
 bool persistent_shape_supported(int width, int heads, int kv_heads, int head_size, int ffn, int blocks);
 hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s);

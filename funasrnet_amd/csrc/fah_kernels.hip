@@ -242,8 +242,27 @@ __global__ __launch_bounds__(128) void qk_prepare_kernel(QkArgs a) {
   __shared__ float y_s[128];
   const int c = threadIdx.x;
   const int frame = blockIdx.y;
-  const int pos = *a.position + frame;
   const int hs = a.head_size, half = hs >> 1;
+  int pos, capacity;
+  const float *rope_cos, *rope_sin;
+  _Float16 *kcache, *vcache;
+  if (a.sessions) {
+    const SessionRef& ss = a.sessions[frame];
+    pos = *ss.position;
+    capacity = ss.capacity;
+    rope_cos = ss.rope_cos;
+    rope_sin = ss.rope_sin;
+    const size_t layer = (size_t)a.layer * a.kv_heads * capacity * hs;
+    kcache = ss.kcache + layer;
+    vcache = ss.vcache + layer;
+  } else {
+    pos = *a.position + frame;
+    capacity = a.capacity;
+    rope_cos = a.rope_cos;
+    rope_sin = a.rope_sin;
+    kcache = a.kcache;
+    vcache = a.vcache;
+  }
   const bool is_q = blockIdx.x < a.heads;
   const int head = is_q ? blockIdx.x : blockIdx.x - a.heads;
   const float* qkv = a.qkv + (size_t)frame * (a.q_width + 2 * a.kv_width);
@@ -257,8 +276,8 @@ __global__ __launch_bounds__(128) void qk_prepare_kernel(QkArgs a) {
   y_s[c] = fmul(fmul(v, inverse), w[c]);
   __syncthreads();
   float r;
-  const float* cosine = a.rope_cos + (size_t)pos * half;
-  const float* sine = a.rope_sin + (size_t)pos * half;
+  const float* cosine = rope_cos + (size_t)pos * half;
+  const float* sine = rope_sin + (size_t)pos * half;
   if (c < half) {
     float x0 = y_s[c], x1 = y_s[c + half];
     r = fadd(fmul(x0, cosine[c]), -fmul(x1, sine[c]));
@@ -269,9 +288,9 @@ __global__ __launch_bounds__(128) void qk_prepare_kernel(QkArgs a) {
   if (is_q) {
     a.q_out[(size_t)frame * a.q_width + head * hs + c] = r;
   } else {
-    size_t row = ((size_t)head * a.capacity + pos) * hs + c;
-    a.kcache[row] = to_half(r);
-    a.vcache[row] = to_half(qkv[a.q_width + a.kv_width + head * hs + c]);
+    size_t row = ((size_t)head * capacity + pos) * hs + c;
+    kcache[row] = to_half(r);
+    vcache[row] = to_half(qkv[a.q_width + a.kv_width + head * hs + c]);
   }
 }
 
@@ -406,6 +425,51 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
   }
 }
 
+// Lock-step sessions: row f of x is the embedding of session f's token
+// (QwenDecoder.Embed, QwenDecoder.cs:143-152), which joins its history.
+template <class Scale>
+__global__ __launch_bounds__(kThreads) void session_embed_kernel(const int8_t* q, const void* scales, int K, int vocab,
+                                                                 const SessionRef* sessions, float* x) {
+  const SessionRef& ss = sessions[blockIdx.x];
+  int t = *ss.token;
+  if (t < 0 || t >= vocab) t = 0;
+  const typename Scale::type* s = reinterpret_cast<const typename Scale::type*>(scales);
+  float* row = x + (size_t)blockIdx.x * K;
+  for (int j = threadIdx.x; j < K; j += blockDim.x) {
+    size_t at = (size_t)t * K + j;
+    row[j] = fmul((float)q[at], Scale::get(s[at / 32]));
+  }
+  if (threadIdx.x == 0) {
+    int n = *ss.history_count;
+    ss.history[n] = t;
+    *ss.history_count = n + 1;
+  }
+}
+
+// Lock-step sessions: greedy token of logits row f (QwenDecoder.Greedy,
+// QwenDecoder.cs:278-326: strict '>' so the first maximum wins, NaN at 0
+// returns 0) into session f's token word, then its position advances.
+__global__ __launch_bounds__(kThreads) void session_greedy_kernel(const float* logits, int vocab,
+                                                                  const SessionRef* sessions) {
+  __shared__ unsigned long long best_s[kThreads / kWave];
+  const float* row = logits + (size_t)blockIdx.x * vocab;
+  unsigned long long best = 0ull;
+  for (int i = threadIdx.x; i < vocab; i += kThreads) {
+    const unsigned long long k = greedy_key(row[i], (uint32_t)i);
+    best = k > best ? k : best;
+  }
+  best = wave_max_u64(best);
+  if ((threadIdx.x & (kWave - 1)) == 0) best_s[threadIdx.x / kWave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kThreads / kWave; ++w) best = best_s[w] > best ? best_s[w] : best;
+    const float first = row[0];
+    const SessionRef& ss = sessions[blockIdx.x];
+    *ss.token = (first != first || best == 0ull) ? 0 : (int)greedy_index(best);
+    *ss.position = *ss.position + 1;
+  }
+}
+
 __global__ void advance_kernel(int* position, int frames) {
   if (threadIdx.x == 0) *position += frames;
 }
@@ -513,6 +577,23 @@ hipError_t launch_greedy_reduce(const unsigned long long* keys, int count, const
   return hipGetLastError();
 }
 
+hipError_t launch_session_embed(const int8_t* q, const void* scales, bool half_scales, int K, int vocab,
+                                const SessionRef* sessions, int count, float* x, hipStream_t s) {
+  if (count < 1) return hipErrorInvalidValue;
+  if (half_scales)
+    session_embed_kernel<ScaleHalf><<<count, kThreads, 0, s>>>(q, scales, K, vocab, sessions, x);
+  else
+    session_embed_kernel<ScaleFloat><<<count, kThreads, 0, s>>>(q, scales, K, vocab, sessions, x);
+  return hipGetLastError();
+}
+
+hipError_t launch_session_greedy(const float* logits, int vocab, const SessionRef* sessions, int count,
+                                 hipStream_t s) {
+  if (count < 1 || vocab < 1) return hipErrorInvalidValue;
+  session_greedy_kernel<<<count, kThreads, 0, s>>>(logits, vocab, sessions);
+  return hipGetLastError();
+}
+
 hipError_t launch_embed(const int8_t* q, const void* scales, bool half_scales, int K, int vocab, const int* token,
                         float* x, int* history, int* history_count, hipStream_t s) {
   if (half_scales)
@@ -541,10 +622,12 @@ size_t attention_lds_bytes(int capacity, int head_size) {
 }
 
 hipError_t prepare_attention(int capacity, int head_size) {
-  size_t bytes = attention_lds_bytes(capacity, head_size);
-  if (!bytes) return hipErrorInvalidValue;
+  if (!attention_lds_bytes(capacity, head_size)) return hipErrorInvalidValue;
+  // The limit is per kernel, not per decoder: set the largest size any
+  // capacity that attention_slices accepts can ask for, so decoders of
+  // different capacities do not lower each other's limit.
   return hipFuncSetAttribute(reinterpret_cast<const void*>(attn_values_kernel),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024 + 16);
 }
 
 hipError_t launch_attention(const AttnArgs& a, int score_groups, hipStream_t s) {

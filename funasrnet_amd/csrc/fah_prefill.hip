@@ -226,10 +226,25 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   __shared__ float inv_s;
   const int head = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hs = 128, kh = head / (a.heads / a.kv_heads);
-  const int pos = a.position + t, n = pos + 1;
+  int pos, capacity;
+  const _Float16 *kcache, *vcache;
+  if (a.sessions) {
+    const SessionRef& ss = a.sessions[t];
+    pos = min(*ss.position, a.max_positions - 1);
+    capacity = ss.capacity;
+    const size_t layer = (size_t)a.layer * a.kv_heads * capacity * hs;
+    kcache = ss.kcache + layer;
+    vcache = ss.vcache + layer;
+  } else {
+    pos = a.position + t;
+    capacity = a.capacity;
+    kcache = a.kcache;
+    vcache = a.vcache;
+  }
+  const int n = pos + 1;
   const float* q = a.q + ((size_t)t * a.heads + head) * hs;
-  const _Float16* kc = a.kcache + (size_t)kh * a.capacity * hs;
-  const _Float16* vc = a.vcache + (size_t)kh * a.capacity * hs;
+  const _Float16* kc = kcache + (size_t)kh * capacity * hs;
+  const _Float16* vc = vcache + (size_t)kh * capacity * hs;
   float* p_s = attn_s;
   if (tid < hs) q_s[tid] = q[tid];
   lds_barrier();
@@ -293,7 +308,20 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
       for (int k = 0; k < 16; ++k) acc = fadd(acc, fmul(x[k], p_s[s + k]));
     }
     for (; s < n; ++s) acc = fadd(acc, fmul(from_half(v[(size_t)s * hs]), p_s[s]));
-    a.out[((size_t)t * a.heads + head) * hs + tid] = acc;
+    if (a.out) a.out[((size_t)t * a.heads + head) * hs + tid] = acc;
+    q_s[tid] = acc;
+  }
+  if (a.xq) {
+    // Q8_0 blocks of this head's output (32 channels each, 8 lanes x 4).
+    lds_barrier();
+    if (tid < hs / 4) {
+      const float4 v4 = *reinterpret_cast<const float4*>(q_s + 4 * tid);
+      float d;
+      const int packed = quantize4(v4.x, v4.y, v4.z, v4.w, &d);
+      const size_t row = (size_t)t * a.heads * hs + (size_t)head * hs;
+      *reinterpret_cast<int*>(a.xq + row + 4 * tid) = packed;
+      if ((tid & 7) == 0) a.xs[row / 32 + tid / 8] = d;
+    }
   }
 }
 
@@ -331,8 +359,9 @@ hipError_t launch_norm_quantize_rows(const float* x, int frames, int K, const fl
 
 hipError_t launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t s) {
   if (a.head_size != 128 || a.frames < 1 || a.heads % a.kv_heads != 0) return hipErrorInvalidValue;
-  const int n = a.position + a.frames;
-  if (n > a.capacity || (size_t)n * 4 > 60 * 1024) return hipErrorInvalidValue;
+  if (!a.out && !a.xq) return hipErrorInvalidValue;
+  const int n = a.sessions ? a.max_positions : a.position + a.frames;
+  if ((!a.sessions && n > a.capacity) || n < 1 || (size_t)n * 4 > 60 * 1024) return hipErrorInvalidValue;
   attn_prefill_kernel<<<dim3(a.heads, a.frames), 256, (size_t)n * 4, s>>>(a);
   return hipGetLastError();
 }

@@ -80,6 +80,8 @@ SIGNATURES = {
     "fah_decoder_embed": (ctypes.c_int, [_vp, _i32p, ctypes.c_int, _f32p]),
     "fah_decoder_greedy": (ctypes.c_int, [_vp, _i32p]),
     "fah_decoder_generate": (ctypes.c_int, [_vp, ctypes.c_int, _i32p]),
+    "fah_decoder_create_session": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(_vp)]),
+    "fah_decoder_generate_sessions": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, ctypes.c_int, _i32p]),
     "fah_decoder_kv_write": (ctypes.c_int, [_vp, ctypes.c_int, _u16p, _u16p, ctypes.c_int]),
     "fah_decoder_kv_read": (ctypes.c_int, [_vp, ctypes.c_int, _u16p, _u16p, ctypes.c_int]),
     "fah_decoder_weight_bytes": (ctypes.c_int64, [_vp]),
@@ -240,7 +242,18 @@ class HipBackend:
 class HipDecoder:
     """QwenDecoder (src/FunAsrNet/QwenDecoder.cs) on the device."""
 
-    def __init__(self, backend: HipBackend, weights: DecoderWeights, capacity: int = 2048):
+    def __init__(self, backend: HipBackend, weights: DecoderWeights | None, capacity: int = 2048,
+                 parent: "HipDecoder | None" = None):
+        if parent is not None:
+            # A session over the parent's device weights (fah_decoder_create_session).
+            h = _vp()
+            _check(load().fah_decoder_create_session(parent.handle, capacity, ctypes.byref(h)))
+            self.handle = h
+            self.config = parent.config
+            self.capacity = capacity
+            self.backend = backend
+            self.parent = parent
+            return
         c = weights.config
         keep = []
 
@@ -271,6 +284,12 @@ class HipDecoder:
         self.config = c
         self.capacity = capacity
         self.backend = backend
+        self.parent = None
+
+    def session(self, capacity: int | None = None) -> "HipDecoder":
+        """A new session sharing this decoder's device weights, with its own
+        KV cache of `capacity` positions (default: this decoder's)."""
+        return HipDecoder(self.backend, None, capacity or self.capacity, parent=self)
 
     def close(self):
         if self.handle:
@@ -321,6 +340,16 @@ class HipDecoder:
         tokens = np.empty(max(steps, 1), dtype=np.int32)
         _check(load().fah_decoder_generate(self.handle, steps, _p(tokens, ctypes.c_int32)))
         return tokens[:steps]
+
+    @staticmethod
+    def generate_sessions(sessions, steps: int) -> np.ndarray:
+        """Lock-step greedy decode of sessions that share one weight set:
+        tokens [len(sessions), steps], row i for sessions[i]."""
+        count = len(sessions)
+        handles = (_vp * count)(*[d.handle for d in sessions])
+        tokens = np.empty((count, max(steps, 1)), dtype=np.int32)
+        _check(load().fah_decoder_generate_sessions(handles, count, steps, _p(tokens, ctypes.c_int32)))
+        return tokens[:, :steps]
 
     def kv_write(self, layer: int, keys_f16: np.ndarray, values_f16: np.ndarray):
         k = np.ascontiguousarray(keys_f16, dtype=np.float16).view(np.uint16)

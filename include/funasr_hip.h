@@ -186,6 +186,24 @@ int fah_decoder_greedy(fah_decoder* decoder, int32_t* token);
  * preceding decode. tokens[steps] receives the chosen tokens. */
 int fah_decoder_generate(fah_decoder* decoder, int steps, int32_t* tokens);
 
+/* A decoder session: shares `parent`'s device weights (they stay alive while
+ * any session does) and has its own F16 KV cache of `capacity` positions,
+ * RoPE table, position and token state. Replaces constructing one
+ * QwenDecoder per FunAsr instance over the same model
+ * (src/FunAsrNet/QwenDecoder.cs:46-112; sessions served by
+ * src/FunAsrNet/BoundedInferencePool.cs:78), without a second weight copy.
+ * Every fah_decoder_* call accepts a session. */
+int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** session);
+
+/* The FunAsr.Transcribe loop (src/FunAsrNet/FunAsr.cs:167-178) of `count`
+ * sessions in lock step: each step embeds every session's token, runs the
+ * layers over all `count` rows at once (each weight read once per step) and
+ * takes every row's greedy token. Each session's tokens equal those of
+ * fah_decoder_generate on it alone. All sessions share one weight set
+ * (fah_decoder_create_session) and each must hold logits from its last
+ * decode. tokens[count][steps], row i for sessions[i]. */
+int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int steps, int32_t* tokens);
+
 /* Overwrite cached K/V rows [0, positions) of one layer from fp16 bit
  * patterns laid out [positions][kv_heads*head_size] (long-context stress
  * inputs; no reference counterpart). */

@@ -1,0 +1,151 @@
+"""Lock-step sessions (fah_decoder_generate_sessions): several decoder
+sessions over one weight set step together, each weight read once per step.
+Every session's tokens and K/V rows must equal those of the same session
+decoded alone, and the oracle's."""
+import numpy as np
+import pytest
+
+from funasrnet_amd import model
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def backend():
+    from funasrnet_amd.hip import HipBackend
+    b = HipBackend(0)
+    yield b
+    b.close()
+
+
+def _prefixes(cfg, lengths, seed0):
+    return [np.random.default_rng(seed0 + i).standard_normal((n, cfg.width)).astype(np.float32)
+            for i, n in enumerate(lengths)]
+
+
+def _alone(backend, w, prefix, steps, capacity):
+    """Tokens and K/V rows of one session decoded by itself."""
+    from funasrnet_amd.hip import HipDecoder
+    d = HipDecoder(backend, w, capacity=capacity)
+    try:
+        d.decode(prefix, prefix.shape[0])
+        toks = d.generate(steps)
+        kv = [d.kv_read(layer, prefix.shape[0] + steps) for layer in (0, w.config.layers - 1)]
+        return toks, kv
+    finally:
+        d.close()
+
+
+def test_sessions_match_each_session_alone(backend, oracle_lib):
+    from funasrnet_amd.hip import HipDecoder
+    cfg = model.small_config(layers=2)
+    w = model.synthetic(cfg, seed=21)
+    lengths, steps = [9, 17, 30, 1, 64], 12
+    prefixes = _prefixes(cfg, lengths, 40)
+    parent = HipDecoder(backend, w, capacity=128)
+    # The parent takes part too; one session has a different capacity.
+    sessions = [parent] + [parent.session(128 if i != 2 else 256) for i in range(1, len(lengths))]
+    try:
+        for d, p in zip(sessions, prefixes):
+            d.decode(p, p.shape[0])
+        print(f"sessions small count={len(sessions)} steps={steps}", flush=True)
+        toks = HipDecoder.generate_sessions(sessions, steps)
+        assert toks.shape == (len(sessions), steps)
+        for i, (d, p) in enumerate(zip(sessions, prefixes)):
+            assert d.position == p.shape[0] + steps
+            alone, kv = _alone(backend, w, p, steps, 128)
+            assert toks[i].tolist() == alone.tolist(), i
+            for layer, (k, v) in zip((0, cfg.layers - 1), kv):
+                ks, vs = d.kv_read(layer, p.shape[0] + steps)
+                assert np.array_equal(ks.view(np.uint16), k.view(np.uint16)), (i, layer)
+                assert np.array_equal(vs.view(np.uint16), v.view(np.uint16)), (i, layer)
+            ref = oracle_lib.Decoder(w, capacity=128)
+            try:
+                lr = ref.decode(p, p.shape[0])
+                expected = []
+                for _ in range(steps):
+                    t = oracle_lib.greedy(lr)
+                    expected.append(t)
+                    lr = ref.decode(ref.embed([t]), 1)
+                assert toks[i].tolist() == expected, i
+            finally:
+                ref.close()
+        # Sessions continue on their own after a lock-step run.
+        more = sessions[1].generate(4)
+        ref_d = HipDecoder(backend, w, capacity=128)
+        try:
+            ref_d.decode(prefixes[1], lengths[1])
+            assert ref_d.generate(steps + 4)[steps:].tolist() == more.tolist()
+        finally:
+            ref_d.close()
+    finally:
+        for d in sessions[1:]:
+            d.close()
+        parent.close()
+
+
+def test_sessions_reject_bad_batches(backend):
+    from funasrnet_amd.hip import HipDecoder
+    cfg = model.small_config(layers=1)
+    w = model.synthetic(cfg, seed=3)
+    a = HipDecoder(backend, w, capacity=32)
+    b = a.session()
+    other = HipDecoder(backend, w, capacity=32)
+    try:
+        x = np.random.default_rng(1).standard_normal((4, cfg.width)).astype(np.float32)
+        a.decode(x, 4)
+        with pytest.raises(RuntimeError, match="no logits"):
+            HipDecoder.generate_sessions([a, b], 2)
+        b.decode(x, 4)
+        other.decode(x, 4)
+        with pytest.raises(ValueError, match="share one decoder"):
+            HipDecoder.generate_sessions([a, other], 2)
+        with pytest.raises(ValueError, match="twice"):
+            HipDecoder.generate_sessions([a, b, a], 2)
+        with pytest.raises(ValueError, match="exhausted"):
+            HipDecoder.generate_sessions([a, b], 29)
+        assert a.position == b.position == 4
+        t = HipDecoder.generate_sessions([b, a], 3)
+        assert t[0].tolist() == t[1].tolist()  # same prefix, same weights
+    finally:
+        b.close()
+        a.close()
+        other.close()
+
+
+def test_sixteen_qwen3_sessions(backend, oracle_lib):
+    """Sixteen 150-row N(0,1) prefixes (seeds 1-16) on the full-size model,
+    32 lock-step steps: each session's tokens equal its decode alone; two
+    sessions are also checked against the oracle."""
+    from funasrnet_amd.hip import HipDecoder
+    cfg = model.QWEN3_0_6B
+    w = model.synthetic(cfg, seed=0)
+    steps, capacity = 32, 192
+    prefixes = [np.random.default_rng(seed).standard_normal((150, cfg.width)).astype(np.float32)
+                for seed in range(1, 17)]
+    parent = HipDecoder(backend, w, capacity=capacity)
+    sessions = [parent] + [parent.session() for _ in range(15)]
+    try:
+        for d, p in zip(sessions, prefixes):
+            d.decode(p, 150)
+        print("sessions qwen3 count=16 steps=32", flush=True)
+        toks = HipDecoder.generate_sessions(sessions, steps)
+        for i in (0, 5, 15):
+            alone, _ = _alone(backend, w, prefixes[i], steps, capacity)
+            assert toks[i].tolist() == alone.tolist(), i
+        for i in (3, 12):
+            ref = oracle_lib.Decoder(w, capacity=capacity)
+            try:
+                lr = ref.decode(prefixes[i], 150)
+                expected = []
+                for _ in range(16):
+                    t = oracle_lib.greedy(lr)
+                    expected.append(t)
+                    lr = ref.decode(ref.embed([t]), 1)
+                assert toks[i, :16].tolist() == expected, i
+            finally:
+                ref.close()
+    finally:
+        for d in sessions[1:]:
+            d.close()
+        parent.close()
