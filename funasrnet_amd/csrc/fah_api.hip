@@ -153,7 +153,7 @@ int pick_group_rows(int rows, int K, int min_rows, bool even) {
 struct SessionBatch {
   std::vector<fah_decoder*> members;
   int max_positions = 0;
-  DeviceBuffer table, x, a, qkv, q, h, xq, xs, logits;
+  DeviceBuffer table, x, a, qkv, q, h, xq, xs, logits, keys;
   hipGraphExec_t graph = nullptr;
   SessionBatch() = default;
   SessionBatch(const SessionBatch&) = delete;
@@ -520,7 +520,8 @@ void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_
       g.resid = resid;
       g.split_base = d->wt->gu_base;
       g.split_extra = d->wt->gu_extra;
-      check(fah::launch_gemm(g, d->wt->half_scales, mode, s), "prefill gemm");
+      if (fah::few_frame_groups(rows, m.cols, T, mode)) check(fah::launch_gemm_few(g, d->wt->half_scales, mode, s), "prefill gemm");
+      else check(fah::launch_gemm(g, d->wt->half_scales, mode, s), "prefill gemm");
     };
     for (int l = 0; l < c.layers; ++l) {
       check(fah::launch_norm_quantize_rows(d->pf_x.as<float>(), T, c.width, d->wt->attn_norm[l].as<float>(), c.eps, xq, xs,
@@ -659,9 +660,8 @@ void run_kind(fah_decoder* d, int kind, hipStream_t s) {
 
 // ---- lock-step sessions ---------------------------------------------------
 
-// Upper bound on sessions in one lock-step batch, and on their positions
-// (the batched attention keeps a row's probabilities in 60 KiB of LDS).
-constexpr int kMaxSessions = 256;
+// Upper bound on the positions of lock-step sessions (the batched attention
+// keeps a row's probabilities in 60 KiB of LDS).
 constexpr int kSessionPositions = 15360;
 
 // One greedy step of every session at once: the embeddings of their tokens,
@@ -691,7 +691,9 @@ void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s)
     g.resid = resid;
     g.split_base = w.gu_base;
     g.split_extra = w.gu_extra;
-    check(fah::launch_gemm(g, w.half_scales, mode, s), "session gemm");
+    g.keys = b.keys.as<unsigned long long>();
+    if (fah::few_frame_groups(rows, m.cols, S, mode)) check(fah::launch_gemm_few(g, w.half_scales, mode, s), "session gemm");
+    else check(fah::launch_gemm(g, w.half_scales, mode == fah::kGemmGreedy ? fah::kGemmPlain : mode, s), "session gemm");
   };
   auto norm_quantize = [&](const float* x, int K, const DeviceBuffer* norm) {
     check(fah::launch_norm_quantize_rows(x, S, K, norm ? norm->as<float>() : nullptr, norm ? c.eps : 0.0f, xq, xs, s),
@@ -738,8 +740,12 @@ void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s)
     gemm(w.down[l], c.width, b.x.as<float>(), b.a.as<float>(), fah::kGemmResidual);
   }
   norm_quantize(b.x.as<float>(), c.width, &w.output_norm);
-  gemm(head_matrix(d), c.vocab, b.logits.as<float>(), nullptr, fah::kGemmPlain);
-  check(fah::launch_session_greedy(b.logits.as<float>(), c.vocab, table, S, s), "session greedy");
+  const int head_groups = fah::few_frame_groups(c.vocab, c.width, S, fah::kGemmGreedy);
+  require(head_groups > 0, "lock-step sessions: the lm_head shape does not fit the few-frame kernel");
+  gemm(head_matrix(d), c.vocab, b.logits.as<float>(), nullptr, fah::kGemmGreedy);
+  check(fah::launch_greedy_keys(b.keys.as<unsigned long long>(), head_groups, b.logits.as<float>(), c.vocab, table,
+                                S, s),
+        "session greedy");
 }
 
 }  // namespace
@@ -1349,7 +1355,7 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
 int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int steps, int32_t* tokens) {
   if (!sessions || count < 1) return fail(FAH_ERROR_ARGUMENT, "no sessions");
   return guarded([&] {
-    require(count <= kMaxSessions, "at most " + std::to_string(kMaxSessions) + " sessions per batch");
+    require(count <= fah::kFewFrames, "at most " + std::to_string(fah::kFewFrames) + " sessions per batch");
     require(steps >= 0 && (steps == 0 || tokens), "invalid generate arguments");
     const fah_decoder* d0 = sessions[0];
     require(d0 != nullptr, "session is NULL");
@@ -1405,6 +1411,7 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
       b->xq.allocate((size_t)count * widest);
       b->xs.allocate((size_t)count * (widest / 32) * 4);
       b->logits.allocate((size_t)count * k.vocab * 4);
+      b->keys.allocate((size_t)count * std::max(1, fah::few_frame_groups(k.vocab, k.width, count, fah::kGemmGreedy)) * 8);
       if (use_graphs()) {
         hipGraph_t graph = nullptr;
         check(hipStreamSynchronize(s), "hipStreamSynchronize");

@@ -134,8 +134,11 @@ struct GemmArgs {
   const float* resid;   // [frames][out_stride] (residual epilogue; may equal out)
   const float* bias;    // [rows] or null (plain epilogue)
   int split_base, split_extra;  // SwiGLU storage: tiles of base(+1) gate rows then the same up rows
+  // Greedy epilogue (few-frame kernel): the largest greedy key of each
+  // workgroup's rows per frame, [frames][workgroups].
+  unsigned long long* keys;
 };
-enum GemmOut { kGemmPlain = 0, kGemmResidual = 1, kGemmSwiGLU = 2 };
+enum GemmOut { kGemmPlain = 0, kGemmResidual = 1, kGemmSwiGLU = 2, kGemmGreedy = 3 };
 
 struct PrefillAttnArgs {
   const float* q;          // [frames][heads*head_size], normalised and rotated
@@ -153,16 +156,26 @@ struct PrefillAttnArgs {
   // layer `layer` at its position; max_positions bounds position + 1.
   const SessionRef* sessions;
   int layer, max_positions;
+  // Set by launch_attn_prefill: V rows are staged in LDS when every row's
+  // positions fit (bound on positions + 1; 0 = read V from global memory).
+  int stage;
 };
 
 hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t s);
+// Few-frame Q8_0 GEMM (frames <= kFewFrames): rows per workgroup chosen for
+// ~256+ workgroups; returns the workgroup count through *groups (0 = the
+// shape does not fit its LDS, use launch_gemm).
+constexpr int kFewFrames = 16;
+int few_frame_groups(int rows, int K, int frames, int out);
+hipError_t launch_gemm_few(const GemmArgs& g, bool half_scales, int out, hipStream_t s);
+hipError_t launch_greedy_keys(const unsigned long long* keys, int groups, const float* logits, int vocab,
+                              const SessionRef* sessions, int count, hipStream_t s);
 hipError_t launch_norm_quantize_rows(const float* x, int frames, int K, const float* norm_w, float eps, int8_t* xq,
                                      float* xs, hipStream_t s);
 hipError_t launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t s);
 hipError_t launch_session_embed(const int8_t* q, const void* scales, bool half_scales, int K, int vocab,
                                 const SessionRef* sessions, int count, float* x, hipStream_t s);
-hipError_t launch_session_greedy(const float* logits, int vocab, const SessionRef* sessions, int count,
-                                 hipStream_t s);
+
 
 bool persistent_shape_supported(int width, int heads, int kv_heads, int head_size, int ffn, int blocks);
 hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s);

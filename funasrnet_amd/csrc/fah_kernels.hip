@@ -446,30 +446,6 @@ __global__ __launch_bounds__(kThreads) void session_embed_kernel(const int8_t* q
   }
 }
 
-// Lock-step sessions: greedy token of logits row f (QwenDecoder.Greedy,
-// QwenDecoder.cs:278-326: strict '>' so the first maximum wins, NaN at 0
-// returns 0) into session f's token word, then its position advances.
-__global__ __launch_bounds__(kThreads) void session_greedy_kernel(const float* logits, int vocab,
-                                                                  const SessionRef* sessions) {
-  __shared__ unsigned long long best_s[kThreads / kWave];
-  const float* row = logits + (size_t)blockIdx.x * vocab;
-  unsigned long long best = 0ull;
-  for (int i = threadIdx.x; i < vocab; i += kThreads) {
-    const unsigned long long k = greedy_key(row[i], (uint32_t)i);
-    best = k > best ? k : best;
-  }
-  best = wave_max_u64(best);
-  if ((threadIdx.x & (kWave - 1)) == 0) best_s[threadIdx.x / kWave] = best;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < kThreads / kWave; ++w) best = best_s[w] > best ? best_s[w] : best;
-    const float first = row[0];
-    const SessionRef& ss = sessions[blockIdx.x];
-    *ss.token = (first != first || best == 0ull) ? 0 : (int)greedy_index(best);
-    *ss.position = *ss.position + 1;
-  }
-}
-
 __global__ void advance_kernel(int* position, int frames) {
   if (threadIdx.x == 0) *position += frames;
 }
@@ -584,13 +560,6 @@ hipError_t launch_session_embed(const int8_t* q, const void* scales, bool half_s
     session_embed_kernel<ScaleHalf><<<count, kThreads, 0, s>>>(q, scales, K, vocab, sessions, x);
   else
     session_embed_kernel<ScaleFloat><<<count, kThreads, 0, s>>>(q, scales, K, vocab, sessions, x);
-  return hipGetLastError();
-}
-
-hipError_t launch_session_greedy(const float* logits, int vocab, const SessionRef* sessions, int count,
-                                 hipStream_t s) {
-  if (count < 1 || vocab < 1) return hipErrorInvalidValue;
-  session_greedy_kernel<<<count, kThreads, 0, s>>>(logits, vocab, sessions);
   return hipGetLastError();
 }
 

@@ -15,6 +15,8 @@
 // register j holds C[m][n] with n = l % 32 and m = 8*(j/4) + 4*(l/32) + j%4;
 // the A (B) operand of lane l is 16 bytes of row (column) l % 32, lanes l and
 // l + 32 holding the two halves of the 32-byte block.
+#include <algorithm>
+
 #include "fah_device.h"
 #include "fah_internal.h"
 
@@ -22,6 +24,7 @@ namespace fah {
 namespace {
 
 constexpr int kGT = 256;  // threads per GEMM workgroup
+using lds_ptr = __attribute__((address_space(3))) void*;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
@@ -246,6 +249,15 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   const _Float16* kc = kcache + (size_t)kh * capacity * hs;
   const _Float16* vc = vcache + (size_t)kh * capacity * hs;
   float* p_s = attn_s;
+  // V rows [0, n) into LDS (direct global->LDS loads, 1 KiB = 4 rows per
+  // instruction), in flight while the scores are computed.
+  char* v_s = reinterpret_cast<char*>(attn_s) + ((4 * a.stage + 15) & ~15);
+  if (a.stage) {
+    const char* src = reinterpret_cast<const char*>(vc);
+    const int bytes = n * hs * 2;
+    for (int c = wave * 1024; c < bytes; c += 4 * 1024)
+      if (c + 16 * lane < bytes) __builtin_amdgcn_global_load_lds(src + c + 16 * lane, (lds_ptr)(v_s + c), 16, 0, 0);
+  }
   if (tid < hs) q_s[tid] = q[tid];
   lds_barrier();
 
@@ -295,8 +307,23 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   lds_barrier();
   const float inverse = inv_s;
   for (int s = tid; s < n; s += 256) p_s[s] = fmul(p_s[s], inverse);
+  if (a.stage) __builtin_amdgcn_s_waitcnt(0);  // this wave's V rows are in LDS
   lds_barrier();
-  if (tid < hs) {
+  if (tid < hs && a.stage) {
+    const _Float16* v = reinterpret_cast<const _Float16*>(v_s) + tid;
+    float acc = 0.0f;
+    int s = 0;
+    for (; s + 16 <= n; s += 16) {
+      float x[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = from_half(v[(s + k) * hs]);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc = fadd(acc, fmul(x[k], p_s[s + k]));
+    }
+    for (; s < n; ++s) acc = fadd(acc, fmul(from_half(v[s * hs]), p_s[s]));
+    if (a.out) a.out[((size_t)t * a.heads + head) * hs + tid] = acc;
+    q_s[tid] = acc;
+  } else if (tid < hs) {
     const _Float16* v = vc + tid;
     float acc = 0.0f;
     int s = 0;
@@ -325,6 +352,177 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   }
 }
 
+// Few-frame Q8_0 GEMM (lock-step sessions, short prefills): the same
+// per-row block order as q8_gemm_kernel, for frames <= kFewFrames, with a
+// few rows per workgroup so that even the 1024-row projections spread over
+// the whole chip. Each lane takes (row, block) pairs, consecutive lanes
+// consecutive blocks of a row (coalesced 32-byte weight loads, issued before
+// the activations are staged); for every frame it forms the exact int32
+// block dot (v_dot4_i32_i8 x 8) and the term (float)dot * w_scale * x_scale
+// into LDS; then one lane per (row, frame) adds the terms in block order
+// from 0f and applies the epilogue. LDS: activations [frames][K], their
+// scales [frames][B], terms [slots][frames][B + 4].
+constexpr int kFewThreads = 256;
+constexpr int kFewPairs = 4;  // (row, block) pairs per lane
+constexpr int kFewMaxK = 3072;
+constexpr size_t kFewLds = 80 * 1024;  // two workgroups per CU
+
+__host__ __device__ inline size_t few_lds_bytes(int slots, int K, int frames) {
+  const int B = K / 32;
+  return (size_t)frames * K + (size_t)frames * B * 4 + (size_t)slots * frames * (B + 4) * 4 +
+         (size_t)frames * 8;
+}
+
+template <class Scale, int OUT>
+__global__ __launch_bounds__(kFewThreads) void q8_gemm_few_kernel(GemmArgs g, int R) {
+  extern __shared__ __attribute__((aligned(16))) char few_s[];
+  constexpr bool kSwiGLU = OUT == kGemmSwiGLU;
+  const int K = g.K, B = K >> 5, S = g.frames, TB = B + 4, tid = threadIdx.x;
+  const int slots = kSwiGLU ? 2 * R : R;
+  const int r0 = blockIdx.x * R;
+  int8_t* x_s = reinterpret_cast<int8_t*>(few_s);                          // [S][K]
+  float* xs_s = reinterpret_cast<float*>(few_s + (size_t)S * K);           // [S][B]
+  float* t_s = xs_s + S * B;                                               // [slots][S][TB]
+  unsigned long long* key_s = reinterpret_cast<unsigned long long*>(t_s + (size_t)slots * S * TB);  // [S]
+  // Storage row of slot i (SwiGLU: slots [0,R) gate rows, [R,2R) up rows).
+  auto storage_row = [&](int i) -> int {
+    if (kSwiGLU) {
+      const int p = r0 + (i < R ? i : i - R);
+      return p < g.rows ? gate_up_row(p, i < R ? 0 : 1, g.split_base, g.split_extra) : -1;
+    }
+    const int r = r0 + i;
+    return r < g.rows ? r : -1;
+  };
+  const typename Scale::type* ws = reinterpret_cast<const typename Scale::type*>(g.ws);
+  // Lane -> (row step, block): every lane keeps one block b for all its rows,
+  // so one LDS read of a frame's activation block serves kFewPairs rows.
+  const int RS = kFewThreads / B;  // rows per step
+  const int lrow = tid / B, b = tid - lrow * B;
+  const bool active = lrow < RS;
+  // Activations and their scales go to LDS by direct global->LDS loads,
+  // issued together with the weight loads; one wait covers both.
+  {
+    const int wave = tid >> 6, lane = tid & 63;
+    const char* src = reinterpret_cast<const char*>(g.xq);
+    const int xbytes = S * K;
+    for (int c = wave * 1024; c < xbytes; c += 4 * 1024)
+      if (c + 16 * lane < xbytes)
+        __builtin_amdgcn_global_load_lds(src + c + 16 * lane, (lds_ptr)(few_s + c), 16, 0, 0);
+    const char* ssrc = reinterpret_cast<const char*>(g.xs);
+    char* sdst = reinterpret_cast<char*>(xs_s);
+    const int sbytes = S * B * 4;
+    for (int c = wave * 1024; c < sbytes; c += 4 * 1024)
+      if (c + 16 * lane < sbytes)
+        __builtin_amdgcn_global_load_lds(ssrc + c + 16 * lane, (lds_ptr)(sdst + c), 16, 0, 0);
+    if (OUT == kGemmGreedy && tid < S) key_s[tid] = 0ull;
+  }
+  uint4 w0[kFewPairs], w1[kFewPairs];
+  float wsc[kFewPairs];
+#pragma unroll
+  for (int k = 0; k < kFewPairs; ++k) {
+    // Unconditional loads (row clamped into the matrix); rows past the tile
+    // or the matrix are never summed.
+    const int i = lrow + RS * k;
+    const int sr = max(0, active && i < slots ? storage_row(i) : 0);
+    const uint4* wp = reinterpret_cast<const uint4*>(g.w + (size_t)sr * K + 32 * b);
+    w0[k] = wp[0];
+    w1[k] = wp[1];
+    wsc[k] = Scale::get(ws[(size_t)sr * B + b]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  lds_barrier();
+  if (active) {
+    for (int f = 0; f < S; ++f) {
+      const uint4* xp = reinterpret_cast<const uint4*>(x_s + (size_t)f * K + 32 * b);
+      const uint4 x0 = xp[0], x1 = xp[1];
+      const float xsv = xs_s[f * B + b];
+#pragma unroll
+      for (int k = 0; k < kFewPairs; ++k) {
+        const int i = lrow + RS * k;
+        if (i < slots) {
+          int dot = 0;
+          dot = __builtin_amdgcn_sdot4((int)w0[k].x, (int)x0.x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w0[k].y, (int)x0.y, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w0[k].z, (int)x0.z, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w0[k].w, (int)x0.w, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w1[k].x, (int)x1.x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w1[k].y, (int)x1.y, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w1[k].z, (int)x1.z, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w1[k].w, (int)x1.w, dot, false);
+          t_s[((size_t)i * S + f) * TB + b] = fmul(fmul((float)dot, wsc[k]), xsv);
+        }
+      }
+    }
+  }
+  lds_barrier();
+  // Ordered block sums: one lane per (row, frame).
+  auto row_sum = [&](int i, int f) {
+    const float* t = t_s + ((size_t)i * S + f) * TB;
+    float sum = 0.0f;
+    int b = 0;
+    for (; b + 4 <= B; b += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(t + b);
+      sum = fadd(sum, v.x);
+      sum = fadd(sum, v.y);
+      sum = fadd(sum, v.z);
+      sum = fadd(sum, v.w);
+    }
+    for (; b < B; ++b) sum = fadd(sum, t[b]);
+    return sum;
+  };
+  for (int t = tid; t < R * S; t += kFewThreads) {
+    const int i = t / S, f = t - i * S, r = r0 + i;
+    if (r >= g.rows) continue;
+    float v = row_sum(i, f);
+    if (kSwiGLU) {
+      // SwiGLU (Elementwise.cs:167-196).
+      const float u = row_sum(R + i, f);
+      v = fmul(fdiv(v, fadd(1.0f, exp_ref(-v))), u);
+    } else if (OUT == kGemmResidual) {
+      v = fadd(v, g.resid[(size_t)f * g.out_stride + r]);
+    } else if (g.bias) {
+      v = fadd(g.bias[r], v);
+    }
+    g.out[(size_t)f * g.out_stride + r] = v;
+    if (OUT == kGemmGreedy) atomicMax(&key_s[f], greedy_key(v, (uint32_t)r));
+  }
+  if (OUT == kGemmGreedy) {
+    lds_barrier();
+    if (tid < S) g.keys[(size_t)tid * gridDim.x + blockIdx.x] = key_s[tid];
+  }
+}
+
+// Greedy token of each session's logits row from the per-workgroup keys of
+// the few-frame lm_head (QwenDecoder.Greedy, QwenDecoder.cs:278-326: first
+// maximum wins, NaN never wins, NaN at index 0 returns 0), into the
+// session's token word; then the session's position advances.
+__global__ __launch_bounds__(256) void greedy_keys_kernel(const unsigned long long* keys, int groups,
+                                                          const float* logits, int vocab,
+                                                          const SessionRef* sessions) {
+  __shared__ unsigned long long best_s[4];
+  const int f = blockIdx.x, tid = threadIdx.x;
+  const unsigned long long* k = keys + (size_t)f * groups;
+  unsigned long long best = 0ull;
+  int i = tid;
+  for (; i + 3 * 256 < groups; i += 4 * 256) {
+    const unsigned long long a = k[i], b = k[i + 256], c = k[i + 512], d = k[i + 768];
+    const unsigned long long ab = a > b ? a : b, cd = c > d ? c : d;
+    const unsigned long long m = ab > cd ? ab : cd;
+    best = m > best ? m : best;
+  }
+  for (; i < groups; i += 256) best = k[i] > best ? k[i] : best;
+  best = wave_max_u64(best);
+  if ((tid & 63) == 0) best_s[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w) best = best_s[w] > best ? best_s[w] : best;
+    const float first = logits[(size_t)f * vocab];
+    const SessionRef& ss = sessions[f];
+    *ss.token = (first != first || best == 0ull) ? 0 : (int)greedy_index(best);
+    *ss.position = *ss.position + 1;
+  }
+}
+
 template <class Scale>
 hipError_t launch_gemm_scaled(const GemmArgs& g, int out, hipStream_t s) {
   const int B = g.K / 32;
@@ -350,6 +548,63 @@ hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t
   return half_scales ? launch_gemm_scaled<ScaleF16>(g, out, s) : launch_gemm_scaled<ScaleF32>(g, out, s);
 }
 
+// Rows per workgroup of the few-frame GEMM: about rows/256 (so that the grid
+// covers the chip), at most kFewPairs pairs per lane and within kFewLds.
+static int few_rows(int rows, int K, int frames, int out) {
+  const int B = K / 32, per = out == kGemmSwiGLU ? 2 : 1;
+  const int cap = kFewPairs * (kFewThreads / B) / per;  // rows a workgroup's lanes can hold
+  int R = std::max(1, std::min(rows / 256, cap));
+  while (R > 1 && few_lds_bytes(per * R, K, frames) > kFewLds) --R;
+  if (R > cap || few_lds_bytes(per * R, K, frames) > kFewLds) return 0;
+  return R;
+}
+
+int few_frame_groups(int rows, int K, int frames, int out) {
+  if (frames < 1 || frames > kFewFrames || K % 128 != 0 || K > kFewMaxK || rows < 1) return 0;
+  const int R = few_rows(rows, K, frames, out);
+  return R ? (rows + R - 1) / R : 0;
+}
+
+template <class Scale, int OUT>
+static hipError_t launch_few_kernel(const GemmArgs& g, int R, int groups, size_t lds, hipStream_t s) {
+  // Dynamic LDS above the 64 KiB default needs the kernel's limit raised
+  // (once per instantiation; not a stream operation, so capture-safe).
+  static const hipError_t raised = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(q8_gemm_few_kernel<Scale, OUT>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      (int)kFewLds);
+  if (raised != hipSuccess) return raised;
+  q8_gemm_few_kernel<Scale, OUT><<<groups, kFewThreads, lds, s>>>(g, R);
+  return hipGetLastError();
+}
+
+template <class Scale>
+static hipError_t launch_few_scaled(const GemmArgs& g, int out, hipStream_t s) {
+  const int R = few_rows(g.rows, g.K, g.frames, out);
+  const int groups = (g.rows + R - 1) / R;
+  const size_t lds = few_lds_bytes(out == kGemmSwiGLU ? 2 * R : R, g.K, g.frames);
+  switch (out) {
+    case kGemmPlain: return launch_few_kernel<Scale, kGemmPlain>(g, R, groups, lds, s);
+    case kGemmResidual: return launch_few_kernel<Scale, kGemmResidual>(g, R, groups, lds, s);
+    case kGemmSwiGLU: return launch_few_kernel<Scale, kGemmSwiGLU>(g, R, groups, lds, s);
+    case kGemmGreedy: return launch_few_kernel<Scale, kGemmGreedy>(g, R, groups, lds, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemm_few(const GemmArgs& g, bool half_scales, int out, hipStream_t s) {
+  if (!few_frame_groups(g.rows, g.K, g.frames, out)) return hipErrorInvalidValue;
+  if (out == kGemmSwiGLU && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
+  if (out == kGemmGreedy && !g.keys) return hipErrorInvalidValue;
+  return half_scales ? launch_few_scaled<ScaleF16>(g, out, s) : launch_few_scaled<ScaleF32>(g, out, s);
+}
+
+hipError_t launch_greedy_keys(const unsigned long long* keys, int groups, const float* logits, int vocab,
+                              const SessionRef* sessions, int count, hipStream_t s) {
+  if (count < 1 || groups < 1) return hipErrorInvalidValue;
+  greedy_keys_kernel<<<count, 256, 0, s>>>(keys, groups, logits, vocab, sessions);
+  return hipGetLastError();
+}
+
 hipError_t launch_norm_quantize_rows(const float* x, int frames, int K, const float* norm_w, float eps, int8_t* xq,
                                      float* xs, hipStream_t s) {
   if (K % 32 != 0 || K > 4096 || frames < 1) return hipErrorInvalidValue;
@@ -357,12 +612,22 @@ hipError_t launch_norm_quantize_rows(const float* x, int frames, int K, const fl
   return hipGetLastError();
 }
 
-hipError_t launch_attn_prefill(const PrefillAttnArgs& a, hipStream_t s) {
+hipError_t launch_attn_prefill(const PrefillAttnArgs& args, hipStream_t s) {
+  PrefillAttnArgs a = args;
   if (a.head_size != 128 || a.frames < 1 || a.heads % a.kv_heads != 0) return hipErrorInvalidValue;
   if (!a.out && !a.xq) return hipErrorInvalidValue;
   const int n = a.sessions ? a.max_positions : a.position + a.frames;
   if ((!a.sessions && n > a.capacity) || n < 1 || (size_t)n * 4 > 60 * 1024) return hipErrorInvalidValue;
-  attn_prefill_kernel<<<dim3(a.heads, a.frames), 256, (size_t)n * 4, s>>>(a);
+  // V rows are staged in LDS when that keeps three workgroups per CU, or,
+  // for grids of at most two workgroups per CU, up to kStageLds.
+  constexpr size_t kStageLds = 150 * 1024;
+  const size_t staged = (((size_t)4 * n + 15) & ~(size_t)15) + (size_t)n * 256;
+  const bool small_grid = (size_t)a.heads * a.frames <= 512;
+  a.stage = staged <= 48 * 1024 || (small_grid && staged <= kStageLds) ? n : 0;
+  static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_prefill_kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStageLds);
+  if (raised != hipSuccess) return raised;
+  attn_prefill_kernel<<<dim3(a.heads, a.frames), 256, a.stage ? staged : (size_t)n * 4, s>>>(a);
   return hipGetLastError();
 }
 

@@ -1,6 +1,7 @@
-"""Prefill (QwenDecoder.Decode with many rows at once) on the MFMA GEMM path
-against the row-by-row decode path and the oracle: identical logits bits and
-F16 KV rows, then identical greedy tokens when decoding continues."""
+"""Prefill (QwenDecoder.Decode with many rows at once) on the Q8_0 GEMMs
+(the few-frame kernel up to 16 rows, MFMA above) against the row-by-row
+decode path and the oracle: identical logits bits and F16 KV rows, then
+identical greedy tokens when decoding continues."""
 import os
 
 import numpy as np
@@ -33,7 +34,8 @@ def _decode(decoder, x, row_by_row):
             os.environ["FAH_PREFILL"] = old
 
 
-@pytest.mark.parametrize("shape,frames", [("small", 37), ("small", 130), ("qwen3", 150)])
+@pytest.mark.parametrize("shape,frames", [("small", 5), ("small", 16), ("small", 37), ("small", 130),
+                                          ("qwen3", 12), ("qwen3", 150)])
 def test_prefill_matches_row_by_row(backend, oracle_lib, shape, frames):
     from funasrnet_amd.hip import HipDecoder
     cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
