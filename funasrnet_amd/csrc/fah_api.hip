@@ -213,6 +213,7 @@ struct fah_decoder {
   std::shared_ptr<DecoderWeights> wt;
   DeviceBuffer rope_cos, rope_sin, kcache, vcache;
   DeviceBuffer x, qkv_out, qh, scores, attn, a, h, logits, keys, token, position, history, history_count, staging;
+  DeviceBuffer row_q, row_s;  // one quantised row (multi-kernel path over persistent-layout weights)
   int lm_groups = 0;
   int host_position = 0;
   bool have_logits = false;
@@ -333,13 +334,36 @@ void enqueue_layers(fah_decoder* d, hipStream_t s) {
     o.resid = d->x.as<float>();
     check(fah::launch_gemv(o, d->wt->half_scales, fah::kInputFloat, fah::kOutResidual, 1, s), "o gemv");
 
-    fah::GemvArgs gu = gemv_args(d->wt->gateup[l]);
-    gu.x = d->a.as<float>();
-    gu.norm_w = d->wt->ffn_norm[l].as<float>();
-    gu.eps = c.eps;
-    gu.out = d->h.as<float>();
-    gu.out_rows = c.ffn;
-    check(fah::launch_gemv(gu, d->wt->half_scales, fah::kInputNorm, fah::kOutSwiGLU, 1, s), "gate/up gemv");
+    if (d->wt->persistent_layout) {
+      // Gate/up stored in the persistent kernel's tiles: the few-frame GEMM
+      // reads any tiling (norm + quantise first).
+      int8_t* xq = d->row_q.as<int8_t>();
+      float* xs = d->row_s.as<float>();
+      check(fah::launch_norm_quantize_rows(d->a.as<float>(), 1, c.width, d->wt->ffn_norm[l].as<float>(), c.eps, xq, xs,
+                                           s),
+            "ffn_norm");
+      fah::GemmArgs g{};
+      g.w = d->wt->gateup[l].q.as<int8_t>();
+      g.ws = d->wt->gateup[l].s.ptr;
+      g.rows = c.ffn;
+      g.K = c.width;
+      g.xq = xq;
+      g.xs = xs;
+      g.frames = 1;
+      g.out = d->h.as<float>();
+      g.out_stride = c.ffn;
+      g.split_base = d->wt->gu_base;
+      g.split_extra = d->wt->gu_extra;
+      check(fah::launch_gemm_few(g, d->wt->half_scales, fah::kGemmSwiGLU, s), "gate/up gemm");
+    } else {
+      fah::GemvArgs gu = gemv_args(d->wt->gateup[l]);
+      gu.x = d->a.as<float>();
+      gu.norm_w = d->wt->ffn_norm[l].as<float>();
+      gu.eps = c.eps;
+      gu.out = d->h.as<float>();
+      gu.out_rows = c.ffn;
+      check(fah::launch_gemv(gu, d->wt->half_scales, fah::kInputNorm, fah::kOutSwiGLU, 1, s), "gate/up gemv");
+    }
 
     fah::GemvArgs dn = gemv_args(d->wt->down[l]);
     dn.x = d->h.as<float>();
@@ -400,6 +424,8 @@ void init_state(fah_decoder* d, hipStream_t s) {
   d->attn.allocate((size_t)q_width * 4);
   d->a.allocate((size_t)k.width * 4);
   d->h.allocate((size_t)k.ffn * 4);
+  d->row_q.allocate((size_t)std::max(std::max(k.width, q_width), k.ffn));
+  d->row_s.allocate((size_t)std::max(std::max(k.width, q_width), k.ffn) / 32 * 4);
   d->logits.allocate((size_t)k.vocab * 4);
   d->lm_groups = (k.vocab + head.group_rows - 1) / head.group_rows;
   d->keys.allocate((size_t)d->lm_groups * 8);
@@ -642,8 +668,15 @@ bool use_graphs() {
   return on;
 }
 
-void run_kind(fah_decoder* d, int kind, hipStream_t s) {
-  if (d->persistent) {
+// Positions from which a persistent-layout decoder takes the multi-kernel
+// step: the persistent kernel's attention workgroups hold about this many
+// K/V rows in LDS; past it their rows stream from HBM through 16 CUs, while
+// the multi-kernel attention spreads scores and value chains over the chip.
+constexpr int kPersistentPositions = 280;
+
+// `position` is the position of the row this step decodes.
+void run_kind(fah_decoder* d, int kind, hipStream_t s, int position) {
+  if (d->persistent && position < kPersistentPositions) {
     fah::PersistentArgs a = d->pargs;
     a.mode = kind;
     check(fah::launch_decode_step(a, d->blocks, s), "persistent decode step");
@@ -1252,7 +1285,7 @@ int fah_decoder_decode(fah_decoder* d, const float* embeddings, int frames, floa
       for (int f = 0; f < frames; ++f) {
         check(hipMemcpyAsync(d->x.ptr, d->staging.as<char>() + row * f, row, hipMemcpyDeviceToDevice, s), "D2D row");
         bool last = f == frames - 1;
-        run_kind(d, last && logits ? 1 : 0, s);
+        run_kind(d, last && logits ? 1 : 0, s, d->host_position + f);
       }
     }
     if (logits)
@@ -1311,7 +1344,7 @@ int fah_decoder_generate(fah_decoder* d, int steps, int32_t* tokens) {
     hipStream_t s = d->context->stream;
     check(hipSetDevice(d->context->device), "hipSetDevice");
     check(hipMemsetAsync(d->history_count.ptr, 0, 4, s), "reset history");
-    for (int i = 0; i < steps; ++i) run_kind(d, 2, s);
+    for (int i = 0; i < steps; ++i) run_kind(d, 2, s, d->host_position + i);
     if (steps > 0)
       check(hipMemcpyAsync(tokens, d->history.ptr, (size_t)steps * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -1338,13 +1371,12 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
               "session capacity exceeds the persistent decode step's limit of " +
                   std::to_string(fah::persistent_max_capacity()) + " positions");
       d->persistent = true;
-    } else {
-      require(fah::attention_slices(capacity, d->cfg.head_size) != 0,
-              "capacity exceeds the attention kernel's LDS budget");
     }
+    require(fah::attention_slices(capacity, d->cfg.head_size) != 0,
+            "capacity exceeds the attention kernel's LDS budget");
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
-    if (!d->persistent) check(fah::prepare_attention(capacity, d->cfg.head_size), "attention LDS budget");
+    check(fah::prepare_attention(capacity, d->cfg.head_size), "attention LDS budget");
     init_state(d.get(), c->stream);
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     *out = d.release();

@@ -16,6 +16,7 @@
 namespace fah {
 
 constexpr int kThreads = 256;
+using lds_ptr = __attribute__((address_space(3))) void*;
 constexpr int kMaxK = 4096;
 
 struct ScaleHalf {
@@ -351,22 +352,20 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
   float* p_s = dyn_s;                                                     // [2][n]
   _Float16* v_s = reinterpret_cast<_Float16*>(dyn_s + ((2 * n + 3) & ~3));  // [n][C], 16-byte aligned
 
-  // 1. V slice into LDS: C/8 16-byte pieces per position, batches of 16 per thread.
+  // 1. V slice into LDS: C/8 16-byte pieces per position, piece j of the
+  // slice at v_s + 16 j. Direct global->LDS loads: every piece is requested
+  // at once (no register round trip), completed before step 3.
   const int pieces = C / 8, total = n * pieces;
   const _Float16* vbase = a.vcache + (size_t)kh * a.capacity * hs + c0;
-  for (int base = 0; base < total; base += kThreads * 8) {
-    // Branch-free loads (indices clamped in range) keep the batch in registers.
-    int4 reg[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int j = min(base + i * kThreads + tid, total - 1);
-      int t = j / pieces, q = j - t * pieces;
-      reg[i] = *reinterpret_cast<const int4*>(vbase + (size_t)t * hs + q * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int j = base + i * kThreads + tid;
-      if (j < total) *reinterpret_cast<int4*>(v_s + (size_t)j * 8) = reg[i];
+  {
+    const int wave = tid / kWave, lane = tid % kWave;
+    for (int j0 = wave * kWave; j0 < total; j0 += kThreads) {
+      const int j = j0 + lane;
+      if (j < total) {
+        const int t = j / pieces, q = j - t * pieces;
+        __builtin_amdgcn_global_load_lds(vbase + (size_t)t * hs + q * 8,
+                                         (lds_ptr)(reinterpret_cast<char*>(v_s) + (size_t)16 * j0), 16, 0, 0);
+      }
     }
   }
 
@@ -375,9 +374,21 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
   const int head = kh * group + hh;
   const float* scores = a.scores + (size_t)head * a.capacity;
   float m = -__builtin_inff();
-  for (int t = lt; t < n; t += 128) {
-    float v = scores[t];
-    p_s[hh * n + t] = v;
+  int t0 = lt;
+  // Eight score loads in flight per lane.
+  for (; t0 + 7 * 128 < n; t0 += 8 * 128) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = scores[t0 + 128 * k];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      p_s[hh * n + t0 + 128 * k] = v[k];
+      m = nan_max(m, v[k]);
+    }
+  }
+  for (; t0 < n; t0 += 128) {
+    float v = scores[t0];
+    p_s[hh * n + t0] = v;
     m = nan_max(m, v);
   }
   for (int s = 32; s >= 1; s >>= 1) m = nan_max(m, __shfl_xor(m, s, kWave));
@@ -388,8 +399,18 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
   __syncthreads();
   const int full = n & ~7;
   if (lt < 8) {
+    // Lane j: p[j] + p[j+8] + ... in order, in double; eight loads ahead.
+    const float* ph = p_s + hh * n;
     double l = 0.0;
-    for (int t = lt; t < full; t += 8) l = l + (double)p_s[hh * n + t];
+    int t = lt;
+    for (; t + 56 < full; t += 64) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = ph[t + 8 * k];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) l = l + (double)v[k];
+    }
+    for (; t < full; t += 8) l = l + (double)ph[t];
     lane_s[hh][lt] = l;
   }
   __syncthreads();
@@ -402,6 +423,7 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
   __syncthreads();
   const float inverse = inv_s[hh];
   for (int t = lt; t < n; t += 128) p_s[hh * n + t] = fmul(p_s[hh * n + t], inverse);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's V pieces are in LDS
   __syncthreads();
 
   // 3. Time-ordered value chains, one per (head, channel) of this slice.
@@ -412,13 +434,37 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
     const _Float16* v = v_s + ch;
     float acc = 0.0f;
     int t = 0;
-    for (; t + 4 <= n; t += 4) {
-      float v0 = from_half(v[(t + 0) * C]), v1 = from_half(v[(t + 1) * C]);
-      float v2 = from_half(v[(t + 2) * C]), v3 = from_half(v[(t + 3) * C]);
-      acc = fadd(acc, fmul(v0, p[t + 0]));
-      acc = fadd(acc, fmul(v1, p[t + 1]));
-      acc = fadd(acc, fmul(v2, p[t + 2]));
-      acc = fadd(acc, fmul(v3, p[t + 3]));
+    // Software-pipelined: the next 16 positions' values and probabilities
+    // are loaded while the current 16 are added, so the chain does not wait
+    // on LDS latency.
+    constexpr int kBlk = 16;
+    float vc[kBlk], pc[kBlk];
+    if (n >= kBlk) {
+#pragma unroll
+      for (int k = 0; k < kBlk; ++k) {
+        vc[k] = from_half(v[k * C]);
+        pc[k] = p[k];
+      }
+    }
+    for (; t + 2 * kBlk <= n; t += kBlk) {
+      float vn[kBlk], pn[kBlk];
+#pragma unroll
+      for (int k = 0; k < kBlk; ++k) {
+        vn[k] = from_half(v[(t + kBlk + k) * C]);
+        pn[k] = p[t + kBlk + k];
+      }
+#pragma unroll
+      for (int k = 0; k < kBlk; ++k) acc = fadd(acc, fmul(vc[k], pc[k]));
+#pragma unroll
+      for (int k = 0; k < kBlk; ++k) {
+        vc[k] = vn[k];
+        pc[k] = pn[k];
+      }
+    }
+    if (t + kBlk <= n) {
+#pragma unroll
+      for (int k = 0; k < kBlk; ++k) acc = fadd(acc, fmul(vc[k], pc[k]));
+      t += kBlk;
     }
     for (; t < n; ++t) acc = fadd(acc, fmul(from_half(v[t * C]), p[t]));
     a.out[(size_t)(kh * group + h2) * hs + c0 + ch] = acc;

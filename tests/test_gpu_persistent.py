@@ -137,3 +137,43 @@ def test_long_cache_matches_graph_path(backend, oracle_lib, shape):
     finally:
         fast.close()
         slow.close()
+
+
+@pytest.mark.parametrize("shape", ["small", "qwen3"])
+def test_steps_across_the_persistent_range(backend, shape):
+    """A decoder with the persistent layout takes the multi-kernel step from
+    position 280 on: generating across that boundary, and decoding single
+    rows after it, matches a decoder that never used the persistent kernel."""
+    cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
+    w = model.synthetic(cfg, seed=15)
+    prefix = np.random.default_rng(16).standard_normal((266, cfg.width)).astype(np.float32)
+    fast = _decoder(backend, w, True, 512)
+    slow = _decoder(backend, w, False, 512)
+    try:
+        assert fast.persistent and not slow.persistent
+        print(f"persistent boundary {shape}", flush=True)
+        lf = fast.decode(prefix, 266)
+        ls = slow.decode(prefix, 266)
+        assert np.array_equal(lf.view(np.uint32), ls.view(np.uint32))
+        tf = fast.generate(30)
+        ts = slow.generate(30)
+        assert tf.tolist() == ts.tolist()
+        x = fast.embed([int(tf[-1])])
+        lf = fast.decode(x, 1)
+        ls = slow.decode(x, 1)
+        assert np.array_equal(lf.view(np.uint32), ls.view(np.uint32))
+        for layer in (0, cfg.layers - 1):
+            kf, vf = fast.kv_read(layer, 297)
+            ks, vs = slow.kv_read(layer, 297)
+            assert np.array_equal(kf.view(np.uint16), ks.view(np.uint16))
+            assert np.array_equal(vf.view(np.uint16), vs.view(np.uint16))
+        # Back below the boundary: the persistent kernel again.
+        fast.set_position(200)
+        slow.set_position(200)
+        lf = fast.decode(x, 1)
+        ls = slow.decode(x, 1)
+        assert np.array_equal(lf.view(np.uint32), ls.view(np.uint32))
+        assert fast.generate(5).tolist() == slow.generate(5).tolist()
+    finally:
+        fast.close()
+        slow.close()
