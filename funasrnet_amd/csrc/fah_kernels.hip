@@ -16,6 +16,7 @@
 namespace fah {
 
 constexpr int kThreads = 256;
+constexpr int kRing = 256, kRingRow = kRing + 4;  // value-chain product ring: positions per slot, padded row
 using lds_ptr = __attribute__((address_space(3))) void*;
 constexpr int kMaxK = 4096;
 
@@ -353,20 +354,25 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
   _Float16* v_s = reinterpret_cast<_Float16*>(dyn_s + ((2 * n + 3) & ~3));  // [n][C], 16-byte aligned
 
   // 1. V slice into LDS: C/8 16-byte pieces per position, piece j of the
-  // slice at v_s + 16 j. Direct global->LDS loads: every piece is requested
-  // at once (no register round trip), completed before step 3.
+  // slice at v_s + 16 j. Batches of 16 pieces per thread: the loads are
+  // unconditional (index clamped) and every store too (pieces past the end
+  // go to a spare slot), so a batch's loads are all in flight at once.
   const int pieces = C / 8, total = n * pieces;
   const _Float16* vbase = a.vcache + (size_t)kh * a.capacity * hs + c0;
-  {
-    const int wave = tid / kWave, lane = tid % kWave;
-    for (int j0 = wave * kWave; j0 < total; j0 += kThreads) {
-      const int j = j0 + lane;
-      if (j < total) {
-        const int t = j / pieces, q = j - t * pieces;
-        __builtin_amdgcn_global_load_lds(vbase + (size_t)t * hs + q * 8,
-                                         (lds_ptr)(reinterpret_cast<char*>(v_s) + (size_t)16 * j0), 16, 0, 0);
-      }
-    }
+  for (int base = 0; base < total; base += kThreads * 8) {
+    int4 r0, r1, r2, r3, r4, r5, r6, r7;
+    auto piece = [&](int i) {
+      const int j = min(base + i * kThreads + tid, total - 1);
+      const int t = j / pieces, q = j - t * pieces;
+      return *reinterpret_cast<const int4*>(vbase + (size_t)t * hs + q * 8);
+    };
+    auto slot = [&](int i) {
+      return reinterpret_cast<int4*>(v_s + (size_t)min(base + i * kThreads + tid, total) * 8);  // total: spare
+    };
+    r0 = piece(0); r1 = piece(1); r2 = piece(2); r3 = piece(3);
+    r4 = piece(4); r5 = piece(5); r6 = piece(6); r7 = piece(7);
+    *slot(0) = r0; *slot(1) = r1; *slot(2) = r2; *slot(3) = r3;
+    *slot(4) = r4; *slot(5) = r5; *slot(6) = r6; *slot(7) = r7;
   }
 
   // 2. Softmax of the two query heads: threads [0,128) head 0, [128,256) head 1.
@@ -423,50 +429,81 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
   __syncthreads();
   const float inverse = inv_s[hh];
   for (int t = lt; t < n; t += 128) p_s[hh * n + t] = fmul(p_s[hh * n + t], inverse);
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's V pieces are in LDS
   __syncthreads();
 
-  // 3. Time-ordered value chains, one per (head, channel) of this slice.
-  if (tid < 2 * C) {
-    const int ch = tid / C == 0 ? tid : tid - C;
-    const int h2 = tid / C;
-    const float* p = p_s + h2 * n;
-    const _Float16* v = v_s + ch;
-    float acc = 0.0f;
-    int t = 0;
-    // Software-pipelined: the next 16 positions' values and probabilities
-    // are loaded while the current 16 are added, so the chain does not wait
-    // on LDS latency.
-    constexpr int kBlk = 16;
-    float vc[kBlk], pc[kBlk];
-    if (n >= kBlk) {
+  // 3. Time-ordered value chains, one per (head, channel) of this slice, run
+  // by wave 0. Waves 1-3 form the products v[t][c] * p[t] of the next block
+  // of kRing positions into a two-slot LDS ring meanwhile, so each chain
+  // step is one add (the product's rounding is the same wherever it is made).
+  const int chains = 2 * C, cshift = __builtin_ctz(C);
+  float* ring = reinterpret_cast<float*>(reinterpret_cast<char*>(v_s) + (((size_t)n * C * 2 + 16 + 15) & ~(size_t)15));
+  const int blocks = (n + kRing - 1) / kRing;
+  const int wave = tid / kWave;
+  auto produce = [&](int j) {
+    float* slot = ring + (size_t)(j & 1) * chains * kRingRow;
+    const int t0 = j * kRing, len = min(kRing, n - t0);
+    const int gshift = cshift - 3;  // 8-channel groups per position: C / 8
+    // One task = one position's 8-channel group: one 16-byte V read and the
+    // two heads' probabilities give 16 products.
+    for (int task = tid - kWave; task < (len << gshift); task += kThreads - kWave) {
+      const int tt = task >> gshift, g = task & ((1 << gshift) - 1), t = t0 + tt;
+      const uint4 raw = *reinterpret_cast<const uint4*>(v_s + (size_t)t * C + 8 * g);
+      const float p0 = p_s[t], p1 = p_s[n + t];
+      const _Float16* hv = reinterpret_cast<const _Float16*>(&raw);
 #pragma unroll
-      for (int k = 0; k < kBlk; ++k) {
-        vc[k] = from_half(v[k * C]);
-        pc[k] = p[k];
+      for (int k = 0; k < 8; ++k) {
+        const float v = from_half(hv[k]);
+        slot[(size_t)(8 * g + k) * kRingRow + tt] = fmul(v, p0);
+        slot[(size_t)(C + 8 * g + k) * kRingRow + tt] = fmul(v, p1);
       }
     }
-    for (; t + 2 * kBlk <= n; t += kBlk) {
-      float vn[kBlk], pn[kBlk];
+  };
+  if (wave > 0) produce(0);
+  lds_barrier();
+  float acc = 0.0f;
+  for (int j = 0; j < blocks; ++j) {
+    if (wave > 0) {
+      if (j + 1 < blocks) produce(j + 1);
+    } else if (tid < chains) {
+      const float* row = ring + (size_t)(j & 1) * chains * kRingRow + (size_t)tid * kRingRow;
+      const int len = min(kRing, n - j * kRing);
+      int tt = 0;
+      if (len == kRing) {
+        // Full block: the next 16 products are read while these 16 are added.
+        float4 q[4], qn[4];
 #pragma unroll
-      for (int k = 0; k < kBlk; ++k) {
-        vn[k] = from_half(v[(t + kBlk + k) * C]);
-        pn[k] = p[t + kBlk + k];
+        for (int k = 0; k < 4; ++k) q[k] = *reinterpret_cast<const float4*>(row + 4 * k);
+#pragma unroll
+        for (int i = 0; i < kRing / 16; ++i) {
+          if (i + 1 < kRing / 16) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) qn[k] = *reinterpret_cast<const float4*>(row + 16 * (i + 1) + 4 * k);
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            acc = fadd(acc, q[k].x);
+            acc = fadd(acc, q[k].y);
+            acc = fadd(acc, q[k].z);
+            acc = fadd(acc, q[k].w);
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) q[k] = qn[k];
+        }
+        tt = kRing;
       }
-#pragma unroll
-      for (int k = 0; k < kBlk; ++k) acc = fadd(acc, fmul(vc[k], pc[k]));
-#pragma unroll
-      for (int k = 0; k < kBlk; ++k) {
-        vc[k] = vn[k];
-        pc[k] = pn[k];
+      for (; tt + 4 <= len; tt += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(row + tt);
+        acc = fadd(acc, q.x);
+        acc = fadd(acc, q.y);
+        acc = fadd(acc, q.z);
+        acc = fadd(acc, q.w);
       }
+      for (; tt < len; ++tt) acc = fadd(acc, row[tt]);
     }
-    if (t + kBlk <= n) {
-#pragma unroll
-      for (int k = 0; k < kBlk; ++k) acc = fadd(acc, fmul(vc[k], pc[k]));
-      t += kBlk;
-    }
-    for (; t < n; ++t) acc = fadd(acc, fmul(from_half(v[t * C]), p[t]));
+    lds_barrier();
+  }
+  if (tid < chains) {
+    const int h2 = tid >> cshift, ch = tid & (C - 1);
     a.out[(size_t)(kh * group + h2) * hs + c0 + ch] = acc;
   }
 }
@@ -624,16 +661,24 @@ hipError_t launch_qk_prepare(const QkArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Dynamic LDS of attn_values_kernel for `capacity` positions and S slices:
+// probabilities 2 x 4 B and V 2C B per position (C = head_size / S), one
+// spare 16-byte V slot, the padding to 16 B after each, and the product ring
+// 2 x 2C x kRingRow floats.
+static size_t values_lds(int capacity, int head_size, int slices) {
+  const int C = head_size / slices;
+  return (size_t)capacity * (2 * C + 8) + 48 + (size_t)2 * 2 * C * kRingRow * 4;
+}
+
 int attention_slices(int capacity, int head_size) {
-  // LDS per workgroup: n * (2 * head_size / S + 8) bytes must fit 160 KB.
   for (int slices = 4; slices <= 16; slices *= 2)
-    if ((size_t)capacity * (2 * head_size / slices + 8) + 1024 <= 160 * 1024) return slices;
+    if (values_lds(capacity, head_size, slices) + 1024 <= 160 * 1024) return slices;
   return 0;
 }
 
 size_t attention_lds_bytes(int capacity, int head_size) {
   int slices = attention_slices(capacity, head_size);
-  return slices ? (size_t)capacity * (2 * head_size / slices + 8) + 16 : 0;
+  return slices ? values_lds(capacity, head_size, slices) : 0;
 }
 
 hipError_t prepare_attention(int capacity, int head_size) {
