@@ -606,10 +606,13 @@ void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_
   }
 }
 
-// Row-by-row decode below this many frames (and with FAH_PREFILL=0).
-bool use_prefill(int frames) {
+// Row-by-row decode below this many frames, for widths the GEMMs do not
+// take (multiples of 128 up to 3072), and with FAH_PREFILL=0.
+bool use_prefill(const fah_decoder* d, int frames) {
   const char* env = std::getenv("FAH_PREFILL");
-  return frames >= 4 && !(env && env[0] == '0');
+  const fah_decoder_config& c = d->cfg;
+  auto fits = [](int k) { return k % 128 == 0 && k <= 3072; };
+  return frames >= 4 && fits(c.width) && fits(c.ffn) && fits(d->q_width) && !(env && env[0] == '0');
 }
 
 hipGraphExec_t capture(fah_decoder* d, int kind) {
@@ -895,7 +898,9 @@ int64_t fah_weight_device_bytes(const fah_weight* w) { return w ? (int64_t)(w->q
 
 // Many rows at once go through the MFMA GEMM (same per-row block order).
 constexpr int kGemmMinFrames = 4;
-bool gemm_fits(const fah_weight* w, int frames) { return frames >= kGemmMinFrames && w->cols <= 3072; }
+bool gemm_fits(const fah_weight* w, int frames) {
+  return frames >= kGemmMinFrames && w->cols <= 3072 && w->cols % 128 == 0;
+}
 
 void launch_weight_gemm(const fah_weight* w, const int8_t* xq, const float* xs, int frames, float* out,
                         const float* bias, hipStream_t s) {
@@ -1279,7 +1284,7 @@ int fah_decoder_decode(fah_decoder* d, const float* embeddings, int frames, floa
     size_t row = (size_t)d->cfg.width * 4;
     d->staging.ensure(row * frames);
     check(hipMemcpyAsync(d->staging.ptr, embeddings, row * frames, hipMemcpyHostToDevice, s), "H2D embeddings");
-    if (use_prefill(frames)) {
+    if (use_prefill(d, frames)) {
       prefill(d, d->staging.as<float>(), frames, logits != nullptr, s);
     } else {
       for (int f = 0; f < frames; ++f) {
@@ -1391,6 +1396,8 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
     require(steps >= 0 && (steps == 0 || tokens), "invalid generate arguments");
     const fah_decoder* d0 = sessions[0];
     require(d0 != nullptr, "session is NULL");
+    require(d0->cfg.width % 128 == 0 && d0->cfg.ffn % 128 == 0 && d0->q_width % 128 == 0 && d0->cfg.ffn <= 3072,
+            "lock-step sessions need projection widths that are multiples of 128, at most 3072");
     // The batched attention keeps one row's probabilities in LDS: positions
     // up to kSessionPositions; the captured step is sized for that bound (or
     // the largest capacity, if smaller) so it serves every later call.

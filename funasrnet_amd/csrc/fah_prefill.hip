@@ -87,33 +87,32 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
   const int ml = lane & 31, half = lane >> 5;
   const int sr = storage_row(32 * rw + ml);
   const int frame = f0 + 32 * fw + ml;
-  const int8_t* ap = sr >= 0 ? g.w + (size_t)sr * g.K + 16 * half : nullptr;
-  const int8_t* bp = frame < g.frames ? g.xq + (size_t)frame * g.K + 16 * half : nullptr;
-  const v4i zero4 = {0, 0, 0, 0};
+  // Rows past the matrix and frames past the input read row / frame 0: their
+  // sums are never stored, and unconditional loads keep the prefetch exact
+  // (a conditional load makes the compiler wait for every load in flight).
+  const int8_t* ap = g.w + (size_t)max(sr, 0) * g.K + 16 * half;
+  const int8_t* bp = g.xq + (size_t)(frame < g.frames ? frame : 0) * g.K + 16 * half;
   const v16i zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   float acc[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
 
-  // Operands of four blocks are loaded one group ahead of their use.
+  // Operands of four blocks are loaded one group ahead of their use (block
+  // index clamped: the loads past the last group are never used).
   auto load4 = [&](v4i* av, v4i* bv, int b0) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int b = b0 + k;
-      av[k] = (ap && b < B) ? *reinterpret_cast<const v4i*>(ap + (size_t)b * 32) : zero4;
-      bv[k] = (bp && b < B) ? *reinterpret_cast<const v4i*>(bp + (size_t)b * 32) : zero4;
+      const int b = min(b0 + k, B - 1);
+      av[k] = *reinterpret_cast<const v4i*>(ap + (size_t)b * 32);
+      bv[k] = *reinterpret_cast<const v4i*>(bp + (size_t)b * 32);
     }
   };
-  v4i a_cur[4], b_cur[4];
-  load4(a_cur, b_cur, 0);
-  for (int b0 = 0; b0 < B; b0 += 4) {
-    v4i a_nx[4], b_nx[4];
-    load4(a_nx, b_nx, b0 + 4);
+  auto compute4 = [&](const v4i* av, const v4i* bv, int b0) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int b = b0 + k;
       if (b < B) {
-        const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_cur[k], b_cur[k], zero16, 0, 0, 0);
+        const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[k], bv[k], zero16, 0, 0, 0);
         const float xsv = xs_s[b * 64 + 32 * fw + ml];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -125,11 +124,16 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
         }
       }
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      a_cur[k] = a_nx[k];
-      b_cur[k] = b_nx[k];
-    }
+  };
+  // Two register sets in turn (no copies between them, so the wait before
+  // a group's MFMAs leaves the other group's loads in flight).
+  v4i aA[4], bA[4], aB[4], bB[4];
+  load4(aA, bA, 0);
+  for (int b0 = 0; b0 < B; b0 += 8) {
+    load4(aB, bB, b0 + 4);
+    compute4(aA, bA, b0);
+    load4(aA, bA, b0 + 8);
+    compute4(aB, bB, b0 + 4);
   }
 
   if (!kSwiGLU) {
@@ -543,7 +547,7 @@ hipError_t launch_gemm_scaled(const GemmArgs& g, int out, hipStream_t s) {
 hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t s) {
   // The row and frame scales of the whole K range live in LDS (512 B per
   // block): K <= 3072 keeps the tile, with the SwiGLU exchange, under 64 KiB.
-  if (g.K % 32 != 0 || g.K > 3072 || g.rows < 1 || g.frames < 1) return hipErrorInvalidValue;
+  if (g.K % 128 != 0 || g.K > 3072 || g.rows < 1 || g.frames < 1) return hipErrorInvalidValue;
   if (out == kGemmSwiGLU && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
   return half_scales ? launch_gemm_scaled<ScaleF16>(g, out, s) : launch_gemm_scaled<ScaleF32>(g, out, s);
 }
