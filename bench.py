@@ -264,6 +264,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU sample length")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the GEMV sweep, prefill, long-cache and sessions measurements")
+    ap.add_argument("--extra-only", choices=["gemv_sweep", "prefill", "long_kv", "sessions"],
+                    help="run one of the extra measurements alone and print its JSON (for profilers)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
@@ -278,6 +280,13 @@ def main() -> int:
 
     cfg = model.QWEN3_0_6B
     weights = model.synthetic(cfg, seed=0)
+    if args.extra_only:
+        backend = HipBackend(0)
+        run = {"gemv_sweep": lambda: gemv_sweep(backend), "prefill": lambda: prefill_ttft(backend, weights),
+               "long_kv": lambda: long_kv(backend, weights), "sessions": lambda: sessions_decode(backend, weights)}
+        print(json.dumps({args.extra_only: run[args.extra_only]()}), flush=True)
+        backend.close()
+        return 0
     prefix = np.random.default_rng(0).standard_normal((PREFIX, cfg.width)).astype(np.float32)
 
     backend = HipBackend(0)
