@@ -527,6 +527,222 @@ __global__ __launch_bounds__(256) void greedy_keys_kernel(const unsigned long lo
   }
 }
 
+// Causal attention for a block of kRowBlock query rows and both query heads
+// of one KV head: 16 (head, row) pairs share every K and V row the block
+// reads. Per pair the arithmetic is the decode path's (AttentionAvx.cs:74-224,
+// SoftmaxAvx.cs:11-58, per row as QwenDecoder.cs:206-224 does): eight
+// channel-strided score accumulators and their pairwise tree, the exact
+// softmax with a double denominator, time-ordered value sums. Layout: scores
+// and probabilities [position][pair] in LDS (pair = head * 8 + row), V rows
+// in double-buffered LDS chunks; output rows quantised to Q8_0 per 32-block.
+constexpr int kRowBlock = 8;
+constexpr int kRowPairs = 2 * kRowBlock;
+constexpr int kVRows = 64;  // V rows per LDS chunk (256 B each)
+
+__host__ __device__ inline size_t rows_lds_bytes(int nmax) {
+  return (size_t)kRowPairs * nmax * 4 + (size_t)2 * kVRows * 256;
+}
+
+__device__ __forceinline__ float max16_nan(float m) {  // over each row of 16 lanes
+  m = nan_max_p(m, u2f(dpp_u32<kDppQuadXor1>(f2u(m))));
+  m = nan_max_p(m, u2f(dpp_u32<kDppQuadXor2>(f2u(m))));
+  m = nan_max_p(m, u2f(dpp_u32<kDppHalfMirror>(f2u(m))));
+  return nan_max_p(m, u2f(dpp_u32<kDppMirror>(f2u(m))));
+}
+
+__global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float rows_s[];
+  __shared__ __attribute__((aligned(16))) float q_s[kRowPairs * 128];  // q rows, then output rows
+  __shared__ double lane_s[kRowPairs * 8];
+  __shared__ float inv_s[kRowPairs];
+  // The last row blocks see the most positions: they are dispatched first.
+  const int kh = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * kRowBlock, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, hs = 128;
+  const int rows = min(kRowBlock, a.frames - r0);
+  const int n0 = a.position + r0 + 1;  // positions the block's first row sees; row rr sees n0 + rr
+  const int nmax = n0 + rows - 1;
+  float* p_s = rows_s;  // [nmax][kRowPairs]
+  char* vbuf = reinterpret_cast<char*>(rows_s + (size_t)kRowPairs * nmax);
+  const _Float16* kc = a.kcache + (size_t)kh * a.capacity * hs;
+  const _Float16* vc = a.vcache + (size_t)kh * a.capacity * hs;
+  for (int i = tid; i < kRowPairs * hs; i += 256) {
+    const int pi = i >> 7, c = i & 127, hh = pi >> 3, rr = pi & 7;
+    q_s[i] = rr < rows ? a.q[((size_t)(r0 + rr) * a.heads + 2 * kh + hh) * hs + c] : 0.0f;
+  }
+  __syncthreads();
+
+  // 1. Scores: one position per lane, its K row held in registers while the
+  // pairs are scored, eight pairs at a time.
+  for (int t = tid; t < nmax; t += 256) {
+    const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)t * hs);
+    uint4 kk[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) kk[i] = row[i];
+#pragma unroll 1
+    for (int part = 0; part < 4; ++part) {  // four pairs at a time
+      float acc[4][8];
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[p][j] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t w[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
+        float k8[8];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          k8[2 * m] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu)));
+          k8[2 * m + 1] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16)));
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float* q = q_s + (4 * part + p) * hs + 8 * i;
+          const float4 q0 = *reinterpret_cast<const float4*>(q);
+          const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
+          acc[p][0] = fadd(acc[p][0], fmul(q0.x, k8[0]));
+          acc[p][1] = fadd(acc[p][1], fmul(q0.y, k8[1]));
+          acc[p][2] = fadd(acc[p][2], fmul(q0.z, k8[2]));
+          acc[p][3] = fadd(acc[p][3], fmul(q0.w, k8[3]));
+          acc[p][4] = fadd(acc[p][4], fmul(q1.x, k8[4]));
+          acc[p][5] = fadd(acc[p][5], fmul(q1.y, k8[5]));
+          acc[p][6] = fadd(acc[p][6], fmul(q1.z, k8[6]));
+          acc[p][7] = fadd(acc[p][7], fmul(q1.w, k8[7]));
+        }
+      }
+      float sc[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float v = fadd(fadd(fadd(acc[p][0], acc[p][4]), fadd(acc[p][1], acc[p][5])),
+                             fadd(fadd(acc[p][2], acc[p][6]), fadd(acc[p][3], acc[p][7])));
+        sc[p] = fdiv(v, a.divisor);
+      }
+      *reinterpret_cast<float4*>(p_s + (size_t)t * kRowPairs + 4 * part) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+    }
+  }
+  __syncthreads();
+
+  // 2. Softmax: 16 lanes per pair, four pairs per wave.
+  const int pi = wave * 4 + (lane >> 4), sub = lane & 15;
+  const int n = (pi & 7) < rows ? n0 + (pi & 7) : 0;
+  {
+    float m = -__builtin_inff();
+    for (int t = sub; t < n; t += 16) m = nan_max_p(m, p_s[t * kRowPairs + pi]);
+    m = max16_nan(m);
+    for (int t = sub; t < n; t += 16) p_s[t * kRowPairs + pi] = exp_ref(fadd(p_s[t * kRowPairs + pi], -m));
+  }
+  __syncthreads();
+  const int full = n & ~7;
+  if (sub < 8) {
+    // Lane j of the pair: p[j] + p[j+8] + ... in order, in double.
+    double l = 0.0;
+    int t = sub;
+    for (; t + 56 < full; t += 64) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = p_s[(t + 8 * k) * kRowPairs + pi];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) l = l + (double)v[k];
+    }
+    for (; t < full; t += 8) l = l + (double)p_s[t * kRowPairs + pi];
+    lane_s[pi * 8 + sub] = l;
+  }
+  __syncthreads();
+  if (sub == 0 && n > 0) {
+    const double* L = lane_s + pi * 8;
+    double sum = ((L[0] + L[4]) + (L[1] + L[5])) + ((L[2] + L[6]) + (L[3] + L[7]));
+    for (int t = full; t < n; ++t) sum = sum + (double)p_s[t * kRowPairs + pi];
+    inv_s[pi] = (float)(1.0 / sum);
+  }
+  __syncthreads();
+  {
+    const float inverse = n > 0 ? inv_s[pi] : 0.0f;
+    for (int t = sub; t < n; t += 16) p_s[t * kRowPairs + pi] = fmul(p_s[t * kRowPairs + pi], inverse);
+  }
+
+  // 3. Time-ordered value sums: lane = (head, channel), one sum per row of
+  // the block; V rows through LDS in chunks, the next chunk's loads in
+  // flight while the current one is added.
+  const int hh = tid >> 7, c = tid & 127;
+  float acc[kRowBlock];
+#pragma unroll
+  for (int rr = 0; rr < kRowBlock; ++rr) acc[rr] = 0.0f;
+  const int chunks = (nmax + kVRows - 1) / kVRows;
+  uint4 pre0, pre1, pre2, pre3;
+#define FAH_LOAD_CHUNK(j)                                                                       \
+  do {                                                                                          \
+    const uint4* src_ = reinterpret_cast<const uint4*>(vc);                                     \
+    pre0 = src_[(size_t)min((j) * kVRows + ((tid) >> 4), nmax - 1) * 16 + (tid & 15)];          \
+    pre1 = src_[(size_t)min((j) * kVRows + ((tid + 256) >> 4), nmax - 1) * 16 + (tid & 15)];    \
+    pre2 = src_[(size_t)min((j) * kVRows + ((tid + 512) >> 4), nmax - 1) * 16 + (tid & 15)];    \
+    pre3 = src_[(size_t)min((j) * kVRows + ((tid + 768) >> 4), nmax - 1) * 16 + (tid & 15)];    \
+  } while (0)
+#define FAH_STORE_CHUNK(j)                                                                      \
+  do {                                                                                          \
+    uint4* dst_ = reinterpret_cast<uint4*>(vbuf + (size_t)((j) & 1) * kVRows * 256);            \
+    dst_[tid] = pre0;                                                                           \
+    dst_[tid + 256] = pre1;                                                                     \
+    dst_[tid + 512] = pre2;                                                                     \
+    dst_[tid + 768] = pre3;                                                                     \
+  } while (0)
+  FAH_LOAD_CHUNK(0);
+  FAH_STORE_CHUNK(0);
+  __syncthreads();
+  for (int j = 0; j < chunks; ++j) {
+    if (j + 1 < chunks) FAH_LOAD_CHUNK(j + 1);
+    const _Float16* vr = reinterpret_cast<const _Float16*>(vbuf + (size_t)(j & 1) * kVRows * 256) + c;
+    const int t0 = j * kVRows, len = min(kVRows, nmax - t0);
+    const int all = max(0, min(len, n0 - t0));  // positions every row of the block sees
+    int tt = 0;
+    for (; tt < all; ++tt) {
+      const float v = from_half(vr[tt * hs]);
+      const float* pp = p_s + (size_t)(t0 + tt) * kRowPairs + 8 * hh;
+      const float4 pa = *reinterpret_cast<const float4*>(pp), pb = *reinterpret_cast<const float4*>(pp + 4);
+      acc[0] = fadd(acc[0], fmul(v, pa.x));
+      acc[1] = fadd(acc[1], fmul(v, pa.y));
+      acc[2] = fadd(acc[2], fmul(v, pa.z));
+      acc[3] = fadd(acc[3], fmul(v, pa.w));
+      acc[4] = fadd(acc[4], fmul(v, pb.x));
+      acc[5] = fadd(acc[5], fmul(v, pb.y));
+      acc[6] = fadd(acc[6], fmul(v, pb.z));
+      acc[7] = fadd(acc[7], fmul(v, pb.w));
+    }
+    for (; tt < len; ++tt) {
+      const int t = t0 + tt;
+      const float v = from_half(vr[tt * hs]);
+      const float* pp = p_s + (size_t)t * kRowPairs + 8 * hh;
+#pragma unroll
+      for (int rr = 0; rr < kRowBlock; ++rr)
+        if (t < n0 + rr) acc[rr] = fadd(acc[rr], fmul(v, pp[rr]));
+    }
+    if (j + 1 < chunks) FAH_STORE_CHUNK(j + 1);
+    __syncthreads();
+  }
+#undef FAH_LOAD_CHUNK
+#undef FAH_STORE_CHUNK
+
+  // 4. Output rows (float and/or Q8_0 blocks).
+#pragma unroll
+  for (int rr = 0; rr < kRowBlock; ++rr) {
+    q_s[(hh * kRowBlock + rr) * hs + c] = acc[rr];
+    if (a.out && rr < rows) a.out[((size_t)(r0 + rr) * a.heads + 2 * kh + hh) * hs + c] = acc[rr];
+  }
+  if (a.xq) {
+    __syncthreads();
+#pragma unroll
+    for (int g0 = 0; g0 < kRowPairs * hs / 4; g0 += 256) {
+      const int g = g0 + tid, pq = g >> 5, c4 = (g & 31) * 4, rr = pq & 7;
+      const float4 v4 = *reinterpret_cast<const float4*>(q_s + pq * hs + c4);
+      float d;
+      const int packed = quantize4(v4.x, v4.y, v4.z, v4.w, &d);
+      if (rr < rows) {
+        const size_t at = ((size_t)(r0 + rr) * a.heads + 2 * kh + (pq >> 3)) * hs + c4;
+        *reinterpret_cast<int*>(a.xq + at) = packed;
+        if ((g & 7) == 0) a.xs[at / 32] = d;
+      }
+    }
+  }
+}
+
 template <class Scale>
 hipError_t launch_gemm_scaled(const GemmArgs& g, int out, hipStream_t s) {
   const int B = g.K / 32;
@@ -631,6 +847,14 @@ hipError_t launch_attn_prefill(const PrefillAttnArgs& args, hipStream_t s) {
   static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_prefill_kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStageLds);
   if (raised != hipSuccess) return raised;
+  // Many rows of one cache (a prefill): blocks of rows share K/V reads.
+  if (!a.sessions && a.heads == 2 * a.kv_heads && a.frames >= 2 * kRowBlock && rows_lds_bytes(n) <= kStageLds) {
+    static const hipError_t raised_rows = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(attn_rows_kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStageLds);
+    if (raised_rows != hipSuccess) return raised_rows;
+    attn_rows_kernel<<<dim3(a.kv_heads, (a.frames + kRowBlock - 1) / kRowBlock), 256, rows_lds_bytes(n), s>>>(a);
+    return hipGetLastError();
+  }
   attn_prefill_kernel<<<dim3(a.heads, a.frames), 256, a.stage ? staged : (size_t)n * 4, s>>>(a);
   return hipGetLastError();
 }
