@@ -254,6 +254,84 @@ def cpu_baseline(weights, prefix, tokens: int, threads: int, seconds_target: flo
     return steps / seconds, used, seconds, passes
 
 
+def cpu_extra_baselines(weights, threads: int):
+    """The oracle on this host beside each extra measurement, on bounded
+    samples of the same workloads (each a few seconds)."""
+    import oracle
+
+    used = oracle.set_threads(threads)
+    cfg = weights.config
+    out = {}
+    # GEMV sweep: the same shapes and generator; the small matrices stay in
+    # the host caches across repetitions (no rotation on the CPU side).
+    rng = np.random.default_rng(3)
+    rows = []
+    for K, N in GEMV_SHAPES:
+        q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+        sc = (np.abs(rng.standard_normal((N, K // 32))) * 0.02 / 127).astype(np.float16).astype(np.float32)
+        xq, xs = oracle.quantize(rng.standard_normal(K).astype(np.float32))
+        algorithmic = N * K * 34 // 32 + K + 4 * (K // 32) + 4 * N
+        reps, t0 = 0, time.perf_counter()
+        while reps == 0 or time.perf_counter() - t0 < 0.3:
+            oracle.gemv_quantized(xq, xs, q, sc)
+            reps += 1
+        us = (time.perf_counter() - t0) * 1e6 / reps
+        rows.append({"shape": f"{K}->{N}", "avg_us": round(us, 1), "achieved_gbs": round(algorithmic / (us * 1e-6) / 1e9, 1)})
+    out["gemv_sweep"] = {"kind": "port", "cores": used, "shapes": rows,
+                         "sample": "oracle_q8_gemv_quantized, >=0.3 s of repetitions per shape"}
+    # Prefill: one decode of the same N(0,1) rows from position 0 (+ greedy).
+    pre = []
+    for n in (375, 750):
+        x = np.random.default_rng(n).standard_normal((n, cfg.width)).astype(np.float32)
+        dec = oracle.Decoder(weights, capacity=n + 8)
+        try:
+            t0 = time.perf_counter()
+            oracle.greedy(dec.decode(x, n))
+            pre.append({"rows": n, "ttft_ms": round((time.perf_counter() - t0) * 1e3, 1)})
+        finally:
+            dec.close()
+    out["prefill"] = {"kind": "port", "cores": used, "rows": pre, "sample": "one prefill per size"}
+    # Long cache: 4,096 fp16 N(0,1) positions in every layer, 4 greedy steps.
+    positions, steps = 4096, 4
+    dec = oracle.Decoder(weights, capacity=positions + steps + 64)
+    try:
+        r = np.random.default_rng(4)
+        width = cfg.kv_heads * cfg.head_size
+        for layer in range(cfg.layers):
+            k = r.standard_normal((positions, width)).astype(np.float16).astype(np.float32)
+            v = r.standard_normal((positions, width)).astype(np.float16).astype(np.float32)
+            dec.set_kv(layer, k, v)
+        dec.set_position(positions)
+        logits = dec.decode(r.standard_normal((1, cfg.width)).astype(np.float32), 1)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            logits = dec.decode(dec.embed([oracle.greedy(logits)]), 1)
+        sec = time.perf_counter() - t0
+    finally:
+        dec.close()
+    out["long_kv"] = {"kind": "port", "cores": used, "tok_s": round(steps / sec, 2),
+                      "sample": f"{steps} greedy steps after 4096 cached positions"}
+    # Sessions: the oracle decodes sessions one after another (no shared
+    # weight pass), 16 sessions x 4 lock-step steps from 8-row prefixes.
+    count, steps, short = 16, 4, 8
+    decs = [oracle.Decoder(weights, capacity=short + steps + 8) for _ in range(count)]
+    try:
+        logits = [d.decode(np.random.default_rng(i + 1).standard_normal((short, cfg.width)).astype(np.float32), short)
+                  for i, d in enumerate(decs)]
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            for i, d in enumerate(decs):
+                logits[i] = d.decode(d.embed([oracle.greedy(logits[i])]), 1)
+        sec = time.perf_counter() - t0
+    finally:
+        for d in decs:
+            d.close()
+    out["sessions"] = {"kind": "port", "cores": used, "tok_s": round(count * steps / sec, 2),
+                       "sample": f"{count} sessions x {steps} lock-step steps, {short}-row prefixes (the prefill "
+                                 "length changes the step's attention share only)"}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -325,6 +403,8 @@ def main() -> int:
         extra["prefill"] = prefill_ttft(backend, weights)
         extra["long_kv"] = long_kv(backend, weights)
         extra["sessions"] = sessions_decode(backend, weights)
+        if not args.no_cpu:
+            extra["cpu_baselines"] = cpu_extra_baselines(weights, min(16, os.cpu_count() or 1))
     backend.close()
 
     baseline = None

@@ -19,6 +19,8 @@ SOURCES = ["fah_kernels.hip", "fah_persistent.hip", "fah_prefill.hip", "fah_api.
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-fno-gpu-flush-denormals-to-zero", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # MFMA results in VGPRs: the fp32 epilogue reads them without accvgpr copies.
+         "-mllvm", "-amdgpu-mfma-vgpr-form",
          "-Wall", "-Wno-unused-function"]
 
 
