@@ -38,6 +38,10 @@ constexpr int kKvBytes = 121 * 1024;     // K/V staging: 512 B per position
 constexpr int kProbOffset = 4 * 128;     // attention probabilities after q/k/v in the tag area
 constexpr long kSpinLimit = 1L << 21;    // bounded polls per gather (~1-2 s)
 constexpr int kSentinelChunks = 0;       // gathers above this many 1 KB chunks poll a sentinel first
+constexpr int kPolls = 4;                // sentinel polls in flight
+// s_waitcnt immediate for vmcnt <= kPolls - 1 (expcnt and lgkmcnt not
+// waited on): vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
+constexpr int kWaitOldestPoll = ((kPolls - 1) & 15) | (((kPolls - 1) >> 4) << 14) | (7 << 4) | (15 << 8);
 using u64 = unsigned long long;
 using lds_ptr = __attribute__((address_space(3))) void*;
 
@@ -131,9 +135,16 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
     const u64* src;
     int off;
     locate(total - 1, src, off);
+    // kPolls sentinel loads in flight, all into the chunk's own LDS place:
+    // returns complete in order, so after waiting for the oldest the LDS copy
+    // is at least that new. Once the pipeline is full each iteration waits
+    // about a quarter round trip, so the data is seen at most that long
+    // after a poll could first have returned it.
+    for (int i = 0; i < kPolls - 1; ++i)
+      __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(tag + off), 16, 0, 16);
     for (;; ++spin) {
       __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(tag + off), 16, 0, 16);
-      __builtin_amdgcn_s_waitcnt(0);
+      __builtin_amdgcn_s_waitcnt(kWaitOldestPoll);
       const uint4 t = *reinterpret_cast<const uint4*>(tag + off + 2 * lane);
       if (__all(t.y == gen && t.w == gen)) break;
       if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
