@@ -514,7 +514,9 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       sub(0);
 
       // Scores, one position per lane: eight accumulators over channels
-      // j, j+8, ..., then the pairwise tree (AttentionAvx.cs:74-160).
+      // j, j+8, ..., then the pairwise tree (AttentionAvx.cs:74-160). Each
+      // lane keeps the maximum of its scores for the softmax shift.
+      float m = -__builtin_inff();
       for (int t = tid; t < n; t += kPT) {
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
         if (t < nlds || t == pos) {
@@ -538,41 +540,42 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
         const float s = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])),
                              fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
-        p_s[t] = fdiv(s, a.divisor);
+        const float sd = fdiv(s, a.divisor);
+        p_s[t] = sd;
+        m = nan_max_p(m, sd);
       }
-      lds_barrier_p();
-      sub(1);
       // Softmax (TensorMath.SoftmaxAvx.cs:11-58).
-      float m = -__builtin_inff();
-      for (int t = tid; t < n; t += kPT) m = nan_max_p(m, p_s[t]);
       m = wave_max_nan(m);
       if (lane == 0) tmax_s[wave] = m;
       lds_barrier_p();
+      sub(1);
       float mx = tmax_s[0];
 #pragma unroll
       for (int i = 1; i < kPT / kWave; ++i) mx = nan_max_p(mx, tmax_s[i]);
       for (int t = tid; t < n; t += kPT) p_s[t] = exp_ref(fadd(p_s[t], -mx));
       lds_barrier_p();
       const int full = n & ~7;
-      if (tid < 8) {
-        // Lane j: p[j] + p[j+8] + ... in order, in double.
+      if (wave == 0) {
+        // Lane j < 8: p[j] + p[j+8] + ... in order, in double; the eight
+        // sums' pairwise tree and the tail in order, read across the wave.
         double acc = 0.0;
-        int t = tid;
-        for (; t + 56 < full; t += 64) {
-          float v[8];
+        if (lane < 8) {
+          int t = lane;
+          for (; t + 56 < full; t += 64) {
+            float v[8];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) v[k] = p_s[t + 8 * k];
+            for (int k = 0; k < 8; ++k) v[k] = p_s[t + 8 * k];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) acc = acc + (double)v[k];
+            for (int k = 0; k < 8; ++k) acc = acc + (double)v[k];
+          }
+          for (; t < full; t += 8) acc = acc + (double)p_s[t];
         }
-        for (; t < full; t += 8) acc = acc + (double)p_s[t];
-        lane_s[tid] = acc;
-      }
-      lds_barrier_p();
-      if (tid == 0) {
-        double sum = ((lane_s[0] + lane_s[4]) + (lane_s[1] + lane_s[5])) + ((lane_s[2] + lane_s[6]) + (lane_s[3] + lane_s[7]));
+        double L[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) L[j] = readlane_double(acc, j);
+        double sum = ((L[0] + L[4]) + (L[1] + L[5])) + ((L[2] + L[6]) + (L[3] + L[7]));
         for (int t = full; t < n; ++t) sum = sum + (double)p_s[t];
-        inv_s = (float)(1.0 / sum);
+        if (lane == 0) inv_s = (float)(1.0 / sum);
       }
       lds_barrier_p();
       const float inverse = inv_s;
@@ -616,6 +619,49 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         auto prob = [&](int t) { return p_s[t]; };
         auto step = [&](int t) { acc = fadd(acc, fmul(from_half(*reinterpret_cast<const _Float16*>(vrow(t))), prob(t))); };
         int t = 0;
+        if (npre >= 32) {
+          // Staged rows: the next 16 positions' values and probabilities are
+          // read while the current 16 are added.
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          h2 va[8], vb[8];
+          float4 pa[4], pb[4];
+          auto fetch = [&](h2* v, float4* pq, int t0) {
+            const char* vr = vrow(t0);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              v[k].x = *reinterpret_cast<const _Float16*>(vr + 1024 * k);
+              v[k].y = *reinterpret_cast<const _Float16*>(vr + 1024 * k + 512);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) pq[k] = *reinterpret_cast<const float4*>(p_s + t0 + 4 * k);
+          };
+          auto add16 = [&](const h2* v, const float4* pq) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              acc = fadd(acc, fmul(from_half(v[2 * k].x), pq[k].x));
+              acc = fadd(acc, fmul(from_half(v[2 * k].y), pq[k].y));
+              acc = fadd(acc, fmul(from_half(v[2 * k + 1].x), pq[k].z));
+              acc = fadd(acc, fmul(from_half(v[2 * k + 1].y), pq[k].w));
+            }
+          };
+          fetch(va, pa, 0);
+          for (; t + 48 <= npre; t += 32) {
+            fetch(vb, pb, t + 16);
+            add16(va, pa);
+            fetch(va, pa, t + 32);
+            add16(vb, pb);
+          }
+          // va holds positions [t, t + 16); t + 16 <= npre here.
+          if (t + 32 <= npre) {
+            fetch(vb, pb, t + 16);
+            add16(va, pa);
+            add16(vb, pb);
+            t += 32;
+          } else {
+            add16(va, pa);
+            t += 16;
+          }
+        }
         for (; t + 16 <= npre; t += 16) chain16(vrow(t), t);
         for (; t < npre; ++t) step(t);
         for (; t < nlds && (t & 3) != 0; ++t) step(t);
