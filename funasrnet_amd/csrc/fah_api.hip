@@ -713,6 +713,10 @@ void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s)
   const fah::SessionRef* table = b.table.as<fah::SessionRef>();
   int8_t* xq = b.xq.as<int8_t>();
   float* xs = b.xs.as<float>();
+  auto norm_quantize = [&](const float* x, int K, const DeviceBuffer* norm) {
+    check(fah::launch_norm_quantize_rows(x, S, K, norm ? norm->as<float>() : nullptr, norm ? c.eps : 0.0f, xq, xs, s),
+          "session norm/quantise");
+  };
   auto gemm = [&](const DeviceMatrix& m, int rows, float* out, const float* resid, int mode) {
     fah::GemmArgs g{};
     g.w = m.q.as<int8_t>();
@@ -731,33 +735,21 @@ void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s)
     if (fah::few_frame_groups(rows, m.cols, S, mode)) check(fah::launch_gemm_few(g, w.half_scales, mode, s), "session gemm");
     else check(fah::launch_gemm(g, w.half_scales, mode == fah::kGemmGreedy ? fah::kGemmPlain : mode, s), "session gemm");
   };
-  auto norm_quantize = [&](const float* x, int K, const DeviceBuffer* norm) {
-    check(fah::launch_norm_quantize_rows(x, S, K, norm ? norm->as<float>() : nullptr, norm ? c.eps : 0.0f, xq, xs, s),
-          "session norm/quantise");
-  };
   check(fah::launch_session_embed(w.embed.q.as<int8_t>(), w.embed.s.ptr, w.half_scales, c.width, c.vocab, table, S,
                                   b.x.as<float>(), s),
         "session embed");
   for (int l = 0; l < c.layers; ++l) {
     norm_quantize(b.x.as<float>(), c.width, &w.attn_norm[l]);
     gemm(w.qkv[l], qkv_rows, b.qkv.as<float>(), nullptr, fah::kGemmPlain);
-    fah::QkArgs qa{};
-    qa.qkv = b.qkv.as<float>();
-    qa.q_norm = w.q_norm[l].as<float>();
-    qa.k_norm = w.k_norm[l].as<float>();
-    qa.q_out = b.q.as<float>();
-    qa.heads = c.heads;
-    qa.kv_heads = c.kv_heads;
-    qa.head_size = c.head_size;
-    qa.q_width = d->q_width;
-    qa.kv_width = d->kv_width;
-    qa.eps = c.eps;
-    qa.frames = S;
-    qa.sessions = table;
-    qa.layer = l;
-    check(fah::launch_qk_prepare(qa, s), "session qk prepare");
+    // Attention with the QK-norm, RoPE and K/V row write of each session's
+    // new position done in the same kernel.
     fah::PrefillAttnArgs pa{};
-    pa.q = b.q.as<float>();
+    pa.qkv = b.qkv.as<float>();
+    pa.q_norm = w.q_norm[l].as<float>();
+    pa.k_norm = w.k_norm[l].as<float>();
+    pa.eps = c.eps;
+    pa.q_width = d->q_width;
+    pa.kv_width = d->kv_width;
     pa.xq = xq;
     pa.xs = xs;
     pa.frames = S;

@@ -159,6 +159,15 @@ struct PrefillAttnArgs {
   // Set by launch_attn_prefill: V rows are staged in LDS when every row's
   // positions fit (bound on positions + 1; 0 = read V from global memory).
   int stage;
+  // Sessions only: when set, the kernel forms this row's q, k and v from the
+  // raw projections ([frames][q_width + 2*kv_width]) itself (QK-norm, RoPE
+  // from the session's tables, F16 rounding) and writes the K/V row, instead
+  // of a separate QK preparation (q is then unused).
+  const float* qkv;
+  const float* q_norm;
+  const float* k_norm;
+  float eps;
+  int q_width, kv_width;
 };
 
 hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t s);

@@ -228,13 +228,19 @@ __global__ __launch_bounds__(256) void norm_quantize_rows_kernel(const float* x,
 __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float attn_s[];  // probabilities [n]
   __shared__ __attribute__((aligned(16))) float q_s[128];
+  __shared__ __attribute__((aligned(16))) _Float16 kcur_s[128];  // fused QK: this position's K and V rows
+  __shared__ _Float16 vcur_s[128];
+  __shared__ float y_s[2][128];
+  __shared__ double red_s[4];
   __shared__ float tmax_s[4];
   __shared__ double lane_s[8];
   __shared__ float inv_s;
   const int head = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hs = 128, kh = head / (a.heads / a.kv_heads);
+  const int hs = 128, group = a.heads / a.kv_heads, kh = head / group;
+  const bool fused = a.qkv != nullptr;
   int pos, capacity;
   const _Float16 *kcache, *vcache;
+  const float *rope_cos = nullptr, *rope_sin = nullptr;
   if (a.sessions) {
     const SessionRef& ss = a.sessions[t];
     pos = min(*ss.position, a.max_positions - 1);
@@ -242,6 +248,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
     const size_t layer = (size_t)a.layer * a.kv_heads * capacity * hs;
     kcache = ss.kcache + layer;
     vcache = ss.vcache + layer;
+    rope_cos = ss.rope_cos;
+    rope_sin = ss.rope_sin;
   } else {
     pos = a.position + t;
     capacity = a.capacity;
@@ -249,32 +257,68 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
     vcache = a.vcache;
   }
   const int n = pos + 1;
-  const float* q = a.q + ((size_t)t * a.heads + head) * hs;
+  const int nv = fused ? pos : n;  // K/V rows read from the cache (fused: this position's are local)
   const _Float16* kc = kcache + (size_t)kh * capacity * hs;
   const _Float16* vc = vcache + (size_t)kh * capacity * hs;
   float* p_s = attn_s;
-  // V rows [0, n) into LDS (direct global->LDS loads, 1 KiB = 4 rows per
+  // V rows [0, nv) into LDS (direct global->LDS loads, 1 KiB = 4 rows per
   // instruction), in flight while the scores are computed.
   char* v_s = reinterpret_cast<char*>(attn_s) + ((4 * a.stage + 15) & ~15);
   if (a.stage) {
     const char* src = reinterpret_cast<const char*>(vc);
-    const int bytes = n * hs * 2;
+    const int bytes = nv * hs * 2;
     for (int c = wave * 1024; c < bytes; c += 4 * 1024)
       if (c + 16 * lane < bytes) __builtin_amdgcn_global_load_lds(src + c + 16 * lane, (lds_ptr)(v_s + c), 16, 0, 0);
   }
-  if (tid < hs) q_s[tid] = q[tid];
+  if (fused) {
+    // QK-norm and RoPE of this head's q (threads 0-127) and of its KV head's
+    // k (128-255), v rounded to F16: qk_prepare_kernel's arithmetic
+    // (QwenDecoder.cs:186-203, Rope.cs:14-55). The first query head of the
+    // pair writes the K/V row; both keep it locally for this position.
+    const int part = tid >> 7, c = tid & 127, half = hs >> 1;
+    const float* raw = a.qkv + (size_t)t * (a.q_width + 2 * a.kv_width);
+    const float v = raw[part == 0 ? head * hs + c : a.q_width + kh * hs + c];
+    const double sq = wave_sum_double((double)v * (double)v);
+    if (lane == 0) red_s[wave] = sq;
+    lds_barrier();
+    const float inverse = rms_inverse(red_s[2 * part] + red_s[2 * part + 1], hs, a.eps);
+    y_s[part][c] = fmul(fmul(v, inverse), (part == 0 ? a.q_norm : a.k_norm)[c]);
+    lds_barrier();
+    const float* cosine = rope_cos + (size_t)pos * half;
+    const float* sine = rope_sin + (size_t)pos * half;
+    float r;
+    if (c < half) r = fadd(fmul(y_s[part][c], cosine[c]), -fmul(y_s[part][c + half], sine[c]));
+    else r = fadd(fmul(y_s[part][c - half], sine[c - half]), fmul(y_s[part][c], cosine[c - half]));
+    if (part == 0) {
+      q_s[c] = r;
+      const _Float16 v16 = to_half(raw[a.q_width + a.kv_width + kh * hs + c]);
+      vcur_s[c] = v16;
+      if (head % group == 0) const_cast<_Float16*>(vc)[(size_t)pos * hs + c] = v16;
+    } else {
+      const _Float16 k16 = to_half(r);
+      kcur_s[c] = k16;
+      if (head % group == 0) const_cast<_Float16*>(kc)[(size_t)pos * hs + c] = k16;
+    }
+  } else if (tid < hs) {
+    q_s[tid] = a.q[((size_t)t * a.heads + head) * hs + tid];
+  }
   lds_barrier();
 
   for (int s = tid; s < n; s += 256) {
     float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)s * hs);
+    if (s < nv) {
+      const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)s * hs);
 #pragma unroll
-    for (int i0 = 0; i0 < 16; i0 += 4) {
-      uint4 kk[4];
+      for (int i0 = 0; i0 < 16; i0 += 4) {
+        uint4 kk[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kk[i] = row[i0 + i];
+        for (int i = 0; i < 4; ++i) kk[i] = row[i0 + i];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) score8(acc, kk[i], q_s + 8 * (i0 + i));
+        for (int i = 0; i < 4; ++i) score8(acc, kk[i], q_s + 8 * (i0 + i));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) score8(acc, reinterpret_cast<const uint4*>(kcur_s)[i], q_s + 8 * i);
     }
     const float sc = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
     p_s[s] = fdiv(sc, a.divisor);
@@ -317,28 +361,30 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
     const _Float16* v = reinterpret_cast<const _Float16*>(v_s) + tid;
     float acc = 0.0f;
     int s = 0;
-    for (; s + 16 <= n; s += 16) {
+    for (; s + 16 <= nv; s += 16) {
       float x[16];
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = from_half(v[(s + k) * hs]);
 #pragma unroll
       for (int k = 0; k < 16; ++k) acc = fadd(acc, fmul(x[k], p_s[s + k]));
     }
-    for (; s < n; ++s) acc = fadd(acc, fmul(from_half(v[s * hs]), p_s[s]));
+    for (; s < nv; ++s) acc = fadd(acc, fmul(from_half(v[s * hs]), p_s[s]));
+    if (fused) acc = fadd(acc, fmul(from_half(vcur_s[tid]), p_s[pos]));
     if (a.out) a.out[((size_t)t * a.heads + head) * hs + tid] = acc;
     q_s[tid] = acc;
   } else if (tid < hs) {
     const _Float16* v = vc + tid;
     float acc = 0.0f;
     int s = 0;
-    for (; s + 16 <= n; s += 16) {
+    for (; s + 16 <= nv; s += 16) {
       float x[16];
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = from_half(v[(size_t)(s + k) * hs]);
 #pragma unroll
       for (int k = 0; k < 16; ++k) acc = fadd(acc, fmul(x[k], p_s[s + k]));
     }
-    for (; s < n; ++s) acc = fadd(acc, fmul(from_half(v[(size_t)s * hs]), p_s[s]));
+    for (; s < nv; ++s) acc = fadd(acc, fmul(from_half(v[(size_t)s * hs]), p_s[s]));
+    if (fused) acc = fadd(acc, fmul(from_half(vcur_s[tid]), p_s[pos]));
     if (a.out) a.out[((size_t)t * a.heads + head) * hs + tid] = acc;
     q_s[tid] = acc;
   }
@@ -836,6 +882,8 @@ hipError_t launch_attn_prefill(const PrefillAttnArgs& args, hipStream_t s) {
   PrefillAttnArgs a = args;
   if (a.head_size != 128 || a.frames < 1 || a.heads % a.kv_heads != 0) return hipErrorInvalidValue;
   if (!a.out && !a.xq) return hipErrorInvalidValue;
+  if (a.qkv && (!a.sessions || !a.q_norm || !a.k_norm)) return hipErrorInvalidValue;
+  if (!a.qkv && !a.q) return hipErrorInvalidValue;
   const int n = a.sessions ? a.max_positions : a.position + a.frames;
   if ((!a.sessions && n > a.capacity) || n < 1 || (size_t)n * 4 > 60 * 1024) return hipErrorInvalidValue;
   // V rows are staged in LDS when that keeps three workgroups per CU, or,
