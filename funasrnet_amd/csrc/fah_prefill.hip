@@ -60,7 +60,7 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
   const int B = g.K >> 5;
   float* ws_s = gemm_s;           // [B][64] tile-row scales
   float* xs_s = gemm_s + 64 * B;  // [B][64] frame scales
-  float* up_s = gemm_s + 128 * B; // SwiGLU: [64 frames][32 rows] up sums
+  float* up_s = gemm_s + 128 * B; // SwiGLU: [64 frames][32 rows] up sums, rows padded to 33 floats
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int rw = wave & 1, fw = wave >> 1;
   const int row0 = blockIdx.x * (kSwiGLU ? 32 : 64);  // logical rows
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
     // SwiGLU (Elementwise.cs:167-196): gate waves meet their up rows in LDS.
     if (rw == 1) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) up_s[(32 * fw + ml) * 32 + 8 * (j >> 2) + 4 * half + (j & 3)] = acc[j];
+      for (int j = 0; j < 16; ++j) up_s[(32 * fw + ml) * 33 + 8 * (j >> 2) + 4 * half + (j & 3)] = acc[j];
     }
     lds_barrier();
     if (rw == 0 && frame < g.frames) {
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
         const int m = 8 * (j >> 2) + 4 * half + (j & 3);
         const int r = row0 + m;
         if (r < g.rows) {
-          const float gv = acc[j], u = up_s[(32 * fw + ml) * 32 + m];
+          const float gv = acc[j], u = up_s[(32 * fw + ml) * 33 + m];
           const float silu = fdiv(gv, fadd(1.0f, exp_ref(-gv)));
           g.out[(size_t)frame * g.out_stride + r] = fmul(silu, u);
         }
@@ -583,10 +583,11 @@ __global__ __launch_bounds__(256) void greedy_keys_kernel(const unsigned long lo
 // in double-buffered LDS chunks; output rows quantised to Q8_0 per 32-block.
 constexpr int kRowBlock = 8;
 constexpr int kRowPairs = 2 * kRowBlock;
+constexpr int kPRow = kRowPairs + 4;  // p_s row stride (floats): 16-byte rows, fewer bank conflicts per column
 constexpr int kVRows = 64;  // V rows per LDS chunk (256 B each)
 
 __host__ __device__ inline size_t rows_lds_bytes(int nmax) {
-  return (size_t)kRowPairs * nmax * 4 + (size_t)2 * kVRows * 256;
+  return (size_t)kPRow * nmax * 4 + (size_t)2 * kVRows * 256;
 }
 
 __device__ __forceinline__ float max16_nan(float m) {  // over each row of 16 lanes
@@ -607,8 +608,8 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
   const int rows = min(kRowBlock, a.frames - r0);
   const int n0 = a.position + r0 + 1;  // positions the block's first row sees; row rr sees n0 + rr
   const int nmax = n0 + rows - 1;
-  float* p_s = rows_s;  // [nmax][kRowPairs]
-  char* vbuf = reinterpret_cast<char*>(rows_s + (size_t)kRowPairs * nmax);
+  float* p_s = rows_s;  // [nmax][kPRow]
+  char* vbuf = reinterpret_cast<char*>(rows_s + (size_t)kPRow * nmax);
   const _Float16* kc = a.kcache + (size_t)kh * a.capacity * hs;
   const _Float16* vc = a.vcache + (size_t)kh * a.capacity * hs;
   for (int i = tid; i < kRowPairs * hs; i += 256) {
@@ -662,7 +663,7 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
                              fadd(fadd(acc[p][2], acc[p][6]), fadd(acc[p][3], acc[p][7])));
         sc[p] = fdiv(v, a.divisor);
       }
-      *reinterpret_cast<float4*>(p_s + (size_t)t * kRowPairs + 4 * part) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+      *reinterpret_cast<float4*>(p_s + (size_t)t * kPRow + 4 * part) = make_float4(sc[0], sc[1], sc[2], sc[3]);
     }
   }
   __syncthreads();
@@ -672,9 +673,9 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
   const int n = (pi & 7) < rows ? n0 + (pi & 7) : 0;
   {
     float m = -__builtin_inff();
-    for (int t = sub; t < n; t += 16) m = nan_max_p(m, p_s[t * kRowPairs + pi]);
+    for (int t = sub; t < n; t += 16) m = nan_max_p(m, p_s[t * kPRow + pi]);
     m = max16_nan(m);
-    for (int t = sub; t < n; t += 16) p_s[t * kRowPairs + pi] = exp_ref(fadd(p_s[t * kRowPairs + pi], -m));
+    for (int t = sub; t < n; t += 16) p_s[t * kPRow + pi] = exp_ref(fadd(p_s[t * kPRow + pi], -m));
   }
   __syncthreads();
   const int full = n & ~7;
@@ -685,24 +686,24 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
     for (; t + 56 < full; t += 64) {
       float v[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = p_s[(t + 8 * k) * kRowPairs + pi];
+      for (int k = 0; k < 8; ++k) v[k] = p_s[(t + 8 * k) * kPRow + pi];
 #pragma unroll
       for (int k = 0; k < 8; ++k) l = l + (double)v[k];
     }
-    for (; t < full; t += 8) l = l + (double)p_s[t * kRowPairs + pi];
+    for (; t < full; t += 8) l = l + (double)p_s[t * kPRow + pi];
     lane_s[pi * 8 + sub] = l;
   }
   __syncthreads();
   if (sub == 0 && n > 0) {
     const double* L = lane_s + pi * 8;
     double sum = ((L[0] + L[4]) + (L[1] + L[5])) + ((L[2] + L[6]) + (L[3] + L[7]));
-    for (int t = full; t < n; ++t) sum = sum + (double)p_s[t * kRowPairs + pi];
+    for (int t = full; t < n; ++t) sum = sum + (double)p_s[t * kPRow + pi];
     inv_s[pi] = (float)(1.0 / sum);
   }
   __syncthreads();
   {
     const float inverse = n > 0 ? inv_s[pi] : 0.0f;
-    for (int t = sub; t < n; t += 16) p_s[t * kRowPairs + pi] = fmul(p_s[t * kRowPairs + pi], inverse);
+    for (int t = sub; t < n; t += 16) p_s[t * kPRow + pi] = fmul(p_s[t * kPRow + pi], inverse);
   }
 
   // 3. Time-ordered value sums: lane = (head, channel), one sum per row of
@@ -741,7 +742,7 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
     int tt = 0;
     for (; tt < all; ++tt) {
       const float v = from_half(vr[tt * hs]);
-      const float* pp = p_s + (size_t)(t0 + tt) * kRowPairs + 8 * hh;
+      const float* pp = p_s + (size_t)(t0 + tt) * kPRow + 8 * hh;
       const float4 pa = *reinterpret_cast<const float4*>(pp), pb = *reinterpret_cast<const float4*>(pp + 4);
       acc[0] = fadd(acc[0], fmul(v, pa.x));
       acc[1] = fadd(acc[1], fmul(v, pa.y));
@@ -755,7 +756,7 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
     for (; tt < len; ++tt) {
       const int t = t0 + tt;
       const float v = from_half(vr[tt * hs]);
-      const float* pp = p_s + (size_t)t * kRowPairs + 8 * hh;
+      const float* pp = p_s + (size_t)t * kPRow + 8 * hh;
 #pragma unroll
       for (int rr = 0; rr < kRowBlock; ++rr)
         if (t < n0 + rr) acc[rr] = fadd(acc[rr], fmul(v, pp[rr]));
@@ -794,7 +795,7 @@ hipError_t launch_gemm_scaled(const GemmArgs& g, int out, hipStream_t s) {
   const int B = g.K / 32;
   const int rows_per_wg = out == kGemmSwiGLU ? 32 : 64;
   dim3 grid((g.rows + rows_per_wg - 1) / rows_per_wg, (g.frames + 63) / 64);
-  const size_t lds = (size_t)128 * B * 4 + (out == kGemmSwiGLU ? 64 * 32 * 4 : 0);
+  const size_t lds = (size_t)128 * B * 4 + (out == kGemmSwiGLU ? 64 * 33 * 4 : 0);
   switch (out) {
     case kGemmPlain: q8_gemm_kernel<Scale, kGemmPlain><<<grid, kGT, lds, s>>>(g); break;
     case kGemmResidual: q8_gemm_kernel<Scale, kGemmResidual><<<grid, kGT, lds, s>>>(g); break;
