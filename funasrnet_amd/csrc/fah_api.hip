@@ -237,31 +237,74 @@ void upload(DeviceBuffer& dst, const void* src, size_t bytes, hipStream_t s) {
 }
 
 // Upload rows in the given order (row_index[i] = source row of storage row i).
+// GGUF Q8_0 blocks on the host -> int8 plane + fp16 scale plane on the
+// device (the split runs on the device; `raw` may be freed on return).
+void upload_blocks(DeviceBuffer& q, DeviceBuffer& sc, const uint8_t* raw, size_t blocks, hipStream_t s) {
+  DeviceBuffer staging;
+  upload(staging, raw, blocks * 34, s);
+  q.allocate(blocks * 32);
+  sc.allocate(blocks * 2);
+  check(fah::launch_unpack_q8_blocks(staging.as<uint8_t>(), (int64_t)blocks, q.as<int8_t>(), sc.as<uint16_t>(), s),
+        "unpack Q8_0 blocks");
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+// Scale of block b of row r of a part, widened exactly to fp32.
+float part_scale(const fah_q8_host* p, size_t r, int b, int B) {
+  if (p->scales) return p->scales[r * B + b];
+  const uint8_t* blk = p->blocks + (r * B + b) * 34;
+  return half_bits_to_float((uint16_t)(blk[0] | (blk[1] << 8)));
+}
+
+// Upload rows in the given order (order[i] = (part, source row) of storage
+// row i). With fp16 scales every row goes through the GGUF block layout and
+// the device split (parts given as GGUF blocks are copied as they are);
+// otherwise the int8 and fp32 planes are assembled on the host.
 void upload_matrix(DeviceMatrix& m, const std::vector<const fah_q8_host*>& parts,
                    const std::vector<std::pair<int, int>>& order, int cols, bool half, hipStream_t s) {
-  int B = cols / 32;
-  size_t rows = order.size();
-  std::vector<int8_t> q(rows * cols);
-  std::vector<uint16_t> hs;
-  std::vector<float> fs;
-  if (half) hs.resize(rows * B); else fs.resize(rows * B);
-  for (size_t i = 0; i < rows; ++i) {
-    const fah_q8_host* p = parts[order[i].first];
-    int r = order[i].second;
-    std::memcpy(&q[i * cols], p->quantized + (size_t)r * cols, cols);
-    for (int b = 0; b < B; ++b) {
-      float v = p->scales[(size_t)r * B + b];
-      if (half) hs[i * B + b] = float_to_half_bits(v); else fs[i * B + b] = v;
+  const int B = cols / 32;
+  const size_t rows = order.size(), row_bytes = (size_t)B * 34;
+  if (half) {
+    std::vector<uint8_t> raw(rows * row_bytes);
+    for (size_t i = 0; i < rows; ++i) {
+      const fah_q8_host* p = parts[order[i].first];
+      const size_t r = (size_t)order[i].second;
+      uint8_t* dst = &raw[i * row_bytes];
+      if (!p->quantized) {
+        std::memcpy(dst, p->blocks + r * row_bytes, row_bytes);
+        continue;
+      }
+      for (int b = 0; b < B; ++b) {
+        const uint16_t h = float_to_half_bits(p->scales[r * B + b]);
+        dst[34 * b] = (uint8_t)(h & 0xff);
+        dst[34 * b + 1] = (uint8_t)(h >> 8);
+        std::memcpy(dst + 34 * b + 2, p->quantized + r * cols + 32 * b, 32);
+      }
     }
+    upload_blocks(m.q, m.s, raw.data(), rows * B, s);
+  } else {
+    std::vector<int8_t> q(rows * cols);
+    std::vector<float> fs(rows * B);
+    for (size_t i = 0; i < rows; ++i) {
+      const fah_q8_host* p = parts[order[i].first];
+      const size_t r = (size_t)order[i].second;
+      for (int b = 0; b < B; ++b) {
+        fs[i * B + b] = part_scale(p, r, b, B);
+        const int8_t* src = p->quantized ? p->quantized + r * cols + 32 * b
+                                         : reinterpret_cast<const int8_t*>(p->blocks + (r * B + b) * 34 + 2);
+        std::memcpy(&q[i * cols + 32 * b], src, 32);
+      }
+    }
+    upload(m.q, q.data(), q.size(), s);
+    upload(m.s, fs.data(), fs.size() * 4, s);
   }
-  upload(m.q, q.data(), q.size(), s);
-  if (half) upload(m.s, hs.data(), hs.size() * 2, s); else upload(m.s, fs.data(), fs.size() * 4, s);
   m.rows = (int)rows;
   m.cols = cols;
 }
 
 void validate_q8(const fah_q8_host* w, int rows, int cols, const char* name) {
-  require(w && w->quantized && w->scales, std::string(name) + ": missing Q8 weight");
+  require(w && ((w->quantized && w->scales) || (!w->quantized && !w->scales && w->blocks)),
+          std::string(name) + ": missing Q8 weight (int8 + scales, or GGUF blocks)");
   require(w->rows == rows && w->cols == cols,
           std::string(name) + ": shape " + std::to_string(w->rows) + "x" + std::to_string(w->cols) + " != " +
               std::to_string(rows) + "x" + std::to_string(cols));
@@ -879,6 +922,25 @@ int fah_weight_q8_upload(fah_context* c, const int8_t* quantized, const float* s
   });
 }
 
+int fah_weight_q8_upload_blocks(fah_context* c, const uint8_t* blocks, int rows, int cols, fah_weight** out) {
+  if (!c || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+  return guarded([&] {
+    require(blocks != nullptr, "Q8 weight needs its GGUF blocks");
+    require(rows > 0 && cols > 0 && cols % 32 == 0, "Invalid row-major Q8 dimensions");
+    std::lock_guard<std::mutex> lock(c->gate);
+    check(hipSetDevice(c->device), "hipSetDevice");
+    auto w = std::make_unique<fah_weight>();
+    w->context = c;
+    w->rows = rows;
+    w->cols = cols;
+    w->half_scales = true;
+    upload_blocks(w->q, w->s, blocks, (size_t)rows * (cols / 32), c->stream);
+    w->group_rows = pick_group_rows(rows, cols, 4, false);
+    *out = w.release();
+    return FAH_OK;
+  });
+}
+
 int fah_weight_release(fah_weight* w) {
   if (!w) return FAH_OK;
   (void)hipSetDevice(w->context->device);
@@ -1110,7 +1172,9 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
     hipStream_t s = c->stream;
 
     bool half = true;
-    auto fits = [&](const fah_q8_host& w) { return scales_fit_half(w.scales, (size_t)w.rows * (w.cols / 32)); };
+    auto fits = [&](const fah_q8_host& w) {
+      return !w.scales || scales_fit_half(w.scales, (size_t)w.rows * (w.cols / 32));  // GGUF blocks: fp16
+    };
     for (int l = 0; l < k.layers && half; ++l) {
       const fah_layer_host& L = layers[l];
       half = fits(L.wq) && fits(L.wk) && fits(L.wv) && fits(L.wo) && fits(L.gate) && fits(L.up) && fits(L.down);

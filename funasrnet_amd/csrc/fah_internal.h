@@ -198,6 +198,8 @@ int gemv_pairs_per_thread(int group_rows, int K);
 hipError_t launch_gemv(const GemvArgs& a, bool half_scales, int in, int out, int frames, hipStream_t s);
 hipError_t launch_greedy_reduce(const unsigned long long* keys, int count, const float* logits, int* token,
                                 hipStream_t s);
+// GGUF Q8_0 blocks (34 B: fp16 scale, 32 int8) -> int8 plane + fp16 scale bits.
+hipError_t launch_unpack_q8_blocks(const uint8_t* raw, int64_t blocks, int8_t* q, uint16_t* s, hipStream_t st);
 hipError_t launch_embed(const int8_t* q, const void* scales, bool half_scales, int K, int vocab, const int* token,
                         float* x, int* history, int* history_count, hipStream_t s);
 hipError_t launch_qk_prepare(const QkArgs& a, hipStream_t s);

@@ -529,6 +529,19 @@ __global__ __launch_bounds__(kThreads) void session_embed_kernel(const int8_t* q
   }
 }
 
+// One GGUF Q8_0 block per thread (TensorMath.Q8Model.cs:15-39 without the
+// fp32 widening: the device keeps the fp16 scale bits): 17 aligned 16-bit
+// reads (blocks start at even offsets), 8 words of codes and the scale out.
+__global__ __launch_bounds__(kThreads) void unpack_q8_blocks_kernel(const uint16_t* raw, int64_t blocks, uint32_t* q,
+                                                                    uint16_t* s) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= blocks) return;
+  const uint16_t* src = raw + b * 17;
+  s[b] = src[0];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[b * 8 + i] = (uint32_t)src[1 + 2 * i] | ((uint32_t)src[2 + 2 * i] << 16);
+}
+
 __global__ void advance_kernel(int* position, int frames) {
   if (threadIdx.x == 0) *position += frames;
 }
@@ -643,6 +656,16 @@ hipError_t launch_session_embed(const int8_t* q, const void* scales, bool half_s
     session_embed_kernel<ScaleHalf><<<count, kThreads, 0, s>>>(q, scales, K, vocab, sessions, x);
   else
     session_embed_kernel<ScaleFloat><<<count, kThreads, 0, s>>>(q, scales, K, vocab, sessions, x);
+  return hipGetLastError();
+}
+
+hipError_t launch_unpack_q8_blocks(const uint8_t* raw, int64_t blocks, int8_t* q, uint16_t* s, hipStream_t st) {
+  if (blocks < 0 || (reinterpret_cast<uintptr_t>(raw) & 1) || (reinterpret_cast<uintptr_t>(q) & 3))
+    return hipErrorInvalidValue;
+  if (blocks == 0) return hipSuccess;
+  const int64_t grid = (blocks + kThreads - 1) / kThreads;
+  unpack_q8_blocks_kernel<<<(unsigned)grid, kThreads, 0, st>>>(reinterpret_cast<const uint16_t*>(raw), blocks,
+                                                               reinterpret_cast<uint32_t*>(q), s);
   return hipGetLastError();
 }
 

@@ -65,6 +65,7 @@ class Weight:
     quantized: np.ndarray | None = None   # int8 [rows * columns]
     scales: np.ndarray | None = None      # float32 [rows * columns / 32]
     scale_bits: np.ndarray | None = None  # raw fp16 bits, kept for re-writing
+    blocks: np.ndarray | None = None      # raw Q8_0 blocks (34 B each), when read with raw_q8
 
     @property
     def columns(self) -> int:
@@ -136,7 +137,10 @@ class Gguf:
         return self.tensors[key]
 
     @classmethod
-    def read(cls, path: str) -> "Gguf":
+    def read(cls, path: str, raw_q8: bool = False) -> "Gguf":
+        """Read a GGUF file. With ``raw_q8`` the Q8_0 tensors keep their
+        34-byte blocks as they are in the file (``Weight.blocks``) instead
+        of being unpacked, for uploads that split them on the device."""
         with open(path, "rb") as f:
             data = memoryview(f.read())
         r = _Reader(data)
@@ -176,7 +180,10 @@ class Gguf:
                 if shape[0] % 32 != 0:
                     raise ValueError("Q8_0 row not aligned")
                 blocks = count // 32
-                w.quantized, w.scales, w.scale_bits = unpack_q8_0(_slice(data, at, blocks * _BLOCK), blocks)
+                if raw_q8:
+                    w.blocks = _slice(data, at, blocks * _BLOCK).copy()
+                else:
+                    w.quantized, w.scales, w.scale_bits = unpack_q8_0(_slice(data, at, blocks * _BLOCK), blocks)
             else:
                 raise ValueError(f"Tensor {name}: GGML type {kind}")
             if name in model.tensors:

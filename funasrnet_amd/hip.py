@@ -37,7 +37,8 @@ _u16p = ctypes.POINTER(ctypes.c_uint16)
 
 
 class Q8Host(ctypes.Structure):
-    _fields_ = [("quantized", _i8p), ("scales", _f32p), ("rows", ctypes.c_int), ("cols", ctypes.c_int)]
+    _fields_ = [("quantized", _i8p), ("scales", _f32p), ("rows", ctypes.c_int), ("cols", ctypes.c_int),
+                ("blocks", ctypes.POINTER(ctypes.c_uint8))]
 
 
 class LayerHost(ctypes.Structure):
@@ -62,6 +63,8 @@ SIGNATURES = {
     "fah_context_set_minimum_operations": (ctypes.c_int, [_vp, ctypes.c_int64]),
     "fah_context_stream": (_vp, [_vp]),
     "fah_weight_q8_upload": (ctypes.c_int, [_vp, _i8p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
+    "fah_weight_q8_upload_blocks": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint8), ctypes.c_int, ctypes.c_int,
+                                                   ctypes.POINTER(_vp)]),
     "fah_weight_release": (ctypes.c_int, [_vp]),
     "fah_weight_device_bytes": (ctypes.c_int64, [_vp]),
     "fah_quantized_linear": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, _vp, _f32p, _f32p]),
@@ -136,13 +139,18 @@ class HipWeight:
     """Device copy of a Q8_0 matrix (Weight.Quantized / Weight.Scales)."""
 
     def __init__(self, backend: "HipBackend", tensor: Q8Tensor):
-        q = np.ascontiguousarray(tensor.quantized, dtype=np.int8)
-        s = np.ascontiguousarray(tensor.scales, dtype=np.float32)
-        self.rows, self.columns = q.shape
+        self.rows, self.columns = tensor.rows, tensor.columns
         self._backend = backend
         h = _vp()
-        _check(load().fah_weight_q8_upload(backend.handle, _p(q, ctypes.c_int8), _p(s, ctypes.c_float), self.rows,
-                                           self.columns, ctypes.byref(h)))
+        if tensor.quantized is None:
+            raw = np.ascontiguousarray(tensor.blocks, dtype=np.uint8)
+            _check(load().fah_weight_q8_upload_blocks(backend.handle, _p(raw, ctypes.c_uint8), self.rows,
+                                                      self.columns, ctypes.byref(h)))
+        else:
+            q = np.ascontiguousarray(tensor.quantized, dtype=np.int8)
+            s = np.ascontiguousarray(tensor.scales, dtype=np.float32)
+            _check(load().fah_weight_q8_upload(backend.handle, _p(q, ctypes.c_int8), _p(s, ctypes.c_float), self.rows,
+                                               self.columns, ctypes.byref(h)))
         self.handle = h
 
     @property
@@ -258,10 +266,14 @@ class HipDecoder:
         keep = []
 
         def q8(t: Q8Tensor) -> Q8Host:
+            if t.quantized is None:  # GGUF blocks, split on the device
+                raw = np.ascontiguousarray(t.blocks, dtype=np.uint8)
+                keep.append(raw)
+                return Q8Host(None, None, t.rows, t.columns, _p(raw, ctypes.c_uint8))
             q = np.ascontiguousarray(t.quantized, dtype=np.int8)
             s = np.ascontiguousarray(t.scales, dtype=np.float32)
             keep.extend([q, s])
-            return Q8Host(_p(q, ctypes.c_int8), _p(s, ctypes.c_float), t.rows, t.columns)
+            return Q8Host(_p(q, ctypes.c_int8), _p(s, ctypes.c_float), t.rows, t.columns, None)
 
         def f32(a):
             a = np.ascontiguousarray(a, dtype=np.float32)

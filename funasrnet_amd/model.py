@@ -48,20 +48,24 @@ QWEN3_0_6B = DecoderConfig()
 @dataclass
 class Q8Tensor:
     """A Q8_0 matrix as the reference holds it after load: int8 [rows, cols]
-    row-major and one float32 scale per 32 values [rows, cols/32]."""
+    row-major and one float32 scale per 32 values [rows, cols/32]. A tensor
+    read raw from a GGUF file has ``blocks`` (rows*cols/32 x 34 bytes) and
+    ``dims`` instead of the unpacked planes."""
 
     name: str
-    quantized: np.ndarray
-    scales: np.ndarray
+    quantized: np.ndarray | None
+    scales: np.ndarray | None
     scale_bits: np.ndarray | None = None
+    blocks: np.ndarray | None = None
+    dims: tuple | None = None  # (rows, cols) when only blocks are held
 
     @property
     def rows(self) -> int:
-        return int(self.quantized.shape[0])
+        return int(self.quantized.shape[0]) if self.quantized is not None else int(self.dims[0])
 
     @property
     def columns(self) -> int:
-        return int(self.quantized.shape[1])
+        return int(self.quantized.shape[1]) if self.quantized is not None else int(self.dims[1])
 
 
 @dataclass
@@ -186,6 +190,8 @@ def from_gguf(model: gguf.Gguf) -> DecoderWeights:
 
     def q8(name) -> Q8Tensor:
         w = model[name]
+        if w.blocks is not None:
+            return Q8Tensor(name, None, None, blocks=w.blocks, dims=(w.rows, w.columns))
         if w.quantized is None:
             raise ValueError(f"{name}: decoder projections must be Q8_0")
         return Q8Tensor(name, w.quantized.reshape(w.rows, w.columns), w.scales.reshape(w.rows, w.columns // 32),

@@ -80,6 +80,14 @@ void* fah_context_stream(fah_context* context);
  * GGUF Q8_0), otherwise as fp32. cols must be a multiple of 32. */
 int fah_weight_q8_upload(fah_context* context, const int8_t* quantized, const float* scales,
                          int rows, int cols, fah_weight** out);
+/* Upload a Q8_0 matrix straight from its GGUF blocks: `blocks` holds
+ * rows*cols/32 blocks of 34 bytes (little-endian fp16 scale, then 32 int8),
+ * row-major, as the tensor data of a GGUF file. Replaces reading the tensor
+ * and unpacking it on the host (src/FunAsrNet/Gguf.cs:132-173,
+ * src/FunAsrNet/TensorMath.Q8Model.cs:15-39) before the upload: the blocks
+ * are split into the int8 plane and the fp16 scale plane on the device, so
+ * no sbyte[]/float[] copy of the matrix exists on the host. */
+int fah_weight_q8_upload_blocks(fah_context* context, const uint8_t* blocks, int rows, int cols, fah_weight** out);
 int fah_weight_release(fah_weight* weight);
 /* Device bytes held by the weight (int8 plane plus scale plane). */
 int64_t fah_weight_device_bytes(const fah_weight* weight);
@@ -137,6 +145,9 @@ typedef struct fah_q8_host {
     const int8_t* quantized; /* [rows*cols] */
     const float* scales;     /* [rows*cols/32] */
     int rows, cols;
+    /* Alternatively (quantized and scales NULL): the GGUF Q8_0 blocks,
+     * rows*cols/32 x 34 bytes, as fah_weight_q8_upload_blocks takes them. */
+    const uint8_t* blocks;
 } fah_q8_host;
 
 typedef struct fah_layer_host {

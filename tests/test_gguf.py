@@ -125,3 +125,20 @@ def test_synthetic_model_round_trip(tmp_path):
     s = np.repeat(emb.scales[7 * cfg.width // 32:8 * cfg.width // 32].astype(np.float64), 32)
     assert np.array_equal(row, (q * s).astype(np.float32))
     assert back.int("qwen3.block_count", 0) == 1
+
+
+def test_raw_q8_read_keeps_the_file_blocks(tmp_path):
+    """Gguf.read(raw_q8=True) returns each Q8_0 tensor's blocks byte for byte
+    (for the device-side split); unpacking them gives the default read."""
+    cfg = model.small_config(layers=1, vocab=128)
+    w = model.synthetic(cfg, seed=4)
+    path = tmp_path / "raw.gguf"
+    model.to_gguf(w, str(path))
+    raw = gguf.Gguf.read(str(path), raw_q8=True)
+    full = gguf.Gguf.read(str(path))
+    t, u = raw["blk.0.ffn_down.weight"], full["blk.0.ffn_down.weight"]
+    assert t.quantized is None and t.blocks.dtype == np.uint8 and t.blocks.size == t.rows * t.columns // 32 * 34
+    q, s, bits = gguf.unpack_q8_0(t.blocks, t.blocks.size // 34)
+    assert np.array_equal(q, u.quantized) and np.array_equal(s.view(np.uint32), u.scales.view(np.uint32))
+    weights = model.from_gguf(raw)
+    assert weights.layers[0].down.rows == cfg.width and weights.layers[0].down.columns == cfg.ffn

@@ -143,3 +143,28 @@ def test_qwen3_0_6b_decode_tokens_match(backend, oracle_lib):
     finally:
         gpu.close()
         ref.close()
+
+
+def test_decoder_from_gguf_blocks(backend, tmp_path):
+    """A decoder built from the GGUF file's raw Q8_0 blocks (split on the
+    device) decodes exactly like one built from the unpacked planes."""
+    from funasrnet_amd import gguf
+    from funasrnet_amd.hip import HipDecoder
+    cfg = model.small_config(layers=2)
+    w = model.synthetic(cfg, seed=17)
+    path = str(tmp_path / "small.gguf")
+    model.to_gguf(w, path)
+    raw = model.from_gguf(gguf.Gguf.read(path, raw_q8=True))
+    unpacked = model.from_gguf(gguf.Gguf.read(path))
+    assert raw.layers[0].wq.quantized is None and raw.layers[0].wq.blocks is not None
+    prefix = np.random.default_rng(18).standard_normal((9, cfg.width)).astype(np.float32)
+    a = HipDecoder(backend, raw, capacity=64)
+    b = HipDecoder(backend, unpacked, capacity=64)
+    try:
+        assert a.weight_bytes == b.weight_bytes
+        la, lb = a.decode(prefix, 9), b.decode(prefix, 9)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        assert a.generate(6).tolist() == b.generate(6).tolist()
+    finally:
+        a.close()
+        b.close()

@@ -147,3 +147,34 @@ def test_declines_small_and_leaves_output_untouched():
             b.try_quantized_linear(np.ones(31, dtype=np.float32), 1, w, None, out)
     finally:
         b.close()
+
+
+@pytest.mark.parametrize("cols,rows", [(1024, 2048), (3072, 1024)])
+def test_gguf_block_upload_equals_unpacked_upload(backend, dev, oracle_lib, cols, rows):
+    """fah_weight_q8_upload_blocks: the GGUF blocks split on the device give
+    the same weight as the host-unpacked planes (identical GEMV bits), with
+    every fp16 scale pattern class present (normal, subnormal, zero, -0)."""
+    from funasrnet_amd import gguf
+    from funasrnet_amd.model import Q8Tensor
+    rng = np.random.default_rng(rows + cols)
+    w = _weights(rng, rows, cols)
+    bits = w.scales.astype(np.float16).view(np.uint16).reshape(-1).copy()
+    bits[:4] = [0x0001, 0x0000, 0x8000, 0x03FF]  # subnormals, +0, -0
+    raw = np.frombuffer(gguf.pack_q8_0(w.quantized, bits), dtype=np.uint8)
+    q, s, _ = gguf.unpack_q8_0(raw, rows * cols // 32)
+    arrays = Q8Tensor("w", q.reshape(rows, cols), s.reshape(rows, -1))
+    blocks = Q8Tensor("w", None, None, blocks=raw, dims=(rows, cols))
+    ha, hb = backend.weight(arrays), backend.weight(blocks)
+    assert ha.device_bytes == hb.device_bytes
+    x = rng.standard_normal(cols).astype(np.float32)
+    xq, xs = oracle_lib.quantize(x)
+    dq, ds = dev.DeviceArray.from_numpy(xq), dev.DeviceArray.from_numpy(xs)
+    oa, ob = dev.DeviceArray(rows, np.float32), dev.DeviceArray(rows, np.float32)
+    backend.gemv_device(dq.ptr, ds.ptr, 1, ha, oa.ptr)
+    backend.gemv_device(dq.ptr, ds.ptr, 1, hb, ob.ptr)
+    backend.synchronize()
+    assert np.array_equal(oa.numpy().view(np.uint32), ob.numpy().view(np.uint32))
+    expected = oracle_lib.gemv_quantized(xq, xs, arrays.quantized, arrays.scales)[0]
+    assert np.array_equal(ob.numpy().view(np.uint32), expected.view(np.uint32))
+    ha.close()
+    hb.close()
