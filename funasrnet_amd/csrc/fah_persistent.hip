@@ -28,8 +28,9 @@
 namespace fah {
 namespace {
 
-constexpr int kPT = 256;                 // threads per workgroup (4 waves: 512 VGPRs each)
-constexpr int kComp = kPT - kWave;       // compute threads (waves 1..3)
+constexpr int kPT = 512;                 // threads per workgroup (8 waves, two per SIMD)
+constexpr int kMem = 256;                // memory threads (waves 0-3): gathers, row sums
+constexpr int kComp = kPT - kMem;        // compute threads (waves 4-7): weight slices
 constexpr int kSlotPairs = 4;            // (row, block) pairs per compute lane per phase
 constexpr int kActFloats = 4096;         // largest phase input (ffn <= 4096)
 constexpr int kTagWords = kActFloats * 3 / 4;  // gathered words held in LDS
@@ -100,20 +101,24 @@ struct NoPre {
   __device__ void operator()() const {}
 };
 
-// Wave 0 gathers tagged words into the LDS staging area `tag` (one u64 per
-// value; consumers read the low 32 bits). Ranges are multiples of 128 words
-// (chunks); each chunk is one direct global->LDS load of 16 bytes per lane.
-// `pre` issues the plain constant copies once, before the first poll, so
-// they share its wait. Chunks whose tags do not all carry `gen` are issued
-// again until every chunk is current. Returns false after a timeout or when
-// another workgroup reported an error.
+// One wave gathers tagged words into the LDS staging area `tag` (one u64
+// per value; consumers read the low 32 bits). Ranges are multiples of 128
+// words (chunks); each chunk is one direct global->LDS load of 16 bytes per
+// lane. The chunks are split into `parts` contiguous parts and this wave
+// takes part `part`, so that several waves can share a vector (a wave issues
+// its loads one after another). `pre` issues the plain constant copies
+// once, before the first poll, so they share its wait. Chunks whose tags do
+// not all carry `gen` are issued again until every chunk is current.
+// Returns false after a timeout or when another workgroup reported an error.
 template <class Pre>
 __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int o1, const u64* s2, int n2, int o2,
-                       uint32_t gen, u64* tag, unsigned* error, Pre pre) {
-  const int lane = threadIdx.x;
+                       uint32_t gen, u64* tag, unsigned* error, Pre pre, int part = 0, int parts = 1) {
+  const int lane = threadIdx.x & (kWave - 1);
   pre();
-  const int c0 = n0 >> 7, c01 = c0 + (n1 >> 7), total = c01 + (n2 >> 7);
-  u64 pending = total >= 64 ? ~0ull : ((1ull << total) - 1ull);
+  const int c0 = n0 >> 7, c01 = c0 + (n1 >> 7), all = c01 + (n2 >> 7);
+  const int first = part * all / parts, total = (part + 1) * all / parts;
+  if (total <= first) return true;
+  u64 pending = (total >= 64 ? ~0ull : ((1ull << total) - 1ull)) & ~((1ull << first) - 1ull);
   auto locate = [&](int k, const u64*& src, int& off) {
     if (k < c0) {
       src = s0 + (k << 7);
@@ -190,6 +195,146 @@ __device__ __forceinline__ bool gather1(const u64* src, int count, uint32_t gen,
 }
 
 __device__ __forceinline__ float tag_value(const u64* tag, int i) { return u2f((uint32_t)tag[i]); }
+
+// round(q * k) for an F16 k, as one mixed-precision fma with a +0 addend:
+// equal to fmul(q, (float)k) except that a -0 product comes out +0. Callers
+// only add it to sums that are never -0, so the sums are unchanged.
+__device__ __forceinline__ float mulh(float q, _Float16 k) { return __builtin_fmaf(q, (float)k, 0.0f); }
+
+// Time-ordered value sum of channel c = 2 * lane + HI over positions
+// [0, pos]: acc = acc + p[t] * v[t][c] from 0f in order (the reference's
+// value loop), V rows of earlier positions staged in LDS at 512 B per
+// position ([0, npre) in kv, [npre, nlds) in ovf; V at byte 256 of a
+// row), later ones read from vglob (this layer and head), this position's
+// value in cur[2]. The dword at byte 4 * lane of a V row holds channels
+// 2 * lane (low half) and 2 * lane + 1 (high half). Blocks of 16
+// positions: 8 paired reads and 4 probability reads, the next block's
+// issued before the current block is added. Writes cur[0][c].
+template <bool HI>
+__device__ __forceinline__ void value_chain(const char* kv, const char* ovf, const float* p, int npre, int nlds,
+                                            int pos, const _Float16* vglob, float (*cur)[128]) {
+  const int lane = threadIdx.x & (kWave - 1), c = 2 * lane + (HI ? 1 : 0);
+  auto half = [](uint32_t d) { return __builtin_bit_cast(_Float16, (uint16_t)(HI ? d >> 16 : d)); };
+  float acc = 0.0f;
+  // Drain earlier scalar loads: with none pending, the waits inside the
+  // block loop can count LDS reads instead of draining them all.
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  auto region = [&](const char* base, int t0, int count) {
+    const char* vr = base + 256 + 4 * lane;
+    // The probabilities through a per-lane pointer, so that their block loads
+    // take immediate offsets from one VGPR and issue with the value loads.
+    using lds_float = __attribute__((address_space(3))) const float;
+    lds_float* pl = (lds_float*)(p + t0);
+    asm volatile("" : "+v"(pl));
+    auto one = [&](int i) { acc = fadd(acc, mulh(p[t0 + i], half(*reinterpret_cast<const uint32_t*>(vr + (size_t)i * 512)))); };
+    int i = 0;
+    for (; i < count && ((t0 + i) & 3) != 0; ++i) one(i);
+    auto fetch = [&](uint32_t* v, float4* pq, int i0) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = *reinterpret_cast<const uint32_t*>(vr + (size_t)(i0 + k) * 512);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        using lds_f4 = __attribute__((address_space(3))) const f4;
+        const f4 v = *reinterpret_cast<lds_f4*>(pl + i0 + 4 * k);
+        pq[k] = make_float4(v.x, v.y, v.z, v.w);
+      }
+    };
+    auto add16 = [&](const uint32_t* v, const float4* pq) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc = fadd(acc, mulh(pq[k].x, half(v[4 * k])));
+        acc = fadd(acc, mulh(pq[k].y, half(v[4 * k + 1])));
+        acc = fadd(acc, mulh(pq[k].z, half(v[4 * k + 2])));
+        acc = fadd(acc, mulh(pq[k].w, half(v[4 * k + 3])));
+      }
+    };
+    if (i + 16 <= count) {
+      uint32_t va[16], vb[16];
+      float4 pa[4], pb[4];
+      // sched_barrier keeps each block's loads ahead of the previous block's
+      // adds (the scheduler would otherwise sink them next to their use).
+      fetch(va, pa, i);
+      for (; i + 48 <= count; i += 32) {
+        fetch(vb, pb, i + 16);
+        __builtin_amdgcn_sched_barrier(0);
+        add16(va, pa);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(va, pa, i + 32);
+        __builtin_amdgcn_sched_barrier(0);
+        add16(vb, pb);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // va holds [i, i + 16); i + 16 <= count here.
+      if (i + 32 <= count) {
+        fetch(vb, pb, i + 16);
+        __builtin_amdgcn_sched_barrier(0);
+        add16(va, pa);
+        add16(vb, pb);
+        i += 32;
+      } else {
+        add16(va, pa);
+        i += 16;
+      }
+    }
+    for (; i < count; ++i) one(i);
+  };
+  region(kv, 0, npre);
+  region(ovf, npre, nlds - npre);
+  int t = nlds;
+  const _Float16* vg = vglob + c;
+  for (; t + 8 <= pos; t += 8) {
+    _Float16 x[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = vg[(size_t)(t + k) * 128];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc = fadd(acc, mulh(p[t + k], x[k]));
+  }
+  for (; t < pos; ++t) acc = fadd(acc, mulh(p[t], vg[(size_t)t * 128]));
+  acc = fadd(acc, fmul(cur[2][c], p[pos]));
+  cur[0][c] = acc;
+}
+
+// score8_mix with q in registers (q[0..7] = channels 8i..8i+7).
+__device__ __forceinline__ void score8_regs(float* acc, const uint4& kk, const float* q) {
+  const uint32_t w[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu));
+    const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16));
+    acc[2 * m] = fadd(acc[2 * m], mulh(q[2 * m], lo));
+    acc[2 * m + 1] = fadd(acc[2 * m + 1], mulh(q[2 * m + 1], hi));
+  }
+}
+
+// Half a K row piece: four F16 channels 8i + 4h .. 8i + 4h + 3 into the
+// four accumulators of lane parity h (q[0..3] the matching q channels).
+__device__ __forceinline__ void score4_regs(float* acc, const uint2& kk, const float* q) {
+  const uint32_t w[2] = {kk.x, kk.y};
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu));
+    const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16));
+    acc[2 * m] = fadd(acc[2 * m], mulh(q[2 * m], lo));
+    acc[2 * m + 1] = fadd(acc[2 * m + 1], mulh(q[2 * m + 1], hi));
+  }
+}
+
+// score8 with mulh products: one 16-byte piece of a K row (8 F16 channels
+// 8i..8i+7) into the eight channel-strided accumulators.
+__device__ __forceinline__ void score8_mix(float* acc, const uint4& kk, const float* q) {
+  const float4 q0 = *reinterpret_cast<const float4*>(q);
+  const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
+  const uint32_t w[4] = {kk.x, kk.y, kk.z, kk.w};
+  const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu));
+    const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16));
+    acc[2 * m] = fadd(acc[2 * m], mulh(qv[2 * m], lo));
+    acc[2 * m + 1] = fadd(acc[2 * m + 1], mulh(qv[2 * m + 1], hi));
+  }
+}
 
 // A compute lane's share of one weight slice: P (row, block) pairs, each 32
 // int8 weights and the block's F16 scale.
@@ -285,78 +430,75 @@ __device__ __forceinline__ float ordered_sum(const float* prod, int r) {
   return sum;
 }
 
-// Block-wide double sum (all threads of the workgroup).
-__device__ __forceinline__ double block_sum_d(double v, double* red) {
-  v = wave_sum_double(v);
-  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
-  lds_barrier_p();
-  double t = 0.0;
-#pragma unroll
-  for (int i = 0; i < kPT / kWave; ++i) t += red[i];
-  lds_barrier_p();
-  return t;
-}
-
 __device__ __forceinline__ float4 tag_float4(const u64* tag, int e) {
   const uint4 a = *reinterpret_cast<const uint4*>(tag + e);
   const uint4 b = *reinterpret_cast<const uint4*>(tag + e + 2);
   return make_float4(u2f(a.x), u2f(a.z), u2f(b.x), u2f(b.z));
 }
 
+// Maximum over each aligned group of 16 lanes, in all 16 lanes.
+__device__ __forceinline__ uint32_t max16_u32(uint32_t m) {
+  uint32_t o = dpp_u32<kDppQuadXor1>(m);
+  m = o > m ? o : m;
+  o = dpp_u32<kDppQuadXor2>(m);
+  m = o > m ? o : m;
+  o = dpp_u32<kDppHalfMirror>(m);
+  m = o > m ? o : m;
+  o = dpp_u32<kDppMirror>(m);
+  return o > m ? o : m;
+}
+
 // RMSNorm (optional, weights in LDS) + activation quantisation of act[0, K)
-// into xq/xs, all threads. Same arithmetic as the multi-kernel GEMV prologue.
-// Thread i takes values 4i + 4*kPT*g; a wave covers 256 consecutive values,
-// so with K a multiple of 256 every wave is either whole or idle in a group,
-// and eight consecutive threads hold one 32-value block.
+// into xq/xs, all threads. The square sum is the multi-kernel GEMV
+// prologue's: threads t < 256 hold values 4t + 1024g, each sums its squares
+// pairwise in order, then the wave trees and the four wave sums in order, so
+// the norm is bit-identical to that path. The scaling and quantisation run
+// on all 512 threads, two values each (values 2t + 1024g): sixteen
+// consecutive threads hold one 32-value block.
 template <int K, bool NORM>
 __device__ __forceinline__ void quantize_input(const u64* act, const float* norm_w, float eps, int* xq, float* xs,
                                                double* red) {
-  static_assert(K % (4 * kWave) == 0, "whole waves per group");
-  constexpr int G = (K + 4 * kPT - 1) / (4 * kPT);
-  float4 v[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const int e = 4 * threadIdx.x + 4 * kPT * g;
-    v[g] = e < K ? tag_float4(act, e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  }
-  if (NORM) {
-    double sq = 0.0;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      sq += (double)v[g].x * (double)v[g].x + (double)v[g].y * (double)v[g].y;
-      sq += (double)v[g].z * (double)v[g].z + (double)v[g].w * (double)v[g].w;
+  static_assert(K % 128 == 0, "whole waves per group");
+  constexpr int G = (K + 2 * kPT - 1) / (2 * kPT);
+  const int tid = threadIdx.x;
+  float inverse = 1.0f;
+  if constexpr (NORM) {
+    static_assert(K <= 4 * kMem, "one norm group");
+    if (tid < kMem) {
+      const int e = 4 * tid;
+      const float4 v = e < K ? tag_float4(act, e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      double sq = 0.0;
+      sq += (double)v.x * (double)v.x + (double)v.y * (double)v.y;
+      sq += (double)v.z * (double)v.z + (double)v.w * (double)v.w;
+      sq = wave_sum_double(sq);
+      if ((tid & (kWave - 1)) == 0) red[tid / kWave] = sq;
     }
-    const double total = block_sum_d(sq, red);
+    lds_barrier_p();
+    double total = 0.0;
+#pragma unroll
+    for (int i = 0; i < kMem / kWave; ++i) total += red[i];
     const float mean = (float)(total / (double)K);
-    const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int e = 4 * threadIdx.x + 4 * kPT * g;
-      if (e < K) {
-        const float4 w = *reinterpret_cast<const float4*>(norm_w + e);
-        v[g].x = fmul(fmul(v[g].x, inverse), w.x);
-        v[g].y = fmul(fmul(v[g].y, inverse), w.y);
-        v[g].z = fmul(fmul(v[g].z, inverse), w.z);
-        v[g].w = fmul(fmul(v[g].w, inverse), w.w);
-      }
-    }
+    inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
   }
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int e = 4 * threadIdx.x + 4 * kPT * g;
+    const int e = 2 * tid + 2 * kPT * g;
     if (e < K) {  // wave-uniform
-      uint32_t m = f2u(v[g].x) & 0x7fffffffu, t;
-      t = f2u(v[g].y) & 0x7fffffffu; m = t > m ? t : m;
-      t = f2u(v[g].z) & 0x7fffffffu; m = t > m ? t : m;
-      t = f2u(v[g].w) & 0x7fffffffu; m = t > m ? t : m;
-      m = max8_u32(m);
+      const uint4 t = *reinterpret_cast<const uint4*>(act + e);
+      float v0 = u2f(t.x), v1 = u2f(t.z);
+      if (NORM) {
+        const float2 w = *reinterpret_cast<const float2*>(norm_w + e);
+        v0 = fmul(fmul(v0, inverse), w.x);
+        v1 = fmul(fmul(v1, inverse), w.y);
+      }
+      uint32_t m = f2u(v0) & 0x7fffffffu;
+      const uint32_t m1 = f2u(v1) & 0x7fffffffu;
+      m = max16_u32(m1 > m ? m1 : m);
       float inv;
       const float d = block_scale(m, &inv);
-      xq[e >> 2] = (int)((uint32_t)(uint8_t)quantize_value(v[g].x, inv) |
-                         ((uint32_t)(uint8_t)quantize_value(v[g].y, inv) << 8) |
-                         ((uint32_t)(uint8_t)quantize_value(v[g].z, inv) << 16) |
-                         ((uint32_t)(uint8_t)quantize_value(v[g].w, inv) << 24));
-      if ((threadIdx.x & 7) == 0) xs[e >> 5] = d;
+      reinterpret_cast<uint16_t*>(xq)[e >> 1] =
+          (uint16_t)((uint32_t)(uint8_t)quantize_value(v0, inv) | ((uint32_t)(uint8_t)quantize_value(v1, inv) << 8));
+      if ((tid & 15) == 0) xs[e >> 5] = d;
     }
   }
 }
@@ -368,7 +510,7 @@ __device__ __forceinline__ void quantize_input(const u64* act, const float* norm
 // one query head each; the other NBK - HQ run the projections, each on an
 // even share of the rows of every matrix. All of them run the lm_head.
 template <int W, int HQ, int HKV, int FF, int NBK>
-__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) void decode_step_kernel(PersistentArgs a) {
+__global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_step_kernel(PersistentArgs a) {
   constexpr int HS = 128, QW = HQ * HS, KVW = HKV * HS, QKVR = QW + 2 * KVW;
   constexpr int B1 = W / 32, Bq = QW / 32, Bf = FF / 32;
   constexpr int NB = NBK, NG = NBK - HQ;
@@ -393,15 +535,15 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __shared__ float row_s[2][64];  // residual rows: [0] x, [1] a
   __shared__ double red_s[kPT / kWave];
   __shared__ int flag_s;
+  __shared__ int okw_s[kMem / kWave];  // per memory wave: its part of the last gather completed
   __shared__ __attribute__((aligned(16))) float cur_s[3][128];  // attention: q, k, v of the current position
   __shared__ float tmax_s[kPT / kWave];
-  __shared__ double lane_s[8];
   __shared__ float inv_s;
   __shared__ __attribute__((aligned(16))) char kv_s[kKvBytes];  // [t][K 128 | V 128] fp16; lm_head products
 
   const int w = blockIdx.x;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int ct = tid - kWave;  // compute-lane index (negative in wave 0)
+  const int ct = tid - kMem;  // compute-lane index (negative in the memory waves)
   const int L = a.layers;
   const int pos = *a.position;
   const uint32_t gen0 = *a.epoch * (uint32_t)(5 * L + 2) + 1u;
@@ -477,76 +619,127 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       }
       lds_barrier_p();
       if (!flag_s) return;
+      auto mark = [&](int event) {  // attention sub-phase stamps (events the projections use)
+        if (tl && tid == 0) tl[event] = __builtin_amdgcn_s_memrealtime();
+      };
 
-      // Norm + rope of q (threads 0-127) and k (128-255); v rounded to F16.
-      {
-        const int part = tid >> 7, c = tid & 127;
-        float v = tag_value(tag_s, part * HS + c);
-        double sq = wave_sum_double((double)v * (double)v);
-        if (lane == 0) red_s[wave] = sq;
-        lds_barrier_p();
-        float mean = (float)((red_s[2 * part] + red_s[2 * part + 1]) / (double)HS);
-        float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, a.eps)));
-        cur_s[part][c] = fmul(fmul(v, inverse), norm_s[part * HS + c]);
-        if (tid < HS) cur_s[2][tid] = from_half(to_half(tag_value(tag_s, 2 * HS + tid)));
-      }
-      lds_barrier_p();
-      float rot = 0.0f;
-      {
-        const int part = tid >> 7, c = tid & 127, half = HS >> 1;
-        const float* cosine = norm_s + 2 * HS;
-        const float* sine = norm_s + 2 * HS + half;
-        if (c < half) rot = fadd(fmul(cur_s[part][c], cosine[c]), -fmul(cur_s[part][c + half], sine[c]));
-        else rot = fadd(fmul(cur_s[part][c - half], sine[c - half]), fmul(cur_s[part][c], cosine[c - half]));
-      }
-      lds_barrier_p();
-      // This position's K row, F16 and swizzled like the staged rows.
+      // QK-norm + RoPE, one wave per vector and channels (c, c + 64) in lane
+      // c, so that the rotation partners sit in one lane: wave 0 q, wave 1 k
+      // (F16-rounded, also as this position's swizzled K row), wave 2 v
+      // rounded to F16. The norm's square sum is the two 64-channel wave
+      // sums added low half first.
       char* kcur = reinterpret_cast<char*>(norm_s + 512);
-      if (tid < 128) {
-        cur_s[0][tid] = rot;
-      } else {
-        const int c = tid - 128;
-        const _Float16 k16 = to_half(rot);
-        cur_s[1][c] = from_half(k16);
-        reinterpret_cast<_Float16*>(kcur + (((c >> 3) ^ (pos & 15)) << 4))[c & 7] = k16;
+      if (wave < 2) {
+        const int c = lane, half = HS / 2;
+        const float lo = tag_value(tag_s, wave * HS + c), hi = tag_value(tag_s, wave * HS + half + c);
+        const double sq = wave_sum_double((double)lo * (double)lo) + wave_sum_double((double)hi * (double)hi);
+        const float mean = (float)(sq / (double)HS);
+        const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, a.eps)));
+        const float* nw = norm_s + wave * HS;
+        const float nlo = fmul(fmul(lo, inverse), nw[c]), nhi = fmul(fmul(hi, inverse), nw[half + c]);
+        const float cs = norm_s[2 * HS + c], sn = norm_s[2 * HS + half + c];
+        const float rlo = fadd(fmul(nlo, cs), -fmul(nhi, sn));
+        const float rhi = fadd(fmul(nlo, sn), fmul(nhi, cs));
+        if (wave == 0) {
+          cur_s[0][c] = rlo;
+          cur_s[0][half + c] = rhi;
+        } else {
+          const _Float16 klo = to_half(rlo), khi = to_half(rhi);
+          cur_s[1][c] = from_half(klo);
+          cur_s[1][half + c] = from_half(khi);
+          const int cc = half + c;
+          reinterpret_cast<_Float16*>(kcur + (((c >> 3) ^ (pos & 15)) << 4))[c & 7] = klo;
+          reinterpret_cast<_Float16*>(kcur + (((cc >> 3) ^ (pos & 15)) << 4))[cc & 7] = khi;
+        }
+      } else if (wave == 2) {
+        cur_s[2][lane] = from_half(to_half(tag_value(tag_s, 2 * HS + lane)));
+        cur_s[2][kWave + lane] = from_half(to_half(tag_value(tag_s, 2 * HS + kWave + lane)));
       }
       lds_barrier_p();
       sub(0);
 
       // Scores, one position per lane: eight accumulators over channels
-      // j, j+8, ..., then the pairwise tree (AttentionAvx.cs:74-160). Each
-      // lane keeps the maximum of its scores for the softmax shift.
+      // j, j+8, ..., then the pairwise tree (AttentionAvx.cs:74-160). The
+      // products q*k are formed by one mixed-precision fma with a +0 addend
+      // (the F16 key widened inside the instruction): round(q*k) + 0 equals
+      // round(q*k) except that a -0 product becomes +0, and no accumulator
+      // here is ever -0 (they start at +0 and x + y is -0 only for -0 + -0),
+      // so every sum is the reference's. Each lane keeps the maximum of its
+      // scores for the softmax shift.
       float m = -__builtin_inff();
-      for (int t = tid; t < n; t += kPT) {
-        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        if (t < nlds || t == pos) {
-          const char* row = t == pos ? kcur : (t < npre ? kv_s + (size_t)t * 512 : ovf_s + (size_t)(t - npre) * 512);
-          const int x = (t & 15) << 4;
+      // Two lanes per position, so that all eight waves share the rows: the
+      // even lane keeps accumulators 0-3 and the odd lane 4-7, i.e. channels
+      // 8i + 4h .. 8i + 4h + 3 (h = lane parity) of every 16-byte piece i,
+      // each accumulator still summed over i = 0..15 in order. q's matching
+      // channels sit in registers; K pieces are read in groups of four
+      // 8-byte halves, the next group in flight while one is multiplied.
+      const int hh = tid & 1;
+      float qr[64];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const uint4 kk = *reinterpret_cast<const uint4*>(row + ((i << 4) ^ x));
-            score8(acc, kk, &cur_s[0][8 * i]);
-          }
+      for (int i = 0; i < 16; ++i) {
+        const float4 v = *reinterpret_cast<const float4*>(&cur_s[0][8 * i + 4 * hh]);
+        qr[4 * i] = v.x;
+        qr[4 * i + 1] = v.y;
+        qr[4 * i + 2] = v.z;
+        qr[4 * i + 3] = v.w;
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): no scalar load pending, so LDS waits can count
+      for (int t = tid >> 1; t < n; t += kPT / 2) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (t < nlds || t == pos) {
+          const char* row = (t == pos ? kcur : (t < npre ? kv_s + (size_t)t * 512 : ovf_s + (size_t)(t - npre) * 512)) + 8 * hh;
+          const int x = (t & 15) << 4;
+          uint2 ka[4], kb[4];
+          auto load4 = [&](uint2* k, int g) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) k[i] = *reinterpret_cast<const uint2*>(row + (((4 * g + i) << 4) ^ x));
+          };
+          auto mul4 = [&](const uint2* k, int g) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) score4_regs(acc, k[i], qr + 4 * (4 * g + i));
+          };
+          load4(ka, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          load4(kb, 1);
+          __builtin_amdgcn_sched_barrier(0);
+          mul4(ka, 0);
+          __builtin_amdgcn_sched_barrier(0);
+          load4(ka, 2);
+          __builtin_amdgcn_sched_barrier(0);
+          mul4(kb, 1);
+          __builtin_amdgcn_sched_barrier(0);
+          load4(kb, 3);
+          __builtin_amdgcn_sched_barrier(0);
+          mul4(ka, 2);
+          __builtin_amdgcn_sched_barrier(0);
+          mul4(kb, 3);
         } else {
-          const uint4* g = reinterpret_cast<const uint4*>(kbase(l) + (size_t)t * HS);
+          const uint2* gk = reinterpret_cast<const uint2*>(kbase(l) + (size_t)t * HS + 4 * hh);
 #pragma unroll
           for (int i0 = 0; i0 < 16; i0 += 4) {
-            uint4 kk[4];
+            uint2 kk[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) kk[i] = g[i0 + i];
+            for (int i = 0; i < 4; ++i) kk[i] = gk[2 * (i0 + i)];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) score8(acc, kk[i], &cur_s[0][8 * (i0 + i)]);
+            for (int i = 0; i < 4; ++i) score4_regs(acc, kk[i], qr + 4 * (i0 + i));
           }
         }
-        const float s = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])),
-                             fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
+        // The partner lane's four accumulators; both lanes form the same tree
+        // ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)).
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = u2f(dpp_u32<kDppQuadXor1>(f2u(acc[j])));
+        const float* lo = hh ? o : acc;
+        const float* hi = hh ? acc : o;
+        const float s = fadd(fadd(fadd(lo[0], hi[0]), fadd(lo[1], hi[1])), fadd(fadd(lo[2], hi[2]), fadd(lo[3], hi[3])));
         const float sd = fdiv(s, a.divisor);
-        p_s[t] = sd;
+        if (hh == 0) p_s[t] = sd;
         m = nan_max_p(m, sd);
       }
       // Softmax (TensorMath.SoftmaxAvx.cs:11-58).
       m = wave_max_nan(m);
       if (lane == 0) tmax_s[wave] = m;
+      mark(e + 8);
       lds_barrier_p();
       sub(1);
       float mx = tmax_s[0];
@@ -554,6 +747,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int i = 1; i < kPT / kWave; ++i) mx = nan_max_p(mx, tmax_s[i]);
       for (int t = tid; t < n; t += kPT) p_s[t] = exp_ref(fadd(p_s[t], -mx));
       lds_barrier_p();
+      mark(e + 9);
       const int full = n & ~7;
       if (wave == 0) {
         // Lane j < 8: p[j] + p[j+8] + ... in order, in double; the eight
@@ -582,103 +776,16 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int t = tid; t < n; t += kPT) p_s[t] = fmul(p_s[t], inverse);
       lds_barrier_p();
       sub(2);
-      // Time-ordered value sums, one lane per channel (AttentionAvx.cs:173-224);
-      // blocks of 16 positions load their values before the chain uses them.
-      if (tid < HS) {
-        const int c = tid;
-        float acc = 0.0f;
-        auto chain16 = [&](const char* vrow, int t) {  // vrow: V row of position t, this channel
-          // Two positions per register (low half t+2k, high half t+2k+1), all
-          // sixteen loads issued before the chain consumes them.
-          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-          h2 v[8];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            v[k].x = *reinterpret_cast<const _Float16*>(vrow + 1024 * k);
-            v[k].y = *reinterpret_cast<const _Float16*>(vrow + 1024 * k + 512);
-          }
-          float p[16];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const float4 q = *reinterpret_cast<const float4*>(p_s + t + 4 * k);
-            p[4 * k] = q.x;
-            p[4 * k + 1] = q.y;
-            p[4 * k + 2] = q.z;
-            p[4 * k + 3] = q.w;
-          }
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            acc = fadd(acc, fmul(from_half(v[k].x), p[2 * k]));
-            acc = fadd(acc, fmul(from_half(v[k].y), p[2 * k + 1]));
-          }
-        };
-        // V of position t: kv_s + 512 t (t < npre), ovf_s + 512 (t - npre) after.
-        auto vrow = [&](int t) {
-          return (t < npre ? kv_s + (size_t)t * 512 : ovf_s + (size_t)(t - npre) * 512) + 256 + 2 * c;
-        };
-        auto prob = [&](int t) { return p_s[t]; };
-        auto step = [&](int t) { acc = fadd(acc, fmul(from_half(*reinterpret_cast<const _Float16*>(vrow(t))), prob(t))); };
-        int t = 0;
-        if (npre >= 32) {
-          // Staged rows: the next 16 positions' values and probabilities are
-          // read while the current 16 are added.
-          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-          h2 va[8], vb[8];
-          float4 pa[4], pb[4];
-          auto fetch = [&](h2* v, float4* pq, int t0) {
-            const char* vr = vrow(t0);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-              v[k].x = *reinterpret_cast<const _Float16*>(vr + 1024 * k);
-              v[k].y = *reinterpret_cast<const _Float16*>(vr + 1024 * k + 512);
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k) pq[k] = *reinterpret_cast<const float4*>(p_s + t0 + 4 * k);
-          };
-          auto add16 = [&](const h2* v, const float4* pq) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              acc = fadd(acc, fmul(from_half(v[2 * k].x), pq[k].x));
-              acc = fadd(acc, fmul(from_half(v[2 * k].y), pq[k].y));
-              acc = fadd(acc, fmul(from_half(v[2 * k + 1].x), pq[k].z));
-              acc = fadd(acc, fmul(from_half(v[2 * k + 1].y), pq[k].w));
-            }
-          };
-          fetch(va, pa, 0);
-          for (; t + 48 <= npre; t += 32) {
-            fetch(vb, pb, t + 16);
-            add16(va, pa);
-            fetch(va, pa, t + 32);
-            add16(vb, pb);
-          }
-          // va holds positions [t, t + 16); t + 16 <= npre here.
-          if (t + 32 <= npre) {
-            fetch(vb, pb, t + 16);
-            add16(va, pa);
-            add16(vb, pb);
-            t += 32;
-          } else {
-            add16(va, pa);
-            t += 16;
-          }
-        }
-        for (; t + 16 <= npre; t += 16) chain16(vrow(t), t);
-        for (; t < npre; ++t) step(t);
-        for (; t < nlds && (t & 3) != 0; ++t) step(t);
-        for (; t + 16 <= nlds; t += 16) chain16(vrow(t), t);
-        for (; t < nlds; ++t) step(t);
-        const _Float16* vglob = vbase(l) + c;
-        for (; t + 8 <= pos; t += 8) {
-          float x[8];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) x[k] = from_half(vglob[(size_t)(t + k) * HS]);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) acc = fadd(acc, fmul(x[k], prob(t + k)));
-        }
-        for (; t < pos; ++t) acc = fadd(acc, fmul(from_half(vglob[(size_t)t * HS]), prob(t)));
-        acc = fadd(acc, fmul(cur_s[2][c], prob(pos)));
-        cur_s[0][c] = acc;
+      // Time-ordered value sums, one lane per channel (AttentionAvx.cs:173-224),
+      // with the same exact mixed-precision products as the scores. Wave 0
+      // takes the even channels and wave 1 the odd ones, so that a lane's
+      // value is the same half of the dword (channels 2l, 2l+1) in every
+      // lane of its wave and one LDS read brings two positions.
+      if (wave < 2) {
+        if (wave == 0) value_chain<false>(kv_s, ovf_s, p_s, npre, nlds, pos, vbase(l), cur_s);
+        else value_chain<true>(kv_s, ovf_s, p_s, npre, nlds, pos, vbase(l), cur_s);
       }
+      mark(e + 10);
       lds_barrier_p();
       if (wave == 0) {
         tag_store(a.tatt + w * HS + lane, gen(l, 2), cur_s[0][lane]);
@@ -731,12 +838,12 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
       for (int k = 0; k < XI; ++k) xr[k] = a.x_in[tid + k * kPT];
     }
-    if (wave > 0) {
+    if (ct >= 0) {
       load_slot<NPQ>(sa, LT[0].wqkv + (size_t)rq.r0 * W, LT[0].sqkv + (size_t)rq.r0 * B1, ct, rq.count * B1);
       // Keep the two slices in issue order: the waits count on it.
       __builtin_amdgcn_sched_barrier(0);
       load_slot<NPO>(sb, LT[0].wo + (size_t)ro.r0 * QW, LT[0].so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
-    } else {
+    } else if (wave == 0) {
       dma(LT[0].attn_norm, norm_s, W * 4);
       __builtin_amdgcn_s_waitcnt(0);
     }
@@ -745,10 +852,28 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       tag_s[tid + k * kPT] = (u64)f2u(a.mode == 2 ? fmul((float)eq[k], (float)es[k]) : xr[k]);
     lds_barrier_p();
 
-    // Each phase: all threads quantise the gathered input, waves 1-3 form the
-    // block products of their slice, then wave 0 sums the rows in order,
-    // publishes them and gathers the next phase's input while waves 1-3 load
-    // the slice of the phase after next.
+    // The next phase's input, gathered by the four memory waves (a quarter of
+    // the chunks each, wave 0 also copies the constants `pre` names) while
+    // the compute waves load the slice of the phase after next. Returns
+    // whether every part completed (after the barrier).
+    auto gather_next = [&](const u64* src, int count, uint32_t gn, auto pre) {
+      if (ct < 0) {
+        const bool ok = wave == 0 ? gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, pre, wave, 4)
+                                  : gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, NoPre{}, wave, 4);
+        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      }
+    };
+    auto gathered = [&] {
+      lds_barrier_p();
+      t_in = __builtin_amdgcn_s_memrealtime();
+      return (okw_s[0] & okw_s[1] & okw_s[2] & okw_s[3]) != 0;
+    };
+
+    // Each phase: all threads quantise the gathered input, the compute waves
+    // form the block products of their slice, then wave 0 sums the rows in
+    // order and publishes them while the memory waves gather the next
+    // phase's input and the compute waves load the slice of the phase after
+    // next.
     for (int l = 0; l < L; ++l) {
       const auto& Ly = LT[l];
       const auto& Nx = LT[l + 1 < L ? l + 1 : l];  // the last layer re-reads its own slices
@@ -758,26 +883,23 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
       lds_barrier_p();
       sub(0);
-      if (wave > 0) slot_products<NPQ, B1>(sa, ct, xq_s, xs_s, prod_s, rq.count * B1);
+      if (ct >= 0) slot_products<NPQ, B1>(sa, ct, xq_s, xs_s, prod_s, rq.count * B1);
       lds_barrier_p();
       sub(1);
       if (wave == 0) {
         if (lane < rq.count) tag_store(a.tqkv + rq.r0 + lane, gen(l, 1), ordered_sum<B1>(prod_s, lane));
         stamps(e + 0, e + 2, e + 1, 1);
         if (tl && lane == 0) tl[e + 4] = t_sub[1];
-        const bool ok = gather1(a.tatt, QW, gen(l, 2), tag_s, a.error, NoPre{});
-        t_in = __builtin_amdgcn_s_memrealtime();
-        flag_s = ok ? 1 : 0;
-      } else {
-        load_slot<NPG>(sa, Ly.wgu + (size_t)2 * rf.r0 * W, Ly.sgu + (size_t)2 * rf.r0 * B1, ct, 2 * rf.count * B1);
       }
-      lds_barrier_p();
-      if (!flag_s) return;
+      if (ct >= 0)
+        load_slot<NPG>(sa, Ly.wgu + (size_t)2 * rf.r0 * W, Ly.sgu + (size_t)2 * rf.r0 * B1, ct, 2 * rf.count * B1);
+      gather_next(a.tatt, QW, gen(l, 2), NoPre{});
+      if (!gathered()) return;
 
       // ---- P3: o projection + residual -------------------------------------
       quantize_input<QW, false>(tag_s, nullptr, 0.0f, xq_s, xs_s, red_s);
       lds_barrier_p();
-      if (wave > 0) slot_products<NPO, Bq>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bq);
+      if (ct >= 0) slot_products<NPO, Bq>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bq);
       lds_barrier_p();
       if (wave == 0) {
         if (lane < ro.count) {
@@ -786,20 +908,16 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           tag_store(a.ta + ro.r0 + lane, gen(l, 3), v);
         }
         stamps(e + 8, e + 9);
-        const bool ok = gather1(a.ta, W, gen(l, 3), tag_s, a.error, [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
-        t_in = __builtin_amdgcn_s_memrealtime();
-        flag_s = ok ? 1 : 0;
-      } else {
-        load_slot<NPD>(sb, Ly.wd + (size_t)ro.r0 * FF, Ly.sd + (size_t)ro.r0 * Bf, ct, ro.count * Bf);
       }
-      lds_barrier_p();
-      if (!flag_s) return;
+      if (ct >= 0) load_slot<NPD>(sb, Ly.wd + (size_t)ro.r0 * FF, Ly.sd + (size_t)ro.r0 * Bf, ct, ro.count * Bf);
+      gather_next(a.ta, W, gen(l, 3), [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
+      if (!gathered()) return;
 
       // ---- P4: ffn_norm + gate/up + SwiGLU -----------------------------------
       quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
       lds_barrier_p();
       sub(0);
-      if (wave > 0) slot_products<NPG, B1>(sa, ct, xq_s, xs_s, prod_s, 2 * rf.count * B1);
+      if (ct >= 0) slot_products<NPG, B1>(sa, ct, xq_s, xs_s, prod_s, 2 * rf.count * B1);
       lds_barrier_p();
       if (wave == 0) {
         // Lanes [0, n) sum the gate rows, [n, 2n) the matching up rows.
@@ -811,20 +929,16 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           tag_store(a.th + rf.r0 + lane, gen(l, 4), fmul(silu, u));
         }
         stamps(e + 10, e + 12, e + 11, 1);
-        const bool ok = gather1(a.th, FF, gen(l, 4), tag_s, a.error, NoPre{});
-        t_in = __builtin_amdgcn_s_memrealtime();
-        flag_s = ok ? 1 : 0;
-      } else {
-        load_slot<NPQ>(sa, Nx.wqkv + (size_t)rq.r0 * W, Nx.sqkv + (size_t)rq.r0 * B1, ct, rq.count * B1);
       }
-      lds_barrier_p();
-      if (!flag_s) return;
+      if (ct >= 0) load_slot<NPQ>(sa, Nx.wqkv + (size_t)rq.r0 * W, Nx.sqkv + (size_t)rq.r0 * B1, ct, rq.count * B1);
+      gather_next(a.th, FF, gen(l, 4), NoPre{});
+      if (!gathered()) return;
 
       // ---- P5: down projection + residual ------------------------------------
       quantize_input<FF, false>(tag_s, nullptr, 0.0f, xq_s, xs_s, red_s);
       lds_barrier_p();
       sub(0);
-      if (wave > 0) slot_products<NPD, Bf>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bf);
+      if (ct >= 0) slot_products<NPD, Bf>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bf);
       lds_barrier_p();
       sub(1);
       if (wave == 0) {
@@ -834,16 +948,12 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
         stamps(e + 13, e + 15, e + 14, 1);
         if (tl && lane == 0) tl[e + 5] = t_sub[1];
-        // Next layer's input with its attn_norm, or the lm_head input with output_norm.
-        const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
-        const bool ok = gather1(a.tx, W, gen(l, 5), tag_s, a.error, [&] { dma(next_norm, norm_s, W * 4); });
-        t_in = __builtin_amdgcn_s_memrealtime();
-        flag_s = ok ? 1 : 0;
-      } else {
-        load_slot<NPO>(sb, Nx.wo + (size_t)ro.r0 * QW, Nx.so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
       }
-      lds_barrier_p();
-      if (!flag_s) return;
+      if (ct >= 0) load_slot<NPO>(sb, Nx.wo + (size_t)ro.r0 * QW, Nx.so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
+      // Next layer's input with its attn_norm, or the lm_head input with output_norm.
+      const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
+      gather_next(a.tx, W, gen(l, 5), [&] { dma(next_norm, norm_s, W * 4); });
+      if (!gathered()) return;
     }
   }
 
@@ -857,15 +967,15 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   // ---- output_norm + tied lm_head + greedy (every workgroup) -----------------
   // Chunks of HR rows, round-robin over workgroups, three in flight per
-  // compute lane; wave 0 sums chunk c (logits staged in LDS) while waves 1-3
-  // form chunk c+1.
+  // compute lane; wave 0 sums chunk c (logits staged in LDS) while the compute
+  // waves form chunk c+1.
   Slot<kSlotPairs> ha, hb, hc;
   auto load_head = [&](Slot<kSlotPairs>& sl, int c) {
     const int cc = c < chunks ? c : chunks - 1;  // clamped chunks are never summed
     const int row0 = cc * HR;
     load_slot<NPH>(sl, a.head_q + (size_t)row0 * W, a.head_s + (size_t)row0 * B1, ct, min(HR, a.vocab - row0) * B1);
   };
-  if (wave > 0) {
+  if (ct >= 0) {
     load_head(ha, w);
     load_head(hb, w + NB);
     load_head(hc, w + 2 * NB);
@@ -882,7 +992,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     float* pr = hprod + parity * HP;
     const int row0 = c * HR;
     const int rows = c < chunks ? min(HR, a.vocab - row0) : 0;
-    if (wave > 0) slot_products<NPH, B1>(sl, ct, xq_s, xs_s, pr, rows * B1);
+    if (ct >= 0) slot_products<NPH, B1>(sl, ct, xq_s, xs_s, pr, rows * B1);
     lds_barrier_p();
     if (tid < rows) {
       const float v = ordered_sum<B1>(pr, tid);
@@ -896,11 +1006,11 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   };
   for (int c = w; c < chunks; c += 3 * NB) {
     head_chunk(ha, c);
-    if (wave > 0) load_head(ha, c + 3 * NB);
+    if (ct >= 0) load_head(ha, c + 3 * NB);
     head_chunk(hb, c + NB);
-    if (wave > 0) load_head(hb, c + 4 * NB);
+    if (ct >= 0) load_head(hb, c + 4 * NB);
     head_chunk(hc, c + 2 * NB);
-    if (wave > 0) load_head(hc, c + 5 * NB);
+    if (ct >= 0) load_head(hc, c + 5 * NB);
   }
   if (wave != 0) return;
   // Wave 0 alone from here: logits out, then this workgroup's best key.
@@ -917,14 +1027,18 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     tag_store_bits(a.tkeys + 2 * w + 1, gen(L, 1), (uint32_t)best);
   }
   if (w != 0) return;
-  if (!gather1(a.tkeys, 2 * NB, gen(L, 1), tag_s, a.error, NoPre{}) || lane != 0) return;
+  if (!gather1(a.tkeys, 2 * NB, gen(L, 1), tag_s, a.error, NoPre{})) return;
+  // The workgroups' keys, a quarter of the grid per lane group, then the wave.
   u64 b = 0ull;
   bool first_nan = false;
-  for (int i = 0; i < NB; ++i) {
+  for (int i = lane; i < NB; i += kWave) {
     const u64 key = ((u64)(uint32_t)tag_s[2 * i] << 32) | (uint32_t)tag_s[2 * i + 1];
     if (key == ~0ull) first_nan = true;
     else b = key > b ? key : b;
   }
+  b = wave_max_u64(b);
+  first_nan = __any(first_nan);
+  if (lane != 0) return;
   *a.token = (first_nan || b == 0ull) ? 0 : (int)greedy_index(b);
   if (tl) tl[16 * L + 2] = __builtin_amdgcn_s_memrealtime();
   *a.position = pos + 1;
