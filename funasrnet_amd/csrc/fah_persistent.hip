@@ -110,9 +110,14 @@ struct NoPre {
 // once, before the first poll, so they share its wait. Chunks whose tags do
 // not all carry `gen` are issued again until every chunk is current.
 // Returns false after a timeout or when another workgroup reported an error.
-template <class Pre>
+struct NoChunk {
+  __device__ void operator()(int) const {}
+};
+
+template <class Pre, class OnChunk = NoChunk>
 __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int o1, const u64* s2, int n2, int o2,
-                       uint32_t gen, u64* tag, unsigned* error, Pre pre, int part = 0, int parts = 1) {
+                       uint32_t gen, u64* tag, unsigned* error, Pre pre, int part = 0, int parts = 1,
+                       OnChunk on_chunk = OnChunk{}) {
   const int lane = threadIdx.x & (kWave - 1);
   pre();
   const int c0 = n0 >> 7, c01 = c0 + (n1 >> 7), all = c01 + (n2 >> 7);
@@ -160,6 +165,7 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
       }
     }
     pending &= ~(1ull << (total - 1));
+    on_chunk(total - 1);
   }
   for (;; ++spin) {
     if (!pending) return true;
@@ -177,7 +183,10 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
       int off;
       locate(k, src, off);
       const uint4 t = *reinterpret_cast<const uint4*>(tag + off + 2 * lane);
-      if (__all(t.y == gen && t.w == gen)) pending &= ~(1ull << k);
+      if (__all(t.y == gen && t.w == gen)) {
+        pending &= ~(1ull << k);
+        on_chunk(k);
+      }
     }
     if (!pending) return true;
     if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
@@ -504,6 +513,59 @@ __device__ __forceinline__ void quantize_input(const u64* act, const float* norm
 }
 
 }  // namespace
+
+// One wave quantises chunk k of a gathered vector (values 128k + 2 lane,
+// +1; sixteen lanes per 32-value block), with the RMSNorm scaling when NORM
+// (the same arithmetic as quantize_input).
+template <bool NORM>
+__device__ __forceinline__ void quantize_chunk(const u64* act, int k, const float* norm_w, float inverse, int* xq,
+                                               float* xs) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int e = 128 * k + 2 * lane;
+  const uint4 t = *reinterpret_cast<const uint4*>(act + e);
+  float v0 = u2f(t.x), v1 = u2f(t.z);
+  if (NORM) {
+    const float2 w = *reinterpret_cast<const float2*>(norm_w + e);
+    v0 = fmul(fmul(v0, inverse), w.x);
+    v1 = fmul(fmul(v1, inverse), w.y);
+  }
+  uint32_t m = f2u(v0) & 0x7fffffffu;
+  const uint32_t m1 = f2u(v1) & 0x7fffffffu;
+  m = max16_u32(m1 > m ? m1 : m);
+  float inv;
+  const float d = block_scale(m, &inv);
+  reinterpret_cast<uint16_t*>(xq)[e >> 1] =
+      (uint16_t)((uint32_t)(uint8_t)quantize_value(v0, inv) | ((uint32_t)(uint8_t)quantize_value(v1, inv) << 8));
+  if ((lane & 15) == 0) xs[e >> 5] = d;
+}
+
+// Memory wave m's part of the RMSNorm square sum of a K-value vector
+// (K <= 1024): threads t = 64m + lane of the GEMV prologue's tree hold values
+// 4t..4t+3, i.e. chunks 2m and 2m + 1, which this wave gathered itself.
+template <int K>
+__device__ __forceinline__ void norm_partial(const u64* act, int m, double* red) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int e = 4 * (kWave * m + lane);
+  const float4 v = e < K ? tag_float4(act, e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  double sq = 0.0;
+  sq += (double)v.x * (double)v.x + (double)v.y * (double)v.y;
+  sq += (double)v.z * (double)v.z + (double)v.w * (double)v.w;
+  sq = wave_sum_double(sq);
+  if (lane == 0) red[m] = sq;
+}
+
+// After the barrier that follows norm_partial: the inverse RMS from the four
+// wave sums in order, then one chunk per wave scaled and quantised.
+template <int K>
+__device__ __forceinline__ void quantize_norm_chunks(const u64* act, const float* norm_w, float eps, const double* red,
+                                                     int* xq, float* xs) {
+  double total = 0.0;
+#pragma unroll
+  for (int i = 0; i < kMem / kWave; ++i) total += red[i];
+  const float mean = (float)(total / (double)K);
+  const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
+  for (int k = threadIdx.x / kWave; k < K / 128; k += kPT / kWave) quantize_chunk<true>(act, k, norm_w, inverse, xq, xs);
+}
 
 // Shape-specialised: W hidden width, HQ/HKV query/kv heads (head size 128),
 // FF feed-forward width, NBK workgroups. Workgroups [0, HQ) run attention,
@@ -851,15 +913,36 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int k = 0; k < XI; ++k)
       tag_s[tid + k * kPT] = (u64)f2u(a.mode == 2 ? fmul((float)eq[k], (float)es[k]) : xr[k]);
     lds_barrier_p();
+    // The layer-0 input's norm partials (later inputs get theirs in the gather).
+    if (ct < 0) {
+      if (wave < W / 256) norm_partial<W>(tag_s, wave, red_s);
+      else if (lane == 0) red_s[wave] = 0.0;
+    }
+    lds_barrier_p();
 
-    // The next phase's input, gathered by the four memory waves (a quarter of
-    // the chunks each, wave 0 also copies the constants `pre` names) while
-    // the compute waves load the slice of the phase after next. Returns
-    // whether every part completed (after the barrier).
-    auto gather_next = [&](const u64* src, int count, uint32_t gn, auto pre) {
+    // The next phase's input, gathered by the memory waves (each a part of
+    // the chunks; wave 0 also copies the constants `pre` names) while the
+    // compute waves load the slice of the phase after next. An input that is
+    // RMS-normalised (W values) is split so that wave m holds chunks 2m and
+    // 2m + 1 and adds its part of the square sum as soon as they are in; the
+    // others are split in four and quantised by all waves after the barrier.
+    auto gather_norm = [&](const u64* src, uint32_t gn, auto pre) {
       if (ct < 0) {
-        const bool ok = wave == 0 ? gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, pre, wave, 4)
-                                  : gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, NoPre{}, wave, 4);
+        constexpr int parts = W / 256;
+        bool ok = true;
+        if (wave < parts) {
+          ok = wave == 0 ? gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, pre, wave, parts)
+                         : gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, NoPre{}, wave, parts);
+          if (ok) norm_partial<W>(tag_s, wave, red_s);
+        } else if (lane == 0) {
+          red_s[wave] = 0.0;
+        }
+        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      }
+    };
+    auto gather_all = [&](const u64* src, int count, uint32_t gn) {
+      if (ct < 0) {
+        const bool ok = gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, NoPre{}, wave, 4);
         if (lane == 0) okw_s[wave] = ok ? 1 : 0;
       }
     };
@@ -880,7 +963,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int e = 16 * l + 1;
       // ---- P1: attn_norm + qkv ----------------------------------------------
       if (tid < ro.count) row_s[0][tid] = tag_value(tag_s, ro.r0 + tid);
-      quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
+      quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
       lds_barrier_p();
       sub(0);
       if (ct >= 0) slot_products<NPQ, B1>(sa, ct, xq_s, xs_s, prod_s, rq.count * B1);
@@ -893,7 +976,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       if (ct >= 0)
         load_slot<NPG>(sa, Ly.wgu + (size_t)2 * rf.r0 * W, Ly.sgu + (size_t)2 * rf.r0 * B1, ct, 2 * rf.count * B1);
-      gather_next(a.tatt, QW, gen(l, 2), NoPre{});
+      gather_all(a.tatt, QW, gen(l, 2));
       if (!gathered()) return;
 
       // ---- P3: o projection + residual -------------------------------------
@@ -910,11 +993,11 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stamps(e + 8, e + 9);
       }
       if (ct >= 0) load_slot<NPD>(sb, Ly.wd + (size_t)ro.r0 * FF, Ly.sd + (size_t)ro.r0 * Bf, ct, ro.count * Bf);
-      gather_next(a.ta, W, gen(l, 3), [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
+      gather_norm(a.ta, gen(l, 3), [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
       if (!gathered()) return;
 
       // ---- P4: ffn_norm + gate/up + SwiGLU -----------------------------------
-      quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
+      quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
       lds_barrier_p();
       sub(0);
       if (ct >= 0) slot_products<NPG, B1>(sa, ct, xq_s, xs_s, prod_s, 2 * rf.count * B1);
@@ -931,7 +1014,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stamps(e + 10, e + 12, e + 11, 1);
       }
       if (ct >= 0) load_slot<NPQ>(sa, Nx.wqkv + (size_t)rq.r0 * W, Nx.sqkv + (size_t)rq.r0 * B1, ct, rq.count * B1);
-      gather_next(a.th, FF, gen(l, 4), NoPre{});
+      gather_all(a.th, FF, gen(l, 4));
       if (!gathered()) return;
 
       // ---- P5: down projection + residual ------------------------------------
@@ -952,7 +1035,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (ct >= 0) load_slot<NPO>(sb, Nx.wo + (size_t)ro.r0 * QW, Nx.so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
       // Next layer's input with its attn_norm, or the lm_head input with output_norm.
       const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
-      gather_next(a.tx, W, gen(l, 5), [&] { dma(next_norm, norm_s, W * 4); });
+      gather_norm(a.tx, gen(l, 5), [&] { dma(next_norm, norm_s, W * 4); });
       if (!gathered()) return;
     }
   }
@@ -980,7 +1063,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     load_head(hb, w + NB);
     load_head(hc, w + 2 * NB);
   }
-  quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
+  // The attention workgroups' lm_head input was gathered whole by wave 0;
+  // the projection workgroups already hold its norm partials.
+  if (w < HQ) quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
+  else quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
   lds_barrier_p();
   constexpr int HP = HR * (B1 + 4);                 // one chunk's padded products
   float* hprod = reinterpret_cast<float*>(kv_s);  // two buffers of HP products
