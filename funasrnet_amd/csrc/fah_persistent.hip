@@ -137,10 +137,9 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
     }
   };
   long spin = 0;
-  // Large vectors: poll one chunk (the last) until it is current before
-  // reading them all, so that consumers that arrive early cost one 1 KB load
-  // per round trip instead of the whole vector. Small ones are polled whole
-  // (one round trip less once the data is there).
+  // Poll the end of the last chunk until it is current before reading them
+  // all (that chunk too), so that consumers that arrive early cost one small
+  // load per round trip instead of the whole vector.
   if (total > kSentinelChunks) {
     const u64* src;
     int off;
@@ -150,12 +149,14 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
     // is at least that new. Once the pipeline is full each iteration waits
     // about a quarter round trip, so the data is seen at most that long
     // after a poll could first have returned it.
+    // Only the chunk's last 64 bytes (lanes 0-3) are polled: the polls of
+    // every consumer together stay a small part of the memory traffic.
     for (int i = 0; i < kPolls - 1; ++i)
-      __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(tag + off), 16, 0, 16);
+      if (lane < 4) __builtin_amdgcn_global_load_lds(src + 120 + 2 * lane, (lds_ptr)(tag + off + 120), 16, 0, 16);
     for (;; ++spin) {
-      __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(tag + off), 16, 0, 16);
+      if (lane < 4) __builtin_amdgcn_global_load_lds(src + 120 + 2 * lane, (lds_ptr)(tag + off + 120), 16, 0, 16);
       __builtin_amdgcn_s_waitcnt(kWaitOldestPoll);
-      const uint4 t = *reinterpret_cast<const uint4*>(tag + off + 2 * lane);
+      const uint4 t = lane < 4 ? *reinterpret_cast<const uint4*>(tag + off + 120 + 2 * lane) : make_uint4(0, gen, 0, gen);
       if (__all(t.y == gen && t.w == gen)) break;
       if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
         if (lane == 0) __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -164,8 +165,6 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
         return false;
       }
     }
-    pending &= ~(1ull << (total - 1));
-    on_chunk(total - 1);
   }
   for (;; ++spin) {
     if (!pending) return true;
