@@ -518,6 +518,8 @@ void init_state(fah_decoder* d, hipStream_t s) {
     a.kv_width = kv_width;
     a.eps = k.eps;
     a.divisor = std::sqrt((float)k.head_size);
+    const char* l2 = std::getenv("FAH_LOCAL_L2");
+    a.local_l2 = (l2 && l2[0] == '0') ? 0 : (fah::persistent_xcd_round_robin(s) ? 1 : 0);
     a.rq = qkv_rows / nb;
     a.ro = k.width / nb;
     a.rgu = k.ffn / nb;
@@ -687,7 +689,12 @@ void check_step_error(fah_decoder* d) {
   check(hipMemcpy(&e, d->error.ptr, 4, hipMemcpyDeviceToHost), "D2H error word");
   if (e) {
     (void)hipMemset(d->error.ptr, 0, 4);
-    throw DeviceError{"persistent decode step: an exchange timed out (workgroups not co-resident?)"};
+    // A launch whose workgroups were not dealt to the XCDs in turn leaves a
+    // role unfilled and times out: later steps use placement-free roles.
+    const bool was_local = d->pargs.local_l2 != 0;
+    d->pargs.local_l2 = 0;
+    throw DeviceError{was_local ? "persistent decode step: an exchange timed out (XCD-local roles are now off)"
+                                : "persistent decode step: an exchange timed out (workgroups not co-resident?)"};
   }
 }
 
@@ -1596,7 +1603,7 @@ int fah_decoder_kv_read(fah_decoder* d, int layer, uint16_t* keys, uint16_t* val
 
 int64_t fah_decoder_weight_bytes(const fah_decoder* d) { return d ? d->wt->weight_bytes : 0; }
 
-int fah_decoder_persistent(const fah_decoder* d) { return d && d->persistent ? 1 : 0; }
+int fah_decoder_persistent(const fah_decoder* d) { return d && d->persistent ? (d->pargs.local_l2 ? 2 : 1) : 0; }
 
 int fah_decoder_timeline(fah_decoder* d, uint64_t* ticks, int count) {
   if (!d || !ticks) return fail(FAH_ERROR_ARGUMENT, "decoder/ticks is NULL");

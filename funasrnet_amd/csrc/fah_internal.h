@@ -116,6 +116,10 @@ struct PersistentArgs {
   unsigned* error;
   float* logits;
   unsigned long long* timeline;  // optional [2][kTimelineEvents] s_memrealtime stamps
+  // 1: workgroup w runs on XCD w % 8 (checked at creation and by every
+  // launch), so the q/k/v rows of kv head x are computed on XCD x and handed
+  // to its attention workgroups through that XCD's L2.
+  int local_l2;
 };
 
 constexpr int kTimelineEvents = 480;
@@ -188,6 +192,9 @@ hipError_t launch_session_embed(const int8_t* q, const void* scales, bool half_s
 
 bool persistent_shape_supported(int width, int heads, int kv_heads, int head_size, int ffn, int blocks);
 hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s);
+// Whether 256 workgroups of the persistent kernel's size land on XCD
+// w % 8 (one launch of a placement probe; false if it cannot tell).
+bool persistent_xcd_round_robin(hipStream_t s);
 int persistent_max_positions();
 int persistent_max_capacity();
 int persistent_threads();

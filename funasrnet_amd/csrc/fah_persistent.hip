@@ -58,6 +58,13 @@ __device__ __forceinline__ void tag_store(u64* p, uint32_t gen, float v) {
 __device__ __forceinline__ void tag_store_bits(u64* p, uint32_t gen, uint32_t bits) {
   __hip_atomic_store(p, ((u64)gen << 32) | (u64)bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Store that other workgroups of the same XCD read through its L2 (not
+// written through to memory).
+__device__ __forceinline__ void tag_store_local(u64* p, uint32_t gen, float v) {
+  __hip_atomic_store(p, ((u64)gen << 32) | (u64)f2u(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// The XCD this wave runs on (hardware register XCC_ID, bits 3:0).
+__device__ __forceinline__ int xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15; }
 __device__ __forceinline__ unsigned error_load(const unsigned* e) {
   return __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -117,7 +124,7 @@ struct NoChunk {
 template <class Pre, class OnChunk = NoChunk>
 __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int o1, const u64* s2, int n2, int o2,
                        uint32_t gen, u64* tag, unsigned* error, Pre pre, int part = 0, int parts = 1,
-                       OnChunk on_chunk = OnChunk{}) {
+                       OnChunk on_chunk = OnChunk{}, u64* seen = nullptr) {
   const int lane = threadIdx.x & (kWave - 1);
   pre();
   const int c0 = n0 >> 7, c01 = c0 + (n1 >> 7), all = c01 + (n2 >> 7);
@@ -157,17 +164,25 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
       if (lane < 4) __builtin_amdgcn_global_load_lds(src + 120 + 2 * lane, (lds_ptr)(tag + off + 120), 16, 0, 16);
       __builtin_amdgcn_s_waitcnt(kWaitOldestPoll);
       const uint4 t = lane < 4 ? *reinterpret_cast<const uint4*>(tag + off + 120 + 2 * lane) : make_uint4(0, gen, 0, gen);
-      if (__all(t.y == gen && t.w == gen)) break;
+      if (__all(t.y == gen && t.w == gen)) {
+        if (seen) seen[0] = __builtin_amdgcn_s_memrealtime();
+        break;
+      }
       if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
-        if (lane == 0) __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_fetch_or(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // Drained here so that no store is pending where the waves rejoin.
         __builtin_amdgcn_s_waitcnt(0);
         return false;
       }
     }
   }
+  int rounds = 0;
   for (;; ++spin) {
-    if (!pending) return true;
+    if (!pending) {
+      if (seen) seen[1] = rounds;
+      return true;
+    }
+    ++rounds;
     for (u64 m = pending; m; m &= m - 1) {
       const u64* src;
       int off;
@@ -189,8 +204,50 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
     }
     if (!pending) return true;
     if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
-      if (lane == 0) __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) __hip_atomic_fetch_or(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // Drained here so that no store is pending where the waves rejoin.
+      __builtin_amdgcn_s_waitcnt(0);
+      return false;
+    }
+  }
+}
+
+// The attention workgroup's q, k and v (three 128-word chunks), polled
+// directly: rounds of three loads, two rounds in flight, each round's
+// chunks checked when it has returned. Its few consumers make the polling
+// traffic negligible, and the data are seen one round trip after they are
+// current instead of a sentinel's round trip plus a read's. Each lane's
+// 16 bytes land in LDS whole, so every tagged word it checks is intact.
+template <class Pre>
+__device__ bool gather_qkv(const u64* q, const u64* k, const u64* v, uint32_t gen, u64* tag, unsigned* error, Pre pre,
+                           u64* seen = nullptr) {
+  const int lane = threadIdx.x & (kWave - 1);
+  pre();
+  auto round = [&] {
+    __builtin_amdgcn_global_load_lds(q + 2 * lane, (lds_ptr)(tag), 16, 0, 16);
+    __builtin_amdgcn_global_load_lds(k + 2 * lane, (lds_ptr)(tag + 128), 16, 0, 16);
+    __builtin_amdgcn_global_load_lds(v + 2 * lane, (lds_ptr)(tag + 256), 16, 0, 16);
+  };
+  // s_waitcnt immediate: vmcnt <= 3 (the newer round), expcnt/lgkmcnt not waited.
+  constexpr int kWaitOlderRound = 3 | (7 << 4) | (15 << 8);
+  round();
+  unsigned done = 0;
+  for (long spin = 0;; ++spin) {
+    round();
+    __builtin_amdgcn_s_waitcnt(kWaitOlderRound);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const uint4 t = *reinterpret_cast<const uint4*>(tag + 128 * c + 2 * lane);
+      if (__all(t.y == gen && t.w == gen)) done |= 1u << c;
+    }
+    if (done == 7u) {
+      if (seen) seen[0] = __builtin_amdgcn_s_memrealtime();
+      // Drained: the newer round writes the same current words.
+      __builtin_amdgcn_s_waitcnt(0);
+      return true;
+    }
+    if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
+      if (lane == 0) __hip_atomic_fetch_or(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __builtin_amdgcn_s_waitcnt(0);
       return false;
     }
@@ -367,6 +424,26 @@ __device__ __forceinline__ void load_slot(Slot<P>& sl, const int8_t* w, const _F
     sl.w[i][0] = p[0];
     sl.w[i][1] = p[1];
     sl.s[i] = s[j];
+  }
+}
+
+// load_slot for a slice whose rows are not contiguous in storage: pair j is
+// slice row r0 + j / B (mapped to its storage row by `row`), block j % B.
+template <int NP, int B, int P, class RowMap>
+__device__ __forceinline__ void load_slot_rows(Slot<P>& sl, const int8_t* w, const _Float16* s, int r0, int ct, int valid,
+                                               RowMap row) {
+  constexpr int kI = (NP + kComp - 1) / kComp;
+  static_assert(kI <= P, "slot capacity");
+#pragma unroll
+  for (int i = 0; i < kI; ++i) {
+    int j = ct + i * kComp;
+    j = j < valid ? j : valid - 1;
+    const int rr = j / B, b = j - rr * B;
+    const size_t at = (size_t)row(r0 + rr) * B + b;
+    const int4* p = reinterpret_cast<const int4*>(w + at * 32);
+    sl.w[i][0] = p[0];
+    sl.w[i][1] = p[1];
+    sl.s[i] = s[at];
   }
 }
 
@@ -575,8 +652,14 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int HS = 128, QW = HQ * HS, KVW = HKV * HS, QKVR = QW + 2 * KVW;
   constexpr int B1 = W / 32, Bq = QW / 32, Bf = FF / 32;
   constexpr int NB = NBK, NG = NBK - HQ;
+  // Attention workgroups: w = x + 8s for kv head x < HKV and s < G, query head
+  // G x + s, so that kv head x's attention runs on XCD x (workgroups are
+  // dealt to the eight XCDs in turn). The q/k/v rows of kv head x (QL rows)
+  // are computed by the NX other workgroups of XCD x.
+  constexpr int G = HQ / HKV, QL = (G + 2) * HS, NX = NB / 8 - G;
+  static_assert(NB % 8 == 0 && HKV <= 8 && G >= 1 && HQ == G * HKV, "attention placement");
   // Largest per-workgroup slices (rows) and their (row, block) pairs.
-  constexpr int RQ = (QKVR + NG - 1) / NG, RO = (W + NG - 1) / NG, RGU = (FF + NG - 1) / NG;
+  constexpr int RQ = (QL + NX - 1) / NX, RO = (W + NG - 1) / NG, RGU = (FF + NG - 1) / NG;
   constexpr int NPQ = RQ * B1, NPO = RO * Bq, NPG = 2 * RGU * B1, NPD = RO * Bf;
   constexpr int PA = (NPQ > NPG ? NPQ : NPG) / kComp + 1;  // slot A: qkv, gate/up
   constexpr int PB = (NPO > NPD ? NPO : NPD) / kComp + 1;  // slot B: o, down
@@ -587,7 +670,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     2 * RGU * (B1 + 4) <= kProdFloats && RO * (Bq + 4) <= kProdFloats && RO * (Bf + 4) <= kProdFloats,
                 "LDS sizing");
   static_assert(W % kPT == 0 && 2 * NPH * 4 <= kKvBytes, "layer-0 input and lm_head product buffers");
-  static_assert(HQ < NB && HQ == 2 * HKV, "paired heads, one attention workgroup per query head");
+  static_assert(HQ < NB && QKVR == HKV * QL, "one attention workgroup per query head");
   __shared__ __attribute__((aligned(16))) u64 tag_s[kTagWords];  // gathered inputs (low 32 bits)
   __shared__ __attribute__((aligned(16))) float norm_s[1024];   // norm weights; attention: q/k norm, cos, sin
   __shared__ __attribute__((aligned(16))) int xq_s[kActFloats / 4];
@@ -602,8 +685,14 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ float inv_s;
   __shared__ __attribute__((aligned(16))) char kv_s[kKvBytes];  // [t][K 128 | V 128] fp16; lm_head products
 
-  const int w = blockIdx.x;
+  // Role index: with local_l2 the role follows the XCD the workgroup runs
+  // on (the hardware deals a launch's workgroups to the eight XCDs in turn,
+  // starting wherever the previous launch stopped), so that role w always
+  // sits on XCD w % 8. Any other dealing leaves some role unfilled; its
+  // exchanges then time out and the launch reports an error.
+  const int w = a.local_l2 ? 8 * ((int)blockIdx.x >> 3) + xcc_id() % 8 : (int)blockIdx.x;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const bool is_attn = (w & 7) < HKV && (w >> 3) < G;
   const int ct = tid - kMem;  // compute-lane index (negative in the memory waves)
   const int L = a.layers;
   const int pos = *a.position;
@@ -631,10 +720,9 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   };
 
-  if (w < HQ) {
+  if (is_attn) {
     // ======================= attention workgroup ================================
-    constexpr int group = HQ / HKV;
-    const int kh = w / group;
+    const int kh = w & 7, hq = G * kh + (w >> 3);
     const int n = pos + 1;
     const int npre = min(pos, a.npre);
     // Positions past the K/V stage go to the free end of the gather area
@@ -666,17 +754,23 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int l = 0; l < L; ++l) {
       const auto& Ly = LT[l];
       const int e = 16 * l + 1;  // timeline events of this layer
+      u64 seen_s[2] = {0, 0};
+      const u64 t_start = __builtin_amdgcn_s_memrealtime();
       if (wave == 0) {
-        const int qo = w * HS, ko = QW + kh * HS, vo = QW + KVW + kh * HS;
-        const bool ok =
-            gather(a.tqkv + qo, HS, 0, a.tqkv + ko, HS, HS, a.tqkv + vo, HS, 2 * HS, gen(l, 1), tag_s, a.error, [&] {
+        const int qo = hq * HS, ko = QW + kh * HS, vo = QW + KVW + kh * HS;
+        const bool ok = gather_qkv(a.tqkv + qo, a.tqkv + ko, a.tqkv + vo, gen(l, 1), tag_s, a.error, [&] {
               dma(Ly.q_norm, norm_s, HS * 4);
               dma(Ly.k_norm, norm_s + HS, HS * 4);
               dma(a.rope_cos + (size_t)pos * (HS / 2), norm_s + 2 * HS, HS * 2);
               dma(a.rope_sin + (size_t)pos * (HS / 2), norm_s + 2 * HS + HS / 2, HS * 2);
-            });
+            }, seen_s);
         t_in = __builtin_amdgcn_s_memrealtime();
         flag_s = ok ? 1 : 0;
+        if (tl && lane == 0) {
+          tl[e + 0] = seen_s[0];
+          tl[e + 1] = seen_s[1];
+          tl[e + 2] = t_start;
+        }
       }
       lds_barrier_p();
       if (!flag_s) return;
@@ -849,9 +943,9 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       mark(e + 10);
       lds_barrier_p();
       if (wave == 0) {
-        tag_store(a.tatt + w * HS + lane, gen(l, 2), cur_s[0][lane]);
-        tag_store(a.tatt + w * HS + kWave + lane, gen(l, 2), cur_s[0][kWave + lane]);
-        if (w % group == 0) {
+        tag_store(a.tatt + hq * HS + lane, gen(l, 2), cur_s[0][lane]);
+        tag_store(a.tatt + hq * HS + kWave + lane, gen(l, 2), cur_s[0][kWave + lane]);
+        if ((w >> 3) == 0) {
           // The first query head of the pair writes this position's K/V row
           // (four channels per lane).
           const int c = 4 * (lane & 31);
@@ -875,8 +969,19 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (!flag_s) return;
   } else {
     // ======================= projection workgroup ===============================
-    const int g = w - HQ;
-    const Rows rq = split_rows<QKVR, NG>(g), ro = split_rows<W, NG>(g), rf = split_rows<FF, NG>(g);
+    // g: rank among the projection workgroups (attention ones below w skipped).
+    int g = w;
+#pragma unroll
+    for (int s8 = 0; s8 < G; ++s8) g -= min(max(w - 8 * s8, 0), HKV);
+    const Rows ro = split_rows<W, NG>(g), rf = split_rows<FF, NG>(g);
+    // q/k/v: this XCD's kv head; none on XCDs past the kv heads, whose
+    // (unused, clamped) slice loads then read kv head 0's rows.
+    const int xk = (w & 7) < HKV ? (w & 7) : 0;
+    const Rows rq = (w & 7) < HKV ? split_rows<QL, NX>((w >> 3) - G) : Rows{0, 0};
+    auto qkv_row = [&](int r) {  // row r of kv head xk's list -> q/k/v row
+      return r < G * HS ? G * HS * xk + r
+                        : (r < (G + 1) * HS ? QW + HS * xk + (r - G * HS) : QW + KVW + HS * xk + (r - (G + 1) * HS));
+    };
     Slot<PA> sa;
     Slot<PB> sb;
     // Layer-0 input: a host row or the embedding of the device token
@@ -900,7 +1005,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int k = 0; k < XI; ++k) xr[k] = a.x_in[tid + k * kPT];
     }
     if (ct >= 0) {
-      load_slot<NPQ>(sa, LT[0].wqkv + (size_t)rq.r0 * W, LT[0].sqkv + (size_t)rq.r0 * B1, ct, rq.count * B1);
+      load_slot_rows<NPQ, B1>(sa, LT[0].wqkv, LT[0].sqkv, rq.r0, ct, max(rq.count, 1) * B1, qkv_row);
       // Keep the two slices in issue order: the waits count on it.
       __builtin_amdgcn_sched_barrier(0);
       load_slot<NPO>(sb, LT[0].wo + (size_t)ro.r0 * QW, LT[0].so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
@@ -969,7 +1074,12 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lds_barrier_p();
       sub(1);
       if (wave == 0) {
-        if (lane < rq.count) tag_store(a.tqkv + rq.r0 + lane, gen(l, 1), ordered_sum<B1>(prod_s, lane));
+        if (lane < rq.count) {
+          const float v = ordered_sum<B1>(prod_s, lane);
+          u64* dst = a.tqkv + qkv_row(rq.r0 + lane);
+          if (a.local_l2) tag_store_local(dst, gen(l, 1), v);
+          else tag_store(dst, gen(l, 1), v);
+        }
         stamps(e + 0, e + 2, e + 1, 1);
         if (tl && lane == 0) tl[e + 4] = t_sub[1];
       }
@@ -1012,7 +1122,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         stamps(e + 10, e + 12, e + 11, 1);
       }
-      if (ct >= 0) load_slot<NPQ>(sa, Nx.wqkv + (size_t)rq.r0 * W, Nx.sqkv + (size_t)rq.r0 * B1, ct, rq.count * B1);
+      if (ct >= 0) load_slot_rows<NPQ, B1>(sa, Nx.wqkv, Nx.sqkv, rq.r0, ct, max(rq.count, 1) * B1, qkv_row);
       gather_all(a.th, FF, gen(l, 4));
       if (!gathered()) return;
 
@@ -1064,7 +1174,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   // The attention workgroups' lm_head input was gathered whole by wave 0;
   // the projection workgroups already hold its norm partials.
-  if (w < HQ) quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
+  if (is_attn) quantize_input<W, true>(tag_s, norm_s, a.eps, xq_s, xs_s, red_s);
   else quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
   lds_barrier_p();
   constexpr int HP = HR * (B1 + 4);                 // one chunk's padded products
@@ -1154,6 +1264,33 @@ hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s
   else
     decode_step_kernel<512, 4, 2, 1024, 256><<<blocks, kPT, 0, s>>>(a);
   return hipGetLastError();
+}
+
+// One workgroup per CU (its LDS alone exceeds half a CU's), each records
+// the XCD it runs on.
+__global__ __launch_bounds__(kPT) void placement_probe_kernel(int* out) {
+  extern __shared__ int lds_pad[];
+  if (threadIdx.x == 0) {
+    lds_pad[0] = xcc_id();
+    out[blockIdx.x] = lds_pad[0];
+  }
+}
+
+bool persistent_xcd_round_robin(hipStream_t s) {
+  constexpr int n = 256;
+  int* d = nullptr;
+  if (hipMalloc(&d, n * sizeof(int)) != hipSuccess) return false;
+  int h[n];
+  bool ok = hipMemsetAsync(d, 0xff, n * sizeof(int), s) == hipSuccess;
+  if (ok) {
+    placement_probe_kernel<<<n, kPT, 96 * 1024, s>>>(d);
+    ok = hipGetLastError() == hipSuccess &&
+         hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, s) == hipSuccess && hipStreamSynchronize(s) == hipSuccess;
+  }
+  (void)hipFree(d);
+  // Eight XCDs dealt in turn: consecutive workgroups on consecutive XCDs.
+  for (int w = 1; ok && w < n; ++w) ok = h[w] >= 0 && h[w] < 8 && h[w] == (h[w - 1] + 1) % 8;
+  return ok && h[0] >= 0 && h[0] < 8;
 }
 
 int persistent_max_positions() { return kKvBytes / 512; }
