@@ -2,23 +2,34 @@
 // greedy) in one launch of one workgroup per CU.
 //
 // Every workgroup owns a fixed slice of rows of every projection. A layer is
-// five phases -- qkv, attention, o, gate/up, down -- separated by all-to-all
-// exchanges of the activation vector through global memory. Each value is
-// published as a 64-bit word (generation << 32 | float bits) with one
-// relaxed device-scope store, so a consumer sees value and readiness in the
-// same load and a phase boundary costs one memory round trip.
+// five phases -- qkv, attention, o, gate/up, down -- separated by exchanges
+// of the activation vector through global memory. Each value is published
+// as a 64-bit word (generation << 32 | float bits) with one relaxed store,
+// so a consumer sees value and readiness in the same load.
 //
-// Roles inside a workgroup (4 waves):
-//  * wave 0 is the memory wave: it gathers the next phase's input and, in
-//    the same batch of direct global->LDS loads, the small per-layer
-//    constants (norm weights, RoPE row) and the K/V rows of earlier
-//    positions for the next attention. Its waits drain only its own loads.
-//  * waves 1-3 are the compute waves: they hold the weight slices of the
+// Placement: the hardware deals a launch's workgroups to the eight XCDs in
+// turn. The attention workgroups of kv head x and the workgroups that form
+// that head's q/k/v rows all sit on XCD x, so that hand-over stays in one
+// L2 (stores that are not written through); the other exchanges cross XCDs
+// (device-scope stores, device-coherent loads).
+//
+// Roles inside a workgroup (8 waves, two per SIMD):
+//  * waves 0-3 are the memory waves: they gather the next phase's input, a
+//    part of the chunks each (wave 0 also fetches the small per-layer
+//    constants in the same batch), each polling only the last 64 bytes of
+//    its part until they are current and then reading the part whole, so
+//    that the polls of all consumers stay a small part of the traffic.
+//    Wave 0 also sums the phase's rows in order and publishes them.
+//  * waves 4-7 are the compute waves: they hold the weight slices of the
 //    next two phases in registers (issued a phase ahead, a fixed number of
-//    loads per phase so that every wait counts exactly the loads it needs),
-//    and issue no other global load in the steady state.
+//    loads per phase so that every wait counts exactly the loads it needs)
+//    and form the block products.
+//  * all eight quantise the phase input.
+// Attention workgroups use all eight waves for the scores, the softmax and
+// the K/V staging; two of them run the time-ordered value sums.
 // The arithmetic of every phase is the one of the multi-kernel path
-// (bit-identical GEMV order, exact softmax and time-ordered value sums).
+// (bit-identical GEMV order, RMSNorm sum tree, exact softmax and
+// time-ordered value sums).
 //
 // Every wait is bounded: a missing generation sets the error word and the
 // workgroup leaves, so a broken launch ends instead of hanging.
