@@ -1069,9 +1069,11 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     // Each phase: all threads quantise the gathered input, the compute waves
     // form the block products of their slice, then wave 0 sums the rows in
-    // order and publishes them while the memory waves gather the next
-    // phase's input and the compute waves load the slice of the phase after
-    // next.
+    // order and publishes them; after a barrier the memory waves gather the
+    // next phase's input and the compute waves load the slice of the phase
+    // after next. The barrier keeps the publication ahead of the slice's
+    // loads: behind the grid's weight burst a store took about a
+    // microsecond longer to reach the other workgroups.
     for (int l = 0; l < L; ++l) {
       const auto& Ly = LT[l];
       const auto& Nx = LT[l + 1 < L ? l + 1 : l];  // the last layer re-reads its own slices
@@ -1094,6 +1096,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stamps(e + 0, e + 2, e + 1, 1);
         if (tl && lane == 0) tl[e + 4] = t_sub[1];
       }
+      lds_barrier_p();
       if (ct >= 0)
         load_slot<NPG>(sa, Ly.wgu + (size_t)2 * rf.r0 * W, Ly.sgu + (size_t)2 * rf.r0 * B1, ct, 2 * rf.count * B1);
       gather_all(a.tatt, QW, gen(l, 2));
@@ -1112,6 +1115,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         stamps(e + 8, e + 9);
       }
+      lds_barrier_p();
       if (ct >= 0) load_slot<NPD>(sb, Ly.wd + (size_t)ro.r0 * FF, Ly.sd + (size_t)ro.r0 * Bf, ct, ro.count * Bf);
       gather_norm(a.ta, gen(l, 3), [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
       if (!gathered()) return;
@@ -1133,6 +1137,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         stamps(e + 10, e + 12, e + 11, 1);
       }
+      lds_barrier_p();
       if (ct >= 0) load_slot_rows<NPQ, B1>(sa, Nx.wqkv, Nx.sqkv, rq.r0, ct, max(rq.count, 1) * B1, qkv_row);
       gather_all(a.th, FF, gen(l, 4));
       if (!gathered()) return;
@@ -1152,6 +1157,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stamps(e + 13, e + 15, e + 14, 1);
         if (tl && lane == 0) tl[e + 5] = t_sub[1];
       }
+      lds_barrier_p();
       if (ct >= 0) load_slot<NPO>(sb, Nx.wo + (size_t)ro.r0 * QW, Nx.so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
       // Next layer's input with its attn_norm, or the lm_head input with output_norm.
       const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
