@@ -200,10 +200,12 @@ struct DecoderWeights {
   int64_t weight_bytes = 0;
   // Persistent kernel's per-layer pointer table (when the layout is the
   // persistent one) and the gate/up storage tiles: base rows, the first
-  // `extra` tiles one more.
+  // `extra` tiles one more, or (persistent layout) the storage row of every
+  // gate and up row in gu_map.
   bool persistent_layout = false;
   DeviceBuffer layer_table;
   int gu_base = 1, gu_extra = 0;
+  DeviceBuffer gu_map;
 };
 
 struct fah_decoder {
@@ -222,7 +224,7 @@ struct fah_decoder {
   // an instantiation and the device has the CUs for it.
   bool persistent = false;
   int blocks = 0;
-  DeviceBuffer tx, tqkv, tatt, ta, th, tkeys, epoch, error, timeline;
+  DeviceBuffer tx, tqkv, tatt, ta, th, tkeys, tattq, thq, epoch, error, timeline;
   fah::PersistentArgs pargs{};
   // Prefill (decode of many rows at once): row buffers grown on demand.
   DeviceBuffer pf_x, pf_a, pf_qkv, pf_q, pf_h, pf_xq, pf_xs;
@@ -397,6 +399,7 @@ void enqueue_layers(fah_decoder* d, hipStream_t s) {
       g.out_stride = c.ffn;
       g.split_base = d->wt->gu_base;
       g.split_extra = d->wt->gu_extra;
+      g.gu_map = d->wt->gu_map.as<int>();
       check(fah::launch_gemm_few(g, d->wt->half_scales, fah::kGemmSwiGLU, s), "gate/up gemm");
     } else {
       fah::GemvArgs gu = gemv_args(d->wt->gateup[l]);
@@ -490,6 +493,8 @@ void init_state(fah_decoder* d, hipStream_t s) {
     tagged(d->ta, k.width);
     tagged(d->th, k.ffn);
     tagged(d->tkeys, 2 * nb);
+    tagged(d->tattq, (size_t)fah::qwords(q_width));
+    tagged(d->thq, (size_t)fah::qwords(k.ffn));
     d->epoch.allocate(16);
     d->error.allocate(16);
     unsigned one = 1;
@@ -532,6 +537,8 @@ void init_state(fah_decoder* d, hipStream_t s) {
     a.ta = d->ta.as<unsigned long long>();
     a.th = d->th.as<unsigned long long>();
     a.tkeys = d->tkeys.as<unsigned long long>();
+    a.tattq = d->tattq.as<unsigned long long>();
+    a.thq = d->thq.as<unsigned long long>();
     a.x_in = d->x.as<float>();
     a.position = d->position.as<int>();
     a.token = d->token.as<int>();
@@ -591,6 +598,7 @@ void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_
       g.resid = resid;
       g.split_base = d->wt->gu_base;
       g.split_extra = d->wt->gu_extra;
+      g.gu_map = d->wt->gu_map.as<int>();
       if (fah::few_frame_groups(rows, m.cols, T, mode)) check(fah::launch_gemm_few(g, d->wt->half_scales, mode, s), "prefill gemm");
       else check(fah::launch_gemm(g, d->wt->half_scales, mode, s), "prefill gemm");
     };
@@ -781,6 +789,7 @@ void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s)
     g.resid = resid;
     g.split_base = w.gu_base;
     g.split_extra = w.gu_extra;
+    g.gu_map = w.gu_map.as<int>();
     g.keys = b.keys.as<unsigned long long>();
     if (fah::few_frame_groups(rows, m.cols, S, mode)) check(fah::launch_gemm_few(g, w.half_scales, mode, s), "session gemm");
     else check(fah::launch_gemm(g, w.half_scales, mode == fah::kGemmGreedy ? fah::kGemmPlain : mode, s), "session gemm");
@@ -1236,11 +1245,18 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
       d->wt->wo[l].group_rows = o_group;
       order.clear();
       if (d->persistent) {
-        const int base = k.ffn / ng, extra = k.ffn % ng;
-        for (int g = 0; g < ng; ++g) {
-          const int r0 = g * base + std::min(g, extra), count = base + (g < extra ? 1 : 0);
-          for (int r = 0; r < count; ++r) order.emplace_back(0, r0 + r);
-          for (int r = 0; r < count; ++r) order.emplace_back(1, r0 + r);
+        const int group = k.heads / k.kv_heads;
+        for (int x = 0; x < 8; ++x)
+          for (int j = 0; j < fah::persistent_xcd_roles(x, k.kv_heads, group, nb); ++j) {
+            const fah::FfnEntries f = fah::persistent_ffn_entries(x, j, k.ffn, k.kv_heads, group, nb);
+            for (int kind = 0; kind < 2; ++kind)
+              for (int e = f.r0; e < f.r0 + f.count; ++e) order.emplace_back(kind, fah::persistent_ffn_row(x, e));
+          }
+        if (l == 0) {
+          std::vector<int> map(2 * (size_t)k.ffn, -1);
+          for (size_t i = 0; i < order.size(); ++i) map[2 * (size_t)order[i].second + order[i].first] = (int)i;
+          for (int v : map) require(v >= 0, "gate/up layout covers every row");
+          upload(d->wt->gu_map, map.data(), map.size() * 4, s);
         }
       } else {
         int R = gu_group / 2;

@@ -87,6 +87,32 @@ struct PersistentLayer {
   const float* ffn_norm;
 };
 
+// Persistent decode, feed-forward rows. The 32-row block b of the ffn
+// activations belongs to XCD b % 8 (role w runs on XCD w % 8). XCD x's
+// ffn / 8 rows (its blocks in order: list entry e is row
+// 32 (x + 8 (e / 32)) + e % 32) are split evenly over its projection roles,
+// the first ones taking one more; role (x, j) stores its gate rows then its
+// up rows at storage row 2 (x ffn / 8 + first entry).
+struct FfnEntries {
+  int r0, count;
+};
+__host__ __device__ inline int persistent_xcd_roles(int x, int kv_heads, int group, int blocks) {
+  return blocks / 8 - (x < kv_heads ? group : 0);
+}
+__host__ __device__ inline FfnEntries persistent_ffn_entries(int x, int j, int ffn, int kv_heads, int group,
+                                                             int blocks) {
+  const int ex = ffn / 8, n = persistent_xcd_roles(x, kv_heads, group, blocks);
+  const int base = ex / n, extra = ex % n;
+  return {j * base + (j < extra ? j : extra), base + (j < extra ? 1 : 0)};
+}
+__host__ __device__ inline int persistent_ffn_row(int x, int e) { return 32 * (x + 8 * (e >> 5)) + (e & 31); }
+
+// A quantised vector in exchange form (K values, K / 32 Q8_0 blocks): tagged
+// words [0, K / 4) hold the packed int8 values (word 8b + k: values
+// 32b + 4k .. +3), words [K / 4, 9K / 32) the block scales, and the rest up
+// to qwords(K) (whole 128-word chunks) are padding that carries the tag only.
+__host__ __device__ constexpr int qwords(int K) { return (9 * (K / 32) + 127) / 128 * 128; }
+
 struct PersistentArgs {
   const PersistentLayer* layer_table;  // device array [layers]
   int layers;
@@ -106,6 +132,9 @@ struct PersistentArgs {
   int head_chunks;      // lm_head chunks of 32 rows
   int npre;             // K/V positions staged in LDS
   unsigned long long *tx, *tqkv, *tatt, *ta, *th, *tkeys;  // tagged exchange words
+  // Quantised exchanges (tagged words, qwords layout): the attention output
+  // for the o projection and the ffn activations for the down projection.
+  unsigned long long *tattq, *thq;
   const float* x_in;    // modes 0/1: the input row
   int mode;             // 0 layers, 1 layers + lm_head + greedy, 2 embed token + 1
   int* position;
@@ -138,6 +167,7 @@ struct GemmArgs {
   const float* resid;   // [frames][out_stride] (residual epilogue; may equal out)
   const float* bias;    // [rows] or null (plain epilogue)
   int split_base, split_extra;  // SwiGLU storage: tiles of base(+1) gate rows then the same up rows
+  const int* gu_map;            // or, when set, the SwiGLU storage row of row r: [2r] gate, [2r + 1] up
   // Greedy epilogue (few-frame kernel): the largest greedy key of each
   // workgroup's rows per frame, [frames][workgroups].
   unsigned long long* keys;

@@ -50,7 +50,10 @@ constexpr int kKvBytes = 121 * 1024;     // K/V staging: 512 B per position
 constexpr int kProbOffset = 4 * 128;     // attention probabilities after q/k/v in the tag area
 constexpr long kSpinLimit = 1L << 21;    // bounded polls per gather (~1-2 s)
 constexpr int kSentinelChunks = 0;       // gathers above this many 1 KB chunks poll a sentinel first
-constexpr int kPolls = 4;                // sentinel polls in flight
+// Sentinel polls in flight per gathering wave. Every consumer polls the same
+// few words, so deeper pipelines only lengthen the queue in front of them:
+// measured on the decode step, 1 beats 2, 4 and 8.
+constexpr int kPolls = 1;
 // s_waitcnt immediate for vmcnt <= kPolls - 1 (expcnt and lgkmcnt not
 // waited on): vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
 constexpr int kWaitOldestPoll = ((kPolls - 1) & 15) | (((kPolls - 1) >> 4) << 14) | (7 << 4) | (15 << 8);
@@ -164,9 +167,7 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
     locate(total - 1, src, off);
     // kPolls sentinel loads in flight, all into the chunk's own LDS place:
     // returns complete in order, so after waiting for the oldest the LDS copy
-    // is at least that new. Once the pipeline is full each iteration waits
-    // about a quarter round trip, so the data is seen at most that long
-    // after a poll could first have returned it.
+    // is at least that new.
     // Only the chunk's last 64 bytes (lanes 0-3) are polled: the polls of
     // every consumer together stay a small part of the memory traffic.
     for (int i = 0; i < kPolls - 1; ++i)
@@ -532,30 +533,113 @@ __device__ __forceinline__ float4 tag_float4(const u64* tag, int e) {
   return make_float4(u2f(a.x), u2f(a.z), u2f(b.x), u2f(b.z));
 }
 
-// Maximum over each aligned group of 16 lanes, in all 16 lanes.
-__device__ __forceinline__ uint32_t max16_u32(uint32_t m) {
+// Maximum over each aligned group of 8 lanes, in all 8 lanes.
+__device__ __forceinline__ uint32_t max8_u32(uint32_t m) {
   uint32_t o = dpp_u32<kDppQuadXor1>(m);
   m = o > m ? o : m;
   o = dpp_u32<kDppQuadXor2>(m);
   m = o > m ? o : m;
   o = dpp_u32<kDppHalfMirror>(m);
-  m = o > m ? o : m;
-  o = dpp_u32<kDppMirror>(m);
   return o > m ? o : m;
+}
+
+// Q8_0 quantisation (TensorMath.QuantizeAvx.cs:15-72) of four consecutive
+// values of a 32-value block whose eight lanes form an aligned group of 8
+// (all 64 lanes active): the block's absolute maximum over DPP, its scale
+// into *scale (every lane of the group) and the four int8 values packed
+// little-endian. The per-value arithmetic is quantize_value/block_scale's.
+__device__ __forceinline__ uint32_t quantize_lane4(float4 v, float* scale) {
+  const uint32_t a0 = f2u(v.x) & 0x7fffffffu, a1 = f2u(v.y) & 0x7fffffffu;
+  const uint32_t a2 = f2u(v.z) & 0x7fffffffu, a3 = f2u(v.w) & 0x7fffffffu;
+  const uint32_t m01 = a1 > a0 ? a1 : a0, m23 = a3 > a2 ? a3 : a2;
+  const uint32_t m = max8_u32(m23 > m01 ? m23 : m01);
+  float inv;
+  *scale = block_scale(m, &inv);
+  return (uint32_t)(uint8_t)quantize_value(v.x, inv) | ((uint32_t)(uint8_t)quantize_value(v.y, inv) << 8) |
+         ((uint32_t)(uint8_t)quantize_value(v.z, inv) << 16) | ((uint32_t)(uint8_t)quantize_value(v.w, inv) << 24);
+}
+
+// Q8_0 quantisation of act[0, K) into xq/xs, optionally RMS-scaled first
+// (x * inverse * w, RmsNorm's order), four values per thread.
+template <int K, bool NORM>
+__device__ __forceinline__ void quantize4(const u64* act, const float* norm_w, float inverse, int* xq, float* xs) {
+  static_assert(K % 256 == 0, "whole waves");
+  for (int i = threadIdx.x; i < K / 4; i += kPT) {  // wave-uniform
+    const int e = 4 * i;
+    float4 v = tag_float4(act, e);
+    if constexpr (NORM) {
+      const float4 w = *reinterpret_cast<const float4*>(norm_w + e);
+      v.x = fmul(fmul(v.x, inverse), w.x);
+      v.y = fmul(fmul(v.y, inverse), w.y);
+      v.z = fmul(fmul(v.z, inverse), w.z);
+      v.w = fmul(fmul(v.w, inverse), w.w);
+    }
+    float d;
+    xq[i] = (int)quantize_lane4(v, &d);
+    if ((i & 7) == 0) xs[e >> 5] = d;
+  }
+}
+
+// A gathered exchange-form vector into the products' xq/xs layout.
+template <int K>
+__device__ __forceinline__ void unpack_qvec(const u64* tag, int* xq, float* xs) {
+  constexpr int NBL = K / 32;
+  for (int i = threadIdx.x; i < 9 * NBL; i += kPT) {
+    const uint32_t v = (uint32_t)tag[i];
+    if (i < 8 * NBL) xq[i] = (int)v;
+    else xs[i - 8 * NBL] = u2f(v);
+  }
+}
+
+// One wave: wait for the 32 activations of block b of a K-value vector
+// (tagged words src[32b, +32), staged in blk), quantise them and publish the
+// block in exchange form at dst, with the padding words assigned to block b.
+// Two polls in flight, as gather_qkv. False after a timeout or another
+// workgroup's error.
+template <int K>
+__device__ bool publish_block(const u64* src, u64* dst, int b, uint32_t gen, u64* blk, unsigned* error,
+                              u64* seen = nullptr) {
+  const int lane = threadIdx.x & (kWave - 1);
+  constexpr int NBL = K / 32, PAD = qwords(K) - 9 * NBL, PER = (PAD + NBL - 1) / NBL;
+  static_assert(9 + PER <= kWave, "padding words per block");
+  const u64* at = src + 32 * b;
+  auto poll = [&] {
+    if (lane < 16) __builtin_amdgcn_global_load_lds(at + 2 * lane, (lds_ptr)blk, 16, 0, 16);
+  };
+  // s_waitcnt immediate: vmcnt <= 1 (the newer poll), expcnt/lgkmcnt not waited.
+  constexpr int kWaitOlderPoll = 1 | (7 << 4) | (15 << 8);
+  poll();
+  for (long spin = 0;; ++spin) {
+    poll();
+    __builtin_amdgcn_s_waitcnt(kWaitOlderPoll);
+    const uint4 t = lane < 16 ? *reinterpret_cast<const uint4*>(blk + 2 * lane) : make_uint4(0, gen, 0, gen);
+    if (__all(t.y == gen && t.w == gen)) break;
+    if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
+      if (lane == 0) __hip_atomic_fetch_or(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      return false;
+    }
+  }
+  if (seen) seen[0] = __builtin_amdgcn_s_memrealtime();
+  // Drained: the newer poll writes the same current words.
+  __builtin_amdgcn_s_waitcnt(0);
+  float d;
+  const uint32_t q = quantize_lane4(tag_float4(blk, 4 * (lane & 7)), &d);
+  if (lane < 8) tag_store_bits(dst + 8 * b + lane, gen, q);
+  else if (lane == 8) tag_store_bits(dst + 8 * NBL + b, gen, f2u(d));
+  else if (lane < 9 + PER && PER * b + (lane - 9) < PAD) tag_store_bits(dst + 9 * NBL + PER * b + (lane - 9), gen, 0u);
+  return true;
 }
 
 // RMSNorm (optional, weights in LDS) + activation quantisation of act[0, K)
 // into xq/xs, all threads. The square sum is the multi-kernel GEMV
 // prologue's: threads t < 256 hold values 4t + 1024g, each sums its squares
 // pairwise in order, then the wave trees and the four wave sums in order, so
-// the norm is bit-identical to that path. The scaling and quantisation run
-// on all 512 threads, two values each (values 2t + 1024g): sixteen
-// consecutive threads hold one 32-value block.
+// the norm is bit-identical to that path. The scaling and quantisation are
+// quantize4's.
 template <int K, bool NORM>
 __device__ __forceinline__ void quantize_input(const u64* act, const float* norm_w, float eps, int* xq, float* xs,
                                                double* red) {
-  static_assert(K % 128 == 0, "whole waves per group");
-  constexpr int G = (K + 2 * kPT - 1) / (2 * kPT);
   const int tid = threadIdx.x;
   float inverse = 1.0f;
   if constexpr (NORM) {
@@ -576,55 +660,10 @@ __device__ __forceinline__ void quantize_input(const u64* act, const float* norm
     const float mean = (float)(total / (double)K);
     inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
   }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const int e = 2 * tid + 2 * kPT * g;
-    if (e < K) {  // wave-uniform
-      const uint4 t = *reinterpret_cast<const uint4*>(act + e);
-      float v0 = u2f(t.x), v1 = u2f(t.z);
-      if (NORM) {
-        const float2 w = *reinterpret_cast<const float2*>(norm_w + e);
-        v0 = fmul(fmul(v0, inverse), w.x);
-        v1 = fmul(fmul(v1, inverse), w.y);
-      }
-      uint32_t m = f2u(v0) & 0x7fffffffu;
-      const uint32_t m1 = f2u(v1) & 0x7fffffffu;
-      m = max16_u32(m1 > m ? m1 : m);
-      float inv;
-      const float d = block_scale(m, &inv);
-      reinterpret_cast<uint16_t*>(xq)[e >> 1] =
-          (uint16_t)((uint32_t)(uint8_t)quantize_value(v0, inv) | ((uint32_t)(uint8_t)quantize_value(v1, inv) << 8));
-      if ((tid & 15) == 0) xs[e >> 5] = d;
-    }
-  }
+  quantize4<K, NORM>(act, norm_w, inverse, xq, xs);
 }
 
 }  // namespace
-
-// One wave quantises chunk k of a gathered vector (values 128k + 2 lane,
-// +1; sixteen lanes per 32-value block), with the RMSNorm scaling when NORM
-// (the same arithmetic as quantize_input).
-template <bool NORM>
-__device__ __forceinline__ void quantize_chunk(const u64* act, int k, const float* norm_w, float inverse, int* xq,
-                                               float* xs) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int e = 128 * k + 2 * lane;
-  const uint4 t = *reinterpret_cast<const uint4*>(act + e);
-  float v0 = u2f(t.x), v1 = u2f(t.z);
-  if (NORM) {
-    const float2 w = *reinterpret_cast<const float2*>(norm_w + e);
-    v0 = fmul(fmul(v0, inverse), w.x);
-    v1 = fmul(fmul(v1, inverse), w.y);
-  }
-  uint32_t m = f2u(v0) & 0x7fffffffu;
-  const uint32_t m1 = f2u(v1) & 0x7fffffffu;
-  m = max16_u32(m1 > m ? m1 : m);
-  float inv;
-  const float d = block_scale(m, &inv);
-  reinterpret_cast<uint16_t*>(xq)[e >> 1] =
-      (uint16_t)((uint32_t)(uint8_t)quantize_value(v0, inv) | ((uint32_t)(uint8_t)quantize_value(v1, inv) << 8));
-  if ((lane & 15) == 0) xs[e >> 5] = d;
-}
 
 // Memory wave m's part of the RMSNorm square sum of a K-value vector
 // (K <= 1024): threads t = 64m + lane of the GEMV prologue's tree hold values
@@ -642,7 +681,7 @@ __device__ __forceinline__ void norm_partial(const u64* act, int m, double* red)
 }
 
 // After the barrier that follows norm_partial: the inverse RMS from the four
-// wave sums in order, then one chunk per wave scaled and quantised.
+// wave sums in order, then the scaled vector quantised.
 template <int K>
 __device__ __forceinline__ void quantize_norm_chunks(const u64* act, const float* norm_w, float eps, const double* red,
                                                      int* xq, float* xs) {
@@ -651,7 +690,7 @@ __device__ __forceinline__ void quantize_norm_chunks(const u64* act, const float
   for (int i = 0; i < kMem / kWave; ++i) total += red[i];
   const float mean = (float)(total / (double)K);
   const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
-  for (int k = threadIdx.x / kWave; k < K / 128; k += kPT / kWave) quantize_chunk<true>(act, k, norm_w, inverse, xq, xs);
+  quantize4<K, true>(act, norm_w, inverse, xq, xs);
 }
 
 // Shape-specialised: W hidden width, HQ/HKV query/kv heads (head size 128),
@@ -670,7 +709,11 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int G = HQ / HKV, QL = (G + 2) * HS, NX = NB / 8 - G;
   static_assert(NB % 8 == 0 && HKV <= 8 && G >= 1 && HQ == G * HKV, "attention placement");
   // Largest per-workgroup slices (rows) and their (row, block) pairs.
-  constexpr int RQ = (QL + NX - 1) / NX, RO = (W + NG - 1) / NG, RGU = (FF + NG - 1) / NG;
+  constexpr int RQ = (QL + NX - 1) / NX, RO = (W + NG - 1) / NG, RGU = (FF / 8 + NX - 1) / NX;
+  // Quantised exchanges: attention output and ffn activations.
+  constexpr int QWA = qwords(QW), QWH = qwords(FF);
+  static_assert(FF % 256 == 0 && RGU < 32 && QWA <= kTagWords && QWH <= kTagWords,
+                "ffn blocks per XCD, one block per owner, gather area");
   constexpr int NPQ = RQ * B1, NPO = RO * Bq, NPG = 2 * RGU * B1, NPD = RO * Bf;
   constexpr int PA = (NPQ > NPG ? NPQ : NPG) / kComp + 1;  // slot A: qkv, gate/up
   constexpr int PB = (NPO > NPD ? NPO : NPD) / kComp + 1;  // slot B: o, down
@@ -954,6 +997,19 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       mark(e + 10);
       lds_barrier_p();
       if (wave == 0) {
+        // The head's four 32-value blocks quantised for the o projection:
+        // lanes 0-31 the packed values (block 4 hq + lane / 8), lanes 32-35
+        // the scales, later lanes this head's share of the padding words.
+        constexpr int NBA = QW / 32, PADA = QWA - 9 * NBA, PERA = (PADA + HQ - 1) / HQ;
+        static_assert(HS == 128 && PERA <= kWave - 36, "padding words per head");
+        float d;
+        const uint32_t q = quantize_lane4(*reinterpret_cast<const float4*>(&cur_s[0][4 * (lane & 31)]), &d);
+        const float dsc = __shfl(d, 8 * (lane & 3), kWave);
+        if (lane < 32) tag_store_bits(a.tattq + 32 * hq + lane, gen(l, 2), q);
+        else if (lane < 36) tag_store_bits(a.tattq + 8 * NBA + 4 * hq + (lane - 32), gen(l, 2), f2u(dsc));
+        else if (lane - 36 < PERA && PERA * hq + (lane - 36) < PADA)
+          tag_store_bits(a.tattq + 9 * NBA + PERA * hq + (lane - 36), gen(l, 2), 0u);
+        // The output values themselves, for tracing.
         tag_store(a.tatt + hq * HS + lane, gen(l, 2), cur_s[0][lane]);
         tag_store(a.tatt + hq * HS + kWave + lane, gen(l, 2), cur_s[0][kWave + lane]);
         if ((w >> 3) == 0) {
@@ -984,7 +1040,18 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     int g = w;
 #pragma unroll
     for (int s8 = 0; s8 < G; ++s8) g -= min(max(w - 8 * s8, 0), HKV);
-    const Rows ro = split_rows<W, NG>(g), rf = split_rows<FF, NG>(g);
+    const Rows ro = split_rows<W, NG>(g);
+    // ffn rows: entries of this XCD's list (persistent_ffn_entries), the
+    // gate/up tile's storage row, and the 32-row block this role quantises
+    // and publishes (the one whose entry 16 it computes), if any.
+    const int fx = w & 7;
+    const FfnEntries rf = persistent_ffn_entries(fx, (w >> 3) - (fx < HKV ? G : 0), FF, HKV, G, NB);
+    const size_t rf_store = 2 * (size_t)(fx * (FF / 8) + rf.r0);
+    int own = -1;
+    {
+      const int k = (rf.r0 + rf.count - 17) >> 5;
+      if (rf.count > 0 && k >= 0 && 32 * k + 16 >= rf.r0) own = fx + 8 * k;
+    }
     // q/k/v: this XCD's kv head; none on XCDs past the kv heads, whose
     // (unused, clamped) slice loads then read kv head 0's rows.
     const int xk = (w & 7) < HKV ? (w & 7) : 0;
@@ -1098,12 +1165,12 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       lds_barrier_p();
       if (ct >= 0)
-        load_slot<NPG>(sa, Ly.wgu + (size_t)2 * rf.r0 * W, Ly.sgu + (size_t)2 * rf.r0 * B1, ct, 2 * rf.count * B1);
-      gather_all(a.tatt, QW, gen(l, 2));
+        load_slot<NPG>(sa, Ly.wgu + rf_store * W, Ly.sgu + rf_store * B1, ct, 2 * rf.count * B1);
+      gather_all(a.tattq, QWA, gen(l, 2));
       if (!gathered()) return;
 
       // ---- P3: o projection + residual -------------------------------------
-      quantize_input<QW, false>(tag_s, nullptr, 0.0f, xq_s, xs_s, red_s);
+      unpack_qvec<QW>(tag_s, xq_s, xs_s);
       lds_barrier_p();
       if (ct >= 0) slot_products<NPO, Bq>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bq);
       lds_barrier_p();
@@ -1133,17 +1200,34 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const float u = __shfl(gs, lane + nr, kWave);
         if (lane < nr) {
           const float silu = fdiv(gs, fadd(1.0f, exp_ref(-gs)));
-          tag_store(a.th + rf.r0 + lane, gen(l, 4), fmul(silu, u));
+          u64* dst = a.th + persistent_ffn_row(fx, rf.r0 + lane);
+          if (a.local_l2) tag_store_local(dst, gen(l, 4), fmul(silu, u));
+          else tag_store(dst, gen(l, 4), fmul(silu, u));
         }
         stamps(e + 10, e + 12, e + 11, 1);
       }
       lds_barrier_p();
       if (ct >= 0) load_slot_rows<NPQ, B1>(sa, Nx.wqkv, Nx.sqkv, rq.r0, ct, max(rq.count, 1) * B1, qkv_row);
-      gather_all(a.th, FF, gen(l, 4));
+      // The block owners quantise their blocks (read through this XCD's L2)
+      // and publish them; every projection workgroup gathers the quantised
+      // vector.
+      if (ct < 0) {
+        bool ok = true;
+        if (wave == 0 && own >= 0) {
+          u64 seen = 0;
+          ok = publish_block<FF>(a.th, a.thq, own, gen(l, 4), tag_s + kTagWords - 32, a.error, &seen);
+          if (tl && lane == 0) {
+            tl[e + 6] = seen;
+            tl[e + 7] = __builtin_amdgcn_s_memrealtime();
+          }
+        }
+        if (ok) ok = gather(a.thq, QWH, 0, nullptr, 0, 0, nullptr, 0, 0, gen(l, 4), tag_s, a.error, NoPre{}, wave, 4);
+        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      }
       if (!gathered()) return;
 
       // ---- P5: down projection + residual ------------------------------------
-      quantize_input<FF, false>(tag_s, nullptr, 0.0f, xq_s, xs_s, red_s);
+      unpack_qvec<FF>(tag_s, xq_s, xs_s);
       lds_barrier_p();
       sub(0);
       if (ct >= 0) slot_products<NPD, Bf>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bf);

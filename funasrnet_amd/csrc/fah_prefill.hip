@@ -70,7 +70,8 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
   auto storage_row = [&](int tr) -> int {
     if (kSwiGLU) {
       const int r = row0 + (tr & 31);
-      return r < g.rows ? gate_up_row(r, tr >> 5, g.split_base, g.split_extra) : -1;
+      if (r >= g.rows) return -1;
+      return g.gu_map ? g.gu_map[2 * r + (tr >> 5)] : gate_up_row(r, tr >> 5, g.split_base, g.split_extra);
     }
     const int r = row0 + tr;
     return r < g.rows ? r : -1;
@@ -438,7 +439,8 @@ __global__ __launch_bounds__(kFewThreads) void q8_gemm_few_kernel(GemmArgs g, in
   auto storage_row = [&](int i) -> int {
     if (kSwiGLU) {
       const int p = r0 + (i < R ? i : i - R);
-      return p < g.rows ? gate_up_row(p, i < R ? 0 : 1, g.split_base, g.split_extra) : -1;
+      if (p >= g.rows) return -1;
+      return g.gu_map ? g.gu_map[2 * p + (i < R ? 0 : 1)] : gate_up_row(p, i < R ? 0 : 1, g.split_base, g.split_extra);
     }
     const int r = r0 + i;
     return r < g.rows ? r : -1;
@@ -811,7 +813,7 @@ hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t
   // The row and frame scales of the whole K range live in LDS (512 B per
   // block): K <= 3072 keeps the tile, with the SwiGLU exchange, under 64 KiB.
   if (g.K % 128 != 0 || g.K > 3072 || g.rows < 1 || g.frames < 1) return hipErrorInvalidValue;
-  if (out == kGemmSwiGLU && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
+  if (out == kGemmSwiGLU && !g.gu_map && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
   return half_scales ? launch_gemm_scaled<ScaleF16>(g, out, s) : launch_gemm_scaled<ScaleF32>(g, out, s);
 }
 
@@ -860,7 +862,7 @@ static hipError_t launch_few_scaled(const GemmArgs& g, int out, hipStream_t s) {
 
 hipError_t launch_gemm_few(const GemmArgs& g, bool half_scales, int out, hipStream_t s) {
   if (!few_frame_groups(g.rows, g.K, g.frames, out)) return hipErrorInvalidValue;
-  if (out == kGemmSwiGLU && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
+  if (out == kGemmSwiGLU && !g.gu_map && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
   if (out == kGemmGreedy && !g.keys) return hipErrorInvalidValue;
   return half_scales ? launch_few_scaled<ScaleF16>(g, out, s) : launch_few_scaled<ScaleF32>(g, out, s);
 }
