@@ -493,6 +493,56 @@ __device__ __forceinline__ void slot_products(const Slot<P>& sl, int ct, const i
   }
 }
 
+// Compute lanes: copy a weight slice of `rows` storage rows (K int8 each,
+// storage row row(r) for slice row r) and then their K / 32 F16 scales into
+// LDS at dst, by direct global->LDS loads of 16-byte pieces, R rounds of
+// kComp pieces: piece p of the slice lands at dst + 16 p. Pieces past the
+// slice re-read its first one into the unused tail (dst holds R rounds).
+template <int K, int R, class RowMap>
+__device__ __forceinline__ void stage_slice(char* dst, const int8_t* w, const _Float16* s, int rows, int ct,
+                                            RowMap row) {
+  static_assert(K % 256 == 0, "whole 16-byte pieces of weights and scales");
+  constexpr int PW = K / 16, PS = K / 256;  // pieces per row: weights, scales
+  const int nw = rows * PW, n = nw + rows * PS;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int p = kComp * k + ct;
+    const char* src;
+    if (p < nw) {
+      const int r = p / PW;
+      src = reinterpret_cast<const char*>(w + (size_t)row(r) * K) + 16 * (p - r * PW);
+    } else if (p < n) {
+      const int q = p - nw, r = q / PS;
+      src = reinterpret_cast<const char*>(s + (size_t)row(r) * (K / 32)) + 16 * (q - r * PS);
+    } else {
+      src = reinterpret_cast<const char*>(w + (size_t)row(0) * K);
+    }
+    __builtin_amdgcn_global_load_lds(src, (lds_ptr)(dst + 16 * (kComp * k + (ct & ~(kWave - 1)))), 16, 0, 0);
+  }
+}
+
+// Rounds of stage_slice for slices of up to `rows` rows of K weights.
+__host__ __device__ constexpr int stage_rounds(int rows, int K) { return (rows * (K / 16 + K / 256) + kComp - 1) / kComp; }
+
+// slot_products for a slice staged in LDS by stage_slice (`rows` rows).
+template <int NP, int B>
+__device__ __forceinline__ void lds_products(const char* sl, int rows, int ct, const int* xq, const float* xs,
+                                             float* prod) {
+  constexpr int K = 32 * B, kI = (NP + kComp - 1) / kComp;
+  const int valid = rows * B;
+  const _Float16* sc = reinterpret_cast<const _Float16*>(sl + (size_t)rows * K);
+#pragma unroll
+  for (int i = 0; i < kI; ++i) {
+    const int j = ct + i * kComp;
+    if (j < valid) {
+      const int r = j / B, b = j - r * B;
+      const int4* wp = reinterpret_cast<const int4*>(sl + (size_t)r * K + 32 * b);
+      const int d = dot32(wp[0], wp[1], xq + b * 8);
+      prod[r * (B + 4) + b] = fmul(fmul((float)d, (float)sc[j]), xs[b]);
+    }
+  }
+}
+
 // Rows [r0, r0 + count) of R rows split as evenly as possible over NG
 // workgroups (the first R % NG take one more).
 struct Rows {
@@ -715,11 +765,14 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   static_assert(FF % 256 == 0 && RGU < 32 && QWA <= kTagWords && QWH <= kTagWords,
                 "ffn blocks per XCD, one block per owner, gather area");
   constexpr int NPQ = RQ * B1, NPO = RO * Bq, NPG = 2 * RGU * B1, NPD = RO * Bf;
-  constexpr int PA = (NPQ > NPG ? NPQ : NPG) / kComp + 1;  // slot A: qkv, gate/up
-  constexpr int PB = (NPO > NPD ? NPO : NPD) / kComp + 1;  // slot B: o, down
+  // Projection workgroups stage their weight slices in the K/V area: q/k/v,
+  // o, gate/up and down at these byte offsets, each a whole number of rounds.
+  constexpr int SQ = stage_rounds(RQ, W), SO = stage_rounds(RO, QW), SG = stage_rounds(2 * RGU, W),
+                SD = stage_rounds(RO, FF);
+  constexpr int OQ = 0, OO = OQ + SQ * kComp * 16, OG = OO + SO * kComp * 16, OD = OG + SG * kComp * 16;
+  static_assert(OD + SD * kComp * 16 <= kKvBytes, "staged slices fit the K/V area");
   constexpr int NPH = kSlotPairs * kComp, HR = NPH / B1;  // lm_head: pairs and rows per chunk
   static_assert(RQ <= 64 && 2 * RGU <= 64 && RO <= 64 && HR <= 64 && HR * B1 == NPH, "row lanes");
-  static_assert(PA <= 5 && PB <= 4, "slot registers");
   static_assert(FF <= kActFloats && QW <= kActFloats && W <= 1024 && RQ * (B1 + 4) <= kProdFloats &&
                     2 * RGU * (B1 + 4) <= kProdFloats && RO * (Bq + 4) <= kProdFloats && RO * (Bf + 4) <= kProdFloats,
                 "LDS sizing");
@@ -1060,8 +1113,24 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       return r < G * HS ? G * HS * xk + r
                         : (r < (G + 1) * HS ? QW + HS * xk + (r - G * HS) : QW + KVW + HS * xk + (r - (G + 1) * HS));
     };
-    Slot<PA> sa;
-    Slot<PB> sb;
+    auto qkv_at = [&](int r) { return qkv_row(rq.r0 + r); };
+    auto o_at = [&](int r) { return ro.r0 + r; };  // o and down rows
+    auto gu_at = [&](int r) { return (int)rf_store + r; };
+    // Compute lanes, after the q/k/v publication of layer l: the slices of
+    // layer l's o, gate/up and down and of layer l + 1's q/k/v, staged while
+    // the attention runs (nothing else then reads weights), so that no
+    // weight stream competes with the exchanges of the later phases.
+    auto stage_window = [&](int l) {
+      const auto& Ly = LT[l];
+      // The piece addresses are recomputed here each layer rather than kept
+      // in registers across the loop.
+      int cl = ct;
+      asm volatile("" : "+v"(cl));
+      stage_slice<QW, SO>(kv_s + OO, Ly.wo, Ly.so, ro.count, cl, o_at);
+      stage_slice<W, SG>(kv_s + OG, Ly.wgu, Ly.sgu, 2 * rf.count, cl, gu_at);
+      stage_slice<FF, SD>(kv_s + OD, Ly.wd, Ly.sd, ro.count, cl, o_at);
+      if (l + 1 < L) stage_slice<W, SQ>(kv_s + OQ, LT[l + 1].wqkv, LT[l + 1].sqkv, rq.count, cl, qkv_at);
+    };
     // Layer-0 input: a host row or the embedding of the device token
     // (QwenDecoder.Embed, Gguf.cs:340-344). Its loads go first so that they
     // do not wait behind the weight slices.
@@ -1083,10 +1152,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int k = 0; k < XI; ++k) xr[k] = a.x_in[tid + k * kPT];
     }
     if (ct >= 0) {
-      load_slot_rows<NPQ, B1>(sa, LT[0].wqkv, LT[0].sqkv, rq.r0, ct, max(rq.count, 1) * B1, qkv_row);
-      // Keep the two slices in issue order: the waits count on it.
-      __builtin_amdgcn_sched_barrier(0);
-      load_slot<NPO>(sb, LT[0].wo + (size_t)ro.r0 * QW, LT[0].so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
+      stage_slice<W, SQ>(kv_s + OQ, LT[0].wqkv, LT[0].sqkv, rq.count, ct, qkv_at);
     } else if (wave == 0) {
       dma(LT[0].attn_norm, norm_s, W * 4);
       __builtin_amdgcn_s_waitcnt(0);
@@ -1148,9 +1214,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // ---- P1: attn_norm + qkv ----------------------------------------------
       if (tid < ro.count) row_s[0][tid] = tag_value(tag_s, ro.r0 + tid);
       quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
+      if (ct >= 0 && l == 0) __builtin_amdgcn_s_waitcnt(0);  // layer 0's staged q/k/v slice
       lds_barrier_p();
       sub(0);
-      if (ct >= 0) slot_products<NPQ, B1>(sa, ct, xq_s, xs_s, prod_s, rq.count * B1);
+      if (ct >= 0) lds_products<NPQ, B1>(kv_s + OQ, rq.count, ct, xq_s, xs_s, prod_s);
       lds_barrier_p();
       sub(1);
       if (wave == 0) {
@@ -1164,15 +1231,15 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (tl && lane == 0) tl[e + 4] = t_sub[1];
       }
       lds_barrier_p();
-      if (ct >= 0)
-        load_slot<NPG>(sa, Ly.wgu + rf_store * W, Ly.sgu + rf_store * B1, ct, 2 * rf.count * B1);
+      if (ct >= 0) stage_window(l);
       gather_all(a.tattq, QWA, gen(l, 2));
+      if (ct >= 0) __builtin_amdgcn_s_waitcnt(0);  // the staged slices are in LDS before the barrier
       if (!gathered()) return;
 
       // ---- P3: o projection + residual -------------------------------------
       unpack_qvec<QW>(tag_s, xq_s, xs_s);
       lds_barrier_p();
-      if (ct >= 0) slot_products<NPO, Bq>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bq);
+      if (ct >= 0) lds_products<NPO, Bq>(kv_s + OO, ro.count, ct, xq_s, xs_s, prod_s);
       lds_barrier_p();
       if (wave == 0) {
         if (lane < ro.count) {
@@ -1182,8 +1249,6 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         stamps(e + 8, e + 9);
       }
-      lds_barrier_p();
-      if (ct >= 0) load_slot<NPD>(sb, Ly.wd + (size_t)ro.r0 * FF, Ly.sd + (size_t)ro.r0 * Bf, ct, ro.count * Bf);
       gather_norm(a.ta, gen(l, 3), [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
       if (!gathered()) return;
 
@@ -1191,7 +1256,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
       lds_barrier_p();
       sub(0);
-      if (ct >= 0) slot_products<NPG, B1>(sa, ct, xq_s, xs_s, prod_s, 2 * rf.count * B1);
+      if (ct >= 0) lds_products<NPG, B1>(kv_s + OG, 2 * rf.count, ct, xq_s, xs_s, prod_s);
       lds_barrier_p();
       if (wave == 0) {
         // Lanes [0, n) sum the gate rows, [n, 2n) the matching up rows.
@@ -1206,8 +1271,6 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         stamps(e + 10, e + 12, e + 11, 1);
       }
-      lds_barrier_p();
-      if (ct >= 0) load_slot_rows<NPQ, B1>(sa, Nx.wqkv, Nx.sqkv, rq.r0, ct, max(rq.count, 1) * B1, qkv_row);
       // The block owners quantise their blocks (read through this XCD's L2)
       // and publish them; every projection workgroup gathers the quantised
       // vector.
@@ -1230,7 +1293,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       unpack_qvec<FF>(tag_s, xq_s, xs_s);
       lds_barrier_p();
       sub(0);
-      if (ct >= 0) slot_products<NPD, Bf>(sb, ct, xq_s, xs_s, prod_s, ro.count * Bf);
+      if (ct >= 0) lds_products<NPD, Bf>(kv_s + OD, ro.count, ct, xq_s, xs_s, prod_s);
       lds_barrier_p();
       sub(1);
       if (wave == 0) {
@@ -1241,8 +1304,6 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stamps(e + 13, e + 15, e + 14, 1);
         if (tl && lane == 0) tl[e + 5] = t_sub[1];
       }
-      lds_barrier_p();
-      if (ct >= 0) load_slot<NPO>(sb, Nx.wo + (size_t)ro.r0 * QW, Nx.so + (size_t)ro.r0 * Bq, ct, ro.count * Bq);
       // Next layer's input with its attn_norm, or the lm_head input with output_norm.
       const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
       gather_norm(a.tx, gen(l, 5), [&] { dma(next_norm, norm_s, W * 4); });
