@@ -493,8 +493,8 @@ void init_state(fah_decoder* d, hipStream_t s) {
     tagged(d->ta, k.width);
     tagged(d->th, k.ffn);
     tagged(d->tkeys, 2 * nb);
-    tagged(d->tattq, (size_t)fah::qwords(q_width));
-    tagged(d->thq, (size_t)fah::qwords(k.ffn));
+    tagged(d->tattq, (size_t)fah::qblock_words(q_width));
+    tagged(d->thq, (size_t)fah::qblock_words(k.ffn));
     d->epoch.allocate(16);
     d->error.allocate(16);
     unsigned one = 1;
@@ -1248,9 +1248,9 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
         const int group = k.heads / k.kv_heads;
         for (int x = 0; x < 8; ++x)
           for (int j = 0; j < fah::persistent_xcd_roles(x, k.kv_heads, group, nb); ++j) {
-            const fah::FfnEntries f = fah::persistent_ffn_entries(x, j, k.ffn, k.kv_heads, group, nb);
+            const fah::XcdEntries f = fah::persistent_xcd_entries(x, j, k.ffn, k.kv_heads, group, nb);
             for (int kind = 0; kind < 2; ++kind)
-              for (int e = f.r0; e < f.r0 + f.count; ++e) order.emplace_back(kind, fah::persistent_ffn_row(x, e));
+              for (int e = f.r0; e < f.r0 + f.count; ++e) order.emplace_back(kind, fah::persistent_xcd_row(x, e, 64));
           }
         if (l == 0) {
           std::vector<int> map(2 * (size_t)k.ffn, -1);

@@ -87,31 +87,38 @@ struct PersistentLayer {
   const float* ffn_norm;
 };
 
-// Persistent decode, feed-forward rows. The 32-row block b of the ffn
-// activations belongs to XCD b % 8 (role w runs on XCD w % 8). XCD x's
-// ffn / 8 rows (its blocks in order: list entry e is row
-// 32 (x + 8 (e / 32)) + e % 32) are split evenly over its projection roles,
-// the first ones taking one more; role (x, j) stores its gate rows then its
+// Persistent decode, row ownership by XCD. A vector of `rows` rows is cut
+// into blocks of `block` rows; block b belongs to XCD b % 8 (role w runs on
+// XCD w % 8). XCD x's rows / 8 rows (its blocks in order: list entry e is
+// row block (x + 8 (e / block)) + e % block) are split evenly over its
+// projection roles, the first ones taking one more. The ffn rows use 64-row
+// blocks (pairs of Q8_0 blocks): role (x, j) stores its gate rows then its
 // up rows at storage row 2 (x ffn / 8 + first entry).
-struct FfnEntries {
+struct XcdEntries {
   int r0, count;
 };
 __host__ __device__ inline int persistent_xcd_roles(int x, int kv_heads, int group, int blocks) {
   return blocks / 8 - (x < kv_heads ? group : 0);
 }
-__host__ __device__ inline FfnEntries persistent_ffn_entries(int x, int j, int ffn, int kv_heads, int group,
+__host__ __device__ inline XcdEntries persistent_xcd_entries(int x, int j, int rows, int kv_heads, int group,
                                                              int blocks) {
-  const int ex = ffn / 8, n = persistent_xcd_roles(x, kv_heads, group, blocks);
+  const int ex = rows / 8, n = persistent_xcd_roles(x, kv_heads, group, blocks);
   const int base = ex / n, extra = ex % n;
   return {j * base + (j < extra ? j : extra), base + (j < extra ? 1 : 0)};
 }
-__host__ __device__ inline int persistent_ffn_row(int x, int e) { return 32 * (x + 8 * (e >> 5)) + (e & 31); }
+__host__ __device__ inline int persistent_xcd_row(int x, int e, int block) {
+  return block * (x + 8 * (e / block)) + e % block;
+}
 
-// A quantised vector in exchange form (K values, K / 32 Q8_0 blocks): tagged
-// words [0, K / 4) hold the packed int8 values (word 8b + k: values
-// 32b + 4k .. +3), words [K / 4, 9K / 32) the block scales, and the rest up
-// to qwords(K) (whole 128-word chunks) are padding that carries the tag only.
-__host__ __device__ constexpr int qwords(int K) { return (9 * (K / 32) + 127) / 128 * 128; }
+// A quantised vector in exchange form (K values, K / 32 Q8_0 blocks): eight
+// 64-bit words per block, word 8b + k holding the packed int8 values
+// 32b + 4k .. +3 in its low half and, in its high half, a 16-bit tag above
+// 16 side bits, which carry the low and high halves of block b's float
+// scale in words 8b and 8b + 1. K / 4 words in all. Every 128-byte line has
+// a single writer (the ffn owners publish two blocks, the attention
+// workgroups four): such lines reach the other XCDs far sooner than lines
+// that several workgroups write parts of.
+__host__ __device__ constexpr int qblock_words(int K) { return K / 4; }
 
 struct PersistentArgs {
   const PersistentLayer* layer_table;  // device array [layers]
@@ -132,7 +139,7 @@ struct PersistentArgs {
   int head_chunks;      // lm_head chunks of 32 rows
   int npre;             // K/V positions staged in LDS
   unsigned long long *tx, *tqkv, *tatt, *ta, *th, *tkeys;  // tagged exchange words
-  // Quantised exchanges (tagged words, qwords layout): the attention output
+  // Quantised exchanges (qblock_words layout): the attention output
   // for the o projection and the ffn activations for the down projection.
   unsigned long long *tattq, *thq;
   const float* x_in;    // modes 0/1: the input row

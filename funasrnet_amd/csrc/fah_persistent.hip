@@ -49,7 +49,10 @@ constexpr int kProdFloats = 1024;        // (row, block) products of one phase
 constexpr int kKvBytes = 121 * 1024;     // K/V staging: 512 B per position
 constexpr int kProbOffset = 4 * 128;     // attention probabilities after q/k/v in the tag area
 constexpr long kSpinLimit = 1L << 21;    // bounded polls per gather (~1-2 s)
-constexpr int kSentinelChunks = 0;       // gathers above this many 1 KB chunks poll a sentinel first
+// A wave polls a sentinel first when its part of a gather has more than this
+// many 1 KB chunks; a part of one chunk is polled whole (one round trip
+// sooner, and little enough traffic).
+constexpr int kSentinelChunks = 1;
 // Sentinel polls in flight per gathering wave. Every consumer polls the same
 // few words, so deeper pipelines only lengthen the queue in front of them:
 // measured on the decode step, 1 beats 2, 4 and 8.
@@ -138,7 +141,7 @@ struct NoChunk {
 template <class Pre, class OnChunk = NoChunk>
 __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int o1, const u64* s2, int n2, int o2,
                        uint32_t gen, u64* tag, unsigned* error, Pre pre, int part = 0, int parts = 1,
-                       OnChunk on_chunk = OnChunk{}, u64* seen = nullptr) {
+                       OnChunk on_chunk = OnChunk{}, u64* seen = nullptr, uint32_t tmask = ~0u) {
   const int lane = threadIdx.x & (kWave - 1);
   pre();
   const int c0 = n0 >> 7, c01 = c0 + (n1 >> 7), all = c01 + (n2 >> 7);
@@ -161,7 +164,7 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
   // Poll the end of the last chunk until it is current before reading them
   // all (that chunk too), so that consumers that arrive early cost one small
   // load per round trip instead of the whole vector.
-  if (total > kSentinelChunks) {
+  if (total - first > kSentinelChunks) {
     const u64* src;
     int off;
     locate(total - 1, src, off);
@@ -176,7 +179,7 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
       if (lane < 4) __builtin_amdgcn_global_load_lds(src + 120 + 2 * lane, (lds_ptr)(tag + off + 120), 16, 0, 16);
       __builtin_amdgcn_s_waitcnt(kWaitOldestPoll);
       const uint4 t = lane < 4 ? *reinterpret_cast<const uint4*>(tag + off + 120 + 2 * lane) : make_uint4(0, gen, 0, gen);
-      if (__all(t.y == gen && t.w == gen)) {
+      if (__all((t.y & tmask) == gen && (t.w & tmask) == gen)) {
         if (seen) seen[0] = __builtin_amdgcn_s_memrealtime();
         break;
       }
@@ -209,7 +212,7 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
       int off;
       locate(k, src, off);
       const uint4 t = *reinterpret_cast<const uint4*>(tag + off + 2 * lane);
-      if (__all(t.y == gen && t.w == gen)) {
+      if (__all((t.y & tmask) == gen && (t.w & tmask) == gen)) {
         pending &= ~(1ull << k);
         on_chunk(k);
       }
@@ -317,14 +320,21 @@ __device__ __forceinline__ void value_chain(const char* kv, const char* ovf, con
         pq[k] = make_float4(v.x, v.y, v.z, v.w);
       }
     };
+    // The sixteen products first, then the in-order adds: each add then
+    // finds its product long finished instead of waiting for the mixed
+    // multiply issued just before it.
     auto add16 = [&](const uint32_t* v, const float4* pq) {
+      float m[16];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        acc = fadd(acc, mulh(pq[k].x, half(v[4 * k])));
-        acc = fadd(acc, mulh(pq[k].y, half(v[4 * k + 1])));
-        acc = fadd(acc, mulh(pq[k].z, half(v[4 * k + 2])));
-        acc = fadd(acc, mulh(pq[k].w, half(v[4 * k + 3])));
+        m[4 * k] = mulh(pq[k].x, half(v[4 * k]));
+        m[4 * k + 1] = mulh(pq[k].y, half(v[4 * k + 1]));
+        m[4 * k + 2] = mulh(pq[k].z, half(v[4 * k + 2]));
+        m[4 * k + 3] = mulh(pq[k].w, half(v[4 * k + 3]));
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc = fadd(acc, m[k]);
     };
     if (i + 16 <= count) {
       uint32_t va[16], vb[16];
@@ -630,31 +640,38 @@ __device__ __forceinline__ void quantize4(const u64* act, const float* norm_w, f
   }
 }
 
-// A gathered exchange-form vector into the products' xq/xs layout.
+// Quantised-exchange words (qblock_words layout): 16-bit tag and 16 side
+// bits above the 32-bit payload; tags are compared under kQTagMask.
+constexpr uint32_t kQTagMask = 0xFFFF0000u;
+__device__ __forceinline__ uint32_t qtag(uint32_t gen) { return gen << 16; }
+__device__ __forceinline__ void qword_store(u64* p, uint32_t gen, uint32_t side, uint32_t payload) {
+  __hip_atomic_store(p, ((u64)(qtag(gen) | (side & 0xFFFFu)) << 32) | (u64)payload, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+// The side bits of word k of a block whose scale is d: the scale's low half
+// in word 0, its high half in word 1.
+__device__ __forceinline__ uint32_t qside(int k, float d) {
+  return k == 0 ? (f2u(d) & 0xFFFFu) : (k == 1 ? f2u(d) >> 16 : 0u);
+}
+
+// A gathered quantised vector into the products' xq/xs layout.
 template <int K>
-__device__ __forceinline__ void unpack_qvec(const u64* tag, int* xq, float* xs) {
-  constexpr int NBL = K / 32;
-  for (int i = threadIdx.x; i < 9 * NBL; i += kPT) {
-    const uint32_t v = (uint32_t)tag[i];
-    if (i < 8 * NBL) xq[i] = (int)v;
-    else xs[i - 8 * NBL] = u2f(v);
+__device__ __forceinline__ void unpack_qblocks(const u64* tag, int* xq, float* xs) {
+  for (int i = threadIdx.x; i < K / 4; i += kPT) {
+    xq[i] = (int)(uint32_t)tag[i];
+    if ((i & 7) == 0) xs[i >> 3] = u2f(((uint32_t)(tag[i] >> 32) & 0xFFFFu) | ((uint32_t)(tag[i + 1] >> 32) << 16));
   }
 }
 
-// One wave: wait for the 32 activations of block b of a K-value vector
-// (tagged words src[32b, +32), staged in blk), quantise them and publish the
-// block in exchange form at dst, with the padding words assigned to block b.
-// Two polls in flight, as gather_qkv. False after a timeout or another
-// workgroup's error.
-template <int K>
-__device__ bool publish_block(const u64* src, u64* dst, int b, uint32_t gen, u64* blk, unsigned* error,
-                              u64* seen = nullptr) {
+// One wave: poll the NW tagged words at[0, NW) (written through this XCD's
+// L2 or to memory) into blk until all carry `gen`, two polls in flight as
+// gather_qkv. False after a timeout or another workgroup's error.
+template <int NW>
+__device__ bool poll_words(const u64* at, uint32_t gen, u64* blk, unsigned* error, u64* seen, uint32_t tmask = ~0u) {
   const int lane = threadIdx.x & (kWave - 1);
-  constexpr int NBL = K / 32, PAD = qwords(K) - 9 * NBL, PER = (PAD + NBL - 1) / NBL;
-  static_assert(9 + PER <= kWave, "padding words per block");
-  const u64* at = src + 32 * b;
+  static_assert(NW % 2 == 0 && NW <= 2 * kWave, "16 bytes per lane");
   auto poll = [&] {
-    if (lane < 16) __builtin_amdgcn_global_load_lds(at + 2 * lane, (lds_ptr)blk, 16, 0, 16);
+    if (lane < NW / 2) __builtin_amdgcn_global_load_lds(at + 2 * lane, (lds_ptr)blk, 16, 0, 16);
   };
   // s_waitcnt immediate: vmcnt <= 1 (the newer poll), expcnt/lgkmcnt not waited.
   constexpr int kWaitOlderPoll = 1 | (7 << 4) | (15 << 8);
@@ -662,8 +679,8 @@ __device__ bool publish_block(const u64* src, u64* dst, int b, uint32_t gen, u64
   for (long spin = 0;; ++spin) {
     poll();
     __builtin_amdgcn_s_waitcnt(kWaitOlderPoll);
-    const uint4 t = lane < 16 ? *reinterpret_cast<const uint4*>(blk + 2 * lane) : make_uint4(0, gen, 0, gen);
-    if (__all(t.y == gen && t.w == gen)) break;
+    const uint4 t = lane < NW / 2 ? *reinterpret_cast<const uint4*>(blk + 2 * lane) : make_uint4(0, gen, 0, gen);
+    if (__all((t.y & tmask) == gen && (t.w & tmask) == gen)) break;
     if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
       if (lane == 0) __hip_atomic_fetch_or(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __builtin_amdgcn_s_waitcnt(0);
@@ -673,11 +690,19 @@ __device__ bool publish_block(const u64* src, u64* dst, int b, uint32_t gen, u64
   if (seen) seen[0] = __builtin_amdgcn_s_memrealtime();
   // Drained: the newer poll writes the same current words.
   __builtin_amdgcn_s_waitcnt(0);
+  return true;
+}
+
+// One wave: wait for the 64 activations of blocks 2n and 2n + 1 of a
+// vector (tagged words src[64n, +64), staged in blk), quantise them and
+// publish both blocks (one whole line) in exchange form at dst.
+__device__ bool publish_pair(const u64* src, u64* dst, int n, uint32_t gen, u64* blk, unsigned* error,
+                             u64* seen = nullptr) {
+  const int lane = threadIdx.x & (kWave - 1);
+  if (!poll_words<64>(src + 64 * n, gen, blk, error, seen)) return false;
   float d;
-  const uint32_t q = quantize_lane4(tag_float4(blk, 4 * (lane & 7)), &d);
-  if (lane < 8) tag_store_bits(dst + 8 * b + lane, gen, q);
-  else if (lane == 8) tag_store_bits(dst + 8 * NBL + b, gen, f2u(d));
-  else if (lane < 9 + PER && PER * b + (lane - 9) < PAD) tag_store_bits(dst + 9 * NBL + PER * b + (lane - 9), gen, 0u);
+  const uint32_t q = quantize_lane4(tag_float4(blk, 4 * (lane & 15)), &d);
+  if (lane < 16) qword_store(dst + 16 * n + lane, gen, qside(lane & 7, d), q);
   return true;
 }
 
@@ -761,9 +786,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Largest per-workgroup slices (rows) and their (row, block) pairs.
   constexpr int RQ = (QL + NX - 1) / NX, RO = (W + NG - 1) / NG, RGU = (FF / 8 + NX - 1) / NX;
   // Quantised exchanges: attention output and ffn activations.
-  constexpr int QWA = qwords(QW), QWH = qwords(FF);
-  static_assert(FF % 256 == 0 && RGU < 32 && QWA <= kTagWords && QWH <= kTagWords,
-                "ffn blocks per XCD, one block per owner, gather area");
+  constexpr int QWA = qblock_words(QW), QWH = qblock_words(FF);
+  static_assert(FF % 512 == 0 && RGU < 64 && QWA % 128 == 0 && QWH % 128 == 0 && QWA <= kTagWords &&
+                    QWH <= kTagWords,
+                "ffn block pairs per XCD, one pair per owner, whole gather chunks");
   constexpr int NPQ = RQ * B1, NPO = RO * Bq, NPG = 2 * RGU * B1, NPD = RO * Bf;
   // Projection workgroups stage their weight slices in the K/V area: q/k/v,
   // o, gate/up and down at these byte offsets, each a whole number of rounds.
@@ -1051,17 +1077,11 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lds_barrier_p();
       if (wave == 0) {
         // The head's four 32-value blocks quantised for the o projection:
-        // lanes 0-31 the packed values (block 4 hq + lane / 8), lanes 32-35
-        // the scales, later lanes this head's share of the padding words.
-        constexpr int NBA = QW / 32, PADA = QWA - 9 * NBA, PERA = (PADA + HQ - 1) / HQ;
-        static_assert(HS == 128 && PERA <= kWave - 36, "padding words per head");
+        // lanes 0-31 write them (block lane / 8), two whole lines.
+        static_assert(HS == 128, "four blocks per head");
         float d;
         const uint32_t q = quantize_lane4(*reinterpret_cast<const float4*>(&cur_s[0][4 * (lane & 31)]), &d);
-        const float dsc = __shfl(d, 8 * (lane & 3), kWave);
-        if (lane < 32) tag_store_bits(a.tattq + 32 * hq + lane, gen(l, 2), q);
-        else if (lane < 36) tag_store_bits(a.tattq + 8 * NBA + 4 * hq + (lane - 32), gen(l, 2), f2u(dsc));
-        else if (lane - 36 < PERA && PERA * hq + (lane - 36) < PADA)
-          tag_store_bits(a.tattq + 9 * NBA + PERA * hq + (lane - 36), gen(l, 2), 0u);
+        if (lane < 32) qword_store(a.tattq + 32 * hq + lane, gen(l, 2), qside(lane & 7, d), q);
         // The output values themselves, for tracing.
         tag_store(a.tatt + hq * HS + lane, gen(l, 2), cur_s[0][lane]);
         tag_store(a.tatt + hq * HS + kWave + lane, gen(l, 2), cur_s[0][kWave + lane]);
@@ -1094,16 +1114,18 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int s8 = 0; s8 < G; ++s8) g -= min(max(w - 8 * s8, 0), HKV);
     const Rows ro = split_rows<W, NG>(g);
-    // ffn rows: entries of this XCD's list (persistent_ffn_entries), the
-    // gate/up tile's storage row, and the 32-row block this role quantises
-    // and publishes (the one whose entry 16 it computes), if any.
+    auto row_at = [&](int r) { return ro.r0 + r; };  // o and down rows
+    // ffn rows: entries of this XCD's list (persistent_xcd_entries, 64-row
+    // block pairs), the gate/up tile's storage row, and the block pair this
+    // role quantises and publishes (the one whose entry 32 it computes), if
+    // any.
     const int fx = w & 7;
-    const FfnEntries rf = persistent_ffn_entries(fx, (w >> 3) - (fx < HKV ? G : 0), FF, HKV, G, NB);
+    const XcdEntries rf = persistent_xcd_entries(fx, (w >> 3) - (fx < HKV ? G : 0), FF, HKV, G, NB);
     const size_t rf_store = 2 * (size_t)(fx * (FF / 8) + rf.r0);
     int own = -1;
     {
-      const int k = (rf.r0 + rf.count - 17) >> 5;
-      if (rf.count > 0 && k >= 0 && 32 * k + 16 >= rf.r0) own = fx + 8 * k;
+      const int k = (rf.r0 + rf.count - 33) >> 6;
+      if (rf.count > 0 && k >= 0 && 64 * k + 32 >= rf.r0) own = fx + 8 * k;
     }
     // q/k/v: this XCD's kv head; none on XCDs past the kv heads, whose
     // (unused, clamped) slice loads then read kv head 0's rows.
@@ -1114,7 +1136,6 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                         : (r < (G + 1) * HS ? QW + HS * xk + (r - G * HS) : QW + KVW + HS * xk + (r - (G + 1) * HS));
     };
     auto qkv_at = [&](int r) { return qkv_row(rq.r0 + r); };
-    auto o_at = [&](int r) { return ro.r0 + r; };  // o and down rows
     auto gu_at = [&](int r) { return (int)rf_store + r; };
     // Compute lanes, after the q/k/v publication of layer l: the slices of
     // layer l's o, gate/up and down and of layer l + 1's q/k/v, staged while
@@ -1126,9 +1147,9 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // in registers across the loop.
       int cl = ct;
       asm volatile("" : "+v"(cl));
-      stage_slice<QW, SO>(kv_s + OO, Ly.wo, Ly.so, ro.count, cl, o_at);
+      stage_slice<QW, SO>(kv_s + OO, Ly.wo, Ly.so, ro.count, cl, row_at);
       stage_slice<W, SG>(kv_s + OG, Ly.wgu, Ly.sgu, 2 * rf.count, cl, gu_at);
-      stage_slice<FF, SD>(kv_s + OD, Ly.wd, Ly.sd, ro.count, cl, o_at);
+      stage_slice<FF, SD>(kv_s + OD, Ly.wd, Ly.sd, ro.count, cl, row_at);
       if (l + 1 < L) stage_slice<W, SQ>(kv_s + OQ, LT[l + 1].wqkv, LT[l + 1].sqkv, rq.count, cl, qkv_at);
     };
     // Layer-0 input: a host row or the embedding of the device token
@@ -1188,9 +1209,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (lane == 0) okw_s[wave] = ok ? 1 : 0;
       }
     };
-    auto gather_all = [&](const u64* src, int count, uint32_t gn) {
+    auto gather_q = [&](const u64* src, int count, uint32_t gn) {
       if (ct < 0) {
-        const bool ok = gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, NoPre{}, wave, 4);
+        const bool ok = gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gn), tag_s, a.error, NoPre{}, wave, 4,
+                               NoChunk{}, nullptr, kQTagMask);
         if (lane == 0) okw_s[wave] = ok ? 1 : 0;
       }
     };
@@ -1212,7 +1234,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const auto& Nx = LT[l + 1 < L ? l + 1 : l];  // the last layer re-reads its own slices
       const int e = 16 * l + 1;
       // ---- P1: attn_norm + qkv ----------------------------------------------
-      if (tid < ro.count) row_s[0][tid] = tag_value(tag_s, ro.r0 + tid);
+      if (tid < ro.count) row_s[0][tid] = tag_value(tag_s, row_at(tid));
       quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
       if (ct >= 0 && l == 0) __builtin_amdgcn_s_waitcnt(0);  // layer 0's staged q/k/v slice
       lds_barrier_p();
@@ -1232,12 +1254,12 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       lds_barrier_p();
       if (ct >= 0) stage_window(l);
-      gather_all(a.tattq, QWA, gen(l, 2));
+      gather_q(a.tattq, QWA, gen(l, 2));
       if (ct >= 0) __builtin_amdgcn_s_waitcnt(0);  // the staged slices are in LDS before the barrier
       if (!gathered()) return;
 
       // ---- P3: o projection + residual -------------------------------------
-      unpack_qvec<QW>(tag_s, xq_s, xs_s);
+      unpack_qblocks<QW>(tag_s, xq_s, xs_s);
       lds_barrier_p();
       if (ct >= 0) lds_products<NPO, Bq>(kv_s + OO, ro.count, ct, xq_s, xs_s, prod_s);
       lds_barrier_p();
@@ -1245,7 +1267,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (lane < ro.count) {
           const float v = fadd(ordered_sum<Bq>(prod_s, lane), row_s[0][lane]);
           row_s[1][lane] = v;
-          tag_store(a.ta + ro.r0 + lane, gen(l, 3), v);
+          tag_store(a.ta + row_at(lane), gen(l, 3), v);
         }
         stamps(e + 8, e + 9);
       }
@@ -1265,32 +1287,34 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const float u = __shfl(gs, lane + nr, kWave);
         if (lane < nr) {
           const float silu = fdiv(gs, fadd(1.0f, exp_ref(-gs)));
-          u64* dst = a.th + persistent_ffn_row(fx, rf.r0 + lane);
+          u64* dst = a.th + persistent_xcd_row(fx, rf.r0 + lane, 64);
           if (a.local_l2) tag_store_local(dst, gen(l, 4), fmul(silu, u));
           else tag_store(dst, gen(l, 4), fmul(silu, u));
         }
         stamps(e + 10, e + 12, e + 11, 1);
       }
-      // The block owners quantise their blocks (read through this XCD's L2)
+      // The pair owners quantise their blocks (read through this XCD's L2)
       // and publish them; every projection workgroup gathers the quantised
       // vector.
       if (ct < 0) {
         bool ok = true;
         if (wave == 0 && own >= 0) {
           u64 seen = 0;
-          ok = publish_block<FF>(a.th, a.thq, own, gen(l, 4), tag_s + kTagWords - 32, a.error, &seen);
+          ok = publish_pair(a.th, a.thq, own, gen(l, 4), tag_s + kTagWords - 64, a.error, &seen);
           if (tl && lane == 0) {
             tl[e + 6] = seen;
             tl[e + 7] = __builtin_amdgcn_s_memrealtime();
           }
         }
-        if (ok) ok = gather(a.thq, QWH, 0, nullptr, 0, 0, nullptr, 0, 0, gen(l, 4), tag_s, a.error, NoPre{}, wave, 4);
+        if (ok)
+          ok = gather(a.thq, QWH, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gen(l, 4)), tag_s, a.error, NoPre{}, wave, 4,
+                      NoChunk{}, nullptr, kQTagMask);
         if (lane == 0) okw_s[wave] = ok ? 1 : 0;
       }
       if (!gathered()) return;
 
       // ---- P5: down projection + residual ------------------------------------
-      unpack_qvec<FF>(tag_s, xq_s, xs_s);
+      unpack_qblocks<FF>(tag_s, xq_s, xs_s);
       lds_barrier_p();
       sub(0);
       if (ct >= 0) lds_products<NPD, Bf>(kv_s + OD, ro.count, ct, xq_s, xs_s, prod_s);
@@ -1299,7 +1323,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (wave == 0) {
         if (lane < ro.count) {
           const float v = fadd(ordered_sum<Bf>(prod_s, lane), row_s[1][lane]);
-          tag_store(a.tx + ro.r0 + lane, gen(l, 5), v);
+          tag_store(a.tx + row_at(lane), gen(l, 5), v);
         }
         stamps(e + 13, e + 15, e + 14, 1);
         if (tl && lane == 0) tl[e + 5] = t_sub[1];
