@@ -57,6 +57,11 @@ constexpr int kSentinelChunks = 1;
 // few words, so deeper pipelines only lengthen the queue in front of them:
 // measured on the decode step, 1 beats 2, 4 and 8.
 constexpr int kPolls = 1;
+// A gather sleeps this long (64-cycle units, about 0.7 us) before its first
+// poll: no data can arrive sooner, and polls issued earlier only queue in
+// front of the producers' stores. Measured on the decode step: 16 and 32
+// are slower, 48 far slower; sleeping after a stale poll is slower too.
+constexpr int kGatherDelay = 24;
 // s_waitcnt immediate for vmcnt <= kPolls - 1 (expcnt and lgkmcnt not
 // waited on): vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
 constexpr int kWaitOldestPoll = ((kPolls - 1) & 15) | (((kPolls - 1) >> 4) << 14) | (7 << 4) | (15 << 8);
@@ -161,6 +166,7 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
     }
   };
   long spin = 0;
+  __builtin_amdgcn_s_sleep(kGatherDelay);
   // Poll the end of the last chunk until it is current before reading them
   // all (that chunk too), so that consumers that arrive early cost one small
   // load per round trip instead of the whole vector.
