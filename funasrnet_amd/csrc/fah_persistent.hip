@@ -5,25 +5,30 @@
 // five phases -- qkv, attention, o, gate/up, down -- separated by exchanges
 // of the activation vector through global memory. Each value is published
 // as a 64-bit word (generation << 32 | float bits) with one relaxed store,
-// so a consumer sees value and readiness in the same load.
+// so a consumer sees value and readiness in the same load. The attention
+// output and the ffn activations, which the next phase quantises without a
+// norm, travel already quantised (Q8_0 blocks with 16-bit tags), each
+// 128-byte line written by a single workgroup.
 //
 // Placement: the hardware deals a launch's workgroups to the eight XCDs in
 // turn. The attention workgroups of kv head x and the workgroups that form
-// that head's q/k/v rows all sit on XCD x, so that hand-over stays in one
-// L2 (stores that are not written through); the other exchanges cross XCDs
+// that head's q/k/v rows all sit on XCD x, and the ffn rows of block pair p
+// are computed on XCD p % 8, so those hand-overs stay in one L2 (stores
+// that are not written through); the other exchanges cross XCDs
 // (device-scope stores, device-coherent loads).
 //
-// Roles inside a workgroup (8 waves, two per SIMD):
+// Roles inside a projection workgroup (8 waves, two per SIMD):
 //  * waves 0-3 are the memory waves: they gather the next phase's input, a
 //    part of the chunks each (wave 0 also fetches the small per-layer
-//    constants in the same batch), each polling only the last 64 bytes of
-//    its part until they are current and then reading the part whole, so
-//    that the polls of all consumers stay a small part of the traffic.
-//    Wave 0 also sums the phase's rows in order and publishes them.
-//  * waves 4-7 are the compute waves: they hold the weight slices of the
-//    next two phases in registers (issued a phase ahead, a fixed number of
-//    loads per phase so that every wait counts exactly the loads it needs)
-//    and form the block products.
+//    constants in the same batch), after a short sleep, polling a part of
+//    one chunk whole and longer parts through their last 64 bytes, so that
+//    the polls of all consumers stay a small part of the traffic. Wave 0
+//    also sums the phase's rows in order and publishes them, and the ffn
+//    block-pair owners' wave 0 quantises and publishes the pair.
+//  * waves 4-7 are the compute waves: while the attention runs they copy
+//    the layer's weight slices (and the next layer's q/k/v slice) into LDS,
+//    so that no weight stream overlaps an exchange, and they form the block
+//    products.
 //  * all eight quantise the phase input.
 // Attention workgroups use all eight waves for the scores, the softmax and
 // the K/V staging; two of them run the time-ordered value sums.
@@ -452,26 +457,6 @@ __device__ __forceinline__ void load_slot(Slot<P>& sl, const int8_t* w, const _F
     sl.w[i][0] = p[0];
     sl.w[i][1] = p[1];
     sl.s[i] = s[j];
-  }
-}
-
-// load_slot for a slice whose rows are not contiguous in storage: pair j is
-// slice row r0 + j / B (mapped to its storage row by `row`), block j % B.
-template <int NP, int B, int P, class RowMap>
-__device__ __forceinline__ void load_slot_rows(Slot<P>& sl, const int8_t* w, const _Float16* s, int r0, int ct, int valid,
-                                               RowMap row) {
-  constexpr int kI = (NP + kComp - 1) / kComp;
-  static_assert(kI <= P, "slot capacity");
-#pragma unroll
-  for (int i = 0; i < kI; ++i) {
-    int j = ct + i * kComp;
-    j = j < valid ? j : valid - 1;
-    const int rr = j / B, b = j - rr * B;
-    const size_t at = (size_t)row(r0 + rr) * B + b;
-    const int4* p = reinterpret_cast<const int4*>(w + at * 32);
-    sl.w[i][0] = p[0];
-    sl.w[i][1] = p[1];
-    sl.s[i] = s[at];
   }
 }
 

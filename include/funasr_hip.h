@@ -240,9 +240,12 @@ int fah_decoder_trace(fah_decoder* decoder, int which, float* out, int count);
  * (src/FunAsrNet/TensorMath.cs:37-40) for a single-launch step. */
 int fah_decoder_timeline(fah_decoder* decoder, uint64_t* ticks, int count);
 
-/* 1 when decode steps run as one persistent launch (one workgroup per CU,
- * phases exchanged through device memory), 0 for the per-kernel graph path.
- * FAH_PERSISTENT=0 in the environment at creation forces the latter. */
+/* 2 when decode steps run as one persistent launch with XCD-local roles
+ * (workgroups take their role from the XCD they run on, and hand data to
+ * workgroups of the same XCD through its L2), 1 for the persistent launch
+ * with roles by workgroup index (after a launch found the XCD dealing it
+ * relies on broken, or with FAH_LOCAL_L2=0 in the environment at creation),
+ * 0 for the per-kernel graph path (FAH_PERSISTENT=0 at creation). */
 int fah_decoder_persistent(const fah_decoder* decoder);
 
 /* Device bytes of the weights streamed per decoded token (all projections
