@@ -18,17 +18,21 @@ def backend():
     b.close()
 
 
-def _decoder(backend, weights, persistent, capacity):
+def _decoder(backend, weights, persistent, capacity, local_l2=None):
     from funasrnet_amd.hip import HipDecoder
-    old = os.environ.get("FAH_PERSISTENT")
-    os.environ["FAH_PERSISTENT"] = "1" if persistent else "0"
+    env = {"FAH_PERSISTENT": "1" if persistent else "0"}
+    if local_l2 is not None:
+        env["FAH_LOCAL_L2"] = "1" if local_l2 else "0"
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
         return HipDecoder(backend, weights, capacity=capacity)
     finally:
-        if old is None:
-            del os.environ["FAH_PERSISTENT"]
-        else:
-            os.environ["FAH_PERSISTENT"] = old
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
 
 
 @pytest.mark.parametrize("shape", ["small", "qwen3"])
@@ -176,4 +180,28 @@ def test_steps_across_the_persistent_range(backend, shape):
         assert fast.generate(5).tolist() == slow.generate(5).tolist()
     finally:
         fast.close()
+        slow.close()
+
+
+@pytest.mark.parametrize("shape", ["small", "qwen3"])
+def test_persistent_without_xcd_roles_matches_graph_path(backend, oracle_lib, shape):
+    """FAH_LOCAL_L2=0: roles by workgroup index, every hand-over through
+    device-scope stores (the mode a launch falls back to when the XCD
+    dealing it relies on is broken) gives the same bits."""
+    from funasrnet_amd.hip import load
+    cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
+    w = model.synthetic(cfg, seed=5)
+    frames = 12 if shape == "small" else 150
+    prefix = np.random.default_rng(13).standard_normal((frames, cfg.width)).astype(np.float32)
+    plain = _decoder(backend, w, True, 1024, local_l2=False)
+    slow = _decoder(backend, w, False, 1024)
+    try:
+        assert load().fah_decoder_persistent(plain.handle) == 1
+        lp = plain.decode(prefix, frames)
+        ls = slow.decode(prefix, frames)
+        assert np.array_equal(lp.view(np.uint32), ls.view(np.uint32))
+        assert plain.greedy() == slow.greedy() == oracle_lib.greedy(ls)
+        assert plain.generate(8).tolist() == slow.generate(8).tolist()
+    finally:
+        plain.close()
         slow.close()
