@@ -393,18 +393,6 @@ __device__ __forceinline__ void value_chain(const char* kv, const char* ovf, con
   cur[0][c] = acc;
 }
 
-// score8_mix with q in registers (q[0..7] = channels 8i..8i+7).
-__device__ __forceinline__ void score8_regs(float* acc, const uint4& kk, const float* q) {
-  const uint32_t w[4] = {kk.x, kk.y, kk.z, kk.w};
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu));
-    const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16));
-    acc[2 * m] = fadd(acc[2 * m], mulh(q[2 * m], lo));
-    acc[2 * m + 1] = fadd(acc[2 * m + 1], mulh(q[2 * m + 1], hi));
-  }
-}
-
 // Half a K row piece: four F16 channels 8i + 4h .. 8i + 4h + 3 into the
 // four accumulators of lane parity h (q[0..3] the matching q channels).
 __device__ __forceinline__ void score4_regs(float* acc, const uint2& kk, const float* q) {
@@ -415,22 +403,6 @@ __device__ __forceinline__ void score4_regs(float* acc, const uint2& kk, const f
     const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16));
     acc[2 * m] = fadd(acc[2 * m], mulh(q[2 * m], lo));
     acc[2 * m + 1] = fadd(acc[2 * m + 1], mulh(q[2 * m + 1], hi));
-  }
-}
-
-// score8 with mulh products: one 16-byte piece of a K row (8 F16 channels
-// 8i..8i+7) into the eight channel-strided accumulators.
-__device__ __forceinline__ void score8_mix(float* acc, const uint4& kk, const float* q) {
-  const float4 q0 = *reinterpret_cast<const float4*>(q);
-  const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
-  const uint32_t w[4] = {kk.x, kk.y, kk.z, kk.w};
-  const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu));
-    const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16));
-    acc[2 * m] = fadd(acc[2 * m], mulh(qv[2 * m], lo));
-    acc[2 * m + 1] = fadd(acc[2 * m + 1], mulh(qv[2 * m + 1], hi));
   }
 }
 
@@ -1181,11 +1153,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     lds_barrier_p();
 
     // The next phase's input, gathered by the memory waves (each a part of
-    // the chunks; wave 0 also copies the constants `pre` names) while the
-    // compute waves load the slice of the phase after next. An input that is
-    // RMS-normalised (W values) is split so that wave m holds chunks 2m and
-    // 2m + 1 and adds its part of the square sum as soon as they are in; the
-    // others are split in four and quantised by all waves after the barrier.
+    // the chunks; wave 0 also copies the constants `pre` names). An input
+    // that is RMS-normalised (W values) is split so that wave m holds chunks
+    // 2m and 2m + 1 and adds its part of the square sum as soon as they are
+    // in; the quantised ones are split in four.
     auto gather_norm = [&](const u64* src, uint32_t gn, auto pre) {
       if (ct < 0) {
         constexpr int parts = W / 256;
@@ -1213,16 +1184,15 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       return (okw_s[0] & okw_s[1] & okw_s[2] & okw_s[3]) != 0;
     };
 
-    // Each phase: all threads quantise the gathered input, the compute waves
-    // form the block products of their slice, then wave 0 sums the rows in
-    // order and publishes them; after a barrier the memory waves gather the
-    // next phase's input and the compute waves load the slice of the phase
-    // after next. The barrier keeps the publication ahead of the slice's
-    // loads: behind the grid's weight burst a store took about a
-    // microsecond longer to reach the other workgroups.
+    // Each phase: all threads quantise (or unpack) the gathered input, the
+    // compute waves form the block products of their LDS slice, then wave 0
+    // sums the rows in order and publishes them, and the memory waves gather
+    // the next phase's input. After the q/k/v publication (and a barrier, so
+    // that the stores leave ahead of the burst) the compute waves stage the
+    // slices of the rest of the layer and the next layer's q/k/v.
     for (int l = 0; l < L; ++l) {
       const auto& Ly = LT[l];
-      const auto& Nx = LT[l + 1 < L ? l + 1 : l];  // the last layer re-reads its own slices
+      const auto& Nx = LT[l + 1 < L ? l + 1 : l];
       const int e = 16 * l + 1;
       // ---- P1: attn_norm + qkv ----------------------------------------------
       if (tid < ro.count) row_s[0][tid] = tag_value(tag_s, row_at(tid));
