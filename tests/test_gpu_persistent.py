@@ -205,3 +205,39 @@ def test_persistent_without_xcd_roles_matches_graph_path(backend, oracle_lib, sh
     finally:
         plain.close()
         slow.close()
+
+
+@pytest.mark.parametrize("bad", ["nan", "inf", "huge"])
+def test_persistent_non_finite_rows_match_graph_path(backend, oracle_lib, bad):
+    """Rows with a NaN, an infinity or values near the float range through one
+    persistent step and through the graph path: the same NaN positions, the
+    same bits elsewhere, the same greedy token (a NaN first logit gives 0)."""
+    cfg = model.small_config(layers=2)
+    w = model.synthetic(cfg, seed=3)
+    frames = 6
+    prefix = np.random.default_rng(17).standard_normal((frames, cfg.width)).astype(np.float32)
+    row = np.random.default_rng(19).standard_normal((1, cfg.width)).astype(np.float32)
+    if bad == "nan":
+        row[0, 37] = np.nan
+    elif bad == "inf":
+        row[0, 100] = np.inf
+    else:
+        row[0, :64] = 3.0e38
+    fast = _decoder(backend, w, True, 256)
+    slow = _decoder(backend, w, False, 256)
+    try:
+        assert fast.persistent and not slow.persistent
+        fast.decode(prefix, frames)
+        slow.decode(prefix, frames)
+        lf = fast.decode(row, 1)
+        ls = slow.decode(row, 1)
+        nf, ns = np.isnan(lf), np.isnan(ls)
+        assert np.array_equal(nf, ns)
+        assert np.array_equal(lf[~nf].view(np.uint32), ls[~ns].view(np.uint32))
+        assert fast.greedy() == slow.greedy() == oracle_lib.greedy(ls)
+        kf, vf = fast.kv_read(cfg.layers - 1, frames + 1)
+        ks, vs = slow.kv_read(cfg.layers - 1, frames + 1)
+        assert np.array_equal(np.isnan(kf), np.isnan(ks)) and np.array_equal(np.isnan(vf), np.isnan(vs))
+    finally:
+        fast.close()
+        slow.close()
