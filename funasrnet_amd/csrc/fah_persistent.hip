@@ -59,9 +59,10 @@ constexpr long kSpinLimit = 1L << 21;    // bounded polls per gather (~1-2 s)
 // sooner, and little enough traffic).
 constexpr int kSentinelChunks = 1;
 // Sentinel polls in flight per gathering wave. Every consumer polls the same
-// few words, so deeper pipelines only lengthen the queue in front of them:
-// measured on the decode step, 1 beats 2, 4 and 8.
-constexpr int kPolls = 1;
+// few words, so deeper pipelines lengthen the queue in front of them:
+// measured on the decode step (with the gather delay below), 2 is a little
+// faster than 1, and 4 and 8 are slower.
+constexpr int kPolls = 2;
 // A gather sleeps this long (64-cycle units, about 0.7 us) before its first
 // poll: no data can arrive sooner, and polls issued earlier only queue in
 // front of the producers' stores. Measured on the decode step: 16 and 32
@@ -1061,7 +1062,12 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         stamps(e + 3, e + 7, e + 4, 3);
       }
       // Stage the next layer's K/V while the projections run.
-      if (l + 1 < L) stage_kv(l + 1);
+      // The next layer's K/V staging starts ~0.9 us later, after the
+      // attention-output exchange has left (measured slightly faster).
+      if (l + 1 < L) {
+        __builtin_amdgcn_s_sleep(32);
+        stage_kv(l + 1);
+      }
     }
     // lm_head input: the last layer's output with output_norm.
     if (wave == 0) {
@@ -1309,15 +1315,19 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // compute lane; wave 0 sums chunk c (logits staged in LDS) while the compute
   // waves form chunk c+1.
   Slot<kSlotPairs> ha, hb, hc;
+  // Chunk c goes to the workgroup with hw = c mod NB, hw = NB - 1 - w: the
+  // chunks that do not divide evenly land on the projection workgroups,
+  // which start the lm_head before the attention ones.
+  const int hw = NB - 1 - w;
   auto load_head = [&](Slot<kSlotPairs>& sl, int c) {
     const int cc = c < chunks ? c : chunks - 1;  // clamped chunks are never summed
     const int row0 = cc * HR;
     load_slot<NPH>(sl, a.head_q + (size_t)row0 * W, a.head_s + (size_t)row0 * B1, ct, min(HR, a.vocab - row0) * B1);
   };
   if (ct >= 0) {
-    load_head(ha, w);
-    load_head(hb, w + NB);
-    load_head(hc, w + 2 * NB);
+    load_head(ha, hw);
+    load_head(hb, hw + NB);
+    load_head(hc, hw + 2 * NB);
   }
   // The attention workgroups' lm_head input was gathered whole by wave 0;
   // the projection workgroups already hold its norm partials.
@@ -1346,7 +1356,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     parity ^= 1;
     ++k;
   };
-  for (int c = w; c < chunks; c += 3 * NB) {
+  for (int c = hw; c < chunks; c += 3 * NB) {
     head_chunk(ha, c);
     if (ct >= 0) load_head(ha, c + 3 * NB);
     head_chunk(hb, c + NB);
@@ -1357,14 +1367,14 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (wave != 0) return;
   // Wave 0 alone from here: logits out, then this workgroup's best key.
   for (int i = 0; i < k; ++i) {
-    const int row0 = (w + i * NB) * HR;
+    const int row0 = (hw + i * NB) * HR;
     for (int r = lane; r < HR; r += kWave)
       if (row0 + r < a.vocab) a.logits[row0 + r] = hlog[i * HR + r];
   }
   best = wave_max_u64(best);
   if (tl && lane == 0) tl[16 * L + 1] = __builtin_amdgcn_s_memrealtime();
   if (lane == 0) {
-    if (w == 0 && nan_first) best = ~0ull;  // forces token 0 below
+    if (nan_first) best = ~0ull;  // (only the holder of chunk 0) forces token 0 below
     tag_store_bits(a.tkeys + 2 * w, gen(L, 1), (uint32_t)(best >> 32));
     tag_store_bits(a.tkeys + 2 * w + 1, gen(L, 1), (uint32_t)best);
   }
