@@ -498,16 +498,17 @@ __device__ __forceinline__ void stage_slice(char* dst, const int8_t* w, const _F
 // Rounds of stage_slice for slices of up to `rows` rows of K weights.
 __host__ __device__ constexpr int stage_rounds(int rows, int K) { return (rows * (K / 16 + K / 256) + kComp - 1) / kComp; }
 
-// slot_products for a slice staged in LDS by stage_slice (`rows` rows).
+// slot_products for a slice staged in LDS by stage_slice (`rows` rows), on
+// all the workgroup's threads (the memory waves have nothing to wait for
+// while the products form).
 template <int NP, int B>
-__device__ __forceinline__ void lds_products(const char* sl, int rows, int ct, const int* xq, const float* xs,
-                                             float* prod) {
-  constexpr int K = 32 * B, kI = (NP + kComp - 1) / kComp;
+__device__ __forceinline__ void lds_products(const char* sl, int rows, const int* xq, const float* xs, float* prod) {
+  constexpr int K = 32 * B, kI = (NP + kPT - 1) / kPT;
   const int valid = rows * B;
   const _Float16* sc = reinterpret_cast<const _Float16*>(sl + (size_t)rows * K);
 #pragma unroll
   for (int i = 0; i < kI; ++i) {
-    const int j = ct + i * kComp;
+    const int j = (int)threadIdx.x + i * kPT;
     if (j < valid) {
       const int r = j / B, b = j - r * B;
       const int4* wp = reinterpret_cast<const int4*>(sl + (size_t)r * K + 32 * b);
@@ -1206,7 +1207,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (ct >= 0 && l == 0) __builtin_amdgcn_s_waitcnt(0);  // layer 0's staged q/k/v slice
       lds_barrier_p();
       sub(0);
-      if (ct >= 0) lds_products<NPQ, B1>(kv_s + OQ, rq.count, ct, xq_s, xs_s, prod_s);
+      lds_products<NPQ, B1>(kv_s + OQ, rq.count, xq_s, xs_s, prod_s);
       lds_barrier_p();
       sub(1);
       if (wave == 0) {
@@ -1228,7 +1229,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // ---- P3: o projection + residual -------------------------------------
       unpack_qblocks<QW>(tag_s, xq_s, xs_s);
       lds_barrier_p();
-      if (ct >= 0) lds_products<NPO, Bq>(kv_s + OO, ro.count, ct, xq_s, xs_s, prod_s);
+      lds_products<NPO, Bq>(kv_s + OO, ro.count, xq_s, xs_s, prod_s);
       lds_barrier_p();
       if (wave == 0) {
         if (lane < ro.count) {
@@ -1245,7 +1246,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
       lds_barrier_p();
       sub(0);
-      if (ct >= 0) lds_products<NPG, B1>(kv_s + OG, 2 * rf.count, ct, xq_s, xs_s, prod_s);
+      lds_products<NPG, B1>(kv_s + OG, 2 * rf.count, xq_s, xs_s, prod_s);
       lds_barrier_p();
       if (wave == 0) {
         // Lanes [0, n) sum the gate rows, [n, 2n) the matching up rows.
@@ -1284,7 +1285,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       unpack_qblocks<FF>(tag_s, xq_s, xs_s);
       lds_barrier_p();
       sub(0);
-      if (ct >= 0) lds_products<NPD, Bf>(kv_s + OD, ro.count, ct, xq_s, xs_s, prod_s);
+      lds_products<NPD, Bf>(kv_s + OD, ro.count, xq_s, xs_s, prod_s);
       lds_barrier_p();
       sub(1);
       if (wave == 0) {
