@@ -27,9 +27,9 @@
 //    block-pair owners' wave 0 quantises and publishes the pair.
 //  * waves 4-7 are the compute waves: while the attention runs they copy
 //    the layer's weight slices (and the next layer's q/k/v slice) into LDS,
-//    so that no weight stream overlaps an exchange, and they form the block
-//    products.
-//  * all eight quantise the phase input.
+//    so that no weight stream overlaps an exchange.
+//  * all eight quantise the phase input and form the block products from
+//    the LDS slices.
 // Attention workgroups use all eight waves for the scores, the softmax and
 // the K/V staging; two of them run the time-ordered value sums.
 // The arithmetic of every phase is the one of the multi-kernel path
@@ -1191,9 +1191,9 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       return (okw_s[0] & okw_s[1] & okw_s[2] & okw_s[3]) != 0;
     };
 
-    // Each phase: all threads quantise (or unpack) the gathered input, the
-    // compute waves form the block products of their LDS slice, then wave 0
-    // sums the rows in order and publishes them, and the memory waves gather
+    // Each phase: all threads quantise (or unpack) the gathered input and
+    // form the block products of the LDS slice, then wave 0 sums the rows in
+    // order and publishes them, and the memory waves gather
     // the next phase's input. After the q/k/v publication (and a barrier, so
     // that the stores leave ahead of the burst) the compute waves stage the
     // slices of the rest of the layer and the next layer's q/k/v.
