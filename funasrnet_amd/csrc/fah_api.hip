@@ -12,6 +12,7 @@
 #include <cstring>
 #include <memory>
 #include <mutex>
+#include <optional>
 #include <string>
 #include <vector>
 
@@ -163,21 +164,91 @@ struct SessionBatch {
   }
 };
 
-}  // namespace
-
-struct fah_context {
+// State of one context: device, stream, working buffers. The handle the
+// caller holds (fah_context) and every weight and decoder made from it share
+// it, so it outlives fah_context_destroy until the last of them is released;
+// after destroy it only reports "disposed".
+struct Ctx {
   int device = 0;
   hipStream_t stream = nullptr;
+  hipEvent_t mark = nullptr;  // recorded by a persistent section on another context of the device
   std::mutex gate;
   bool disposed = false;
   int64_t minimum_operations = 250000;
   DeviceBuffer in, out, q, s;
   std::string name;
   std::unique_ptr<SessionBatch> batch;  // last lock-step batch (its sessions alive)
+  Ctx() = default;
+  Ctx(const Ctx&) = delete;
+  Ctx& operator=(const Ctx&) = delete;
+  ~Ctx();
+};
+
+// Work of every context on one device is enqueued under this lock. The
+// persistent decode step needs every CU of the device to itself (one
+// workgroup per CU, all co-resident, dealt to the XCDs in turn), so a
+// persistent section holds the lock from before its launches until its
+// stream has drained, after making its stream wait for the work already
+// enqueued on the other contexts' streams: no other context's kernel can
+// then run beside it.
+struct DeviceGate {
+  std::mutex m;
+  std::vector<Ctx*> members;
+};
+constexpr int kMaxDevices = 64;
+DeviceGate& device_gate(int device) {
+  static DeviceGate gates[kMaxDevices];
+  return gates[device];
+}
+
+Ctx::~Ctx() {
+  if (!stream) return;
+  (void)hipSetDevice(device);
+  (void)hipStreamSynchronize(stream);
+  batch.reset();
+  {
+    DeviceGate& g = device_gate(device);
+    std::lock_guard<std::mutex> lock(g.m);
+    g.members.erase(std::remove(g.members.begin(), g.members.end(), this), g.members.end());
+  }
+  in.release();
+  out.release();
+  q.release();
+  s.release();
+  if (mark) (void)hipEventDestroy(mark);
+  (void)hipStreamDestroy(stream);
+}
+
+// Enqueue section for ordinary work: holds the device lock while the caller
+// enqueues (not while the work runs).
+struct DeviceWork {
+  std::lock_guard<std::mutex> lock;
+  explicit DeviceWork(const Ctx& c) : lock(device_gate(c.device).m) {}
+};
+
+// Persistent section: the device lock, the other streams' pending work
+// ahead of this stream, and this stream drained before the lock is let go.
+struct PersistentSection {
+  Ctx& c;
+  std::unique_lock<std::mutex> lock;
+  explicit PersistentSection(Ctx& ctx) : c(ctx), lock(device_gate(ctx.device).m) {
+    for (Ctx* o : device_gate(c.device).members) {
+      if (o == &c) continue;
+      check(hipEventRecord(o->mark, o->stream), "hipEventRecord");
+      check(hipStreamWaitEvent(c.stream, o->mark, 0), "hipStreamWaitEvent");
+    }
+  }
+  ~PersistentSection() { (void)hipStreamSynchronize(c.stream); }
+};
+
+}  // namespace
+
+struct fah_context {
+  std::shared_ptr<Ctx> st;
 };
 
 struct fah_weight {
-  fah_context* context = nullptr;
+  std::shared_ptr<Ctx> ctx;
   int rows = 0, cols = 0;
   bool half_scales = true;
   DeviceBuffer q, s;
@@ -209,7 +280,7 @@ struct DecoderWeights {
 };
 
 struct fah_decoder {
-  fah_context* context = nullptr;
+  std::shared_ptr<Ctx> ctx;
   fah_decoder_config cfg{};
   int q_width = 0, kv_width = 0;
   std::shared_ptr<DecoderWeights> wt;
@@ -669,7 +740,7 @@ bool use_prefill(const fah_decoder* d, int frames) {
 }
 
 hipGraphExec_t capture(fah_decoder* d, int kind) {
-  hipStream_t s = d->context->stream;
+  hipStream_t s = d->ctx->stream;
   hipGraph_t graph = nullptr;
   check(hipStreamSynchronize(s), "hipStreamSynchronize");
   check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
@@ -689,14 +760,36 @@ hipGraphExec_t capture(fah_decoder* d, int kind) {
   return exec;
 }
 
-// The persistent kernel reports a missed exchange (bounded wait expired)
-// through its error word instead of hanging; surface it and clear it.
-void check_step_error(fah_decoder* d) {
+// Error word values: bit 0 a bounded wait expired (an exchange never came),
+// bit 1 preset by the host (fah_decoder_fail_next_step), bit 2 the device
+// position lay outside the cache. While the word is set every launch ends at
+// its entry check, so the steps enqueued after a failed one do nothing.
+constexpr unsigned kErrorTimeout = 1u, kErrorPreset = 2u, kErrorPosition = 4u;
+
+// After a persistent launch: if the error word is set, restore the device
+// state from the host's and throw. The epoch moves past every generation the
+// failed launch may have published (so none of its words can look current
+// to the next launch), the device position returns to the host position, the
+// history is emptied and the word cleared; the logits of the failed call are
+// not valid, so the caller decodes again before greedy or generate.
+void recover_step_error(fah_decoder* d) {
   if (!d->persistent) return;
-  unsigned e = 0;
-  check(hipMemcpy(&e, d->error.ptr, 4, hipMemcpyDeviceToHost), "D2H error word");
-  if (e) {
-    (void)hipMemset(d->error.ptr, 0, 4);
+  hipStream_t s = d->ctx->stream;
+  unsigned e = 0, epoch = 0;
+  check(hipMemcpyAsync(&e, d->error.ptr, 4, hipMemcpyDeviceToHost, s), "D2H error word");
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  if (!e) return;
+  check(hipMemcpyAsync(&epoch, d->epoch.ptr, 4, hipMemcpyDeviceToHost, s), "D2H epoch");
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  epoch += 2;
+  const int position = d->host_position, zero = 0;
+  check(hipMemcpyAsync(d->epoch.ptr, &epoch, 4, hipMemcpyHostToDevice, s), "H2D epoch");
+  check(hipMemcpyAsync(d->position.ptr, &position, 4, hipMemcpyHostToDevice, s), "H2D position");
+  check(hipMemcpyAsync(d->history_count.ptr, &zero, 4, hipMemcpyHostToDevice, s), "H2D history count");
+  check(hipMemcpyAsync(d->error.ptr, &zero, 4, hipMemcpyHostToDevice, s), "H2D error word");
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  d->have_logits = false;
+  if (e & kErrorTimeout) {
     // A launch whose workgroups were not dealt to the XCDs in turn leaves a
     // role unfilled and times out: later steps use placement-free roles.
     const bool was_local = d->pargs.local_l2 != 0;
@@ -704,6 +797,8 @@ void check_step_error(fah_decoder* d) {
     throw DeviceError{was_local ? "persistent decode step: an exchange timed out (XCD-local roles are now off)"
                                 : "persistent decode step: an exchange timed out (workgroups not co-resident?)"};
   }
+  if (e & kErrorPosition) throw DeviceError{"persistent decode step: device position outside the cache"};
+  throw DeviceError{"persistent decode step: stopped by the host (fah_decoder_fail_next_step)"};
 }
 
 // Enqueue one decoder row: kind 0 = layers only, 1 = layers + lm_head +
@@ -853,100 +948,107 @@ int fah_context_create(int device, fah_context** out) {
   if (!out) return fail(FAH_ERROR_ARGUMENT, "out is NULL");
   return guarded([&] {
     int n = fah_device_count();
-    require(device >= 0 && device < n, "no HIP device " + std::to_string(device));
+    require(device >= 0 && device < n && device < kMaxDevices, "no HIP device " + std::to_string(device));
     check(hipSetDevice(device), "hipSetDevice");
-    auto* c = new fah_context();
-    c->device = device;
-    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
-    if (e != hipSuccess) {
-      delete c;
-      check(e, "hipStreamCreate");
-    }
+    auto st = std::make_shared<Ctx>();
+    st->device = device;
+    hipStream_t stream = nullptr;
+    check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+    st->stream = stream;
+    check(hipEventCreateWithFlags(&st->mark, hipEventDisableTiming), "hipEventCreate");
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->name = std::string("HIP ") + prop.gcnArchName;
-    else c->name = "HIP";
-    *out = c;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) st->name = std::string("HIP ") + prop.gcnArchName;
+    else st->name = "HIP";
+    {
+      DeviceGate& g = device_gate(device);
+      std::lock_guard<std::mutex> lock(g.m);
+      g.members.push_back(st.get());
+    }
+    auto* h = new fah_context();
+    h->st = std::move(st);
+    *out = h;
     return FAH_OK;
   });
 }
 
-int fah_context_destroy(fah_context* c) {
-  if (!c) return FAH_OK;
-  {
-    std::lock_guard<std::mutex> lock(c->gate);
-    if (c->stream) {
-      (void)hipSetDevice(c->device);
-      (void)hipStreamSynchronize(c->stream);
-      c->batch.reset();
-      (void)hipStreamDestroy(c->stream);
-    }
-    c->disposed = true;
+// The handle goes; the state stays while weights or decoders made from it
+// exist (their later calls report FAH_ERROR_DISPOSED, their release works).
+int fah_context_destroy(fah_context* h) {
+  if (!h) return FAH_OK;
+  std::shared_ptr<Ctx> st = std::move(h->st);
+  delete h;
+  if (st) {
+    std::lock_guard<std::mutex> lock(st->gate);
+    (void)hipSetDevice(st->device);
+    (void)hipStreamSynchronize(st->stream);
+    st->batch.reset();
+    st->disposed = true;
   }
-  delete c;
   return FAH_OK;
 }
 
-int fah_context_synchronize(fah_context* c) {
-  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+int fah_context_synchronize(fah_context* h) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
   return guarded([&] {
     std::lock_guard<std::mutex> lock(c->gate);
+    check(hipSetDevice(c->device), "hipSetDevice");
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return FAH_OK;
   });
 }
 
-const char* fah_context_name(const fah_context* c) { return c ? c->name.c_str() : ""; }
+const char* fah_context_name(const fah_context* h) { return h ? h->st->name.c_str() : ""; }
 
-int fah_context_set_minimum_operations(fah_context* c, int64_t operations) {
-  if (!c || operations < 0) return fail(FAH_ERROR_ARGUMENT, "invalid minimum operations");
-  c->minimum_operations = operations;
+int fah_context_set_minimum_operations(fah_context* h, int64_t operations) {
+  if (!h || operations < 0) return fail(FAH_ERROR_ARGUMENT, "invalid minimum operations");
+  h->st->minimum_operations = operations;
   return FAH_OK;
 }
 
-void* fah_context_stream(fah_context* c) { return c ? (void*)c->stream : nullptr; }
+void* fah_context_stream(fah_context* h) { return h ? (void*)h->st->stream : nullptr; }
 
-int fah_weight_q8_upload(fah_context* c, const int8_t* quantized, const float* scales, int rows, int cols,
+int fah_weight_q8_upload(fah_context* h, const int8_t* quantized, const float* scales, int rows, int cols,
                          fah_weight** out) {
-  if (!c || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+  if (!h || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+  Ctx* c = h->st.get();
   return guarded([&] {
     require(quantized && scales, "Q8 weight needs quantized bytes and scales");
     require(rows > 0 && cols > 0 && cols % 32 == 0, "Invalid row-major Q8 dimensions");
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
-    auto* w = new fah_weight();
-    try {
-      w->context = c;
-      w->rows = rows;
-      w->cols = cols;
-      size_t nb = (size_t)rows * (cols / 32);
-      w->half_scales = scales_fit_half(scales, nb);
-      upload(w->q, quantized, (size_t)rows * cols, c->stream);
-      if (w->half_scales) {
-        std::vector<uint16_t> h(nb);
-        for (size_t i = 0; i < nb; ++i) h[i] = float_to_half_bits(scales[i]);
-        upload(w->s, h.data(), nb * 2, c->stream);
-      } else {
-        upload(w->s, scales, nb * 4, c->stream);
-      }
-      w->group_rows = pick_group_rows(rows, cols, 4, false);
-    } catch (...) {
-      delete w;
-      throw;
+    DeviceWork work(*c);
+    auto w = std::make_unique<fah_weight>();
+    w->ctx = h->st;
+    w->rows = rows;
+    w->cols = cols;
+    size_t nb = (size_t)rows * (cols / 32);
+    w->half_scales = scales_fit_half(scales, nb);
+    upload(w->q, quantized, (size_t)rows * cols, c->stream);
+    if (w->half_scales) {
+      std::vector<uint16_t> hs(nb);
+      for (size_t i = 0; i < nb; ++i) hs[i] = float_to_half_bits(scales[i]);
+      upload(w->s, hs.data(), nb * 2, c->stream);
+    } else {
+      upload(w->s, scales, nb * 4, c->stream);
     }
-    *out = w;
+    w->group_rows = pick_group_rows(rows, cols, 4, false);
+    *out = w.release();
     return FAH_OK;
   });
 }
 
-int fah_weight_q8_upload_blocks(fah_context* c, const uint8_t* blocks, int rows, int cols, fah_weight** out) {
-  if (!c || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+int fah_weight_q8_upload_blocks(fah_context* h, const uint8_t* blocks, int rows, int cols, fah_weight** out) {
+  if (!h || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+  Ctx* c = h->st.get();
   return guarded([&] {
     require(blocks != nullptr, "Q8 weight needs its GGUF blocks");
     require(rows > 0 && cols > 0 && cols % 32 == 0, "Invalid row-major Q8 dimensions");
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
     auto w = std::make_unique<fah_weight>();
-    w->context = c;
+    w->ctx = h->st;
     w->rows = rows;
     w->cols = cols;
     w->half_scales = true;
@@ -957,10 +1059,17 @@ int fah_weight_q8_upload_blocks(fah_context* c, const uint8_t* blocks, int rows,
   });
 }
 
+// Drains the context's stream first (device-pointer calls may still read the
+// weight), then frees it; valid before or after fah_context_destroy.
 int fah_weight_release(fah_weight* w) {
   if (!w) return FAH_OK;
-  (void)hipSetDevice(w->context->device);
-  delete w;
+  std::shared_ptr<Ctx> st = w->ctx;
+  {
+    std::lock_guard<std::mutex> lock(st->gate);
+    (void)hipSetDevice(st->device);
+    (void)hipStreamSynchronize(st->stream);
+    delete w;
+  }
   return FAH_OK;
 }
 
@@ -998,17 +1107,19 @@ static fah::GemvArgs weight_args(const fah_weight* w) {
   return a;
 }
 
-int fah_quantized_linear(fah_context* c, const float* input, int frames, const fah_weight* w, const float* bias,
+int fah_quantized_linear(fah_context* h, const float* input, int frames, const fah_weight* w, const float* bias,
                          float* output) {
-  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
   if (!w || frames <= 0 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
   if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return FAH_DECLINED;
   return guarded([&] {
     require(input && output, "Q8 GPU projection needs input and output");
-    require(w->context == c, "weight belongs to another context");
+    require(w->ctx.get() == c, "weight belongs to another context");
     std::lock_guard<std::mutex> lock(c->gate);
     if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
     check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
     size_t in_bytes = (size_t)frames * w->cols * 4, out_bytes = (size_t)frames * w->rows * 4;
     c->in.ensure(in_bytes + (bias ? (size_t)w->rows * 4 : 0));
     c->out.ensure(out_bytes);
@@ -1039,9 +1150,10 @@ int fah_quantized_linear(fah_context* c, const float* input, int frames, const f
   });
 }
 
-int fah_linear_many(fah_context* c, const float* input, int frames, const fah_weight* const* weights, int count,
+int fah_linear_many(fah_context* h, const float* input, int frames, const fah_weight* const* weights, int count,
                     float* const* outputs) {
-  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
   if (count == 0) return FAH_OK;
   if (!weights || count < 0 || frames <= 0) return FAH_DECLINED;
   int cols = weights[0] ? weights[0]->cols : 0;
@@ -1055,12 +1167,13 @@ int fah_linear_many(fah_context* c, const float* input, int frames, const fah_we
     require(input && outputs, "grouped projection needs input and outputs");
     for (int i = 0; i < count; ++i) {
       require(weights[i]->cols == cols, "Grouped projection dimensions differ");
-      require(weights[i]->context == c, "weight belongs to another context");
+      require(weights[i]->ctx.get() == c, "weight belongs to another context");
       require(outputs[i] != nullptr, "grouped projection output is NULL");
     }
     std::lock_guard<std::mutex> lock(c->gate);
     if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
     check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
     size_t n = (size_t)frames * cols;
     c->in.ensure(n * 4);
     c->q.ensure(n);
@@ -1098,26 +1211,31 @@ int fah_linear_many(fah_context* c, const float* input, int frames, const fah_we
   });
 }
 
-int fah_quantize_device(fah_context* c, const float* x, int64_t n, int8_t* q, float* scales) {
-  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+int fah_quantize_device(fah_context* h, const float* x, int64_t n, int8_t* q, float* scales) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
   return guarded([&] {
     require(n >= 0 && n % 32 == 0, "Quantization needs matching complete blocks");
     require(n == 0 || (x && q && scales), "NULL buffer");
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
     check(fah::launch_quantize(x, n, q, scales, c->stream), "quantize");
     return FAH_OK;
   });
 }
 
-int fah_q8_gemv_device(fah_context* c, const int8_t* q, const float* scales, int frames, const fah_weight* w,
+int fah_q8_gemv_device(fah_context* h, const int8_t* q, const float* scales, int frames, const fah_weight* w,
                        float* out) {
-  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
   if (!w || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
   return guarded([&] {
     require(frames > 0 && q && scales && out, "invalid GEMV arguments");
+    require(w->ctx.get() == c, "weight belongs to another context");
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
     if (gemm_fits(w, frames)) {
       launch_weight_gemm(w, q, scales, frames, out, nullptr, c->stream);
     } else {
@@ -1132,21 +1250,25 @@ int fah_q8_gemv_device(fah_context* c, const int8_t* q, const float* scales, int
   });
 }
 
-int fah_q8_block_dots_device(fah_context* c, const int8_t* q, const fah_weight* w, int32_t* dots) {
-  if (!c) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+int fah_q8_block_dots_device(fah_context* h, const int8_t* q, const fah_weight* w, int32_t* dots) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
   return guarded([&] {
     require(w && q && dots, "invalid block-dot arguments");
+    require(w->ctx.get() == c, "weight belongs to another context");
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
     check(fah::launch_block_dots(q, w->q.as<int8_t>(), w->rows, w->cols, dots, c->stream), "block dots");
     return FAH_OK;
   });
 }
 
-int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_layer_host* layers,
+int fah_decoder_create(fah_context* h, const fah_decoder_config* cfg, const fah_layer_host* layers,
                        const fah_q8_host* token_embd, const fah_q8_host* output, const float* output_norm,
                        fah_decoder** out) {
-  if (!c || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+  if (!h || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+  Ctx* c = h->st.get();
   return guarded([&] {
     require(cfg && layers && token_embd && output_norm, "decoder needs config, layers, embeddings and norm");
     const fah_decoder_config& k = *cfg;
@@ -1178,9 +1300,10 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
 
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
     check(fah::prepare_attention(k.capacity, k.head_size), "attention LDS budget");
     auto d = std::make_unique<fah_decoder>();
-    d->context = c;
+    d->ctx = h->st;
     d->cfg = k;
     d->q_width = q_width;
     d->kv_width = kv_width;
@@ -1321,10 +1444,11 @@ int fah_decoder_create(fah_context* c, const fah_decoder_config* cfg, const fah_
 
 int fah_decoder_destroy(fah_decoder* d) {
   if (!d) return FAH_OK;
-  std::lock_guard<std::mutex> lock(d->context->gate);
-  (void)hipSetDevice(d->context->device);
-  (void)hipStreamSynchronize(d->context->stream);
-  auto& batch = d->context->batch;
+  std::shared_ptr<Ctx> st = d->ctx;
+  std::lock_guard<std::mutex> lock(st->gate);
+  (void)hipSetDevice(st->device);
+  (void)hipStreamSynchronize(st->stream);
+  auto& batch = st->batch;
   if (batch && std::find(batch->members.begin(), batch->members.end(), d) != batch->members.end()) batch.reset();
   for (hipGraphExec_t g : {d->graph_row, d->graph_logits, d->graph_step})
     if (g) (void)hipGraphExecDestroy(g);
@@ -1332,14 +1456,53 @@ int fah_decoder_destroy(fah_decoder* d) {
   return FAH_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Decoder calls after fah_context_destroy report FAH_ERROR_DISPOSED (the
+// reference's ObjectDisposedException, VulkanQuantizedBackend.cs:54-56).
+struct DisposedError {};
+void require_live(const fah_decoder* d) {
+  if (d->ctx->disposed) throw DisposedError{};
+}
+
+template <typename F>
+int guarded_decoder(F&& f) {
+  return guarded([&] {
+    try {
+      return f();
+    } catch (const DisposedError&) {
+      return fail(FAH_ERROR_DISPOSED, "decoder used after its context was destroyed");
+    }
+  });
+}
+
+// Device section of a decoder call: exclusive use of the device around
+// persistent launches, the plain enqueue lock otherwise.
+struct DecoderSection {
+  std::optional<PersistentSection> persistent;
+  std::optional<DeviceWork> work;
+  DecoderSection(fah_decoder* d, bool exclusive) {
+    if (exclusive && d->persistent) persistent.emplace(*d->ctx);
+    else work.emplace(*d->ctx);
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
 int fah_decoder_set_position(fah_decoder* d, int position) {
   if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
-  return guarded([&] {
+  return guarded_decoder([&] {
     require(position >= 0 && position <= d->cfg.capacity, "position out of range");
-    std::lock_guard<std::mutex> lock(d->context->gate);
-    check(hipSetDevice(d->context->device), "hipSetDevice");
-    check(hipMemcpyAsync(d->position.ptr, &position, 4, hipMemcpyHostToDevice, d->context->stream), "H2D");
-    check(hipStreamSynchronize(d->context->stream), "sync");
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    DeviceWork work(*d->ctx);
+    check(hipMemcpyAsync(d->position.ptr, &position, 4, hipMemcpyHostToDevice, d->ctx->stream), "H2D");
+    check(hipStreamSynchronize(d->ctx->stream), "sync");
     d->host_position = position;
     d->have_logits = false;
     return FAH_OK;
@@ -1354,28 +1517,33 @@ int fah_decoder_position(const fah_decoder* d, int* position) {
 
 int fah_decoder_decode(fah_decoder* d, const float* embeddings, int frames, float* logits) {
   if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
-  return guarded([&] {
+  return guarded_decoder([&] {
     require(embeddings && frames >= 1 && d->host_position + frames <= d->cfg.capacity,
             "Decoder context exhausted or invalid embeddings");
-    std::lock_guard<std::mutex> lock(d->context->gate);
-    hipStream_t s = d->context->stream;
-    check(hipSetDevice(d->context->device), "hipSetDevice");
-    size_t row = (size_t)d->cfg.width * 4;
-    d->staging.ensure(row * frames);
-    check(hipMemcpyAsync(d->staging.ptr, embeddings, row * frames, hipMemcpyHostToDevice, s), "H2D embeddings");
-    if (use_prefill(d, frames)) {
-      prefill(d, d->staging.as<float>(), frames, logits != nullptr, s);
-    } else {
-      for (int f = 0; f < frames; ++f) {
-        check(hipMemcpyAsync(d->x.ptr, d->staging.as<char>() + row * f, row, hipMemcpyDeviceToDevice, s), "D2D row");
-        bool last = f == frames - 1;
-        run_kind(d, last && logits ? 1 : 0, s, d->host_position + f);
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
+    hipStream_t s = d->ctx->stream;
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    const bool batched = use_prefill(d, frames);
+    {
+      DecoderSection section(d, !batched);
+      size_t row = (size_t)d->cfg.width * 4;
+      d->staging.ensure(row * frames);
+      check(hipMemcpyAsync(d->staging.ptr, embeddings, row * frames, hipMemcpyHostToDevice, s), "H2D embeddings");
+      if (batched) {
+        prefill(d, d->staging.as<float>(), frames, logits != nullptr, s);
+      } else {
+        for (int f = 0; f < frames; ++f) {
+          check(hipMemcpyAsync(d->x.ptr, d->staging.as<char>() + row * f, row, hipMemcpyDeviceToDevice, s), "D2D row");
+          bool last = f == frames - 1;
+          run_kind(d, last && logits ? 1 : 0, s, d->host_position + f);
+        }
       }
+      if (logits)
+        check(hipMemcpyAsync(logits, d->logits.ptr, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, s), "D2H");
+      check(hipStreamSynchronize(s), "hipStreamSynchronize");
     }
-    if (logits)
-      check(hipMemcpyAsync(logits, d->logits.ptr, (size_t)d->cfg.vocab * 4, hipMemcpyDeviceToHost, s), "D2H");
-    check(hipStreamSynchronize(s), "hipStreamSynchronize");
-    check_step_error(d);
+    recover_step_error(d);
     d->host_position += frames;
     d->have_logits = logits != nullptr;
     return FAH_OK;
@@ -1384,12 +1552,14 @@ int fah_decoder_decode(fah_decoder* d, const float* embeddings, int frames, floa
 
 int fah_decoder_embed(fah_decoder* d, const int32_t* tokens, int count, float* out) {
   if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
-  return guarded([&] {
+  return guarded_decoder([&] {
     require(count >= 0 && (count == 0 || (tokens && out)), "invalid embed arguments");
     for (int i = 0; i < count; ++i) require(tokens[i] >= 0 && tokens[i] < d->cfg.vocab, "token out of range");
-    std::lock_guard<std::mutex> lock(d->context->gate);
-    hipStream_t s = d->context->stream;
-    check(hipSetDevice(d->context->device), "hipSetDevice");
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
+    hipStream_t s = d->ctx->stream;
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    DeviceWork work(*d->ctx);
     d->staging.ensure((size_t)d->cfg.width * 4 + 16);
     int* tok = reinterpret_cast<int*>(d->staging.as<char>() + (size_t)d->cfg.width * 4);
     for (int i = 0; i < count; ++i) {
@@ -1408,43 +1578,64 @@ int fah_decoder_embed(fah_decoder* d, const int32_t* tokens, int count, float* o
 
 int fah_decoder_greedy(fah_decoder* d, int32_t* token) {
   if (!d || !token) return fail(FAH_ERROR_ARGUMENT, "decoder/token is NULL");
-  return guarded([&] {
+  return guarded_decoder([&] {
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
     if (!d->have_logits) return fail(FAH_ERROR_STATE, "no logits: decode with logits first");
-    std::lock_guard<std::mutex> lock(d->context->gate);
-    check(hipSetDevice(d->context->device), "hipSetDevice");
-    check(hipMemcpyAsync(token, d->token.ptr, 4, hipMemcpyDeviceToHost, d->context->stream), "D2H token");
-    check(hipStreamSynchronize(d->context->stream), "sync");
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    DeviceWork work(*d->ctx);
+    check(hipMemcpyAsync(token, d->token.ptr, 4, hipMemcpyDeviceToHost, d->ctx->stream), "D2H token");
+    check(hipStreamSynchronize(d->ctx->stream), "sync");
     return FAH_OK;
   });
 }
 
 int fah_decoder_generate(fah_decoder* d, int steps, int32_t* tokens) {
   if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
-  return guarded([&] {
+  return guarded_decoder([&] {
     require(steps >= 0 && (steps == 0 || tokens), "invalid generate arguments");
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
     if (!d->have_logits) return fail(FAH_ERROR_STATE, "no logits: decode with logits first");
     require(d->host_position + steps <= d->cfg.capacity, "Decoder context exhausted");
-    std::lock_guard<std::mutex> lock(d->context->gate);
-    hipStream_t s = d->context->stream;
-    check(hipSetDevice(d->context->device), "hipSetDevice");
-    check(hipMemsetAsync(d->history_count.ptr, 0, 4, s), "reset history");
-    for (int i = 0; i < steps; ++i) run_kind(d, 2, s, d->host_position + i);
-    if (steps > 0)
-      check(hipMemcpyAsync(tokens, d->history.ptr, (size_t)steps * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
-    check(hipStreamSynchronize(s), "hipStreamSynchronize");
-    check_step_error(d);
+    hipStream_t s = d->ctx->stream;
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    {
+      DecoderSection section(d, true);
+      check(hipMemsetAsync(d->history_count.ptr, 0, 4, s), "reset history");
+      for (int i = 0; i < steps; ++i) run_kind(d, 2, s, d->host_position + i);
+      if (steps > 0)
+        check(hipMemcpyAsync(tokens, d->history.ptr, (size_t)steps * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
+      check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    }
+    recover_step_error(d);
     d->host_position += steps;
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_fail_next_step(fah_decoder* d) {
+  if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
+  return guarded_decoder([&] {
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
+    if (!d->persistent) return FAH_DECLINED;
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    DeviceWork work(*d->ctx);
+    const unsigned preset = kErrorPreset;
+    check(hipMemcpyAsync(d->error.ptr, &preset, 4, hipMemcpyHostToDevice, d->ctx->stream), "H2D error word");
+    check(hipStreamSynchronize(d->ctx->stream), "sync");
     return FAH_OK;
   });
 }
 
 int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** out) {
   if (!parent || !out) return fail(FAH_ERROR_ARGUMENT, "parent/session is NULL");
-  return guarded([&] {
+  return guarded_decoder([&] {
     require(capacity >= 1, "capacity must be positive");
-    fah_context* c = parent->context;
+    Ctx* c = parent->ctx.get();
     auto d = std::make_unique<fah_decoder>();
-    d->context = c;
+    d->ctx = parent->ctx;
     d->cfg = parent->cfg;
     d->cfg.capacity = capacity;
     d->q_width = parent->q_width;
@@ -1459,7 +1650,9 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
     require(fah::attention_slices(capacity, d->cfg.head_size) != 0,
             "capacity exceeds the attention kernel's LDS budget");
     std::lock_guard<std::mutex> lock(c->gate);
+    require_live(parent);
     check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
     check(fah::prepare_attention(capacity, d->cfg.head_size), "attention LDS budget");
     init_state(d.get(), c->stream);
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
@@ -1470,7 +1663,7 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
 
 int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int steps, int32_t* tokens) {
   if (!sessions || count < 1) return fail(FAH_ERROR_ARGUMENT, "no sessions");
-  return guarded([&] {
+  return guarded_decoder([&] {
     require(count <= fah::kFewFrames, "at most " + std::to_string(fah::kFewFrames) + " sessions per batch");
     require(steps >= 0 && (steps == 0 || tokens), "invalid generate arguments");
     const fah_decoder* d0 = sessions[0];
@@ -1484,7 +1677,7 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
     for (int i = 0; i < count; ++i) {
       const fah_decoder* d = sessions[i];
       require(d != nullptr, "session is NULL");
-      require(d->wt == d0->wt && d->context == d0->context, "sessions must share one decoder's weights");
+      require(d->wt == d0->wt && d->ctx == d0->ctx, "sessions must share one decoder's weights");
       for (int j = 0; j < i; ++j) require(sessions[j] != d, "a session appears twice");
       if (!d->have_logits)
         return fail(FAH_ERROR_STATE, "session " + std::to_string(i) + " has no logits: decode with logits first");
@@ -1494,10 +1687,12 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
       bound = std::max(bound, std::min(d->cfg.capacity, kSessionPositions));
     }
     if (steps == 0) return FAH_OK;
-    fah_context* c = d0->context;
+    Ctx* c = d0->ctx.get();
     std::lock_guard<std::mutex> lock(c->gate);
+    require_live(d0);
     hipStream_t s = c->stream;
     check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
     std::vector<fah_decoder*> members(sessions, sessions + count);
     if (!c->batch || c->batch->members != members || c->batch->max_positions != bound) {
       c->batch.reset();
@@ -1568,13 +1763,15 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
 
 int fah_decoder_kv_write(fah_decoder* d, int layer, const uint16_t* keys, const uint16_t* values, int positions) {
   if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
-  return guarded([&] {
+  return guarded_decoder([&] {
     const fah_decoder_config& k = d->cfg;
     require(layer >= 0 && layer < k.layers && positions >= 0 && positions <= k.capacity && keys && values,
             "invalid KV write");
-    std::lock_guard<std::mutex> lock(d->context->gate);
-    hipStream_t s = d->context->stream;
-    check(hipSetDevice(d->context->device), "hipSetDevice");
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
+    hipStream_t s = d->ctx->stream;
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    DeviceWork work(*d->ctx);
     size_t layer_elems = (size_t)k.kv_heads * k.capacity * k.head_size;
     for (int h = 0; h < k.kv_heads; ++h) {
       // host [t][h][c] -> device [h][t][c]
@@ -1594,13 +1791,15 @@ int fah_decoder_kv_write(fah_decoder* d, int layer, const uint16_t* keys, const 
 
 int fah_decoder_kv_read(fah_decoder* d, int layer, uint16_t* keys, uint16_t* values, int positions) {
   if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
-  return guarded([&] {
+  return guarded_decoder([&] {
     const fah_decoder_config& k = d->cfg;
     require(layer >= 0 && layer < k.layers && positions >= 0 && positions <= k.capacity && keys && values,
             "invalid KV read");
-    std::lock_guard<std::mutex> lock(d->context->gate);
-    hipStream_t s = d->context->stream;
-    check(hipSetDevice(d->context->device), "hipSetDevice");
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
+    hipStream_t s = d->ctx->stream;
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    DeviceWork work(*d->ctx);
     size_t layer_elems = (size_t)k.kv_heads * k.capacity * k.head_size;
     for (int h = 0; h < k.kv_heads; ++h) {
       check(hipMemcpy2DAsync(keys + (size_t)h * k.head_size, (size_t)d->kv_width * 2,
@@ -1624,37 +1823,44 @@ int fah_decoder_persistent(const fah_decoder* d) { return d && d->persistent ? (
 int fah_decoder_timeline(fah_decoder* d, uint64_t* ticks, int count) {
   if (!d || !ticks) return fail(FAH_ERROR_ARGUMENT, "decoder/ticks is NULL");
   if (!d->timeline.ptr) return FAH_DECLINED;
-  return guarded([&] {
+  return guarded_decoder([&] {
     require(count >= 0 && count <= d->blocks * fah::kTimelineEvents, "invalid timeline size");
-    std::lock_guard<std::mutex> lock(d->context->gate);
-    check(hipSetDevice(d->context->device), "hipSetDevice");
-    check(hipStreamSynchronize(d->context->stream), "sync");
-    check(hipMemcpy(ticks, d->timeline.ptr, (size_t)count * 8, hipMemcpyDeviceToHost), "D2H timeline");
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    DeviceWork work(*d->ctx);
+    check(hipMemcpyAsync(ticks, d->timeline.ptr, (size_t)count * 8, hipMemcpyDeviceToHost, d->ctx->stream),
+          "D2H timeline");
+    check(hipStreamSynchronize(d->ctx->stream), "sync");
     return FAH_OK;
   });
 }
 
 int fah_decoder_trace(fah_decoder* d, int which, float* out, int count) {
   if (!d) return fail(FAH_ERROR_ARGUMENT, "decoder is NULL");
-  return guarded([&] {
+  return guarded_decoder([&] {
     const fah_decoder_config& k = d->cfg;
     const int sizes[5] = {k.width, d->q_width + 2 * d->kv_width, d->q_width, k.width, k.ffn};
     require(which >= 0 && which < 5 && out && count >= 0 && count <= sizes[which], "invalid trace request");
-    std::lock_guard<std::mutex> lock(d->context->gate);
-    check(hipSetDevice(d->context->device), "hipSetDevice");
-    hipStream_t s = d->context->stream;
-    check(hipStreamSynchronize(s), "sync");
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
+    check(hipSetDevice(d->ctx->device), "hipSetDevice");
+    DeviceWork work(*d->ctx);
+    hipStream_t s = d->ctx->stream;
     if (d->persistent) {
       DeviceBuffer* tagged[5] = {&d->tx, &d->tqkv, &d->tatt, &d->ta, &d->th};
       std::vector<unsigned long long> words(count);
-      check(hipMemcpy(words.data(), tagged[which]->ptr, (size_t)count * 8, hipMemcpyDeviceToHost), "D2H trace");
+      check(hipMemcpyAsync(words.data(), tagged[which]->ptr, (size_t)count * 8, hipMemcpyDeviceToHost, s),
+            "D2H trace");
+      check(hipStreamSynchronize(s), "sync");
       for (int i = 0; i < count; ++i) {
         uint32_t bits = (uint32_t)words[i];
         std::memcpy(&out[i], &bits, 4);
       }
     } else {
       DeviceBuffer* plain[5] = {&d->x, &d->qkv_out, &d->attn, &d->a, &d->h};
-      check(hipMemcpy(out, plain[which]->ptr, (size_t)count * 4, hipMemcpyDeviceToHost), "D2H trace");
+      check(hipMemcpyAsync(out, plain[which]->ptr, (size_t)count * 4, hipMemcpyDeviceToHost, s), "D2H trace");
+      check(hipStreamSynchronize(s), "sync");
     }
     return FAH_OK;
   });

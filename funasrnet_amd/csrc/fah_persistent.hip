@@ -794,6 +794,14 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int ct = tid - kMem;  // compute-lane index (negative in the memory waves)
   const int L = a.layers;
   const int pos = *a.position;
+  // A set error word (an earlier launch failed, or the host stopped the
+  // step) ends every launch here until the host has restored the state; a
+  // position outside the cache ends it before anything is written.
+  if (error_load(a.error) != 0) return;
+  if (pos < 0 || pos >= a.capacity) {
+    if (tid == 0) __hip_atomic_fetch_or(a.error, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   const uint32_t gen0 = *a.epoch * (uint32_t)(5 * L + 2) + 1u;
   const int chunks = (a.vocab + HR - 1) / HR;
   auto gen = [&](int l, int p) { return gen0 + (uint32_t)(5 * l + p); };

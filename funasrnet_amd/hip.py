@@ -91,6 +91,7 @@ SIGNATURES = {
     "fah_decoder_persistent": (ctypes.c_int, [_vp]),
     "fah_decoder_trace": (ctypes.c_int, [_vp, ctypes.c_int, _f32p, ctypes.c_int]),
     "fah_decoder_timeline": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int]),
+    "fah_decoder_fail_next_step": (ctypes.c_int, [_vp]),
 }
 
 _lib = None

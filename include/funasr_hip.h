@@ -17,8 +17,17 @@
  *                     returns the message for the calling thread.
  * Host pointers are only read or written during the call. Weights are copied
  * to the device once at upload and are immutable afterwards. A context owns
- * one HIP stream; calls on one context are serialised by the library, calls
- * on different contexts may run concurrently.
+ * one HIP stream; calls on one context are serialised by the library. Calls
+ * on different contexts may be made from different threads: their work is
+ * enqueued under a per-device lock, and a persistent decode step (which
+ * needs every CU of the device) first waits for the work already enqueued
+ * by the other contexts and keeps the device to itself until it has
+ * finished, so their kernels never run beside it.
+ *
+ * Lifetime: weights and decoders keep their context's state alive.
+ * fah_context_destroy releases the handle (which must not be used again);
+ * later calls on its weights and decoders return FAH_ERROR_DISPOSED, and
+ * fah_weight_release / fah_decoder_destroy still free them, in any order.
  */
 #ifndef FUNASR_HIP_H
 #define FUNASR_HIP_H
@@ -239,6 +248,16 @@ int fah_decoder_trace(fah_decoder* decoder, int which, float* out, int count);
  * rocprof-style per-op timing of the reference's LinearMeasured callback
  * (src/FunAsrNet/TensorMath.cs:37-40) for a single-launch step. */
 int fah_decoder_timeline(fah_decoder* decoder, uint64_t* ticks, int count);
+
+/* Test hook for the persistent step's failure path: presets the device
+ * error word, so that the next persistent launch of this decoder ends at its
+ * entry check (every workgroup exits normally) and the call reports
+ * FAH_ERROR_DEVICE. The failed call restores the device state from the
+ * host's (position, epoch, empty history) and drops its logits, as after an
+ * exchange that timed out. FAH_DECLINED when the decoder does not run the
+ * persistent step. No reference counterpart (the reference's failure path is
+ * a thrown exception, Vk.cs:57-61). */
+int fah_decoder_fail_next_step(fah_decoder* decoder);
 
 /* 2 when decode steps run as one persistent launch with XCD-local roles
  * (workgroups take their role from the XCD they run on, and hand data to

@@ -93,7 +93,8 @@ def test_long_cache_matches_graph_path(backend, oracle_lib, shape):
     """A cache pre-filled with 4096 F16 N(0,1) rows in every layer: the
     persistent kernel (staged rows, spill area and global rows) and the
     per-kernel path (16 channel slices at this capacity) give identical
-    logits bits, K/V rows and tokens; the small shape matches the oracle."""
+    logits bits, K/V rows and tokens, and match the oracle (the full-size
+    shape too: the long-cache decode of survey config 3, 8 steps)."""
     cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
     w = model.synthetic(cfg, seed=12)
     positions, capacity, steps = 4096, 4224, 8
@@ -122,22 +123,27 @@ def test_long_cache_matches_graph_path(backend, oracle_lib, shape):
             assert np.array_equal(kf.view(np.uint16), ks.view(np.uint16))
             assert np.array_equal(vf.view(np.uint16), vs.view(np.uint16))
             assert np.array_equal(kf[:positions * cfg.kv_width].view(np.uint16), kv[layer][0].view(np.uint16).ravel())
-        if shape == "small":
-            ref = oracle_lib.Decoder(w, capacity=capacity)
-            try:
-                for layer, (k, v) in enumerate(kv):
-                    ref.set_kv(layer, k.astype(np.float32), v.astype(np.float32))
-                ref.set_position(positions)
-                lr = ref.decode(x, 1)
-                assert np.abs(lf.astype(np.float64) - lr).max() <= 1e-2
-                expected = []
-                for _ in range(steps):
-                    t = oracle_lib.greedy(lr)
-                    expected.append(t)
-                    lr = ref.decode(ref.embed([t]), 1)
-                assert tf.tolist() == expected
-            finally:
-                ref.close()
+        ref = oracle_lib.Decoder(w, capacity=capacity)
+        try:
+            for layer, (k, v) in enumerate(kv):
+                ref.set_kv(layer, k.astype(np.float32), v.astype(np.float32))
+            ref.set_position(positions)
+            lr = ref.decode(x, 1)
+            assert np.abs(lf.astype(np.float64) - lr).max() <= 1e-2
+            assert np.array_equal(lf.view(np.uint32), lr.view(np.uint32))
+            expected = []
+            for _ in range(steps):
+                t = oracle_lib.greedy(lr)
+                expected.append(t)
+                lr = ref.decode(ref.embed([t]), 1)
+            assert tf.tolist() == expected
+            for layer in (0, cfg.layers - 1):
+                kf, vf = fast.kv_read(layer, positions + 1 + steps)
+                ko, vo = ref.kv(layer)
+                assert np.array_equal(kf.astype(np.float32), ko.reshape(kf.shape)), layer
+                assert np.array_equal(vf.astype(np.float32), vo.reshape(vf.shape)), layer
+        finally:
+            ref.close()
     finally:
         fast.close()
         slow.close()

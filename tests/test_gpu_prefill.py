@@ -35,8 +35,12 @@ def _decode(decoder, x, row_by_row):
 
 
 @pytest.mark.parametrize("shape,frames", [("small", 5), ("small", 16), ("small", 37), ("small", 130),
-                                          ("qwen3", 12), ("qwen3", 150)])
+                                          ("qwen3", 12), ("qwen3", 150), ("qwen3", 375), ("qwen3", 750)])
 def test_prefill_matches_row_by_row(backend, oracle_lib, shape, frames):
+    """Every size, including the long audio prefixes of 375 and 750 rows:
+    the batched prefill equals the row-by-row decode bit for bit (logits and
+    every layer's K/V rows), and matches the oracle (logits within the
+    tolerance and bit-identical, the greedy token, then 8 generated tokens)."""
     from funasrnet_amd.hip import HipDecoder
     cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
     w = model.synthetic(cfg, seed=5)
@@ -57,16 +61,27 @@ def test_prefill_matches_row_by_row(backend, oracle_lib, shape, frames):
         tb = batched.generate(8)
         tr = rows.generate(8)
         assert np.array_equal(tb, tr)
-        if shape == "small":
-            ref = oracle_lib.Decoder(w, capacity=capacity)
-            try:
-                lo = ref.decode(prefix, frames)
-                diff = np.abs(lb.astype(np.float64) - lo.astype(np.float64))
-                assert diff.max() <= ATOL
-                assert np.all(diff <= RTOL * np.maximum(1.0, np.abs(lo)))
-                assert int(np.argmax(lo)) == int(tb[0])
-            finally:
-                ref.close()
+        ref = oracle_lib.Decoder(w, capacity=capacity)
+        try:
+            lo = ref.decode(prefix, frames)
+            diff = np.abs(lb.astype(np.float64) - lo.astype(np.float64))
+            assert diff.max() <= ATOL
+            assert np.all(diff <= RTOL * np.maximum(1.0, np.abs(lo)))
+            assert np.array_equal(lb.view(np.uint32), lo.view(np.uint32))
+            assert int(np.argmax(lo)) == int(tb[0]) == oracle_lib.greedy(lo)
+            for layer in (0, cfg.layers - 1):
+                kb, vb = batched.kv_read(layer, frames)
+                ko, vo = ref.kv(layer)
+                assert np.array_equal(kb.astype(np.float32), ko.reshape(kb.shape)), layer
+                assert np.array_equal(vb.astype(np.float32), vo.reshape(vb.shape)), layer
+            expected = []
+            for _ in range(8):
+                t = oracle_lib.greedy(lo)
+                expected.append(t)
+                lo = ref.decode(ref.embed([t]), 1)
+            assert tb.tolist() == expected
+        finally:
+            ref.close()
     finally:
         batched.close()
         rows.close()
