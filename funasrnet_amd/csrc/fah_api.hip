@@ -241,6 +241,32 @@ struct PersistentSection {
   ~PersistentSection() { (void)hipStreamSynchronize(c.stream); }
 };
 
+// Workspace of fah_quantized_linear_noalloc: the staged input, bias and
+// output and the quantised activations, in one fixed device array per GPU
+// (no hipMalloc on that path). Host code never passes `scratch` itself (its
+// host-side name is not a device address): it uses the address that
+// hipGetSymbolAddress returned for the device, kept in scratch_ptr.
+constexpr size_t kScratchBytes = 8u << 20;
+}  // namespace
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+namespace {
+std::mutex g_scratch_gate;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Once per device, with that device current (called by fah_context_create).
+void init_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_gate);
+  if (g_scratch_ptr[device]) return;
+  void* ptr = nullptr;
+  check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  g_scratch_ptr[device] = ptr;
+}
+
+void* scratch_ptr(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_gate);
+  return g_scratch_ptr[device];
+}
+
 }  // namespace
 
 struct fah_context {
@@ -952,6 +978,7 @@ int fah_context_create(int device, fah_context** out) {
     check(hipSetDevice(device), "hipSetDevice");
     auto st = std::make_shared<Ctx>();
     st->device = device;
+    init_scratch(device);
     hipStream_t stream = nullptr;
     check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
     st->stream = stream;
@@ -1145,6 +1172,55 @@ int fah_quantized_linear(fah_context* h, const float* input, int frames, const f
       check(fah::launch_gemv(a, w->half_scales, fah::kInputFloat, fah::kOutPlain, frames, c->stream), "gemv");
     }
     check(hipMemcpyAsync(output, c->out.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return FAH_OK;
+  });
+}
+
+int fah_quantized_linear_noalloc(fah_context* h, const float* input, int frames, const fah_weight* w,
+                                 const float* bias, float* output) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
+  if (!w || frames <= 0 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
+  if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return FAH_DECLINED;
+  return guarded([&] {
+    require(input && output, "Q8 GPU projection needs input and output");
+    require(w->ctx.get() == c, "weight belongs to another context");
+    auto aligned = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const size_t in_bytes = (size_t)frames * w->cols * 4, out_bytes = (size_t)frames * w->rows * 4;
+    const size_t n = (size_t)frames * w->cols;
+    const size_t at_bias = aligned(in_bytes), at_out = at_bias + aligned(bias ? (size_t)w->rows * 4 : 0);
+    const size_t at_q = at_out + aligned(out_bytes), at_s = at_q + aligned(n), end = at_s + aligned(n / 32 * 4);
+    require(end <= kScratchBytes, "projection needs " + std::to_string(end) +
+                                      " bytes of workspace; the allocation-free path holds " +
+                                      std::to_string(kScratchBytes));
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    char* base = static_cast<char*>(scratch_ptr(c->device));
+    require(base != nullptr, "no workspace for this device");
+    // Held until the work has finished: no other call of this library can
+    // use the device's workspace meanwhile.
+    std::lock_guard<std::mutex> device(device_gate(c->device).m);
+    float* din = reinterpret_cast<float*>(base);
+    float* dbias = bias ? reinterpret_cast<float*>(base + at_bias) : nullptr;
+    float* dout = reinterpret_cast<float*>(base + at_out);
+    check(hipMemcpyAsync(din, input, in_bytes, hipMemcpyHostToDevice, c->stream), "H2D input");
+    if (bias) check(hipMemcpyAsync(dbias, bias, (size_t)w->rows * 4, hipMemcpyHostToDevice, c->stream), "H2D bias");
+    if (gemm_fits(w, frames)) {
+      int8_t* q = reinterpret_cast<int8_t*>(base + at_q);
+      float* sc = reinterpret_cast<float*>(base + at_s);
+      check(fah::launch_quantize(din, (int64_t)n, q, sc, c->stream), "quantize");
+      launch_weight_gemm(w, q, sc, frames, dout, dbias, c->stream);
+    } else {
+      fah::GemvArgs a = weight_args(w);
+      a.x = din;
+      a.out = dout;
+      a.out_rows = w->rows;
+      a.bias = dbias;
+      check(fah::launch_gemv(a, w->half_scales, fah::kInputFloat, fah::kOutPlain, frames, c->stream), "gemv");
+    }
+    check(hipMemcpyAsync(output, dout, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return FAH_OK;
   });

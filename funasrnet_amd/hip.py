@@ -68,6 +68,7 @@ SIGNATURES = {
     "fah_weight_release": (ctypes.c_int, [_vp]),
     "fah_weight_device_bytes": (ctypes.c_int64, [_vp]),
     "fah_quantized_linear": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, _vp, _f32p, _f32p]),
+    "fah_quantized_linear_noalloc": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, _vp, _f32p, _f32p]),
     "fah_linear_many": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, ctypes.POINTER(_vp), ctypes.c_int,
                                        ctypes.POINTER(_f32p)]),
     "fah_quantize_device": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, _vp, _vp]),

@@ -112,6 +112,21 @@ int64_t fah_weight_device_bytes(const fah_weight* weight);
 int fah_quantized_linear(fah_context* context, const float* input, int frames, const fah_weight* weight,
                          const float* bias, float* output);
 
+/* fah_quantized_linear without any device allocation. No counterpart in the
+ * reference: for callers that cannot allocate device memory (tight serving
+ * loops, code that must not call hipMalloc). Same arguments, results
+ * (bit for bit), declines and errors as fah_quantized_linear; the staged
+ * input, bias and output and the quantised activations live in a fixed
+ * 8 MiB workspace per GPU (a static device array, held until the process
+ * ends) instead of context buffers. A projection whose workspace
+ * (frames*cols*5.125 + rows*4*(frames+1) bytes, each part rounded up to 256)
+ * exceeds 8 MiB is rejected with FAH_ERROR_ARGUMENT. Nothing in the
+ * workspace needs to start at zero. Calls that overlap on one GPU would race
+ * on its workspace: the library serialises them (the call keeps the
+ * device's work lock until its output is back). */
+int fah_quantized_linear_noalloc(fah_context* context, const float* input, int frames, const fah_weight* weight,
+                                 const float* bias, float* output);
+
 /* IGroupedComputeBackend.TryLinearMany
  * (src/FunAsrNet/IGroupedComputeBackend.cs:4-13; CPU version
  * src/FunAsrNet/TensorMath.Interleaved.cs:22-46): one shared activation
