@@ -233,9 +233,10 @@ __device__ __forceinline__ void score8(float* acc, const uint4& kk, const float*
 }
 
 __device__ __forceinline__ float nan_max_p(float a, float b) {
-  if (a != a) return a;
-  if (b != b) return b;
-  return b > a ? b : a;
+  // Selects, not branches: a if a is NaN, else b if b is NaN, else the larger.
+  const float larger = b > a ? b : a;
+  const float r = b != b ? b : larger;
+  return a != a ? a : r;
 }
 
 // nan_max_p over the 64 lanes of a wave (all active), in every lane.

@@ -150,7 +150,7 @@ struct NoChunk {
 };
 
 template <class Pre, class OnChunk = NoChunk>
-__device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int o1, const u64* s2, int n2, int o2,
+__device__ __forceinline__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int o1, const u64* s2, int n2, int o2,
                        uint32_t gen, u64* tag, unsigned* error, Pre pre, int part = 0, int parts = 1,
                        OnChunk on_chunk = OnChunk{}, u64* seen = nullptr, uint32_t tmask = ~0u) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -246,7 +246,7 @@ __device__ bool gather(const u64* s0, int n0, int o0, const u64* s1, int n1, int
 // current instead of a sentinel's round trip plus a read's. Each lane's
 // 16 bytes land in LDS whole, so every tagged word it checks is intact.
 template <class Pre>
-__device__ bool gather_qkv(const u64* q, const u64* k, const u64* v, uint32_t gen, u64* tag, unsigned* error, Pre pre,
+__device__ __forceinline__ bool gather_qkv(const u64* q, const u64* k, const u64* v, uint32_t gen, u64* tag, unsigned* error, Pre pre,
                            u64* seen = nullptr) {
   const int lane = threadIdx.x & (kWave - 1);
   pre();
@@ -632,7 +632,7 @@ __device__ __forceinline__ void unpack_qblocks(const u64* tag, int* xq, float* x
 // L2 or to memory) into blk until all carry `gen`, two polls in flight as
 // gather_qkv. False after a timeout or another workgroup's error.
 template <int NW>
-__device__ bool poll_words(const u64* at, uint32_t gen, u64* blk, unsigned* error, u64* seen, uint32_t tmask = ~0u) {
+__device__ __forceinline__ bool poll_words(const u64* at, uint32_t gen, u64* blk, unsigned* error, u64* seen, uint32_t tmask = ~0u) {
   const int lane = threadIdx.x & (kWave - 1);
   static_assert(NW % 2 == 0 && NW <= 2 * kWave, "16 bytes per lane");
   auto poll = [&] {
@@ -661,7 +661,7 @@ __device__ bool poll_words(const u64* at, uint32_t gen, u64* blk, unsigned* erro
 // One wave: wait for the 64 activations of blocks 2n and 2n + 1 of a
 // vector (tagged words src[64n, +64), staged in blk), quantise them and
 // publish both blocks (one whole line) in exchange form at dst.
-__device__ bool publish_pair(const u64* src, u64* dst, int n, uint32_t gen, u64* blk, unsigned* error,
+__device__ __forceinline__ bool publish_pair(const u64* src, u64* dst, int n, uint32_t gen, u64* blk, unsigned* error,
                              u64* seen = nullptr) {
   const int lane = threadIdx.x & (kWave - 1);
   if (!poll_words<64>(src + 64 * n, gen, blk, error, seen)) return false;
@@ -779,7 +779,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ int flag_s;
   __shared__ int okw_s[kMem / kWave];  // per memory wave: its part of the last gather completed
   __shared__ __attribute__((aligned(16))) float cur_s[3][128];  // attention: q, k, v of the current position
-  __shared__ float tmax_s[kPT / kWave];
+  __shared__ __attribute__((aligned(16))) float tmax_s[kPT / kWave];
   __shared__ float inv_s;
   __shared__ __attribute__((aligned(16))) char kv_s[kKvBytes];  // [t][K 128 | V 128] fp16; lm_head products
 
@@ -1003,9 +1003,14 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       mark(e + 8);
       lds_barrier_p();
       sub(1);
-      float mx = tmax_s[0];
-#pragma unroll
-      for (int i = 1; i < kPT / kWave; ++i) mx = nan_max_p(mx, tmax_s[i]);
+      // The eight wave maxima in two reads, combined in order in registers.
+      float mx;
+      {
+        const float4 m0 = *reinterpret_cast<const float4*>(&tmax_s[0]);
+        const float4 m1 = *reinterpret_cast<const float4*>(&tmax_s[4]);
+        mx = nan_max_p(nan_max_p(nan_max_p(m0.x, m0.y), m0.z), m0.w);
+        mx = nan_max_p(nan_max_p(nan_max_p(nan_max_p(mx, m1.x), m1.y), m1.z), m1.w);
+      }
       for (int t = tid; t < n; t += kPT) p_s[t] = exp_ref(fadd(p_s[t], -mx));
       lds_barrier_p();
       mark(e + 9);
