@@ -181,13 +181,56 @@ def long_kv(backend, weights, positions: int = 4096, steps: int = 64):
         kv = sum(114688 * (positions + 1 + i + 1) for i in range(steps)) / steps
         step_bytes = cfg.weight_bytes_per_token() + kv
         gbs = step_bytes / (ms * 1e-3) / 1e9
-        return {"positions": positions, "steps": steps, "ms_per_step": round(ms, 4), "tok_s": round(1000.0 / ms, 2),
-                "bytes_per_token": int(step_bytes), "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        out = {"positions": positions, "steps": steps, "ms_per_step": round(ms, 4), "tok_s": round(1000.0 / ms, 2),
+               "bytes_per_token": int(step_bytes), "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    finally:
+        dec.close()
+    out["attention"] = long_kv_attention(backend, weights, positions)
+    return out
+
+
+def long_kv_attention(backend, weights, positions: int, steps: int = 16):
+    """The attention kernels alone at a long cache: a decoder created with
+    FAH_ATTENTION_TIMES=1 runs the same steps one by one with HIP events
+    around every layer's attention launches (scores, softmax, value sums);
+    K/V-read GB/s = the K/V bytes of all layers over their attention time."""
+    from funasrnet_amd.hip import HipDecoder
+
+    cfg = weights.config
+    old = os.environ.get("FAH_ATTENTION_TIMES")
+    os.environ["FAH_ATTENTION_TIMES"] = "1"
+    try:
+        dec = HipDecoder(backend, weights, capacity=positions + steps + 64)
+    finally:
+        if old is None:
+            del os.environ["FAH_ATTENTION_TIMES"]
+        else:
+            os.environ["FAH_ATTENTION_TIMES"] = old
+    try:
+        rng = np.random.default_rng(4)
+        width = cfg.kv_heads * cfg.head_size
+        for layer in range(cfg.layers):
+            k = rng.standard_normal((positions, width)).astype(np.float16)
+            v = rng.standard_normal((positions, width)).astype(np.float16)
+            dec.kv_write(layer, k, v)
+        dec.set_position(positions)
+        dec.decode(rng.standard_normal((1, cfg.width)).astype(np.float32), 1)
+        dec.attention_time()
+        dec.generate(steps)
+        ms, counted = dec.attention_time()
+        kv = sum(114688 * (positions + 1 + i + 1) for i in range(counted))
+        us_per_layer = ms * 1000.0 / counted / cfg.layers
+        gbs = kv / (ms * 1e-3) / 1e9
+        return {"kernels": "attn_scores_kernel + attn_values_kernel", "steps": counted,
+                "ms_per_token": round(ms / counted, 4), "us_per_layer": round(us_per_layer, 2),
+                "kv_bytes_per_token": int(kv / counted), "kv_read_gbs": round(gbs, 1),
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
     finally:
         dec.close()
 
 
-def sessions_decode(backend, weights, count: int = 16, steps: int = 128, prefix: int = 150, warmup: int = 4):
+def sessions_decode(backend, weights, count: int = 16, steps: int = 128, prefix: int = 150, warmup: int = 4,
+                    check: int | None = None):
     """Lock-step decode of `count` sessions over one weight set: 150-row
     N(0,1) prefixes (seeds 1..count), `warmup` lock-step steps (the first
     call captures the step), then `steps` timed steps (wall clock around one
@@ -203,7 +246,7 @@ def sessions_decode(backend, weights, count: int = 16, steps: int = 128, prefix:
         for seed, d in enumerate(sessions, 1):
             x = np.random.default_rng(seed).standard_normal((prefix, cfg.width)).astype(np.float32)
             d.decode(x, prefix)
-        HipDecoder.generate_sessions(sessions, warmup)
+        warm = HipDecoder.generate_sessions(sessions, warmup)
         t0 = time.perf_counter()
         toks = HipDecoder.generate_sessions(sessions, steps)
         wall = time.perf_counter() - t0
@@ -213,14 +256,53 @@ def sessions_decode(backend, weights, count: int = 16, steps: int = 128, prefix:
         step_bytes = cfg.weight_bytes_per_token() + kv
         gbs = step_bytes / (ms * 1e-3) / 1e9
         distinct = len({tuple(t) for t in toks.tolist()})
-        return {"sessions": count, "steps": steps, "ms_per_step": round(ms, 4),
-                "tok_s": round(count * 1000.0 / ms, 1), "bytes_per_step": int(step_bytes),
-                "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "distinct_token_rows": distinct}
+        result = {"sessions": count, "steps": steps, "ms_per_step": round(ms, 4),
+                  "tok_s": round(count * 1000.0 / ms, 1), "bytes_per_step": int(step_bytes),
+                  "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                  "distinct_token_rows": distinct}
     finally:
         for d in sessions[1:]:
             d.close()
         parent.close()
+    if check is not None:
+        result["oracle_check"] = sessions_oracle_check(weights, warm, toks, prefix, check)
+    return result
+
+
+def sessions_oracle_check(weights, warm, toks, prefix: int, threads: int):
+    """Every session's tokens (warm-up and timed steps) against the oracle
+    decoding that session alone (FunAsr.Transcribe's loop, FunAsr.cs:167-178);
+    the oracle's time doubles as the CPU baseline of the same workload."""
+    import oracle
+
+    used = oracle.set_threads(threads)
+    cfg = weights.config
+    count, steps = toks.shape[0], warm.shape[1] + toks.shape[1]
+    equal, first_divergence, seconds = 0, {}, 0.0
+    for i in range(count):
+        x = np.random.default_rng(i + 1).standard_normal((prefix, cfg.width)).astype(np.float32)
+        dec = oracle.Decoder(weights, capacity=prefix + steps + 8)
+        try:
+            logits = dec.decode(x, prefix)
+            expected = []
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                t = oracle.greedy(logits)
+                expected.append(t)
+                logits = dec.decode(dec.embed([t]), 1)
+            seconds += time.perf_counter() - t0
+        finally:
+            dec.close()
+        got = warm[i].tolist() + toks[i].tolist()
+        if got == expected:
+            equal += 1
+        else:
+            first_divergence[i] = next(j for j, (a, b) in enumerate(zip(got, expected)) if a != b)
+    return {"sessions_equal": equal, "sessions": count, "steps_compared": steps,
+            "first_divergence": first_divergence,
+            "cpu": {"kind": "port", "cores": used, "tok_s": round(count * steps / seconds, 2),
+                    "sample": f"oracle, each of the {count} sessions decoded alone for {steps} greedy steps "
+                              f"after its {prefix}-row prefix (decode time only)"}}
 
 
 def cpu_baseline(weights, prefix, tokens: int, threads: int, seconds_target: float):
@@ -341,24 +423,6 @@ def cpu_extra_baselines(weights, threads: int):
         dec.close()
     out["long_kv"] = {"kind": "port", "cores": used, "tok_s": round(steps / sec, 2),
                       "sample": f"{steps} greedy steps after 4096 cached positions"}
-    # Sessions: the oracle decodes sessions one after another (no shared
-    # weight pass), 16 sessions x 4 lock-step steps from 8-row prefixes.
-    count, steps, short = 16, 4, 8
-    decs = [oracle.Decoder(weights, capacity=short + steps + 8) for _ in range(count)]
-    try:
-        logits = [d.decode(np.random.default_rng(i + 1).standard_normal((short, cfg.width)).astype(np.float32), short)
-                  for i, d in enumerate(decs)]
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            for i, d in enumerate(decs):
-                logits[i] = d.decode(d.embed([oracle.greedy(logits[i])]), 1)
-        sec = time.perf_counter() - t0
-    finally:
-        for d in decs:
-            d.close()
-    out["sessions"] = {"kind": "port", "cores": used, "tok_s": round(count * steps / sec, 2),
-                       "sample": f"{count} sessions x {steps} lock-step steps, {short}-row prefixes (the prefill "
-                                 "length changes the step's attention share only)"}
     return out
 
 
@@ -432,7 +496,8 @@ def main() -> int:
         extra["gemv_sweep"] = gemv_sweep(backend)
         extra["prefill"] = prefill_ttft(backend, weights)
         extra["long_kv"] = long_kv(backend, weights)
-        extra["sessions"] = sessions_decode(backend, weights)
+        extra["sessions"] = sessions_decode(backend, weights,
+                                            check=None if args.no_cpu else min(16, os.cpu_count() or 1))
         if not args.no_cpu:
             extra["cpu_baselines"] = cpu_extra_baselines(weights, min(16, os.cpu_count() or 1))
     backend.close()

@@ -325,6 +325,16 @@ struct fah_decoder {
   fah::PersistentArgs pargs{};
   // Prefill (decode of many rows at once): row buffers grown on demand.
   DeviceBuffer pf_x, pf_a, pf_qkv, pf_q, pf_h, pf_xq, pf_xs;
+  // Attention timing of the multi-kernel step (FAH_ATTENTION_TIMES=1 at
+  // creation): events around every layer's attention kernels, the steps
+  // launched one by one and their attention time summed.
+  bool attention_times = false;
+  std::vector<hipEvent_t> attn_events;
+  double attn_ms = 0.0;
+  int attn_steps = 0;
+  ~fah_decoder() {
+    for (hipEvent_t e : attn_events) (void)hipEventDestroy(e);
+  }
 };
 
 namespace {
@@ -467,7 +477,9 @@ void enqueue_layers(fah_decoder* d, hipStream_t s) {
     at.head_size = c.head_size;
     at.capacity = c.capacity;
     at.divisor = std::sqrt((float)c.head_size);
+    if (d->attention_times) check(hipEventRecord(d->attn_events[2 * l], s), "hipEventRecord");
     check(fah::launch_attention(at, 16, s), "attention");
+    if (d->attention_times) check(hipEventRecord(d->attn_events[2 * l + 1], s), "hipEventRecord");
 
     fah::GemvArgs o = gemv_args(d->wt->wo[l]);
     o.x = d->attn.as<float>();
@@ -555,6 +567,12 @@ void init_state(fah_decoder* d, hipStream_t s) {
   upload(d->rope_cos, cs.data(), cs.size() * 4, s);
   upload(d->rope_sin, sn.data(), sn.size() * 4, s);
 
+  const char* at_env = std::getenv("FAH_ATTENTION_TIMES");
+  if (at_env && at_env[0] == '1') {
+    d->attention_times = true;
+    d->attn_events.assign(2 * (size_t)k.layers, nullptr);
+    for (hipEvent_t& e : d->attn_events) check(hipEventCreate(&e), "hipEventCreate");
+  }
   size_t kv_elems = (size_t)k.layers * k.kv_heads * k.capacity * k.head_size;
   d->kcache.allocate(kv_elems * 2);
   d->vcache.allocate(kv_elems * 2);
@@ -862,6 +880,17 @@ void run_kind(fah_decoder* d, int kind, hipStream_t s, int position) {
     fah::PersistentArgs a = d->pargs;
     a.mode = kind;
     check(fah::launch_decode_step(a, d->blocks, s), "persistent decode step");
+    return;
+  }
+  if (d->attention_times) {
+    enqueue_kind(d, kind, s);
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    for (int l = 0; l < d->cfg.layers; ++l) {
+      float ms = 0.0f;
+      check(hipEventElapsedTime(&ms, d->attn_events[2 * l], d->attn_events[2 * l + 1]), "hipEventElapsedTime");
+      d->attn_ms += ms;
+    }
+    ++d->attn_steps;
     return;
   }
   if (!use_graphs()) {
@@ -1908,6 +1937,20 @@ int fah_decoder_timeline(fah_decoder* d, uint64_t* ticks, int count) {
     check(hipMemcpyAsync(ticks, d->timeline.ptr, (size_t)count * 8, hipMemcpyDeviceToHost, d->ctx->stream),
           "D2H timeline");
     check(hipStreamSynchronize(d->ctx->stream), "sync");
+    return FAH_OK;
+  });
+}
+
+int fah_decoder_attention_time(fah_decoder* d, double* milliseconds, int* steps) {
+  if (!d || !milliseconds || !steps) return fail(FAH_ERROR_ARGUMENT, "decoder/milliseconds/steps is NULL");
+  if (!d->attention_times) return FAH_DECLINED;
+  return guarded_decoder([&] {
+    std::lock_guard<std::mutex> lock(d->ctx->gate);
+    require_live(d);
+    *milliseconds = d->attn_ms;
+    *steps = d->attn_steps;
+    d->attn_ms = 0.0;
+    d->attn_steps = 0;
     return FAH_OK;
   });
 }

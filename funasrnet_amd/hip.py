@@ -93,6 +93,7 @@ SIGNATURES = {
     "fah_decoder_trace": (ctypes.c_int, [_vp, ctypes.c_int, _f32p, ctypes.c_int]),
     "fah_decoder_timeline": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.c_int]),
     "fah_decoder_fail_next_step": (ctypes.c_int, [_vp]),
+    "fah_decoder_attention_time": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
 }
 
 _lib = None
@@ -400,6 +401,13 @@ class HipDecoder:
         out = np.zeros(256 * 480, dtype=np.uint64)
         rc = _check(load().fah_decoder_timeline(self.handle, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), out.size))
         return None if rc == DECLINED else out.reshape(256, 480)
+
+    def attention_time(self):
+        """(milliseconds, steps) of attention kernels since the last call, or
+        None unless the decoder was created with FAH_ATTENTION_TIMES=1."""
+        ms, steps = ctypes.c_double(), ctypes.c_int()
+        rc = _check(load().fah_decoder_attention_time(self.handle, ctypes.byref(ms), ctypes.byref(steps)))
+        return None if rc == DECLINED else (ms.value, steps.value)
 
     @property
     def persistent(self) -> bool:

@@ -264,6 +264,16 @@ int fah_decoder_trace(fah_decoder* decoder, int which, float* out, int count);
  * (src/FunAsrNet/TensorMath.cs:37-40) for a single-launch step. */
 int fah_decoder_timeline(fah_decoder* decoder, uint64_t* ticks, int count);
 
+/* Device time of the attention kernels (scores, softmax, value sums) of the
+ * multi-kernel steps run since the last call, summed over layers and steps,
+ * and the number of steps; reading resets both. Only recorded when
+ * FAH_ATTENTION_TIMES=1 at creation (the steps then run one by one with
+ * HIP events around each layer's attention, outside graphs; FAH_DECLINED
+ * otherwise, and for steps of the persistent kernel). The per-operation
+ * timing the reference reports through TensorMath.LinearMeasured
+ * (src/FunAsrNet/TensorMath.cs:37-40), for the attention of long caches. */
+int fah_decoder_attention_time(fah_decoder* decoder, double* milliseconds, int* steps);
+
 /* Test hook for the persistent step's failure path: presets the device
  * error word, so that the next persistent launch of this decoder ends at its
  * entry check (every workgroup exits normally) and the call reports
