@@ -279,6 +279,9 @@ struct fah_weight {
   bool half_scales = true;
   DeviceBuffer q, s;
   int group_rows = 1;
+  // FP32 weight (Weight.Values): `f` holds [rows][cols] floats, q/s unused.
+  bool f32 = false;
+  DeviceBuffer f;
 };
 
 struct DeviceMatrix {
@@ -1129,7 +1132,30 @@ int fah_weight_release(fah_weight* w) {
   return FAH_OK;
 }
 
-int64_t fah_weight_device_bytes(const fah_weight* w) { return w ? (int64_t)(w->q.bytes + w->s.bytes) : 0; }
+int64_t fah_weight_device_bytes(const fah_weight* w) {
+  return w ? (int64_t)(w->q.bytes + w->s.bytes + w->f.bytes) : 0;
+}
+
+int fah_weight_f32_upload(fah_context* h, const float* values, int rows, int cols, fah_weight** out) {
+  if (!h || !out) return fail(FAH_ERROR_ARGUMENT, "context/out is NULL");
+  Ctx* c = h->st.get();
+  return guarded([&] {
+    require(values != nullptr, "FP32 weight needs its values");
+    require(rows > 0 && cols > 0, "Invalid row-major FP32 dimensions");
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
+    auto w = std::make_unique<fah_weight>();
+    w->ctx = h->st;
+    w->rows = rows;
+    w->cols = cols;
+    w->f32 = true;
+    upload(w->f, values, (size_t)rows * cols * 4, c->stream);
+    *out = w.release();
+    return FAH_OK;
+  });
+}
 
 // Many rows at once go through the MFMA GEMM (same per-row block order).
 constexpr int kGemmMinFrames = 4;
@@ -1167,7 +1193,7 @@ int fah_quantized_linear(fah_context* h, const float* input, int frames, const f
                          float* output) {
   if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
   Ctx* c = h->st.get();
-  if (!w || frames <= 0 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
+  if (!w || w->f32 || frames <= 0 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
   if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return FAH_DECLINED;
   return guarded([&] {
     require(input && output, "Q8 GPU projection needs input and output");
@@ -1210,7 +1236,7 @@ int fah_quantized_linear_noalloc(fah_context* h, const float* input, int frames,
                                  const float* bias, float* output) {
   if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
   Ctx* c = h->st.get();
-  if (!w || frames <= 0 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
+  if (!w || w->f32 || frames <= 0 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
   if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return FAH_DECLINED;
   return guarded([&] {
     require(input && output, "Q8 GPU projection needs input and output");
@@ -1263,8 +1289,9 @@ int fah_linear_many(fah_context* h, const float* input, int frames, const fah_we
   if (!weights || count < 0 || frames <= 0) return FAH_DECLINED;
   int cols = weights[0] ? weights[0]->cols : 0;
   int64_t total_rows = 0;
+  const bool f32 = weights[0] && weights[0]->f32;
   for (int i = 0; i < count; ++i) {
-    if (!weights[i] || weights[i]->cols > fah::gemv_max_k()) return FAH_DECLINED;
+    if (!weights[i] || weights[i]->f32 != f32 || (!f32 && weights[i]->cols > fah::gemv_max_k())) return FAH_DECLINED;
     total_rows += weights[i]->rows;
   }
   if ((int64_t)frames * cols * total_rows < c->minimum_operations) return FAH_DECLINED;
@@ -1287,30 +1314,140 @@ int fah_linear_many(fah_context* h, const float* input, int frames, const fah_we
     for (int i = 0; i < count; ++i) out_total += (size_t)frames * weights[i]->rows;
     c->out.ensure(out_total * 4);
     check(hipMemcpyAsync(c->in.ptr, input, n * 4, hipMemcpyHostToDevice, c->stream), "H2D input");
-    check(fah::launch_quantize(c->in.as<float>(), (int64_t)n, c->q.as<int8_t>(), c->s.as<float>(), c->stream),
-          "quantize");
-    size_t at = 0;
-    for (int i = 0; i < count; ++i) {
-      if (gemm_fits(weights[i], frames)) {
-        launch_weight_gemm(weights[i], c->q.as<int8_t>(), c->s.as<float>(), frames, c->out.as<float>() + at, nullptr,
-                           c->stream);
-      } else {
-        fah::GemvArgs a = weight_args(weights[i]);
-        a.xq = c->q.as<int8_t>();
-        a.xs = c->s.as<float>();
-        a.out = c->out.as<float>() + at;
-        a.out_rows = weights[i]->rows;
-        check(fah::launch_gemv(a, weights[i]->half_scales, fah::kInputQuantized, fah::kOutPlain, frames, c->stream),
-              "gemv");
+    if (f32) {
+      // FP32 group (IGroupedComputeBackend over Weight.Values): each weight
+      // through the same kernel as fah_linear, so the bits equal separate calls.
+      size_t at = 0;
+      for (int i = 0; i < count; ++i) {
+        check(fah::launch_f32_linear(c->in.as<float>(), weights[i]->f.as<float>(), nullptr, c->out.as<float>() + at,
+                                     frames, weights[i]->rows, cols, false, c->stream),
+              "f32 linear");
+        at += (size_t)frames * weights[i]->rows;
       }
-      at += (size_t)frames * weights[i]->rows;
+    } else {
+      check(fah::launch_quantize(c->in.as<float>(), (int64_t)n, c->q.as<int8_t>(), c->s.as<float>(), c->stream),
+            "quantize");
+      size_t at = 0;
+      for (int i = 0; i < count; ++i) {
+        if (gemm_fits(weights[i], frames)) {
+          launch_weight_gemm(weights[i], c->q.as<int8_t>(), c->s.as<float>(), frames, c->out.as<float>() + at, nullptr,
+                             c->stream);
+        } else {
+          fah::GemvArgs a = weight_args(weights[i]);
+          a.xq = c->q.as<int8_t>();
+          a.xs = c->s.as<float>();
+          a.out = c->out.as<float>() + at;
+          a.out_rows = weights[i]->rows;
+          check(fah::launch_gemv(a, weights[i]->half_scales, fah::kInputQuantized, fah::kOutPlain, frames, c->stream),
+                "gemv");
+        }
+        at += (size_t)frames * weights[i]->rows;
+      }
     }
-    at = 0;
+    size_t at = 0;
     for (int i = 0; i < count; ++i) {
       size_t bytes = (size_t)frames * weights[i]->rows * 4;
       check(hipMemcpyAsync(outputs[i], c->out.as<float>() + at, bytes, hipMemcpyDeviceToHost, c->stream), "D2H");
       at += (size_t)frames * weights[i]->rows;
     }
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return FAH_OK;
+  });
+}
+
+int fah_linear(fah_context* h, const float* input, int frames, const fah_weight* w, const float* bias, float* output) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
+  if (!w || !w->f32 || frames <= 0) return FAH_DECLINED;
+  if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return FAH_DECLINED;
+  return guarded([&] {
+    require(input && output, "FP32 GPU projection needs input and output");
+    require(w->ctx.get() == c, "weight belongs to another context");
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
+    const size_t in_bytes = (size_t)frames * w->cols * 4, out_bytes = (size_t)frames * w->rows * 4;
+    c->in.ensure(in_bytes + (bias ? (size_t)w->rows * 4 : 0));
+    c->out.ensure(out_bytes);
+    check(hipMemcpyAsync(c->in.ptr, input, in_bytes, hipMemcpyHostToDevice, c->stream), "H2D input");
+    float* dbias = nullptr;
+    if (bias) {
+      dbias = reinterpret_cast<float*>(c->in.as<char>() + in_bytes);
+      check(hipMemcpyAsync(dbias, bias, (size_t)w->rows * 4, hipMemcpyHostToDevice, c->stream), "H2D bias");
+    }
+    check(fah::launch_f32_linear(c->in.as<float>(), w->f.as<float>(), dbias, c->out.as<float>(), frames, w->rows,
+                                 w->cols, false, c->stream),
+          "f32 linear");
+    check(hipMemcpyAsync(output, c->out.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return FAH_OK;
+  });
+}
+
+int fah_relu_projection(fah_context* h, const float* input, int frames, const fah_weight* first,
+                        const float* first_bias, const fah_weight* second, const float* second_bias, float* output) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
+  if (!first || !second || !first->f32 || !second->f32 || frames <= 0 || first->rows != second->cols ||
+      first->rows % 4 != 0)
+    return FAH_DECLINED;
+  if ((int64_t)frames * first->rows * first->cols < c->minimum_operations ||
+      (int64_t)frames * second->rows * second->cols < c->minimum_operations)
+    return FAH_DECLINED;
+  return guarded([&] {
+    require(input && output, "ReLU projection needs input and output");
+    require(first->ctx.get() == c && second->ctx.get() == c, "weight belongs to another context");
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
+    const int H = first->rows, N = second->rows, K = first->cols;
+    const size_t in_bytes = (size_t)frames * K * 4, mid_bytes = (size_t)frames * H * 4, out_bytes = (size_t)frames * N * 4;
+    const size_t b1 = first_bias ? (size_t)H * 4 : 0, b2 = second_bias ? (size_t)N * 4 : 0;
+    c->in.ensure(in_bytes + b1 + b2);
+    c->out.ensure(mid_bytes + out_bytes);
+    check(hipMemcpyAsync(c->in.ptr, input, in_bytes, hipMemcpyHostToDevice, c->stream), "H2D input");
+    float* d1 = first_bias ? reinterpret_cast<float*>(c->in.as<char>() + in_bytes) : nullptr;
+    float* d2 = second_bias ? reinterpret_cast<float*>(c->in.as<char>() + in_bytes + b1) : nullptr;
+    if (d1) check(hipMemcpyAsync(d1, first_bias, b1, hipMemcpyHostToDevice, c->stream), "H2D bias");
+    if (d2) check(hipMemcpyAsync(d2, second_bias, b2, hipMemcpyHostToDevice, c->stream), "H2D bias");
+    float* mid = c->out.as<float>();
+    float* dout = reinterpret_cast<float*>(c->out.as<char>() + mid_bytes);
+    // The intermediate stays on the device (IReluProjectionBackend.cs:4-16).
+    check(fah::launch_f32_linear(c->in.as<float>(), first->f.as<float>(), d1, mid, frames, H, K, true, c->stream),
+          "f32 linear + ReLU");
+    check(fah::launch_f32_linear(mid, second->f.as<float>(), d2, dout, frames, N, H, false, c->stream), "f32 linear");
+    check(hipMemcpyAsync(output, dout, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return FAH_OK;
+  });
+}
+
+int fah_attention(fah_context* h, const float* query, const float* key, const float* value, int frames, int width,
+                  int heads, float* output) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
+  if (!fah::f32_attention_supported(frames, width, heads)) return FAH_DECLINED;
+  if (c->minimum_operations > 0 && (frames < 160 || (int64_t)frames * frames * width < c->minimum_operations))
+    return FAH_DECLINED;
+  return guarded([&] {
+    require(query && key && value && output, "GPU attention needs query, key, value and output");
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
+    const size_t bytes = (size_t)frames * width * 4;
+    c->in.ensure(3 * bytes);
+    c->out.ensure(bytes);
+    float* dq = c->in.as<float>();
+    float* dk = reinterpret_cast<float*>(c->in.as<char>() + bytes);
+    float* dv = reinterpret_cast<float*>(c->in.as<char>() + 2 * bytes);
+    check(hipMemcpyAsync(dq, query, bytes, hipMemcpyHostToDevice, c->stream), "H2D query");
+    check(hipMemcpyAsync(dk, key, bytes, hipMemcpyHostToDevice, c->stream), "H2D key");
+    check(hipMemcpyAsync(dv, value, bytes, hipMemcpyHostToDevice, c->stream), "H2D value");
+    check(fah::launch_f32_attention(dq, dk, dv, c->out.as<float>(), frames, width, heads, c->stream), "attention");
+    check(hipMemcpyAsync(output, c->out.ptr, bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return FAH_OK;
   });
@@ -1334,7 +1471,7 @@ int fah_q8_gemv_device(fah_context* h, const int8_t* q, const float* scales, int
                        float* out) {
   if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
   Ctx* c = h->st.get();
-  if (!w || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
+  if (!w || w->f32 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
   return guarded([&] {
     require(frames > 0 && q && scales && out, "invalid GEMV arguments");
     require(w->ctx.get() == c, "weight belongs to another context");
@@ -1360,6 +1497,7 @@ int fah_q8_block_dots_device(fah_context* h, const int8_t* q, const fah_weight* 
   Ctx* c = h->st.get();
   return guarded([&] {
     require(w && q && dots, "invalid block-dot arguments");
+    require(!w->f32, "block dots need a Q8_0 weight");
     require(w->ctx.get() == c, "weight belongs to another context");
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");

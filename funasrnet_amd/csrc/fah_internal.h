@@ -227,6 +227,16 @@ hipError_t launch_session_embed(const int8_t* q, const void* scales, bool half_s
                                 const SessionRef* sessions, int count, float* x, hipStream_t s);
 
 
+// FP32 projections y[M][N] = x[M][K] W[N][K]^T (+ bias) (ReLU): fp32 MFMA
+// GEMM, or a GEMV for up to 4 frames of at most 4096 columns.
+hipError_t launch_f32_linear(const float* x, const float* w, const float* bias, float* out, int M, int N, int K,
+                             bool relu, hipStream_t s);
+// Non-causal multi-head attention over [frames][width] rows (head size
+// width / heads <= 256, frames <= 4096).
+bool f32_attention_supported(int frames, int width, int heads);
+hipError_t launch_f32_attention(const float* q, const float* k, const float* v, float* out, int frames, int width,
+                                int heads, hipStream_t s);
+
 bool persistent_shape_supported(int width, int heads, int kv_heads, int head_size, int ffn, int blocks);
 hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s);
 // Whether 256 workgroups of the persistent kernel's size land on XCD

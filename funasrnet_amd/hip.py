@@ -65,7 +65,11 @@ SIGNATURES = {
     "fah_weight_q8_upload": (ctypes.c_int, [_vp, _i8p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
     "fah_weight_q8_upload_blocks": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_uint8), ctypes.c_int, ctypes.c_int,
                                                    ctypes.POINTER(_vp)]),
+    "fah_weight_f32_upload": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
     "fah_weight_release": (ctypes.c_int, [_vp]),
+    "fah_linear": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, _vp, _f32p, _f32p]),
+    "fah_relu_projection": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, _vp, _f32p, _vp, _f32p, _f32p]),
+    "fah_attention": (ctypes.c_int, [_vp, _f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]),
     "fah_weight_device_bytes": (ctypes.c_int64, [_vp]),
     "fah_quantized_linear": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, _vp, _f32p, _f32p]),
     "fah_quantized_linear_noalloc": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, _vp, _f32p, _f32p]),
@@ -172,8 +176,39 @@ class HipWeight:
             pass
 
 
+class HipFloatWeight:
+    """Device copy of an FP32 matrix (Weight.Values, rows x columns)."""
+
+    def __init__(self, backend: "HipBackend", values: np.ndarray):
+        v = np.ascontiguousarray(values, dtype=np.float32)
+        if v.ndim != 2:
+            raise ValueError("FP32 weight must be a rows x columns matrix")
+        self.rows, self.columns = v.shape
+        h = _vp()
+        _check(load().fah_weight_f32_upload(backend.handle, _p(v, ctypes.c_float), self.rows, self.columns,
+                                            ctypes.byref(h)))
+        self.handle = h
+
+    @property
+    def device_bytes(self) -> int:
+        return load().fah_weight_device_bytes(self.handle)
+
+    def close(self):
+        if self.handle:
+            load().fah_weight_release(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class HipBackend:
-    """IQuantizedComputeBackend + IGroupedComputeBackend over one context."""
+    """IFloatComputeBackend (TryLinear), IQuantizedComputeBackend,
+    IGroupedComputeBackend, IReluProjectionBackend and
+    IAttentionComputeBackend over one context."""
 
     def __init__(self, device: int = 0, minimum_operations: int | None = None):
         h = _vp()
@@ -202,6 +237,64 @@ class HipBackend:
             self._weights[key] = (tensor, HipWeight(self, tensor))
         return self._weights[key][1]
 
+    def float_weight(self, values: np.ndarray) -> HipFloatWeight:
+        """Device FP32 weight cached by array identity (VulkanFloatBackend.cs:242-283)."""
+        key = ("f32", id(values))
+        if key not in self._weights:
+            self._weights[key] = (values, HipFloatWeight(self, values))
+        return self._weights[key][1]
+
+    def try_linear(self, input: np.ndarray, frames: int, weight: np.ndarray, bias, output: np.ndarray) -> bool:
+        """IFloatComputeBackend.TryLinear: output[frames, rows] = input W^T + bias
+        for an FP32 weight [rows, columns]; False (output untouched) when declined."""
+        w = self.float_weight(weight)
+        x = np.ascontiguousarray(input, dtype=np.float32)
+        if x.size != frames * w.columns or output.size != frames * w.rows:
+            raise ValueError("GPU linear projection shape mismatch")
+        out = np.empty(frames * w.rows, dtype=np.float32)
+        b = None if bias is None else _p(np.ascontiguousarray(bias, dtype=np.float32), ctypes.c_float)
+        rc = _check(load().fah_linear(self.handle, _p(x, ctypes.c_float), frames, w.handle, b, _p(out, ctypes.c_float)))
+        if rc == DECLINED:
+            return False
+        output.reshape(-1)[:] = out
+        return True
+
+    def try_relu_projection(self, input: np.ndarray, frames: int, first: np.ndarray, first_bias, second: np.ndarray,
+                            second_bias, output: np.ndarray) -> bool:
+        """IReluProjectionBackend.TryReluProjection: ReLU(x W1^T + b1) W2^T + b2."""
+        w1, w2 = self.float_weight(first), self.float_weight(second)
+        x = np.ascontiguousarray(input, dtype=np.float32)
+        if x.size != frames * w1.columns or output.size != frames * w2.rows:
+            raise ValueError("ReLU projection input, weight or output shape mismatch")
+        out = np.empty(frames * w2.rows, dtype=np.float32)
+        b1 = None if first_bias is None else _p(np.ascontiguousarray(first_bias, dtype=np.float32), ctypes.c_float)
+        b2 = None if second_bias is None else _p(np.ascontiguousarray(second_bias, dtype=np.float32), ctypes.c_float)
+        rc = _check(load().fah_relu_projection(self.handle, _p(x, ctypes.c_float), frames, w1.handle, b1, w2.handle, b2,
+                                               _p(out, ctypes.c_float)))
+        if rc == DECLINED:
+            return False
+        output.reshape(-1)[:] = out
+        return True
+
+    def try_attention(self, query: np.ndarray, key: np.ndarray, value: np.ndarray, frames: int, width: int,
+                      heads: int, output: np.ndarray) -> bool:
+        """IAttentionComputeBackend.TryAttention over [frames, width] rows."""
+        q = np.ascontiguousarray(query, dtype=np.float32)
+        k = np.ascontiguousarray(key, dtype=np.float32)
+        v = np.ascontiguousarray(value, dtype=np.float32)
+        count = frames * width
+        if min(frames, width, heads) < 1 or width % heads or width // heads > 256 or frames > 4096:
+            return False
+        if q.size != count or k.size != count or v.size != count or output.size != count:
+            raise ValueError("GPU attention input/output shapes differ")
+        out = np.empty(count, dtype=np.float32)
+        rc = _check(load().fah_attention(self.handle, _p(q, ctypes.c_float), _p(k, ctypes.c_float),
+                                         _p(v, ctypes.c_float), frames, width, heads, _p(out, ctypes.c_float)))
+        if rc == DECLINED:
+            return False
+        output.reshape(-1)[:] = out
+        return True
+
     def try_quantized_linear(self, input: np.ndarray, frames: int, weight: Q8Tensor, bias, output: np.ndarray) -> bool:
         w = self.weight(weight)
         x = np.ascontiguousarray(input, dtype=np.float32)
@@ -217,7 +310,8 @@ class HipBackend:
         return True
 
     def try_linear_many(self, input: np.ndarray, frames: int, weights: list):
-        ws = [self.weight(t) for t in weights]
+        """IGroupedComputeBackend.TryLinearMany over Q8_0 tensors or FP32 arrays."""
+        ws = [self.float_weight(t) if isinstance(t, np.ndarray) else self.weight(t) for t in weights]
         x = np.ascontiguousarray(input, dtype=np.float32)
         outs = [np.empty(frames * w.rows, dtype=np.float32) for w in ws]
         handles = (_vp * len(ws))(*[w.handle for w in ws])

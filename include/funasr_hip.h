@@ -97,6 +97,11 @@ int fah_weight_q8_upload(fah_context* context, const int8_t* quantized, const fl
  * are split into the int8 plane and the fp16 scale plane on the device, so
  * no sbyte[]/float[] copy of the matrix exists on the host. */
 int fah_weight_q8_upload_blocks(fah_context* context, const uint8_t* blocks, int rows, int cols, fah_weight** out);
+/* Upload an FP32 matrix (Weight.Values, src/FunAsrNet/Gguf.cs:264-345:
+ * float[rows*cols] row-major, Columns = cols, Rows = rows; F16 tensors come
+ * widened exactly). Serves fah_linear, fah_relu_projection and FP32 groups
+ * of fah_linear_many; the Q8_0 entry points decline it. */
+int fah_weight_f32_upload(fah_context* context, const float* values, int rows, int cols, fah_weight** out);
 int fah_weight_release(fah_weight* weight);
 /* Device bytes held by the weight (int8 plane plus scale plane). */
 int64_t fah_weight_device_bytes(const fah_weight* weight);
@@ -127,10 +132,44 @@ int fah_quantized_linear(fah_context* context, const float* input, int frames, c
 int fah_quantized_linear_noalloc(fah_context* context, const float* input, int frames, const fah_weight* weight,
                                  const float* bias, float* output);
 
+/* IFloatComputeBackend.TryLinear (src/FunAsrNet/IFloatComputeBackend.cs:11-18;
+ * reference device version src/FunAsrNet.Vulkan/VulkanFloatBackend.cs:127-171):
+ * output[frames*rows] = input[frames*cols] W^T (+ bias) for an FP32 weight,
+ * on fp32 MFMA (or a bandwidth-bound GEMV for up to 4 frames). Declines
+ * (output untouched) Q8_0 weights and projections below the minimum
+ * operations. Float order differs from the CPU kernels, as the reference's
+ * own device path does (its check: 2e-4 x max(1, |expected|)). The encoder's
+ * projections (src/FunAsrNet/FunEncoder.cs:100) and the original-weights
+ * decoder's GEMVs (FloatVectorShader.cs) go through it. */
+int fah_linear(fah_context* context, const float* input, int frames, const fah_weight* weight, const float* bias,
+               float* output);
+
+/* IReluProjectionBackend.TryReluProjection (src/FunAsrNet/IReluProjectionBackend.cs:4-16;
+ * device version VulkanReluProjection.cs): output = ReLU(input W1^T + b1)
+ * W2^T + b2 with the intermediate kept on the device; bit for bit the two
+ * fah_linear calls with the ReLU (v < 0 ? 0 : v) between them. Biases may be
+ * NULL. Declines unless both weights are FP32, first rows == second cols and
+ * first rows % 4 == 0 (the reference's conditions), or below the minimum
+ * operations. */
+int fah_relu_projection(fah_context* context, const float* input, int frames, const fah_weight* first,
+                        const float* first_bias, const fah_weight* second, const float* second_bias, float* output);
+
+/* IAttentionComputeBackend.TryAttention (src/FunAsrNet/IAttentionComputeBackend.cs:4-16;
+ * CPU version TensorMath.cs:619-666, device version VulkanAttention.cs):
+ * non-causal multi-head attention over [frames][width] query, key and value
+ * rows, `heads` heads of width / heads channels: per head and query row,
+ * scores dot(q, k) / sqrtf(size), softmax, weighted values. Declines frames
+ * outside 1..4096, width not a multiple of heads, head size above 256, and
+ * (with a positive minimum) fewer than 160 frames or frames^2 * width below
+ * the minimum operations -- the reference's conditions. */
+int fah_attention(fah_context* context, const float* query, const float* key, const float* value, int frames,
+                  int width, int heads, float* output);
+
 /* IGroupedComputeBackend.TryLinearMany
  * (src/FunAsrNet/IGroupedComputeBackend.cs:4-13; CPU version
  * src/FunAsrNet/TensorMath.Interleaved.cs:22-46): one shared activation
- * quantisation, outputs[i][frames*rows_i]. All weights share cols. */
+ * quantisation, outputs[i][frames*rows_i]. All weights share cols. A group of
+ * FP32 weights gives, per weight, the bits of fah_linear. */
 int fah_linear_many(fah_context* context, const float* input, int frames, const fah_weight* const* weights,
                     int count, float* const* outputs);
 

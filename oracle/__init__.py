@@ -85,6 +85,10 @@ def _load():
         "oracle_decoder_keys": (_f32p, [ctypes.c_void_p, ctypes.c_int]),
         "oracle_decoder_values": (_f32p, [ctypes.c_void_p, ctypes.c_int]),
         "oracle_last_error": (ctypes.c_char_p, []),
+        "oracle_float_linear_f64": (None, [_f32p, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_int, _f32p,
+                                           ctypes.POINTER(ctypes.c_double)]),
+        "oracle_attention_f64": (None, [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.POINTER(ctypes.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -229,6 +233,27 @@ def dot(a, b) -> float:
     a = np.ascontiguousarray(a, dtype=np.float32)
     b = np.ascontiguousarray(b, dtype=np.float32)
     return lib().oracle_dot(_p(a, ctypes.c_float), _p(b, ctypes.c_float), a.size)
+
+
+def float_linear_f64(x, frames: int, w, bias=None) -> np.ndarray:
+    """y[frames, rows] = x W^T (+ bias) in double (FP32 projection reference)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    out = np.empty(frames * rows, dtype=np.float64)
+    b = None if bias is None else _p(np.ascontiguousarray(bias, dtype=np.float32), ctypes.c_float)
+    lib().oracle_float_linear_f64(_p(x, ctypes.c_float), frames, cols, _p(w, ctypes.c_float), rows, b,
+                                  out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    return out.reshape(frames, rows)
+
+
+def attention_f64(q, k, v, frames: int, width: int, heads: int) -> np.ndarray:
+    """Non-causal multi-head attention in double over [frames, width] rows."""
+    q, k, v = (np.ascontiguousarray(a, dtype=np.float32).reshape(-1) for a in (q, k, v))
+    out = np.empty(frames * width, dtype=np.float64)
+    lib().oracle_attention_f64(_p(q, ctypes.c_float), _p(k, ctypes.c_float), _p(v, ctypes.c_float), frames, width,
+                               heads, out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    return out.reshape(frames, width)
 
 
 def greedy(logits) -> int:

@@ -346,6 +346,56 @@ void oracle_softmax(float* x, int n) {
     for (i = 0; i < n; ++i) x[i] = x[i] * inverse;
 }
 
+/* The double reference the reference's FP32 device checks compare against
+ * (tools/FunAsrNet.Benchmarks/FloatGpuChecks.cs compares with a CPU linear
+ * at 2e-4 x max(1, |expected|); TensorMath.cs:79-200 computes
+ * y = x W^T + b with Weight.Values rows of `cols` floats). */
+void oracle_float_linear_f64(const float* x, int frames, int cols, const float* w, int rows, const float* bias,
+                             double* out) {
+#pragma omp parallel for schedule(static) if ((long)frames * rows * cols > 1000000)
+    for (int index = 0; index < frames * rows; ++index) {
+        int f = index / rows, n = index % rows;
+        const float* xr = x + (int64_t)f * cols;
+        const float* wr = w + (int64_t)n * cols;
+        double sum = 0.0;
+        for (int k = 0; k < cols; ++k) sum += (double)xr[k] * (double)wr[k];
+        out[index] = sum + (bias ? (double)bias[n] : 0.0);
+    }
+}
+
+/* tools/FunAsrNet.Benchmarks/AttentionGpuChecks.cs (Reference): per head and
+ * query row, double dot products divided by sqrt(size), max-shifted exp,
+ * probabilities and weighted values in double (the semantics of
+ * TensorMath.cs:646-666 AttentionReference). */
+void oracle_attention_f64(const float* q, const float* k, const float* v, int frames, int width, int heads,
+                          double* out) {
+    int size = width / heads;
+    double divisor = sqrt((double)size);
+#pragma omp parallel for schedule(dynamic)
+    for (int index = 0; index < frames * heads; ++index) {
+        int t = index / heads, h = index % heads, at = t * width + h * size;
+        double* scores = (double*)malloc(sizeof(double) * (size_t)frames);
+        double max = -INFINITY;
+        for (int s = 0; s < frames; ++s) {
+            double d = 0.0;
+            for (int c = 0; c < size; ++c) d += (double)q[at + c] * (double)k[s * width + h * size + c];
+            scores[s] = d / divisor;
+            if (scores[s] > max) max = scores[s];
+        }
+        double sum = 0.0;
+        for (int s = 0; s < frames; ++s) {
+            scores[s] = exp(scores[s] - max);
+            sum += scores[s];
+        }
+        for (int c = 0; c < size; ++c) {
+            double acc = 0.0;
+            for (int s = 0; s < frames; ++s) acc += scores[s] / sum * (double)v[s * width + h * size + c];
+            out[at + c] = acc;
+        }
+        free(scores);
+    }
+}
+
 /* src/FunAsrNet/TensorMath.Elementwise.cs:167-196: g / (1 + exp(-g)) * up. */
 void oracle_silu_multiply(float* gate, const float* up, int64_t n) {
     for (int64_t i = 0; i < n; ++i) {

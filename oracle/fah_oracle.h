@@ -35,6 +35,18 @@
  *                              double cos/sin at 2 ulp-scale tolerance
  *   oracle_decoder_*           composition of the above; pinned by the
  *                              properties in tests/test_oracle_decoder.py
+ *   oracle_float_linear_f64    the independent double reference the
+ *                              reference's device checks use for FP32
+ *                              projections; pinned: integer-valued inputs
+ *                              exactly equal to an int64 brute force, random
+ *                              inputs vs numpy's float64 matmul, identity and
+ *                              zero weights (tests/test_oracle_float.py)
+ *   oracle_attention_f64       double reference of non-causal multi-head
+ *                              attention (AttentionGpuChecks.cs Reference);
+ *                              pinned: q = k = 0 gives the mean of v, one
+ *                              frame gives v, one dominant key gives its v,
+ *                              heads computed independently, permuting keys
+ *                              and values together changes nothing
  */
 #ifndef FAH_ORACLE_H
 #define FAH_ORACLE_H
@@ -101,6 +113,14 @@ typedef struct oracle_model {
     oracle_q8 output;           /* q == NULL -> tied to token_embd */
     const float* output_norm;   /* [width] */
 } oracle_model;
+
+/* FP32 projection in double: out[f][n] = sum_k x[f][k] w[n][k] (+ bias[n]),
+ * each product and sum in double, then rounded once. */
+void oracle_float_linear_f64(const float* x, int frames, int cols, const float* w, int rows, const float* bias,
+                             double* out);
+/* Non-causal multi-head attention in double over [frames][width] rows. */
+void oracle_attention_f64(const float* q, const float* k, const float* v, int frames, int width, int heads,
+                          double* out);
 
 typedef struct oracle_decoder oracle_decoder;
 
