@@ -117,6 +117,93 @@ def gemv_sweep(backend, rotate_bytes: int = 512 << 20):
     return results
 
 
+FP32_MFMA_PEAK = 157.3e12
+
+
+def float_gemv_sweep(backend, rotate_bytes: int = 512 << 20):
+    """FP32 ("original weights") GEMV at the decoder's projection shapes
+    (K -> N, 4 B per weight), each launch on a different copy, rotating
+    through at least `rotate_bytes` so that launches stream from HBM."""
+    from funasrnet_amd import device
+
+    rng = np.random.default_rng(5)
+    results = []
+    for K, N in GEMV_SHAPES:
+        w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        algorithmic = 4 * (N * K + K + N)
+        copies = [backend.float_weight(w.copy()) for _ in range(max(2, -(-rotate_bytes // algorithmic)))]
+        x = device.DeviceArray.from_numpy(rng.standard_normal(K).astype(np.float32))
+        out = device.DeviceArray(N, np.float32)
+        for c in copies:
+            backend.linear_device(x.ptr, 1, c, None, out.ptr)
+        backend.synchronize()
+        start, end = device.Event(), device.Event()
+        start.record(backend.stream)
+        for c in copies:
+            backend.linear_device(x.ptr, 1, c, None, out.ptr)
+        end.record(backend.stream)
+        end.synchronize()
+        avg_us = start.elapsed_ms(end) * 1000.0 / len(copies)
+        gbs = algorithmic / (avg_us * 1e-6) / 1e9
+        results.append({"shape": f"{K}->{N}", "avg_us": round(avg_us, 3), "algorithmic_bytes": algorithmic,
+                        "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": len(copies)})
+        for c in copies:
+            c.close()
+        backend._weights.clear()
+        x.free()
+        out.free()
+    return results
+
+
+def encoder_float(backend, frames: int = 1000, repeats: int = 20):
+    """The encoder's FP32 operations at one 60 s segment's shape (1000
+    frames, width 512, 4 heads; FunEncoder.cs:100-300): the projections on
+    fp32 MFMA (TFLOP/s against the 157.3 TFLOP/s dense fp32 peak) and the
+    non-causal attention, device-resident, HIP events over `repeats` runs."""
+    from funasrnet_amd import device
+
+    rng = np.random.default_rng(6)
+    out = {"frames": frames, "linear": []}
+    for K, N in ((512, 1536), (512, 512), (512, 2048), (2048, 512)):
+        w = backend.float_weight((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+        x = device.DeviceArray.from_numpy(rng.standard_normal((frames, K)).astype(np.float32))
+        y = device.DeviceArray(frames * N, np.float32)
+        backend.linear_device(x.ptr, frames, w, None, y.ptr)
+        backend.synchronize()
+        start, end = device.Event(), device.Event()
+        start.record(backend.stream)
+        for _ in range(repeats):
+            backend.linear_device(x.ptr, frames, w, None, y.ptr)
+        end.record(backend.stream)
+        end.synchronize()
+        us = start.elapsed_ms(end) * 1000.0 / repeats
+        flops = 2.0 * frames * N * K
+        out["linear"].append({"shape": f"{frames}x{K}->{N}", "avg_us": round(us, 2),
+                              "tflops": round(flops / (us * 1e-6) / 1e12, 2),
+                              "frac_of_fp32_mfma_peak": round(flops / (us * 1e-6) / FP32_MFMA_PEAK, 4)})
+        x.free()
+        y.free()
+    backend._weights.clear()
+    width, heads = 512, 4
+    q, k, v = (device.DeviceArray.from_numpy(rng.standard_normal((frames, width)).astype(np.float32)) for _ in range(3))
+    y = device.DeviceArray(frames * width, np.float32)
+    backend.attention_device(q.ptr, k.ptr, v.ptr, frames, width, heads, y.ptr)
+    backend.synchronize()
+    start, end = device.Event(), device.Event()
+    start.record(backend.stream)
+    for _ in range(repeats):
+        backend.attention_device(q.ptr, k.ptr, v.ptr, frames, width, heads, y.ptr)
+    end.record(backend.stream)
+    end.synchronize()
+    us = start.elapsed_ms(end) * 1000.0 / repeats
+    flops = 4.0 * frames * frames * width
+    out["attention"] = {"shape": f"{frames} frames x {width} ({heads} heads)", "avg_us": round(us, 2),
+                        "tflops": round(flops / (us * 1e-6) / 1e12, 2)}
+    for a in (q, k, v, y):
+        a.free()
+    return out
+
+
 def prefill_ttft(backend, weights, rows_list=(375, 750)):
     """Time to first token: one decode call on `rows` N(0,1) rows from
     position 0 (the MFMA GEMM prefill) plus the greedy pick, wall clock, best
@@ -436,7 +523,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU sample length")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the GEMV sweep, prefill, long-cache and sessions measurements")
-    ap.add_argument("--extra-only", choices=["gemv_sweep", "prefill", "long_kv", "sessions"],
+    ap.add_argument("--extra-only", choices=["gemv_sweep", "prefill", "long_kv", "sessions", "float_gemv_sweep",
+                                             "encoder_float"],
                     help="run one of the extra measurements alone and print its JSON (for profilers)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -455,7 +543,8 @@ def main() -> int:
     if args.extra_only:
         backend = HipBackend(0)
         run = {"gemv_sweep": lambda: gemv_sweep(backend), "prefill": lambda: prefill_ttft(backend, weights),
-               "long_kv": lambda: long_kv(backend, weights), "sessions": lambda: sessions_decode(backend, weights)}
+               "long_kv": lambda: long_kv(backend, weights), "sessions": lambda: sessions_decode(backend, weights),
+               "float_gemv_sweep": lambda: float_gemv_sweep(backend), "encoder_float": lambda: encoder_float(backend)}
         print(json.dumps({args.extra_only: run[args.extra_only]()}), flush=True)
         backend.close()
         return 0
@@ -494,6 +583,8 @@ def main() -> int:
     extra = {}
     if not args.no_extra:
         extra["gemv_sweep"] = gemv_sweep(backend)
+        extra["float_gemv_sweep"] = float_gemv_sweep(backend)
+        extra["encoder_float"] = encoder_float(backend)
         extra["prefill"] = prefill_ttft(backend, weights)
         extra["long_kv"] = long_kv(backend, weights)
         extra["sessions"] = sessions_decode(backend, weights,

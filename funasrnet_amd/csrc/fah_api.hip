@@ -1385,6 +1385,23 @@ int fah_linear(fah_context* h, const float* input, int frames, const fah_weight*
   });
 }
 
+int fah_linear_device(fah_context* h, const float* x, int frames, const fah_weight* w, const float* bias, float* out) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
+  if (!w || !w->f32) return FAH_DECLINED;
+  return guarded([&] {
+    require(frames > 0 && x && out, "invalid FP32 projection arguments");
+    require(w->ctx.get() == c, "weight belongs to another context");
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
+    check(fah::launch_f32_linear(x, w->f.as<float>(), bias, out, frames, w->rows, w->cols, false, c->stream),
+          "f32 linear");
+    return FAH_OK;
+  });
+}
+
 int fah_relu_projection(fah_context* h, const float* input, int frames, const fah_weight* first,
                         const float* first_bias, const fah_weight* second, const float* second_bias, float* output) {
   if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
@@ -1449,6 +1466,22 @@ int fah_attention(fah_context* h, const float* query, const float* key, const fl
     check(fah::launch_f32_attention(dq, dk, dv, c->out.as<float>(), frames, width, heads, c->stream), "attention");
     check(hipMemcpyAsync(output, c->out.ptr, bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return FAH_OK;
+  });
+}
+
+int fah_attention_device(fah_context* h, const float* query, const float* key, const float* value, int frames,
+                         int width, int heads, float* output) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
+  if (!fah::f32_attention_supported(frames, width, heads)) return FAH_DECLINED;
+  return guarded([&] {
+    require(query && key && value && output, "GPU attention needs query, key, value and output");
+    std::lock_guard<std::mutex> lock(c->gate);
+    if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
+    check(fah::launch_f32_attention(query, key, value, output, frames, width, heads, c->stream), "attention");
     return FAH_OK;
   });
 }

@@ -78,6 +78,8 @@ SIGNATURES = {
     "fah_quantize_device": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, _vp, _vp]),
     "fah_q8_gemv_device": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, _vp, _vp]),
     "fah_q8_block_dots_device": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
+    "fah_linear_device": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp, _vp]),
+    "fah_attention_device": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]),
     "fah_decoder_create": (ctypes.c_int, [_vp, ctypes.POINTER(DecoderConfigC), ctypes.POINTER(LayerHost),
                                           ctypes.POINTER(Q8Host), ctypes.POINTER(Q8Host), _f32p,
                                           ctypes.POINTER(_vp)]),
@@ -325,6 +327,13 @@ class HipBackend:
 
     def gemv_device(self, q_ptr: int, s_ptr: int, frames: int, weight: HipWeight, out_ptr: int) -> int:
         return _check(load().fah_q8_gemv_device(self.handle, q_ptr, s_ptr, frames, weight.handle, out_ptr))
+
+    def linear_device(self, x_ptr: int, frames: int, weight: HipFloatWeight, bias_ptr, out_ptr: int) -> int:
+        return _check(load().fah_linear_device(self.handle, x_ptr, frames, weight.handle, bias_ptr, out_ptr))
+
+    def attention_device(self, q_ptr: int, k_ptr: int, v_ptr: int, frames: int, width: int, heads: int,
+                         out_ptr: int) -> int:
+        return _check(load().fah_attention_device(self.handle, q_ptr, k_ptr, v_ptr, frames, width, heads, out_ptr))
 
     def block_dots_device(self, q_ptr: int, weight: HipWeight, dots_ptr: int):
         _check(load().fah_q8_block_dots_device(self.handle, q_ptr, weight.handle, dots_ptr))

@@ -184,6 +184,17 @@ int fah_quantize_device(fah_context* context, const float* x, int64_t n, int8_t*
 int fah_q8_gemv_device(fah_context* context, const int8_t* q, const float* scales, int frames,
                        const fah_weight* weight, float* out);
 
+/* fah_linear on device-resident buffers: out[frames*rows] = x[frames*cols]
+ * W^T (+ bias[rows], may be NULL) for an FP32 weight, ordered on the context
+ * stream (no copies, no wait). */
+int fah_linear_device(fah_context* context, const float* x, int frames, const fah_weight* weight, const float* bias,
+                      float* out);
+
+/* fah_attention on device-resident [frames][width] buffers, ordered on the
+ * context stream (no copies, no wait); same declines. */
+int fah_attention_device(fah_context* context, const float* query, const float* key, const float* value, int frames,
+                         int width, int heads, float* output);
+
 /* Exact int32 block dots dots[rows*cols/32] of one quantised activation row
  * against every weight row (the integer part of the projection,
  * TensorMath.QuantizedRowsAvx.cs:80-87), for bit-exact verification. */
