@@ -87,12 +87,13 @@ __global__ __launch_bounds__(256) void f32_gemm_kernel(const float* __restrict__
 }
 
 // ---- GEMV (few frames, weight-bandwidth bound) ------------------------------
-// One wave per weight row at a time, every lane a strided share of the row
-// (four floats per lane per step when rows are 16-byte aligned), the frames'
-// inputs in LDS, then a wave reduction per frame.
+// Each wave takes RW consecutive weight rows at a time (their loads all in
+// flight together), every lane a strided share of each row (four floats per
+// lane per step when rows are 16-byte aligned), the frames' inputs in LDS,
+// then a wave reduction per row and frame.
 constexpr int kVMaxFrames = 4, kVMaxK = 4096;
 
-template <bool RELU, bool VEC>
+template <bool RELU, bool VEC, int kVRows>
 __global__ __launch_bounds__(256) void f32_gemv_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                        const float* __restrict__ bias, float* __restrict__ out, int M,
                                                        int N, int K) {
@@ -101,40 +102,62 @@ __global__ __launch_bounds__(256) void f32_gemv_kernel(const float* __restrict__
   for (int i = tid; i < M * K; i += 256) x_s[i] = x[i];
   __syncthreads();
   const int waves = gridDim.x * 4;
-  for (int n = blockIdx.x * 4 + (tid >> 6); n < N; n += waves) {
-    float acc[kVMaxFrames] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const float* row = w + (size_t)n * K;
+  for (int n0 = (blockIdx.x * 4 + (tid >> 6)) * kVRows; n0 < N; n0 += waves * kVRows) {
+    float acc[kVRows][kVMaxFrames];
+#pragma unroll
+    for (int r = 0; r < kVRows; ++r)
+#pragma unroll
+      for (int f = 0; f < kVMaxFrames; ++f) acc[r][f] = 0.0f;
+    // Rows past N re-read row N - 1 (never stored).
+    const float* rows[kVRows];
+#pragma unroll
+    for (int r = 0; r < kVRows; ++r) rows[r] = w + (size_t)min(n0 + r, N - 1) * K;
     if (VEC) {
       for (int k = 4 * lane; k < K; k += 256) {
-        const float4 v = *reinterpret_cast<const float4*>(row + k);
+        float4 v[kVRows];
+#pragma unroll
+        for (int r = 0; r < kVRows; ++r) v[r] = *reinterpret_cast<const float4*>(rows[r] + k);
 #pragma unroll
         for (int f = 0; f < kVMaxFrames; ++f)
           if (f < M) {
             const float4 u = *reinterpret_cast<const float4*>(x_s + f * K + k);
-            acc[f] = __builtin_fmaf(v.x, u.x, acc[f]);
-            acc[f] = __builtin_fmaf(v.y, u.y, acc[f]);
-            acc[f] = __builtin_fmaf(v.z, u.z, acc[f]);
-            acc[f] = __builtin_fmaf(v.w, u.w, acc[f]);
+#pragma unroll
+            for (int r = 0; r < kVRows; ++r) {
+              acc[r][f] = __builtin_fmaf(v[r].x, u.x, acc[r][f]);
+              acc[r][f] = __builtin_fmaf(v[r].y, u.y, acc[r][f]);
+              acc[r][f] = __builtin_fmaf(v[r].z, u.z, acc[r][f]);
+              acc[r][f] = __builtin_fmaf(v[r].w, u.w, acc[r][f]);
+            }
           }
       }
     } else {
       for (int k = lane; k < K; k += 64) {
-        const float v = row[k];
+        float v[kVRows];
+#pragma unroll
+        for (int r = 0; r < kVRows; ++r) v[r] = rows[r][k];
 #pragma unroll
         for (int f = 0; f < kVMaxFrames; ++f)
-          if (f < M) acc[f] = __builtin_fmaf(v, x_s[f * K + k], acc[f]);
+          if (f < M) {
+            const float u = x_s[f * K + k];
+#pragma unroll
+            for (int r = 0; r < kVRows; ++r) acc[r][f] = __builtin_fmaf(v[r], u, acc[r][f]);
+          }
       }
     }
 #pragma unroll
-    for (int f = 0; f < kVMaxFrames; ++f) {
-      if (f >= M) break;
-      float s = acc[f];
+    for (int r = 0; r < kVRows; ++r) {
+      const int n = n0 + r;
 #pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-      if (lane == 0) {
-        float v = s + (bias ? bias[n] : 0.0f);
-        if (RELU) v = v < 0.0f ? 0.0f : v;
-        out[(size_t)f * N + n] = v;
+      for (int f = 0; f < kVMaxFrames; ++f) {
+        if (f >= M) break;
+        float s = acc[r][f];
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+        if (lane == 0 && n < N) {
+          float v = s + (bias ? bias[n] : 0.0f);
+          if (RELU) v = v < 0.0f ? 0.0f : v;
+          out[(size_t)f * N + n] = v;
+        }
       }
     }
   }
@@ -251,15 +274,20 @@ hipError_t launch_f32_linear(const float* x, const float* w, const float* bias, 
                              bool relu, hipStream_t s) {
   if (M < 1 || N < 1 || K < 1) return hipErrorInvalidValue;
   if (M <= kVMaxFrames && K <= kVMaxK) {
-    const int groups = std::min((N + 3) / 4, 2048);
+    // Four rows per wave when that still leaves 512+ workgroups, else one.
+    const bool wide = N >= 4 * 4 * 512;
+    const int per = wide ? 16 : 4;
+    const int groups = std::min((N + per - 1) / per, 2048);
     const bool vec = K % 4 == 0;
-    if (relu) {
-      if (vec) f32_gemv_kernel<true, true><<<groups, 256, 0, s>>>(x, w, bias, out, M, N, K);
-      else f32_gemv_kernel<true, false><<<groups, 256, 0, s>>>(x, w, bias, out, M, N, K);
+#define FAH_GEMV(R, V, RW) f32_gemv_kernel<R, V, RW><<<groups, 256, 0, s>>>(x, w, bias, out, M, N, K)
+    if (wide) {
+      if (relu) vec ? FAH_GEMV(true, true, 4) : FAH_GEMV(true, false, 4);
+      else vec ? FAH_GEMV(false, true, 4) : FAH_GEMV(false, false, 4);
     } else {
-      if (vec) f32_gemv_kernel<false, true><<<groups, 256, 0, s>>>(x, w, bias, out, M, N, K);
-      else f32_gemv_kernel<false, false><<<groups, 256, 0, s>>>(x, w, bias, out, M, N, K);
+      if (relu) vec ? FAH_GEMV(true, true, 1) : FAH_GEMV(true, false, 1);
+      else vec ? FAH_GEMV(false, true, 1) : FAH_GEMV(false, false, 1);
     }
+#undef FAH_GEMV
     return hipGetLastError();
   }
   const dim3 grid((N + kGT - 1) / kGT, (M + kGT - 1) / kGT);
