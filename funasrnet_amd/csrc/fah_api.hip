@@ -7,7 +7,9 @@
 #include "fah_internal.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
+#include <condition_variable>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
@@ -37,6 +39,11 @@ struct ArgumentError {
   std::string what;
 };
 
+// A call in the wrong state (FAH_ERROR_STATE), e.g. greedy without logits.
+struct StateError {
+  std::string what;
+};
+
 void require(bool ok, const std::string& what) {
   if (!ok) throw ArgumentError{what};
 }
@@ -47,6 +54,8 @@ int guarded(F&& f) {
     return f();
   } catch (const ArgumentError& e) {
     return fail(FAH_ERROR_ARGUMENT, e.what);
+  } catch (const StateError& e) {
+    return fail(FAH_ERROR_STATE, e.what);
   } catch (const DeviceError& e) {
     return fail(FAH_ERROR_DEVICE, e.what);
   } catch (const std::bad_alloc&) {
@@ -155,6 +164,7 @@ struct SessionBatch {
   std::vector<fah_decoder*> members;
   int max_positions = 0;
   DeviceBuffer table, x, a, qkv, q, h, xq, xs, logits, keys;
+  std::vector<fah::SessionRef> host_table;  // source of the last table upload (alive until the next)
   hipGraphExec_t graph = nullptr;
   SessionBatch() = default;
   SessionBatch(const SessionBatch&) = delete;
@@ -338,6 +348,33 @@ struct fah_decoder {
   ~fah_decoder() {
     for (hipEvent_t e : attn_events) (void)hipEventDestroy(e);
   }
+};
+
+// One blocking step request of a session in a step batcher.
+struct BatchRequest {
+  fah_decoder* session = nullptr;
+  int32_t token = 0;
+  int status = FAH_OK;
+  std::string error;
+  bool done = false;
+};
+
+// Cross-context step batcher: greedy steps of sessions of one weight set,
+// requested from different threads, run together as one lock-step batch.
+struct fah_batcher {
+  std::shared_ptr<Ctx> ctx;
+  std::shared_ptr<DecoderWeights> wt;
+  int max_positions = 0;
+  std::chrono::microseconds window{0};
+  std::mutex m;
+  std::condition_variable cv;
+  std::vector<BatchRequest*> pending;
+  std::vector<fah_decoder*> joined;
+  bool running = false;  // a leader is collecting or running a batch
+  int64_t batches_run = 0, rows_run = 0;
+  // The captured step of each batch size (the session table is rewritten
+  // before each launch).
+  std::unique_ptr<SessionBatch> by_size[fah::kFewFrames + 1];
 };
 
 namespace {
@@ -986,6 +1023,91 @@ void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s)
   check(fah::launch_greedy_keys(b.keys.as<unsigned long long>(), head_groups, b.logits.as<float>(), c.vocab, table,
                                 S, s),
         "session greedy");
+}
+
+// Session references of `sessions` into b.table, ordered on the stream; the
+// captured step reads the table when it runs, so a batch's graph serves any
+// sessions of its size.
+void upload_session_table(SessionBatch& b, fah_decoder* const* sessions, int count, hipStream_t s) {
+  b.host_table.assign(count, fah::SessionRef{});
+  for (int i = 0; i < count; ++i) {
+    const fah_decoder* d = sessions[i];
+    fah::SessionRef& r = b.host_table[i];
+    r.kcache = d->kcache.as<_Float16>();
+    r.vcache = d->vcache.as<_Float16>();
+    r.rope_cos = d->rope_cos.as<float>();
+    r.rope_sin = d->rope_sin.as<float>();
+    r.position = d->position.as<int>();
+    r.token = d->token.as<int>();
+    r.history = d->history.as<int>();
+    r.history_count = d->history_count.as<int>();
+    r.capacity = d->cfg.capacity;
+  }
+  check(hipMemcpyAsync(b.table.ptr, b.host_table.data(), (size_t)count * sizeof(fah::SessionRef),
+                       hipMemcpyHostToDevice, s),
+        "H2D session table");
+}
+
+// Row buffers and the captured lock-step step of `count` sessions of d0's
+// weights whose positions stay below `bound`.
+std::unique_ptr<SessionBatch> make_session_batch(const fah_decoder* d0, int count, int bound, hipStream_t s) {
+  auto b = std::make_unique<SessionBatch>();
+  b->members.assign(count, nullptr);
+  b->max_positions = bound;
+  const fah_decoder_config& k = d0->cfg;
+  const int widest = std::max(std::max(k.width, d0->q_width), k.ffn);
+  b->table.allocate((size_t)count * sizeof(fah::SessionRef));
+  b->x.allocate((size_t)count * k.width * 4);
+  b->a.allocate((size_t)count * k.width * 4);
+  b->qkv.allocate((size_t)count * (d0->q_width + 2 * d0->kv_width) * 4);
+  b->q.allocate((size_t)count * d0->q_width * 4);
+  b->h.allocate((size_t)count * k.ffn * 4);
+  b->xq.allocate((size_t)count * widest);
+  b->xs.allocate((size_t)count * (widest / 32) * 4);
+  b->logits.allocate((size_t)count * k.vocab * 4);
+  b->keys.allocate((size_t)count * std::max(1, fah::few_frame_groups(k.vocab, k.width, count, fah::kGemmGreedy)) * 8);
+  if (use_graphs()) {
+    hipGraph_t graph = nullptr;
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    try {
+      enqueue_sessions_step(d0, *b, s);
+    } catch (...) {
+      hipGraph_t dead = nullptr;
+      (void)hipStreamEndCapture(s, &dead);
+      if (dead) (void)hipGraphDestroy(dead);
+      throw;
+    }
+    check(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
+    hipError_t e = hipGraphInstantiate(&b->graph, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    check(e, "hipGraphInstantiate");
+  }
+  return b;
+}
+
+// Checks shared by the lock-step entry points: sessions of one weight set,
+// distinct, holding logits, with room for `steps` more positions; returns
+// the position bound the batch's step is sized for.
+int check_sessions(fah_decoder* const* sessions, int count, int steps) {
+  require(count >= 1 && count <= fah::kFewFrames, "at most " + std::to_string(fah::kFewFrames) + " sessions per batch");
+  const fah_decoder* d0 = sessions[0];
+  require(d0 != nullptr, "session is NULL");
+  require(d0->cfg.width % 128 == 0 && d0->cfg.ffn % 128 == 0 && d0->q_width % 128 == 0 && d0->cfg.ffn <= 3072,
+          "lock-step sessions need projection widths that are multiples of 128, at most 3072");
+  int bound = 0;
+  for (int i = 0; i < count; ++i) {
+    const fah_decoder* d = sessions[i];
+    require(d != nullptr, "session is NULL");
+    require(d->wt == d0->wt && d->ctx == d0->ctx, "sessions must share one decoder's weights");
+    for (int j = 0; j < i; ++j) require(sessions[j] != d, "a session appears twice");
+    if (!d->have_logits) throw StateError{"session " + std::to_string(i) + " has no logits: decode with logits first"};
+    require(d->host_position + steps <= d->cfg.capacity, "Decoder context exhausted");
+    require(d->host_position + steps <= kSessionPositions,
+            "lock-step sessions are limited to " + std::to_string(kSessionPositions) + " positions");
+    bound = std::max(bound, std::min(d->cfg.capacity, kSessionPositions));
+  }
+  return bound;
 }
 
 }  // namespace
@@ -1940,29 +2062,12 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
 int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int steps, int32_t* tokens) {
   if (!sessions || count < 1) return fail(FAH_ERROR_ARGUMENT, "no sessions");
   return guarded_decoder([&] {
-    require(count <= fah::kFewFrames, "at most " + std::to_string(fah::kFewFrames) + " sessions per batch");
     require(steps >= 0 && (steps == 0 || tokens), "invalid generate arguments");
-    const fah_decoder* d0 = sessions[0];
-    require(d0 != nullptr, "session is NULL");
-    require(d0->cfg.width % 128 == 0 && d0->cfg.ffn % 128 == 0 && d0->q_width % 128 == 0 && d0->cfg.ffn <= 3072,
-            "lock-step sessions need projection widths that are multiples of 128, at most 3072");
-    // The batched attention keeps one row's probabilities in LDS: positions
-    // up to kSessionPositions; the captured step is sized for that bound (or
-    // the largest capacity, if smaller) so it serves every later call.
-    int bound = 0;
-    for (int i = 0; i < count; ++i) {
-      const fah_decoder* d = sessions[i];
-      require(d != nullptr, "session is NULL");
-      require(d->wt == d0->wt && d->ctx == d0->ctx, "sessions must share one decoder's weights");
-      for (int j = 0; j < i; ++j) require(sessions[j] != d, "a session appears twice");
-      if (!d->have_logits)
-        return fail(FAH_ERROR_STATE, "session " + std::to_string(i) + " has no logits: decode with logits first");
-      require(d->host_position + steps <= d->cfg.capacity, "Decoder context exhausted");
-      require(d->host_position + steps <= kSessionPositions,
-              "lock-step sessions are limited to " + std::to_string(kSessionPositions) + " positions");
-      bound = std::max(bound, std::min(d->cfg.capacity, kSessionPositions));
-    }
+    // The captured step is sized for kSessionPositions (or the largest
+    // capacity, if smaller) so it serves every later call on these sessions.
+    const int bound = check_sessions(sessions, count, steps);
     if (steps == 0) return FAH_OK;
+    const fah_decoder* d0 = sessions[0];
     Ctx* c = d0->ctx.get();
     std::lock_guard<std::mutex> lock(c->gate);
     require_live(d0);
@@ -1972,52 +2077,9 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
     std::vector<fah_decoder*> members(sessions, sessions + count);
     if (!c->batch || c->batch->members != members || c->batch->max_positions != bound) {
       c->batch.reset();
-      auto b = std::make_unique<SessionBatch>();
+      auto b = make_session_batch(d0, count, bound, s);
+      upload_session_table(*b, sessions, count, s);
       b->members = members;
-      b->max_positions = bound;
-      const fah_decoder_config& k = d0->cfg;
-      const int widest = std::max(std::max(k.width, d0->q_width), k.ffn);
-      std::vector<fah::SessionRef> table(count);
-      for (int i = 0; i < count; ++i) {
-        fah_decoder* d = sessions[i];
-        fah::SessionRef& r = table[i];
-        r.kcache = d->kcache.as<_Float16>();
-        r.vcache = d->vcache.as<_Float16>();
-        r.rope_cos = d->rope_cos.as<float>();
-        r.rope_sin = d->rope_sin.as<float>();
-        r.position = d->position.as<int>();
-        r.token = d->token.as<int>();
-        r.history = d->history.as<int>();
-        r.history_count = d->history_count.as<int>();
-        r.capacity = d->cfg.capacity;
-      }
-      upload(b->table, table.data(), table.size() * sizeof(fah::SessionRef), s);
-      b->x.allocate((size_t)count * k.width * 4);
-      b->a.allocate((size_t)count * k.width * 4);
-      b->qkv.allocate((size_t)count * (d0->q_width + 2 * d0->kv_width) * 4);
-      b->q.allocate((size_t)count * d0->q_width * 4);
-      b->h.allocate((size_t)count * k.ffn * 4);
-      b->xq.allocate((size_t)count * widest);
-      b->xs.allocate((size_t)count * (widest / 32) * 4);
-      b->logits.allocate((size_t)count * k.vocab * 4);
-      b->keys.allocate((size_t)count * std::max(1, fah::few_frame_groups(k.vocab, k.width, count, fah::kGemmGreedy)) * 8);
-      if (use_graphs()) {
-        hipGraph_t graph = nullptr;
-        check(hipStreamSynchronize(s), "hipStreamSynchronize");
-        check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-        try {
-          enqueue_sessions_step(d0, *b, s);
-        } catch (...) {
-          hipGraph_t dead = nullptr;
-          (void)hipStreamEndCapture(s, &dead);
-          if (dead) (void)hipGraphDestroy(dead);
-          throw;
-        }
-        check(hipStreamEndCapture(s, &graph), "hipStreamEndCapture");
-        hipError_t e = hipGraphInstantiate(&b->graph, graph, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(graph);
-        check(e, "hipGraphInstantiate");
-      }
       c->batch = std::move(b);
     }
     SessionBatch& b = *c->batch;
@@ -2035,6 +2097,165 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
     for (int i = 0; i < count; ++i) sessions[i]->host_position += steps;
     return FAH_OK;
   });
+}
+
+int fah_batcher_create(fah_decoder* parent, int max_positions, int window_us, fah_batcher** out) {
+  if (!parent || !out) return fail(FAH_ERROR_ARGUMENT, "parent/out is NULL");
+  return guarded_decoder([&] {
+    require(max_positions >= 1 && max_positions <= kSessionPositions,
+            "batched sessions are limited to " + std::to_string(kSessionPositions) + " positions");
+    require(window_us >= 0 && window_us <= 1000000, "collection window out of range (0..1 s)");
+    const fah_decoder_config& k = parent->cfg;
+    require(k.width % 128 == 0 && k.ffn % 128 == 0 && parent->q_width % 128 == 0 && k.ffn <= 3072,
+            "lock-step sessions need projection widths that are multiples of 128, at most 3072");
+    std::lock_guard<std::mutex> lock(parent->ctx->gate);
+    require_live(parent);
+    auto b = std::make_unique<fah_batcher>();
+    b->ctx = parent->ctx;
+    b->wt = parent->wt;
+    b->max_positions = max_positions;
+    b->window = std::chrono::microseconds(window_us);
+    *out = b.release();
+    return FAH_OK;
+  });
+}
+
+int fah_batcher_destroy(fah_batcher* b) {
+  if (!b) return FAH_OK;
+  {
+    std::lock_guard<std::mutex> lk(b->m);
+    if (b->running || !b->pending.empty()) return fail(FAH_ERROR_STATE, "step batcher busy: a step is in progress");
+  }
+  std::shared_ptr<Ctx> st = b->ctx;
+  {
+    std::lock_guard<std::mutex> lock(st->gate);
+    (void)hipSetDevice(st->device);
+    (void)hipStreamSynchronize(st->stream);
+    delete b;
+  }
+  return FAH_OK;
+}
+
+int fah_batcher_join(fah_batcher* b, fah_decoder* session) {
+  if (!b || !session) return fail(FAH_ERROR_ARGUMENT, "batcher/session is NULL");
+  return guarded_decoder([&] {
+    require(session->wt == b->wt && session->ctx == b->ctx, "session does not share the batcher's weights");
+    std::lock_guard<std::mutex> lk(b->m);
+    if (std::find(b->joined.begin(), b->joined.end(), session) == b->joined.end()) b->joined.push_back(session);
+    b->cv.notify_all();
+    return FAH_OK;
+  });
+}
+
+int fah_batcher_leave(fah_batcher* b, fah_decoder* session) {
+  if (!b || !session) return fail(FAH_ERROR_ARGUMENT, "batcher/session is NULL");
+  std::lock_guard<std::mutex> lk(b->m);
+  b->joined.erase(std::remove(b->joined.begin(), b->joined.end(), session), b->joined.end());
+  b->cv.notify_all();
+  return FAH_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// One lock-step batch of the requests' sessions (one greedy step each, as
+// fah_decoder_generate(session, 1)): the batch size's captured step with
+// this batch's session table. Errors go to every request of the batch.
+void run_batch(fah_batcher* b, const std::vector<BatchRequest*>& reqs) {
+  std::vector<fah_decoder*> sessions;
+  for (BatchRequest* r : reqs) sessions.push_back(r->session);
+  const int count = (int)sessions.size();
+  int status = FAH_OK;
+  std::string message;
+  std::vector<int32_t> tokens(count, 0);
+  status = guarded_decoder([&] {
+    (void)check_sessions(sessions.data(), count, 1);
+    for (fah_decoder* d : sessions)
+      require(d->host_position + 1 <= b->max_positions, "session past the batcher's position bound");
+    Ctx* c = b->ctx.get();
+    std::lock_guard<std::mutex> lock(c->gate);
+    require_live(sessions[0]);
+    hipStream_t s = c->stream;
+    check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
+    auto& batch = b->by_size[count];
+    if (!batch) batch = make_session_batch(sessions[0], count, b->max_positions, s);
+    upload_session_table(*batch, sessions.data(), count, s);
+    for (fah_decoder* d : sessions) check(hipMemsetAsync(d->history_count.ptr, 0, 4, s), "reset history");
+    if (batch->graph) check(hipGraphLaunch(batch->graph, s), "hipGraphLaunch");
+    else enqueue_sessions_step(sessions[0], *batch, s);
+    for (int i = 0; i < count; ++i)
+      check(hipMemcpyAsync(&tokens[i], sessions[i]->history.ptr, 4, hipMemcpyDeviceToHost, s), "D2H token");
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    for (fah_decoder* d : sessions) d->host_position += 1;
+    return FAH_OK;
+  });
+  if (status != FAH_OK) message = fah_last_error();
+  for (int i = 0; i < count; ++i) {
+    reqs[i]->status = status;
+    reqs[i]->error = message;
+    reqs[i]->token = tokens[i];
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int fah_batcher_step(fah_batcher* b, fah_decoder* session, int32_t* token) {
+  if (!b || !session || !token) return fail(FAH_ERROR_ARGUMENT, "batcher/session/token is NULL");
+  if (session->wt != b->wt || session->ctx != b->ctx)
+    return fail(FAH_ERROR_ARGUMENT, "session does not share the batcher's weights");
+  BatchRequest req;
+  req.session = session;
+  std::unique_lock<std::mutex> lk(b->m);
+  for (BatchRequest* r : b->pending)
+    if (r->session == session) return fail(FAH_ERROR_STATE, "the session already has a step pending");
+  b->pending.push_back(&req);
+  b->cv.notify_all();
+  while (!req.done) {
+    if (!b->running) {
+      // Leader: collect the steps of the joined sessions (or of whoever
+      // arrives within the window), then run them as one batch.
+      b->running = true;
+      const auto deadline = std::chrono::steady_clock::now() + b->window;
+      auto want = [&] {
+        size_t joined_pending = 0;
+        for (BatchRequest* r : b->pending)
+          if (std::find(b->joined.begin(), b->joined.end(), r->session) != b->joined.end()) ++joined_pending;
+        const size_t full = std::min<size_t>(fah::kFewFrames, b->pending.size());
+        return full >= (size_t)fah::kFewFrames || (!b->joined.empty() && joined_pending >= b->joined.size());
+      };
+      while (!want()) {
+        if (b->cv.wait_until(lk, deadline) == std::cv_status::timeout) break;
+      }
+      const size_t n = std::min<size_t>(fah::kFewFrames, b->pending.size());
+      std::vector<BatchRequest*> batch(b->pending.begin(), b->pending.begin() + n);
+      b->pending.erase(b->pending.begin(), b->pending.begin() + n);
+      lk.unlock();
+      run_batch(b, batch);
+      lk.lock();
+      for (BatchRequest* r : batch) r->done = true;
+      ++b->batches_run;
+      b->rows_run += (int64_t)n;
+      b->running = false;
+      b->cv.notify_all();
+      continue;
+    }
+    b->cv.wait(lk);
+  }
+  if (req.status != FAH_OK) return fail(req.status, req.error);
+  *token = req.token;
+  return FAH_OK;
+}
+
+int fah_batcher_stats(fah_batcher* b, int64_t* batches, int64_t* rows) {
+  if (!b || !batches || !rows) return fail(FAH_ERROR_ARGUMENT, "batcher/batches/rows is NULL");
+  std::lock_guard<std::mutex> lk(b->m);
+  *batches = b->batches_run;
+  *rows = b->rows_run;
+  return FAH_OK;
 }
 
 int fah_decoder_kv_write(fah_decoder* d, int layer, const uint16_t* keys, const uint16_t* values, int positions) {

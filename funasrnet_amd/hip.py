@@ -92,6 +92,12 @@ SIGNATURES = {
     "fah_decoder_generate": (ctypes.c_int, [_vp, ctypes.c_int, _i32p]),
     "fah_decoder_create_session": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.POINTER(_vp)]),
     "fah_decoder_generate_sessions": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.c_int, ctypes.c_int, _i32p]),
+    "fah_batcher_create": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]),
+    "fah_batcher_destroy": (ctypes.c_int, [_vp]),
+    "fah_batcher_join": (ctypes.c_int, [_vp, _vp]),
+    "fah_batcher_leave": (ctypes.c_int, [_vp, _vp]),
+    "fah_batcher_step": (ctypes.c_int, [_vp, _vp, _i32p]),
+    "fah_batcher_stats": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
     "fah_decoder_kv_write": (ctypes.c_int, [_vp, ctypes.c_int, _u16p, _u16p, ctypes.c_int]),
     "fah_decoder_kv_read": (ctypes.c_int, [_vp, ctypes.c_int, _u16p, _u16p, ctypes.c_int]),
     "fah_decoder_weight_bytes": (ctypes.c_int64, [_vp]),
@@ -515,3 +521,45 @@ class HipDecoder:
     @property
     def persistent(self) -> bool:
         return bool(load().fah_decoder_persistent(self.handle))
+
+
+class HipStepBatcher:
+    """Cross-context step batching over the sessions of one decoder
+    (fah_batcher_*): worker threads each call step() for their own session
+    once per token; concurrent steps run as one lock-step batch."""
+
+    def __init__(self, parent: HipDecoder, max_positions: int, window_us: int = 200):
+        h = _vp()
+        _check(load().fah_batcher_create(parent.handle, max_positions, window_us, ctypes.byref(h)))
+        self.handle = h
+        self.parent = parent
+
+    def join(self, session: HipDecoder):
+        _check(load().fah_batcher_join(self.handle, session.handle))
+
+    def leave(self, session: HipDecoder):
+        _check(load().fah_batcher_leave(self.handle, session.handle))
+
+    def step(self, session: HipDecoder) -> int:
+        """One greedy step of `session` (its next token), batched with the
+        steps other threads request meanwhile."""
+        t = ctypes.c_int32()
+        _check(load().fah_batcher_step(self.handle, session.handle, ctypes.byref(t)))
+        return t.value
+
+    def stats(self):
+        """(batches run, session steps served)."""
+        a, b = ctypes.c_int64(), ctypes.c_int64()
+        _check(load().fah_batcher_stats(self.handle, ctypes.byref(a), ctypes.byref(b)))
+        return a.value, b.value
+
+    def close(self):
+        if self.handle:
+            _check(load().fah_batcher_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

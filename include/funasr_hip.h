@@ -50,6 +50,7 @@ extern "C" {
 typedef struct fah_context fah_context;
 typedef struct fah_weight fah_weight;
 typedef struct fah_decoder fah_decoder;
+typedef struct fah_batcher fah_batcher;
 
 /* Library ------------------------------------------------------------------ */
 
@@ -288,6 +289,38 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
  * (fah_decoder_create_session) and each must hold logits from its last
  * decode. tokens[count][steps], row i for sessions[i]. */
 int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int steps, int32_t* tokens);
+
+/* Cross-context step batching (the server side of FunAsr.Transcribe,
+ * src/FunAsrNet/FunAsr.cs:167-178, run by the worker threads of
+ * BoundedInferencePool, src/FunAsrNet/BoundedInferencePool.cs:22-230, over
+ * the N contexts of SpeechRuntime, src/FunAsrNet.Server/SpeechRuntime.cs:16-23).
+ * A batcher serves the sessions of one decoder's weights (the parent and its
+ * fah_decoder_create_session sessions). Each worker thread calls
+ * fah_batcher_step for its own session once per token; the steps requested
+ * at the same time run as one lock-step batch (each weight read once per
+ * step, up to 16 sessions), and each session's tokens equal those of
+ * fah_decoder_generate on it alone. No reference counterpart: the reference
+ * runs each context's decode separately.
+ *
+ * The first waiting thread collects: it runs the batch once every joined
+ * session has a step pending, 16 steps are pending, or `window_us` has
+ * passed since it began to collect (sessions that never join are batched
+ * with whatever arrives within the window). Sessions must stay below
+ * `max_positions` positions (at most 15360). */
+int fah_batcher_create(fah_decoder* parent, int max_positions, int window_us, fah_batcher** out);
+/* FAH_ERROR_STATE while a step is in progress. */
+int fah_batcher_destroy(fah_batcher* batcher);
+/* Register / unregister a session whose steps the collector waits for (a
+ * worker joins when its session starts decoding and leaves when it stops). */
+int fah_batcher_join(fah_batcher* batcher, fah_decoder* session);
+int fah_batcher_leave(fah_batcher* batcher, fah_decoder* session);
+/* One greedy step of `session` (Greedy -> Embed -> Decode(1), as
+ * fah_decoder_generate(session, 1, token)), batched with the steps other
+ * threads request at the same time; blocks until it has run. The session
+ * must hold logits from its last decode. */
+int fah_batcher_step(fah_batcher* batcher, fah_decoder* session, int32_t* token);
+/* Batches run and session steps served so far. */
+int fah_batcher_stats(fah_batcher* batcher, int64_t* batches, int64_t* rows);
 
 /* Overwrite cached K/V rows [0, positions) of one layer from fp16 bit
  * patterns laid out [positions][kv_heads*head_size] (long-context stress

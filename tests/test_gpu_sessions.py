@@ -152,3 +152,63 @@ def test_sixteen_qwen3_sessions(backend, oracle_lib):
         for d in sessions[1:]:
             d.close()
         parent.close()
+
+
+@pytest.mark.parametrize("shape", ["small", "qwen3"])
+def test_step_batcher_threads(backend, oracle_lib, shape):
+    """Eight worker threads, each decoding its own session (own prefix) with
+    the cross-context step batcher, one blocking step per token: every
+    session's tokens equal fah_decoder_generate on it alone, and the steps
+    really ran in batches."""
+    import threading
+    from funasrnet_amd.hip import HipDecoder, HipStepBatcher
+    cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
+    w = model.synthetic(cfg, seed=41)
+    count, steps, frames = 8, 24, 20 if shape == "small" else 150
+    capacity = frames + steps + 8
+    prefixes = [np.random.default_rng(100 + i).standard_normal((frames, cfg.width)).astype(np.float32)
+                for i in range(count)]
+    expected = []
+    alone = HipDecoder(backend, w, capacity=capacity)
+    try:
+        for p in prefixes:
+            alone.set_position(0)
+            alone.decode(p, frames)
+            expected.append(alone.generate(steps).tolist())
+    finally:
+        alone.close()
+    parent = HipDecoder(backend, w, capacity=capacity)
+    sessions = [parent] + [parent.session() for _ in range(count - 1)]
+    batcher = HipStepBatcher(parent, max_positions=capacity, window_us=2000)
+    results, errors = [None] * count, []
+
+    def worker(i):
+        try:
+            d = sessions[i]
+            d.decode(prefixes[i], frames)
+            batcher.join(d)
+            toks = [batcher.step(d) for _ in range(steps)]
+            batcher.leave(d)
+            results[i] = toks
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    print(f"step batcher {shape}: {count} threads x {steps} steps", flush=True)
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(count)]
+    try:
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=300)
+        assert not any(t.is_alive() for t in threads)
+        assert not errors, errors
+        assert results == expected
+        batches, rows = batcher.stats()
+        assert rows == count * steps
+        assert batches < rows, (batches, rows)  # steps were merged
+        print(f"batches {batches}, rows {rows}, mean batch {rows / batches:.2f}", flush=True)
+    finally:
+        batcher.close()
+        for d in sessions[1:]:
+            d.close()
+        parent.close()
