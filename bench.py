@@ -356,6 +356,61 @@ def sessions_decode(backend, weights, count: int = 16, steps: int = 128, prefix:
     return result
 
 
+def step_batcher_decode(backend, weights, count: int = 16, steps: int = 128, prefix: int = 150):
+    """Server-style decode: `count` worker threads, each with its own session
+    and 150-row prefix (seeds 1..count), each calling the cross-context step
+    batcher once per token (FunAsr.Transcribe's loop run by a pool's
+    workers); aggregate tok/s over the threads' decode phase (wall clock),
+    and the mean batch the batcher formed."""
+    import threading
+    from funasrnet_amd.hip import HipDecoder, HipStepBatcher
+
+    cfg = weights.config
+    capacity = prefix + steps + 8
+    parent = HipDecoder(backend, weights, capacity=capacity)
+    sessions = [parent] + [parent.session() for _ in range(count - 1)]
+    batcher = HipStepBatcher(parent, max_positions=capacity, window_us=2000)
+    start_gate = threading.Barrier(count + 1)
+    times = [0.0] * count
+    errors = []
+
+    def worker(i):
+        try:
+            d = sessions[i]
+            d.decode(np.random.default_rng(i + 1).standard_normal((prefix, cfg.width)).astype(np.float32), prefix)
+            batcher.join(d)
+            start_gate.wait()
+            for _ in range(steps):
+                batcher.step(d)
+            times[i] = time.perf_counter()
+            batcher.leave(d)
+        except Exception as e:  # reported in the result
+            errors.append(repr(e))
+            try:
+                start_gate.abort()
+            except Exception:
+                pass
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(count)]
+    try:
+        for t in threads:
+            t.start()
+        start_gate.wait()
+        t0 = time.perf_counter()
+        for t in threads:
+            t.join()
+        wall = max(times) - t0
+        batches, rows = batcher.stats()
+        return {"sessions": count, "steps": steps, "tok_s": round(count * steps / wall, 1),
+                "ms_per_batch": round(wall * 1e3 / max(batches, 1), 4), "batches": batches,
+                "mean_batch": round(rows / max(batches, 1), 2), "errors": errors}
+    finally:
+        batcher.close()
+        for d in sessions[1:]:
+            d.close()
+        parent.close()
+
+
 def sessions_oracle_check(weights, warm, toks, prefix: int, threads: int):
     """Every session's tokens (warm-up and timed steps) against the oracle
     decoding that session alone (FunAsr.Transcribe's loop, FunAsr.cs:167-178);
@@ -524,7 +579,7 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the GEMV sweep, prefill, long-cache and sessions measurements")
     ap.add_argument("--extra-only", choices=["gemv_sweep", "prefill", "long_kv", "sessions", "float_gemv_sweep",
-                                             "encoder_float"],
+                                             "encoder_float", "step_batcher"],
                     help="run one of the extra measurements alone and print its JSON (for profilers)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -544,7 +599,8 @@ def main() -> int:
         backend = HipBackend(0)
         run = {"gemv_sweep": lambda: gemv_sweep(backend), "prefill": lambda: prefill_ttft(backend, weights),
                "long_kv": lambda: long_kv(backend, weights), "sessions": lambda: sessions_decode(backend, weights),
-               "float_gemv_sweep": lambda: float_gemv_sweep(backend), "encoder_float": lambda: encoder_float(backend)}
+               "float_gemv_sweep": lambda: float_gemv_sweep(backend), "encoder_float": lambda: encoder_float(backend),
+               "step_batcher": lambda: step_batcher_decode(backend, weights)}
         print(json.dumps({args.extra_only: run[args.extra_only]()}), flush=True)
         backend.close()
         return 0
@@ -589,6 +645,7 @@ def main() -> int:
         extra["long_kv"] = long_kv(backend, weights)
         extra["sessions"] = sessions_decode(backend, weights,
                                             check=None if args.no_cpu else min(16, os.cpu_count() or 1))
+        extra["step_batcher"] = step_batcher_decode(backend, weights)
         if not args.no_cpu:
             extra["cpu_baselines"] = cpu_extra_baselines(weights, min(16, os.cpu_count() or 1))
     backend.close()
