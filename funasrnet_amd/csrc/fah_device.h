@@ -61,6 +61,12 @@ __device__ __forceinline__ float exp_ref(float value) {
 __device__ __forceinline__ _Float16 to_half(float f) { return (_Float16)f; }
 __device__ __forceinline__ float from_half(_Float16 h) { return (float)h; }
 
+// round(q * k) for an F16 k, as one mixed-precision fma with a +0 addend
+// (no separate conversion): equal to fmul(q, (float)k) except that a -0
+// product comes out +0. Callers only add it to sums that start at +0 and so
+// are never -0 (x + -0 = x + +0 for every x but -0), which are unchanged.
+__device__ __forceinline__ float mulh(float q, _Float16 k) { return __builtin_fmaf(q, (float)k, 0.0f); }
+
 // One 32-value block of TensorMath.Quantize (src/FunAsrNet/TensorMath.cs:397-411,
 // TensorMath.QuantizeAvx.cs:15-72): d = amax/127f; inv = d==0 ? 0 : 1f/d;
 // q = clamp(round_half_away(x*inv), -127, 127) with .NET's saturating
@@ -216,20 +222,21 @@ __device__ __forceinline__ void score8(float* acc, const uint4& kk, const float*
   const float4 q0 = *reinterpret_cast<const float4*>(q);
   const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
   const uint32_t w[4] = {kk.x, kk.y, kk.z, kk.w};
-  float k[8];
+  _Float16 k[8];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    k[2 * m] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu)));
-    k[2 * m + 1] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16)));
+    k[2 * m] = __builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu));
+    k[2 * m + 1] = __builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16));
   }
-  acc[0] = fadd(acc[0], fmul(q0.x, k[0]));
-  acc[1] = fadd(acc[1], fmul(q0.y, k[1]));
-  acc[2] = fadd(acc[2], fmul(q0.z, k[2]));
-  acc[3] = fadd(acc[3], fmul(q0.w, k[3]));
-  acc[4] = fadd(acc[4], fmul(q1.x, k[4]));
-  acc[5] = fadd(acc[5], fmul(q1.y, k[5]));
-  acc[6] = fadd(acc[6], fmul(q1.z, k[6]));
-  acc[7] = fadd(acc[7], fmul(q1.w, k[7]));
+  // The accumulators start at +0 (mulh's condition).
+  acc[0] = fadd(acc[0], mulh(q0.x, k[0]));
+  acc[1] = fadd(acc[1], mulh(q0.y, k[1]));
+  acc[2] = fadd(acc[2], mulh(q0.z, k[2]));
+  acc[3] = fadd(acc[3], mulh(q0.w, k[3]));
+  acc[4] = fadd(acc[4], mulh(q1.x, k[4]));
+  acc[5] = fadd(acc[5], mulh(q1.y, k[5]));
+  acc[6] = fadd(acc[6], mulh(q1.z, k[6]));
+  acc[7] = fadd(acc[7], mulh(q1.w, k[7]));
 }
 
 __device__ __forceinline__ float nan_max_p(float a, float b) {

@@ -288,10 +288,6 @@ __device__ __forceinline__ bool gather1(const u64* src, int count, uint32_t gen,
 
 __device__ __forceinline__ float tag_value(const u64* tag, int i) { return u2f((uint32_t)tag[i]); }
 
-// round(q * k) for an F16 k, as one mixed-precision fma with a +0 addend:
-// equal to fmul(q, (float)k) except that a -0 product comes out +0. Callers
-// only add it to sums that are never -0, so the sums are unchanged.
-__device__ __forceinline__ float mulh(float q, _Float16 k) { return __builtin_fmaf(q, (float)k, 0.0f); }
 
 // Time-ordered value sum of channel c = 2 * lane + HI over positions
 // [0, pos]: acc = acc + p[t] * v[t][c] from 0f in order (the reference's

@@ -363,14 +363,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
     float acc = 0.0f;
     int s = 0;
     for (; s + 16 <= nv; s += 16) {
-      float x[16];
+      _Float16 x[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) x[k] = from_half(v[(s + k) * hs]);
+      for (int k = 0; k < 16; ++k) x[k] = v[(s + k) * hs];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) acc = fadd(acc, fmul(x[k], p_s[s + k]));
+      for (int k = 0; k < 16; ++k) acc = fadd(acc, mulh(p_s[s + k], x[k]));
     }
-    for (; s < nv; ++s) acc = fadd(acc, fmul(from_half(v[s * hs]), p_s[s]));
-    if (fused) acc = fadd(acc, fmul(from_half(vcur_s[tid]), p_s[pos]));
+    for (; s < nv; ++s) acc = fadd(acc, mulh(p_s[s], v[s * hs]));
+    if (fused) acc = fadd(acc, mulh(p_s[pos], vcur_s[tid]));
     if (a.out) a.out[((size_t)t * a.heads + head) * hs + tid] = acc;
     q_s[tid] = acc;
   } else if (tid < hs) {
@@ -378,14 +378,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
     float acc = 0.0f;
     int s = 0;
     for (; s + 16 <= nv; s += 16) {
-      float x[16];
+      _Float16 x[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) x[k] = from_half(v[(size_t)(s + k) * hs]);
+      for (int k = 0; k < 16; ++k) x[k] = v[(size_t)(s + k) * hs];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) acc = fadd(acc, fmul(x[k], p_s[s + k]));
+      for (int k = 0; k < 16; ++k) acc = fadd(acc, mulh(p_s[s + k], x[k]));
     }
-    for (; s < nv; ++s) acc = fadd(acc, fmul(from_half(v[(size_t)s * hs]), p_s[s]));
-    if (fused) acc = fadd(acc, fmul(from_half(vcur_s[tid]), p_s[pos]));
+    for (; s < nv; ++s) acc = fadd(acc, mulh(p_s[s], v[(size_t)s * hs]));
+    if (fused) acc = fadd(acc, mulh(p_s[pos], vcur_s[tid]));
     if (a.out) a.out[((size_t)t * a.heads + head) * hs + tid] = acc;
     q_s[tid] = acc;
   }
@@ -585,11 +585,15 @@ __global__ __launch_bounds__(256) void greedy_keys_kernel(const unsigned long lo
 // in double-buffered LDS chunks; output rows quantised to Q8_0 per 32-block.
 constexpr int kRowBlock = 8;
 constexpr int kRowPairs = 2 * kRowBlock;
-constexpr int kPRow = kRowPairs + 4;  // p_s row stride (floats): 16-byte rows, fewer bank conflicts per column
-constexpr int kVRows = 64;  // V rows per LDS chunk (256 B each)
+// p_s row stride (floats): 8-byte rows; 18 puts the 16 lanes that walk one
+// pair's column on distinct banks.
+constexpr int kPRow = kRowPairs + 2;
+constexpr int kVRows = 16;   // V rows per LDS chunk (256 B each): one 16-byte load per thread
+constexpr int kVBufs = 3;    // chunks in LDS: the one being added and two in flight
 
+// Dynamic LDS of attn_rows_kernel: at 750 positions two workgroups fit a CU.
 __host__ __device__ inline size_t rows_lds_bytes(int nmax) {
-  return (size_t)kPRow * nmax * 4 + (size_t)2 * kVRows * 256;
+  return (((size_t)kPRow * nmax * 4 + 15) & ~(size_t)15) + (size_t)kVBufs * kVRows * 256;
 }
 
 __device__ __forceinline__ float max16_nan(float m) {  // over each row of 16 lanes
@@ -611,7 +615,7 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
   const int n0 = a.position + r0 + 1;  // positions the block's first row sees; row rr sees n0 + rr
   const int nmax = n0 + rows - 1;
   float* p_s = rows_s;  // [nmax][kPRow]
-  char* vbuf = reinterpret_cast<char*>(rows_s + (size_t)kPRow * nmax);
+  char* vbuf = reinterpret_cast<char*>(rows_s) + (((size_t)kPRow * nmax * 4 + 15) & ~(size_t)15);
   const _Float16* kc = a.kcache + (size_t)kh * a.capacity * hs;
   const _Float16* vc = a.vcache + (size_t)kh * a.capacity * hs;
   for (int i = tid; i < kRowPairs * hs; i += 256) {
@@ -637,25 +641,25 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const uint32_t w[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
-        float k8[8];
+        _Float16 k8[8];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          k8[2 * m] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu)));
-          k8[2 * m + 1] = from_half(__builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16)));
+          k8[2 * m] = __builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu));
+          k8[2 * m + 1] = __builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16));
         }
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const float* q = q_s + (4 * part + p) * hs + 8 * i;
           const float4 q0 = *reinterpret_cast<const float4*>(q);
           const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
-          acc[p][0] = fadd(acc[p][0], fmul(q0.x, k8[0]));
-          acc[p][1] = fadd(acc[p][1], fmul(q0.y, k8[1]));
-          acc[p][2] = fadd(acc[p][2], fmul(q0.z, k8[2]));
-          acc[p][3] = fadd(acc[p][3], fmul(q0.w, k8[3]));
-          acc[p][4] = fadd(acc[p][4], fmul(q1.x, k8[4]));
-          acc[p][5] = fadd(acc[p][5], fmul(q1.y, k8[5]));
-          acc[p][6] = fadd(acc[p][6], fmul(q1.z, k8[6]));
-          acc[p][7] = fadd(acc[p][7], fmul(q1.w, k8[7]));
+          acc[p][0] = fadd(acc[p][0], mulh(q0.x, k8[0]));
+          acc[p][1] = fadd(acc[p][1], mulh(q0.y, k8[1]));
+          acc[p][2] = fadd(acc[p][2], mulh(q0.z, k8[2]));
+          acc[p][3] = fadd(acc[p][3], mulh(q0.w, k8[3]));
+          acc[p][4] = fadd(acc[p][4], mulh(q1.x, k8[4]));
+          acc[p][5] = fadd(acc[p][5], mulh(q1.y, k8[5]));
+          acc[p][6] = fadd(acc[p][6], mulh(q1.z, k8[6]));
+          acc[p][7] = fadd(acc[p][7], mulh(q1.w, k8[7]));
         }
       }
       float sc[4];
@@ -665,7 +669,9 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
                              fadd(fadd(acc[p][2], acc[p][6]), fadd(acc[p][3], acc[p][7])));
         sc[p] = fdiv(v, a.divisor);
       }
-      *reinterpret_cast<float4*>(p_s + (size_t)t * kPRow + 4 * part) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+      float2* out2 = reinterpret_cast<float2*>(p_s + (size_t)t * kPRow + 4 * part);
+      out2[0] = make_float2(sc[0], sc[1]);
+      out2[1] = make_float2(sc[2], sc[3]);
     }
   }
   __syncthreads();
@@ -709,65 +715,58 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
   }
 
   // 3. Time-ordered value sums: lane = (head, channel), one sum per row of
-  // the block; V rows through LDS in chunks, the next chunk's loads in
-  // flight while the current one is added.
+  // the block. V rows reach LDS in chunks of kVRows by direct global->LDS
+  // loads (one 16-byte load per thread per chunk), two chunks ahead of the
+  // one being added.
   const int hh = tid >> 7, c = tid & 127;
   float acc[kRowBlock];
 #pragma unroll
   for (int rr = 0; rr < kRowBlock; ++rr) acc[rr] = 0.0f;
   const int chunks = (nmax + kVRows - 1) / kVRows;
-  uint4 pre0, pre1, pre2, pre3;
-#define FAH_LOAD_CHUNK(j)                                                                       \
-  do {                                                                                          \
-    const uint4* src_ = reinterpret_cast<const uint4*>(vc);                                     \
-    pre0 = src_[(size_t)min((j) * kVRows + ((tid) >> 4), nmax - 1) * 16 + (tid & 15)];          \
-    pre1 = src_[(size_t)min((j) * kVRows + ((tid + 256) >> 4), nmax - 1) * 16 + (tid & 15)];    \
-    pre2 = src_[(size_t)min((j) * kVRows + ((tid + 512) >> 4), nmax - 1) * 16 + (tid & 15)];    \
-    pre3 = src_[(size_t)min((j) * kVRows + ((tid + 768) >> 4), nmax - 1) * 16 + (tid & 15)];    \
-  } while (0)
-#define FAH_STORE_CHUNK(j)                                                                      \
-  do {                                                                                          \
-    uint4* dst_ = reinterpret_cast<uint4*>(vbuf + (size_t)((j) & 1) * kVRows * 256);            \
-    dst_[tid] = pre0;                                                                           \
-    dst_[tid + 256] = pre1;                                                                     \
-    dst_[tid + 512] = pre2;                                                                     \
-    dst_[tid + 768] = pre3;                                                                     \
-  } while (0)
-  FAH_LOAD_CHUNK(0);
-  FAH_STORE_CHUNK(0);
-  __syncthreads();
+  auto issue = [&](int j) {
+    const int row = min(j * kVRows + (tid >> 4), nmax - 1);
+    const char* src = reinterpret_cast<const char*>(vc) + (size_t)row * 256 + 16 * (tid & 15);
+    char* dst = vbuf + (size_t)(j % kVBufs) * kVRows * 256 + wave * 1024;
+    __builtin_amdgcn_global_load_lds(src, (lds_ptr)dst, 16, 0, 0);
+  };
+  // s_waitcnt immediate for vmcnt <= 1 (the newest chunk may stay in
+  // flight); expcnt and lgkmcnt not waited on.
+  constexpr int kWaitOlderChunk = 1 | (7 << 4) | (15 << 8);
+  issue(0);
+  if (chunks > 1) issue(1);
   for (int j = 0; j < chunks; ++j) {
-    if (j + 1 < chunks) FAH_LOAD_CHUNK(j + 1);
-    const _Float16* vr = reinterpret_cast<const _Float16*>(vbuf + (size_t)(j & 1) * kVRows * 256) + c;
+    if (j + 1 < chunks) __builtin_amdgcn_s_waitcnt(kWaitOlderChunk);
+    else __builtin_amdgcn_s_waitcnt(0);
+    // Every thread's part of chunk j is in LDS, and chunk j - 1's buffer,
+    // which chunk j + 2 reuses, is no longer read.
+    __syncthreads();
+    if (j + 2 < chunks) issue(j + 2);
+    const _Float16* vr = reinterpret_cast<const _Float16*>(vbuf + (size_t)(j % kVBufs) * kVRows * 256) + c;
     const int t0 = j * kVRows, len = min(kVRows, nmax - t0);
     const int all = max(0, min(len, n0 - t0));  // positions every row of the block sees
     int tt = 0;
     for (; tt < all; ++tt) {
-      const float v = from_half(vr[tt * hs]);
-      const float* pp = p_s + (size_t)(t0 + tt) * kPRow + 8 * hh;
-      const float4 pa = *reinterpret_cast<const float4*>(pp), pb = *reinterpret_cast<const float4*>(pp + 4);
-      acc[0] = fadd(acc[0], fmul(v, pa.x));
-      acc[1] = fadd(acc[1], fmul(v, pa.y));
-      acc[2] = fadd(acc[2], fmul(v, pa.z));
-      acc[3] = fadd(acc[3], fmul(v, pa.w));
-      acc[4] = fadd(acc[4], fmul(v, pb.x));
-      acc[5] = fadd(acc[5], fmul(v, pb.y));
-      acc[6] = fadd(acc[6], fmul(v, pb.z));
-      acc[7] = fadd(acc[7], fmul(v, pb.w));
+      const _Float16 v = vr[tt * hs];
+      const float2* pp = reinterpret_cast<const float2*>(p_s + (size_t)(t0 + tt) * kPRow + 8 * hh);
+      const float2 pa = pp[0], pb = pp[1], pc = pp[2], pd = pp[3];
+      acc[0] = fadd(acc[0], mulh(pa.x, v));
+      acc[1] = fadd(acc[1], mulh(pa.y, v));
+      acc[2] = fadd(acc[2], mulh(pb.x, v));
+      acc[3] = fadd(acc[3], mulh(pb.y, v));
+      acc[4] = fadd(acc[4], mulh(pc.x, v));
+      acc[5] = fadd(acc[5], mulh(pc.y, v));
+      acc[6] = fadd(acc[6], mulh(pd.x, v));
+      acc[7] = fadd(acc[7], mulh(pd.y, v));
     }
     for (; tt < len; ++tt) {
       const int t = t0 + tt;
-      const float v = from_half(vr[tt * hs]);
+      const _Float16 v = vr[tt * hs];
       const float* pp = p_s + (size_t)t * kPRow + 8 * hh;
 #pragma unroll
       for (int rr = 0; rr < kRowBlock; ++rr)
-        if (t < n0 + rr) acc[rr] = fadd(acc[rr], fmul(v, pp[rr]));
+        if (t < n0 + rr) acc[rr] = fadd(acc[rr], mulh(pp[rr], v));
     }
-    if (j + 1 < chunks) FAH_STORE_CHUNK(j + 1);
-    __syncthreads();
   }
-#undef FAH_LOAD_CHUNK
-#undef FAH_STORE_CHUNK
 
   // 4. Output rows (float and/or Q8_0 blocks).
 #pragma unroll
