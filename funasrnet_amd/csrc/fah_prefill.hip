@@ -5,16 +5,14 @@
 //
 // q8_gemm_kernel: out[t][r] = sum over blocks b, in order, from 0f, of
 // ((float)dot_b * w_scale[r][b]) * x_scale[t][b]. The exact int32 32-term
-// block dots come from one v_mfma_i32_32x32x32_i8 per block with a zero
-// accumulator (a 32-row x 32-frame tile per wave); the fp32 steps then run
-// on the accumulator registers in block order, so the result is the one of
-// the reference's per-row loop for every frame. A workgroup (4 waves) owns a
-// 64-row x 64-frame tile; its row and frame scales are staged in LDS as fp32.
+// block dots come from one v_mfma_i32_16x16x32_i8 per block and 16x16 tile
+// with a zero accumulator; the fp32 steps then run on the result registers
+// in block order, so the result is the one of the reference's per-row loop
+// for every frame. Row and frame scales are staged in LDS as fp32.
 //
-// Accumulator layout of v_mfma_i32_32x32x32_i8 (checked on gfx950): lane l,
-// register j holds C[m][n] with n = l % 32 and m = 8*(j/4) + 4*(l/32) + j%4;
-// the A (B) operand of lane l is 16 bytes of row (column) l % 32, lanes l and
-// l + 32 holding the two halves of the 32-byte block.
+// Lane layout of v_mfma_i32_16x16x32_i8 (checked on gfx950): the A (B)
+// operand of lane l is the 8 bytes [8 (l / 16), 8 (l / 16) + 8) of row
+// (column) l % 16; result register j of lane l is C[4 (l / 16) + j][l % 16].
 #include <algorithm>
 
 #include "fah_device.h"
@@ -26,7 +24,6 @@ namespace {
 constexpr int kGT = 256;  // threads per GEMM workgroup
 using lds_ptr = __attribute__((address_space(3))) void*;
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 
 struct ScaleF16 {
   using type = _Float16;
@@ -53,120 +50,209 @@ __device__ __forceinline__ int gate_up_row(int r, int kind, int base, int extra)
   return 2 * r0 + kind * count + (r - r0);
 }
 
-template <class Scale, int OUT>
+// One wave owns a (16 TR) x (16 TF) tile of 16x16 MFMA tiles; a workgroup
+// (4 waves, 2 x 2) owns (32 TR) x (32 TF). SwiGLU workgroups hold 16 TR gate
+// rows (waves 0 and 2) and the matching 16 TR up rows (waves 1 and 3).
+// Operands move through LDS in stages of four blocks (128 bytes of every
+// tile row, 16 bytes a lane): the next stage's global loads are in flight in
+// registers while the current stage is computed, then written to the other
+// LDS buffer. The 16-byte chunk c of tile row t sits at slot c ^ (t & 7), so
+// that the 16 rows of an MFMA operand read spread over the banks.
+constexpr int kStages = 2;
+constexpr int kStageBlocks = 4;
+
+template <class Scale, int OUT, int TR, int TF>
 __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) float gemm_s[];
   constexpr bool kSwiGLU = OUT == kGemmSwiGLU;
+  constexpr int RW = 16 * TR, FW = 16 * TF;  // wave tile
+  constexpr int RT = 2 * RW, FT = 2 * FW;    // workgroup tile (SwiGLU: gate rows then up rows)
+  constexpr int LR = kSwiGLU ? RW : RT;      // logical rows per workgroup
+  constexpr int US = LR + 4;                 // up_s row stride (floats)
+  constexpr int kRowBytes = 32 * kStageBlocks;
+  constexpr int kStageBytes = (RT + FT) * kRowBytes;
   const int B = g.K >> 5;
-  float* ws_s = gemm_s;           // [B][64] tile-row scales
-  float* xs_s = gemm_s + 64 * B;  // [B][64] frame scales
-  float* up_s = gemm_s + 128 * B; // SwiGLU: [64 frames][32 rows] up sums, rows padded to 33 floats
+  char* stage_s = reinterpret_cast<char*>(gemm_s);                             // [kStages][RT + FT][128 B]
+  float* ws_s = reinterpret_cast<float*>(stage_s + kStages * kStageBytes);     // [B][RT] row scales
+  float* xs_s = ws_s + B * RT;                                                 // [B][FT] frame scales
+  float* up_s = xs_s + B * FT;                                                 // SwiGLU: [FT][US] up sums
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int rw = wave & 1, fw = wave >> 1;
-  const int row0 = blockIdx.x * (kSwiGLU ? 32 : 64);  // logical rows
-  const int f0 = blockIdx.y * 64;
-  // Tile row tr (0..63) -> storage row, or -1 past the end. SwiGLU tiles
-  // hold 32 gate rows (tr < 32) and the matching 32 up rows.
+  const int wr = wave & 1, wf = wave >> 1;
+  const int row0 = blockIdx.x * LR, f0 = blockIdx.y * FT;
+  // Tile row tr (0..RT-1) -> storage row, or -1 past the end.
   auto storage_row = [&](int tr) -> int {
     if (kSwiGLU) {
-      const int r = row0 + (tr & 31);
+      const int r = row0 + tr % RW;
       if (r >= g.rows) return -1;
-      return g.gu_map ? g.gu_map[2 * r + (tr >> 5)] : gate_up_row(r, tr >> 5, g.split_base, g.split_extra);
+      return g.gu_map ? g.gu_map[2 * r + tr / RW] : gate_up_row(r, tr / RW, g.split_base, g.split_extra);
     }
     const int r = row0 + tr;
     return r < g.rows ? r : -1;
   };
+
+  // Stage loads: piece j of a stage is tile rows 8j..8j+7 (rows [0, RT) are
+  // weight rows, [RT, RT + FT) frames); lane l takes row 8j + l/8, chunk
+  // (l%8) ^ (row & 7), and writes it to slot l%8. Rows past the matrix and
+  // frames past the input load row / frame 0: never stored.
+  constexpr int kLoads = (RT + FT) / 8;
+  static_assert(kLoads % 4 == 0, "every wave moves the same number of pieces");
+  constexpr int kPerWave = kLoads / 4;
+  const int8_t* src[kPerWave];
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const int t = 8 * (wave + 4 * i) + (lane >> 3);
+    const int chunk = (lane & 7) ^ (t & 7);
+    if (t < RT) {
+      const int sr = storage_row(t);
+      src[i] = g.w + (size_t)max(sr, 0) * g.K + 16 * chunk;
+    } else {
+      const int f = f0 + t - RT;
+      src[i] = g.xq + (size_t)(f < g.frames ? f : 0) * g.K + 16 * chunk;
+    }
+  }
+  v4i pending[kPerWave];
+  auto fetch = [&](int st) {  // stage st: blocks [4 st, 4 st + 4)
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) pending[i] = *reinterpret_cast<const v4i*>(src[i] + (size_t)st * kRowBytes);
+  };
+  auto put = [&](int st) {
+    char* dst = stage_s + (st % kStages) * kStageBytes + 16 * lane;
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) *reinterpret_cast<v4i*>(dst + (wave + 4 * i) * 1024) = pending[i];
+  };
+  const int stages = B / kStageBlocks;
+  fetch(0);
+
   const typename Scale::type* ws = reinterpret_cast<const typename Scale::type*>(g.ws);
-  for (int i = tid; i < 64 * B; i += kGT) {
-    const int b = i >> 6, t = i & 63;
+  for (int i = tid; i < B * RT; i += kGT) {
+    const int b = i / RT, t = i % RT;
     const int sr = storage_row(t);
     ws_s[i] = sr >= 0 ? Scale::get(ws[(size_t)sr * B + b]) : 0.0f;
+  }
+  for (int i = tid; i < B * FT; i += kGT) {
+    const int b = i / FT, t = i % FT;
     xs_s[i] = f0 + t < g.frames ? g.xs[(size_t)(f0 + t) * B + b] : 0.0f;
   }
+  put(0);
+  fetch(min(1, stages - 1));
   lds_barrier();
 
-  const int ml = lane & 31, half = lane >> 5;
-  const int sr = storage_row(32 * rw + ml);
-  const int frame = f0 + 32 * fw + ml;
-  // Rows past the matrix and frames past the input read row / frame 0: their
-  // sums are never stored, and unconditional loads keep the prefetch exact
-  // (a conditional load makes the compiler wait for every load in flight).
-  const int8_t* ap = g.w + (size_t)max(sr, 0) * g.K + 16 * half;
-  const int8_t* bp = g.xq + (size_t)(frame < g.frames ? frame : 0) * g.K + 16 * half;
-  const v16i zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  float acc[16];
+  // MFMA operand of lane l: 8 bytes of row (frame) l % 16 at byte 8 (l / 16)
+  // of the block; result register j of lane l: row 4 (l / 16) + j, frame l % 16.
+  const int l16 = lane & 15, kq = lane >> 4;
+  int a_at[TR], b_at[TF];  // byte offsets of this lane's operand rows in a stage
 #pragma unroll
-  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  for (int tr = 0; tr < TR; ++tr) a_at[tr] = (wr * RW + 16 * tr + l16) * kRowBytes;
+#pragma unroll
+  for (int tf = 0; tf < TF; ++tf) b_at[tf] = (RT + wf * FW + 16 * tf + l16) * kRowBytes;
+  // Chunk 2 blk + kq/2 of row t sits at slot (2 blk + kq/2) ^ (t & 7); every
+  // operand row of this lane has t & 7 == l16 & 7.
+  auto at = [&](int row_at, int blk) { return row_at + 16 * ((2 * blk + (kq >> 1)) ^ (l16 & 7)) + 8 * (kq & 1); };
+  const v4i zero4 = {0, 0, 0, 0};
+  float acc[TR][TF][4];
+#pragma unroll
+  for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+    for (int tf = 0; tf < TF; ++tf)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[tr][tf][j] = 0.0f;
 
-  // Operands of four blocks are loaded one group ahead of their use (block
-  // index clamped: the loads past the last group are never used).
-  auto load4 = [&](v4i* av, v4i* bv, int b0) {
+  for (int st = 0; st < stages; ++st) {
+    const char* sa = stage_s + (st % kStages) * kStageBytes;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int b = min(b0 + k, B - 1);
-      av[k] = *reinterpret_cast<const v4i*>(ap + (size_t)b * 32);
-      bv[k] = *reinterpret_cast<const v4i*>(bp + (size_t)b * 32);
-    }
-  };
-  auto compute4 = [&](const v4i* av, const v4i* bv, int b0) {
+    for (int blk = 0; blk < kStageBlocks; ++blk) {
+      const int b = st * kStageBlocks + blk;
+      long av[TR], bv[TF];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int b = b0 + k;
-      if (b < B) {
-        const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[k], bv[k], zero16, 0, 0, 0);
-        const float xsv = xs_s[b * 64 + 32 * fw + ml];
+      for (int tr = 0; tr < TR; ++tr) av[tr] = *reinterpret_cast<const long*>(sa + at(a_at[tr], blk));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 w4 = *reinterpret_cast<const float4*>(ws_s + b * 64 + 32 * rw + 8 * q + 4 * half);
-          acc[4 * q + 0] = fadd(acc[4 * q + 0], fmul(fmul((float)c[4 * q + 0], w4.x), xsv));
-          acc[4 * q + 1] = fadd(acc[4 * q + 1], fmul(fmul((float)c[4 * q + 1], w4.y), xsv));
-          acc[4 * q + 2] = fadd(acc[4 * q + 2], fmul(fmul((float)c[4 * q + 2], w4.z), xsv));
-          acc[4 * q + 3] = fadd(acc[4 * q + 3], fmul(fmul((float)c[4 * q + 3], w4.w), xsv));
+      for (int tf = 0; tf < TF; ++tf) bv[tf] = *reinterpret_cast<const long*>(sa + at(b_at[tf], blk));
+      v4i d[TR][TF];
+#pragma unroll
+      for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+        for (int tf = 0; tf < TF; ++tf) d[tr][tf] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[tr], bv[tf], zero4, 0, 0, 0);
+      // The reference's ((float)dot * w_scale) * x_scale, added in block order.
+      float4 w4[TR];
+      float xv[TF];
+#pragma unroll
+      for (int tr = 0; tr < TR; ++tr) w4[tr] = *reinterpret_cast<const float4*>(ws_s + b * RT + wr * RW + 16 * tr + 4 * kq);
+#pragma unroll
+      for (int tf = 0; tf < TF; ++tf) xv[tf] = xs_s[b * FT + wf * FW + 16 * tf + l16];
+#pragma unroll
+      for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+        for (int tf = 0; tf < TF; ++tf) {
+          acc[tr][tf][0] = fadd(acc[tr][tf][0], fmul(fmul((float)d[tr][tf][0], w4[tr].x), xv[tf]));
+          acc[tr][tf][1] = fadd(acc[tr][tf][1], fmul(fmul((float)d[tr][tf][1], w4[tr].y), xv[tf]));
+          acc[tr][tf][2] = fadd(acc[tr][tf][2], fmul(fmul((float)d[tr][tf][2], w4[tr].z), xv[tf]));
+          acc[tr][tf][3] = fadd(acc[tr][tf][3], fmul(fmul((float)d[tr][tf][3], w4[tr].w), xv[tf]));
         }
-      }
     }
-  };
-  // Two register sets in turn (no copies between them, so the wait before
-  // a group's MFMAs leaves the other group's loads in flight).
-  v4i aA[4], bA[4], aB[4], bB[4];
-  load4(aA, bA, 0);
-  for (int b0 = 0; b0 < B; b0 += 8) {
-    load4(aB, bB, b0 + 4);
-    compute4(aA, bA, b0);
-    load4(aA, bA, b0 + 8);
-    compute4(aB, bB, b0 + 4);
+    // Stage st + 1 into the other buffer (last read at stage st - 1, before
+    // the previous barrier), then stage st + 2's loads into the registers
+    // (past the last stage: the last one again, unused).
+    put(st + 1);
+    fetch(min(st + 2, stages - 1));
+    lds_barrier();
   }
 
   if (!kSwiGLU) {
-    if (frame < g.frames) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int r = row0 + 32 * rw + 8 * (j >> 2) + 4 * half + (j & 3);
-        if (r < g.rows) {
-          float v = acc[j];
-          float* o = g.out + (size_t)frame * g.out_stride + r;
-          if (OUT == kGemmResidual) v = fadd(v, g.resid[(size_t)frame * g.out_stride + r]);
-          if (OUT == kGemmPlain && g.bias) v = fadd(g.bias[r], v);
-          *o = v;
+    for (int tf = 0; tf < TF; ++tf) {
+      const int f = f0 + wf * FW + 16 * tf + l16;
+      if (f >= g.frames) continue;
+#pragma unroll
+      for (int tr = 0; tr < TR; ++tr) {
+        const int r = row0 + wr * RW + 16 * tr + 4 * kq;
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = acc[tr][tf][j];
+          if (r + j < g.rows) {
+            if (OUT == kGemmResidual) v[j] = fadd(v[j], g.resid[(size_t)f * g.out_stride + r + j]);
+            if (OUT == kGemmPlain && g.bias) v[j] = fadd(g.bias[r + j], v[j]);
+          }
+        }
+        float* o = g.out + (size_t)f * g.out_stride + r;
+        if (r + 3 < g.rows && ((g.out_stride | r) & 3) == 0) {
+          *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (r + j < g.rows) o[j] = v[j];
         }
       }
     }
   } else {
     // SwiGLU (Elementwise.cs:167-196): gate waves meet their up rows in LDS.
-    if (rw == 1) {
+    if (wr == 1) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) up_s[(32 * fw + ml) * 33 + 8 * (j >> 2) + 4 * half + (j & 3)] = acc[j];
+      for (int tf = 0; tf < TF; ++tf)
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr)
+          *reinterpret_cast<float4*>(up_s + (wf * FW + 16 * tf + l16) * US + 16 * tr + 4 * kq) =
+              make_float4(acc[tr][tf][0], acc[tr][tf][1], acc[tr][tf][2], acc[tr][tf][3]);
     }
     lds_barrier();
-    if (rw == 0 && frame < g.frames) {
+    if (wr == 0) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int m = 8 * (j >> 2) + 4 * half + (j & 3);
-        const int r = row0 + m;
-        if (r < g.rows) {
-          const float gv = acc[j], u = up_s[(32 * fw + ml) * 33 + m];
-          const float silu = fdiv(gv, fadd(1.0f, exp_ref(-gv)));
-          g.out[(size_t)frame * g.out_stride + r] = fmul(silu, u);
+      for (int tf = 0; tf < TF; ++tf) {
+        const int f = f0 + wf * FW + 16 * tf + l16;
+        if (f >= g.frames) continue;
+#pragma unroll
+        for (int tr = 0; tr < TR; ++tr) {
+          const float4 u = *reinterpret_cast<const float4*>(up_s + (wf * FW + 16 * tf + l16) * US + 16 * tr + 4 * kq);
+          const float uj[4] = {u.x, u.y, u.z, u.w};
+          const int r = row0 + 16 * tr + 4 * kq;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (r + j < g.rows) {
+              const float gv = acc[tr][tf][j];
+              const float silu = fdiv(gv, fadd(1.0f, exp_ref(-gv)));
+              g.out[(size_t)f * g.out_stride + r + j] = fmul(silu, uj[j]);
+            }
+          }
         }
       }
     }
@@ -791,26 +877,47 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
   }
 }
 
+template <class Scale, int OUT, int TR, int TF>
+static hipError_t launch_gemm_tiles(const GemmArgs& g, hipStream_t s) {
+  constexpr int RW = 16 * TR, FW = 16 * TF;
+  constexpr int LR = OUT == kGemmSwiGLU ? RW : 2 * RW;
+  const int B = g.K / 32;
+  const size_t lds = (size_t)kStages * (2 * RW + 2 * FW) * 32 * kStageBlocks + (size_t)B * (2 * RW + 2 * FW) * 4 +
+                     (OUT == kGemmSwiGLU ? (size_t)2 * FW * (LR + 4) * 4 : 0);
+  static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(q8_gemm_kernel<Scale, OUT, TR, TF>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (raised != hipSuccess) return raised;
+  dim3 grid((g.rows + LR - 1) / LR, (g.frames + 2 * FW - 1) / (2 * FW));
+  q8_gemm_kernel<Scale, OUT, TR, TF><<<grid, kGT, lds, s>>>(g);
+  return hipGetLastError();
+}
+
+// Largest wave tile that still gives the chip about two waves per SIMD.
+template <class Scale, int OUT>
+static hipError_t launch_gemm_out(const GemmArgs& g, hipStream_t s) {
+  const long rows = (long)g.rows * (OUT == kGemmSwiGLU ? 2 : 1);
+  auto waves = [&](int tr, int tf) { return ((rows + 16 * tr - 1) / (16 * tr)) * ((g.frames + 16 * tf - 1) / (16 * tf)); };
+  constexpr long kWant = 2048;
+  if (waves(2, 2) >= kWant) return launch_gemm_tiles<Scale, OUT, 2, 2>(g, s);
+  if (waves(2, 1) >= kWant) return launch_gemm_tiles<Scale, OUT, 2, 1>(g, s);
+  return launch_gemm_tiles<Scale, OUT, 1, 1>(g, s);
+}
+
 template <class Scale>
 hipError_t launch_gemm_scaled(const GemmArgs& g, int out, hipStream_t s) {
-  const int B = g.K / 32;
-  const int rows_per_wg = out == kGemmSwiGLU ? 32 : 64;
-  dim3 grid((g.rows + rows_per_wg - 1) / rows_per_wg, (g.frames + 63) / 64);
-  const size_t lds = (size_t)128 * B * 4 + (out == kGemmSwiGLU ? 64 * 33 * 4 : 0);
   switch (out) {
-    case kGemmPlain: q8_gemm_kernel<Scale, kGemmPlain><<<grid, kGT, lds, s>>>(g); break;
-    case kGemmResidual: q8_gemm_kernel<Scale, kGemmResidual><<<grid, kGT, lds, s>>>(g); break;
-    case kGemmSwiGLU: q8_gemm_kernel<Scale, kGemmSwiGLU><<<grid, kGT, lds, s>>>(g); break;
+    case kGemmPlain: return launch_gemm_out<Scale, kGemmPlain>(g, s);
+    case kGemmResidual: return launch_gemm_out<Scale, kGemmResidual>(g, s);
+    case kGemmSwiGLU: return launch_gemm_out<Scale, kGemmSwiGLU>(g, s);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t s) {
-  // The row and frame scales of the whole K range live in LDS (512 B per
-  // block): K <= 3072 keeps the tile, with the SwiGLU exchange, under 64 KiB.
+  // Two operand stages and the row and frame scales of the whole K range
+  // (512 B per block) live in LDS: K <= 3072 keeps a workgroup under 90 KiB.
   if (g.K % 128 != 0 || g.K > 3072 || g.rows < 1 || g.frames < 1) return hipErrorInvalidValue;
   if (out == kGemmSwiGLU && !g.gu_map && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
   return half_scales ? launch_gemm_scaled<ScaleF16>(g, out, s) : launch_gemm_scaled<ScaleF32>(g, out, s);
