@@ -24,6 +24,7 @@ namespace {
 constexpr int kGT = 256;  // threads per GEMM workgroup
 using lds_ptr = __attribute__((address_space(3))) void*;
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 struct ScaleF16 {
   using type = _Float16;
@@ -70,12 +71,13 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
   constexpr int LR = kSwiGLU ? RW : RT;      // logical rows per workgroup
   constexpr int US = LR + 4;                 // up_s row stride (floats)
   constexpr int kRowBytes = 32 * kStageBlocks;
-  constexpr int kStageBytes = (RT + FT) * kRowBytes;
+  // A stage: operand rows [RT + FT][128 B], then the stage's scales as fp32,
+  // [4][RT] for the rows and [4][FT] for the frames.
+  constexpr int kOperandBytes = (RT + FT) * kRowBytes;
+  constexpr int kStageBytes = kOperandBytes + (RT + FT) * kStageBlocks * 4;
   const int B = g.K >> 5;
-  char* stage_s = reinterpret_cast<char*>(gemm_s);                             // [kStages][RT + FT][128 B]
-  float* ws_s = reinterpret_cast<float*>(stage_s + kStages * kStageBytes);     // [B][RT] row scales
-  float* xs_s = ws_s + B * RT;                                                 // [B][FT] frame scales
-  float* up_s = xs_s + B * FT;                                                 // SwiGLU: [FT][US] up sums
+  char* stage_s = reinterpret_cast<char*>(gemm_s);                                 // [kStages][kStageBytes]
+  float* up_s = reinterpret_cast<float*>(stage_s + kStages * kStageBytes);         // SwiGLU: [FT][US] up sums
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wr = wave & 1, wf = wave >> 1;
   const int row0 = blockIdx.x * LR, f0 = blockIdx.y * FT;
@@ -92,10 +94,13 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
 
   // Stage loads: piece j of a stage is tile rows 8j..8j+7 (rows [0, RT) are
   // weight rows, [RT, RT + FT) frames); lane l takes row 8j + l/8, chunk
-  // (l%8) ^ (row & 7), and writes it to slot l%8. Rows past the matrix and
-  // frames past the input load row / frame 0: never stored.
+  // (l%8) ^ (row & 7), and writes it to slot l%8. Threads [0, RT) also take
+  // their row's four block scales, threads [RT, RT + FT) their frame's. Rows
+  // past the matrix and frames past the input load row / frame 0 (scale 0):
+  // never stored.
   constexpr int kLoads = (RT + FT) / 8;
   static_assert(kLoads % 4 == 0, "every wave moves the same number of pieces");
+  static_assert(RT + FT <= kGT, "one scale load per thread");
   constexpr int kPerWave = kLoads / 4;
   const int8_t* src[kPerWave];
 #pragma unroll
@@ -110,29 +115,36 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
       src[i] = g.xq + (size_t)(f < g.frames ? f : 0) * g.K + 16 * chunk;
     }
   }
+  // Scales of a stage: thread t takes block t % 4 of row t / 4 and of frame
+  // t / 4 (rows and frames past the tile or the matrix read row / frame 0,
+  // and past the matrix store scale 0).
+  using ST = typename Scale::type;
+  static_assert(RT <= 64 && FT <= 64, "one row scale and one frame scale per thread");
+  const int sblk = tid & 3, srow = tid >> 2;
+  const int s_sr = srow < RT ? storage_row(srow) : -1;
+  const int s_f = f0 + srow;
+  const bool row_live = s_sr >= 0, frame_live = srow < FT && s_f < g.frames;
+  const ST* wsrc = reinterpret_cast<const ST*>(g.ws) + (size_t)max(s_sr, 0) * B + sblk;
+  const float* xsrc = g.xs + (size_t)(frame_live ? s_f : 0) * B + sblk;
   v4i pending[kPerWave];
+  ST wraw;
+  float xraw;
   auto fetch = [&](int st) {  // stage st: blocks [4 st, 4 st + 4)
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) pending[i] = *reinterpret_cast<const v4i*>(src[i] + (size_t)st * kRowBytes);
+    wraw = wsrc[kStageBlocks * st];
+    xraw = xsrc[kStageBlocks * st];
   };
   auto put = [&](int st) {
-    char* dst = stage_s + (st % kStages) * kStageBytes + 16 * lane;
+    char* base = stage_s + (st % kStages) * kStageBytes;
 #pragma unroll
-    for (int i = 0; i < kPerWave; ++i) *reinterpret_cast<v4i*>(dst + (wave + 4 * i) * 1024) = pending[i];
+    for (int i = 0; i < kPerWave; ++i) *reinterpret_cast<v4i*>(base + (wave + 4 * i) * 1024 + 16 * lane) = pending[i];
+    float* sc = reinterpret_cast<float*>(base + kOperandBytes);  // [4][RT] rows, then [4][FT] frames
+    if (srow < RT) sc[sblk * RT + srow] = row_live ? Scale::get(wraw) : 0.0f;
+    if (srow < FT) sc[kStageBlocks * RT + sblk * FT + srow] = frame_live ? xraw : 0.0f;
   };
   const int stages = B / kStageBlocks;
   fetch(0);
-
-  const typename Scale::type* ws = reinterpret_cast<const typename Scale::type*>(g.ws);
-  for (int i = tid; i < B * RT; i += kGT) {
-    const int b = i / RT, t = i % RT;
-    const int sr = storage_row(t);
-    ws_s[i] = sr >= 0 ? Scale::get(ws[(size_t)sr * B + b]) : 0.0f;
-  }
-  for (int i = tid; i < B * FT; i += kGT) {
-    const int b = i / FT, t = i % FT;
-    xs_s[i] = f0 + t < g.frames ? g.xs[(size_t)(f0 + t) * B + b] : 0.0f;
-  }
   put(0);
   fetch(min(1, stages - 1));
   lds_barrier();
@@ -159,9 +171,10 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
 
   for (int st = 0; st < stages; ++st) {
     const char* sa = stage_s + (st % kStages) * kStageBytes;
+    const float* ws_s = reinterpret_cast<const float*>(sa + kOperandBytes);  // [4][RT]
+    const float* xs_s = ws_s + kStageBlocks * RT;                           // [4][FT]
 #pragma unroll
     for (int blk = 0; blk < kStageBlocks; ++blk) {
-      const int b = st * kStageBlocks + blk;
       long av[TR], bv[TF];
 #pragma unroll
       for (int tr = 0; tr < TR; ++tr) av[tr] = *reinterpret_cast<const long*>(sa + at(a_at[tr], blk));
@@ -176,9 +189,9 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
       float4 w4[TR];
       float xv[TF];
 #pragma unroll
-      for (int tr = 0; tr < TR; ++tr) w4[tr] = *reinterpret_cast<const float4*>(ws_s + b * RT + wr * RW + 16 * tr + 4 * kq);
+      for (int tr = 0; tr < TR; ++tr) w4[tr] = *reinterpret_cast<const float4*>(ws_s + blk * RT + wr * RW + 16 * tr + 4 * kq);
 #pragma unroll
-      for (int tf = 0; tf < TF; ++tf) xv[tf] = xs_s[b * FT + wf * FW + 16 * tf + l16];
+      for (int tf = 0; tf < TF; ++tf) xv[tf] = xs_s[blk * FT + wf * FW + 16 * tf + l16];
 #pragma unroll
       for (int tr = 0; tr < TR; ++tr)
 #pragma unroll
@@ -881,8 +894,7 @@ template <class Scale, int OUT, int TR, int TF>
 static hipError_t launch_gemm_tiles(const GemmArgs& g, hipStream_t s) {
   constexpr int RW = 16 * TR, FW = 16 * TF;
   constexpr int LR = OUT == kGemmSwiGLU ? RW : 2 * RW;
-  const int B = g.K / 32;
-  const size_t lds = (size_t)kStages * (2 * RW + 2 * FW) * 32 * kStageBlocks + (size_t)B * (2 * RW + 2 * FW) * 4 +
+  const size_t lds = (size_t)kStages * (2 * RW + 2 * FW) * (32 + 4) * kStageBlocks +
                      (OUT == kGemmSwiGLU ? (size_t)2 * FW * (LR + 4) * 4 : 0);
   static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(q8_gemm_kernel<Scale, OUT, TR, TF>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -916,8 +928,8 @@ hipError_t launch_gemm_scaled(const GemmArgs& g, int out, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t s) {
-  // Two operand stages and the row and frame scales of the whole K range
-  // (512 B per block) live in LDS: K <= 3072 keeps a workgroup under 90 KiB.
+  // Operands and scales move through LDS in stages of four blocks, so K only
+  // bounds the int32 offsets; 3072 is the widest decoder matrix.
   if (g.K % 128 != 0 || g.K > 3072 || g.rows < 1 || g.frames < 1) return hipErrorInvalidValue;
   if (out == kGemmSwiGLU && !g.gu_map && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
   return half_scales ? launch_gemm_scaled<ScaleF16>(g, out, s) : launch_gemm_scaled<ScaleF32>(g, out, s);
