@@ -688,7 +688,7 @@ constexpr int kRowPairs = 2 * kRowBlock;
 // pair's column on distinct banks.
 constexpr int kPRow = kRowPairs + 2;
 constexpr int kVRows = 16;   // V rows per LDS chunk (256 B each): one 16-byte load per thread
-constexpr int kVBufs = 3;    // chunks in LDS: the one being added and two in flight
+constexpr int kVBufs = 2;    // chunks in LDS: the one being added and the next
 
 // Dynamic LDS of attn_rows_kernel: at 750 positions two workgroups fit a CU.
 __host__ __device__ inline size_t rows_lds_bytes(int nmax) {
@@ -814,32 +814,26 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
   }
 
   // 3. Time-ordered value sums: lane = (head, channel), one sum per row of
-  // the block. V rows reach LDS in chunks of kVRows by direct global->LDS
-  // loads (one 16-byte load per thread per chunk), two chunks ahead of the
-  // one being added.
+  // the block. V rows pass through LDS in chunks of kVRows (one 16-byte load
+  // per thread per chunk): the next chunk's loads are in flight in registers
+  // while the current chunk is added, then go to the other LDS buffer.
   const int hh = tid >> 7, c = tid & 127;
   float acc[kRowBlock];
 #pragma unroll
   for (int rr = 0; rr < kRowBlock; ++rr) acc[rr] = 0.0f;
   const int chunks = (nmax + kVRows - 1) / kVRows;
-  auto issue = [&](int j) {
+  typedef int v4i_t __attribute__((ext_vector_type(4)));
+  v4i_t vpend;
+  auto fetch_v = [&](int j) {  // rows past the last are read again, unused
     const int row = min(j * kVRows + (tid >> 4), nmax - 1);
-    const char* src = reinterpret_cast<const char*>(vc) + (size_t)row * 256 + 16 * (tid & 15);
-    char* dst = vbuf + (size_t)(j % kVBufs) * kVRows * 256 + wave * 1024;
-    __builtin_amdgcn_global_load_lds(src, (lds_ptr)dst, 16, 0, 0);
+    vpend = *reinterpret_cast<const v4i_t*>(reinterpret_cast<const char*>(vc) + (size_t)row * 256 + 16 * (tid & 15));
   };
-  // s_waitcnt immediate for vmcnt <= 1 (the newest chunk may stay in
-  // flight); expcnt and lgkmcnt not waited on.
-  constexpr int kWaitOlderChunk = 1 | (7 << 4) | (15 << 8);
-  issue(0);
-  if (chunks > 1) issue(1);
+  auto put_v = [&](int j) { *reinterpret_cast<v4i_t*>(vbuf + (size_t)(j % kVBufs) * kVRows * 256 + 16 * tid) = vpend; };
+  fetch_v(0);
+  put_v(0);
+  fetch_v(min(1, chunks - 1));
+  lds_barrier();
   for (int j = 0; j < chunks; ++j) {
-    if (j + 1 < chunks) __builtin_amdgcn_s_waitcnt(kWaitOlderChunk);
-    else __builtin_amdgcn_s_waitcnt(0);
-    // Every thread's part of chunk j is in LDS, and chunk j - 1's buffer,
-    // which chunk j + 2 reuses, is no longer read.
-    __syncthreads();
-    if (j + 2 < chunks) issue(j + 2);
     const _Float16* vr = reinterpret_cast<const _Float16*>(vbuf + (size_t)(j % kVBufs) * kVRows * 256) + c;
     const int t0 = j * kVRows, len = min(kVRows, nmax - t0);
     const int all = max(0, min(len, n0 - t0));  // positions every row of the block sees
@@ -865,6 +859,11 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
       for (int rr = 0; rr < kRowBlock; ++rr)
         if (t < n0 + rr) acc[rr] = fadd(acc[rr], mulh(pp[rr], v));
     }
+    // Chunk j + 1 into the other buffer (last read at chunk j - 1, before the
+    // previous barrier), then chunk j + 2's loads into the registers.
+    put_v(j + 1);
+    fetch_v(min(j + 2, chunks - 1));
+    lds_barrier();
   }
 
   // 4. Output rows (float and/or Q8_0 blocks).
