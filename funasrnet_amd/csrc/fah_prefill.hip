@@ -173,7 +173,10 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
     const char* sa = stage_s + (st % kStages) * kStageBytes;
     const float* ws_s = reinterpret_cast<const float*>(sa + kOperandBytes);  // [4][RT]
     const float* xs_s = ws_s + kStageBlocks * RT;                           // [4][FT]
-#pragma unroll
+    // Four-tile waves keep two blocks in flight (fewer registers, more waves
+    // a SIMD); single-tile waves all four.
+    constexpr int kBlkUnroll = TR * TF >= 4 ? 2 : kStageBlocks;
+#pragma unroll kBlkUnroll
     for (int blk = 0; blk < kStageBlocks; ++blk) {
       long av[TR], bv[TF];
 #pragma unroll
