@@ -337,7 +337,7 @@ struct fah_decoder {
   DeviceBuffer tx, tqkv, tatt, ta, th, tkeys, tattq, thq, epoch, error, timeline;
   fah::PersistentArgs pargs{};
   // Prefill (decode of many rows at once): row buffers grown on demand.
-  DeviceBuffer pf_x, pf_a, pf_qkv, pf_q, pf_h, pf_xq, pf_xs;
+  DeviceBuffer pf_x, pf_a, pf_qkv, pf_q, pf_h, pf_xq, pf_xs, pf_hq, pf_hs;
   // Attention timing of the multi-kernel step (FAH_ATTENTION_TIMES=1 at
   // creation): events around every layer's attention kernels, the steps
   // launched one by one and their attention time summed.
@@ -739,14 +739,26 @@ void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_
           "D2D prefill rows");
     int8_t* xq = d->pf_xq.as<int8_t>();
     float* xs = d->pf_xs.as<float>();
-    auto gemm = [&](const DeviceMatrix& m, int rows, float* out, int stride, const float* resid, int mode) {
+    // More rows than the few-frame kernel takes: the SwiGLU GEMM writes the
+    // Q8_0 blocks of its output itself (into pf_hq / pf_hs, which the down
+    // projection reads), with no separate quantisation pass.
+    const bool fused_h = !fah::few_frame_groups(c.ffn, c.width, T, fah::kGemmSwiGLU) && c.ffn % 32 == 0;
+    if (fused_h) {
+      d->pf_hq.ensure((size_t)T * c.ffn);
+      d->pf_hs.ensure((size_t)T * c.ffn / 32 * 4);
+    }
+    auto gemm = [&](const DeviceMatrix& m, int rows, float* out, int stride, const float* resid, int mode,
+                    const int8_t* in_q = nullptr, const float* in_s = nullptr, int8_t* out_q = nullptr,
+                    float* out_s = nullptr) {
       fah::GemmArgs g{};
       g.w = m.q.as<int8_t>();
       g.ws = m.s.ptr;
       g.rows = rows;
       g.K = m.cols;
-      g.xq = xq;
-      g.xs = xs;
+      g.xq = in_q ? in_q : xq;
+      g.xs = in_s ? in_s : xs;
+      g.out_q = out_q;
+      g.out_s = out_s;
       g.frames = T;
       g.out = out;
       g.out_stride = stride;
@@ -799,10 +811,17 @@ void prefill(fah_decoder* d, const float* x, int frames, bool logits, hipStream_
       check(fah::launch_norm_quantize_rows(d->pf_a.as<float>(), T, c.width, d->wt->ffn_norm[l].as<float>(), c.eps, xq, xs,
                                            s),
             "prefill ffn_norm");
-      gemm(d->wt->gateup[l], c.ffn, d->pf_h.as<float>(), c.ffn, nullptr, fah::kGemmSwiGLU);
-      check(fah::launch_norm_quantize_rows(d->pf_h.as<float>(), T, c.ffn, nullptr, 0.0f, xq, xs, s),
-            "prefill quantise ffn");
-      gemm(d->wt->down[l], c.width, d->pf_x.as<float>(), c.width, d->pf_a.as<float>(), fah::kGemmResidual);
+      if (fused_h) {
+        gemm(d->wt->gateup[l], c.ffn, d->pf_h.as<float>(), c.ffn, nullptr, fah::kGemmSwiGLU, nullptr, nullptr,
+             d->pf_hq.as<int8_t>(), d->pf_hs.as<float>());
+        gemm(d->wt->down[l], c.width, d->pf_x.as<float>(), c.width, d->pf_a.as<float>(), fah::kGemmResidual,
+             d->pf_hq.as<int8_t>(), d->pf_hs.as<float>());
+      } else {
+        gemm(d->wt->gateup[l], c.ffn, d->pf_h.as<float>(), c.ffn, nullptr, fah::kGemmSwiGLU);
+        check(fah::launch_norm_quantize_rows(d->pf_h.as<float>(), T, c.ffn, nullptr, 0.0f, xq, xs, s),
+              "prefill quantise ffn");
+        gemm(d->wt->down[l], c.width, d->pf_x.as<float>(), c.width, d->pf_a.as<float>(), fah::kGemmResidual);
+      }
     }
     check(fah::launch_advance(d->position.as<int>(), T, s), "advance");
     if (logits && done + T == frames) {

@@ -178,6 +178,11 @@ struct GemmArgs {
   // Greedy epilogue (few-frame kernel): the largest greedy key of each
   // workgroup's rows per frame, [frames][workgroups].
   unsigned long long* keys;
+  // Optional Q8_0 output of the SwiGLU epilogue of q8_gemm_kernel (rows a
+  // multiple of 32), in place of `out`: codes [frames][rows], scales
+  // [frames][rows/32].
+  int8_t* out_q;
+  float* out_s;
 };
 enum GemmOut { kGemmPlain = 0, kGemmResidual = 1, kGemmSwiGLU = 2, kGemmGreedy = 3 };
 

@@ -255,19 +255,55 @@ __global__ __launch_bounds__(kGT) void q8_gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int tf = 0; tf < TF; ++tf) {
         const int f = f0 + wf * FW + 16 * tf + l16;
-        if (f >= g.frames) continue;
+        float h[TR][4];
 #pragma unroll
         for (int tr = 0; tr < TR; ++tr) {
           const float4 u = *reinterpret_cast<const float4*>(up_s + (wf * FW + 16 * tf + l16) * US + 16 * tr + 4 * kq);
           const float uj[4] = {u.x, u.y, u.z, u.w};
-          const int r = row0 + 16 * tr + 4 * kq;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            if (r + j < g.rows) {
-              const float gv = acc[tr][tf][j];
-              const float silu = fdiv(gv, fadd(1.0f, exp_ref(-gv)));
-              g.out[(size_t)f * g.out_stride + r + j] = fmul(silu, uj[j]);
+            const float gv = acc[tr][tf][j];
+            const float silu = fdiv(gv, fadd(1.0f, exp_ref(-gv)));
+            h[tr][j] = fmul(silu, uj[j]);
+          }
+        }
+        if (TR == 2 && g.out_q) {
+          // The 32 rows of the workgroup are one Q8_0 block of frame f, held
+          // by lanes l16, l16 + 16, l16 + 32, l16 + 48 (eight values each):
+          // TensorMath.Quantize of the block (amax over the bit patterns).
+          uint32_t m = 0;
+#pragma unroll
+          for (int tr = 0; tr < TR; ++tr)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint32_t a = f2u(h[tr][j]) & 0x7fffffffu;
+              m = a > m ? a : m;
             }
+          uint32_t o = (uint32_t)__shfl_xor((int)m, 16);
+          m = o > m ? o : m;
+          o = (uint32_t)__shfl_xor((int)m, 32);
+          m = o > m ? o : m;
+          float inverse;
+          const float d = block_scale(m, &inverse);
+          if (f < g.frames) {
+            int8_t* q = g.out_q + (size_t)f * g.rows + row0 + 4 * kq;
+#pragma unroll
+            for (int tr = 0; tr < TR; ++tr) {
+              const uint32_t packed = (uint32_t)(uint8_t)quantize_value(h[tr][0], inverse) |
+                                      ((uint32_t)(uint8_t)quantize_value(h[tr][1], inverse) << 8) |
+                                      ((uint32_t)(uint8_t)quantize_value(h[tr][2], inverse) << 16) |
+                                      ((uint32_t)(uint8_t)quantize_value(h[tr][3], inverse) << 24);
+              *reinterpret_cast<uint32_t*>(q + 16 * tr) = packed;
+            }
+            if (kq == 0) g.out_s[(size_t)f * (g.rows / 32) + row0 / 32] = d;
+          }
+        } else if (f < g.frames) {
+#pragma unroll
+          for (int tr = 0; tr < TR; ++tr) {
+            const int r = row0 + 16 * tr + 4 * kq;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (r + j < g.rows) g.out[(size_t)f * g.out_stride + r + j] = h[tr][j];
           }
         }
       }
@@ -913,7 +949,8 @@ static hipError_t launch_gemm_out(const GemmArgs& g, hipStream_t s) {
   auto waves = [&](int tr, int tf) { return ((rows + 16 * tr - 1) / (16 * tr)) * ((g.frames + 16 * tf - 1) / (16 * tf)); };
   constexpr long kWant = 2048;
   if (waves(2, 2) >= kWant) return launch_gemm_tiles<Scale, OUT, 2, 2>(g, s);
-  if (waves(2, 1) >= kWant) return launch_gemm_tiles<Scale, OUT, 2, 1>(g, s);
+  // A quantised SwiGLU output needs 32-row tiles (one Q8_0 block a frame).
+  if (waves(2, 1) >= kWant || (OUT == kGemmSwiGLU && g.out_q)) return launch_gemm_tiles<Scale, OUT, 2, 1>(g, s);
   return launch_gemm_tiles<Scale, OUT, 1, 1>(g, s);
 }
 
@@ -934,6 +971,7 @@ hipError_t launch_gemm(const GemmArgs& g, bool half_scales, int out, hipStream_t
   // bounds the int32 offsets; 3072 is the widest decoder matrix.
   if (g.K % 128 != 0 || g.K > 3072 || g.rows < 1 || g.frames < 1) return hipErrorInvalidValue;
   if (out == kGemmSwiGLU && !g.gu_map && (g.split_base < 1 || g.split_extra < 0)) return hipErrorInvalidValue;
+  if (g.out_q && (out != kGemmSwiGLU || g.rows % 32 != 0 || !g.out_s)) return hipErrorInvalidValue;
   return half_scales ? launch_gemm_scaled<ScaleF16>(g, out, s) : launch_gemm_scaled<ScaleF32>(g, out, s);
 }
 
