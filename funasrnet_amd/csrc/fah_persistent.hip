@@ -701,29 +701,37 @@ __device__ __forceinline__ void quantize_input(const u64* act, const float* norm
 
 }  // namespace
 
-// Memory wave m's part of the RMSNorm square sum of a K-value vector
-// (K <= 1024): threads t = 64m + lane of the GEMV prologue's tree hold values
-// 4t..4t+3, i.e. chunks 2m and 2m + 1, which this wave gathered itself.
+// Chunk c's part of the RMSNorm square sum of a K-value vector (K <= 1024):
+// values 128c .. 128c + 127, i.e. threads 32c .. 32c + 31 of the GEMV
+// prologue's tree (four values each), which hold one half (lanes 0-31 or
+// 32-63) of one of its waves. The DPP steps of wave_sum_double stay inside
+// rows of 16 lanes, so lanes 0 and 16 here hold exactly that wave's row sums
+// of this half, and red[c] = row0 + row1 is the half the wave's tree adds
+// last: the full tree is (red[2m] + red[2m + 1]) per wave m.
 template <int K>
-__device__ __forceinline__ void norm_partial(const u64* act, int m, double* red) {
+__device__ __forceinline__ void norm_chunk_partial(const u64* act, int c, double* red) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int e = 4 * (kWave * m + lane);
-  const float4 v = e < K ? tag_float4(act, e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  const int e = 128 * c + 4 * lane;
+  const float4 v = (lane < 32 && e < K) ? tag_float4(act, e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   double sq = 0.0;
   sq += (double)v.x * (double)v.x + (double)v.y * (double)v.y;
   sq += (double)v.z * (double)v.z + (double)v.w * (double)v.w;
-  sq = wave_sum_double(sq);
-  if (lane == 0) red[m] = sq;
+  sq += dpp_double<kDppQuadXor1>(sq);
+  sq += dpp_double<kDppQuadXor2>(sq);
+  sq += dpp_double<kDppHalfMirror>(sq);
+  sq += dpp_double<kDppMirror>(sq);
+  const double half = readlane_double(sq, 0) + readlane_double(sq, 16);
+  if (lane == 0) red[c] = half;
 }
 
-// After the barrier that follows norm_partial: the inverse RMS from the four
-// wave sums in order, then the scaled vector quantised.
+// After the barrier that follows norm_chunk_partial: the inverse RMS from the
+// four wave sums (each the sum of its two halves) in order, then the scaled vector quantised.
 template <int K>
 __device__ __forceinline__ void quantize_norm_chunks(const u64* act, const float* norm_w, float eps, const double* red,
                                                      int* xq, float* xs) {
   double total = 0.0;
 #pragma unroll
-  for (int i = 0; i < kMem / kWave; ++i) total += red[i];
+  for (int i = 0; i < kMem / kWave; ++i) total += red[2 * i] + red[2 * i + 1];
   const float mean = (float)(total / (double)K);
   const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
   quantize4<K, true>(act, norm_w, inverse, xq, xs);
@@ -773,7 +781,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ float row_s[2][64];  // residual rows: [0] x, [1] a
   __shared__ double red_s[kPT / kWave];
   __shared__ int flag_s;
-  __shared__ int okw_s[kMem / kWave];  // per memory wave: its part of the last gather completed
+  __shared__ int okw_s[kPT / kWave];  // per wave: its part of the last gather completed
   __shared__ __attribute__((aligned(16))) float cur_s[3][128];  // attention: q, k, v of the current position
   __shared__ __attribute__((aligned(16))) float tmax_s[kPT / kWave];
   __shared__ float inv_s;
@@ -1162,42 +1170,41 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       tag_s[tid + k * kPT] = (u64)f2u(a.mode == 2 ? fmul((float)eq[k], (float)es[k]) : xr[k]);
     lds_barrier_p();
     // The layer-0 input's norm partials (later inputs get theirs in the gather).
-    if (ct < 0) {
-      if (wave < W / 256) norm_partial<W>(tag_s, wave, red_s);
-      else if (lane == 0) red_s[wave] = 0.0;
-    }
+    norm_chunk_partial<W>(tag_s, wave, red_s);
     lds_barrier_p();
 
-    // The next phase's input, gathered by the memory waves (each a part of
-    // the chunks; wave 0 also copies the constants `pre` names). An input
-    // that is RMS-normalised (W values) is split so that wave m holds chunks
-    // 2m and 2m + 1 and adds its part of the square sum as soon as they are
-    // in; the quantised ones are split in four.
+    // The next phase's input. An input that is RMS-normalised (W values, one
+    // 1 KB chunk per wave) is gathered by all eight waves (wave 0 also copies
+    // the constants `pre` names), each polling its chunk whole and adding
+    // that chunk's part of the square sum as soon as it is in; the quantised
+    // attention output is gathered by the memory waves (a quarter each) while
+    // the compute waves stage weight slices.
     auto gather_norm = [&](const u64* src, uint32_t gn, auto pre) {
-      if (ct < 0) {
-        constexpr int parts = W / 256;
-        bool ok = true;
-        if (wave < parts) {
-          ok = wave == 0 ? gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, pre, wave, parts)
-                         : gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, NoPre{}, wave, parts);
-          if (ok) norm_partial<W>(tag_s, wave, red_s);
-        } else if (lane == 0) {
-          red_s[wave] = 0.0;
-        }
-        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      constexpr int parts = W / 128;
+      bool ok = true;
+      if (wave < parts) {
+        ok = wave == 0 ? gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, pre, wave, parts)
+                       : gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, NoPre{}, wave, parts);
+        if (ok) norm_chunk_partial<W>(tag_s, wave, red_s);
+      } else if (lane == 0) {
+        red_s[wave] = 0.0;
       }
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
     };
     auto gather_q = [&](const u64* src, int count, uint32_t gn) {
-      if (ct < 0) {
-        const bool ok = gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gn), tag_s, a.error, NoPre{}, wave, 4,
-                               NoChunk{}, nullptr, kQTagMask);
-        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
-      }
+      bool ok = true;
+      if (ct < 0)
+        ok = gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gn), tag_s, a.error, NoPre{}, wave, 4, NoChunk{},
+                    nullptr, kQTagMask);
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
     };
     auto gathered = [&] {
       lds_barrier_p();
       t_in = __builtin_amdgcn_s_memrealtime();
-      return (okw_s[0] & okw_s[1] & okw_s[2] & okw_s[3]) != 0;
+      int all = 1;
+#pragma unroll
+      for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
+      return all != 0;
     };
 
     // Each phase: all threads quantise (or unpack) the gathered input and
@@ -1273,7 +1280,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // The pair owners quantise their blocks (read through this XCD's L2)
       // and publish them; every projection workgroup gathers the quantised
       // vector.
-      if (ct < 0) {
+      // The quantised ffn vector (QWH / 128 <= 8 chunks) is gathered one
+      // chunk per wave, polled whole; wave 0 (the owner's publisher) and as
+      // few others as possible take none.
+      {
         bool ok = true;
         if (wave == 0 && own >= 0) {
           u64 seen = 0;
@@ -1284,8 +1294,8 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
         }
         if (ok)
-          ok = gather(a.thq, QWH, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gen(l, 4)), tag_s, a.error, NoPre{}, wave, 4,
-                      NoChunk{}, nullptr, kQTagMask);
+          ok = gather(a.thq, QWH, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gen(l, 4)), tag_s, a.error, NoPre{}, wave,
+                      kPT / kWave, NoChunk{}, nullptr, kQTagMask);
         if (lane == 0) okw_s[wave] = ok ? 1 : 0;
       }
       if (!gathered()) return;
