@@ -718,20 +718,32 @@ __global__ __launch_bounds__(256) void greedy_keys_kernel(const unsigned long lo
 // reads. Per pair the arithmetic is the decode path's (AttentionAvx.cs:74-224,
 // SoftmaxAvx.cs:11-58, per row as QwenDecoder.cs:206-224 does): eight
 // channel-strided score accumulators and their pairwise tree, the exact
-// softmax with a double denominator, time-ordered value sums. Layout: scores
-// and probabilities [position][pair] in LDS (pair = head * 8 + row), V rows
-// in double-buffered LDS chunks; output rows quantised to Q8_0 per 32-block.
+// softmax with a double denominator, time-ordered value sums; output rows
+// quantised to Q8_0 per 32-block.
+//
+// The products go to the matrix cores: a K = 1 fp32 MFMA
+// (v_mfma_f32_16x16x1f32, four 16 x 16 blocks, zero accumulator input) is an
+// outer product whose every element is the IEEE product round(a * b) -- the
+// reference's fmul, signed zeros included -- so the VALU only runs the adds,
+// in the reference's order. Scores: for each channel, the outer product of
+// 64 positions' k (one per lane) and the 16 pairs' q; lane l then holds pair
+// l % 16 at positions t0 + 16 b + 4 (l / 16) + r (vgpr 4 b + r). Value sums:
+// for each position, the outer product of the 16 pairs' probabilities and 64
+// channels' v; lane l of value wave w holds channel 64 w + 16 b + l % 16 for
+// pair 4 (l / 16) + r. Probabilities are [pair][position] in LDS; V rows
+// pass through a two-slot LDS ring filled by waves 2-3 while waves 0-1 add.
 constexpr int kRowBlock = 8;
 constexpr int kRowPairs = 2 * kRowBlock;
-// p_s row stride (floats): 8-byte rows; 18 puts the 16 lanes that walk one
-// pair's column on distinct banks.
-constexpr int kPRow = kRowPairs + 2;
-constexpr int kVRows = 16;   // V rows per LDS chunk (256 B each): one 16-byte load per thread
-constexpr int kVBufs = 2;    // chunks in LDS: the one being added and the next
+constexpr int kQRow = 132;   // q_s row stride (floats): 16 pair rows on distinct bank groups
+constexpr int kVRing = 32;   // V rows per ring slot (8 KB)
+
+// Probability row stride (floats) for nmax positions: whole 64-position
+// score passes, plus four so that the 16 pair rows start on distinct banks.
+__host__ __device__ inline int rows_p_stride(int nmax) { return ((nmax + 63) & ~63) + 4; }
 
 // Dynamic LDS of attn_rows_kernel: at 750 positions two workgroups fit a CU.
 __host__ __device__ inline size_t rows_lds_bytes(int nmax) {
-  return (((size_t)kPRow * nmax * 4 + 15) & ~(size_t)15) + (size_t)kVBufs * kVRows * 256;
+  return (size_t)kRowPairs * rows_p_stride(nmax) * 4 + (size_t)2 * kVRing * 256;
 }
 
 __device__ __forceinline__ float max16_nan(float m) {  // over each row of 16 lanes
@@ -741,9 +753,17 @@ __device__ __forceinline__ float max16_nan(float m) {  // over each row of 16 la
   return nan_max_p(m, u2f(dpp_u32<kDppMirror>(f2u(m))));
 }
 
-__global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Every element of the 4-block 16 x 16 outer product: round(a * b) exactly.
+__device__ __forceinline__ f32x16 outer16(float a, float b) {
+  const f32x16 zero = {};
+  return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, zero, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_rows_kernel(PrefillAttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float rows_s[];
-  __shared__ __attribute__((aligned(16))) float q_s[kRowPairs * 128];  // q rows, then output rows
+  __shared__ __attribute__((aligned(16))) float q_s[kRowPairs * kQRow];  // q rows, then output rows
   __shared__ double lane_s[kRowPairs * 8];
   __shared__ float inv_s[kRowPairs];
   // The last row blocks see the most positions: they are dispatched first.
@@ -752,64 +772,87 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
   const int rows = min(kRowBlock, a.frames - r0);
   const int n0 = a.position + r0 + 1;  // positions the block's first row sees; row rr sees n0 + rr
   const int nmax = n0 + rows - 1;
-  float* p_s = rows_s;  // [nmax][kPRow]
-  char* vbuf = reinterpret_cast<char*>(rows_s) + (((size_t)kPRow * nmax * 4 + 15) & ~(size_t)15);
+  const int PS = rows_p_stride(nmax);
+  float* p_s = rows_s;  // [pair][PS]
+  char* ring = reinterpret_cast<char*>(rows_s + (size_t)kRowPairs * PS);
   const _Float16* kc = a.kcache + (size_t)kh * a.capacity * hs;
   const _Float16* vc = a.vcache + (size_t)kh * a.capacity * hs;
   for (int i = tid; i < kRowPairs * hs; i += 256) {
     const int pi = i >> 7, c = i & 127, hh = pi >> 3, rr = pi & 7;
-    q_s[i] = rr < rows ? a.q[((size_t)(r0 + rr) * a.heads + 2 * kh + hh) * hs + c] : 0.0f;
+    q_s[pi * kQRow + c] = rr < rows ? a.q[((size_t)(r0 + rr) * a.heads + 2 * kh + hh) * hs + c] : 0.0f;
   }
   __syncthreads();
 
-  // 1. Scores: one position per lane, its K row held in registers while the
-  // pairs are scored, eight pairs at a time.
-  for (int t = tid; t < nmax; t += 256) {
-    const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)t * hs);
+  // 1. Scores, 64 positions per wave pass: lane l loads position t0 + l's K
+  // row; per channel one outer product with the pairs' q (pair l % 16's q
+  // from LDS), its 16 products added to the channel's accumulator (c % 8) of
+  // each (pair, position) the lane holds.
+  const int mp = lane & 15, mg = lane >> 4;
+  for (int t0 = 64 * wave; t0 < nmax; t0 += 256) {
+    const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)min(t0 + lane, nmax - 1) * hs);
     uint4 kk[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) kk[i] = row[i];
-#pragma unroll 1
-    for (int part = 0; part < 4; ++part) {  // four pairs at a time
-      float acc[4][8];
+    const float* qrow = q_s + mp * kQRow;
+    // Two passes over the row, each with four of the eight accumulators:
+    // channels 8i + {0, 1, 4, 5}, then 8i + {2, 3, 6, 7}; the tree
+    // ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)) is formed half by half.
+    f32x16 half[2];
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
+    for (int g = 0; g < 2; ++g) {
+      f32x16 acc[4];  // channels j = 2g, 2g + 1, 2g + 4, 2g + 5
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[p][j] = 0.0f;
+      for (int u = 0; u < 4; ++u) acc[u] = f32x16{};
+      // Operands of step s = 4 i + u: piece i's channel 8i + {2g, 2g+1, 2g+4, 2g+5}[u].
+      auto qload = [&](int i, float* qv) {
+        const float2 qa = *reinterpret_cast<const float2*>(qrow + 8 * i + 2 * g);
+        const float2 qb = *reinterpret_cast<const float2*>(qrow + 8 * i + 4 + 2 * g);
+        qv[0] = qa.x;
+        qv[1] = qa.y;
+        qv[2] = qb.x;
+        qv[3] = qb.y;
+      };
+      auto kval = [&](int i, int u) {
+        const uint32_t w = (u < 2) ? (g ? kk[i].y : kk[i].x) : (g ? kk[i].w : kk[i].z);
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)((u & 1) ? w >> 16 : w & 0xffffu));
+      };
+      // Software pipeline: the next step's outer product is issued before
+      // this step's adds, the next piece's q is read a piece ahead.
+      float qc[4], qn[4];
+      qload(0, qc);
+      f32x16 dc = outer16(kval(0, 0), qc[0]);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const uint32_t w[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
-        _Float16 k8[8];
+        if (i + 1 < 16) qload(i + 1, qn);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          k8[2 * m] = __builtin_bit_cast(_Float16, (uint16_t)(w[m] & 0xffffu));
-          k8[2 * m + 1] = __builtin_bit_cast(_Float16, (uint16_t)(w[m] >> 16));
+        for (int u = 0; u < 4; ++u) {
+          f32x16 dn;
+          if (u < 3) dn = outer16(kval(i, u + 1), qc[u + 1]);
+          else if (i + 1 < 16) dn = outer16(kval(i + 1, 0), qn[0]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[u][v] = fadd(acc[u][v], dc[v]);
+          __builtin_amdgcn_sched_barrier(0);
+          dc = dn;
         }
+        if (i + 1 < 16) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const float* q = q_s + (4 * part + p) * hs + 8 * i;
-          const float4 q0 = *reinterpret_cast<const float4*>(q);
-          const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
-          acc[p][0] = fadd(acc[p][0], mulh(q0.x, k8[0]));
-          acc[p][1] = fadd(acc[p][1], mulh(q0.y, k8[1]));
-          acc[p][2] = fadd(acc[p][2], mulh(q0.z, k8[2]));
-          acc[p][3] = fadd(acc[p][3], mulh(q0.w, k8[3]));
-          acc[p][4] = fadd(acc[p][4], mulh(q1.x, k8[4]));
-          acc[p][5] = fadd(acc[p][5], mulh(q1.y, k8[5]));
-          acc[p][6] = fadd(acc[p][6], mulh(q1.z, k8[6]));
-          acc[p][7] = fadd(acc[p][7], mulh(q1.w, k8[7]));
+          for (int u = 0; u < 4; ++u) qc[u] = qn[u];
         }
       }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) half[g][v] = fadd(fadd(acc[0][v], acc[2][v]), fadd(acc[1][v], acc[3][v]));
+    }
+    float* prow = p_s + (size_t)mp * PS + t0 + 4 * mg;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
       float sc[4];
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const float v = fadd(fadd(fadd(acc[p][0], acc[p][4]), fadd(acc[p][1], acc[p][5])),
-                             fadd(fadd(acc[p][2], acc[p][6]), fadd(acc[p][3], acc[p][7])));
-        sc[p] = fdiv(v, a.divisor);
+      for (int r = 0; r < 4; ++r) {
+        const int v = 4 * b + r;
+        sc[r] = fdiv(fadd(half[0][v], half[1][v]), a.divisor);
       }
-      float2* out2 = reinterpret_cast<float2*>(p_s + (size_t)t * kPRow + 4 * part);
-      out2[0] = make_float2(sc[0], sc[1]);
-      out2[1] = make_float2(sc[2], sc[3]);
+      *reinterpret_cast<float4*>(prow + 16 * b) = make_float4(sc[0], sc[1], sc[2], sc[3]);
     }
   }
   __syncthreads();
@@ -817,11 +860,12 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
   // 2. Softmax: 16 lanes per pair, four pairs per wave.
   const int pi = wave * 4 + (lane >> 4), sub = lane & 15;
   const int n = (pi & 7) < rows ? n0 + (pi & 7) : 0;
+  float* pp = p_s + (size_t)pi * PS;
   {
     float m = -__builtin_inff();
-    for (int t = sub; t < n; t += 16) m = nan_max_p(m, p_s[t * kPRow + pi]);
+    for (int t = sub; t < n; t += 16) m = nan_max_p(m, pp[t]);
     m = max16_nan(m);
-    for (int t = sub; t < n; t += 16) p_s[t * kPRow + pi] = exp_ref(fadd(p_s[t * kPRow + pi], -m));
+    for (int t = sub; t < n; t += 16) pp[t] = exp_ref(fadd(pp[t], -m));
   }
   __syncthreads();
   const int full = n & ~7;
@@ -832,91 +876,100 @@ __global__ __launch_bounds__(256) void attn_rows_kernel(PrefillAttnArgs a) {
     for (; t + 56 < full; t += 64) {
       float v[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = p_s[(t + 8 * k) * kPRow + pi];
+      for (int k = 0; k < 8; ++k) v[k] = pp[t + 8 * k];
 #pragma unroll
       for (int k = 0; k < 8; ++k) l = l + (double)v[k];
     }
-    for (; t < full; t += 8) l = l + (double)p_s[t * kPRow + pi];
+    for (; t < full; t += 8) l = l + (double)pp[t];
     lane_s[pi * 8 + sub] = l;
   }
   __syncthreads();
   if (sub == 0 && n > 0) {
     const double* L = lane_s + pi * 8;
     double sum = ((L[0] + L[4]) + (L[1] + L[5])) + ((L[2] + L[6]) + (L[3] + L[7]));
-    for (int t = full; t < n; ++t) sum = sum + (double)p_s[t * kPRow + pi];
+    for (int t = full; t < n; ++t) sum = sum + (double)pp[t];
     inv_s[pi] = (float)(1.0 / sum);
   }
   __syncthreads();
   {
     const float inverse = n > 0 ? inv_s[pi] : 0.0f;
-    for (int t = sub; t < n; t += 16) p_s[t * kPRow + pi] = fmul(p_s[t * kPRow + pi], inverse);
+    for (int t = sub; t < n; t += 16) pp[t] = fmul(pp[t], inverse);
   }
 
-  // 3. Time-ordered value sums: lane = (head, channel), one sum per row of
-  // the block. V rows pass through LDS in chunks of kVRows (one 16-byte load
-  // per thread per chunk): the next chunk's loads are in flight in registers
-  // while the current chunk is added, then go to the other LDS buffer.
-  const int hh = tid >> 7, c = tid & 127;
-  float acc[kRowBlock];
+  // 3. Time-ordered value sums, all four waves: wave w owns channels
+  // 32 w .. 32 w + 31 as two groups of 16. One outer product covers four
+  // positions t .. t + 3 (one per 16 x 16 block: the 16 pairs' probabilities
+  // at t + b times 16 channels' v at t + b), so lane l holds, for channel
+  // 32 w + 16 h + l % 16 and pairs 4 (l / 16) + r, the products of four
+  // consecutive positions and adds them in order. V rows pass through a
+  // two-slot LDS ring (direct global->LDS loads of 16-byte pieces, the next
+  // chunk's issued before this one is added; a slot is refilled only after
+  // the barrier that follows its last use).
+  const int chunks = (nmax + kVRing - 1) / kVRing;
+  auto fill = [&](int j) {  // rows past the last are read again, unused
 #pragma unroll
-  for (int rr = 0; rr < kRowBlock; ++rr) acc[rr] = 0.0f;
-  const int chunks = (nmax + kVRows - 1) / kVRows;
-  typedef int v4i_t __attribute__((ext_vector_type(4)));
-  v4i_t vpend;
-  auto fetch_v = [&](int j) {  // rows past the last are read again, unused
-    const int row = min(j * kVRows + (tid >> 4), nmax - 1);
-    vpend = *reinterpret_cast<const v4i_t*>(reinterpret_cast<const char*>(vc) + (size_t)row * 256 + 16 * (tid & 15));
+    for (int m = 0; m < 2; ++m) {
+      const int piece = tid + 256 * m, rr = piece >> 4;
+      const int row = min(j * kVRing + rr, nmax - 1);
+      const char* src = reinterpret_cast<const char*>(vc) + (size_t)row * 256 + 16 * (piece & 15);
+      __builtin_amdgcn_global_load_lds(src, (lds_ptr)(ring + (size_t)(j & 1) * kVRing * 256 + 1024 * (4 * m + wave)), 16, 0, 0);
+    }
   };
-  auto put_v = [&](int j) { *reinterpret_cast<v4i_t*>(vbuf + (size_t)(j % kVBufs) * kVRows * 256 + 16 * tid) = vpend; };
-  fetch_v(0);
-  put_v(0);
-  fetch_v(min(1, chunks - 1));
-  lds_barrier();
+  fill(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // the normalised probabilities and the first V chunk
+  float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  const float* pa = p_s + (size_t)mp * PS + mg;  // A operand: pair mp at position t + l / 16
   for (int j = 0; j < chunks; ++j) {
-    const _Float16* vr = reinterpret_cast<const _Float16*>(vbuf + (size_t)(j % kVBufs) * kVRows * 256) + c;
-    const int t0 = j * kVRows, len = min(kVRows, nmax - t0);
-    const int all = max(0, min(len, n0 - t0));  // positions every row of the block sees
-    int tt = 0;
-    for (; tt < all; ++tt) {
-      const _Float16 v = vr[tt * hs];
-      const float2* pp = reinterpret_cast<const float2*>(p_s + (size_t)(t0 + tt) * kPRow + 8 * hh);
-      const float2 pa = pp[0], pb = pp[1], pc = pp[2], pd = pp[3];
-      acc[0] = fadd(acc[0], mulh(pa.x, v));
-      acc[1] = fadd(acc[1], mulh(pa.y, v));
-      acc[2] = fadd(acc[2], mulh(pb.x, v));
-      acc[3] = fadd(acc[3], mulh(pb.y, v));
-      acc[4] = fadd(acc[4], mulh(pc.x, v));
-      acc[5] = fadd(acc[5], mulh(pc.y, v));
-      acc[6] = fadd(acc[6], mulh(pd.x, v));
-      acc[7] = fadd(acc[7], mulh(pd.y, v));
-    }
-    for (; tt < len; ++tt) {
-      const int t = t0 + tt;
-      const _Float16 v = vr[tt * hs];
-      const float* pp = p_s + (size_t)t * kPRow + 8 * hh;
+    if (j + 1 < chunks) fill(j + 1);
+    const _Float16* vr = reinterpret_cast<const _Float16*>(ring + (size_t)(j & 1) * kVRing * 256) + mg * hs + 32 * wave + mp;
+    const int t0 = j * kVRing, len = min(kVRing, nmax - t0);
+    for (int s = 0; s < len; s += 4) {
+      const int t = t0 + s;
+      const float av = pa[t];
+      const f32x16 d0 = outer16(av, (float)vr[s * hs]);
+      const f32x16 d1 = outer16(av, (float)vr[s * hs + 16]);
+      if (t + 3 < n0) {  // every row of the block sees all four positions
 #pragma unroll
-      for (int rr = 0; rr < kRowBlock; ++rr)
-        if (t < n0 + rr) acc[rr] = fadd(acc[rr], mulh(pp[rr], v));
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc[0][r] = fadd(acc[0][r], d0[4 * b + r]);
+            acc[1][r] = fadd(acc[1][r], d1[4 * b + r]);
+          }
+      } else {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int rr = (4 * mg + r) & 7;  // the pair's row: it sees positions < n0 + rr
+            if (t + b < n0 + rr) {
+              acc[0][r] = fadd(acc[0][r], d0[4 * b + r]);
+              acc[1][r] = fadd(acc[1][r], d1[4 * b + r]);
+            }
+          }
+      }
     }
-    // Chunk j + 1 into the other buffer (last read at chunk j - 1, before the
-    // previous barrier), then chunk j + 2's loads into the registers.
-    put_v(j + 1);
-    fetch_v(min(j + 2, chunks - 1));
-    lds_barrier();
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
   }
 
-  // 4. Output rows (float and/or Q8_0 blocks).
+  // 4. Output rows (float and/or Q8_0 blocks): pair 4 mg + r, channel
+  // 32 w + 16 h + mp.
 #pragma unroll
-  for (int rr = 0; rr < kRowBlock; ++rr) {
-    q_s[(hh * kRowBlock + rr) * hs + c] = acc[rr];
-    if (a.out && rr < rows) a.out[((size_t)(r0 + rr) * a.heads + 2 * kh + hh) * hs + c] = acc[rr];
-  }
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int pq = 4 * mg + r, c = 32 * wave + 16 * h + mp, rr = pq & 7;
+      q_s[pq * kQRow + c] = acc[h][r];
+      if (a.out && rr < rows) a.out[((size_t)(r0 + rr) * a.heads + 2 * kh + (pq >> 3)) * hs + c] = acc[h][r];
+    }
   if (a.xq) {
     __syncthreads();
 #pragma unroll
     for (int g0 = 0; g0 < kRowPairs * hs / 4; g0 += 256) {
       const int g = g0 + tid, pq = g >> 5, c4 = (g & 31) * 4, rr = pq & 7;
-      const float4 v4 = *reinterpret_cast<const float4*>(q_s + pq * hs + c4);
+      const float4 v4 = *reinterpret_cast<const float4*>(q_s + pq * kQRow + c4);
       float d;
       const int packed = quantize4(v4.x, v4.y, v4.z, v4.w, &d);
       if (rr < rows) {
