@@ -324,7 +324,7 @@ struct fah_decoder {
   int q_width = 0, kv_width = 0;
   std::shared_ptr<DecoderWeights> wt;
   DeviceBuffer rope_cos, rope_sin, kcache, vcache;
-  DeviceBuffer x, qkv_out, qh, scores, attn, a, h, logits, keys, token, position, history, history_count, staging;
+  DeviceBuffer x, qkv_out, qh, scores, block_max, exp_t, attn, a, h, logits, keys, token, position, history, history_count, staging;
   DeviceBuffer row_q, row_s;  // one quantised row (multi-kernel path over persistent-layout weights)
   int lm_groups = 0;
   int host_position = 0;
@@ -511,6 +511,9 @@ void enqueue_layers(fah_decoder* d, hipStream_t s) {
     at.vcache = qa.vcache;
     at.position = pos;
     at.scores = d->scores.as<float>();
+    at.block_max = d->block_max.as<float>();
+    at.exp_t = d->exp_t.as<double>();
+    at.exp_stride = fah::attention_exp_stride(c.capacity);
     at.out = d->attn.as<float>();
     at.heads = c.heads;
     at.kv_heads = c.kv_heads;
@@ -621,7 +624,11 @@ void init_state(fah_decoder* d, hipStream_t s) {
   d->x.allocate((size_t)k.width * 4);
   d->qkv_out.allocate((size_t)qkv_rows * 4);
   d->qh.allocate((size_t)q_width * 4);
-  d->scores.allocate((size_t)k.heads * k.capacity * 4);
+  // Scores, then probabilities, [heads][capacity]; the values kernel copies
+  // each head's row in 16-byte pieces, up to 3 floats past the capacity.
+  d->scores.allocate(((size_t)k.heads * k.capacity + 4) * 4);
+  d->block_max.allocate((size_t)k.heads * ((k.capacity + 255) / 256) * 4);
+  d->exp_t.allocate((size_t)k.heads * 8 * fah::attention_exp_stride(k.capacity) * 8);
   d->attn.allocate((size_t)q_width * 4);
   d->a.allocate((size_t)k.width * 4);
   d->h.allocate((size_t)k.ffn * 4);

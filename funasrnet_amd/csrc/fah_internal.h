@@ -66,7 +66,10 @@ struct AttnArgs {
   const _Float16* kcache;  // [kv_heads][capacity][head_size]
   const _Float16* vcache;
   const int* position;
-  float* scores;           // [heads][capacity]
+  float* scores;           // [heads][capacity]: scores, then exponentials in place
+  float* block_max;        // [heads][capacity / 256 rounded up]: each score block's maximum
+  double* exp_t;           // [heads][8][exp_stride]: numerators as doubles, position 8 i + j at [j][i]
+  int exp_stride;          // capacity / 8 rounded up to a multiple of 2
   float* out;              // [heads][head_size]
   int heads, kv_heads, head_size, capacity;
   float divisor;           // sqrtf(head_size)
@@ -263,6 +266,8 @@ hipError_t launch_embed(const int8_t* q, const void* scales, bool half_scales, i
                         float* x, int* history, int* history_count, hipStream_t s);
 hipError_t launch_qk_prepare(const QkArgs& a, hipStream_t s);
 int attention_slices(int capacity, int head_size);
+// Row stride (doubles) of AttnArgs::exp_t for a cache of `capacity` positions.
+inline int attention_exp_stride(int capacity) { return ((capacity + 7) / 8 + 1) & ~1; }
 hipError_t prepare_attention(int capacity, int head_size);
 hipError_t launch_attention(const AttnArgs& a, int score_groups, hipStream_t s);
 hipError_t launch_advance(int* position, int frames, hipStream_t s);

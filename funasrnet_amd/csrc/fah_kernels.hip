@@ -16,7 +16,6 @@
 namespace fah {
 
 constexpr int kThreads = 256;
-constexpr int kRing = 256, kRingRow = kRing + 4;  // value-chain product ring: positions per slot, padded row
 using lds_ptr = __attribute__((address_space(3))) void*;
 constexpr int kMaxK = 4096;
 
@@ -296,36 +295,6 @@ __global__ __launch_bounds__(128) void qk_prepare_kernel(QkArgs a) {
   }
 }
 
-// Attention scores of one query head over positions [0, pos]: eight lane
-// accumulators (channel c -> lane c % 8) of product-then-add, folded as
-// ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)), divided by sqrtf(head_size)
-// (TensorMath.AttentionAvx.cs:74-160, AudioKernels.cs:94-147).
-// Grid (heads, G): each workgroup walks chunks of 32 positions.
-__global__ __launch_bounds__(kThreads) void attn_scores_kernel(AttnArgs a) {
-  const int head = blockIdx.x, kh = head / (a.heads / a.kv_heads);
-  const int hs = a.head_size;
-  const int n = *a.position + 1;
-  const int j = threadIdx.x & 7, local = threadIdx.x >> 3;
-  const float* q = a.q + head * hs;
-  float qv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) qv[i] = q[8 * i + j];
-  const _Float16* kbase = a.kcache + (size_t)kh * a.capacity * hs;
-  for (int t0 = blockIdx.y * 32; t0 < n; t0 += gridDim.y * 32) {
-    int t = t0 + local;
-    float acc = 0.0f;
-    if (t < n) {
-      const _Float16* k = kbase + (size_t)t * hs;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc = fadd(acc, fmul(qv[i], from_half(k[8 * i + j])));
-    }
-    float s = fadd(acc, __shfl_xor(acc, 4, 8));
-    s = fadd(s, __shfl_xor(s, 1, 8));
-    s = fadd(s, __shfl_xor(s, 2, 8));
-    if (t < n && j == 0) a.scores[(size_t)head * a.capacity + t] = fdiv(s, a.divisor);
-  }
-}
-
 // NaN-propagating maximum (Math.Max semantics for the softmax shift).
 __device__ __forceinline__ float nan_max(float a, float b) {
   if (a != a) return a;
@@ -333,149 +302,250 @@ __device__ __forceinline__ float nan_max(float a, float b) {
   return b > a ? b : a;
 }
 
-// Softmax (TensorMath.SoftmaxAvx.cs:11-58) of both query heads of one KV
-// head, then the value sums out[c] = sum over t of v[t][c] * p[t] in time
-// order from 0f (TensorMath.AttentionAvx.cs:173-224). Workgroup
-// (kv head, channel slice of 128/S): the V slice of every position is staged
-// in LDS with all loads issued first, so HBM latency is paid once and
-// overlaps the softmax; one thread then owns one (head, channel) chain.
-// Dynamic LDS: n * 2C bytes of V (fp16) + 2 * n floats of probabilities.
-__global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int slices) {
-  extern __shared__ float dyn_s[];
-  __shared__ float max_s[kThreads / kWave];
-  __shared__ double lane_s[2][8];
-  __shared__ float inv_s[2];
-  const int kh = blockIdx.x / slices, part = blockIdx.x % slices;
-  const int hs = a.head_size, C = hs / slices, c0 = part * C;
+// Attention scores of one query head over positions [0, pos]: eight
+// accumulators (channel c -> accumulator c % 8) of product-then-add, folded
+// as ((a0+a4)+(a1+a5)) + ((a2+a6)+(a3+a7)), divided by sqrtf(head_size)
+// (TensorMath.AttentionAvx.cs:74-160, AudioKernels.cs:94-147). Grid (heads,
+// position blocks of kThreads): one lane per position, its K row loaded
+// whole (16 x 16 bytes in flight), q read from LDS. The products are one
+// mixed-precision fma with a +0 addend: round(q * k) except that a -0
+// product becomes +0, and no accumulator is ever -0 (they start at +0), so
+// every sum is the reference's.
+__global__ __launch_bounds__(kThreads) void attn_scores_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float q_s[128];
+  __shared__ float bm_s[kThreads / kWave];
+  const int head = blockIdx.x, kh = head / (a.heads / a.kv_heads);
+  const int hs = a.head_size, tid = threadIdx.x;
   const int n = *a.position + 1;
-  const int tid = threadIdx.x;
+  if ((int)blockIdx.y * kThreads >= n) return;  // a block past the current position
+  const int t = blockIdx.y * kThreads + tid;
+  if (tid < hs) q_s[tid] = a.q[head * hs + tid];
+  uint4 kk[16];
+  const uint4* row = reinterpret_cast<const uint4*>(a.kcache + ((size_t)kh * a.capacity + min(t, n - 1)) * hs);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) kk[i] = row[i];
+  __syncthreads();
+  // Lanes past the current position compute the last position's score
+  // again: it joins the block maximum only, the score store is skipped.
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float4 q0 = *reinterpret_cast<const float4*>(q_s + 8 * i);
+    const float4 q1 = *reinterpret_cast<const float4*>(q_s + 8 * i + 4);
+    const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const uint32_t w[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const _Float16 k = __builtin_bit_cast(_Float16, (uint16_t)((j & 1) ? w[j >> 1] >> 16 : w[j >> 1] & 0xffffu));
+      acc[j] = fadd(acc[j], mulh(qv[j], k));
+    }
+  }
+  const float s = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
+  const float sd = fdiv(s, a.divisor);
+  if (t < n) a.scores[(size_t)head * a.capacity + t] = sd;
+  // The block's maximum (NaN-propagating, order-free) for the softmax shift.
+  float m = sd;
+  for (int o = 32; o >= 1; o >>= 1) m = nan_max(m, __shfl_xor(m, o, kWave));
+  if ((tid & (kWave - 1)) == 0) bm_s[tid / kWave] = m;
+  __syncthreads();
+  if (tid == 0) {
+    const int waves = (min(n - (int)blockIdx.y * kThreads, kThreads) + kWave - 1) / kWave;
+    float b = bm_s[0];
+    for (int w = 1; w < waves; ++w) b = nan_max(b, bm_s[w]);
+    a.block_max[(size_t)head * gridDim.y + blockIdx.y] = b;
+  }
+}
+
+// Softmax numerators (TensorMath.SoftmaxAvx.cs:11-58) in place: e[t] =
+// exp(s[t] - max) (ExpAvx), the maximum over the score blocks' maxima
+// (NaN-propagating). Grid (heads, position blocks of kThreads). Each value
+// is also stored as a double by residue t % 8 (exp_t), the layout of the
+// denominator's lane sums; the denominator and the normalisation run in
+// attn_values_kernel.
+__global__ __launch_bounds__(kThreads) void attn_exp_kernel(AttnArgs a) {
+  const int head = blockIdx.x, tid = threadIdx.x;
+  const int n = *a.position + 1, blocks = (n + kThreads - 1) / kThreads;
+  const int t = blockIdx.y * kThreads + tid;
+  if ((int)blockIdx.y >= blocks) return;
+  const float* bm = a.block_max + (size_t)head * gridDim.y;
+  float mx = bm[0];
+  for (int b = 1; b < blocks; ++b) mx = nan_max(mx, bm[b]);
+  if (t < n) {
+    float* sc = a.scores + (size_t)head * a.capacity + t;
+    const float e = exp_ref(fadd(*sc, -mx));
+    *sc = e;
+    // By residue for the denominator's eight in-order lane sums.
+    a.exp_t[((size_t)head * 8 + (t & 7)) * a.exp_stride + (t >> 3)] = (double)e;
+  }
+}
+
+// One wave: (float)(1 / sum) of the softmax denominator in double
+// (SoftmaxAvx.cs:11-58): lane j < 8 adds e[j], e[j+8], ... (t < full) in
+// order from row j of et (the values as doubles by residue, row stride
+// `stride` doubles, two a 16-byte read, 16 reads a batch), then the eight
+// sums' pairwise tree, then the tail [full, n) of e (position order) in
+// order. Valid in lane 0.
+__device__ __forceinline__ float softmax_inverse(const double* et, int stride, const float* e, int n) {
+  const int lane = threadIdx.x & (kWave - 1), full = n & ~7, m = full >> 3;  // values a lane adds
+  double l = 0.0;
+  if (lane < 8) {
+    const double* row = et + (size_t)lane * stride;
+    int i = 0;
+    for (; i + 32 <= m; i += 32) {
+      double2 v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = *reinterpret_cast<const double2*>(row + i + 2 * k);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        l = l + v[k].x;
+        l = l + v[k].y;
+      }
+    }
+    for (; i < m; ++i) l = l + row[i];
+  }
+  double L[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) L[j] = readlane_double(l, j);
+  double sum = ((L[0] + L[4]) + (L[1] + L[5])) + ((L[2] + L[6]) + (L[3] + L[7]));
+  for (int t = full; t < n; ++t) sum = sum + (double)e[t];
+  return (float)(1.0 / sum);
+}
+
+// Value sums out[c] = sum over t of v[t][c] * p[t] in time order from 0f
+// (TensorMath.AttentionAvx.cs:173-224) for both query heads of one KV head
+// and a slice of kValC channels: 2 kValC chains, run by lanes of wave 0 (one
+// add per position); waves 1-7 copy V rows of the slice into a three-slot
+// LDS ring two blocks ahead (direct global->LDS loads) and form the
+// products v * p of the next block into a two-slot product ring, so each
+// chain step is one add (the product's rounding is the same wherever it is
+// made). Before the first block, waves 0 and 1 form the two heads'
+// softmax denominators from the numerators by residue (staged in the
+// product ring's space when they fit). Dynamic LDS: see values_lds.
+constexpr int kValThreads = 512;
+constexpr int kValC = 16;                      // channels per workgroup
+constexpr int kValChains = 2 * kValC;          // both query heads
+constexpr int kValBlk = 256;                   // positions per ring block
+constexpr int kValRow = kValBlk + 12;          // product ring row (floats; also the residue rows' room)
+constexpr int kValVSlot = kValBlk * kValC * 2; // V ring slot (bytes)
+constexpr int kValPSlot = kValChains * kValRow * 4;  // product ring slot (bytes)
+
+__global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float dyn_s[];
+  __shared__ float inv_s[2];
+  constexpr int kWaves = kValThreads / kWave;
+  const int slices = a.head_size / kValC;
+  const int kh = blockIdx.x / slices, c0 = (blockIdx.x % slices) * kValC;
+  const int hs = a.head_size, n = *a.position + 1, tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   const int group = a.heads / a.kv_heads;
-  float* p_s = dyn_s;                                                     // [2][n]
-  _Float16* v_s = reinterpret_cast<_Float16*>(dyn_s + ((2 * n + 3) & ~3));  // [n][C], 16-byte aligned
-
-  // 1. V slice into LDS: C/8 16-byte pieces per position, piece j of the
-  // slice at v_s + 16 j. Batches of 16 pieces per thread: the loads are
-  // unconditional (index clamped) and every store too (pieces past the end
-  // go to a spare slot), so a batch's loads are all in flight at once.
-  const int pieces = C / 8, total = n * pieces;
+  const int np = (n + 3) & ~3;
+  float* p_s = dyn_s;                                               // [2][np]
+  char* vring = reinterpret_cast<char*>(dyn_s + 2 * np);            // [3][kValBlk][kValC] fp16
+  float* pring = reinterpret_cast<float*>(vring + 3 * kValVSlot);   // [2][kValChains][kValRow]
+  const int blocks = (n + kValBlk - 1) / kValBlk;
   const _Float16* vbase = a.vcache + (size_t)kh * a.capacity * hs + c0;
-  for (int base = 0; base < total; base += kThreads * 8) {
-    int4 r0, r1, r2, r3, r4, r5, r6, r7;
-    auto piece = [&](int i) {
-      const int j = min(base + i * kThreads + tid, total - 1);
-      const int t = j / pieces, q = j - t * pieces;
-      return *reinterpret_cast<const int4*>(vbase + (size_t)t * hs + q * 8);
-    };
-    auto slot = [&](int i) {
-      return reinterpret_cast<int4*>(v_s + (size_t)min(base + i * kThreads + tid, total) * 8);  // total: spare
-    };
-    r0 = piece(0); r1 = piece(1); r2 = piece(2); r3 = piece(3);
-    r4 = piece(4); r5 = piece(5); r6 = piece(6); r7 = piece(7);
-    *slot(0) = r0; *slot(1) = r1; *slot(2) = r2; *slot(3) = r3;
-    *slot(4) = r4; *slot(5) = r5; *slot(6) = r6; *slot(7) = r7;
-  }
-
-  // 2. Softmax of the two query heads: threads [0,128) head 0, [128,256) head 1.
-  const int hh = tid >> 7, lt = tid & 127;
-  const int head = kh * group + hh;
-  const float* scores = a.scores + (size_t)head * a.capacity;
-  float m = -__builtin_inff();
-  int t0 = lt;
-  // Eight score loads in flight per lane.
-  for (; t0 + 7 * 128 < n; t0 += 8 * 128) {
-    float v[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = scores[t0 + 128 * k];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      p_s[hh * n + t0 + 128 * k] = v[k];
-      m = nan_max(m, v[k]);
+  // V block j into ring slot j % 3: 2 pieces of 16 bytes a position, piece
+  // q of the block at byte 16 q; `first`/`step` spread the pieces over the
+  // calling waves (positions past n repeat the last one, never used).
+  auto fill = [&](int j, int first, int step) {
+    char* dst = vring + (size_t)(j % 3) * kValVSlot;
+    for (int q0 = first * 64; q0 < 2 * kValBlk; q0 += step * 64) {
+      const int q = q0 + lane, t = min(j * kValBlk + (q >> 1), n - 1);
+      __builtin_amdgcn_global_load_lds(vbase + (size_t)t * hs + 8 * (q & 1), (lds_ptr)(dst + 16 * q0), 16, 0, 0);
     }
-  }
-  for (; t0 < n; t0 += 128) {
-    float v = scores[t0];
-    p_s[hh * n + t0] = v;
-    m = nan_max(m, v);
-  }
-  for (int s = 32; s >= 1; s >>= 1) m = nan_max(m, __shfl_xor(m, s, kWave));
-  if ((tid & (kWave - 1)) == 0) max_s[tid / kWave] = m;
-  __syncthreads();
-  const float mx = nan_max(max_s[hh * 2], max_s[hh * 2 + 1]);
-  for (int t = lt; t < n; t += 128) p_s[hh * n + t] = exp_ref(fadd(p_s[hh * n + t], -mx));
-  __syncthreads();
-  const int full = n & ~7;
-  if (lt < 8) {
-    // Lane j: p[j] + p[j+8] + ... in order, in double; eight loads ahead.
-    const float* ph = p_s + hh * n;
-    double l = 0.0;
-    int t = lt;
-    for (; t + 56 < full; t += 64) {
-      float v[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = ph[t + 8 * k];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) l = l + (double)v[k];
-    }
-    for (; t < full; t += 8) l = l + (double)ph[t];
-    lane_s[hh][lt] = l;
-  }
-  __syncthreads();
-  if (lt == 0) {
-    const double* L = lane_s[hh];
-    double sum = ((L[0] + L[4]) + (L[1] + L[5])) + ((L[2] + L[6]) + (L[3] + L[7]));
-    for (int t = full; t < n; ++t) sum = sum + (double)p_s[hh * n + t];
-    inv_s[hh] = (float)(1.0 / sum);
-  }
-  __syncthreads();
-  const float inverse = inv_s[hh];
-  for (int t = lt; t < n; t += 128) p_s[hh * n + t] = fmul(p_s[hh * n + t], inverse);
-  __syncthreads();
-
-  // 3. Time-ordered value chains, one per (head, channel) of this slice, run
-  // by wave 0. Waves 1-3 form the products v[t][c] * p[t] of the next block
-  // of kRing positions into a two-slot LDS ring meanwhile, so each chain
-  // step is one add (the product's rounding is the same wherever it is made).
-  const int chains = 2 * C, cshift = __builtin_ctz(C);
-  float* ring = reinterpret_cast<float*>(reinterpret_cast<char*>(v_s) + (((size_t)n * C * 2 + 16 + 15) & ~(size_t)15));
-  const int blocks = (n + kRing - 1) / kRing;
-  const int wave = tid / kWave;
+  };
+  // The residue rows of both heads' numerators (m doubles a row, 16-byte
+  // pieces; row r at `rs` doubles, two more than m rounded up to 2 so that
+  // the eight lanes reading a column hit different banks), in the product
+  // ring's space when they fit; else read from global memory.
+  const int m = (n & ~7) >> 3, rs = ((m + 1) & ~1) + 2;
+  const bool staged = (size_t)16 * rs * 8 <= (size_t)2 * kValPSlot;
+  double* et_s = reinterpret_cast<double*>(pring);
+  const double* et_g = a.exp_t + (size_t)kh * group * 8 * a.exp_stride;
+  // Products of block j into product slot j & 1: task = (four positions,
+  // 4-channel quarter), whose 8 product rows of four positions each are
+  // written as float4; rows [0, kValC) head 0, [kValC, 2 kValC) head 1.
+  // Positions past n are formed from the clamped V rows and garbage
+  // probabilities and never added.
+  float inv0 = 0.0f, inv1 = 0.0f;  // softmax inverses of the two heads
   auto produce = [&](int j) {
-    float* slot = ring + (size_t)(j & 1) * chains * kRingRow;
-    const int t0 = j * kRing, len = min(kRing, n - t0);
-    const int gshift = cshift - 3;  // 8-channel groups per position: C / 8
-    // One task = one position's 8-channel group: one 16-byte V read and the
-    // two heads' probabilities give 16 products.
-    for (int task = tid - kWave; task < (len << gshift); task += kThreads - kWave) {
-      const int tt = task >> gshift, g = task & ((1 << gshift) - 1), t = t0 + tt;
-      const uint4 raw = *reinterpret_cast<const uint4*>(v_s + (size_t)t * C + 8 * g);
-      const float p0 = p_s[t], p1 = p_s[n + t];
-      const _Float16* hv = reinterpret_cast<const _Float16*>(&raw);
+    const char* vs = vring + (size_t)(j % 3) * kValVSlot;
+    float* ps = pring + (size_t)(j & 1) * kValChains * kValRow;
+    const int t0 = j * kValBlk, len = min(kValBlk, n - t0);
+    for (int task = tid - kWave; task < 4 * ((len + 3) >> 2); task += kValThreads - kWave) {
+      const int tq = 4 * (task >> 2), q = task & 3, t = t0 + tq;
+      uint2 raw[4];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float v = from_half(hv[k]);
-        slot[(size_t)(8 * g + k) * kRingRow + tt] = fmul(v, p0);
-        slot[(size_t)(C + 8 * g + k) * kRingRow + tt] = fmul(v, p1);
+      for (int u = 0; u < 4; ++u) raw[u] = *reinterpret_cast<const uint2*>(vs + 32 * (tq + u) + 8 * q);
+      // The probabilities p = e * inverse (the softmax's last step).
+      const float4 e0 = *reinterpret_cast<const float4*>(p_s + t);
+      const float4 e1 = *reinterpret_cast<const float4*>(p_s + np + t);
+      const float4 p0 = make_float4(fmul(e0.x, inv0), fmul(e0.y, inv0), fmul(e0.z, inv0), fmul(e0.w, inv0));
+      const float4 p1 = make_float4(fmul(e1.x, inv1), fmul(e1.y, inv1), fmul(e1.z, inv1), fmul(e1.w, inv1));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = from_half(reinterpret_cast<const _Float16*>(&raw[u])[k]);
+        *reinterpret_cast<float4*>(ps + (size_t)(4 * q + k) * kValRow + tq) =
+            make_float4(fmul(v[0], p0.x), fmul(v[1], p0.y), fmul(v[2], p0.z), fmul(v[3], p0.w));
+        *reinterpret_cast<float4*>(ps + (size_t)(kValC + 4 * q + k) * kValRow + tq) =
+            make_float4(fmul(v[0], p1.x), fmul(v[1], p1.y), fmul(v[2], p1.z), fmul(v[3], p1.w));
       }
     }
   };
+  // The numerators of both heads (written by attn_exp_kernel), their
+  // residue rows and the first two V blocks, by all waves.
+  {
+    for (int h = 0; h < 2; ++h) {
+      const char* src = reinterpret_cast<const char*>(a.scores + (size_t)(kh * group + h) * a.capacity);
+      char* dst = reinterpret_cast<char*>(p_s + h * np);
+      const int bytes = np * 4;
+      for (int c = wave * 1024; c < bytes; c += kWaves * 1024)
+        if (c + 16 * lane < bytes) __builtin_amdgcn_global_load_lds(src + c + 16 * lane, (lds_ptr)(dst + c), 16, 0, 0);
+    }
+    if (staged) {
+      const int rb = rs * 8;  // bytes a staged row
+      for (int r = wave; r < 16; r += kWaves) {
+        const char* src = reinterpret_cast<const char*>(et_g + (size_t)r * a.exp_stride);
+        char* dst = reinterpret_cast<char*>(et_s) + (size_t)r * rb;
+        for (int c = 0; c < m * 8; c += 1024)
+          if (c + 16 * lane < m * 8 + 8) __builtin_amdgcn_global_load_lds(src + c + 16 * lane, (lds_ptr)(dst + c), 16, 0, 0);
+      }
+    }
+    fill(0, wave, kWaves);
+    if (blocks > 1) fill(1, wave, kWaves);
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  lds_barrier();
+  // The two heads' denominators, one wave each.
+  if (wave < 2) {
+    const float inv = staged ? softmax_inverse(et_s + (size_t)wave * 8 * rs, rs, p_s + wave * np, n)
+                             : softmax_inverse(et_g + (size_t)wave * 8 * a.exp_stride, a.exp_stride, p_s + wave * np, n);
+    if (lane == 0) inv_s[wave] = inv;
+  }
+  lds_barrier();
+  inv0 = inv_s[0];
+  inv1 = inv_s[1];
   if (wave > 0) produce(0);
   lds_barrier();
   float acc = 0.0f;
   for (int j = 0; j < blocks; ++j) {
     if (wave > 0) {
+      if (j + 2 < blocks) fill(j + 2, wave - 1, kWaves - 1);
       if (j + 1 < blocks) produce(j + 1);
-    } else if (tid < chains) {
-      const float* row = ring + (size_t)(j & 1) * chains * kRingRow + (size_t)tid * kRingRow;
-      const int len = min(kRing, n - j * kRing);
+      __builtin_amdgcn_s_waitcnt(0);
+    } else if (tid < kValChains) {
+      const float* row = pring + (size_t)(j & 1) * kValChains * kValRow + (size_t)tid * kValRow;
+      const int len = min(kValBlk, n - j * kValBlk);
       int tt = 0;
-      if (len == kRing) {
+      if (len == kValBlk) {
         // Full block: the next 16 products are read while these 16 are added.
         float4 q[4], qn[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) q[k] = *reinterpret_cast<const float4*>(row + 4 * k);
 #pragma unroll
-        for (int i = 0; i < kRing / 16; ++i) {
-          if (i + 1 < kRing / 16) {
+        for (int i = 0; i < kValBlk / 16; ++i) {
+          if (i + 1 < kValBlk / 16) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) qn[k] = *reinterpret_cast<const float4*>(row + 16 * (i + 1) + 4 * k);
           }
@@ -489,7 +559,7 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
 #pragma unroll
           for (int k = 0; k < 4; ++k) q[k] = qn[k];
         }
-        tt = kRing;
+        tt = kValBlk;
       }
       for (; tt + 4 <= len; tt += 4) {
         const float4 q = *reinterpret_cast<const float4*>(row + tt);
@@ -502,8 +572,8 @@ __global__ __launch_bounds__(kThreads) void attn_values_kernel(AttnArgs a, int s
     }
     lds_barrier();
   }
-  if (tid < chains) {
-    const int h2 = tid >> cshift, ch = tid & (C - 1);
+  if (tid < kValChains) {
+    const int h2 = tid / kValC, ch = tid % kValC;
     a.out[(size_t)(kh * group + h2) * hs + c0 + ch] = acc;
   }
 }
@@ -684,43 +754,49 @@ hipError_t launch_qk_prepare(const QkArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Dynamic LDS of attn_values_kernel for `capacity` positions and S slices:
-// probabilities 2 x 4 B and V 2C B per position (C = head_size / S), one
-// spare 16-byte V slot, the padding to 16 B after each, and the product ring
-// 2 x 2C x kRingRow floats.
-static size_t values_lds(int capacity, int head_size, int slices) {
-  const int C = head_size / slices;
-  return (size_t)capacity * (2 * C + 8) + 48 + (size_t)2 * 2 * C * kRingRow * 4;
+// Dynamic LDS of attn_values_kernel for `capacity` positions: both heads'
+// probabilities (rounded up to 4 positions), the three-slot V ring and the
+// two-slot product ring.
+static size_t values_lds(int capacity) {
+  return (size_t)2 * ((capacity + 3) & ~3) * 4 + 3 * kValVSlot + 2 * kValPSlot;
 }
 
 int attention_slices(int capacity, int head_size) {
-  for (int slices = 4; slices <= 16; slices *= 2)
-    if (values_lds(capacity, head_size, slices) + 1024 <= 160 * 1024) return slices;
-  return 0;
+  if (head_size % kValC != 0 || values_lds(capacity) > 160 * 1024 - 1024) return 0;
+  return head_size / kValC;
 }
 
 size_t attention_lds_bytes(int capacity, int head_size) {
-  int slices = attention_slices(capacity, head_size);
-  return slices ? values_lds(capacity, head_size, slices) : 0;
+  return attention_slices(capacity, head_size) ? values_lds(capacity) : 0;
 }
 
 hipError_t prepare_attention(int capacity, int head_size) {
   if (!attention_lds_bytes(capacity, head_size)) return hipErrorInvalidValue;
-  // The limit is per kernel, not per decoder: set the largest size any
+  // The limits are per kernel, not per decoder: set the largest size any
   // capacity that attention_slices accepts can ask for, so decoders of
   // different capacities do not lower each other's limit.
   return hipFuncSetAttribute(reinterpret_cast<const void*>(attn_values_kernel),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024 + 16);
+                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
 }
 
-hipError_t launch_attention(const AttnArgs& a, int score_groups, hipStream_t s) {
-  if (a.head_size != 128 || a.heads != 2 * a.kv_heads) return hipErrorInvalidValue;
+// Scores (one lane per position) with each block's maximum, the softmax
+// numerators in place, then the denominators and the value sums. The grids
+// cover the cache's capacity: workgroups past the current position return
+// at once.
+hipError_t launch_attention(const AttnArgs& a, int /*score_groups*/, hipStream_t s) {
+  if (a.head_size != 128 || a.heads != 2 * a.kv_heads || !a.block_max || !a.exp_t ||
+      a.exp_stride < attention_exp_stride(a.capacity))
+    return hipErrorInvalidValue;
   int slices = attention_slices(a.capacity, a.head_size);
   if (!slices) return hipErrorInvalidValue;
-  attn_scores_kernel<<<dim3(a.heads, score_groups), kThreads, 0, s>>>(a);
+  const dim3 grid(a.heads, (a.capacity + kThreads - 1) / kThreads);
+  attn_scores_kernel<<<grid, kThreads, 0, s>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  attn_values_kernel<<<a.kv_heads * slices, kThreads, attention_lds_bytes(a.capacity, a.head_size), s>>>(a, slices);
+  attn_exp_kernel<<<grid, kThreads, 0, s>>>(a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  attn_values_kernel<<<a.kv_heads * slices, kValThreads, attention_lds_bytes(a.capacity, a.head_size), s>>>(a);
   return hipGetLastError();
 }
 
