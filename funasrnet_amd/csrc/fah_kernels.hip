@@ -414,11 +414,11 @@ __device__ __forceinline__ float softmax_inverse(const double* et, int stride, c
 // Value sums out[c] = sum over t of v[t][c] * p[t] in time order from 0f
 // (TensorMath.AttentionAvx.cs:173-224) for both query heads of one KV head
 // and a slice of kValC channels: 2 kValC chains, run by lanes of wave 0 (one
-// add per position); waves 1-7 copy V rows of the slice into a three-slot
-// LDS ring two blocks ahead (direct global->LDS loads) and form the
-// products v * p of the next block into a two-slot product ring, so each
-// chain step is one add (the product's rounding is the same wherever it is
-// made). Before the first block, waves 0 and 1 form the two heads'
+// add per position); wave 4 copies V rows of the slice into a three-slot
+// LDS ring two blocks ahead (direct global->LDS loads) and the other six
+// waves form the products v * p of the next block into a two-slot product
+// ring, so each chain step is one add (the product's rounding is the same
+// wherever it is made). Before the first block, waves 0 and 1 form the two heads'
 // softmax denominators from the numerators by residue (staged in the
 // product ring's space when they fit). Dynamic LDS: see values_lds.
 constexpr int kValThreads = 512;
@@ -461,6 +461,12 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
   const bool staged = (size_t)16 * rs * 8 <= (size_t)2 * kValPSlot;
   double* et_s = reinterpret_cast<double*>(pring);
   const double* et_g = a.exp_t + (size_t)kh * group * 8 * a.exp_stride;
+  // Wave 0 runs the chains; wave 4, which shares its SIMD, only issues the
+  // V loads, so that the chains have the SIMD's issue slots to themselves;
+  // the other six waves form the products.
+  constexpr int kProducers = kWaves - 2;
+  const bool producer = wave != 0 && wave != kWaves / 2;
+  const int prank = wave < kWaves / 2 ? wave - 1 : wave - 2;
   // Products of block j into product slot j & 1: task = (four positions,
   // 4-channel quarter), whose 8 product rows of four positions each are
   // written as float4; rows [0, kValC) head 0, [kValC, 2 kValC) head 1.
@@ -471,7 +477,7 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
     const char* vs = vring + (size_t)(j % 3) * kValVSlot;
     float* ps = pring + (size_t)(j & 1) * kValChains * kValRow;
     const int t0 = j * kValBlk, len = min(kValBlk, n - t0);
-    for (int task = tid - kWave; task < 4 * ((len + 3) >> 2); task += kValThreads - kWave) {
+    for (int task = prank * kWave + lane; task < 4 * ((len + 3) >> 2); task += kProducers * kWave) {
       const int tq = 4 * (task >> 2), q = task & 3, t = t0 + tq;
       uint2 raw[4];
 #pragma unroll
@@ -526,38 +532,39 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
   lds_barrier();
   inv0 = inv_s[0];
   inv1 = inv_s[1];
-  if (wave > 0) produce(0);
+  if (producer) produce(0);
   lds_barrier();
   float acc = 0.0f;
   for (int j = 0; j < blocks; ++j) {
-    if (wave > 0) {
-      if (j + 2 < blocks) fill(j + 2, wave - 1, kWaves - 1);
+    if (producer) {
       if (j + 1 < blocks) produce(j + 1);
+    } else if (wave == kWaves / 2) {
+      if (j + 2 < blocks) fill(j + 2, 0, 1);
       __builtin_amdgcn_s_waitcnt(0);
     } else if (tid < kValChains) {
       const float* row = pring + (size_t)(j & 1) * kValChains * kValRow + (size_t)tid * kValRow;
       const int len = min(kValBlk, n - j * kValBlk);
       int tt = 0;
       if (len == kValBlk) {
-        // Full block: the next 16 products are read while these 16 are added.
-        float4 q[4], qn[4];
+        // Full block: products read three groups of 16 ahead of the adds.
+        float4 q[4][4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) q[k] = *reinterpret_cast<const float4*>(row + 4 * k);
+        for (int g = 0; g < 3; ++g)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) q[g][k] = *reinterpret_cast<const float4*>(row + 16 * g + 4 * k);
 #pragma unroll
         for (int i = 0; i < kValBlk / 16; ++i) {
-          if (i + 1 < kValBlk / 16) {
+          if (i + 3 < kValBlk / 16) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) qn[k] = *reinterpret_cast<const float4*>(row + 16 * (i + 1) + 4 * k);
+            for (int k = 0; k < 4; ++k) q[(i + 3) & 3][k] = *reinterpret_cast<const float4*>(row + 16 * (i + 3) + 4 * k);
           }
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            acc = fadd(acc, q[k].x);
-            acc = fadd(acc, q[k].y);
-            acc = fadd(acc, q[k].z);
-            acc = fadd(acc, q[k].w);
+            acc = fadd(acc, q[i & 3][k].x);
+            acc = fadd(acc, q[i & 3][k].y);
+            acc = fadd(acc, q[i & 3][k].z);
+            acc = fadd(acc, q[i & 3][k].w);
           }
-#pragma unroll
-          for (int k = 0; k < 4; ++k) q[k] = qn[k];
         }
         tt = kValBlk;
       }
