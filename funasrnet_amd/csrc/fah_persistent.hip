@@ -487,7 +487,10 @@ __device__ __forceinline__ void stage_slice(char* dst, const int8_t* w, const _F
     } else {
       src = reinterpret_cast<const char*>(w + (size_t)row(0) * K);
     }
-    __builtin_amdgcn_global_load_lds(src, (lds_ptr)(dst + 16 * (kComp * k + (ct & ~(kWave - 1)))), 16, 0, 0);
+    // aux 2 = nt: the layer weights stream through once a token and would
+    // only evict the lm_head's rows (read again every token) from the
+    // memory-side cache.
+    __builtin_amdgcn_global_load_lds(src, (lds_ptr)(dst + 16 * (kComp * k + (ct & ~(kWave - 1)))), 16, 0, 2);
   }
 }
 
