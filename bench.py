@@ -704,6 +704,10 @@ def main() -> int:
                    "global_batch": 1, "prefix": PREFIX, "decode_steps": args.steps, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": ("recorded, not measured in this run: profiles/decode_step_traffic.json, "
+                                        "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes of decode_step_kernel on "
+                                        "this workload, scaled by the same counters on the lm_head GEMV")
+                                       if traffic is not None else None,
                      "kernel": kernel, "avg_us": round(step_us, 3),
                      "algorithmic_bytes_per_launch": int(step_bytes)},
         "gemv_lm_head": {"kernel": gemv["kernel"], "avg_us": round(gemv["avg_us"], 3),
