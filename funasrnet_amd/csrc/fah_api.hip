@@ -692,7 +692,6 @@ void init_state(fah_decoder* d, hipStream_t s) {
     a.rgu = k.ffn / nb;
     a.rd = k.width / nb;
     a.head_chunks = (k.vocab + 31) / 32;
-    a.npre = fah::persistent_max_positions();
     a.tx = d->tx.as<unsigned long long>();
     a.tqkv = d->tqkv.as<unsigned long long>();
     a.tatt = d->tatt.as<unsigned long long>();
@@ -935,14 +934,15 @@ bool use_graphs() {
 }
 
 // Positions from which a persistent-layout decoder takes the multi-kernel
-// step: the persistent kernel's attention workgroups hold about this many
-// K/V rows in LDS; past it their rows stream from HBM through 16 CUs, while
-// the multi-kernel attention spreads scores and value chains over the chip.
-constexpr int kPersistentPositions = 280;
+// step: the persistent kernel's attention workgroups hold the V rows of
+// fewer positions than fah::persistent_max_positions() in LDS and their K
+// rows in registers; past it the multi-kernel attention spreads scores and
+// value chains over the chip.
+constexpr int kPersistentPositions = 480;
 
 // `position` is the position of the row this step decodes.
 void run_kind(fah_decoder* d, int kind, hipStream_t s, int position) {
-  if (d->persistent && position < kPersistentPositions) {
+  if (d->persistent && position < std::min(kPersistentPositions, fah::persistent_max_positions())) {
     fah::PersistentArgs a = d->pargs;
     a.mode = kind;
     check(fah::launch_decode_step(a, d->blocks, s), "persistent decode step");
@@ -1766,7 +1766,6 @@ int fah_decoder_create(fah_context* h, const fah_decoder_config* cfg, const fah_
     const int nb = 256;
     d->persistent = !(env && env[0] == '0') && half && cus >= nb &&
                     fah::persistent_shape_supported(k.width, k.heads, k.kv_heads, k.head_size, k.ffn, nb) &&
-                    k.capacity <= fah::persistent_max_capacity() &&
                     fah::persistent_blocks_per_cu(k.width) >= 1;
     d->wt->persistent_layout = d->persistent;
     // Gate/up storage tiles: R gate rows then the matching R up rows. The
@@ -2065,12 +2064,7 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
     d->q_width = parent->q_width;
     d->kv_width = parent->kv_width;
     d->wt = parent->wt;
-    if (d->wt->persistent_layout) {
-      require(capacity <= fah::persistent_max_capacity(),
-              "session capacity exceeds the persistent decode step's limit of " +
-                  std::to_string(fah::persistent_max_capacity()) + " positions");
-      d->persistent = true;
-    }
+    if (d->wt->persistent_layout) d->persistent = true;
     require(fah::attention_slices(capacity, d->cfg.head_size) != 0,
             "capacity exceeds the attention kernel's LDS budget");
     std::lock_guard<std::mutex> lock(c->gate);

@@ -140,7 +140,6 @@ struct PersistentArgs {
   float eps, divisor;
   int rq, ro, rgu, rd;  // rows per workgroup: qkv, o, gate (and up), down
   int head_chunks;      // lm_head chunks of 32 rows
-  int npre;             // K/V positions staged in LDS
   unsigned long long *tx, *tqkv, *tatt, *ta, *th, *tkeys;  // tagged exchange words
   // Quantised exchanges (qblock_words layout): the attention output
   // for the o projection and the ffn activations for the down projection.
@@ -250,8 +249,8 @@ hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s
 // Whether 256 workgroups of the persistent kernel's size land on XCD
 // w % 8 (one launch of a placement probe; false if it cannot tell).
 bool persistent_xcd_round_robin(hipStream_t s);
+// Positions the persistent kernel takes (position + 1 at most this).
 int persistent_max_positions();
-int persistent_max_capacity();
 int persistent_threads();
 int persistent_blocks_per_cu(int width);
 

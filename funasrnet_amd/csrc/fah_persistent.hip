@@ -54,6 +54,12 @@ constexpr int kProdFloats = 1024;        // (row, block) products of one phase
 constexpr int kKvBytes = 121 * 1024;     // K/V staging: 512 B per position
 constexpr int kProbOffset = 4 * 128;     // attention probabilities after q/k/v in the tag area
 constexpr long kSpinLimit = 1L << 21;    // bounded polls per gather (~1-2 s)
+// Positions an attention workgroup takes: the V rows of the earlier ones
+// fill its K/V area (256 B each), their K rows sit in registers (two passes
+// of 256 positions, two lanes each), their probabilities in the gather
+// area after the q/k/v words.
+constexpr int kExactPositions = kKvBytes / 256;
+static_assert(kExactPositions <= 512 && kProbOffset + (kExactPositions + 1) / 2 <= kTagWords, "attention layout");
 // A wave polls a sentinel first when its part of a gather has more than this
 // many 1 KB chunks; a part of one chunk is polled whole (one round trip
 // sooner, and little enough traffic).
@@ -291,16 +297,15 @@ __device__ __forceinline__ float tag_value(const u64* tag, int i) { return u2f((
 
 // Time-ordered value sum of channel c = 2 * lane + HI over positions
 // [0, pos]: acc = acc + p[t] * v[t][c] from 0f in order (the reference's
-// value loop), V rows of earlier positions staged in LDS at 512 B per
-// position ([0, npre) in kv, [npre, nlds) in ovf; V at byte 256 of a
-// row), later ones read from vglob (this layer and head), this position's
-// value in cur[2]. The dword at byte 4 * lane of a V row holds channels
-// 2 * lane (low half) and 2 * lane + 1 (high half). Blocks of 16
-// positions: 8 paired reads and 4 probability reads, the next block's
-// issued before the current block is added. Writes cur[0][c].
+// value loop), V rows of earlier positions staged in LDS at 256 B per
+// position ([0, nlds) in vs), later ones read from vglob (this layer and
+// head), this position's value in cur[2]. The dword at byte 4 * lane of a
+// V row holds channels 2 * lane (low half) and 2 * lane + 1 (high half).
+// Blocks of 16 positions: 8 paired reads and 4 probability reads, the next
+// block's issued before the current block is added. Writes cur[0][c].
 template <bool HI>
-__device__ __forceinline__ void value_chain(const char* kv, const char* ovf, const float* p, int npre, int nlds,
-                                            int pos, const _Float16* vglob, float (*cur)[128]) {
+__device__ __forceinline__ void value_chain(const char* vs, const float* p, int nlds, int pos,
+                                            const _Float16* vglob, float (*cur)[128]) {
   const int lane = threadIdx.x & (kWave - 1), c = 2 * lane + (HI ? 1 : 0);
   auto half = [](uint32_t d) { return __builtin_bit_cast(_Float16, (uint16_t)(HI ? d >> 16 : d)); };
   float acc = 0.0f;
@@ -308,18 +313,18 @@ __device__ __forceinline__ void value_chain(const char* kv, const char* ovf, con
   // block loop can count LDS reads instead of draining them all.
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   auto region = [&](const char* base, int t0, int count) {
-    const char* vr = base + 256 + 4 * lane;
+    const char* vr = base + 4 * lane;
     // The probabilities through a per-lane pointer, so that their block loads
     // take immediate offsets from one VGPR and issue with the value loads.
     using lds_float = __attribute__((address_space(3))) const float;
     lds_float* pl = (lds_float*)(p + t0);
     asm volatile("" : "+v"(pl));
-    auto one = [&](int i) { acc = fadd(acc, mulh(p[t0 + i], half(*reinterpret_cast<const uint32_t*>(vr + (size_t)i * 512)))); };
+    auto one = [&](int i) { acc = fadd(acc, mulh(p[t0 + i], half(*reinterpret_cast<const uint32_t*>(vr + (size_t)i * 256)))); };
     int i = 0;
     for (; i < count && ((t0 + i) & 3) != 0; ++i) one(i);
     auto fetch = [&](uint32_t* v, float4* pq, int i0) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = *reinterpret_cast<const uint32_t*>(vr + (size_t)(i0 + k) * 512);
+      for (int k = 0; k < 16; ++k) v[k] = *reinterpret_cast<const uint32_t*>(vr + (size_t)(i0 + k) * 256);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         typedef float f4 __attribute__((ext_vector_type(4)));
@@ -374,8 +379,7 @@ __device__ __forceinline__ void value_chain(const char* kv, const char* ovf, con
     }
     for (; i < count; ++i) one(i);
   };
-  region(kv, 0, npre);
-  region(ovf, npre, nlds - npre);
+  region(vs, 0, nlds);
   int t = nlds;
   const _Float16* vg = vglob + c;
   for (; t + 8 <= pos; t += 8) {
@@ -805,7 +809,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // step) ends every launch here until the host has restored the state; a
   // position outside the cache ends it before anything is written.
   if (error_load(a.error) != 0) return;
-  if (pos < 0 || pos >= a.capacity) {
+  if (pos < 0 || pos >= a.capacity || pos >= kExactPositions) {
     if (tid == 0) __hip_atomic_fetch_or(a.error, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
@@ -837,22 +841,35 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // ======================= attention workgroup ================================
     const int kh = w & 7, hq = G * kh + (w >> 3);
     const int n = pos + 1;
-    const int npre = min(pos, a.npre);
-    // Positions past the K/V stage go to the free end of the gather area
-    // (after the probabilities).
-    const int ovf_at = (kProbOffset * 8 + 4 * n + 15) & ~15;
-    const int nlds = min(pos, npre + max(0, (kTagWords * 8 - ovf_at) / 512));
-    char* ovf_s = reinterpret_cast<char*>(tag_s) + ovf_at;
+    const int nlds = pos;  // every earlier position's V row fits the K/V area (pos < kExactPositions)
     float* p_s = reinterpret_cast<float*>(tag_s + kProbOffset);  // attention probabilities after q/k/v
     const size_t kv_layer = (size_t)HKV * a.capacity * HS;
     const size_t kv_head = (size_t)kh * a.capacity * HS;
     auto kbase = [&](int l) { return a.kcache + kv_layer * l + kv_head; };
     auto vbase = [&](int l) { return a.vcache + kv_layer * l + kv_head; };
-    // Every wave stages its share of layer l's K/V rows (earlier positions)
-    // and waits for them; readers are behind the next barrier.
+    // Layer l's rows of the earlier positions: every wave stages its share
+    // of the V rows (1 KB pieces round-robin) in the K/V area, and each lane
+    // pair loads the two halves of the K rows of positions (tid >> 1) and
+    // (tid >> 1) + 256 into registers (lane parity h: channels 8i + 4h ..
+    // 8i + 4h + 3 of every 16-byte piece i), all waited for here; readers
+    // are behind the next barrier.
+    const int hh = tid & 1;
+    uint2 kr[2][16];
     auto stage_kv = [&](int l) {
-      dma_kv(kbase(l), vbase(l), 0, npre, kv_s, wave, kPT / kWave);
-      dma_kv(kbase(l), vbase(l), npre, nlds, ovf_s, wave, kPT / kWave);
+      const char* src = reinterpret_cast<const char*>(vbase(l));
+      const int bytes = nlds * 256;
+      for (int c = wave * 1024; c < bytes; c += kPT / kWave * 1024)
+        if (c + 16 * lane < bytes) __builtin_amdgcn_global_load_lds(src + c + 16 * lane, (lds_ptr)(kv_s + c), 16, 0, 0);
+      if (pos > 0) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          if (g == 0 || pos > kPT / 2) {
+            const uint2* kp = reinterpret_cast<const uint2*>(kbase(l) + (size_t)min((tid >> 1) + g * (kPT / 2), pos - 1) * HS + 4 * hh);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) kr[g][i] = kp[2 * i];
+          }
+        }
+      }
       __builtin_amdgcn_s_waitcnt(0);
     };
     if (a.mode == 2 && w == 0 && tid == 0) {
@@ -926,22 +943,20 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lds_barrier_p();
       sub(0);
 
-      // Scores, one position per lane: eight accumulators over channels
+      // Scores, one position per lane pair: eight accumulators over channels
       // j, j+8, ..., then the pairwise tree (AttentionAvx.cs:74-160). The
       // products q*k are formed by one mixed-precision fma with a +0 addend
       // (the F16 key widened inside the instruction): round(q*k) + 0 equals
       // round(q*k) except that a -0 product becomes +0, and no accumulator
       // here is ever -0 (they start at +0 and x + y is -0 only for -0 + -0),
-      // so every sum is the reference's. Each lane keeps the maximum of its
-      // scores for the softmax shift.
+      // so every sum is the reference's. The even lane of a pair keeps
+      // accumulators 0-3 and the odd lane 4-7, i.e. channels 8i + 4h ..
+      // 8i + 4h + 3 (h = lane parity) of every 16-byte piece i, each
+      // accumulator still summed over i = 0..15 in order; q's matching
+      // channels sit in registers, the K row halves of earlier positions too
+      // (staged with the V rows), this position's row in LDS. Each lane keeps
+      // the maximum of its scores for the softmax shift.
       float m = -__builtin_inff();
-      // Two lanes per position, so that all eight waves share the rows: the
-      // even lane keeps accumulators 0-3 and the odd lane 4-7, i.e. channels
-      // 8i + 4h .. 8i + 4h + 3 (h = lane parity) of every 16-byte piece i,
-      // each accumulator still summed over i = 0..15 in order. q's matching
-      // channels sit in registers; K pieces are read in groups of four
-      // 8-byte halves, the next group in flight while one is multiplied.
-      const int hh = tid & 1;
       float qr[64];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -951,58 +966,36 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         qr[4 * i + 2] = v.z;
         qr[4 * i + 3] = v.w;
       }
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): no scalar load pending, so LDS waits can count
-      for (int t = tid >> 1; t < n; t += kPT / 2) {
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (t < nlds || t == pos) {
-          const char* row = (t == pos ? kcur : (t < npre ? kv_s + (size_t)t * 512 : ovf_s + (size_t)(t - npre) * 512)) + 8 * hh;
-          const int x = (t & 15) << 4;
-          uint2 ka[4], kb[4];
-          auto load4 = [&](uint2* k, int g) {
+      // This position's row (LDS, swizzled pieces) into the registers of the
+      // lane pair that scores it, so that every pair runs the same code.
+      if (pos < kPT / 2) {
+        if ((tid >> 1) == pos) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) k[i] = *reinterpret_cast<const uint2*>(row + (((4 * g + i) << 4) ^ x));
-          };
-          auto mul4 = [&](const uint2* k, int g) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) score4_regs(acc, k[i], qr + 4 * (4 * g + i));
-          };
-          load4(ka, 0);
-          __builtin_amdgcn_sched_barrier(0);
-          load4(kb, 1);
-          __builtin_amdgcn_sched_barrier(0);
-          mul4(ka, 0);
-          __builtin_amdgcn_sched_barrier(0);
-          load4(ka, 2);
-          __builtin_amdgcn_sched_barrier(0);
-          mul4(kb, 1);
-          __builtin_amdgcn_sched_barrier(0);
-          load4(kb, 3);
-          __builtin_amdgcn_sched_barrier(0);
-          mul4(ka, 2);
-          __builtin_amdgcn_sched_barrier(0);
-          mul4(kb, 3);
-        } else {
-          const uint2* gk = reinterpret_cast<const uint2*>(kbase(l) + (size_t)t * HS + 4 * hh);
-#pragma unroll
-          for (int i0 = 0; i0 < 16; i0 += 4) {
-            uint2 kk[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) kk[i] = gk[2 * (i0 + i)];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) score4_regs(acc, kk[i], qr + 4 * (i0 + i));
-          }
+          for (int i = 0; i < 16; ++i) kr[0][i] = *reinterpret_cast<const uint2*>(kcur + 8 * hh + ((i ^ (pos & 15)) << 4));
         }
-        // The partner lane's four accumulators; both lanes form the same tree
-        // ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)).
-        float o[4];
+      } else if ((tid >> 1) + kPT / 2 == pos) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = u2f(dpp_u32<kDppQuadXor1>(f2u(acc[j])));
-        const float* lo = hh ? o : acc;
-        const float* hi = hh ? acc : o;
-        const float s = fadd(fadd(fadd(lo[0], hi[0]), fadd(lo[1], hi[1])), fadd(fadd(lo[2], hi[2]), fadd(lo[3], hi[3])));
-        const float sd = fdiv(s, a.divisor);
-        if (hh == 0) p_s[t] = sd;
-        m = nan_max_p(m, sd);
+        for (int i = 0; i < 16; ++i) kr[1][i] = *reinterpret_cast<const uint2*>(kcur + 8 * hh + ((i ^ (pos & 15)) << 4));
+      }
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int t = (tid >> 1) + g * (kPT / 2);
+        if (t < n) {  // both lanes of a pair
+          float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int i = 0; i < 16; ++i) score4_regs(acc, kr[g][i], qr + 4 * i);
+          // The partner lane's four accumulators; both lanes form the same
+          // tree ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)).
+          float o[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[j] = u2f(dpp_u32<kDppQuadXor1>(f2u(acc[j])));
+          const float* lo = hh ? o : acc;
+          const float* hi = hh ? acc : o;
+          const float sc = fadd(fadd(fadd(lo[0], hi[0]), fadd(lo[1], hi[1])), fadd(fadd(lo[2], hi[2]), fadd(lo[3], hi[3])));
+          const float sd = fdiv(sc, a.divisor);
+          if (hh == 0) p_s[t] = sd;
+          m = nan_max_p(m, sd);
+        }
       }
       // Softmax (TensorMath.SoftmaxAvx.cs:11-58).
       m = wave_max_nan(m);
@@ -1055,8 +1048,8 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // value is the same half of the dword (channels 2l, 2l+1) in every
       // lane of its wave and one LDS read brings two positions.
       if (wave < 2) {
-        if (wave == 0) value_chain<false>(kv_s, ovf_s, p_s, npre, nlds, pos, vbase(l), cur_s);
-        else value_chain<true>(kv_s, ovf_s, p_s, npre, nlds, pos, vbase(l), cur_s);
+        if (wave == 0) value_chain<false>(kv_s, p_s, nlds, pos, vbase(l), cur_s);
+        else value_chain<true>(kv_s, p_s, nlds, pos, vbase(l), cur_s);
       }
       mark(e + 10);
       lds_barrier_p();
@@ -1430,11 +1423,10 @@ bool persistent_shape_supported(int width, int heads, int kv_heads, int head_siz
 
 // Attention probabilities of every position live in the gather area after
 // the q/k/v words.
-int persistent_max_capacity() { return (kTagWords - kProbOffset) * 2; }
+int persistent_max_positions() { return kExactPositions; }
 
 hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s) {
   if (!persistent_shape_supported(a.width, a.heads, a.kv_heads, a.head_size, a.ffn, blocks)) return hipErrorInvalidValue;
-  if (a.capacity > persistent_max_capacity()) return hipErrorInvalidValue;
   // lm_head: two product buffers and this workgroup's logits share the K/V stage.
   const int rows = kSlotPairs * kComp / (a.width / 32);
   const int per_wg = ((a.vocab + rows - 1) / rows + 3 * blocks - 1) / (3 * blocks) * 3;
@@ -1473,7 +1465,6 @@ bool persistent_xcd_round_robin(hipStream_t s) {
   return ok && h[0] >= 0 && h[0] < 8;
 }
 
-int persistent_max_positions() { return kKvBytes / 512; }
 
 int persistent_threads() { return kPT; }
 

@@ -152,18 +152,19 @@ def test_long_cache_matches_graph_path(backend, oracle_lib, shape):
 @pytest.mark.parametrize("shape", ["small", "qwen3"])
 def test_steps_across_the_persistent_range(backend, shape):
     """A decoder with the persistent layout takes the multi-kernel step from
-    position 280 on: generating across that boundary, and decoding single
-    rows after it, matches a decoder that never used the persistent kernel."""
+    position 480 on: generating across that boundary (from a 466-row
+    prefix), and decoding single rows after it, matches a decoder that never
+    used the persistent kernel."""
     cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
     w = model.synthetic(cfg, seed=15)
-    prefix = np.random.default_rng(16).standard_normal((266, cfg.width)).astype(np.float32)
+    prefix = np.random.default_rng(16).standard_normal((466, cfg.width)).astype(np.float32)
     fast = _decoder(backend, w, True, 512)
     slow = _decoder(backend, w, False, 512)
     try:
         assert fast.persistent and not slow.persistent
         print(f"persistent boundary {shape}", flush=True)
-        lf = fast.decode(prefix, 266)
-        ls = slow.decode(prefix, 266)
+        lf = fast.decode(prefix, 466)
+        ls = slow.decode(prefix, 466)
         assert np.array_equal(lf.view(np.uint32), ls.view(np.uint32))
         tf = fast.generate(30)
         ts = slow.generate(30)
@@ -173,8 +174,8 @@ def test_steps_across_the_persistent_range(backend, shape):
         ls = slow.decode(x, 1)
         assert np.array_equal(lf.view(np.uint32), ls.view(np.uint32))
         for layer in (0, cfg.layers - 1):
-            kf, vf = fast.kv_read(layer, 297)
-            ks, vs = slow.kv_read(layer, 297)
+            kf, vf = fast.kv_read(layer, 497)
+            ks, vs = slow.kv_read(layer, 497)
             assert np.array_equal(kf.view(np.uint16), ks.view(np.uint16))
             assert np.array_equal(vf.view(np.uint16), vs.view(np.uint16))
         # Back below the boundary: the persistent kernel again.
@@ -187,6 +188,39 @@ def test_steps_across_the_persistent_range(backend, shape):
     finally:
         fast.close()
         slow.close()
+
+
+def test_persistent_after_long_prefix_matches_oracle(backend, oracle_lib):
+    """Config 2's 375-row prefix, then 16 greedy steps on the persistent
+    kernel (positions 375-390, past the V rows its attention workgroups
+    once held): every token equals the oracle's and the next row's logits
+    are bit-identical to the oracle's."""
+    cfg = model.QWEN3_0_6B
+    w = model.synthetic(cfg, seed=21)
+    frames, steps = 375, 16
+    prefix = np.random.default_rng(22).standard_normal((frames, cfg.width)).astype(np.float32)
+    fast = _decoder(backend, w, True, 512)
+    ref = oracle_lib.Decoder(w, capacity=512)
+    try:
+        assert fast.persistent
+        print(f"persistent after {frames}-row prefix", flush=True)
+        lf = fast.decode(prefix, frames)
+        lr = ref.decode(prefix, frames)
+        assert np.array_equal(lf.view(np.uint32), lr.view(np.uint32))
+        toks = fast.generate(steps)
+        expected = []
+        for _ in range(steps):
+            t = oracle_lib.greedy(lr)
+            expected.append(t)
+            lr = ref.decode(ref.embed([t]), 1)
+        assert toks.tolist() == expected
+        t = int(toks[-1])
+        lf = fast.decode(fast.embed([t]), 1)
+        lr = ref.decode(ref.embed([t]), 1)
+        assert np.array_equal(lf.view(np.uint32), lr.view(np.uint32))
+    finally:
+        fast.close()
+        ref.close()
 
 
 @pytest.mark.parametrize("shape", ["small", "qwen3"])
