@@ -409,25 +409,35 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
     for (int c = wave * 1024; c < bytes; c += 4 * 1024)
       if (c + 16 * lane < bytes) __builtin_amdgcn_global_load_lds(src + c + 16 * lane, (lds_ptr)(v_s + c), 16, 0, 0);
   }
+  // The K row of this thread's first position, requested now so that its
+  // latency passes during the q/k preparation.
+  uint4 k0[16];
+  if (tid < nv) {
+    const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)tid * hs);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) k0[i] = row[i];
+  }
   if (fused) {
     // QK-norm and RoPE of this head's q (threads 0-127) and of its KV head's
     // k (128-255), v rounded to F16: qk_prepare_kernel's arithmetic
     // (QwenDecoder.cs:186-203, Rope.cs:14-55). The first query head of the
-    // pair writes the K/V row; both keep it locally for this position.
+    // pair writes the K/V row; both keep it locally for this position. The
+    // norm weight and the RoPE factors are loaded with the raw value.
     const int part = tid >> 7, c = tid & 127, half = hs >> 1;
     const float* raw = a.qkv + (size_t)t * (a.q_width + 2 * a.kv_width);
     const float v = raw[part == 0 ? head * hs + c : a.q_width + kh * hs + c];
+    const float nw = (part == 0 ? a.q_norm : a.k_norm)[c];
+    const float cs = rope_cos[(size_t)pos * half + (c & (half - 1))];
+    const float sn = rope_sin[(size_t)pos * half + (c & (half - 1))];
     const double sq = wave_sum_double((double)v * (double)v);
     if (lane == 0) red_s[wave] = sq;
     lds_barrier();
     const float inverse = rms_inverse(red_s[2 * part] + red_s[2 * part + 1], hs, a.eps);
-    y_s[part][c] = fmul(fmul(v, inverse), (part == 0 ? a.q_norm : a.k_norm)[c]);
+    y_s[part][c] = fmul(fmul(v, inverse), nw);
     lds_barrier();
-    const float* cosine = rope_cos + (size_t)pos * half;
-    const float* sine = rope_sin + (size_t)pos * half;
     float r;
-    if (c < half) r = fadd(fmul(y_s[part][c], cosine[c]), -fmul(y_s[part][c + half], sine[c]));
-    else r = fadd(fmul(y_s[part][c - half], sine[c - half]), fmul(y_s[part][c], cosine[c - half]));
+    if (c < half) r = fadd(fmul(y_s[part][c], cs), -fmul(y_s[part][c + half], sn));
+    else r = fadd(fmul(y_s[part][c - half], sn), fmul(y_s[part][c], cs));
     if (part == 0) {
       q_s[c] = r;
       const _Float16 v16 = to_half(raw[a.q_width + a.kv_width + kh * hs + c]);
@@ -443,7 +453,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   }
   lds_barrier();
 
-  for (int s = tid; s < n; s += 256) {
+  if (tid < nv) {
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) score8(acc, k0[i], q_s + 8 * i);
+    const float sc = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
+    p_s[tid] = fdiv(sc, a.divisor);
+  }
+  for (int s = tid < nv ? tid + 256 : tid; s < n; s += 256) {
     float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     if (s < nv) {
       const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)s * hs);
