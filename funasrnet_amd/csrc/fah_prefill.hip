@@ -14,6 +14,7 @@
 // operand of lane l is the 8 bytes [8 (l / 16), 8 (l / 16) + 8) of row
 // (column) l % 16; result register j of lane l is C[4 (l / 16) + j][l % 16].
 #include <algorithm>
+#include <cstdlib>
 
 #include "fah_device.h"
 #include "fah_internal.h"
@@ -699,6 +700,108 @@ __global__ __launch_bounds__(kFewThreads) void q8_gemm_few_kernel(GemmArgs g, in
   }
 }
 
+// The lm_head of 8 to 16 frames (lock-step sessions): each wave takes
+// tiles of 16 rows and all frames, one v_mfma_i32_16x16x32_i8 per block
+// with the frames' activations as the A operand and the tile's weights as B
+// (lane l: 8 bytes of frame / row l % 16 at byte 8 (l / 16) of the block),
+// so that result register j of lane l is the exact int32 block dot of
+// frame 4 (l / 16) + j and row l % 16. Each lane adds its four terms
+// ((float)dot * w_scale) * x_scale in block order from 0f in registers: the
+// row sums of q8_gemm_few_kernel, bit for bit. The frames' activations are
+// staged in LDS once per workgroup (rows padded by 16 bytes, so that the 16
+// frames of an operand read spread over the banks), their block scales
+// transposed to [block][frame]. The weights come straight from memory, each
+// lane the 8-byte pieces of its row, 16 blocks a step, the next step's
+// (the next tile's first, at a tile's end) requested before the current
+// one is used. Per frame, the greedy key of the workgroup's rows.
+constexpr int kM16MaxK = 3072;
+constexpr int kM16Waves = 4;
+constexpr int kM16MaxGroups = 1024;
+
+__host__ __device__ inline size_t m16_lds_bytes(int K) {
+  return (size_t)16 * (K + 16) + (size_t)(K / 32) * 16 * 4 + 16 * 8;
+}
+
+template <class Scale>
+__global__ __launch_bounds__(64 * kM16Waves) void q8_head_mfma16_kernel(GemmArgs g, int tiles) {
+  extern __shared__ __attribute__((aligned(16))) char m16_s[];
+  const int K = g.K, B = K >> 5, S = g.frames, XR = K + 16;
+  int8_t* x_s = reinterpret_cast<int8_t*>(m16_s);                                    // [16][XR]
+  float* xs_s = reinterpret_cast<float*>(m16_s + (size_t)16 * XR);                   // [B][16]
+  unsigned long long* key_s = reinterpret_cast<unsigned long long*>(xs_s + B * 16);  // [16]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, kq = lane >> 4;
+  const typename Scale::type* ws = reinterpret_cast<const typename Scale::type*>(g.ws);
+  const int stride = gridDim.x * kM16Waves;
+  int t = blockIdx.x * kM16Waves + wave;
+  // One step's weights: 16 blocks from block b0 of tile tt (row clamped into
+  // the matrix; rows past the end are never written).
+  auto load = [&](int tt, int b0, long* wv, float* wsv) {
+    const int sr = min(16 * tt + l16, g.rows - 1);
+    const int8_t* wrow = g.w + (size_t)sr * K + 8 * kq + 32 * b0;
+    const typename Scale::type* wsr = ws + (size_t)sr * B + b0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      wv[i] = *reinterpret_cast<const long*>(wrow + 32 * i);
+      wsv[i] = Scale::get(wsr[i]);
+    }
+  };
+  long wa[16], wb[16];
+  float sa[16], sb[16];
+  if (t < tiles) load(t, 0, wa, sa);
+  {
+    const char* src = reinterpret_cast<const char*>(g.xq);
+    for (int f = wave; f < S; f += kM16Waves)
+      for (int c = 0; c < K; c += 1024)
+        if (c + 16 * lane < K)
+          __builtin_amdgcn_global_load_lds(src + (size_t)f * K + c + 16 * lane, (lds_ptr)(x_s + f * XR + c), 16, 0, 0);
+    for (int i = tid; i < S * B; i += 64 * kM16Waves) {
+      const int f = i / B, b = i - f * B;
+      xs_s[b * 16 + f] = g.xs[i];
+    }
+    if (tid < 16) key_s[tid] = 0ull;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  lds_barrier();
+  const v4i zero4 = {0, 0, 0, 0};
+  float acc[4];
+  auto step = [&](int b0, const long* wv, const float* wsv) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int b = b0 + i;
+      const long av = *reinterpret_cast<const long*>(x_s + l16 * XR + 32 * b + 8 * kq);
+      const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv[i], zero4, 0, 0, 0);
+      const float4 xv = *reinterpret_cast<const float4*>(xs_s + b * 16 + 4 * kq);
+      acc[0] = fadd(acc[0], fmul(fmul((float)d[0], wsv[i]), xv.x));
+      acc[1] = fadd(acc[1], fmul(fmul((float)d[1], wsv[i]), xv.y));
+      acc[2] = fadd(acc[2], fmul(fmul((float)d[2], wsv[i]), xv.z));
+      acc[3] = fadd(acc[3], fmul(fmul((float)d[3], wsv[i]), xv.w));
+    }
+  };
+  for (; t < tiles; t += stride) {
+    acc[0] = acc[1] = acc[2] = acc[3] = 0.0f;
+    // Steps in pairs (B is a multiple of 32): buffer a holds block b0,
+    // buffer b block b0 + 16; each is refilled one step ahead.
+    for (int b0 = 0; b0 < B; b0 += 32) {
+      load(t, b0 + 16, wb, sb);
+      step(b0, wa, sa);
+      if (b0 + 32 < B) load(t, b0 + 32, wa, sa);
+      else if (t + stride < tiles) load(t + stride, 0, wa, sa);
+      step(b0 + 16, wb, sb);
+    }
+    const int r = 16 * t + l16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int f = 4 * kq + j;
+      if (f < S && r < g.rows) {
+        g.out[(size_t)f * g.out_stride + r] = acc[j];
+        atomicMax(&key_s[f], greedy_key(acc[j], (uint32_t)r));
+      }
+    }
+  }
+  lds_barrier();
+  if (tid < S) g.keys[(size_t)tid * gridDim.x + blockIdx.x] = key_s[tid];
+}
+
 // Greedy token of each session's logits row from the per-workgroup keys of
 // the few-frame lm_head (QwenDecoder.Greedy, QwenDecoder.cs:278-326: first
 // maximum wins, NaN never wins, NaN at index 0 returns 0), into the
@@ -1056,7 +1159,23 @@ static int few_rows(int rows, int K, int frames, int out) {
   return R;
 }
 
+// Workgroups of q8_head_mfma16_kernel for this shape, or 0 where it does not
+// apply (FAH_FEW_MFMA=0 turns it off). At the q/k/v and gate/up shapes of
+// the sessions it measured slower than q8_gemm_few_kernel (its 256-384
+// single-tile waves each run a 32-block chain), so only the lm_head
+// (thousands of tiles) takes it.
+static int mfma16_groups(int rows, int K, int frames, int out) {
+  static const bool on = [] {
+    const char* v = std::getenv("FAH_FEW_MFMA");
+    return !(v && v[0] == '0');
+  }();
+  if (!on || out != kGemmGreedy || frames < 8 || frames > 16 || K % 1024 != 0 || K > kM16MaxK || rows < 16) return 0;
+  const int tiles = (rows + 15) / 16;
+  return std::min((tiles + kM16Waves - 1) / kM16Waves, kM16MaxGroups);
+}
+
 int few_frame_groups(int rows, int K, int frames, int out) {
+  if (const int m = mfma16_groups(rows, K, frames, out)) return m;
   if (frames < 1 || frames > kFewFrames || K % 128 != 0 || K > kFewMaxK || rows < 1) return 0;
   const int R = few_rows(rows, K, frames, out);
   return R ? (rows + R - 1) / R : 0;
@@ -1076,6 +1195,10 @@ static hipError_t launch_few_kernel(const GemmArgs& g, int R, int groups, size_t
 
 template <class Scale>
 static hipError_t launch_few_scaled(const GemmArgs& g, int out, hipStream_t s) {
+  if (const int m = mfma16_groups(g.rows, g.K, g.frames, out)) {
+    q8_head_mfma16_kernel<Scale><<<m, 64 * kM16Waves, m16_lds_bytes(g.K), s>>>(g, (g.rows + 15) / 16);
+    return hipGetLastError();
+  }
   const int R = few_rows(g.rows, g.K, g.frames, out);
   const int groups = (g.rows + R - 1) / R;
   const size_t lds = few_lds_bytes(out == kGemmSwiGLU ? 2 * R : R, g.K, g.frames);
