@@ -736,9 +736,14 @@ __device__ __forceinline__ void norm_chunk_partial(const u64* act, int c, double
 template <int K>
 __device__ __forceinline__ void quantize_norm_chunks(const u64* act, const float* norm_w, float eps, const double* red,
                                                      int* xq, float* xs) {
+  // The eight halves read at once (one LDS round trip), then added in order.
+  double2 h[kMem / kWave];
+#pragma unroll
+  for (int i = 0; i < kMem / kWave; ++i) h[i] = *reinterpret_cast<const double2*>(red + 2 * i);
+  __builtin_amdgcn_sched_barrier(0);
   double total = 0.0;
 #pragma unroll
-  for (int i = 0; i < kMem / kWave; ++i) total += red[2 * i] + red[2 * i + 1];
+  for (int i = 0; i < kMem / kWave; ++i) total += h[i].x + h[i].y;
   const float mean = (float)(total / (double)K);
   const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
   quantize4<K, true>(act, norm_w, inverse, xq, xs);
@@ -786,7 +791,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ float xs_s[kActFloats / 32];
   __shared__ float prod_s[kProdFloats];
   __shared__ float row_s[2][64];  // residual rows: [0] x, [1] a
-  __shared__ double red_s[kPT / kWave];
+  __shared__ __attribute__((aligned(16))) double red_s[kPT / kWave];
   __shared__ int flag_s;
   __shared__ int okw_s[kPT / kWave];  // per wave: its part of the last gather completed
   __shared__ __attribute__((aligned(16))) float cur_s[3][128];  // attention: q, k, v of the current position
@@ -1214,7 +1219,6 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const auto& Nx = LT[l + 1 < L ? l + 1 : l];
       const int e = 16 * l + 1;
       // ---- P1: attn_norm + qkv ----------------------------------------------
-      if (tid < ro.count) row_s[0][tid] = tag_value(tag_s, row_at(tid));
       quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
       if (ct >= 0 && l == 0) __builtin_amdgcn_s_waitcnt(0);  // layer 0's staged q/k/v slice
       lds_barrier_p();
@@ -1222,6 +1226,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lds_products<NPQ, B1>(kv_s + OQ, rq.count, xq_s, xs_s, prod_s);
       lds_barrier_p();
       sub(1);
+      // This workgroup's residual rows of x (read in the o epilogue), while
+      // wave 0 sums the q/k/v rows; the gather area keeps x until the
+      // attention output arrives, after the next barrier.
+      if (wave == 1 && lane < ro.count) row_s[0][lane] = tag_value(tag_s, row_at(lane));
       if (wave == 0) {
         if (lane < rq.count) {
           const float v = ordered_sum<B1>(prod_s, lane);
