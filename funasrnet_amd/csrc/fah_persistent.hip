@@ -539,18 +539,29 @@ __device__ __forceinline__ float ordered_sum(const float* prod, int r) {
   static_assert(B % 16 == 0, "whole float4 batches");
   const float* row = prod + r * (B + 4);
   float sum = 0.0f;
+  // Batches of 16 products, the next batch's reads issued before the
+  // current batch is added (one LDS round trip in all, not one a batch).
+  float4 q[2][4];
+  auto load = [&](float4* d, int b) {
 #pragma unroll
-  for (int b = 0; b < B; b += 16) {
-    float4 q[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) q[k] = *reinterpret_cast<const float4*>(row + b + 4 * k);
+    for (int k = 0; k < 4; ++k) d[k] = *reinterpret_cast<const float4*>(row + b + 4 * k);
+  };
+  auto add = [&](const float4* d) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      sum = fadd(sum, q[k].x);
-      sum = fadd(sum, q[k].y);
-      sum = fadd(sum, q[k].z);
-      sum = fadd(sum, q[k].w);
+      sum = fadd(sum, d[k].x);
+      sum = fadd(sum, d[k].y);
+      sum = fadd(sum, d[k].z);
+      sum = fadd(sum, d[k].w);
     }
+  };
+  load(q[0], 0);
+#pragma unroll
+  for (int b = 0; b < B; b += 16) {
+    if (b + 16 < B) load(q[((b >> 4) + 1) & 1], b + 16);
+    __builtin_amdgcn_sched_barrier(0);
+    add(q[(b >> 4) & 1]);
+    __builtin_amdgcn_sched_barrier(0);
   }
   return sum;
 }
