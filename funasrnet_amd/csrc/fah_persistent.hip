@@ -209,6 +209,36 @@ __device__ __forceinline__ bool gather(const u64* s0, int n0, int o0, const u64*
       }
     }
   }
+  if (total - first == 1) {
+    // One chunk: polled whole with two reads in flight, the newer issued
+    // before the older is checked. Both land in the chunk's LDS place and
+    // each lane's 16 bytes land whole, so a checked lane holds intact words;
+    // a later read returns data at least as new.
+    const u64* src;
+    int off;
+    locate(first, src, off);
+    auto poll = [&] { __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(tag + off), 16, 0, 16); };
+    // s_waitcnt immediate: vmcnt <= 1 (the newer read), expcnt/lgkmcnt not waited.
+    constexpr int kWaitOlderRead = 1 | (7 << 4) | (15 << 8);
+    poll();
+    for (;; ++spin) {
+      poll();
+      __builtin_amdgcn_s_waitcnt(kWaitOlderRead);
+      const uint4 t = *reinterpret_cast<const uint4*>(tag + off + 2 * lane);
+      if (__all((t.y & tmask) == gen && (t.w & tmask) == gen)) {
+        // Drained: the newer read writes the same current words.
+        __builtin_amdgcn_s_waitcnt(0);
+        on_chunk(first);
+        if (seen) seen[1] = 1;
+        return true;
+      }
+      if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(error))) {
+        if (lane == 0) __hip_atomic_fetch_or(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        return false;
+      }
+    }
+  }
   int rounds = 0;
   for (;; ++spin) {
     if (!pending) {
