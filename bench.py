@@ -277,22 +277,31 @@ def long_kv(backend, weights, positions: int = 4096, steps: int = 64):
 
 
 def long_kv_attention(backend, weights, positions: int, steps: int = 16):
-    """The attention kernels alone at a long cache: a decoder created with
-    FAH_ATTENTION_TIMES=1 runs the same steps one by one with HIP events
-    around every layer's attention launches (scores, softmax, value sums);
-    K/V-read GB/s = the K/V bytes of all layers over their attention time."""
+    """The attention alone at a long cache, K/V-read GB/s = the K/V bytes of
+    a layer over its attention time.
+
+    Persistent decoder (created with FAH_TIMELINE=1): the steps run one by
+    one and each layer's attention time is read from the phase timeline,
+    from the attention workgroups' q/k/v hand-over (the projection
+    workgroups then start reading the K rows for the scores) to the
+    publication of the attention output, median over the 16 attention
+    workgroups, layers 1..L-2 and steps. Multi-kernel decoder
+    (FAH_PERSISTENT=0; created with FAH_ATTENTION_TIMES=1): HIP events around
+    every layer's attention launches."""
     from funasrnet_amd.hip import HipDecoder
 
     cfg = weights.config
-    old = os.environ.get("FAH_ATTENTION_TIMES")
-    os.environ["FAH_ATTENTION_TIMES"] = "1"
+    keys = ("FAH_TIMELINE", "FAH_ATTENTION_TIMES")
+    old = {k: os.environ.get(k) for k in keys}
+    os.environ.update({k: "1" for k in keys})
     try:
         dec = HipDecoder(backend, weights, capacity=positions + steps + 64)
     finally:
-        if old is None:
-            del os.environ["FAH_ATTENTION_TIMES"]
-        else:
-            os.environ["FAH_ATTENTION_TIMES"] = old
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
     try:
         rng = np.random.default_rng(4)
         width = cfg.kv_heads * cfg.head_size
@@ -302,6 +311,21 @@ def long_kv_attention(backend, weights, positions: int, steps: int = 16):
             dec.kv_write(layer, k, v)
         dec.set_position(positions)
         dec.decode(rng.standard_normal((1, cfg.width)).astype(np.float32), 1)
+        if dec.persistent:
+            spans = []
+            for i in range(steps):
+                dec.generate(1)
+                tl = dec.timeline().astype(np.int64)[:cfg.heads]
+                for layer in range(1, cfg.layers - 1):
+                    e = 16 * layer + 1
+                    spans.append(float(np.median(tl[:, e + 7] - tl[:, e + 0])) * 0.01)  # 100 MHz ticks -> us
+            us = float(np.median(spans))
+            n = positions + 1 + steps // 2
+            kv_layer = 114688 // cfg.layers * n
+            gbs = kv_layer / (us * 1e-6) / 1e9
+            return {"kernels": "decode_step_kernel attention (phase timeline)", "steps": steps,
+                    "us_per_layer": round(us, 2), "kv_bytes_per_layer": int(kv_layer), "kv_read_gbs": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)}
         dec.attention_time()
         dec.generate(steps)
         ms, counted = dec.attention_time()

@@ -334,7 +334,8 @@ struct fah_decoder {
   // an instantiation and the device has the CUs for it.
   bool persistent = false;
   int blocks = 0;
-  DeviceBuffer tx, tqkv, tatt, ta, th, tkeys, tattq, thq, epoch, error, timeline;
+  int persistent_positions = 0;  // positions below which steps take the persistent kernel
+  DeviceBuffer tx, tqkv, tatt, ta, th, tkeys, tattq, thq, tscore, epoch, error, timeline;
   fah::PersistentArgs pargs{};
   // Prefill (decode of many rows at once): row buffers grown on demand.
   DeviceBuffer pf_x, pf_a, pf_qkv, pf_q, pf_h, pf_xq, pf_xs, pf_hq, pf_hs;
@@ -657,6 +658,8 @@ void init_state(fah_decoder* d, hipStream_t s) {
     tagged(d->tkeys, 2 * nb);
     tagged(d->tattq, (size_t)fah::qblock_words(q_width));
     tagged(d->thq, (size_t)fah::qblock_words(k.ffn));
+    const int score_stride = (k.capacity + 127) & ~127;
+    tagged(d->tscore, (size_t)k.heads * score_stride);
     d->epoch.allocate(16);
     d->error.allocate(16);
     unsigned one = 1;
@@ -700,6 +703,22 @@ void init_state(fah_decoder* d, hipStream_t s) {
     a.tkeys = d->tkeys.as<unsigned long long>();
     a.tattq = d->tattq.as<unsigned long long>();
     a.thq = d->thq.as<unsigned long long>();
+    a.tscore = d->tscore.as<unsigned long long>();
+    a.score_stride = score_stride;
+    // FAH_LONG_FROM: the long-cache attention from this position on (at
+    // most, and by default, the positions the attention workgroups hold).
+    a.long_from = fah::persistent_exact_positions();
+    if (const char* lf = std::getenv("FAH_LONG_FROM")) a.long_from = std::max(0, std::min(a.long_from, std::atoi(lf)));
+    // Past kLongPersistentPositions the multi-kernel step is the faster one:
+    // its value chains run on many workgroups at once, while the persistent
+    // kernel's run on one per query head (measured, a token: persistent
+    // 1.49 ms at 2,500 cached positions and 1.67 ms at 3,000; the
+    // multi-kernel step over these weights 1.64 ms at 2,816 and 1.87 ms at
+    // 4,096). FAH_PERSISTENT_POSITIONS moves the switch.
+    constexpr int kLongPersistentPositions = 3072;
+    d->persistent_positions = std::min(kLongPersistentPositions, fah::persistent_max_positions());
+    if (const char* pp = std::getenv("FAH_PERSISTENT_POSITIONS"))
+      d->persistent_positions = std::max(0, std::min(fah::persistent_max_positions(), std::atoi(pp)));
     a.x_in = d->x.as<float>();
     a.position = d->position.as<int>();
     a.token = d->token.as<int>();
@@ -933,19 +952,14 @@ bool use_graphs() {
   return on;
 }
 
-// Positions from which a persistent-layout decoder takes the multi-kernel
-// step: the persistent kernel's attention workgroups hold the V rows of
-// fewer positions than fah::persistent_max_positions() in LDS and their K
-// rows in registers; past it the multi-kernel attention spreads scores and
-// value chains over the chip.
-constexpr int kPersistentPositions = 480;
-
-// `position` is the position of the row this step decodes.
+// `position` is the position of the row this step decodes. A
+// persistent-layout decoder takes the persistent kernel below
+// d->persistent_positions and the multi-kernel step from it on.
 void run_kind(fah_decoder* d, int kind, hipStream_t s, int position) {
-  if (d->persistent && position < std::min(kPersistentPositions, fah::persistent_max_positions())) {
+  if (d->persistent && position < d->persistent_positions) {
     fah::PersistentArgs a = d->pargs;
     a.mode = kind;
-    check(fah::launch_decode_step(a, d->blocks, s), "persistent decode step");
+    check(fah::launch_decode_step(a, d->blocks, s, position >= a.long_from), "persistent decode step");
     return;
   }
   if (d->attention_times) {

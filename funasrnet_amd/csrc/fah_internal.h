@@ -144,6 +144,13 @@ struct PersistentArgs {
   // Quantised exchanges (qblock_words layout): the attention output
   // for the o projection and the ffn activations for the down projection.
   unsigned long long *tattq, *thq;
+  // Long caches: scores of the earlier positions, [heads][score_stride]
+  // tagged words (score_stride = capacity rounded up to 128), written by
+  // the projection workgroups of the kv head's XCD from position long_from
+  // on.
+  unsigned long long* tscore;
+  int score_stride;
+  int long_from;
   const float* x_in;    // modes 0/1: the input row
   int mode;             // 0 layers, 1 layers + lm_head + greedy, 2 embed token + 1
   int* position;
@@ -245,12 +252,17 @@ hipError_t launch_f32_attention(const float* q, const float* k, const float* v, 
                                 int heads, hipStream_t s);
 
 bool persistent_shape_supported(int width, int heads, int kv_heads, int head_size, int ffn, int blocks);
-hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s);
+// long_cache: the step at a position from a.long_from on (the long-cache
+// attention); the kernel ends with error 4 if the device position disagrees.
+hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s, bool long_cache);
 // Whether 256 workgroups of the persistent kernel's size land on XCD
 // w % 8 (one launch of a placement probe; false if it cannot tell).
 bool persistent_xcd_round_robin(hipStream_t s);
-// Positions the persistent kernel takes (position + 1 at most this).
+// Positions the persistent kernel takes (position + 1 at most this), and
+// the positions below which its attention workgroups hold every earlier
+// K/V row (PersistentArgs::long_from at most this).
 int persistent_max_positions();
+int persistent_exact_positions();
 int persistent_threads();
 int persistent_blocks_per_cu(int width);
 

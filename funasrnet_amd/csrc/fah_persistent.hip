@@ -38,6 +38,8 @@
 //
 // Every wait is bounded: a missing generation sets the error word and the
 // workgroup leaves, so a broken launch ends instead of hanging.
+#include <algorithm>
+
 #include "fah_device.h"
 #include "fah_internal.h"
 
@@ -60,6 +62,20 @@ constexpr long kSpinLimit = 1L << 21;    // bounded polls per gather (~1-2 s)
 // area after the q/k/v words.
 constexpr int kExactPositions = kKvBytes / 256;
 static_assert(kExactPositions <= 512 && kProbOffset + (kExactPositions + 1) / 2 <= kTagWords, "attention layout");
+// Long caches (positions from PersistentArgs::long_from on): the projection
+// workgroups of an XCD score the earlier positions of its kv head, the
+// attention workgroup gathers those scores (tagged words at the end of its
+// K/V area), keeps the probabilities of all n = pos + 1 positions in the
+// gather area after the q/k/v words and streams the V rows through a ring
+// of kRing slots of kSegPos positions: the slots below the scores are
+// filled ahead, the others once the scores are read.
+constexpr int kLongPositions = 2 * (kTagWords - kProbOffset);
+constexpr int kSegPos = 64, kSegBytes = kSegPos * 256, kRing = 7;
+constexpr int kScoreBytes = kLongPositions * 8, kScoreOffset = kKvBytes - kScoreBytes;
+constexpr int kRingAhead = kScoreOffset / kSegBytes;  // slots clear of the scores
+static_assert(kExactPositions <= kLongPositions && kLongPositions % 128 == 0 && kRing * kSegBytes <= kKvBytes &&
+                  kRingAhead >= 2 && kRingAhead < kRing,
+              "long attention layout");
 // A wave polls a sentinel first when its part of a gather has more than this
 // many 1 KB chunks; a part of one chunk is polled whole (one round trip
 // sooner, and little enough traffic).
@@ -325,24 +341,36 @@ __device__ __forceinline__ bool gather1(const u64* src, int count, uint32_t gen,
 __device__ __forceinline__ float tag_value(const u64* tag, int i) { return u2f((uint32_t)tag[i]); }
 
 
-// Time-ordered value sum of channel c = 2 * lane + HI over positions
-// [0, pos]: acc = acc + p[t] * v[t][c] from 0f in order (the reference's
-// value loop), V rows of earlier positions staged in LDS at 256 B per
-// position ([0, nlds) in vs), later ones read from vglob (this layer and
-// head), this position's value in cur[2]. The dword at byte 4 * lane of a
-// V row holds channels 2 * lane (low half) and 2 * lane + 1 (high half).
-// Blocks of 16 positions: 8 paired reads and 4 probability reads, the next
-// block's issued before the current block is added. Writes cur[0][c].
+// QK-norm + RoPE of one 128-channel head vector across a wave
+// (QwenDecoder.cs:188-194, Rope.cs:14-55): lane c holds channels c and
+// c + 64, the rotation partners; nw the norm weights, cs the position's 64
+// cosines followed by its 64 sines. The square sum is the two 64-channel
+// wave sums added low half first. Returns the rotated (c, c + 64) pair.
+__device__ __forceinline__ float2 head_norm_rope(float lo, float hi, const float* nw, const float* cs, float eps) {
+  const int c = threadIdx.x & (kWave - 1);
+  const double sq = wave_sum_double((double)lo * (double)lo) + wave_sum_double((double)hi * (double)hi);
+  const float mean = (float)(sq / 128.0);
+  const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
+  const float nlo = fmul(fmul(lo, inverse), nw[c]), nhi = fmul(fmul(hi, inverse), nw[64 + c]);
+  const float co = cs[c], sn = cs[64 + c];
+  return make_float2(fadd(fmul(nlo, co), -fmul(nhi, sn)), fadd(fmul(nlo, sn), fmul(nhi, co)));
+}
+
+// Part of the time-ordered value sum of channel c = 2 * lane + HI: acc =
+// acc + p[t] * v[t][c] in order (the reference's value loop) over
+// positions [t0, t0 + count), whose V rows sit at 256 B per position from
+// `base`. The dword at byte 4 * lane of a V row holds channels 2 * lane (low
+// half) and 2 * lane + 1 (high half). Blocks of 16 positions: 8 paired
+// reads and 4 probability reads, the next block's issued before the
+// current block is added.
 template <bool HI>
-__device__ __forceinline__ void value_chain(const char* vs, const float* p, int nlds, int pos,
-                                            const _Float16* vglob, float (*cur)[128]) {
-  const int lane = threadIdx.x & (kWave - 1), c = 2 * lane + (HI ? 1 : 0);
+__device__ __forceinline__ void value_region(const char* base, const float* p, int t0, int count, float& acc) {
+  const int lane = threadIdx.x & (kWave - 1);
   auto half = [](uint32_t d) { return __builtin_bit_cast(_Float16, (uint16_t)(HI ? d >> 16 : d)); };
-  float acc = 0.0f;
   // Drain earlier scalar loads: with none pending, the waits inside the
   // block loop can count LDS reads instead of draining them all.
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  auto region = [&](const char* base, int t0, int count) {
+  {
     const char* vr = base + 4 * lane;
     // The probabilities through a per-lane pointer, so that their block loads
     // take immediate offsets from one VGPR and issue with the value loads.
@@ -408,8 +436,19 @@ __device__ __forceinline__ void value_chain(const char* vs, const float* p, int 
       }
     }
     for (; i < count; ++i) one(i);
-  };
-  region(vs, 0, nlds);
+  }
+}
+
+// The whole value sum of channel c = 2 * lane + HI over positions [0, pos]:
+// the V rows of positions [0, nlds) staged at 256 B per position in vs, later
+// ones read from vglob (this layer and head), this position's value in
+// cur[2]. Writes cur[0][c].
+template <bool HI>
+__device__ __forceinline__ void value_chain(const char* vs, const float* p, int nlds, int pos,
+                                            const _Float16* vglob, float (*cur)[128]) {
+  const int lane = threadIdx.x & (kWave - 1), c = 2 * lane + (HI ? 1 : 0);
+  float acc = 0.0f;
+  value_region<HI>(vs, p, 0, nlds, acc);
   int t = nlds;
   const _Float16* vg = vglob + c;
   for (; t + 8 <= pos; t += 8) {
@@ -424,6 +463,7 @@ __device__ __forceinline__ void value_chain(const char* vs, const float* p, int 
   cur[0][c] = acc;
 }
 
+
 // Half a K row piece: four F16 channels 8i + 4h .. 8i + 4h + 3 into the
 // four accumulators of lane parity h (q[0..3] the matching q channels).
 __device__ __forceinline__ void score4_regs(float* acc, const uint2& kk, const float* q) {
@@ -435,6 +475,25 @@ __device__ __forceinline__ void score4_regs(float* acc, const uint2& kk, const f
     acc[2 * m] = fadd(acc[2 * m], mulh(q[2 * m], lo));
     acc[2 * m + 1] = fadd(acc[2 * m + 1], mulh(q[2 * m + 1], hi));
   }
+}
+
+// One position's score by a lane pair (lane parity h, its K row halves in
+// k, the matching q channels in q): eight accumulators over channels j,
+// j + 8, ..., four in each lane, then the pairwise tree
+// ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)) formed by both lanes
+// from the partner's accumulators, divided by the divisor
+// (AttentionAvx.cs:74-160).
+__device__ __forceinline__ float pair_score(const uint2* k, const float* q, int h, float divisor) {
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) score4_regs(acc, k[i], q + 4 * i);
+  float o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = u2f(dpp_u32<kDppQuadXor1>(f2u(acc[j])));
+  const float* lo = h ? o : acc;
+  const float* hi = h ? acc : o;
+  const float sc = fadd(fadd(fadd(lo[0], hi[0]), fadd(lo[1], hi[1])), fadd(fadd(lo[2], hi[2]), fadd(lo[3], hi[3])));
+  return fdiv(sc, divisor);
 }
 
 // A compute lane's share of one weight slice: P (row, block) pairs, each 32
@@ -794,7 +853,7 @@ __device__ __forceinline__ void quantize_norm_chunks(const u64* act, const float
 // FF feed-forward width, NBK workgroups. Workgroups [0, HQ) run attention,
 // one query head each; the other NBK - HQ run the projections, each on an
 // even share of the rows of every matrix. All of them run the lm_head.
-template <int W, int HQ, int HKV, int FF, int NBK>
+template <int W, int HQ, int HKV, int FF, int NBK, bool LONG>
 __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_step_kernel(PersistentArgs a) {
   constexpr int HS = 128, QW = HQ * HS, KVW = HKV * HS, QKVR = QW + 2 * KVW;
   constexpr int B1 = W / 32, Bq = QW / 32, Bf = FF / 32;
@@ -855,7 +914,13 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // step) ends every launch here until the host has restored the state; a
   // position outside the cache ends it before anything is written.
   if (error_load(a.error) != 0) return;
-  if (pos < 0 || pos >= a.capacity || pos >= kExactPositions) {
+  // LONG: the long-cache attention (scores spread over the projection
+  // workgroups, V rows streamed), for positions from long_from on; below it
+  // every earlier row is held by the attention workgroups. A separate
+  // instantiation, so that neither step carries the other's registers.
+  constexpr bool lng = LONG;
+  if (pos < 0 || pos >= a.capacity ||
+      (LONG ? (pos < a.long_from || pos >= kLongPositions) : (pos >= a.long_from || pos >= kExactPositions))) {
     if (tid == 0) __hip_atomic_fetch_or(a.error, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
@@ -918,6 +983,41 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       __builtin_amdgcn_s_waitcnt(0);
     };
+    // Long caches: segment k of layer l's earlier V rows (positions
+    // [kSegPos k, kSegPos (k + 1)), rows past pos - 1 clamped to it) into
+    // ring slot k % kRing, four 1 KB loads by each of waves 4-7. The first
+    // kRingAhead segments are issued during the previous layer
+    // (ring_prefetch), the rest of the first kRing once the scores have been
+    // read, then one per segment added. ring_wait(j, last): segment j has
+    // landed, with segments up to `last` issued after it (four loads each).
+    char* ring = kv_s;
+    const int nseg = (pos + kSegPos - 1) / kSegPos;
+    static_assert(kSegBytes / 4096 == 4 && 4 * (kRing - 1) <= 63, "ring wait counts");
+    auto ring_wait = [&](int j, int last) {
+      switch (max(0, min(last, nseg - 1) - j)) {
+        case 0: __builtin_amdgcn_s_waitcnt(0); break;
+        case 1: __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (15 << 8)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8)); break;
+        case 3: __builtin_amdgcn_s_waitcnt(12 | (7 << 4) | (15 << 8)); break;
+        case 4: __builtin_amdgcn_s_waitcnt(0 | (1 << 14) | (7 << 4) | (15 << 8)); break;
+        case 5: __builtin_amdgcn_s_waitcnt(4 | (1 << 14) | (7 << 4) | (15 << 8)); break;
+        default: __builtin_amdgcn_s_waitcnt(8 | (1 << 14) | (7 << 4) | (15 << 8)); break;
+      }
+    };
+    auto ring_issue = [&](int l, int k) {
+      const char* src = reinterpret_cast<const char*>(vbase(l));
+      char* dst = ring + (k % kRing) * kSegBytes + (wave - 4) * 1024;
+#pragma unroll
+      for (int i = 0; i < kSegBytes / 4096; ++i) {
+        const int b = (wave - 4) * 1024 + i * 4096 + 16 * lane;
+        const int t = min(k * kSegPos + (b >> 8), pos - 1);
+        __builtin_amdgcn_global_load_lds(src + (size_t)t * 256 + (b & 255), (lds_ptr)(dst + i * 4096), 16, 0, 0);
+      }
+    };
+    auto ring_prefetch = [&](int l) {
+      if (wave >= 4)
+        for (int k = 0; k < min(kRingAhead, nseg); ++k) ring_issue(l, k);
+    };
     if (a.mode == 2 && w == 0 && tid == 0) {
       int token = *a.token;
       if (token < 0 || token >= a.vocab) token = 0;
@@ -925,7 +1025,8 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       a.history[hcount] = token;
       *a.history_count = hcount + 1;
     }
-    stage_kv(0);
+    if (lng) ring_prefetch(0);
+    else stage_kv(0);
 
     for (int l = 0; l < L; ++l) {
       const auto& Ly = LT[l];
@@ -962,15 +1063,9 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       char* kcur = reinterpret_cast<char*>(norm_s + 512);
       if (wave < 2) {
         const int c = lane, half = HS / 2;
-        const float lo = tag_value(tag_s, wave * HS + c), hi = tag_value(tag_s, wave * HS + half + c);
-        const double sq = wave_sum_double((double)lo * (double)lo) + wave_sum_double((double)hi * (double)hi);
-        const float mean = (float)(sq / (double)HS);
-        const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, a.eps)));
-        const float* nw = norm_s + wave * HS;
-        const float nlo = fmul(fmul(lo, inverse), nw[c]), nhi = fmul(fmul(hi, inverse), nw[half + c]);
-        const float cs = norm_s[2 * HS + c], sn = norm_s[2 * HS + half + c];
-        const float rlo = fadd(fmul(nlo, cs), -fmul(nhi, sn));
-        const float rhi = fadd(fmul(nlo, sn), fmul(nhi, cs));
+        const float2 r = head_norm_rope(tag_value(tag_s, wave * HS + c), tag_value(tag_s, wave * HS + half + c),
+                                        norm_s + wave * HS, norm_s + 2 * HS, a.eps);
+        const float rlo = r.x, rhi = r.y;
         if (wave == 0) {
           cur_s[0][c] = rlo;
           cur_s[0][half + c] = rhi;
@@ -1014,8 +1109,8 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       // This position's row (LDS, swizzled pieces) into the registers of the
       // lane pair that scores it, so that every pair runs the same code.
-      if (pos < kPT / 2) {
-        if ((tid >> 1) == pos) {
+      if (lng || pos < kPT / 2) {
+        if (lng ? tid < 2 : (tid >> 1) == pos) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) kr[0][i] = *reinterpret_cast<const uint2*>(kcur + 8 * hh + ((i ^ (pos & 15)) << 4));
         }
@@ -1023,24 +1118,35 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int i = 0; i < 16; ++i) kr[1][i] = *reinterpret_cast<const uint2*>(kcur + 8 * hh + ((i ^ (pos & 15)) << 4));
       }
+      auto score_pair = [&](const uint2* k, int t) {  // both lanes of a pair
+        const float sd = pair_score(k, qr, hh, a.divisor);
+        if (hh == 0) p_s[t] = sd;
+        m = nan_max_p(m, sd);
+      };
+      if (lng) {
+        // This position by lanes 0-1; the earlier ones scored by the
+        // projection workgroups of this XCD, gathered by all eight waves
+        // (padded to whole chunks).
+        if (tid < 2) score_pair(kr[0], pos);
+        u64* sc = reinterpret_cast<u64*>(kv_s + kScoreOffset);
+        const bool ok = gather(a.tscore + (size_t)hq * a.score_stride, (pos + 127) & ~127, 0, nullptr, 0, 0, nullptr, 0,
+                               0, gen(l, 1), sc, a.error, NoPre{}, wave, kPT / kWave);
+        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+        lds_barrier_p();
+        int all = 1;
 #pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const int t = (tid >> 1) + g * (kPT / 2);
-        if (t < n) {  // both lanes of a pair
-          float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-          for (int i = 0; i < 16; ++i) score4_regs(acc, kr[g][i], qr + 4 * i);
-          // The partner lane's four accumulators; both lanes form the same
-          // tree ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)).
-          float o[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) o[j] = u2f(dpp_u32<kDppQuadXor1>(f2u(acc[j])));
-          const float* lo = hh ? o : acc;
-          const float* hi = hh ? acc : o;
-          const float sc = fadd(fadd(fadd(lo[0], hi[0]), fadd(lo[1], hi[1])), fadd(fadd(lo[2], hi[2]), fadd(lo[3], hi[3])));
-          const float sd = fdiv(sc, a.divisor);
-          if (hh == 0) p_s[t] = sd;
+        for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
+        if (!all) return;
+        for (int t = tid; t < pos; t += kPT) {
+          const float sd = tag_value(sc, t);
+          p_s[t] = sd;
           m = nan_max_p(m, sd);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const int t = (tid >> 1) + g * (kPT / 2);
+          if (t < n) score_pair(kr[g], t);
         }
       }
       // Softmax (TensorMath.SoftmaxAvx.cs:11-58).
@@ -1049,6 +1155,10 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       mark(e + 8);
       lds_barrier_p();
       sub(1);
+      // The scores have been read: the ring slots over them take the next
+      // segments.
+      if (lng && wave >= 4)
+        for (int k = kRingAhead; k < min(kRing, nseg); ++k) ring_issue(l, k);
       // The eight wave maxima in two reads, combined in order in registers.
       float mx;
       {
@@ -1086,14 +1196,37 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lds_barrier_p();
       const float inverse = inv_s;
       for (int t = tid; t < n; t += kPT) p_s[t] = fmul(p_s[t], inverse);
+      if (lng && wave >= 4) ring_wait(0, kRing - 1);  // the ring's first segment
       lds_barrier_p();
       sub(2);
       // Time-ordered value sums, one lane per channel (AttentionAvx.cs:173-224),
-      // with the same exact mixed-precision products as the scores. Wave 0
-      // takes the even channels and wave 1 the odd ones, so that a lane's
-      // value is the same half of the dword (channels 2l, 2l+1) in every
-      // lane of its wave and one LDS read brings two positions.
-      if (wave < 2) {
+      // with the same exact mixed-precision products as the scores.
+      if (lng) {
+        // Wave 0 takes the even channels and wave 1 the odd ones, so that a
+        // lane's value is the same half of the dword (channels 2l, 2l+1) in
+        // every lane of its wave and one LDS read brings two positions.
+        const bool chain = wave < 2;
+        // The ring: the chain waves add segment k while waves 4-7 issue
+        // segment k + kRing - 1 into the slot read in step k - 1 (segments
+        // up to kRing - 1 are already issued) and wait for segment k + 1.
+        float acc = 0.0f;
+        for (int k = 0; k < nseg; ++k) {
+          if (chain) {
+            const char* base = ring + (k % kRing) * kSegBytes;
+            const int cnt = min(kSegPos, pos - k * kSegPos);
+            if (wave == 0) value_region<false>(base, p_s, k * kSegPos, cnt, acc);
+            else value_region<true>(base, p_s, k * kSegPos, cnt, acc);
+          } else if (wave >= 4) {
+            if (k >= 1 && k + kRing - 1 < nseg) ring_issue(l, k + kRing - 1);
+            ring_wait(k + 1, k + kRing - 1);
+          }
+          lds_barrier_p();
+        }
+        if (chain) {
+          const int c = 2 * lane + wave;
+          cur_s[0][c] = fadd(acc, fmul(cur_s[2][c], p_s[pos]));
+        }
+      } else if (wave < 2) {
         if (wave == 0) value_chain<false>(kv_s, p_s, nlds, pos, vbase(l), cur_s);
         else value_chain<true>(kv_s, p_s, nlds, pos, vbase(l), cur_s);
       }
@@ -1126,7 +1259,8 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // attention-output exchange has left (measured slightly faster).
       if (l + 1 < L) {
         __builtin_amdgcn_s_sleep(32);
-        stage_kv(l + 1);
+        if (lng) ring_prefetch(l + 1);
+        else stage_kv(l + 1);
       }
     }
     // lm_head input: the last layer's output with output_norm.
@@ -1248,6 +1382,87 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
       return all != 0;
     };
+    // Long caches, after the q/k/v publication of layer l: this workgroup's
+    // share [t0, t1) of the earlier positions of kv head fx, scored against
+    // both of its query heads (lane pair per position, the attention
+    // workgroups' arithmetic: QK-norm + RoPE of each q by one wave, then
+    // pair_score), stored as tagged words; the last share also tags the
+    // words up to the next multiple of 128, so that the attention
+    // workgroups gather whole chunks. The K rows are requested first, into
+    // the K/V area (free from P1's products until stage_window): row r of the
+    // share at byte 256 r, its 16-byte piece i at slot i ^ (r & 15).
+    static_assert(kLongPositions <= (kPT / 2) * NX && (kLongPositions + NX - 1) / NX * 256 <= kKvBytes,
+                  "one position per lane pair, the share's K rows in the K/V area");
+    auto score_earlier = [&](int l) -> bool {
+      const auto& Ly = LT[l];
+      const int j = (w >> 3) - G;
+      const int t0 = pos * j / NX, t1 = pos * (j + 1) / NX;
+      const int h = tid & 1, r = tid >> 1, t = t0 + r;
+      {
+        const char* kb = reinterpret_cast<const char*>(a.kcache + ((size_t)l * HKV + fx) * a.capacity * HS) +
+                         (size_t)t0 * 256;
+        const int bytes = (t1 - t0) * 256;
+        for (int c = wave * 1024; c < bytes; c += kPT / kWave * 1024) {
+          const int b = c + 16 * lane, br = b >> 8;
+          if (b < bytes)
+            __builtin_amdgcn_global_load_lds(kb + (size_t)br * 256 + ((((b >> 4) & 15) ^ (br & 15)) << 4),
+                                             (lds_ptr)(kv_s + c), 16, 0, 0);
+        }
+      }
+      bool ok = true;
+      if (wave < G)
+        ok = gather(a.tqkv + (size_t)G * fx * HS, G * HS, 0, nullptr, 0, 0, nullptr, 0, 0, gen(l, 1), tag_s, a.error,
+                    [&] {
+                      if (wave == 0) {
+                        dma(Ly.q_norm, norm_s, HS * 4);
+                        dma(a.rope_cos + (size_t)pos * (HS / 2), norm_s + 2 * HS, HS * 2);
+                        dma(a.rope_sin + (size_t)pos * (HS / 2), norm_s + 2 * HS + HS / 2, HS * 2);
+                      }
+                    },
+                    wave, G);
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      if (!gathered()) return false;
+      if (wave < G) {
+        const float2 qn = head_norm_rope(tag_value(tag_s, wave * HS + lane), tag_value(tag_s, wave * HS + HS / 2 + lane),
+                                         norm_s, norm_s + 2 * HS, a.eps);
+        cur_s[wave][lane] = qn.x;
+        cur_s[wave][HS / 2 + lane] = qn.y;
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's K rows
+      lds_barrier_p();
+      if (t < t1) {
+        uint2 kk[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) kk[i] = *reinterpret_cast<const uint2*>(kv_s + r * 256 + 8 * h + ((i ^ (r & 15)) << 4));
+#pragma unroll
+        for (int s = 0; s < G; ++s) {
+          float qr[64];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(&cur_s[s][8 * i + 4 * h]);
+            qr[4 * i] = v.x;
+            qr[4 * i + 1] = v.y;
+            qr[4 * i + 2] = v.z;
+            qr[4 * i + 3] = v.w;
+          }
+          const float sd = pair_score(kk, qr, h, a.divisor);
+          if (h == (s & 1)) {
+            u64* dst = a.tscore + (size_t)(G * fx + s) * a.score_stride + t;
+            if (a.local_l2) tag_store_local(dst, gen(l, 1), sd);
+            else tag_store(dst, gen(l, 1), sd);
+          }
+        }
+      }
+      const int pad = ((pos + 127) & ~127) - pos;
+      if (j == NX - 1 && pad > 0) {
+        for (int i = tid; i < G * pad; i += kPT) {
+          u64* dst = a.tscore + (size_t)(G * fx + i / pad) * a.score_stride + pos + i % pad;
+          if (a.local_l2) tag_store_local(dst, gen(l, 1), 0.0f);
+          else tag_store(dst, gen(l, 1), 0.0f);
+        }
+      }
+      return true;
+    };
 
     // Each phase: all threads quantise (or unpack) the gathered input and
     // form the block products of the LDS slice, then wave 0 sums the rows in
@@ -1282,6 +1497,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (tl && lane == 0) tl[e + 4] = t_sub[1];
       }
       lds_barrier_p();
+      if (lng && fx < HKV && !score_earlier(l)) return;
       if (ct >= 0) stage_window(l);
       gather_q(a.tattq, QWA, gen(l, 2));
       if (ct >= 0) __builtin_amdgcn_s_waitcnt(0);  // the staged slices are in LDS before the barrier
@@ -1472,18 +1688,22 @@ bool persistent_shape_supported(int width, int heads, int kv_heads, int head_siz
 
 // Attention probabilities of every position live in the gather area after
 // the q/k/v words.
-int persistent_max_positions() { return kExactPositions; }
+int persistent_max_positions() { return kLongPositions; }
+int persistent_exact_positions() { return kExactPositions; }
 
-hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s) {
+hipError_t launch_decode_step(const PersistentArgs& a, int blocks, hipStream_t s, bool long_cache) {
   if (!persistent_shape_supported(a.width, a.heads, a.kv_heads, a.head_size, a.ffn, blocks)) return hipErrorInvalidValue;
   // lm_head: two product buffers and this workgroup's logits share the K/V stage.
   const int rows = kSlotPairs * kComp / (a.width / 32);
   const int per_wg = ((a.vocab + rows - 1) / rows + 3 * blocks - 1) / (3 * blocks) * 3;
   if ((2 * rows * (a.width / 32 + 4) + per_wg * rows) * 4 > kKvBytes) return hipErrorInvalidValue;
-  if (a.width == 1024)
-    decode_step_kernel<1024, 16, 8, 3072, 256><<<blocks, kPT, 0, s>>>(a);
-  else
-    decode_step_kernel<512, 4, 2, 1024, 256><<<blocks, kPT, 0, s>>>(a);
+  if (a.width == 1024) {
+    if (long_cache) decode_step_kernel<1024, 16, 8, 3072, 256, true><<<blocks, kPT, 0, s>>>(a);
+    else decode_step_kernel<1024, 16, 8, 3072, 256, false><<<blocks, kPT, 0, s>>>(a);
+  } else {
+    if (long_cache) decode_step_kernel<512, 4, 2, 1024, 256, true><<<blocks, kPT, 0, s>>>(a);
+    else decode_step_kernel<512, 4, 2, 1024, 256, false><<<blocks, kPT, 0, s>>>(a);
+  }
   return hipGetLastError();
 }
 
@@ -1520,10 +1740,15 @@ int persistent_threads() { return kPT; }
 // Workgroups of the persistent kernel that fit on one CU at once.
 int persistent_blocks_per_cu(int width) {
   int blocks = 0;
-  hipError_t e = width == 1024
-                     ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_step_kernel<1024, 16, 8, 3072, 256>, kPT, 0)
-                     : hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_step_kernel<512, 4, 2, 1024, 256>, kPT, 0);
-  return e == hipSuccess ? blocks : 0;
+  auto fit = [&](auto kernel) {
+    int b = 0;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, kernel, kPT, 0) == hipSuccess ? b : 0;
+  };
+  if (width == 1024)
+    blocks = std::min(fit(decode_step_kernel<1024, 16, 8, 3072, 256, false>), fit(decode_step_kernel<1024, 16, 8, 3072, 256, true>));
+  else
+    blocks = std::min(fit(decode_step_kernel<512, 4, 2, 1024, 256, false>), fit(decode_step_kernel<512, 4, 2, 1024, 256, true>));
+  return blocks;
 }
 
 }  // namespace fah

@@ -121,7 +121,7 @@ def test_capacity_exhaustion_and_restore(backend):
 
 
 def test_qwen3_0_6b_decode_tokens_match(backend, oracle_lib):
-    """Config 0 at full size: 150-row N(0,1) prefix, then 128 greedy steps;
+    """Qwen3-0.6B at full size: 150-row N(0,1) prefix, then 128 greedy steps;
     the token sequence must equal the oracle's."""
     from funasrnet_amd.hip import HipDecoder
     w = model.synthetic(model.QWEN3_0_6B, seed=0)
@@ -129,7 +129,7 @@ def test_qwen3_0_6b_decode_tokens_match(backend, oracle_lib):
     gpu = HipDecoder(backend, w, capacity=2048)
     ref = oracle_lib.Decoder(w, capacity=2048)
     try:
-        print("config 0: qwen3 150 rows + 128 steps", flush=True)
+        print("qwen3 150 rows + 128 steps", flush=True)
         lg = gpu.decode(prefix, 150)
         lr = ref.decode(prefix, 150)
         assert_logits_close(lg, lr)

@@ -18,11 +18,15 @@ def backend():
     b.close()
 
 
-def _decoder(backend, weights, persistent, capacity, local_l2=None):
+def _decoder(backend, weights, persistent, capacity, local_l2=None, long_from=None, persistent_positions=None):
     from funasrnet_amd.hip import HipDecoder
     env = {"FAH_PERSISTENT": "1" if persistent else "0"}
     if local_l2 is not None:
         env["FAH_LOCAL_L2"] = "1" if local_l2 else "0"
+    if long_from is not None:
+        env["FAH_LONG_FROM"] = str(long_from)
+    if persistent_positions is not None:
+        env["FAH_PERSISTENT_POSITIONS"] = str(persistent_positions)
     old = {k: os.environ.get(k) for k in env}
     os.environ.update(env)
     try:
@@ -88,21 +92,23 @@ def test_persistent_against_oracle_tokens(backend, oracle_lib):
         ref.close()
 
 
-@pytest.mark.parametrize("shape", ["small", "qwen3"])
-def test_long_cache_matches_graph_path(backend, oracle_lib, shape):
-    """A cache pre-filled with 4096 F16 N(0,1) rows in every layer: the
-    persistent kernel (staged rows, spill area and global rows) and the
-    per-kernel path (16 channel slices at this capacity) give identical
-    logits bits, K/V rows and tokens, and match the oracle (the full-size
-    shape too: the long-cache decode of survey config 3, 8 steps)."""
+@pytest.mark.parametrize("shape,positions,persistent_positions",
+                         [("small", 4096, 5120), ("qwen3", 4096, 5120), ("qwen3", 2048, None)])
+def test_long_cache_matches_graph_path(backend, oracle_lib, shape, positions, persistent_positions):
+    """A cache pre-filled with F16 N(0,1) rows in every layer: the persistent
+    kernel's long-cache attention (scores on the projection workgroups, V
+    rows streamed; at 4096 positions with FAH_PERSISTENT_POSITIONS past its
+    default switch, at 2048 by default) and the per-kernel path give
+    identical logits bits, K/V rows and tokens, and match the oracle (the
+    full-size shape too, 8 greedy steps)."""
     cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
     w = model.synthetic(cfg, seed=12)
-    positions, capacity, steps = 4096, 4224, 8
+    capacity, steps = positions + 128, 8
     rng = np.random.default_rng(13)
     kv = [(rng.standard_normal((positions, cfg.kv_width)).astype(np.float16),
            rng.standard_normal((positions, cfg.kv_width)).astype(np.float16)) for _ in range(cfg.layers)]
     x = rng.standard_normal((1, cfg.width)).astype(np.float32)
-    fast = _decoder(backend, w, True, capacity)
+    fast = _decoder(backend, w, True, capacity, persistent_positions=persistent_positions)
     slow = _decoder(backend, w, False, capacity)
     try:
         assert fast.persistent and not slow.persistent
@@ -151,10 +157,11 @@ def test_long_cache_matches_graph_path(backend, oracle_lib, shape):
 
 @pytest.mark.parametrize("shape", ["small", "qwen3"])
 def test_steps_across_the_persistent_range(backend, shape):
-    """A decoder with the persistent layout takes the multi-kernel step from
-    position 480 on: generating across that boundary (from a 466-row
-    prefix), and decoding single rows after it, matches a decoder that never
-    used the persistent kernel."""
+    """The persistent kernel's attention workgroups hold every earlier K/V
+    row below position 483 and take the long-cache attention from there on:
+    generating across that boundary (from a 466-row prefix), and decoding
+    single rows after it, matches a decoder that never used the persistent
+    kernel."""
     cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
     w = model.synthetic(cfg, seed=15)
     prefix = np.random.default_rng(16).standard_normal((466, cfg.width)).astype(np.float32)
@@ -191,7 +198,7 @@ def test_steps_across_the_persistent_range(backend, shape):
 
 
 def test_persistent_after_long_prefix_matches_oracle(backend, oracle_lib):
-    """Config 2's 375-row prefix, then 16 greedy steps on the persistent
+    """A 375-row prefix, then 16 greedy steps on the persistent
     kernel (positions 375-390, past the V rows its attention workgroups
     once held): every token equals the oracle's and the next row's logits
     are bit-identical to the oracle's."""
@@ -218,6 +225,49 @@ def test_persistent_after_long_prefix_matches_oracle(backend, oracle_lib):
         lf = fast.decode(fast.embed([t]), 1)
         lr = ref.decode(ref.embed([t]), 1)
         assert np.array_equal(lf.view(np.uint32), lr.view(np.uint32))
+    finally:
+        fast.close()
+        ref.close()
+
+
+@pytest.mark.parametrize("shape,local_l2", [("small", True), ("qwen3", True), ("qwen3", False)])
+def test_long_attention_at_every_position_matches_oracle(backend, oracle_lib, shape, local_l2):
+    """FAH_LONG_FROM=0: the long-cache attention (scores by the projection
+    workgroups, V rows through the ring) at every position. From an empty
+    cache, 40 single-row steps (shares of the earlier positions empty below
+    30, partial ring segments and padded score chunks), then a 150-row
+    prefix and 16 greedy steps: logits bits and tokens equal the oracle's."""
+    cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
+    w = model.synthetic(cfg, seed=31)
+    rng = np.random.default_rng(32)
+    fast = _decoder(backend, w, True, 256, local_l2=local_l2, long_from=0)
+    ref = oracle_lib.Decoder(w, capacity=256)
+    try:
+        assert fast.persistent
+        print(f"long attention everywhere {shape} local_l2={local_l2}", flush=True)
+        for step in range(40):
+            x = rng.standard_normal((1, cfg.width)).astype(np.float32)
+            lf = fast.decode(x, 1)
+            lr = ref.decode(x, 1)
+            assert np.array_equal(lf.view(np.uint32), lr.view(np.uint32)), step
+        for layer in (0, cfg.layers - 1):
+            kf, vf = fast.kv_read(layer, 40)
+            ko, vo = ref.kv(layer)
+            assert np.array_equal(kf.astype(np.float32), ko), layer
+            assert np.array_equal(vf.astype(np.float32), vo), layer
+        fast.set_position(0)
+        ref.set_position(0)
+        prefix = rng.standard_normal((150, cfg.width)).astype(np.float32)
+        lf = fast.decode(prefix, 150)
+        lr = ref.decode(prefix, 150)
+        assert np.array_equal(lf.view(np.uint32), lr.view(np.uint32))
+        toks = fast.generate(16)
+        expected = []
+        for _ in range(16):
+            t = oracle_lib.greedy(lr)
+            expected.append(t)
+            lr = ref.decode(ref.embed([t]), 1)
+        assert toks.tolist() == expected
     finally:
         fast.close()
         ref.close()
