@@ -273,21 +273,49 @@ def long_kv(backend, weights, positions: int = 4096, steps: int = 64):
     finally:
         dec.close()
     out["attention"] = long_kv_attention(backend, weights, positions)
+    out["shorter_caches"] = {str(p): long_kv_tok_s(backend, weights, p) for p in (750, 2048)}
     return out
+
+
+def long_kv_tok_s(backend, weights, positions: int, steps: int = 32) -> float:
+    """Greedy decode tok/s after `positions` cached fp16(N(0,1)) rows (the
+    persistent kernel's long-cache attention below its switch)."""
+    from funasrnet_amd import device
+    from funasrnet_amd.hip import HipDecoder
+
+    cfg = weights.config
+    dec = HipDecoder(backend, weights, capacity=positions + steps + 64)
+    try:
+        rng = np.random.default_rng(4)
+        for layer in range(cfg.layers):
+            dec.kv_write(layer, rng.standard_normal((positions, cfg.kv_width)).astype(np.float16),
+                         rng.standard_normal((positions, cfg.kv_width)).astype(np.float16))
+        dec.set_position(positions)
+        dec.decode(rng.standard_normal((1, cfg.width)).astype(np.float32), 1)
+        dec.generate(4)
+        device.synchronize()
+        start, end = device.Event(), device.Event()
+        start.record(backend.stream)
+        dec.generate(steps)
+        end.record(backend.stream)
+        end.synchronize()
+        return round(1000.0 * steps / start.elapsed_ms(end), 2)
+    finally:
+        dec.close()
 
 
 def long_kv_attention(backend, weights, positions: int, steps: int = 16):
     """The attention alone at a long cache, K/V-read GB/s = the K/V bytes of
-    a layer over its attention time.
+    a layer over its attention time. The decoder is created with
+    FAH_TIMELINE=1 and FAH_ATTENTION_TIMES=1 and runs the steps one by one.
 
-    Persistent decoder (created with FAH_TIMELINE=1): the steps run one by
-    one and each layer's attention time is read from the phase timeline,
+    Steps on the multi-kernel path (past the persistent kernel's range):
+    HIP events around every layer's attention launches. Steps on the
+    persistent kernel: each layer's attention time from the phase timeline,
     from the attention workgroups' q/k/v hand-over (the projection
     workgroups then start reading the K rows for the scores) to the
     publication of the attention output, median over the 16 attention
-    workgroups, layers 1..L-2 and steps. Multi-kernel decoder
-    (FAH_PERSISTENT=0; created with FAH_ATTENTION_TIMES=1): HIP events around
-    every layer's attention launches."""
+    workgroups, layers 1..L-2 and steps."""
     from funasrnet_amd.hip import HipDecoder
 
     cfg = weights.config
@@ -311,14 +339,18 @@ def long_kv_attention(backend, weights, positions: int, steps: int = 16):
             dec.kv_write(layer, k, v)
         dec.set_position(positions)
         dec.decode(rng.standard_normal((1, cfg.width)).astype(np.float32), 1)
-        if dec.persistent:
-            spans = []
-            for i in range(steps):
-                dec.generate(1)
-                tl = dec.timeline().astype(np.int64)[:cfg.heads]
+        dec.attention_time()
+        spans = []
+        for i in range(steps):
+            dec.generate(1)
+            tl = dec.timeline()
+            if tl is not None:
+                tl = tl.astype(np.int64)[:cfg.heads]
                 for layer in range(1, cfg.layers - 1):
                     e = 16 * layer + 1
                     spans.append(float(np.median(tl[:, e + 7] - tl[:, e + 0])) * 0.01)  # 100 MHz ticks -> us
+        ms, counted = dec.attention_time()
+        if counted == 0:
             us = float(np.median(spans))
             n = positions + 1 + steps // 2
             kv_layer = 114688 // cfg.layers * n
@@ -326,9 +358,6 @@ def long_kv_attention(backend, weights, positions: int, steps: int = 16):
             return {"kernels": "decode_step_kernel attention (phase timeline)", "steps": steps,
                     "us_per_layer": round(us, 2), "kv_bytes_per_layer": int(kv_layer), "kv_read_gbs": round(gbs, 1),
                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
-        dec.attention_time()
-        dec.generate(steps)
-        ms, counted = dec.attention_time()
         kv = sum(114688 * (positions + 1 + i + 1) for i in range(counted))
         us_per_layer = ms * 1000.0 / counted / cfg.layers
         gbs = kv / (ms * 1e-3) / 1e9
