@@ -1167,34 +1167,65 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         mx = nan_max_p(nan_max_p(nan_max_p(m0.x, m0.y), m0.z), m0.w);
         mx = nan_max_p(nan_max_p(nan_max_p(nan_max_p(mx, m1.x), m1.y), m1.z), m1.w);
       }
-      for (int t = tid; t < n; t += kPT) p_s[t] = exp_ref(fadd(p_s[t], -mx));
-      lds_barrier_p();
-      mark(e + 9);
-      const int full = n & ~7;
-      if (wave == 0) {
-        // Lane j < 8: p[j] + p[j+8] + ... in order, in double; the eight
-        // sums' pairwise tree and the tail in order, read across the wave.
-        double acc = 0.0;
-        if (lane < 8) {
-          int t = lane;
-          for (; t + 56 < full; t += 64) {
-            float v[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = p_s[t + 8 * k];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) acc = acc + (double)v[k];
-          }
-          for (; t < full; t += 8) acc = acc + (double)p_s[t];
-        }
-        double L[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) L[j] = readlane_double(acc, j);
-        double sum = ((L[0] + L[4]) + (L[1] + L[5])) + ((L[2] + L[6]) + (L[3] + L[7]));
-        for (int t = full; t < n; ++t) sum = sum + (double)p_s[t];
-        if (lane == 0) inv_s = (float)(1.0 / sum);
+      // The numerators e = exp(s - max). When every one is 0 or at least
+      // 2^-17 (and at most 1), each is a multiple of 2^-40 and every partial
+      // sum of them stays below 2^13: all of them are exact doubles, so any
+      // order of the double additions gives the reference's sum bit for bit,
+      // and the sum is formed as wave trees here. Otherwise wave 0 adds them
+      // in the reference's order below.
+      double dpart = 0.0;
+      bool dexact = true;
+      for (int t = tid; t < n; t += kPT) {
+        const float ev = exp_ref(fadd(p_s[t], -mx));
+        p_s[t] = ev;
+        dpart += (double)ev;
+        dexact = dexact && (ev == 0.0f || (ev >= 0x1p-17f && ev <= 1.0f));
+      }
+      static_assert(kLongPositions <= 8191, "exact double sums below 2^13");
+      dpart = wave_sum_double(dpart);
+      const bool wexact = __all(dexact);
+      if (lane == 0) {
+        red_s[wave] = dpart;
+        okw_s[wave] = wexact ? 1 : 0;
       }
       lds_barrier_p();
-      const float inverse = inv_s;
+      mark(e + 9);
+      int exact = 1;
+#pragma unroll
+      for (int i = 0; i < kPT / kWave; ++i) exact &= okw_s[i];
+      float inverse;
+      if (exact) {
+        double sum = 0.0;
+#pragma unroll
+        for (int i = 0; i < kPT / kWave; ++i) sum += red_s[i];
+        inverse = (float)(1.0 / sum);
+      } else {
+        const int full = n & ~7;
+        if (wave == 0) {
+          // Lane j < 8: p[j] + p[j+8] + ... in order, in double; the eight
+          // sums' pairwise tree and the tail in order, read across the wave.
+          double acc = 0.0;
+          if (lane < 8) {
+            int t = lane;
+            for (; t + 56 < full; t += 64) {
+              float v[8];
+#pragma unroll
+              for (int k = 0; k < 8; ++k) v[k] = p_s[t + 8 * k];
+#pragma unroll
+              for (int k = 0; k < 8; ++k) acc = acc + (double)v[k];
+            }
+            for (; t < full; t += 8) acc = acc + (double)p_s[t];
+          }
+          double L[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) L[j] = readlane_double(acc, j);
+          double sum = ((L[0] + L[4]) + (L[1] + L[5])) + ((L[2] + L[6]) + (L[3] + L[7]));
+          for (int t = full; t < n; ++t) sum = sum + (double)p_s[t];
+          if (lane == 0) inv_s = (float)(1.0 / sum);
+        }
+        lds_barrier_p();
+        inverse = inv_s;
+      }
       for (int t = tid; t < n; t += kPT) p_s[t] = fmul(p_s[t], inverse);
       if (lng && wave >= 4) ring_wait(0, kRing - 1);  // the ring's first segment
       lds_barrier_p();

@@ -273,6 +273,39 @@ def test_long_attention_at_every_position_matches_oracle(backend, oracle_lib, sh
         ref.close()
 
 
+@pytest.mark.parametrize("long_from", [None, 0])
+def test_peaked_attention_matches_oracle(backend, oracle_lib, long_from):
+    """K rows scaled by 24 give scores far apart, so many softmax numerators
+    fall below 2^-17 and the denominator takes the reference's sequential
+    order (not the exact wave-tree sum that flatter scores allow): logits
+    bits equal the oracle's over 6 steps at 300 cached positions, with the
+    short-cache attention and (FAH_LONG_FROM=0) the long-cache one."""
+    cfg = model.small_config(layers=2)
+    w = model.synthetic(cfg, seed=41)
+    positions, capacity = 300, 512
+    rng = np.random.default_rng(42)
+    kv = [((24.0 * rng.standard_normal((positions, cfg.kv_width))).astype(np.float16),
+           rng.standard_normal((positions, cfg.kv_width)).astype(np.float16)) for _ in range(cfg.layers)]
+    fast = _decoder(backend, w, True, capacity, long_from=long_from)
+    ref = oracle_lib.Decoder(w, capacity=capacity)
+    try:
+        assert fast.persistent
+        print(f"peaked attention long_from={long_from}", flush=True)
+        for layer, (k, v) in enumerate(kv):
+            fast.kv_write(layer, k, v)
+            ref.set_kv(layer, k.astype(np.float32), v.astype(np.float32))
+        fast.set_position(positions)
+        ref.set_position(positions)
+        for step in range(6):
+            x = rng.standard_normal((1, cfg.width)).astype(np.float32)
+            lf = fast.decode(x, 1)
+            lr = ref.decode(x, 1)
+            assert np.array_equal(lf.view(np.uint32), lr.view(np.uint32)), step
+    finally:
+        fast.close()
+        ref.close()
+
+
 @pytest.mark.parametrize("shape", ["small", "qwen3"])
 def test_persistent_without_xcd_roles_matches_graph_path(backend, oracle_lib, shape):
     """FAH_LOCAL_L2=0: roles by workgroup index, every hand-over through
