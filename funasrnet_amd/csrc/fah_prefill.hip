@@ -375,6 +375,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   __shared__ float tmax_s[4];
   __shared__ double lane_s[8];
   __shared__ float inv_s;
+  __shared__ int exact_s[4];
   const int head = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hs = 128, group = a.heads / a.kv_heads, kh = head / group;
   const bool fused = a.qkv != nullptr;
@@ -487,30 +488,52 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
   if (lane == 0) tmax_s[wave] = m;
   lds_barrier();
   const float mx = nan_max_p(nan_max_p(tmax_s[0], tmax_s[1]), nan_max_p(tmax_s[2], tmax_s[3]));
-  for (int s = tid; s < n; s += 256) p_s[s] = exp_ref(fadd(p_s[s], -mx));
+  // The numerators; when each is 0 or in [2^-17, 1] and there are fewer
+  // than 8192, every partial sum of them is an exact double, so their wave
+  // trees give the reference's in-order sum bit for bit. Otherwise the
+  // reference's order: eight residue chains, their pairwise tree, the tail.
+  double dpart = 0.0;
+  bool dexact = n < 8192;
+  for (int s = tid; s < n; s += 256) {
+    const float ev = exp_ref(fadd(p_s[s], -mx));
+    p_s[s] = ev;
+    dpart += (double)ev;
+    dexact = dexact && (ev == 0.0f || (ev >= 0x1p-17f && ev <= 1.0f));
+  }
+  dpart = wave_sum_double(dpart);
+  const bool wexact = __all(dexact);
+  if (lane == 0) {
+    lane_s[wave] = dpart;
+    exact_s[wave] = wexact ? 1 : 0;
+  }
   lds_barrier();
-  const int full = n & ~7;
-  if (tid < 8) {
-    double acc = 0.0;
-    int s = tid;
-    for (; s + 56 < full; s += 64) {
-      float v[8];
+  float inverse;
+  if (exact_s[0] & exact_s[1] & exact_s[2] & exact_s[3]) {
+    inverse = (float)(1.0 / (((lane_s[0] + lane_s[1]) + lane_s[2]) + lane_s[3]));
+  } else {  // (every thread takes the same branch)
+    const int full = n & ~7;
+    if (tid < 8) {
+      double acc = 0.0;
+      int s = tid;
+      for (; s + 56 < full; s += 64) {
+        float v[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = p_s[s + 8 * k];
+        for (int k = 0; k < 8; ++k) v[k] = p_s[s + 8 * k];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc = acc + (double)v[k];
+        for (int k = 0; k < 8; ++k) acc = acc + (double)v[k];
+      }
+      for (; s < full; s += 8) acc = acc + (double)p_s[s];
+      lane_s[tid] = acc;
     }
-    for (; s < full; s += 8) acc = acc + (double)p_s[s];
-    lane_s[tid] = acc;
+    lds_barrier();
+    if (tid == 0) {
+      double sum = ((lane_s[0] + lane_s[4]) + (lane_s[1] + lane_s[5])) + ((lane_s[2] + lane_s[6]) + (lane_s[3] + lane_s[7]));
+      for (int s = full; s < n; ++s) sum = sum + (double)p_s[s];
+      inv_s = (float)(1.0 / sum);
+    }
+    lds_barrier();
+    inverse = inv_s;
   }
-  lds_barrier();
-  if (tid == 0) {
-    double sum = ((lane_s[0] + lane_s[4]) + (lane_s[1] + lane_s[5])) + ((lane_s[2] + lane_s[6]) + (lane_s[3] + lane_s[7]));
-    for (int s = full; s < n; ++s) sum = sum + (double)p_s[s];
-    inv_s = (float)(1.0 / sum);
-  }
-  lds_barrier();
-  const float inverse = inv_s;
   for (int s = tid; s < n; s += 256) p_s[s] = fmul(p_s[s], inverse);
   if (a.stage) __builtin_amdgcn_s_waitcnt(0);  // this wave's V rows are in LDS
   lds_barrier();
