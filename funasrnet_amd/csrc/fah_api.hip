@@ -324,7 +324,7 @@ struct fah_decoder {
   int q_width = 0, kv_width = 0;
   std::shared_ptr<DecoderWeights> wt;
   DeviceBuffer rope_cos, rope_sin, kcache, vcache;
-  DeviceBuffer x, qkv_out, qh, scores, block_max, exp_t, attn, a, h, logits, keys, token, position, history, history_count, staging;
+  DeviceBuffer x, qkv_out, qh, scores, block_max, block_sum, exp_t, attn, a, h, logits, keys, token, position, history, history_count, staging;
   DeviceBuffer row_q, row_s;  // one quantised row (multi-kernel path over persistent-layout weights)
   int lm_groups = 0;
   int host_position = 0;
@@ -514,6 +514,7 @@ void enqueue_layers(fah_decoder* d, hipStream_t s) {
     at.scores = d->scores.as<float>();
     at.block_max = d->block_max.as<float>();
     at.exp_t = d->exp_t.as<double>();
+    at.block_sum = d->block_sum.as<double>();
     at.exp_stride = fah::attention_exp_stride(c.capacity);
     at.out = d->attn.as<float>();
     at.heads = c.heads;
@@ -629,6 +630,7 @@ void init_state(fah_decoder* d, hipStream_t s) {
   // each head's row in 16-byte pieces, up to 3 floats past the capacity.
   d->scores.allocate(((size_t)k.heads * k.capacity + 4) * 4);
   d->block_max.allocate((size_t)k.heads * ((k.capacity + 255) / 256) * 4);
+  d->block_sum.allocate((size_t)k.heads * ((k.capacity + 255) / 256) * 8);
   d->exp_t.allocate((size_t)k.heads * 8 * fah::attention_exp_stride(k.capacity) * 8);
   d->attn.allocate((size_t)q_width * 4);
   d->a.allocate((size_t)k.width * 4);

@@ -69,6 +69,10 @@ struct AttnArgs {
   float* scores;           // [heads][capacity]: scores, then exponentials in place
   float* block_max;        // [heads][capacity / 256 rounded up]: each score block's maximum
   double* exp_t;           // [heads][8][exp_stride]: numerators as doubles, position 8 i + j at [j][i]
+  // [heads][capacity / 256 rounded up]: each numerator block's exact double
+  // sum, NaN when a numerator of the block is outside {0} u [2^-17, 1] or
+  // there are 8192 positions or more (the denominator then takes exp_t).
+  double* block_sum;
   int exp_stride;          // capacity / 8 rounded up to a multiple of 2
   float* out;              // [heads][head_size]
   int heads, kv_heads, head_size, capacity;

@@ -370,12 +370,39 @@ __global__ __launch_bounds__(kThreads) void attn_exp_kernel(AttnArgs a) {
   const float* bm = a.block_max + (size_t)head * gridDim.y;
   float mx = bm[0];
   for (int b = 1; b < blocks; ++b) mx = nan_max(mx, bm[b]);
+  double part = 0.0;
+  bool exact = n < 8192;
   if (t < n) {
     float* sc = a.scores + (size_t)head * a.capacity + t;
     const float e = exp_ref(fadd(*sc, -mx));
     *sc = e;
     // By residue for the denominator's eight in-order lane sums.
     a.exp_t[((size_t)head * 8 + (t & 7)) * a.exp_stride + (t >> 3)] = (double)e;
+    part = (double)e;
+    exact = exact && (e == 0.0f || (e >= 0x1p-17f && e <= 1.0f));
+  }
+  // The block's sum for the denominator's exact shortcut: when every
+  // numerator is 0 or in [2^-17, 1] and there are fewer than 8192, all
+  // partial sums are exact doubles, so any order of addition is the
+  // reference's (NaN marks a block that does not qualify).
+  __shared__ double part_s[kThreads / kWave];
+  __shared__ int exact_s[kThreads / kWave];
+  part = wave_sum_double(part);
+  const bool wexact = __all(exact);
+  const int wave = tid / kWave;
+  if ((tid & (kWave - 1)) == 0) {
+    part_s[wave] = part;
+    exact_s[wave] = wexact ? 1 : 0;
+  }
+  lds_barrier();
+  if (tid == 0) {
+    double sum = 0.0;
+    int all = 1;
+    for (int w = 0; w < kThreads / kWave; ++w) {
+      sum += part_s[w];
+      all &= exact_s[w];
+    }
+    a.block_sum[(size_t)head * gridDim.y + blockIdx.y] = all ? sum : __builtin_nan("");
   }
 }
 
@@ -523,10 +550,18 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
     __builtin_amdgcn_s_waitcnt(0);
   }
   lds_barrier();
-  // The two heads' denominators, one wave each.
+  // The two heads' denominators, one wave each: the exact block sums of
+  // attn_exp_kernel when every block qualifies (any order of exact
+  // additions is the reference's), else the residue chains.
   if (wave < 2) {
-    const float inv = staged ? softmax_inverse(et_s + (size_t)wave * 8 * rs, rs, p_s + wave * np, n)
-                             : softmax_inverse(et_g + (size_t)wave * 8 * a.exp_stride, a.exp_stride, p_s + wave * np, n);
+    const double* bs = a.block_sum + (size_t)(kh * group + wave) * ((a.capacity + kThreads - 1) / kThreads);
+    double total = 0.0;
+    for (int b = lane; b < blocks; b += kWave) total += bs[b];
+    total = wave_sum_double(total);
+    float inv;
+    if (total == total) inv = (float)(1.0 / total);
+    else inv = staged ? softmax_inverse(et_s + (size_t)wave * 8 * rs, rs, p_s + wave * np, n)
+                      : softmax_inverse(et_g + (size_t)wave * 8 * a.exp_stride, a.exp_stride, p_s + wave * np, n);
     if (lane == 0) inv_s[wave] = inv;
   }
   lds_barrier();

@@ -273,24 +273,25 @@ def test_long_attention_at_every_position_matches_oracle(backend, oracle_lib, sh
         ref.close()
 
 
-@pytest.mark.parametrize("long_from", [None, 0])
-def test_peaked_attention_matches_oracle(backend, oracle_lib, long_from):
+@pytest.mark.parametrize("persistent,long_from", [(True, None), (True, 0), (False, None)])
+def test_peaked_attention_matches_oracle(backend, oracle_lib, persistent, long_from):
     """K rows scaled by 24 give scores far apart, so many softmax numerators
     fall below 2^-17 and the denominator takes the reference's sequential
     order (not the exact wave-tree sum that flatter scores allow): logits
     bits equal the oracle's over 6 steps at 300 cached positions, with the
-    short-cache attention and (FAH_LONG_FROM=0) the long-cache one."""
+    persistent kernel's short-cache attention, its long-cache one
+    (FAH_LONG_FROM=0) and the multi-kernel step."""
     cfg = model.small_config(layers=2)
     w = model.synthetic(cfg, seed=41)
     positions, capacity = 300, 512
     rng = np.random.default_rng(42)
     kv = [((24.0 * rng.standard_normal((positions, cfg.kv_width))).astype(np.float16),
            rng.standard_normal((positions, cfg.kv_width)).astype(np.float16)) for _ in range(cfg.layers)]
-    fast = _decoder(backend, w, True, capacity, long_from=long_from)
+    fast = _decoder(backend, w, persistent, capacity, long_from=long_from)
     ref = oracle_lib.Decoder(w, capacity=capacity)
     try:
-        assert fast.persistent
-        print(f"peaked attention long_from={long_from}", flush=True)
+        assert bool(fast.persistent) == persistent
+        print(f"peaked attention persistent={persistent} long_from={long_from}", flush=True)
         for layer, (k, v) in enumerate(kv):
             fast.kv_write(layer, k, v)
             ref.set_kv(layer, k.astype(np.float32), v.astype(np.float32))
