@@ -1195,10 +1195,11 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int i = 0; i < kPT / kWave; ++i) exact &= okw_s[i];
       float inverse;
       if (exact) {
-        double sum = 0.0;
-#pragma unroll
-        for (int i = 0; i < kPT / kWave; ++i) sum += red_s[i];
-        inverse = (float)(1.0 / sum);
+        // Exact in any order: a tree of the eight wave sums.
+        static_assert(kPT / kWave == 8, "eight wave sums");
+        const double2 r0 = *reinterpret_cast<const double2*>(red_s), r1 = *reinterpret_cast<const double2*>(red_s + 2);
+        const double2 r2 = *reinterpret_cast<const double2*>(red_s + 4), r3 = *reinterpret_cast<const double2*>(red_s + 6);
+        inverse = (float)(1.0 / (((r0.x + r0.y) + (r1.x + r1.y)) + ((r2.x + r2.y) + (r3.x + r3.y))));
       } else {
         const int full = n & ~7;
         if (wave == 0) {
@@ -1676,22 +1677,37 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     head_chunk(hc, c + 2 * NB);
     if (ct >= 0) load_head(hc, c + 5 * NB);
   }
-  if (wave != 0) return;
-  // Wave 0 alone from here: logits out, then this workgroup's best key.
-  for (int i = 0; i < k; ++i) {
-    const int row0 = (hw + i * NB) * HR;
-    for (int r = lane; r < HR; r += kWave)
-      if (row0 + r < a.vocab) a.logits[row0 + r] = hlog[i * HR + r];
-  }
-  best = wave_max_u64(best);
-  if (tl && lane == 0) tl[16 * L + 1] = __builtin_amdgcn_s_memrealtime();
-  if (lane == 0) {
-    if (nan_first) best = ~0ull;  // (only the holder of chunk 0) forces token 0 below
-    tag_store_bits(a.tkeys + 2 * w, gen(L, 1), (uint32_t)(best >> 32));
-    tag_store_bits(a.tkeys + 2 * w + 1, gen(L, 1), (uint32_t)best);
+  if (wave == 0) {
+    // Wave 0: logits out, then this workgroup's best key.
+    for (int i = 0; i < k; ++i) {
+      const int row0 = (hw + i * NB) * HR;
+      for (int r = lane; r < HR; r += kWave)
+        if (row0 + r < a.vocab) a.logits[row0 + r] = hlog[i * HR + r];
+    }
+    best = wave_max_u64(best);
+    if (tl && lane == 0) tl[16 * L + 1] = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) {
+      if (nan_first) best = ~0ull;  // (only the holder of chunk 0) forces token 0 below
+      tag_store_bits(a.tkeys + 2 * w, gen(L, 1), (uint32_t)(best >> 32));
+      tag_store_bits(a.tkeys + 2 * w + 1, gen(L, 1), (uint32_t)best);
+    }
   }
   if (w != 0) return;
-  if (!gather1(a.tkeys, 2 * NB, gen(L, 1), tag_s, a.error, NoPre{})) return;
+  // Workgroup 0: the 2 NB key words (one chunk per wave, polled whole).
+  {
+    constexpr int kKeyParts = 2 * NB / 128;
+    static_assert(2 * NB % 128 == 0 && kKeyParts <= kPT / kWave, "one key chunk per wave");
+    bool ok = true;
+    if (wave < kKeyParts)
+      ok = gather(a.tkeys, 2 * NB, 0, nullptr, 0, 0, nullptr, 0, 0, gen(L, 1), tag_s, a.error, NoPre{}, wave, kKeyParts);
+    if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+    lds_barrier_p();
+    if (wave != 0) return;
+    int all = 1;
+#pragma unroll
+    for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
+    if (!all) return;
+  }
   // The workgroups' keys, a quarter of the grid per lane group, then the wave.
   u64 b = 0ull;
   bool first_nan = false;
