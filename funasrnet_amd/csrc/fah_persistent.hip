@@ -1441,17 +1441,18 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                              (lds_ptr)(kv_s + c), 16, 0, 0);
         }
       }
+      // q comes through this XCD's L2 (as to the attention workgroups), so
+      // it is polled at once, two reads in flight, without the cross-XCD
+      // gather delay; wave s takes query head G fx + s.
       bool ok = true;
-      if (wave < G)
-        ok = gather(a.tqkv + (size_t)G * fx * HS, G * HS, 0, nullptr, 0, 0, nullptr, 0, 0, gen(l, 1), tag_s, a.error,
-                    [&] {
-                      if (wave == 0) {
-                        dma(Ly.q_norm, norm_s, HS * 4);
-                        dma(a.rope_cos + (size_t)pos * (HS / 2), norm_s + 2 * HS, HS * 2);
-                        dma(a.rope_sin + (size_t)pos * (HS / 2), norm_s + 2 * HS + HS / 2, HS * 2);
-                      }
-                    },
-                    wave, G);
+      if (wave < G) {
+        if (wave == 0) {
+          dma(Ly.q_norm, norm_s, HS * 4);
+          dma(a.rope_cos + (size_t)pos * (HS / 2), norm_s + 2 * HS, HS * 2);
+          dma(a.rope_sin + (size_t)pos * (HS / 2), norm_s + 2 * HS + HS / 2, HS * 2);
+        }
+        ok = poll_words<HS>(a.tqkv + (size_t)(G * fx + wave) * HS, gen(l, 1), tag_s + wave * HS, a.error, nullptr);
+      }
       if (lane == 0) okw_s[wave] = ok ? 1 : 0;
       if (!gathered()) return false;
       if (wave < G) {
