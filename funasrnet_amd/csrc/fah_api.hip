@@ -713,11 +713,11 @@ void init_state(fah_decoder* d, hipStream_t s) {
     if (const char* lf = std::getenv("FAH_LONG_FROM")) a.long_from = std::max(0, std::min(a.long_from, std::atoi(lf)));
     // Past kLongPersistentPositions the multi-kernel step is the faster one:
     // its value chains run on many workgroups at once, while the persistent
-    // kernel's run on one per query head (measured, a token: persistent
-    // 1.49 ms at 2,500 cached positions and 1.67 ms at 3,000; the
-    // multi-kernel step over these weights 1.64 ms at 2,816 and 1.87 ms at
-    // 4,096). FAH_PERSISTENT_POSITIONS moves the switch.
-    constexpr int kLongPersistentPositions = 3072;
+    // kernel's run on one per query head (measured, a token, persistent
+    // against the multi-kernel step over these weights: 1.42 / 1.56 ms at
+    // 2,560 cached positions, 1.61 / 1.64 at 3,072, 1.79 / 1.71 at 3,584).
+    // FAH_PERSISTENT_POSITIONS moves the switch.
+    constexpr int kLongPersistentPositions = 3200;
     d->persistent_positions = std::min(kLongPersistentPositions, fah::persistent_max_positions());
     if (const char* pp = std::getenv("FAH_PERSISTENT_POSITIONS"))
       d->persistent_positions = std::max(0, std::min(fah::persistent_max_positions(), std::atoi(pp)));
