@@ -637,7 +637,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
-              f"(requested --gpus {args.gpus}); see DESIGN.md for how sessions would shard.", file=sys.stderr)
+              f"(requested --gpus {args.gpus}); lock-step sessions would shard by giving each GPU its own "
+              f"sessions and a copy of the weights.", file=sys.stderr)
         return 2
     if PREFIX + max(args.steps, args.warmup) + 1 > 2048:
         print("steps + prefix exceed the decoder capacity (2048)", file=sys.stderr)

@@ -1,8 +1,9 @@
 """ctypes wrapper over the CPU oracle (oracle/fah_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
-and by bench.py's ``cpu_baseline`` leg, always as the checker or the timed CPU
-baseline, never as the product path. The C source restates the reference's
+and by bench.py's ``cpu_baseline`` leg, always as the reference the GPU
+results are compared against or the timed CPU baseline, never as the product
+path. The C source restates the reference's
 x64 C# arithmetic; see the header of fah_oracle.h for which functions are
 pinned by which independent checks.
 """

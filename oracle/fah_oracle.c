@@ -1,8 +1,8 @@
 /*
  * CPU oracle for the Qwen3 Q8_0 decoder path -- TEST INFRASTRUCTURE ONLY.
  *
- * A scalar C restatement of the reference's x64 C# path. It is the checker
- * the HIP library is compared against; the product never links or calls it.
+ * A scalar C restatement of the reference's x64 C# path. Tests compare the
+ * HIP library against it; the product never links or calls it.
  * Each function names the reference lines (paths relative to the reference
  * checkout) whose arithmetic and operation order it follows. Compile with
  * -ffp-contract=off so that no multiply-add is fused: .NET's RyuJIT does not

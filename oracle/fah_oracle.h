@@ -2,8 +2,8 @@
  * CPU oracle for the Qwen3 Q8_0 decoder path.
  *
  * TEST INFRASTRUCTURE ONLY. This is a scalar C restatement of the reference's
- * x64 C# path (src/FunAsrNet, .NET 10, AVX2/AVX-VNNI branch), written to serve
- * as the parity checker for the HIP library. Only tests/, the smoke() entry
+ * x64 C# path (src/FunAsrNet, .NET 10, AVX2/AVX-VNNI branch), written as the
+ * parity reference for the HIP library. Only tests/, the smoke() entry
  * point and bench.py's cpu_baseline leg may load it. The product path never
  * calls into it and has no CPU fallback.
  *
