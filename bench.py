@@ -409,12 +409,29 @@ def sessions_decode(backend, weights, count: int = 16, steps: int = 128, prefix:
     return result
 
 
-def step_batcher_decode(backend, weights, count: int = 16, steps: int = 128, prefix: int = 150):
+def compare_sessions(got, expected):
+    """Per-session token equality against the oracle's token lists (each
+    session decoded alone), with the first differing step of each session
+    that differs."""
+    equal, first_divergence = 0, {}
+    for i, (g, e) in enumerate(zip(got, expected)):
+        e = e[: len(g)]
+        if g == e:
+            equal += 1
+        else:
+            first_divergence[i] = next((j for j, (a, b) in enumerate(zip(g, e)) if a != b), min(len(g), len(e)))
+    return {"sessions_equal": equal, "sessions": len(got), "steps_compared": min(len(g) for g in got),
+            "first_divergence": first_divergence}
+
+
+def step_batcher_decode(backend, weights, count: int = 16, steps: int = 128, prefix: int = 150, expected=None):
     """Server-style decode: `count` worker threads, each with its own session
     and 150-row prefix (seeds 1..count), each calling the cross-context step
     batcher once per token (FunAsr.Transcribe's loop run by a pool's
     workers); aggregate tok/s over the threads' decode phase (wall clock),
-    and the mean batch the batcher formed."""
+    and the mean batch the batcher formed. With `expected` (the oracle's
+    tokens of each session decoded alone) every session's tokens are
+    compared with it."""
     import threading
     from funasrnet_amd.hip import HipDecoder, HipStepBatcher
 
@@ -426,6 +443,7 @@ def step_batcher_decode(backend, weights, count: int = 16, steps: int = 128, pre
     start_gate = threading.Barrier(count + 1)
     times = [0.0] * count
     errors = []
+    got = [[] for _ in range(count)]
 
     def worker(i):
         try:
@@ -434,7 +452,7 @@ def step_batcher_decode(backend, weights, count: int = 16, steps: int = 128, pre
             batcher.join(d)
             start_gate.wait()
             for _ in range(steps):
-                batcher.step(d)
+                got[i].append(batcher.step(d))
             times[i] = time.perf_counter()
             batcher.leave(d)
         except Exception as e:  # reported in the result
@@ -454,9 +472,12 @@ def step_batcher_decode(backend, weights, count: int = 16, steps: int = 128, pre
             t.join()
         wall = max(times) - t0
         batches, rows = batcher.stats()
-        return {"sessions": count, "steps": steps, "tok_s": round(count * steps / wall, 1),
-                "ms_per_batch": round(wall * 1e3 / max(batches, 1), 4), "batches": batches,
-                "mean_batch": round(rows / max(batches, 1), 2), "errors": errors}
+        result = {"sessions": count, "steps": steps, "tok_s": round(count * steps / wall, 1),
+                  "ms_per_batch": round(wall * 1e3 / max(batches, 1), 4), "batches": batches,
+                  "mean_batch": round(rows / max(batches, 1), 2), "errors": errors}
+        if expected is not None:
+            result["oracle_check"] = compare_sessions(got, expected)
+        return result
     finally:
         batcher.close()
         for d in sessions[1:]:
@@ -473,7 +494,7 @@ def sessions_oracle_check(weights, warm, toks, prefix: int, threads: int):
     used = oracle.set_threads(threads)
     cfg = weights.config
     count, steps = toks.shape[0], warm.shape[1] + toks.shape[1]
-    equal, first_divergence, seconds = 0, {}, 0.0
+    equal, first_divergence, seconds, tokens = 0, {}, 0.0, []
     for i in range(count):
         x = np.random.default_rng(i + 1).standard_normal((prefix, cfg.width)).astype(np.float32)
         dec = oracle.Decoder(weights, capacity=prefix + steps + 8)
@@ -488,13 +509,14 @@ def sessions_oracle_check(weights, warm, toks, prefix: int, threads: int):
             seconds += time.perf_counter() - t0
         finally:
             dec.close()
+        tokens.append(expected)
         got = warm[i].tolist() + toks[i].tolist()
         if got == expected:
             equal += 1
         else:
             first_divergence[i] = next(j for j, (a, b) in enumerate(zip(got, expected)) if a != b)
     return {"sessions_equal": equal, "sessions": count, "steps_compared": steps,
-            "first_divergence": first_divergence,
+            "first_divergence": first_divergence, "_tokens": tokens,
             "cpu": {"kind": "port", "cores": used, "tok_s": round(count * steps / seconds, 2),
                     "sample": f"oracle, each of the {count} sessions decoded alone for {steps} greedy steps "
                               f"after its {prefix}-row prefix (decode time only)"}}
@@ -699,7 +721,8 @@ def main() -> int:
         extra["long_kv"] = long_kv(backend, weights)
         extra["sessions"] = sessions_decode(backend, weights,
                                             check=None if args.no_cpu else min(16, os.cpu_count() or 1))
-        extra["step_batcher"] = step_batcher_decode(backend, weights)
+        oracle_tokens = extra["sessions"].get("oracle_check", {}).pop("_tokens", None)
+        extra["step_batcher"] = step_batcher_decode(backend, weights, expected=oracle_tokens)
         if not args.no_cpu:
             extra["cpu_baselines"] = cpu_extra_baselines(weights, min(16, os.cpu_count() or 1))
     backend.close()

@@ -183,8 +183,12 @@ public sealed unsafe class HipBackend : IFloatComputeBackend, IQuantizedComputeB
         {
             if (StepBatching && _decoders.TryGetValue(model, out var first))
             {
-                step = first.CreateSession(capacity);   // same device weights, own K/V
-                return true;
+                if (!first.IsDisposed)
+                {
+                    step = first.CreateSession(capacity);   // same device weights, own K/V
+                    return true;
+                }
+                _decoders.Remove(model);   // its sessions keep their batcher; new decoders start afresh
             }
             var created = HipDecoderStep.Create(Live, model, capacity, StepBatching);
             if (created is null)

@@ -9,14 +9,17 @@ public sealed unsafe class HipDecoderStep : IDecoderStep
 {
     private IntPtr _decoder;
     private readonly HipStepBatcher? _batcher;
-    private readonly List<HipDecoderStep> _sessions = [];
+    private bool _joined;   // registered with the batcher: this decoder is stepping
 
     private HipDecoderStep(IntPtr decoder, HipStepBatcher? batcher)
     {
         _decoder = decoder;
         _batcher = batcher;
-        _batcher?.Join(this);
+        _batcher?.AddUser();
     }
+
+    /// <summary>True once <see cref="Dispose"/> has run.</summary>
+    internal bool IsDisposed => _decoder == IntPtr.Zero;
 
     internal IntPtr Handle
     {
@@ -105,7 +108,19 @@ public sealed unsafe class HipDecoderStep : IDecoderStep
                     output is null ? null : &outputHost, outputNorm, out decoder));
             }
             // The host arrays may be released now: the weights live on the device.
-            var batcher = batching ? new HipStepBatcher(decoder, capacity) : null;
+            HipStepBatcher? batcher = null;
+            if (batching)
+            {
+                try
+                {
+                    batcher = new HipStepBatcher(decoder, capacity);
+                }
+                catch
+                {
+                    Native.fah_decoder_destroy(decoder);
+                    throw;
+                }
+            }
             return new HipDecoderStep(decoder, batcher);
         }
         finally
@@ -122,9 +137,7 @@ public sealed unsafe class HipDecoderStep : IDecoderStep
     internal HipDecoderStep CreateSession(int capacity)
     {
         Native.Check(Native.fah_decoder_create_session(Handle, capacity, out var session));
-        var step = new HipDecoderStep(session, _batcher);
-        _sessions.Add(step);
-        return step;
+        return new HipDecoderStep(session, _batcher);
     }
 
     public int Position
@@ -136,25 +149,51 @@ public sealed unsafe class HipDecoderStep : IDecoderStep
         }
     }
 
-    public void SetPosition(int position) => Native.Check(Native.fah_decoder_set_position(Handle, position));
+    public void SetPosition(int position)
+    {
+        Leave();
+        Native.Check(Native.fah_decoder_set_position(Handle, position));
+    }
 
     public void Decode(float[] embeddings, int frames, float[]? logits)
     {
+        if (frames > 1)
+        {
+            Leave();   // a prefill: the next request's first step joins again
+        }
         fixed (float* x = embeddings) fixed (float* y = logits)
         {
             Native.Check(Native.fah_decoder_decode(Handle, x, frames, y));
         }
     }
 
+    /// <summary>Greedy -> Embed -> Decode(1) (FunAsr.cs:167-178). With a batcher the
+    /// decoder joins it at its first step after a prefill, so the collecting thread
+    /// waits only for decoders that are stepping; a decoder whose next position is
+    /// past the batcher's bound steps on its own.</summary>
     public int NextToken()
     {
-        if (_batcher is not null)
+        if (_batcher is not null && Position < _batcher.MaxPositions)
         {
+            if (!_joined)
+            {
+                _batcher.Join(this);
+                _joined = true;
+            }
             return _batcher.Step(this);
         }
         int token;
         Native.Check(Native.fah_decoder_generate(Handle, 1, &token));
         return token;
+    }
+
+    private void Leave()
+    {
+        if (_joined)
+        {
+            _batcher!.Leave(this);
+            _joined = false;
+        }
     }
 
     public void Dispose()
@@ -163,12 +202,12 @@ public sealed unsafe class HipDecoderStep : IDecoderStep
         {
             return;
         }
-        _batcher?.Leave(this);
-        if (_sessions.Count == 0 && _batcher is not null && _batcher.Owner == _decoder)
-        {
-            _batcher.Dispose();
-        }
-        Native.fah_decoder_destroy(_decoder);
+        Leave();
+        IntPtr decoder = _decoder;
         _decoder = IntPtr.Zero;
+        Native.Check(Native.fah_decoder_destroy(decoder));
+        // The batcher is shared by the first decoder of a model and its
+        // sessions; the last of them to go destroys it.
+        _batcher?.ReleaseUser();
     }
 }

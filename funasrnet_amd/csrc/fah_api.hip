@@ -230,10 +230,14 @@ Ctx::~Ctx() {
 }
 
 // Enqueue section for ordinary work: holds the device lock while the caller
-// enqueues (not while the work runs).
+// enqueues. Calls that then wait for their stream release it first, so the
+// wait and the copy back do not hold up other contexts of the device.
 struct DeviceWork {
-  std::lock_guard<std::mutex> lock;
+  std::unique_lock<std::mutex> lock;
   explicit DeviceWork(const Ctx& c) : lock(device_gate(c.device).m) {}
+  void release() {
+    if (lock.owns_lock()) lock.unlock();
+  }
 };
 
 // Persistent section: the device lock, the other streams' pending work
@@ -371,6 +375,10 @@ struct fah_batcher {
   std::condition_variable cv;
   std::vector<BatchRequest*> pending;
   std::vector<fah_decoder*> joined;
+  // Joined sessions that had no step in the last batch (busy elsewhere:
+  // encoding, prefilling, idle between requests). The collector stops
+  // waiting for them until they request a step again.
+  std::vector<fah_decoder*> idle;
   bool running = false;  // a leader is collecting or running a batch
   int64_t batches_run = 0, rows_run = 0;
   // The captured step of each batch size (the session table is rewritten
@@ -1391,6 +1399,7 @@ int fah_quantized_linear(fah_context* h, const float* input, int frames, const f
       check(fah::launch_gemv(a, w->half_scales, fah::kInputFloat, fah::kOutPlain, frames, c->stream), "gemv");
     }
     check(hipMemcpyAsync(output, c->out.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
+    work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return FAH_OK;
   });
@@ -1421,6 +1430,13 @@ int fah_quantized_linear_noalloc(fah_context* h, const float* input, int frames,
     // Held until the work has finished: no other call of this library can
     // use the device's workspace meanwhile.
     std::lock_guard<std::mutex> device(device_gate(c->device).m);
+    // On every exit, error paths included, the stream drains before the
+    // device lock is let go (destroyed first): nothing this call enqueued
+    // still writes the workspace when another call may take it.
+    struct Drain {
+      hipStream_t s;
+      ~Drain() { (void)hipStreamSynchronize(s); }
+    } drain{c->stream};
     float* din = reinterpret_cast<float*>(base);
     float* dbias = bias ? reinterpret_cast<float*>(base + at_bias) : nullptr;
     float* dout = reinterpret_cast<float*>(base + at_out);
@@ -1514,6 +1530,7 @@ int fah_linear_many(fah_context* h, const float* input, int frames, const fah_we
       check(hipMemcpyAsync(outputs[i], c->out.as<float>() + at, bytes, hipMemcpyDeviceToHost, c->stream), "D2H");
       at += (size_t)frames * weights[i]->rows;
     }
+    work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return FAH_OK;
   });
@@ -1544,6 +1561,7 @@ int fah_linear(fah_context* h, const float* input, int frames, const fah_weight*
                                  w->cols, false, c->stream),
           "f32 linear");
     check(hipMemcpyAsync(output, c->out.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
+    work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return FAH_OK;
   });
@@ -1600,6 +1618,7 @@ int fah_relu_projection(fah_context* h, const float* input, int frames, const fa
           "f32 linear + ReLU");
     check(fah::launch_f32_linear(mid, second->f.as<float>(), d2, dout, frames, N, H, false, c->stream), "f32 linear");
     check(hipMemcpyAsync(output, dout, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
+    work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return FAH_OK;
   });
@@ -1629,6 +1648,7 @@ int fah_attention(fah_context* h, const float* query, const float* key, const fl
     check(hipMemcpyAsync(dv, value, bytes, hipMemcpyHostToDevice, c->stream), "H2D value");
     check(fah::launch_f32_attention(dq, dk, dv, c->out.as<float>(), frames, width, heads, c->stream), "attention");
     check(hipMemcpyAsync(output, c->out.ptr, bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
+    work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     return FAH_OK;
   });
@@ -2089,6 +2109,7 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
     DeviceWork work(*c);
     check(fah::prepare_attention(capacity, d->cfg.head_size), "attention LDS budget");
     init_state(d.get(), c->stream);
+    work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     *out = d.release();
     return FAH_OK;
@@ -2129,6 +2150,7 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
       check(hipMemcpyAsync(tokens + (size_t)i * steps, sessions[i]->history.ptr, (size_t)steps * 4,
                            hipMemcpyDeviceToHost, s),
             "D2H tokens");
+    work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
     for (int i = 0; i < count; ++i) sessions[i]->host_position += steps;
     return FAH_OK;
@@ -2187,6 +2209,7 @@ int fah_batcher_leave(fah_batcher* b, fah_decoder* session) {
   if (!b || !session) return fail(FAH_ERROR_ARGUMENT, "batcher/session is NULL");
   std::lock_guard<std::mutex> lk(b->m);
   b->joined.erase(std::remove(b->joined.begin(), b->joined.end(), session), b->joined.end());
+  b->idle.erase(std::remove(b->idle.begin(), b->idle.end(), session), b->idle.end());
   b->cv.notify_all();
   return FAH_OK;
 }
@@ -2195,43 +2218,65 @@ int fah_batcher_leave(fah_batcher* b, fah_decoder* session) {
 
 namespace {
 
+// Checks of one session's own step through a batcher; a failure goes to
+// that session's request alone (the reference throws for that decoder only,
+// QwenDecoder.cs:163).
+void check_batch_session(const fah_batcher* b, const fah_decoder* d) {
+  require_live(d);
+  if (!d->have_logits) throw StateError{"session has no logits: decode with logits first"};
+  require(d->host_position + 1 <= d->cfg.capacity, "Decoder context exhausted");
+  require(d->host_position + 1 <= b->max_positions,
+          "session at position " + std::to_string(d->host_position) + " is past the batcher's bound of " +
+              std::to_string(b->max_positions) + " positions");
+}
+
 // One lock-step batch of the requests' sessions (one greedy step each, as
 // fah_decoder_generate(session, 1)): the batch size's captured step with
-// this batch's session table. Errors go to every request of the batch.
+// this batch's session table. A request whose session fails its own checks
+// gets that error and is left out; the others run. A device error of the
+// batch itself goes to every request that was in it.
 void run_batch(fah_batcher* b, const std::vector<BatchRequest*>& reqs) {
+  std::vector<BatchRequest*> ok;
+  for (BatchRequest* r : reqs) {
+    r->status = guarded_decoder([&] {
+      check_batch_session(b, r->session);
+      return FAH_OK;
+    });
+    if (r->status != FAH_OK) r->error = fah_last_error();
+    else ok.push_back(r);
+  }
+  if (ok.empty()) return;
   std::vector<fah_decoder*> sessions;
-  for (BatchRequest* r : reqs) sessions.push_back(r->session);
+  for (BatchRequest* r : ok) sessions.push_back(r->session);
   const int count = (int)sessions.size();
-  int status = FAH_OK;
-  std::string message;
   std::vector<int32_t> tokens(count, 0);
-  status = guarded_decoder([&] {
+  const int status = guarded_decoder([&] {
     (void)check_sessions(sessions.data(), count, 1);
-    for (fah_decoder* d : sessions)
-      require(d->host_position + 1 <= b->max_positions, "session past the batcher's position bound");
     Ctx* c = b->ctx.get();
     std::lock_guard<std::mutex> lock(c->gate);
     require_live(sessions[0]);
     hipStream_t s = c->stream;
     check(hipSetDevice(c->device), "hipSetDevice");
-    DeviceWork work(*c);
-    auto& batch = b->by_size[count];
-    if (!batch) batch = make_session_batch(sessions[0], count, b->max_positions, s);
-    upload_session_table(*batch, sessions.data(), count, s);
-    for (fah_decoder* d : sessions) check(hipMemsetAsync(d->history_count.ptr, 0, 4, s), "reset history");
-    if (batch->graph) check(hipGraphLaunch(batch->graph, s), "hipGraphLaunch");
-    else enqueue_sessions_step(sessions[0], *batch, s);
-    for (int i = 0; i < count; ++i)
-      check(hipMemcpyAsync(&tokens[i], sessions[i]->history.ptr, 4, hipMemcpyDeviceToHost, s), "D2H token");
+    {
+      DeviceWork work(*c);
+      auto& batch = b->by_size[count];
+      if (!batch) batch = make_session_batch(sessions[0], count, b->max_positions, s);
+      upload_session_table(*batch, sessions.data(), count, s);
+      for (fah_decoder* d : sessions) check(hipMemsetAsync(d->history_count.ptr, 0, 4, s), "reset history");
+      if (batch->graph) check(hipGraphLaunch(batch->graph, s), "hipGraphLaunch");
+      else enqueue_sessions_step(sessions[0], *batch, s);
+      for (int i = 0; i < count; ++i)
+        check(hipMemcpyAsync(&tokens[i], sessions[i]->history.ptr, 4, hipMemcpyDeviceToHost, s), "D2H token");
+    }
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
     for (fah_decoder* d : sessions) d->host_position += 1;
     return FAH_OK;
   });
-  if (status != FAH_OK) message = fah_last_error();
+  const std::string message = status != FAH_OK ? fah_last_error() : std::string();
   for (int i = 0; i < count; ++i) {
-    reqs[i]->status = status;
-    reqs[i]->error = message;
-    reqs[i]->token = tokens[i];
+    ok[i]->status = status;
+    ok[i]->error = message;
+    ok[i]->token = tokens[i];
   }
 }
 
@@ -2243,25 +2288,38 @@ int fah_batcher_step(fah_batcher* b, fah_decoder* session, int32_t* token) {
   if (!b || !session || !token) return fail(FAH_ERROR_ARGUMENT, "batcher/session/token is NULL");
   if (session->wt != b->wt || session->ctx != b->ctx)
     return fail(FAH_ERROR_ARGUMENT, "session does not share the batcher's weights");
+  // The session's own checks first: a step it cannot take fails here, for
+  // this caller alone, and never enters a batch.
+  const int checked = guarded_decoder([&] {
+    check_batch_session(b, session);
+    return FAH_OK;
+  });
+  if (checked != FAH_OK) return checked;
   BatchRequest req;
   req.session = session;
   std::unique_lock<std::mutex> lk(b->m);
   for (BatchRequest* r : b->pending)
     if (r->session == session) return fail(FAH_ERROR_STATE, "the session already has a step pending");
   b->pending.push_back(&req);
+  b->idle.erase(std::remove(b->idle.begin(), b->idle.end(), session), b->idle.end());
   b->cv.notify_all();
   while (!req.done) {
     if (!b->running) {
-      // Leader: collect the steps of the joined sessions (or of whoever
-      // arrives within the window), then run them as one batch.
+      // Leader: collect the steps of the joined sessions that are stepping
+      // (or of whoever arrives within the window), then run them as one
+      // batch. A joined session that had no step in the last batch is idle
+      // and not waited for until it requests a step again.
       b->running = true;
       const auto deadline = std::chrono::steady_clock::now() + b->window;
+      auto is_joined = [&](const fah_decoder* d) {
+        return std::find(b->joined.begin(), b->joined.end(), d) != b->joined.end();
+      };
       auto want = [&] {
         size_t joined_pending = 0;
         for (BatchRequest* r : b->pending)
-          if (std::find(b->joined.begin(), b->joined.end(), r->session) != b->joined.end()) ++joined_pending;
-        const size_t full = std::min<size_t>(fah::kFewFrames, b->pending.size());
-        return full >= (size_t)fah::kFewFrames || (!b->joined.empty() && joined_pending >= b->joined.size());
+          if (is_joined(r->session)) ++joined_pending;
+        const size_t expected = b->joined.size() - b->idle.size();
+        return b->pending.size() >= (size_t)fah::kFewFrames || (expected > 0 && joined_pending >= expected);
       };
       while (!want()) {
         if (b->cv.wait_until(lk, deadline) == std::cv_status::timeout) break;
@@ -2269,12 +2327,22 @@ int fah_batcher_step(fah_batcher* b, fah_decoder* session, int32_t* token) {
       const size_t n = std::min<size_t>(fah::kFewFrames, b->pending.size());
       std::vector<BatchRequest*> batch(b->pending.begin(), b->pending.begin() + n);
       b->pending.erase(b->pending.begin(), b->pending.begin() + n);
+      for (fah_decoder* d : b->joined) {
+        bool stepping = false;
+        for (BatchRequest* r : batch) stepping = stepping || r->session == d;
+        for (BatchRequest* r : b->pending) stepping = stepping || r->session == d;
+        if (!stepping && std::find(b->idle.begin(), b->idle.end(), d) == b->idle.end()) b->idle.push_back(d);
+      }
       lk.unlock();
       run_batch(b, batch);
       lk.lock();
-      for (BatchRequest* r : batch) r->done = true;
-      ++b->batches_run;
-      b->rows_run += (int64_t)n;
+      int64_t served = 0;
+      for (BatchRequest* r : batch) {
+        r->done = true;
+        served += r->status == FAH_OK;
+      }
+      b->batches_run += served > 0;
+      b->rows_run += served;
       b->running = false;
       b->cv.notify_all();
       continue;

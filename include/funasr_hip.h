@@ -303,10 +303,17 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
  * runs each context's decode separately.
  *
  * The first waiting thread collects: it runs the batch once every joined
- * session has a step pending, 16 steps are pending, or `window_us` has
- * passed since it began to collect (sessions that never join are batched
- * with whatever arrives within the window). Sessions must stay below
- * `max_positions` positions (at most 15360). */
+ * session that is stepping has a step pending, 16 steps are pending, or
+ * `window_us` has passed since it began to collect (sessions that never join
+ * are batched with whatever arrives within the window). A joined session
+ * with no step in the last batch counts as idle and is not waited for until
+ * it requests a step again. Sessions must stay below `max_positions`
+ * positions (at most 15360).
+ *
+ * Errors are per request: a session that cannot take its step (no logits,
+ * its capacity or the batcher's bound reached, context destroyed) gets the
+ * error at once and never enters a batch, and the other sessions' steps run
+ * as usual. Only a device error of a batch reaches every request in it. */
 int fah_batcher_create(fah_decoder* parent, int max_positions, int window_us, fah_batcher** out);
 /* FAH_ERROR_STATE while a step is in progress. */
 int fah_batcher_destroy(fah_batcher* batcher);
@@ -319,7 +326,7 @@ int fah_batcher_leave(fah_batcher* batcher, fah_decoder* session);
  * threads request at the same time; blocks until it has run. The session
  * must hold logits from its last decode. */
 int fah_batcher_step(fah_batcher* batcher, fah_decoder* session, int32_t* token);
-/* Batches run and session steps served so far. */
+/* Batches run and session steps served (successful steps) so far. */
 int fah_batcher_stats(fah_batcher* batcher, int64_t* batches, int64_t* rows);
 
 /* Overwrite cached K/V rows [0, positions) of one layer from fp16 bit

@@ -154,13 +154,48 @@ def test_sixteen_qwen3_sessions(backend, oracle_lib):
         parent.close()
 
 
+def _oracle_tokens(oracle_lib, w, prefix, steps, capacity):
+    """Greedy tokens of one session decoded by the oracle: prefix, then
+    Greedy -> Embed -> Decode(1) (FunAsr.cs:167-178)."""
+    ref = oracle_lib.Decoder(w, capacity=capacity)
+    try:
+        lr = ref.decode(prefix, prefix.shape[0])
+        out = []
+        for _ in range(steps):
+            t = oracle_lib.greedy(lr)
+            out.append(t)
+            lr = ref.decode(ref.embed([t]), 1)
+        return out
+    finally:
+        ref.close()
+
+
+def _run_workers(count, worker):
+    import threading
+    errors = [None] * count
+
+    def wrapped(i):
+        try:
+            worker(i)
+        except Exception as e:  # reported by the caller
+            errors[i] = e
+
+    threads = [threading.Thread(target=wrapped, args=(i,)) for i in range(count)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=300)
+    assert not any(t.is_alive() for t in threads)
+    return errors
+
+
 @pytest.mark.parametrize("shape", ["small", "qwen3"])
 def test_step_batcher_threads(backend, oracle_lib, shape):
-    """Eight worker threads, each decoding its own session (own prefix) with
+    """Eight worker threads (BoundedInferencePool.cs:78 over the contexts of
+    SpeechRuntime.cs:16-23), each decoding its own session (own prefix) with
     the cross-context step batcher, one blocking step per token: every
-    session's tokens equal fah_decoder_generate on it alone, and the steps
-    really ran in batches."""
-    import threading
+    session's tokens equal the oracle's decode of that session alone, and the
+    steps really ran in batches."""
     from funasrnet_amd.hip import HipDecoder, HipStepBatcher
     cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
     w = model.synthetic(cfg, seed=41)
@@ -168,45 +203,129 @@ def test_step_batcher_threads(backend, oracle_lib, shape):
     capacity = frames + steps + 8
     prefixes = [np.random.default_rng(100 + i).standard_normal((frames, cfg.width)).astype(np.float32)
                 for i in range(count)]
-    expected = []
-    alone = HipDecoder(backend, w, capacity=capacity)
-    try:
-        for p in prefixes:
-            alone.set_position(0)
-            alone.decode(p, frames)
-            expected.append(alone.generate(steps).tolist())
-    finally:
-        alone.close()
+    expected = [_oracle_tokens(oracle_lib, w, p, steps, capacity) for p in prefixes]
     parent = HipDecoder(backend, w, capacity=capacity)
     sessions = [parent] + [parent.session() for _ in range(count - 1)]
     batcher = HipStepBatcher(parent, max_positions=capacity, window_us=2000)
-    results, errors = [None] * count, []
+    results = [None] * count
 
     def worker(i):
-        try:
-            d = sessions[i]
-            d.decode(prefixes[i], frames)
-            batcher.join(d)
-            toks = [batcher.step(d) for _ in range(steps)]
-            batcher.leave(d)
-            results[i] = toks
-        except Exception as e:  # reported below
-            errors.append(repr(e))
+        d = sessions[i]
+        d.decode(prefixes[i], frames)
+        batcher.join(d)
+        results[i] = [batcher.step(d) for _ in range(steps)]
+        batcher.leave(d)
 
     print(f"step batcher {shape}: {count} threads x {steps} steps", flush=True)
-    threads = [threading.Thread(target=worker, args=(i,)) for i in range(count)]
     try:
-        for t in threads:
-            t.start()
-        for t in threads:
-            t.join(timeout=300)
-        assert not any(t.is_alive() for t in threads)
-        assert not errors, errors
-        assert results == expected
+        errors = _run_workers(count, worker)
+        assert not any(errors), errors
+        diverged = [i for i in range(count) if results[i] != expected[i]]
+        assert not diverged, f"sessions differing from the oracle: {diverged}"
         batches, rows = batcher.stats()
         assert rows == count * steps
         assert batches < rows, (batches, rows)  # steps were merged
         print(f"batches {batches}, rows {rows}, mean batch {rows / batches:.2f}", flush=True)
+    finally:
+        batcher.close()
+        for d in sessions[1:]:
+            d.close()
+        parent.close()
+
+
+def test_step_batcher_isolates_failures(backend, oracle_lib):
+    """One of eight sessions runs out of room (its own capacity, then the
+    batcher's bound for another): each gets its error alone, at the step
+    where the reference's decoder would throw (QwenDecoder.cs:163), and the
+    other sessions' tokens still equal the oracle's."""
+    from funasrnet_amd.hip import HipDecoder, HipStepBatcher
+    cfg = model.small_config(layers=2)
+    w = model.synthetic(cfg, seed=43)
+    count, steps, frames = 8, 16, 20
+    bound = frames + steps + 4
+    prefixes = [np.random.default_rng(300 + i).standard_normal((frames, cfg.width)).astype(np.float32)
+                for i in range(count)]
+    expected = [_oracle_tokens(oracle_lib, w, p, steps, bound) for p in prefixes]
+    parent = HipDecoder(backend, w, capacity=bound)
+    # Session 3 holds frames + 6 positions: its 7th step is refused. Session
+    # 5 holds more than the batcher's bound; it starts past the bound.
+    caps = [bound] * count
+    caps[3] = frames + 6
+    caps[5] = bound + 64
+    sessions = [parent] + [parent.session(caps[i]) for i in range(1, count)]
+    batcher = HipStepBatcher(parent, max_positions=bound, window_us=2000)
+    results = [[] for _ in range(count)]
+
+    def worker(i):
+        d = sessions[i]
+        if i == 5:
+            d.decode(np.zeros((bound, cfg.width), np.float32), bound)
+        else:
+            d.decode(prefixes[i], frames)
+        batcher.join(d)
+        try:
+            for _ in range(steps):
+                results[i].append(batcher.step(d))
+        finally:
+            batcher.leave(d)
+
+    print("step batcher failure isolation: 8 threads, sessions 3 and 5 run out of room", flush=True)
+    try:
+        errors = _run_workers(count, worker)
+        assert isinstance(errors[3], ValueError) and "exhausted" in str(errors[3]), errors[3]
+        assert results[3] == expected[3][:6]
+        assert sessions[3].position == frames + 6
+        assert isinstance(errors[5], ValueError) and "bound" in str(errors[5]), errors[5]
+        assert results[5] == [] and sessions[5].position == bound
+        for i in range(count):
+            if i in (3, 5):
+                continue
+            assert errors[i] is None, (i, errors[i])
+            assert results[i] == expected[i], i
+        batches, rows = batcher.stats()
+        assert rows == (count - 2) * steps + 6
+    finally:
+        batcher.close()
+        for d in sessions[1:]:
+            d.close()
+        parent.close()
+
+
+def test_step_batcher_idle_joined_session(backend):
+    """A joined session that stops stepping (its worker encodes or prefills)
+    holds up the collector once, for one window, not at every step."""
+    import time
+    from funasrnet_amd.hip import HipDecoder, HipStepBatcher
+    cfg = model.small_config(layers=1)
+    w = model.synthetic(cfg, seed=45)
+    steps, frames, window_us = 20, 8, 100_000
+    parent = HipDecoder(backend, w, capacity=64)
+    sessions = [parent] + [parent.session() for _ in range(3)]
+    batcher = HipStepBatcher(parent, max_positions=64, window_us=window_us)
+    x = np.random.default_rng(7).standard_normal((frames, cfg.width)).astype(np.float32)
+    try:
+        for d in sessions:
+            d.decode(x, frames)
+            batcher.join(d)
+        idle = sessions[3]  # joined, never steps
+        results = [None] * 3
+
+        def worker(i):
+            results[i] = [batcher.step(sessions[i]) for _ in range(steps)]
+
+        print("step batcher: 3 stepping sessions and 1 idle joined session", flush=True)
+        t0 = time.perf_counter()
+        errors = _run_workers(3, worker)
+        elapsed = time.perf_counter() - t0
+        assert not any(errors), errors
+        assert results[0] == results[1] == results[2]  # same prefix, same weights
+        # Waiting a window at each of the 20 steps would take 2 s.
+        assert elapsed < 6 * window_us * 1e-6, elapsed
+        batches, rows = batcher.stats()
+        assert rows == 3 * steps
+        assert idle.position == frames
+        for d in sessions:
+            batcher.leave(d)
     finally:
         batcher.close()
         for d in sessions[1:]:
