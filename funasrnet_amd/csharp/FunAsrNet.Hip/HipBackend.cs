@@ -204,6 +204,37 @@ public sealed unsafe class HipBackend : IFloatComputeBackend, IQuantizedComputeB
         }
     }
 
+    /// <summary>Counter snapshot per seam entry point, as VulkanFloatBackend.Statistics()
+    /// reports its calls, transfers and end-to-end time (VulkanFloatBackend.cs:86-118),
+    /// with each kind's kernel time measured on the device.</summary>
+    public object Statistics()
+    {
+        lock (_gate)
+        {
+            var stats = new Native.CallStats[Native.CallKinds.Length];
+            fixed (Native.CallStats* p = stats)
+            {
+                Native.Check(Native.fah_context_statistics(Live, p, stats.Length));
+            }
+            var calls = new Dictionary<string, object>();
+            for (int i = 0; i < stats.Length; i++)
+            {
+                var s = stats[i];
+                calls[Native.CallKinds[i]] = new
+                {
+                    calls = s.Calls,
+                    declined = s.Declined,
+                    operations = s.Operations,
+                    uploadedBytes = s.UploadedBytes,
+                    downloadedBytes = s.DownloadedBytes,
+                    deviceSeconds = s.DeviceMilliseconds / 1000.0,
+                    endToEndSeconds = s.TotalMilliseconds / 1000.0,
+                };
+            }
+            return new { device = Name, precision = "FP32 + original Q8_0", calls };
+        }
+    }
+
     /// <summary>Device copy of a weight, uploaded once per managed array
     /// (VulkanFloatBackend.cs:242-283); released with the array or the context.</summary>
     private WeightHandle Upload(Weight weight)

@@ -49,7 +49,21 @@ internal static unsafe partial class Native
         public float* AttnNorm, QNorm, KNorm, FfnNorm;
     }
 
+    /// <summary>fah_call_stats: one seam entry point's counters.</summary>
+    [StructLayout(LayoutKind.Sequential)]
+    internal struct CallStats
+    {
+        public long Calls, Declined, Operations, UploadedBytes, DownloadedBytes;
+        public double DeviceMilliseconds, TotalMilliseconds;
+    }
+
+    /// <summary>FAH_CALL_* order of fah_context_statistics.</summary>
+    internal static readonly string[] CallKinds =
+        ["quantizedLinear", "quantizedLinearNoAlloc", "linearMany", "linear", "reluProjection", "attention"];
+
     [LibraryImport(Lib)] internal static partial int fah_abi_version();
+    [LibraryImport(Lib)] internal static partial int fah_context_statistics(IntPtr context, CallStats* stats, int kinds);
+    [LibraryImport(Lib)] internal static partial int fah_context_reset_statistics(IntPtr context);
     [LibraryImport(Lib)] internal static partial IntPtr fah_last_error();
     [LibraryImport(Lib)] internal static partial int fah_device_count();
     [LibraryImport(Lib)] internal static partial int fah_context_create(int device, out IntPtr context);

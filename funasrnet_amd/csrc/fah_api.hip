@@ -188,6 +188,13 @@ struct Ctx {
   DeviceBuffer in, out, q, s;
   std::string name;
   std::unique_ptr<SessionBatch> batch;  // last lock-step batch (its sessions alive)
+  // Seam-call statistics (fah_context_statistics) and the call observer;
+  // t0/t1 bracket a call's kernels on the stream.
+  std::mutex stats_m;
+  fah_call_stats stats[FAH_CALL_KINDS] = {};
+  fah_call_observer observer = nullptr;
+  void* observer_user = nullptr;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
   Ctx() = default;
   Ctx(const Ctx&) = delete;
   Ctx& operator=(const Ctx&) = delete;
@@ -226,6 +233,8 @@ Ctx::~Ctx() {
   q.release();
   s.release();
   if (mark) (void)hipEventDestroy(mark);
+  if (t0) (void)hipEventDestroy(t0);
+  if (t1) (void)hipEventDestroy(t1);
   (void)hipStreamDestroy(stream);
 }
 
@@ -254,6 +263,45 @@ struct PersistentSection {
   }
   ~PersistentSection() { (void)hipStreamSynchronize(c.stream); }
 };
+
+// Accounting of one seam call that runs on the device: its kernels between
+// the context's two events, its wall time from construction to done(), and
+// the bytes it copies. done() runs after the stream has drained.
+struct CallMeter {
+  Ctx& c;
+  int kind;
+  int64_t up = 0, down = 0;
+  std::chrono::steady_clock::time_point start = std::chrono::steady_clock::now();
+  CallMeter(Ctx& ctx, int k) : c(ctx), kind(k) {}
+  void kernels_begin() { check(hipEventRecord(c.t0, c.stream), "hipEventRecord"); }
+  void kernels_end() { check(hipEventRecord(c.t1, c.stream), "hipEventRecord"); }
+  void done(int frames, int cols, int rows, int64_t operations) {
+    float device_ms = 0.0f;
+    (void)hipEventElapsedTime(&device_ms, c.t0, c.t1);
+    const double total_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - start).count();
+    fah_call_observer observer;
+    void* user;
+    {
+      std::lock_guard<std::mutex> lock(c.stats_m);
+      fah_call_stats& s = c.stats[kind];
+      ++s.calls;
+      s.operations += operations;
+      s.uploaded_bytes += up;
+      s.downloaded_bytes += down;
+      s.device_ms += device_ms;
+      s.total_ms += total_ms;
+      observer = c.observer;
+      user = c.observer_user;
+    }
+    if (observer) observer(user, kind, frames, cols, rows, device_ms, total_ms);
+  }
+};
+
+int declined(Ctx* c, int kind) {
+  std::lock_guard<std::mutex> lock(c->stats_m);
+  ++c->stats[kind].declined;
+  return FAH_DECLINED;
+}
 
 // Workspace of fah_quantized_linear_noalloc: the staged input, bias and
 // output and the quantised activations, in one fixed device array per GPU
@@ -1187,6 +1235,8 @@ int fah_context_create(int device, fah_context** out) {
     check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
     st->stream = stream;
     check(hipEventCreateWithFlags(&st->mark, hipEventDisableTiming), "hipEventCreate");
+    check(hipEventCreate(&st->t0), "hipEventCreate");
+    check(hipEventCreate(&st->t1), "hipEventCreate");
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) st->name = std::string("HIP ") + prop.gcnArchName;
     else st->name = "HIP";
@@ -1238,6 +1288,31 @@ int fah_context_set_minimum_operations(fah_context* h, int64_t operations) {
 }
 
 void* fah_context_stream(fah_context* h) { return h ? (void*)h->st->stream : nullptr; }
+
+int fah_context_statistics(fah_context* h, fah_call_stats* out, int kinds) {
+  if (!h || (kinds > 0 && !out) || kinds < 0) return fail(FAH_ERROR_ARGUMENT, "invalid statistics request");
+  Ctx* c = h->st.get();
+  std::lock_guard<std::mutex> lock(c->stats_m);
+  for (int i = 0; i < std::min(kinds, (int)FAH_CALL_KINDS); ++i) out[i] = c->stats[i];
+  return FAH_OK;
+}
+
+int fah_context_reset_statistics(fah_context* h) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
+  std::lock_guard<std::mutex> lock(c->stats_m);
+  for (fah_call_stats& s : c->stats) s = fah_call_stats{};
+  return FAH_OK;
+}
+
+int fah_context_set_call_observer(fah_context* h, fah_call_observer observer, void* user) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
+  std::lock_guard<std::mutex> lock(c->stats_m);
+  c->observer = observer;
+  c->observer_user = user;
+  return FAH_OK;
+}
 
 int fah_weight_q8_upload(fah_context* h, const int8_t* quantized, const float* scales, int rows, int cols,
                          fah_weight** out) {
@@ -1365,16 +1440,19 @@ int fah_quantized_linear(fah_context* h, const float* input, int frames, const f
                          float* output) {
   if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
   Ctx* c = h->st.get();
-  if (!w || w->f32 || frames <= 0 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
-  if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return FAH_DECLINED;
+  if (!w || w->f32 || frames <= 0 || w->cols > fah::gemv_max_k()) return declined(c, FAH_CALL_QUANTIZED_LINEAR);
+  if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return declined(c, FAH_CALL_QUANTIZED_LINEAR);
   return guarded([&] {
     require(input && output, "Q8 GPU projection needs input and output");
     require(w->ctx.get() == c, "weight belongs to another context");
     std::lock_guard<std::mutex> lock(c->gate);
     if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    CallMeter meter(*c, FAH_CALL_QUANTIZED_LINEAR);
     check(hipSetDevice(c->device), "hipSetDevice");
     DeviceWork work(*c);
     size_t in_bytes = (size_t)frames * w->cols * 4, out_bytes = (size_t)frames * w->rows * 4;
+    meter.up = (int64_t)in_bytes + (bias ? (int64_t)w->rows * 4 : 0);
+    meter.down = (int64_t)out_bytes;
     c->in.ensure(in_bytes + (bias ? (size_t)w->rows * 4 : 0));
     c->out.ensure(out_bytes);
     check(hipMemcpyAsync(c->in.ptr, input, in_bytes, hipMemcpyHostToDevice, c->stream), "H2D input");
@@ -1387,6 +1465,7 @@ int fah_quantized_linear(fah_context* h, const float* input, int frames, const f
       size_t n = (size_t)frames * w->cols;
       c->q.ensure(n);
       c->s.ensure(n / 32 * 4);
+      meter.kernels_begin();
       check(fah::launch_quantize(c->in.as<float>(), (int64_t)n, c->q.as<int8_t>(), c->s.as<float>(), c->stream),
             "quantize");
       launch_weight_gemm(w, c->q.as<int8_t>(), c->s.as<float>(), frames, c->out.as<float>(), dbias, c->stream);
@@ -1396,11 +1475,14 @@ int fah_quantized_linear(fah_context* h, const float* input, int frames, const f
       a.out = c->out.as<float>();
       a.out_rows = w->rows;
       a.bias = dbias;
+      meter.kernels_begin();
       check(fah::launch_gemv(a, w->half_scales, fah::kInputFloat, fah::kOutPlain, frames, c->stream), "gemv");
     }
+    meter.kernels_end();
     check(hipMemcpyAsync(output, c->out.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
     work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    meter.done(frames, w->cols, w->rows, (int64_t)frames * w->cols * w->rows);
     return FAH_OK;
   });
 }
@@ -1409,8 +1491,9 @@ int fah_quantized_linear_noalloc(fah_context* h, const float* input, int frames,
                                  const float* bias, float* output) {
   if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
   Ctx* c = h->st.get();
-  if (!w || w->f32 || frames <= 0 || w->cols > fah::gemv_max_k()) return FAH_DECLINED;
-  if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return FAH_DECLINED;
+  if (!w || w->f32 || frames <= 0 || w->cols > fah::gemv_max_k())
+    return declined(c, FAH_CALL_QUANTIZED_LINEAR_NOALLOC);
+  if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return declined(c, FAH_CALL_QUANTIZED_LINEAR_NOALLOC);
   return guarded([&] {
     require(input && output, "Q8 GPU projection needs input and output");
     require(w->ctx.get() == c, "weight belongs to another context");
@@ -1424,6 +1507,9 @@ int fah_quantized_linear_noalloc(fah_context* h, const float* input, int frames,
                                       std::to_string(kScratchBytes));
     std::lock_guard<std::mutex> lock(c->gate);
     if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    CallMeter meter(*c, FAH_CALL_QUANTIZED_LINEAR_NOALLOC);
+    meter.up = (int64_t)in_bytes + (bias ? (int64_t)w->rows * 4 : 0);
+    meter.down = (int64_t)out_bytes;
     check(hipSetDevice(c->device), "hipSetDevice");
     char* base = static_cast<char*>(scratch_ptr(c->device));
     require(base != nullptr, "no workspace for this device");
@@ -1442,6 +1528,7 @@ int fah_quantized_linear_noalloc(fah_context* h, const float* input, int frames,
     float* dout = reinterpret_cast<float*>(base + at_out);
     check(hipMemcpyAsync(din, input, in_bytes, hipMemcpyHostToDevice, c->stream), "H2D input");
     if (bias) check(hipMemcpyAsync(dbias, bias, (size_t)w->rows * 4, hipMemcpyHostToDevice, c->stream), "H2D bias");
+    meter.kernels_begin();
     if (gemm_fits(w, frames)) {
       int8_t* q = reinterpret_cast<int8_t*>(base + at_q);
       float* sc = reinterpret_cast<float*>(base + at_s);
@@ -1455,8 +1542,10 @@ int fah_quantized_linear_noalloc(fah_context* h, const float* input, int frames,
       a.bias = dbias;
       check(fah::launch_gemv(a, w->half_scales, fah::kInputFloat, fah::kOutPlain, frames, c->stream), "gemv");
     }
+    meter.kernels_end();
     check(hipMemcpyAsync(output, dout, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    meter.done(frames, w->cols, w->rows, (int64_t)frames * w->cols * w->rows);
     return FAH_OK;
   });
 }
@@ -1466,15 +1555,16 @@ int fah_linear_many(fah_context* h, const float* input, int frames, const fah_we
   if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
   Ctx* c = h->st.get();
   if (count == 0) return FAH_OK;
-  if (!weights || count < 0 || frames <= 0) return FAH_DECLINED;
+  if (!weights || count < 0 || frames <= 0) return declined(c, FAH_CALL_LINEAR_MANY);
   int cols = weights[0] ? weights[0]->cols : 0;
   int64_t total_rows = 0;
   const bool f32 = weights[0] && weights[0]->f32;
   for (int i = 0; i < count; ++i) {
-    if (!weights[i] || weights[i]->f32 != f32 || (!f32 && weights[i]->cols > fah::gemv_max_k())) return FAH_DECLINED;
+    if (!weights[i] || weights[i]->f32 != f32 || (!f32 && weights[i]->cols > fah::gemv_max_k()))
+      return declined(c, FAH_CALL_LINEAR_MANY);
     total_rows += weights[i]->rows;
   }
-  if ((int64_t)frames * cols * total_rows < c->minimum_operations) return FAH_DECLINED;
+  if ((int64_t)frames * cols * total_rows < c->minimum_operations) return declined(c, FAH_CALL_LINEAR_MANY);
   return guarded([&] {
     require(input && outputs, "grouped projection needs input and outputs");
     for (int i = 0; i < count; ++i) {
@@ -1484,9 +1574,12 @@ int fah_linear_many(fah_context* h, const float* input, int frames, const fah_we
     }
     std::lock_guard<std::mutex> lock(c->gate);
     if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    CallMeter meter(*c, FAH_CALL_LINEAR_MANY);
     check(hipSetDevice(c->device), "hipSetDevice");
     DeviceWork work(*c);
     size_t n = (size_t)frames * cols;
+    meter.up = (int64_t)n * 4;
+    meter.down = (int64_t)frames * total_rows * 4;
     c->in.ensure(n * 4);
     c->q.ensure(n);
     c->s.ensure(n / 32 * 4);
@@ -1494,6 +1587,7 @@ int fah_linear_many(fah_context* h, const float* input, int frames, const fah_we
     for (int i = 0; i < count; ++i) out_total += (size_t)frames * weights[i]->rows;
     c->out.ensure(out_total * 4);
     check(hipMemcpyAsync(c->in.ptr, input, n * 4, hipMemcpyHostToDevice, c->stream), "H2D input");
+    meter.kernels_begin();
     if (f32) {
       // FP32 group (IGroupedComputeBackend over Weight.Values): each weight
       // through the same kernel as fah_linear, so the bits equal separate calls.
@@ -1524,6 +1618,7 @@ int fah_linear_many(fah_context* h, const float* input, int frames, const fah_we
         at += (size_t)frames * weights[i]->rows;
       }
     }
+    meter.kernels_end();
     size_t at = 0;
     for (int i = 0; i < count; ++i) {
       size_t bytes = (size_t)frames * weights[i]->rows * 4;
@@ -1532,6 +1627,7 @@ int fah_linear_many(fah_context* h, const float* input, int frames, const fah_we
     }
     work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    meter.done(frames, cols, (int)total_rows, (int64_t)frames * cols * total_rows);
     return FAH_OK;
   });
 }
@@ -1539,16 +1635,19 @@ int fah_linear_many(fah_context* h, const float* input, int frames, const fah_we
 int fah_linear(fah_context* h, const float* input, int frames, const fah_weight* w, const float* bias, float* output) {
   if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
   Ctx* c = h->st.get();
-  if (!w || !w->f32 || frames <= 0) return FAH_DECLINED;
-  if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return FAH_DECLINED;
+  if (!w || !w->f32 || frames <= 0) return declined(c, FAH_CALL_LINEAR);
+  if ((int64_t)frames * w->cols * w->rows < c->minimum_operations) return declined(c, FAH_CALL_LINEAR);
   return guarded([&] {
     require(input && output, "FP32 GPU projection needs input and output");
     require(w->ctx.get() == c, "weight belongs to another context");
     std::lock_guard<std::mutex> lock(c->gate);
     if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    CallMeter meter(*c, FAH_CALL_LINEAR);
     check(hipSetDevice(c->device), "hipSetDevice");
     DeviceWork work(*c);
     const size_t in_bytes = (size_t)frames * w->cols * 4, out_bytes = (size_t)frames * w->rows * 4;
+    meter.up = (int64_t)in_bytes + (bias ? (int64_t)w->rows * 4 : 0);
+    meter.down = (int64_t)out_bytes;
     c->in.ensure(in_bytes + (bias ? (size_t)w->rows * 4 : 0));
     c->out.ensure(out_bytes);
     check(hipMemcpyAsync(c->in.ptr, input, in_bytes, hipMemcpyHostToDevice, c->stream), "H2D input");
@@ -1557,12 +1656,15 @@ int fah_linear(fah_context* h, const float* input, int frames, const fah_weight*
       dbias = reinterpret_cast<float*>(c->in.as<char>() + in_bytes);
       check(hipMemcpyAsync(dbias, bias, (size_t)w->rows * 4, hipMemcpyHostToDevice, c->stream), "H2D bias");
     }
+    meter.kernels_begin();
     check(fah::launch_f32_linear(c->in.as<float>(), w->f.as<float>(), dbias, c->out.as<float>(), frames, w->rows,
                                  w->cols, false, c->stream),
           "f32 linear");
+    meter.kernels_end();
     check(hipMemcpyAsync(output, c->out.ptr, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
     work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    meter.done(frames, w->cols, w->rows, (int64_t)frames * w->cols * w->rows);
     return FAH_OK;
   });
 }
@@ -1590,20 +1692,23 @@ int fah_relu_projection(fah_context* h, const float* input, int frames, const fa
   Ctx* c = h->st.get();
   if (!first || !second || !first->f32 || !second->f32 || frames <= 0 || first->rows != second->cols ||
       first->rows % 4 != 0)
-    return FAH_DECLINED;
+    return declined(c, FAH_CALL_RELU_PROJECTION);
   if ((int64_t)frames * first->rows * first->cols < c->minimum_operations ||
       (int64_t)frames * second->rows * second->cols < c->minimum_operations)
-    return FAH_DECLINED;
+    return declined(c, FAH_CALL_RELU_PROJECTION);
   return guarded([&] {
     require(input && output, "ReLU projection needs input and output");
     require(first->ctx.get() == c && second->ctx.get() == c, "weight belongs to another context");
     std::lock_guard<std::mutex> lock(c->gate);
     if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    CallMeter meter(*c, FAH_CALL_RELU_PROJECTION);
     check(hipSetDevice(c->device), "hipSetDevice");
     DeviceWork work(*c);
     const int H = first->rows, N = second->rows, K = first->cols;
     const size_t in_bytes = (size_t)frames * K * 4, mid_bytes = (size_t)frames * H * 4, out_bytes = (size_t)frames * N * 4;
     const size_t b1 = first_bias ? (size_t)H * 4 : 0, b2 = second_bias ? (size_t)N * 4 : 0;
+    meter.up = (int64_t)(in_bytes + b1 + b2);
+    meter.down = (int64_t)out_bytes;
     c->in.ensure(in_bytes + b1 + b2);
     c->out.ensure(mid_bytes + out_bytes);
     check(hipMemcpyAsync(c->in.ptr, input, in_bytes, hipMemcpyHostToDevice, c->stream), "H2D input");
@@ -1614,12 +1719,15 @@ int fah_relu_projection(fah_context* h, const float* input, int frames, const fa
     float* mid = c->out.as<float>();
     float* dout = reinterpret_cast<float*>(c->out.as<char>() + mid_bytes);
     // The intermediate stays on the device (IReluProjectionBackend.cs:4-16).
+    meter.kernels_begin();
     check(fah::launch_f32_linear(c->in.as<float>(), first->f.as<float>(), d1, mid, frames, H, K, true, c->stream),
           "f32 linear + ReLU");
     check(fah::launch_f32_linear(mid, second->f.as<float>(), d2, dout, frames, N, H, false, c->stream), "f32 linear");
+    meter.kernels_end();
     check(hipMemcpyAsync(output, dout, out_bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
     work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    meter.done(frames, K, N, (int64_t)frames * H * (K + N));
     return FAH_OK;
   });
 }
@@ -1628,16 +1736,19 @@ int fah_attention(fah_context* h, const float* query, const float* key, const fl
                   int heads, float* output) {
   if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
   Ctx* c = h->st.get();
-  if (!fah::f32_attention_supported(frames, width, heads)) return FAH_DECLINED;
+  if (!fah::f32_attention_supported(frames, width, heads)) return declined(c, FAH_CALL_ATTENTION);
   if (c->minimum_operations > 0 && (frames < 160 || (int64_t)frames * frames * width < c->minimum_operations))
-    return FAH_DECLINED;
+    return declined(c, FAH_CALL_ATTENTION);
   return guarded([&] {
     require(query && key && value && output, "GPU attention needs query, key, value and output");
     std::lock_guard<std::mutex> lock(c->gate);
     if (c->disposed) return fail(FAH_ERROR_DISPOSED, "context disposed");
+    CallMeter meter(*c, FAH_CALL_ATTENTION);
     check(hipSetDevice(c->device), "hipSetDevice");
     DeviceWork work(*c);
     const size_t bytes = (size_t)frames * width * 4;
+    meter.up = 3 * (int64_t)bytes;
+    meter.down = (int64_t)bytes;
     c->in.ensure(3 * bytes);
     c->out.ensure(bytes);
     float* dq = c->in.as<float>();
@@ -1646,10 +1757,13 @@ int fah_attention(fah_context* h, const float* query, const float* key, const fl
     check(hipMemcpyAsync(dq, query, bytes, hipMemcpyHostToDevice, c->stream), "H2D query");
     check(hipMemcpyAsync(dk, key, bytes, hipMemcpyHostToDevice, c->stream), "H2D key");
     check(hipMemcpyAsync(dv, value, bytes, hipMemcpyHostToDevice, c->stream), "H2D value");
+    meter.kernels_begin();
     check(fah::launch_f32_attention(dq, dk, dv, c->out.as<float>(), frames, width, heads, c->stream), "attention");
+    meter.kernels_end();
     check(hipMemcpyAsync(output, c->out.ptr, bytes, hipMemcpyDeviceToHost, c->stream), "D2H output");
     work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    meter.done(frames, width, width, 2 * (int64_t)frames * frames * width);
     return FAH_OK;
   });
 }
@@ -1680,6 +1794,22 @@ int fah_quantize_device(fah_context* h, const float* x, int64_t n, int8_t* q, fl
     check(hipSetDevice(c->device), "hipSetDevice");
     DeviceWork work(*c);
     check(fah::launch_quantize(x, n, q, scales, c->stream), "quantize");
+    return FAH_OK;
+  });
+}
+
+int fah_rms_norm_device(fah_context* h, const float* x, int rows, int width, const float* scale, float eps,
+                        float* y) {
+  if (!h) return fail(FAH_ERROR_ARGUMENT, "context is NULL");
+  Ctx* c = h->st.get();
+  return guarded([&] {
+    require(rows >= 0 && (width == 128 || (width > 0 && width % 4 == 0 && width <= 4096)),
+            "Invalid normalization dimensions");
+    require(rows == 0 || (x && scale && y), "NULL buffer");
+    std::lock_guard<std::mutex> lock(c->gate);
+    check(hipSetDevice(c->device), "hipSetDevice");
+    DeviceWork work(*c);
+    check(fah::launch_rms_norm_rows(x, rows, width, scale, eps, y, c->stream), "rms norm");
     return FAH_OK;
   });
 }

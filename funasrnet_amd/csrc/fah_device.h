@@ -183,12 +183,63 @@ __device__ __forceinline__ double block_sum_double(double v, double* scratch) {
   return total;
 }
 
+// The reference's square sum of an RMSNorm row
+// (src/FunAsrNet/TensorMath.Elementwise.cs:58-76 with mean 0): four double
+// chains j = 0..3 over x[4i + j] in index order (the lanes of its two
+// Vector128<double> accumulators), combined as (s0 + s2) + (s1 + s3), then
+// the tail one value at a time. x(k) returns value k as a float. One thread
+// does the whole sum (the rare path of rms_mean below).
+template <class Read>
+__device__ __forceinline__ double sum_sq_reference(Read x, int width) {
+  double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+  int k = 0;
+  for (; k + 4 <= width; k += 4) {
+    const double a = x(k), b = x(k + 1), c = x(k + 2), d = x(k + 3);
+    s0 = s0 + a * a;
+    s1 = s1 + b * b;
+    s2 = s2 + c * c;
+    s3 = s3 + d * d;
+  }
+  double r = (s0 + s2) + (s1 + s3);
+  for (; k < width; ++k) {
+    const double z = x(k);
+    r = r + z * z;
+  }
+  return r;
+}
+
+// The float mean (float)(S / width) of the reference's ordered square sum S,
+// from `tree`, the same squares summed in another order. The squares are
+// exact in double and nonnegative, so the reference's sum lies within
+// (width/4 + 1) u S of the exact sum and a tree of depth D within D u S
+// (u = 2^-53, recursive summation bounds). delta = (width/4 + 40) 2^-52 tree
+// is at least twice their sum for any tree depth below width/4 + 78, so when
+// tree - delta and tree + delta give the same float mean, so does S
+// (rounding is monotone). Otherwise (about one row in 10^6, or a non-finite
+// sum) the reference's sum is formed in its own order from x(k).
+template <class Read>
+__device__ __forceinline__ float rms_mean(double tree, int width, Read x) {
+  const double delta = tree * ((double)(width / 4 + 40) * 0x1p-52);
+  const float lo = (float)((tree - delta) / (double)width);
+  const float hi = (float)((tree + delta) / (double)width);
+  if (lo == hi) return lo;
+  return (float)(sum_sq_reference(x, width) / (double)width);
+}
+
 // RMSNorm inverse of src/FunAsrNet/TensorMath.Elementwise.cs:58-78 (rms):
-// 1f / sqrtf((float)(sum_sq / width) + eps). The double sum is a tree here;
-// the reference's sequential lane order only changes double rounding, which
-// reaches the float result with probability ~1e-7 per row.
-__device__ __forceinline__ float rms_inverse(double sum_sq, int width, float eps) {
-  float mean = (float)(sum_sq / (double)width);
+// 1f / MathF.Sqrt((float)(S / width) + eps) with the reference's S.
+template <class Read>
+__device__ __forceinline__ float rms_inverse(double tree, int width, float eps, Read x) {
+  return fdiv(1.0f, sqrt_rn(fadd(rms_mean(tree, width, x), eps)));
+}
+
+// RMSNorm inverse of one 128-channel head vector held by a whole wave, lane
+// c holding channels c and c + 64 (the QK-norm of the persistent step): the
+// two 64-channel wave trees added low half first; the rare reference-order
+// path reads the channels across the wave.
+__device__ __forceinline__ float head_rms_inverse(float lo, float hi, float eps) {
+  const double sq = wave_sum_double((double)lo * (double)lo) + wave_sum_double((double)hi * (double)hi);
+  const float mean = rms_mean(sq, 128, [&](int k) { return __shfl(k < 64 ? lo : hi, k & 63, kWave); });
   return fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
 }
 

@@ -104,7 +104,8 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(GemvArgs a) {
           sq += (double)xv[c].z * (double)xv[c].z + (double)xv[c].w * (double)xv[c].w;
         }
       }
-      inverse = rms_inverse(block_sum_double(sq, red_s), K, a.eps);
+      const float* row = a.x + (size_t)frame * K;
+      inverse = rms_inverse(block_sum_double(sq, red_s), K, a.eps, [&](int k) { return row[k]; });
     }
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(128) void qk_prepare_kernel(QkArgs a) {
   double sq = wave_sum_double((double)v * (double)v);
   if (c % kWave == 0) red_s[c / kWave] = sq;
   __syncthreads();
-  float inverse = rms_inverse(red_s[0] + red_s[1], hs, a.eps);
+  float inverse = rms_inverse(red_s[0] + red_s[1], hs, a.eps, [&](int k) { return src[k]; });
   y_s[c] = fmul(fmul(v, inverse), w[c]);
   __syncthreads();
   float r;
@@ -844,6 +845,56 @@ hipError_t launch_attention(const AttnArgs& a, int /*score_groups*/, hipStream_t
 
 hipError_t launch_advance(int* position, int frames, hipStream_t s) {
   advance_kernel<<<1, 64, 0, s>>>(position, frames);
+  return hipGetLastError();
+}
+
+// RMSNorm of rows with the decoder kernels' norm arithmetic (the ABI's
+// fah_rms_norm_device): width 128 as the persistent step's QK-norm (one full
+// wave, lane c holding channels c and c + 64), other widths (a multiple of 4,
+// at most 4096) as the norm prologues (256 threads holding values 4t + 1024c,
+// then the block tree). y = (x * inverse) * scale, TensorMath.Elementwise.cs:80-92.
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* x, int width, const float* scale, float eps,
+                                                            float* y) {
+  __shared__ double red_s[4];
+  const int tid = threadIdx.x;
+  const float* row = x + (size_t)blockIdx.x * width;
+  float* out = y + (size_t)blockIdx.x * width;
+  if (width == 128) {
+    if (tid >= kWave) return;
+    const float lo = row[tid], hi = row[tid + 64];
+    const float inverse = head_rms_inverse(lo, hi, eps);
+    out[tid] = fmul(fmul(lo, inverse), scale[tid]);
+    out[tid + 64] = fmul(fmul(hi, inverse), scale[tid + 64]);
+    return;
+  }
+  constexpr int kChunks = 4;
+  float4 v[kChunks];
+  double sq = 0.0;
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e = c * 1024 + 4 * tid;
+    v[c] = e < width ? *reinterpret_cast<const float4*>(row + e) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    sq += (double)v[c].x * (double)v[c].x + (double)v[c].y * (double)v[c].y;
+    sq += (double)v[c].z * (double)v[c].z + (double)v[c].w * (double)v[c].w;
+  }
+  const float inverse = rms_inverse(block_sum_double(sq, red_s), width, eps, [&](int k) { return row[k]; });
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e = c * 1024 + 4 * tid;
+    if (e < width) {
+      const float4 w = *reinterpret_cast<const float4*>(scale + e);
+      *reinterpret_cast<float4*>(out + e) =
+          make_float4(fmul(fmul(v[c].x, inverse), w.x), fmul(fmul(v[c].y, inverse), w.y),
+                      fmul(fmul(v[c].z, inverse), w.z), fmul(fmul(v[c].w, inverse), w.w));
+    }
+  }
+}
+
+hipError_t launch_rms_norm_rows(const float* x, int rows, int width, const float* scale, float eps, float* y,
+                                hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (width != 128 && (width % 4 != 0 || width > 4096)) return hipErrorInvalidValue;
+  rms_norm_rows_kernel<<<(unsigned)rows, 256, 0, s>>>(x, width, scale, eps, y);
   return hipGetLastError();
 }
 

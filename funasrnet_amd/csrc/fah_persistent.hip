@@ -344,13 +344,11 @@ __device__ __forceinline__ float tag_value(const u64* tag, int i) { return u2f((
 // QK-norm + RoPE of one 128-channel head vector across a wave
 // (QwenDecoder.cs:188-194, Rope.cs:14-55): lane c holds channels c and
 // c + 64, the rotation partners; nw the norm weights, cs the position's 64
-// cosines followed by its 64 sines. The square sum is the two 64-channel
-// wave sums added low half first. Returns the rotated (c, c + 64) pair.
+// cosines followed by its 64 sines. The norm is head_rms_inverse's (the
+// reference's float mean). Returns the rotated (c, c + 64) pair.
 __device__ __forceinline__ float2 head_norm_rope(float lo, float hi, const float* nw, const float* cs, float eps) {
   const int c = threadIdx.x & (kWave - 1);
-  const double sq = wave_sum_double((double)lo * (double)lo) + wave_sum_double((double)hi * (double)hi);
-  const float mean = (float)(sq / 128.0);
-  const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
+  const float inverse = head_rms_inverse(lo, hi, eps);
   const float nlo = fmul(fmul(lo, inverse), nw[c]), nhi = fmul(fmul(hi, inverse), nw[64 + c]);
   const float co = cs[c], sn = cs[64 + c];
   return make_float2(fadd(fmul(nlo, co), -fmul(nhi, sn)), fadd(fmul(nlo, sn), fmul(nhi, co)));
@@ -800,7 +798,7 @@ __device__ __forceinline__ void quantize_input(const u64* act, const float* norm
     double total = 0.0;
 #pragma unroll
     for (int i = 0; i < kMem / kWave; ++i) total += red[i];
-    const float mean = (float)(total / (double)K);
+    const float mean = rms_mean(total, K, [&](int k) { return tag_value(act, k); });
     inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
   }
   quantize4<K, NORM>(act, norm_w, inverse, xq, xs);
@@ -844,7 +842,7 @@ __device__ __forceinline__ void quantize_norm_chunks(const u64* act, const float
   double total = 0.0;
 #pragma unroll
   for (int i = 0; i < kMem / kWave; ++i) total += h[i].x + h[i].y;
-  const float mean = (float)(total / (double)K);
+  const float mean = rms_mean(total, K, [&](int k) { return tag_value(act, k); });
   const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
   quantize4<K, true>(act, norm_w, inverse, xq, xs);
 }

@@ -334,7 +334,7 @@ __global__ __launch_bounds__(256) void norm_quantize_rows_kernel(const float* x,
       sq += (double)v[c].x * (double)v[c].x + (double)v[c].y * (double)v[c].y;
       sq += (double)v[c].z * (double)v[c].z + (double)v[c].w * (double)v[c].w;
     }
-    const float inverse = rms_inverse(block_sum_double(sq, red_s), K, eps);
+    const float inverse = rms_inverse(block_sum_double(sq, red_s), K, eps, [&](int k) { return row[k]; });
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
       const int e = c * 1024 + 4 * tid;
@@ -434,7 +434,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
     const double sq = wave_sum_double((double)v * (double)v);
     if (lane == 0) red_s[wave] = sq;
     lds_barrier();
-    const float inverse = rms_inverse(red_s[2 * part] + red_s[2 * part + 1], hs, a.eps);
+    const float* src = raw + (part == 0 ? head * hs : a.q_width + kh * hs);
+    const float inverse =
+        rms_inverse(red_s[2 * part] + red_s[2 * part + 1], hs, a.eps, [&](int k) { return src[k]; });
     y_s[part][c] = fmul(fmul(v, inverse), nw);
     lds_barrier();
     float r;

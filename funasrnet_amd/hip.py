@@ -51,8 +51,23 @@ class DecoderConfigC(ctypes.Structure):
         ("eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("capacity", ctypes.c_int)]
 
 
+class CallStats(ctypes.Structure):
+    """fah_call_stats: one seam entry point's counters."""
+    _fields_ = [(n, ctypes.c_int64) for n in ("calls", "declined", "operations", "uploaded_bytes",
+                                               "downloaded_bytes")] + [
+        ("device_ms", ctypes.c_double), ("total_ms", ctypes.c_double)]
+
+
+# Seam entry points in fah_context_statistics order (FAH_CALL_*).
+CALL_KINDS = ("quantized_linear", "quantized_linear_noalloc", "linear_many", "linear", "relu_projection", "attention")
+CALL_OBSERVER = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_double, ctypes.c_double)
+
 # Every symbol of include/funasr_hip.h with its signature.
 SIGNATURES = {
+    "fah_context_statistics": (ctypes.c_int, [_vp, ctypes.POINTER(CallStats), ctypes.c_int]),
+    "fah_context_reset_statistics": (ctypes.c_int, [_vp]),
+    "fah_context_set_call_observer": (ctypes.c_int, [_vp, CALL_OBSERVER, _vp]),
     "fah_abi_version": (ctypes.c_int, []),
     "fah_last_error": (ctypes.c_char_p, []),
     "fah_device_count": (ctypes.c_int, []),
@@ -76,6 +91,7 @@ SIGNATURES = {
     "fah_linear_many": (ctypes.c_int, [_vp, _f32p, ctypes.c_int, ctypes.POINTER(_vp), ctypes.c_int,
                                        ctypes.POINTER(_f32p)]),
     "fah_quantize_device": (ctypes.c_int, [_vp, _vp, ctypes.c_int64, _vp, _vp]),
+    "fah_rms_norm_device": (ctypes.c_int, [_vp, _vp, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_float, _vp]),
     "fah_q8_gemv_device": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int, _vp, _vp]),
     "fah_q8_block_dots_device": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
     "fah_linear_device": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _vp, _vp, _vp]),
@@ -237,6 +253,32 @@ class HipBackend:
     def synchronize(self):
         _check(load().fah_context_synchronize(self.handle))
 
+    def statistics(self) -> dict:
+        """Per seam entry point: calls, declined, operations, uploaded and
+        downloaded bytes, device and wall milliseconds
+        (VulkanFloatBackend.Statistics() analogue)."""
+        recs = (CallStats * len(CALL_KINDS))()
+        _check(load().fah_context_statistics(self.handle, recs, len(CALL_KINDS)))
+        return {k: {f: getattr(r, f) for f, _ in CallStats._fields_} for k, r in zip(CALL_KINDS, recs)}
+
+    def reset_statistics(self):
+        _check(load().fah_context_reset_statistics(self.handle))
+
+    def set_call_observer(self, fn):
+        """fn(kind_name, frames, cols, rows, device_ms, total_ms) after every
+        seam call that ran on the device (TensorMath.LinearMeasured analogue);
+        None removes it."""
+        if fn is None:
+            self._observer = None
+            _check(load().fah_context_set_call_observer(self.handle, CALL_OBSERVER(), None))
+            return
+
+        def trampoline(_user, kind, frames, cols, rows, device_ms, total_ms):
+            fn(CALL_KINDS[kind], frames, cols, rows, device_ms, total_ms)
+
+        self._observer = CALL_OBSERVER(trampoline)  # kept alive while installed
+        _check(load().fah_context_set_call_observer(self.handle, self._observer, None))
+
     def weight(self, tensor: Q8Tensor) -> HipWeight:
         """Device weight cached by tensor identity (the reference keys its
         cache on the managed array, VulkanFloatBackend.cs:242-283)."""
@@ -330,6 +372,10 @@ class HipBackend:
     # device-pointer entry points (pointers are integers, e.g. torch data_ptr())
     def quantize_device(self, x_ptr: int, n: int, q_ptr: int, s_ptr: int):
         _check(load().fah_quantize_device(self.handle, x_ptr, n, q_ptr, s_ptr))
+
+    def rms_norm_device(self, x_ptr: int, rows: int, width: int, scale_ptr: int, eps: float, y_ptr: int):
+        """RMSNorm rows on the device (QwenDecoder.Norm's arithmetic)."""
+        _check(load().fah_rms_norm_device(self.handle, x_ptr, rows, width, scale_ptr, eps, y_ptr))
 
     def gemv_device(self, q_ptr: int, s_ptr: int, frames: int, weight: HipWeight, out_ptr: int) -> int:
         return _check(load().fah_q8_gemv_device(self.handle, q_ptr, s_ptr, frames, weight.handle, out_ptr))

@@ -80,6 +80,42 @@ int fah_context_set_minimum_operations(fah_context* context, int64_t operations)
  * (device-pointer entry points below) with the library's. */
 void* fah_context_stream(fah_context* context);
 
+/* Seam-call statistics. Replaces the counters of
+ * VulkanFloatBackend.Statistics() (src/FunAsrNet.Vulkan/VulkanFloatBackend.cs:86-118:
+ * calls per kind, uploaded/downloaded bytes, end-to-end seconds) and the
+ * per-projection timing of TensorMath.LinearMeasured
+ * (src/FunAsrNet/TensorMath.cs:37-40, invoked at TensorMath.cs:198 and
+ * TensorMath.QuantizedGroupAvx.cs:100), with the device time of each call's
+ * kernels added (HIP events on the context stream around them). */
+enum {
+  FAH_CALL_QUANTIZED_LINEAR = 0,   /* fah_quantized_linear */
+  FAH_CALL_QUANTIZED_LINEAR_NOALLOC = 1,
+  FAH_CALL_LINEAR_MANY = 2,        /* fah_linear_many, Q8_0 or FP32 group */
+  FAH_CALL_LINEAR = 3,             /* fah_linear */
+  FAH_CALL_RELU_PROJECTION = 4,    /* fah_relu_projection */
+  FAH_CALL_ATTENTION = 5,          /* fah_attention */
+  FAH_CALL_KINDS = 6
+};
+typedef struct fah_call_stats {
+  int64_t calls;             /* calls that ran on the device */
+  int64_t declined;          /* calls declined (FAH_DECLINED: the CPU path ran) */
+  int64_t operations;        /* multiply-adds of the calls that ran */
+  int64_t uploaded_bytes;    /* host -> device, inputs and biases */
+  int64_t downloaded_bytes;  /* device -> host, outputs */
+  double device_ms;          /* kernel time of the calls that ran */
+  double total_ms;           /* wall time inside those calls, copies and waits included */
+} fah_call_stats;
+/* Copies the first min(kinds, FAH_CALL_KINDS) records (index = FAH_CALL_*). */
+int fah_context_statistics(fah_context* context, fah_call_stats* out, int kinds);
+int fah_context_reset_statistics(fah_context* context);
+/* Called on the calling thread at the end of every seam call that ran on the
+ * device (kind, frames, input columns, output rows of all its weights,
+ * kernel milliseconds, wall milliseconds), before the call returns; it must
+ * not call this library on the same context. NULL removes it. */
+typedef void (*fah_call_observer)(void* user, int kind, int frames, int cols, int rows, double device_ms,
+                                  double total_ms);
+int fah_context_set_call_observer(fah_context* context, fah_call_observer observer, void* user);
+
 /* Weights ------------------------------------------------------------------ */
 
 /* Upload a Q8_0 matrix in the reference's post-load layout: `quantized` is
@@ -179,6 +215,15 @@ int fah_linear_many(fah_context* context, const float* input, int frames, const 
 
 /* TensorMath.Quantize (src/FunAsrNet/TensorMath.cs:378-412): n % 32 == 0. */
 int fah_quantize_device(fah_context* context, const float* x, int64_t n, int8_t* q, float* scales);
+
+/* RMSNorm of `rows` rows, TensorMath.Norm with rms = true
+ * (src/FunAsrNet/TensorMath.cs:537-573, TensorMath.Elementwise.cs:26-100, as
+ * QwenDecoder.Norm calls it, QwenDecoder.cs:354-360): y = (x * inverse) *
+ * scale with the reference's float mean of its ordered double square sum.
+ * Width 128 runs the decode step's QK-norm arithmetic, other widths (a
+ * multiple of 4, at most 4096) its layer-norm arithmetic. */
+int fah_rms_norm_device(fah_context* context, const float* x, int rows, int width, const float* scale, float eps,
+                        float* y);
 
 /* Q8_0 x quantised-activation GEMV/GEMM: out[frames*rows] from q[frames*cols],
  * scales[frames*cols/32] (TensorMath.QuantizedRowsAvx.cs:17-60 order). */

@@ -86,6 +86,16 @@ def _load():
         "oracle_decoder_keys": (_f32p, [ctypes.c_void_p, ctypes.c_int]),
         "oracle_decoder_values": (_f32p, [ctypes.c_void_p, ctypes.c_int]),
         "oracle_last_error": (ctypes.c_char_p, []),
+        "oracle_decoder_capture_norms": (None, [ctypes.c_void_p, _f32p, ctypes.c_int64, _f32p, ctypes.c_int64]),
+        "oracle_decoder_captured": (ctypes.c_int64, [ctypes.c_void_p, ctypes.c_int]),
+        "oracle_sum_sq_gpu_tree": (ctypes.c_double, [_f32p, ctypes.c_int]),
+        "oracle_sum_sq_reference": (ctypes.c_double, [_f32p, ctypes.c_int]),
+        "oracle_rms_mean_settled": (ctypes.c_int, [ctypes.c_double, ctypes.c_int, _f32p]),
+        "oracle_norm_order_stats": (ctypes.c_int, [_f32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                                   ctypes.c_int64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_int64)]),
+        "oracle_norm_order_find": (ctypes.c_int64, [_f32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                                    ctypes.c_uint64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                                    _f32p]),
         "oracle_float_linear_f64": (None, [_f32p, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_int, _f32p,
                                            ctypes.POINTER(ctypes.c_double)]),
         "oracle_attention_f64": (None, [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -257,6 +267,49 @@ def attention_f64(q, k, v, frames: int, width: int, heads: int) -> np.ndarray:
     return out.reshape(frames, width)
 
 
+def sum_sq_gpu_tree(x) -> float:
+    """The GPU kernels' pairwise-tree square sum of one RMSNorm row."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return lib().oracle_sum_sq_gpu_tree(_p(x, ctypes.c_float), x.size)
+
+
+def sum_sq_reference(x) -> float:
+    """The reference's four-chain square sum (TensorMath.Elementwise.cs:58-71)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return lib().oracle_sum_sq_reference(_p(x, ctypes.c_float), x.size)
+
+
+def rms_mean_settled(tree: float, width: int):
+    """(settled, mean) of the GPU's exactness test on a tree sum."""
+    m = np.zeros(1, np.float32)
+    ok = lib().oracle_rms_mean_settled(float(tree), width, _p(m, ctypes.c_float))
+    return bool(ok), m[0]
+
+
+def norm_order_stats(pool, width: int, rows: int, seed: int, rowwise: bool = False):
+    """Counts over `rows` sample rows drawn from `pool`: rows, rows whose
+    tree float mean differs from the reference's, rows the GPU test leaves to
+    the reference's order, rows it settles wrongly (must be 0). A flat pool
+    (a power-of-two number of values) is mixed into rows; a rowwise pool
+    [n, width] gives whole rows. Values get random low mantissa bits."""
+    pool = np.ascontiguousarray(pool, dtype=np.float32)
+    counts = (ctypes.c_int64 * 4)()
+    _check(lib().oracle_norm_order_stats(_p(pool, ctypes.c_float), pool.size, width, int(rowwise), rows, seed,
+                                         counts))
+    return tuple(counts)
+
+
+def norm_order_find(pool, width: int, seed: int, start: int, rows: int, want: int,
+                    rowwise: bool = False) -> np.ndarray:
+    """Sample rows (same draw as norm_order_stats) whose tree float mean
+    differs from the reference's."""
+    pool = np.ascontiguousarray(pool, dtype=np.float32)
+    out = np.zeros((want, width), np.float32)
+    n = lib().oracle_norm_order_find(_p(pool, ctypes.c_float), pool.size, width, int(rowwise), seed, start, rows,
+                                     want, _p(out, ctypes.c_float))
+    return out[:n]
+
+
 def greedy(logits) -> int:
     x = np.ascontiguousarray(logits, dtype=np.float32)
     return lib().oracle_greedy(_p(x, ctypes.c_float), x.size)
@@ -344,6 +397,22 @@ class Decoder:
         _check(lib().oracle_decoder_decode(self._handle, _p(x, ctypes.c_float), frames,
                                            None if logits is None else _p(logits, ctypes.c_float)))
         return logits
+
+    def capture_norms(self, wide_rows: int, head_rows: int):
+        """Record the input rows of the next decodes' RMSNorms (width-wide
+        and per-head), up to the given counts; returns the two arrays, filled
+        as the decodes run (see captured())."""
+        cfg = self.config
+        self._cap = (np.zeros((max(wide_rows, 1), cfg.width), np.float32),
+                     np.zeros((max(head_rows, 1), cfg.head_size), np.float32))
+        lib().oracle_decoder_capture_norms(self._handle, _p(self._cap[0], ctypes.c_float), wide_rows,
+                                           _p(self._cap[1], ctypes.c_float), head_rows)
+        return self._cap
+
+    def captured(self):
+        """(width-wide rows, head rows) recorded so far."""
+        return (self._cap[0][:lib().oracle_decoder_captured(self._handle, 0)],
+                self._cap[1][:lib().oracle_decoder_captured(self._handle, 1)])
 
     def kv(self, layer: int):
         """Copies of the cached K and V rows [position, kv_heads*head_size]."""

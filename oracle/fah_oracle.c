@@ -484,7 +484,26 @@ struct oracle_decoder {
     float** values;
     float* rope_cos; /* [capacity][head_size/2] */
     float* rope_sin;
+    /* Optional capture of RMSNorm input rows (tests only): width-wide rows
+     * (attention, ffn and output norms) and head rows (QK-norms). */
+    float* cap_wide; int64_t cap_wide_max, cap_wide_n;
+    float* cap_head; int64_t cap_head_max, cap_head_n;
 };
+
+void oracle_decoder_capture_norms(oracle_decoder* d, float* wide, int64_t wide_rows, float* heads, int64_t head_rows) {
+    d->cap_wide = wide; d->cap_wide_max = wide ? wide_rows : 0; d->cap_wide_n = 0;
+    d->cap_head = heads; d->cap_head_max = heads ? head_rows : 0; d->cap_head_n = 0;
+}
+
+int64_t oracle_decoder_captured(const oracle_decoder* d, int heads) { return heads ? d->cap_head_n : d->cap_wide_n; }
+
+static void capture_rows(float* dst, int64_t max, int64_t* n, const float* rows, int64_t count, int width) {
+    if (!dst) return;
+    if (count > max - *n) count = max - *n;
+    if (count <= 0) return;
+    memcpy(dst + *n * width, rows, sizeof(float) * (size_t)(count * width));
+    *n += count;
+}
 
 oracle_decoder* oracle_decoder_create(const oracle_model* model, int capacity) {
     if (!model || capacity < 1 || model->heads % model->kv_heads != 0) { fail("Invalid GQA head counts"); return NULL; }
@@ -563,12 +582,15 @@ int oracle_decoder_decode(oracle_decoder* d, const float* embeddings, int frames
     memcpy(x, embeddings, sizeof(float) * fw);
     for (int layer = 0; layer < m->layers; ++layer) {
         const oracle_layer* L = &m->layer[layer];
+        capture_rows(d->cap_wide, d->cap_wide_max, &d->cap_wide_n, x, frames, width);
         oracle_rms_norm(x, (int64_t)fw, width, L->attn_norm, m->eps, h);
         /* LinearMany: one shared quantisation (TensorMath.QuantizedGroupAvx.cs:105-190) */
         oracle_quantize(h, (int64_t)fw, xq, xs);
         oracle_q8_gemv_quantized(xq, xs, frames, L->wq.q, L->wq.scales, L->wq.rows, width, NULL, q);
         oracle_q8_gemv_quantized(xq, xs, frames, L->wk.q, L->wk.scales, L->wk.rows, width, NULL, k);
         oracle_q8_gemv_quantized(xq, xs, frames, L->wv.q, L->wv.scales, L->wv.rows, width, NULL, v);
+        capture_rows(d->cap_head, d->cap_head_max, &d->cap_head_n, q, (int64_t)frames * m->heads, hs);
+        capture_rows(d->cap_head, d->cap_head_max, &d->cap_head_n, k, (int64_t)frames * m->kv_heads, hs);
         oracle_rms_norm(q, (int64_t)frames * q_width, hs, L->q_norm, m->eps, qn);
         oracle_rms_norm(k, (int64_t)frames * kv_width, hs, L->k_norm, m->eps, kn);
         for (int t = 0; t < frames; ++t) {
@@ -582,6 +604,7 @@ int oracle_decoder_decode(oracle_decoder* d, const float* embeddings, int frames
         oracle_attention(qn, d->keys[layer], d->values[layer], frames, d->position, m->heads, m->kv_heads, hs, attn);
         linear(&L->wo, attn, frames, a);
         oracle_add(a, x, (int64_t)fw);
+        capture_rows(d->cap_wide, d->cap_wide_max, &d->cap_wide_n, a, frames, width);
         oracle_rms_norm(a, (int64_t)fw, width, L->ffn_norm, m->eps, h);
         oracle_quantize(h, (int64_t)fw, xq, xs);
         oracle_q8_gemv_quantized(xq, xs, frames, L->gate.q, L->gate.scales, L->gate.rows, width, NULL, gate);
@@ -593,6 +616,7 @@ int oracle_decoder_decode(oracle_decoder* d, const float* embeddings, int frames
     d->position += frames;
     if (logits) {
         float* last = x + (size_t)(frames - 1) * width;
+        capture_rows(d->cap_wide, d->cap_wide_max, &d->cap_wide_n, last, 1, width);
         oracle_rms_norm(last, width, width, m->output_norm, m->eps, h);
         const oracle_q8* out = m->output.q ? &m->output : &m->token_embd;
         linear(out, h, 1, logits);
@@ -600,4 +624,159 @@ int oracle_decoder_decode(oracle_decoder* d, const float* embeddings, int frames
     free(x); free(h); free(a); free(q); free(qn); free(k); free(kn); free(v);
     free(attn); free(gate); free(up); free(xq); free(xs);
     return 0;
+}
+
+
+/* ---- RMSNorm square-sum order (tests only) ---------------------------------
+ *
+ * The reference sums an RMSNorm row's squares in double in four chains
+ * (TensorMath.Elementwise.cs:58-71, restated in oracle_rms_norm). The GPU
+ * kernels sum them as pairwise trees and use the tree's float mean only when
+ * its error bound cannot reach a float rounding boundary (rms_mean in
+ * fah_device.h), otherwise the reference's chains. These functions restate
+ * both and count how often the orders' float means differ. */
+
+static double pair_tree(const double* v, int n) {
+    if (n == 1) return v[0];
+    return pair_tree(v, n / 2) + pair_tree(v + n / 2, n / 2);
+}
+
+/* The GPU kernels' square sum of one row. Width 128 (QK-norm): 64-lane wave
+ * trees over channels 0-63 and 64-127, the low one first. Other widths (a
+ * multiple of 4, at most 4096; the 1024-wide layer norms): 256 threads, thread
+ * t holding values 4t + 1024c and summing ((0 + (a^2 + b^2)) + (c^2 + d^2)) per
+ * chunk c in order; a pairwise tree over each 64-lane wave (DPP steps within
+ * rows of 16 lanes, then (r0 + r16) + (r32 + r48)); the four wave sums added
+ * in order from 0. */
+double oracle_sum_sq_gpu_tree(const float* x, int width) {
+    double lane[256];
+    if (width == 128) {
+        for (int c = 0; c < 128; ++c) lane[c] = (double)x[c] * (double)x[c];
+        return pair_tree(lane, 64) + pair_tree(lane + 64, 64);
+    }
+    for (int t = 0; t < 256; ++t) {
+        double sq = 0.0;
+        for (int c = 0; c < 4; ++c) {
+            const int e = c * 1024 + 4 * t;
+            if (e >= width) continue;
+            const double a = x[e], b = x[e + 1], cc = x[e + 2], dd = x[e + 3];
+            sq = sq + (a * a + b * b);
+            sq = sq + (cc * cc + dd * dd);
+        }
+        lane[t] = sq;
+    }
+    double total = 0.0;
+    for (int w = 0; w < 4; ++w) total = total + pair_tree(lane + 64 * w, 64);
+    return total;
+}
+
+/* The reference's square sum (oracle_rms_norm's chains). */
+double oracle_sum_sq_reference(const float* x, int width) {
+    double s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+    int k = 0;
+    for (; k <= width - 4; k += 4) {
+        double a = x[k], b = x[k + 1], c = x[k + 2], dd = x[k + 3];
+        s0 = s0 + a * a;
+        s1 = s1 + b * b;
+        s2 = s2 + c * c;
+        s3 = s3 + dd * dd;
+    }
+    double r = (s0 + s2) + (s1 + s3);
+    for (; k < width; ++k) r = r + (double)x[k] * (double)x[k];
+    return r;
+}
+
+/* rms_mean's test (fah_device.h): 1 and the mean when tree -/+ delta give the
+ * same float mean, else 0. */
+int oracle_rms_mean_settled(double tree, int width, float* mean) {
+    const double delta = tree * ((double)(width / 4 + 40) * 0x1p-52);
+    const float lo = (float)((tree - delta) / (double)width);
+    const float hi = (float)((tree + delta) / (double)width);
+    *mean = lo;
+    return lo == hi;
+}
+
+static uint64_t splitmix(uint64_t* s) {
+    uint64_t z = (*s += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+/* Row r of a sample. Mixed (pool_n a power of two): values of `pool` from a
+ * random start with a random odd stride. Rowwise (pool holds whole rows,
+ * pool_n a multiple of width): one of the pool's rows at random. Either way
+ * each value gets a random sign and its three low mantissa bits replaced at
+ * random (new rounding cases, same magnitudes and, rowwise, the same
+ * per-channel structure). */
+static void sample_row(const float* pool, int64_t pool_n, int width, int rowwise, uint64_t seed, int64_t r,
+                       float* row) {
+    uint64_t st = seed ^ ((uint64_t)r * 0x2545f4914f6cdd1dull);
+    const uint64_t mask = (uint64_t)pool_n - 1;
+    uint64_t base = splitmix(&st), stride = splitmix(&st) | 1u;
+    if (rowwise) {
+        base = (base % (uint64_t)(pool_n / width)) * (uint64_t)width;
+        stride = 1;
+    }
+    uint64_t bits = 0;
+    for (int k = 0; k < width; ++k) {
+        if ((k & 7) == 0) bits = splitmix(&st);
+        const uint64_t at = base + (uint64_t)k * stride;
+        float v = pool[rowwise ? at : (at & mask)];
+        uint32_t u;
+        memcpy(&u, &v, 4);
+        const uint32_t b = (uint32_t)(bits >> (8 * (k & 7)));
+        if (u & 0x7f800000u) u = (u & ~7u) | (b & 7u);
+        u ^= (b & 8u) << 28;
+        memcpy(&v, &u, 4);
+        row[k] = v;
+    }
+}
+
+/* counts[0] rows, [1] rows whose GPU-tree float mean differs from the
+ * reference's, [2] rows rms_mean does not settle from the tree (it then forms
+ * the reference's sum), [3] rows it settles to a mean that differs from the
+ * reference's (must stay 0). */
+int oracle_norm_order_stats(const float* pool, int64_t pool_n, int width, int rowwise, int64_t rows, uint64_t seed,
+                            int64_t* counts) {
+    if (pool_n <= 0 || width < 4 || width > 4096 || width % 4) return fail("bad sample");
+    if (rowwise ? pool_n % width != 0 : (pool_n & (pool_n - 1)) != 0) return fail("bad sample pool");
+    int64_t differ = 0, unsettled = 0, wrong = 0;
+#pragma omp parallel reduction(+ : differ, unsettled, wrong)
+    {
+        float* row = (float*)malloc(sizeof(float) * (size_t)width);
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            sample_row(pool, pool_n, width, rowwise, seed, r, row);
+            const double tree = oracle_sum_sq_gpu_tree(row, width);
+            const float ref = (float)(oracle_sum_sq_reference(row, width) / (double)width);
+            const float plain = (float)(tree / (double)width);
+            float settled;
+            differ += plain != ref;
+            if (oracle_rms_mean_settled(tree, width, &settled)) wrong += settled != ref;
+            else ++unsettled;
+        }
+        free(row);
+    }
+    counts[0] = rows;
+    counts[1] = differ;
+    counts[2] = unsettled;
+    counts[3] = wrong;
+    return 0;
+}
+
+/* Up to `want` sample rows (from row `start` on) whose GPU-tree float mean
+ * differs from the reference's, into out [want][width]; returns how many. */
+int64_t oracle_norm_order_find(const float* pool, int64_t pool_n, int width, int rowwise, uint64_t seed,
+                               int64_t start, int64_t rows, int64_t want, float* out) {
+    int64_t found = 0;
+    float* row = (float*)malloc(sizeof(float) * (size_t)width);
+    for (int64_t r = start; r < start + rows && found < want; ++r) {
+        sample_row(pool, pool_n, width, rowwise, seed, r, row);
+        const float plain = (float)(oracle_sum_sq_gpu_tree(row, width) / (double)width);
+        const float ref = (float)(oracle_sum_sq_reference(row, width) / (double)width);
+        if (plain != ref) memcpy(out + found++ * width, row, sizeof(float) * (size_t)width);
+    }
+    free(row);
+    return found;
 }

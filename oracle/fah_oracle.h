@@ -20,7 +20,12 @@
  *   oracle_half_to_float       pinned: exhaustive 65536 patterns vs numpy
  *   oracle_rotate_half         pinned: scalar rotation restated in numpy
  *   oracle_greedy              pinned: numpy first-max scan incl. NaN/inf/-0
- *   oracle_rms_norm            pinned: double reference at 1e-5 (tolerance)
+ *   oracle_rms_norm            pinned bit for bit: the four chains restated
+ *                              with numpy's sequential sums, then the float
+ *                              steps in numpy float32; and a double reference
+ *                              at 1e-5 (tests/test_oracle_norm_order.py)
+ *   oracle_sum_sq_gpu_tree     pinned: an independent numpy pairwise tree
+ *   oracle_norm_order_*        counts built on the two sums above
  *   oracle_exp                 pinned: follows ExpAvx.cs (reference's own x64
  *                              exp on .NET 11); vs double exp <= 1 ulp. The
  *                              .NET 10 runtime Vector256.Exp is not in the
@@ -132,9 +137,23 @@ int oracle_decoder_set_position(oracle_decoder* d, int position);
 int oracle_decoder_decode(oracle_decoder* d, const float* embeddings, int frames, float* logits);
 int oracle_decoder_embed(const oracle_decoder* d, const int32_t* tokens, int count, float* out);
 /* Cached K/V rows (fp32 holding F16-rounded values), [capacity][kv_heads*head_size]. */
+/* Tests only: copy the input rows of the width-wide RMSNorms (attention,
+ * ffn, output) and of the QK-norms (per head) of the next decodes, up to the
+ * given row counts; oracle_decoder_captured reports how many were taken. */
+void oracle_decoder_capture_norms(oracle_decoder* d, float* wide, int64_t wide_rows, float* heads, int64_t head_rows);
+int64_t oracle_decoder_captured(const oracle_decoder* d, int heads);
 float* oracle_decoder_keys(oracle_decoder* d, int layer);
 float* oracle_decoder_values(oracle_decoder* d, int layer);
 const char* oracle_last_error(void);
+
+/* --- RMSNorm square-sum order (tests only) ----------------------------- */
+double oracle_sum_sq_gpu_tree(const float* x, int width);
+double oracle_sum_sq_reference(const float* x, int width);
+int oracle_rms_mean_settled(double tree, int width, float* mean);
+int oracle_norm_order_stats(const float* pool, int64_t pool_n, int width, int rowwise, int64_t rows, uint64_t seed,
+                            int64_t* counts);
+int64_t oracle_norm_order_find(const float* pool, int64_t pool_n, int width, int rowwise, uint64_t seed,
+                               int64_t start, int64_t rows, int64_t want, float* out);
 
 #ifdef __cplusplus
 }
