@@ -45,7 +45,8 @@ def test_linear_and_group(backend, oracle_lib, frames, width):
 
 def test_linear_bias_and_decoder_gemv_shapes(backend, oracle_lib):
     rng = np.random.default_rng(7)
-    for frames, cols, rows in [(1, 1024, 2048), (1, 3072, 1024), (2, 1024, 6144), (64, 560, 1536), (150, 512, 2048)]:
+    for frames, cols, rows in [(1, 1024, 2048), (1, 3072, 1024), (2, 1024, 6144), (64, 560, 1536), (150, 512, 2048),
+                               (1000, 512, 1536), (1000, 2048, 512), (257, 516, 100), (5, 36, 70)]:
         x = rng.standard_normal((frames, cols)).astype(np.float32)
         w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
         b = rng.standard_normal(rows).astype(np.float32)
@@ -90,7 +91,8 @@ def test_relu_projection_declines(backend):
 
 @pytest.mark.parametrize("frames,width,heads", [(1, 7, 1), (2, 7, 1), (3, 256, 1), (17, 96, 3), (100, 512, 4),
                                                 (129, 1024, 8), (400, 512, 4), (257, 256, 1), (1024, 16, 2),
-                                                (1025, 16, 2), (4096, 8, 1)])
+                                                (1025, 16, 2), (4096, 8, 1), (1, 128, 1), (33, 512, 8),
+                                                (300, 256, 4), (1000, 512, 4)])
 def test_attention(backend, oracle_lib, frames, width, heads):
     rng = np.random.default_rng(170719 + frames + width)
     q = (rng.random((frames, width)) * 2 - 1).astype(np.float32)
