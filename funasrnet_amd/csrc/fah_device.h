@@ -212,35 +212,74 @@ __device__ __forceinline__ double sum_sq_reference(Read x, int width) {
 // from `tree`, the same squares summed in another order. The squares are
 // exact in double and nonnegative, so the reference's sum lies within
 // (width/4 + 1) u S of the exact sum and a tree of depth D within D u S
-// (u = 2^-53, recursive summation bounds). delta = (width/4 + 40) 2^-52 tree
-// is at least twice their sum for any tree depth below width/4 + 78, so when
-// tree - delta and tree + delta give the same float mean, so does S
-// (rounding is monotone). Otherwise (about one row in 10^6, or a non-finite
-// sum) the reference's sum is formed in its own order from x(k).
-template <class Read>
-__device__ __forceinline__ float rms_mean(double tree, int width, Read x) {
-  const double delta = tree * ((double)(width / 4 + 40) * 0x1p-52);
-  const float lo = (float)((tree - delta) / (double)width);
-  const float hi = (float)((tree + delta) / (double)width);
-  if (lo == hi) return lo;
-  return (float)(sum_sq_reference(x, width) / (double)width);
+// (u = 2^-53, recursive summation bounds): for any tree depth below
+// width/4 + 78 the two means differ by less than 2 (width/4 + 40) ulps of the
+// double mean m = tree / width (plus half an ulp where the division rounds).
+// Rounding to float only changes at the midpoints between floats, where the
+// 29 bits of m below the float mantissa read 2^28. When m is further than
+// that margin from a midpoint and at least 2^-126 (a normal float), S rounds
+// to the same float as m. Otherwise (about one row in 10^6, an all-zero row,
+// or a sum below 2^-126) the reference's sum is formed in its own order.
+// Infinite and NaN sums are infinite and NaN in any order.
+__device__ __forceinline__ bool rms_mean_unsettled(double m, int width) {
+  const uint64_t bits = (uint64_t)__double_as_longlong(m);
+  const uint32_t low = (uint32_t)bits & 0x1fffffffu, high = (uint32_t)(bits >> 32);
+  const uint32_t margin = 2u * (uint32_t)(width / 4 + 40) + 2u;
+  return low + margin - (1u << 28) <= 2u * margin || high < (897u << 20);
 }
 
-// RMSNorm inverse of src/FunAsrNet/TensorMath.Elementwise.cs:58-78 (rms):
-// 1f / MathF.Sqrt((float)(S / width) + eps) with the reference's S.
+// RMSNorm inverse of src/FunAsrNet/TensorMath.Elementwise.cs:58-78 (rms),
+// 1f / MathF.Sqrt((float)(S / width) + eps), from the tree's sum, and
+// whether the reference's S might give another one (rms_mean_unsettled).
+// Latency-bound callers use the inverse at once and redo their step with
+// rms_inverse_reference in the rare case, testing the flag afterwards, so
+// that no branch sits between the sum and the loads that follow it.
+struct RmsGuess {
+  float inverse;
+  bool unsettled;
+};
+__device__ __forceinline__ RmsGuess rms_inverse_guess(double tree, int width, float eps) {
+  const double m = tree / (double)width;
+  return RmsGuess{fdiv(1.0f, sqrt_rn(fadd((float)m, eps))), rms_mean_unsettled(m, width)};
+}
+template <class Read>
+__device__ __forceinline__ float rms_inverse_reference(int width, float eps, Read x) {
+  return fdiv(1.0f, sqrt_rn(fadd((float)(sum_sq_reference(x, width) / (double)width), eps)));
+}
+// A wave-uniform flag (every lane holds the same `tree`): one scalar test.
+__device__ __forceinline__ bool wave_any(bool flag) { return __builtin_amdgcn_ballot_w64(flag) != 0; }
+
+// The reference's inverse directly (x(k) returns value k of the row).
 template <class Read>
 __device__ __forceinline__ float rms_inverse(double tree, int width, float eps, Read x) {
-  return fdiv(1.0f, sqrt_rn(fadd(rms_mean(tree, width, x), eps)));
+  const RmsGuess g = rms_inverse_guess(tree, width, eps);
+  if (__builtin_expect(wave_any(g.unsettled), 0)) return rms_inverse_reference(width, eps, x);
+  return g.inverse;
 }
 
-// RMSNorm inverse of one 128-channel head vector held by a whole wave, lane
-// c holding channels c and c + 64 (the QK-norm of the persistent step): the
-// two 64-channel wave trees added low half first; the rare reference-order
-// path reads the channels across the wave.
-__device__ __forceinline__ float head_rms_inverse(float lo, float hi, float eps) {
+// QK-norm (+ RoPE) of one 128-channel head vector held by a whole wave
+// (QwenDecoder.cs:188-194, Rope.cs:14-55): lane c holds channels c and
+// c + 64, the rotation partners; nw the norm weights, cs the position's 64
+// cosines followed by its 64 sines (unused without ROPE). The square sum is
+// the two 64-channel wave trees added low half first; the rare
+// reference-order path reads the channels across the wave and redoes the
+// step. Returns the (c, c + 64) pair, rotated with ROPE.
+template <bool ROPE>
+__device__ __forceinline__ float2 head_norm_rope(float lo, float hi, const float* nw, const float* cs, float eps) {
+  const int c = threadIdx.x & (kWave - 1);
   const double sq = wave_sum_double((double)lo * (double)lo) + wave_sum_double((double)hi * (double)hi);
-  const float mean = rms_mean(sq, 128, [&](int k) { return __shfl(k < 64 ? lo : hi, k & 63, kWave); });
-  return fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
+  const RmsGuess g = rms_inverse_guess(sq, 128, eps);
+  const float w0 = nw[c], w1 = nw[64 + c];
+  const float co = ROPE ? cs[c] : 1.0f, sn = ROPE ? cs[64 + c] : 0.0f;
+  auto step = [&](float inverse) {
+    const float nlo = fmul(fmul(lo, inverse), w0), nhi = fmul(fmul(hi, inverse), w1);
+    if (!ROPE) return make_float2(nlo, nhi);
+    return make_float2(fadd(fmul(nlo, co), -fmul(nhi, sn)), fadd(fmul(nlo, sn), fmul(nhi, co)));
+  };
+  float2 r = step(g.inverse);
+  if (__builtin_expect(wave_any(g.unsettled), 0))
+    r = step(rms_inverse_reference(128, eps, [&](int k) { return __shfl(k < 64 ? lo : hi, k & 63, kWave); }));
+  return r;
 }
 
 // Quantise four consecutive values held by this lane; the 32-value block is

@@ -861,10 +861,9 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* x, int 
   float* out = y + (size_t)blockIdx.x * width;
   if (width == 128) {
     if (tid >= kWave) return;
-    const float lo = row[tid], hi = row[tid + 64];
-    const float inverse = head_rms_inverse(lo, hi, eps);
-    out[tid] = fmul(fmul(lo, inverse), scale[tid]);
-    out[tid + 64] = fmul(fmul(hi, inverse), scale[tid + 64]);
+    const float2 r = head_norm_rope<false>(row[tid], row[tid + 64], scale, nullptr, eps);
+    out[tid] = r.x;
+    out[tid + 64] = r.y;
     return;
   }
   constexpr int kChunks = 4;

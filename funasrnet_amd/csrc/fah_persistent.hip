@@ -341,19 +341,6 @@ __device__ __forceinline__ bool gather1(const u64* src, int count, uint32_t gen,
 __device__ __forceinline__ float tag_value(const u64* tag, int i) { return u2f((uint32_t)tag[i]); }
 
 
-// QK-norm + RoPE of one 128-channel head vector across a wave
-// (QwenDecoder.cs:188-194, Rope.cs:14-55): lane c holds channels c and
-// c + 64, the rotation partners; nw the norm weights, cs the position's 64
-// cosines followed by its 64 sines. The norm is head_rms_inverse's (the
-// reference's float mean). Returns the rotated (c, c + 64) pair.
-__device__ __forceinline__ float2 head_norm_rope(float lo, float hi, const float* nw, const float* cs, float eps) {
-  const int c = threadIdx.x & (kWave - 1);
-  const float inverse = head_rms_inverse(lo, hi, eps);
-  const float nlo = fmul(fmul(lo, inverse), nw[c]), nhi = fmul(fmul(hi, inverse), nw[64 + c]);
-  const float co = cs[c], sn = cs[64 + c];
-  return make_float2(fadd(fmul(nlo, co), -fmul(nhi, sn)), fadd(fmul(nlo, sn), fmul(nhi, co)));
-}
-
 // Part of the time-ordered value sum of channel c = 2 * lane + HI: acc =
 // acc + p[t] * v[t][c] in order (the reference's value loop) over
 // positions [t0, t0 + count), whose V rows sit at 256 B per position from
@@ -783,6 +770,7 @@ __device__ __forceinline__ void quantize_input(const u64* act, const float* norm
                                                double* red) {
   const int tid = threadIdx.x;
   float inverse = 1.0f;
+  bool unsettled = false;
   if constexpr (NORM) {
     static_assert(K <= 4 * kMem, "one norm group");
     if (tid < kMem) {
@@ -798,10 +786,16 @@ __device__ __forceinline__ void quantize_input(const u64* act, const float* norm
     double total = 0.0;
 #pragma unroll
     for (int i = 0; i < kMem / kWave; ++i) total += red[i];
-    const float mean = rms_mean(total, K, [&](int k) { return tag_value(act, k); });
-    inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
+    const RmsGuess g = rms_inverse_guess(total, K, eps);
+    inverse = g.inverse;
+    unsettled = g.unsettled;
   }
   quantize4<K, NORM>(act, norm_w, inverse, xq, xs);
+  // (Rare) the reference's own square sum decides the inverse: the same
+  // threads quantise the same values again with it.
+  if constexpr (NORM)
+    if (__builtin_expect(wave_any(unsettled), 0))
+      quantize4<K, true>(act, norm_w, rms_inverse_reference(K, eps, [&](int k) { return tag_value(act, k); }), xq, xs);
 }
 
 }  // namespace
@@ -842,9 +836,12 @@ __device__ __forceinline__ void quantize_norm_chunks(const u64* act, const float
   double total = 0.0;
 #pragma unroll
   for (int i = 0; i < kMem / kWave; ++i) total += h[i].x + h[i].y;
-  const float mean = rms_mean(total, K, [&](int k) { return tag_value(act, k); });
-  const float inverse = fdiv(1.0f, sqrt_rn(fadd(mean, eps)));
-  quantize4<K, true>(act, norm_w, inverse, xq, xs);
+  const RmsGuess g = rms_inverse_guess(total, K, eps);
+  quantize4<K, true>(act, norm_w, g.inverse, xq, xs);
+  // (Rare) the reference's own square sum decides: the same threads
+  // quantise the same values again.
+  if (__builtin_expect(wave_any(g.unsettled), 0))
+    quantize4<K, true>(act, norm_w, rms_inverse_reference(K, eps, [&](int k) { return tag_value(act, k); }), xq, xs);
 }
 
 // Shape-specialised: W hidden width, HQ/HKV query/kv heads (head size 128),
@@ -1061,7 +1058,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       char* kcur = reinterpret_cast<char*>(norm_s + 512);
       if (wave < 2) {
         const int c = lane, half = HS / 2;
-        const float2 r = head_norm_rope(tag_value(tag_s, wave * HS + c), tag_value(tag_s, wave * HS + half + c),
+        const float2 r = head_norm_rope<true>(tag_value(tag_s, wave * HS + c), tag_value(tag_s, wave * HS + half + c),
                                         norm_s + wave * HS, norm_s + 2 * HS, a.eps);
         const float rlo = r.x, rhi = r.y;
         if (wave == 0) {
@@ -1454,7 +1451,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (lane == 0) okw_s[wave] = ok ? 1 : 0;
       if (!gathered()) return false;
       if (wave < G) {
-        const float2 qn = head_norm_rope(tag_value(tag_s, wave * HS + lane), tag_value(tag_s, wave * HS + HS / 2 + lane),
+        const float2 qn = head_norm_rope<true>(tag_value(tag_s, wave * HS + lane), tag_value(tag_s, wave * HS + HS / 2 + lane),
                                          norm_s, norm_s + 2 * HS, a.eps);
         cur_s[wave][lane] = qn.x;
         cur_s[wave][HS / 2 + lane] = qn.y;

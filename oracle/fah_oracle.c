@@ -686,14 +686,18 @@ double oracle_sum_sq_reference(const float* x, int width) {
     return r;
 }
 
-/* rms_mean's test (fah_device.h): 1 and the mean when tree -/+ delta give the
- * same float mean, else 0. */
+/* rms_inverse's test (rms_mean_unsettled, fah_device.h): 1 and the mean
+ * when the double mean m = tree / width lies more than 2 (width/4 + 40) + 2
+ * ulps from a float rounding midpoint (its 29 bits below the float mantissa
+ * against 2^28) and is at least 2^-126, else 0. */
 int oracle_rms_mean_settled(double tree, int width, float* mean) {
-    const double delta = tree * ((double)(width / 4 + 40) * 0x1p-52);
-    const float lo = (float)((tree - delta) / (double)width);
-    const float hi = (float)((tree + delta) / (double)width);
-    *mean = lo;
-    return lo == hi;
+    const double m = tree / (double)width;
+    uint64_t bits;
+    memcpy(&bits, &m, 8);
+    const uint32_t low = (uint32_t)bits & 0x1fffffffu, high = (uint32_t)(bits >> 32);
+    const uint32_t margin = 2u * (uint32_t)(width / 4 + 40) + 2u;
+    *mean = (float)m;
+    return !(low + margin - (1u << 28) <= 2u * margin || high < (897u << 20));
 }
 
 static uint64_t splitmix(uint64_t* s) {

@@ -98,10 +98,16 @@ def test_crafted_rows_differ_and_are_left_to_the_reference_order(oracle_lib):
         settled, _ = oracle_lib.rms_mean_settled(oracle_lib.sum_sq_gpu_tree(norm_rows.midpoint(width)), width)
         assert not settled
         for special in (np.inf, np.nan):
+            # Infinite and NaN sums are such in any order: settled, same mean.
             x = np.ones(width, f32)
             x[3] = special
-            assert not oracle_lib.rms_mean_settled(oracle_lib.sum_sq_gpu_tree(x), width)[0]
-        assert oracle_lib.rms_mean_settled(0.0, width) == (True, f32(0))
+            settled, mean = oracle_lib.rms_mean_settled(oracle_lib.sum_sq_gpu_tree(x), width)
+            ref = f32(oracle_lib.sum_sq_reference(x) / width)
+            assert settled and (mean == ref or (np.isnan(mean) and np.isnan(ref)))
+        tiny = np.zeros(width, f32)
+        tiny[0] = f32(1e-40)  # square sum below 2^-126: the reference path
+        assert not oracle_lib.rms_mean_settled(oracle_lib.sum_sq_gpu_tree(tiny), width)[0]
+        assert not oracle_lib.rms_mean_settled(0.0, width)[0]  # all-zero rows take the reference path
 
 
 @pytest.fixture(scope="module")
