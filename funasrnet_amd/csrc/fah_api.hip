@@ -164,6 +164,7 @@ struct SessionBatch {
   std::vector<fah_decoder*> members;
   int max_positions = 0;
   DeviceBuffer table, x, a, qkv, q, h, xq, xs, logits, keys;
+  DeviceBuffer tokens;  // the step batcher's gathered tokens, one per session
   std::vector<fah::SessionRef> host_table;  // source of the last table upload (alive until the next)
   hipGraphExec_t graph = nullptr;
   SessionBatch() = default;
@@ -1126,11 +1127,13 @@ void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s)
 // Session references of `sessions` into b.table, ordered on the stream; the
 // captured step reads the table when it runs, so a batch's graph serves any
 // sessions of its size.
+// The device table of the sessions' buffers, uploaded only when it differs
+// from the last upload (a recurring batch keeps its table).
 void upload_session_table(SessionBatch& b, fah_decoder* const* sessions, int count, hipStream_t s) {
-  b.host_table.assign(count, fah::SessionRef{});
+  std::vector<fah::SessionRef> table(count, fah::SessionRef{});
   for (int i = 0; i < count; ++i) {
     const fah_decoder* d = sessions[i];
-    fah::SessionRef& r = b.host_table[i];
+    fah::SessionRef& r = table[i];
     r.kcache = d->kcache.as<_Float16>();
     r.vcache = d->vcache.as<_Float16>();
     r.rope_cos = d->rope_cos.as<float>();
@@ -1141,6 +1144,10 @@ void upload_session_table(SessionBatch& b, fah_decoder* const* sessions, int cou
     r.history_count = d->history_count.as<int>();
     r.capacity = d->cfg.capacity;
   }
+  if (b.host_table.size() == table.size() &&
+      std::memcmp(b.host_table.data(), table.data(), table.size() * sizeof(fah::SessionRef)) == 0)
+    return;
+  b.host_table = std::move(table);
   check(hipMemcpyAsync(b.table.ptr, b.host_table.data(), (size_t)count * sizeof(fah::SessionRef),
                        hipMemcpyHostToDevice, s),
         "H2D session table");
@@ -2376,6 +2383,11 @@ void run_batch(fah_batcher* b, const std::vector<BatchRequest*>& reqs) {
     else ok.push_back(r);
   }
   if (ok.empty()) return;
+  // A stable order (by session) keeps the table of a recurring batch the
+  // same, so it is uploaded only when the members change.
+  std::sort(ok.begin(), ok.end(), [](const BatchRequest* x, const BatchRequest* y) {
+    return std::less<const fah_decoder*>()(x->session, y->session);
+  });
   std::vector<fah_decoder*> sessions;
   for (BatchRequest* r : ok) sessions.push_back(r->session);
   const int count = (int)sessions.size();
@@ -2392,11 +2404,13 @@ void run_batch(fah_batcher* b, const std::vector<BatchRequest*>& reqs) {
       auto& batch = b->by_size[count];
       if (!batch) batch = make_session_batch(sessions[0], count, b->max_positions, s);
       upload_session_table(*batch, sessions.data(), count, s);
-      for (fah_decoder* d : sessions) check(hipMemsetAsync(d->history_count.ptr, 0, 4, s), "reset history");
+      const fah::SessionRef* table = batch->table.as<fah::SessionRef>();
+      batch->tokens.ensure((size_t)fah::kFewFrames * 4);
+      check(fah::launch_session_batch_io(table, count, nullptr, s), "reset histories");
       if (batch->graph) check(hipGraphLaunch(batch->graph, s), "hipGraphLaunch");
       else enqueue_sessions_step(sessions[0], *batch, s);
-      for (int i = 0; i < count; ++i)
-        check(hipMemcpyAsync(&tokens[i], sessions[i]->history.ptr, 4, hipMemcpyDeviceToHost, s), "D2H token");
+      check(fah::launch_session_batch_io(table, count, batch->tokens.as<int>(), s), "gather tokens");
+      check(hipMemcpyAsync(tokens.data(), batch->tokens.ptr, (size_t)count * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
     }
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
     for (fah_decoder* d : sessions) d->host_position += 1;

@@ -287,6 +287,7 @@ hipError_t prepare_attention(int capacity, int head_size);
 hipError_t launch_attention(const AttnArgs& a, int score_groups, hipStream_t s);
 hipError_t launch_advance(int* position, int frames, hipStream_t s);
 hipError_t launch_quantize(const float* x, int64_t n, int8_t* q, float* scales, hipStream_t s);
+hipError_t launch_session_batch_io(const SessionRef* sessions, int count, int* out, hipStream_t s);
 hipError_t launch_rms_norm_rows(const float* x, int rows, int width, const float* scale, float eps, float* y,
                                 hipStream_t s);
 hipError_t launch_block_dots(const int8_t* x, const int8_t* w, int rows, int K, int* dots, hipStream_t s);

@@ -642,6 +642,17 @@ __global__ __launch_bounds__(kThreads) void session_embed_kernel(const int8_t* q
   }
 }
 
+// Step-batcher bookkeeping around one lock-step step of the table's
+// sessions: before it (out == nullptr) every history count is cleared; after
+// it, each session's emitted token (its history's first entry) is gathered
+// into out[i], so that one copy brings the batch's tokens back.
+__global__ __launch_bounds__(64) void session_batch_io_kernel(const SessionRef* sessions, int count, int* out) {
+  const int i = threadIdx.x;
+  if (i >= count) return;
+  if (out) out[i] = sessions[i].history[0];
+  else *sessions[i].history_count = 0;
+}
+
 // One GGUF Q8_0 block per thread (TensorMath.Q8Model.cs:15-39 without the
 // fp32 widening: the device keeps the fp16 scale bits): 17 aligned 16-bit
 // reads (blocks start at even offsets), 8 words of codes and the scale out.
@@ -894,6 +905,12 @@ hipError_t launch_rms_norm_rows(const float* x, int rows, int width, const float
   if (rows <= 0) return hipSuccess;
   if (width != 128 && (width % 4 != 0 || width > 4096)) return hipErrorInvalidValue;
   rms_norm_rows_kernel<<<(unsigned)rows, 256, 0, s>>>(x, width, scale, eps, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_session_batch_io(const SessionRef* sessions, int count, int* out, hipStream_t s) {
+  if (count < 1 || count > 64) return hipErrorInvalidValue;
+  session_batch_io_kernel<<<1, 64, 0, s>>>(sessions, count, out);
   return hipGetLastError();
 }
 
