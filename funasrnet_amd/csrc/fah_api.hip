@@ -388,7 +388,7 @@ struct fah_decoder {
   bool persistent = false;
   int blocks = 0;
   int persistent_positions = 0;  // positions below which steps take the persistent kernel
-  DeviceBuffer tx, tqkv, tatt, ta, th, tkeys, tattq, thq, tscore, epoch, error, timeline;
+  DeviceBuffer tx, tqkv, tatt, ta, th, tkeys, tattq, thq, tscore, tready, epoch, error, timeline;
   fah::PersistentArgs pargs{};
   // Prefill (decode of many rows at once): row buffers grown on demand.
   DeviceBuffer pf_x, pf_a, pf_qkv, pf_q, pf_h, pf_xq, pf_xs, pf_hq, pf_hs;
@@ -719,6 +719,7 @@ void init_state(fah_decoder* d, hipStream_t s) {
     tagged(d->thq, (size_t)fah::qblock_words(k.ffn));
     const int score_stride = (k.capacity + 127) & ~127;
     tagged(d->tscore, (size_t)k.heads * score_stride);
+    tagged(d->tready, 2 * (size_t)k.heads);
     d->epoch.allocate(16);
     d->error.allocate(16);
     unsigned one = 1;
@@ -763,6 +764,7 @@ void init_state(fah_decoder* d, hipStream_t s) {
     a.tattq = d->tattq.as<unsigned long long>();
     a.thq = d->thq.as<unsigned long long>();
     a.tscore = d->tscore.as<unsigned long long>();
+    a.tready = d->tready.as<unsigned long long>();
     a.score_stride = score_stride;
     // FAH_LONG_FROM: the long-cache attention from this position on (at
     // most, and by default, the positions the attention workgroups hold).

@@ -151,8 +151,11 @@ struct PersistentArgs {
   // Long caches: scores of the earlier positions, [heads][score_stride]
   // tagged words (score_stride = capacity rounded up to 128), written by
   // the projection workgroups of the kv head's XCD from position long_from
-  // on.
+  // on, then overwritten with the probabilities by the attention
+  // workgroups; tready[2 h], [2 h + 1]: head h's probabilities are all
+  // written (the first word carries p[pos]).
   unsigned long long* tscore;
+  unsigned long long* tready;
   int score_stride;
   int long_from;
   const float* x_in;    // modes 0/1: the input row

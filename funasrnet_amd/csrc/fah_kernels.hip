@@ -582,7 +582,10 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
       const int len = min(kValBlk, n - j * kValBlk);
       int tt = 0;
       if (len == kValBlk) {
-        // Full block: products read three groups of 16 ahead of the adds.
+        // Full block: products read three groups of 16 ahead of the adds
+        // (the scheduling barrier keeps the loads that far ahead, so that
+        // each add finds its product in registers: LDS latency is several
+        // adds long).
         float4 q[4][4];
 #pragma unroll
         for (int g = 0; g < 3; ++g)
@@ -594,6 +597,7 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) q[(i + 3) & 3][k] = *reinterpret_cast<const float4*>(row + 16 * (i + 3) + 4 * k);
           }
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             acc = fadd(acc, q[i & 3][k].x);

@@ -39,6 +39,8 @@
 // Every wait is bounded: a missing generation sets the error word and the
 // workgroup leaves, so a broken launch ends instead of hanging.
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 #include "fah_device.h"
 #include "fah_internal.h"
@@ -65,17 +67,23 @@ static_assert(kExactPositions <= 512 && kProbOffset + (kExactPositions + 1) / 2 
 // Long caches (positions from PersistentArgs::long_from on): the projection
 // workgroups of an XCD score the earlier positions of its kv head, the
 // attention workgroup gathers those scores (tagged words at the end of its
-// K/V area), keeps the probabilities of all n = pos + 1 positions in the
-// gather area after the q/k/v words and streams the V rows through a ring
-// of kRing slots of kSegPos positions: the slots below the scores are
-// filled ahead, the others once the scores are read.
+// K/V area), forms the probabilities of all n = pos + 1 positions in the
+// gather area after the q/k/v words and publishes them; the value sums run
+// on projection workgroups of the same XCD, one per (query head, 32-channel
+// block), each streaming its slice of the V rows and the probabilities
+// through a ring of kValSlots blocks of kValPos positions.
 constexpr int kLongPositions = 2 * (kTagWords - kProbOffset);
-constexpr int kSegPos = 64, kSegBytes = kSegPos * 256, kRing = 7;
 constexpr int kScoreBytes = kLongPositions * 8, kScoreOffset = kKvBytes - kScoreBytes;
-constexpr int kRingAhead = kScoreOffset / kSegBytes;  // slots clear of the scores
-static_assert(kExactPositions <= kLongPositions && kLongPositions % 128 == 0 && kRing * kSegBytes <= kKvBytes &&
-                  kRingAhead >= 2 && kRingAhead < kRing,
-              "long attention layout");
+static_assert(kExactPositions <= kLongPositions && kLongPositions % 128 == 0, "long attention layout");
+constexpr int kValPos = 64;                       // positions per value block
+constexpr int kValCh = 32;                        // channels per value workgroup (one quantised block)
+constexpr int kValRow = kValPos + 4;              // product row (floats): 4-bank offset per chain
+constexpr int kValPSlot = kValCh * kValRow * 4;   // product slot: 32 chains
+constexpr int kValVBytes = kValPos * kValCh * 2;  // V slice of a block (fp16)
+constexpr int kValSlot = kValVBytes + kValPos * 8;  // V slice, then the block's tagged probabilities
+constexpr int kValSlots = 12;                     // V/probability ring depth (blocks)
+constexpr int kValRing = kKvBytes - kValSlots * kValSlot;  // the ring sits at the end of the K/V area
+static_assert(4 * (kValSlots - 3) <= 63, "ring wait counts");
 // A wave polls a sentinel first when its part of a gather has more than this
 // many 1 KB chunks; a part of one chunk is polled whole (one round trip
 // sooner, and little enough traffic).
@@ -100,6 +108,38 @@ __device__ __forceinline__ void lds_barrier_p() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Workgroup barrier that orders LDS without waiting for this wave's direct
+// global->LDS loads still in flight (a release fence on LDS drains them
+// all): every wave's own LDS reads and writes are complete first (skipped
+// with READS_ONLY by a wave whose reads in flight are of data nobody
+// overwrites before its next barrier); direct loads that the other waves
+// read are waited for on their issuing wave's counter before it arrives.
+// The memory clobber keeps the compiler's LDS accesses on their side.
+template <bool READS_ONLY = false>
+__device__ __forceinline__ void lds_barrier_nodma() {
+  if (READS_ONLY) asm volatile("s_barrier" ::: "memory");
+  else asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+// 16 bytes of LDS read past the compiler, which would drain every direct
+// global->LDS load of this wave first (it cannot tell the addresses apart).
+__device__ __forceinline__ uint4 lds_read16_nodma(const __attribute__((address_space(3))) char* p) {
+  uint4 v;
+  const uint32_t at = (uint32_t)(uintptr_t)p;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(at) : "memory");
+  return v;
+}
+
+// s_waitcnt for vmcnt <= n with n known only at run time (0 <= n < N;
+// expcnt and lgkmcnt not waited on): vmcnt bits [3:0] and [15:14].
+template <int... I>
+__device__ __forceinline__ void vm_wait_n(int n, std::integer_sequence<int, I...>) {
+  ((n == I ? __builtin_amdgcn_s_waitcnt((I & 15) | ((I >> 4) << 14) | (7 << 4) | (15 << 8)) : (void)0), ...);
+}
+template <int N>
+__device__ __forceinline__ void vm_wait(int n) {
+  vm_wait_n(n, std::make_integer_sequence<int, N>{});
 }
 
 __device__ __forceinline__ void tag_store(u64* p, uint32_t gen, float v) {
@@ -978,41 +1018,6 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       __builtin_amdgcn_s_waitcnt(0);
     };
-    // Long caches: segment k of layer l's earlier V rows (positions
-    // [kSegPos k, kSegPos (k + 1)), rows past pos - 1 clamped to it) into
-    // ring slot k % kRing, four 1 KB loads by each of waves 4-7. The first
-    // kRingAhead segments are issued during the previous layer
-    // (ring_prefetch), the rest of the first kRing once the scores have been
-    // read, then one per segment added. ring_wait(j, last): segment j has
-    // landed, with segments up to `last` issued after it (four loads each).
-    char* ring = kv_s;
-    const int nseg = (pos + kSegPos - 1) / kSegPos;
-    static_assert(kSegBytes / 4096 == 4 && 4 * (kRing - 1) <= 63, "ring wait counts");
-    auto ring_wait = [&](int j, int last) {
-      switch (max(0, min(last, nseg - 1) - j)) {
-        case 0: __builtin_amdgcn_s_waitcnt(0); break;
-        case 1: __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (15 << 8)); break;
-        case 2: __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8)); break;
-        case 3: __builtin_amdgcn_s_waitcnt(12 | (7 << 4) | (15 << 8)); break;
-        case 4: __builtin_amdgcn_s_waitcnt(0 | (1 << 14) | (7 << 4) | (15 << 8)); break;
-        case 5: __builtin_amdgcn_s_waitcnt(4 | (1 << 14) | (7 << 4) | (15 << 8)); break;
-        default: __builtin_amdgcn_s_waitcnt(8 | (1 << 14) | (7 << 4) | (15 << 8)); break;
-      }
-    };
-    auto ring_issue = [&](int l, int k) {
-      const char* src = reinterpret_cast<const char*>(vbase(l));
-      char* dst = ring + (k % kRing) * kSegBytes + (wave - 4) * 1024;
-#pragma unroll
-      for (int i = 0; i < kSegBytes / 4096; ++i) {
-        const int b = (wave - 4) * 1024 + i * 4096 + 16 * lane;
-        const int t = min(k * kSegPos + (b >> 8), pos - 1);
-        __builtin_amdgcn_global_load_lds(src + (size_t)t * 256 + (b & 255), (lds_ptr)(dst + i * 4096), 16, 0, 0);
-      }
-    };
-    auto ring_prefetch = [&](int l) {
-      if (wave >= 4)
-        for (int k = 0; k < min(kRingAhead, nseg); ++k) ring_issue(l, k);
-    };
     if (a.mode == 2 && w == 0 && tid == 0) {
       int token = *a.token;
       if (token < 0 || token >= a.vocab) token = 0;
@@ -1020,8 +1025,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       a.history[hcount] = token;
       *a.history_count = hcount + 1;
     }
-    if (lng) ring_prefetch(0);
-    else stage_kv(0);
+    if (!lng) stage_kv(0);
 
     for (int l = 0; l < L; ++l) {
       const auto& Ly = LT[l];
@@ -1150,10 +1154,6 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       mark(e + 8);
       lds_barrier_p();
       sub(1);
-      // The scores have been read: the ring slots over them take the next
-      // segments.
-      if (lng && wave >= 4)
-        for (int k = kRingAhead; k < min(kRing, nseg); ++k) ring_issue(l, k);
       // The eight wave maxima in two reads, combined in order in registers.
       float mx;
       {
@@ -1222,53 +1222,51 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         lds_barrier_p();
         inverse = inv_s;
       }
-      for (int t = tid; t < n; t += kPT) p_s[t] = fmul(p_s[t], inverse);
-      if (lng && wave >= 4) ring_wait(0, kRing - 1);  // the ring's first segment
+      if (lng) {
+        // For the value workgroups of this XCD: the probabilities of the
+        // earlier positions as tagged words over this head's scores, then,
+        // once every wave's stores are written, a ready pair carrying p[pos].
+        u64* pd = a.tscore + (size_t)hq * a.score_stride;
+        for (int t = tid; t < n; t += kPT) {
+          const float pv = fmul(p_s[t], inverse);
+          p_s[t] = pv;
+          if (t < pos) {
+            if (a.local_l2) tag_store_local(pd + t, gen(l, 2), pv);
+            else tag_store(pd + t, gen(l, 2), pv);
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+      } else {
+        for (int t = tid; t < n; t += kPT) p_s[t] = fmul(p_s[t], inverse);
+      }
       lds_barrier_p();
       sub(2);
-      // Time-ordered value sums, one lane per channel (AttentionAvx.cs:173-224),
-      // with the same exact mixed-precision products as the scores.
       if (lng) {
-        // Wave 0 takes the even channels and wave 1 the odd ones, so that a
-        // lane's value is the same half of the dword (channels 2l, 2l+1) in
-        // every lane of its wave and one LDS read brings two positions.
-        const bool chain = wave < 2;
-        // The ring: the chain waves add segment k while waves 4-7 issue
-        // segment k + kRing - 1 into the slot read in step k - 1 (segments
-        // up to kRing - 1 are already issued) and wait for segment k + 1.
-        float acc = 0.0f;
-        for (int k = 0; k < nseg; ++k) {
-          if (chain) {
-            const char* base = ring + (k % kRing) * kSegBytes;
-            const int cnt = min(kSegPos, pos - k * kSegPos);
-            if (wave == 0) value_region<false>(base, p_s, k * kSegPos, cnt, acc);
-            else value_region<true>(base, p_s, k * kSegPos, cnt, acc);
-          } else if (wave >= 4) {
-            if (k >= 1 && k + kRing - 1 < nseg) ring_issue(l, k + kRing - 1);
-            ring_wait(k + 1, k + kRing - 1);
-          }
-          lds_barrier_p();
-        }
-        if (chain) {
-          const int c = 2 * lane + wave;
-          cur_s[0][c] = fadd(acc, fmul(cur_s[2][c], p_s[pos]));
+        if (tid < 2) {
+          const float v = tid == 0 ? p_s[pos] : 0.0f;
+          if (a.local_l2) tag_store_local(a.tready + 2 * hq + tid, gen(l, 2), v);
+          else tag_store(a.tready + 2 * hq + tid, gen(l, 2), v);
         }
       } else if (wave < 2) {
+        // Time-ordered value sums, one lane per channel (AttentionAvx.cs:173-224),
+        // with the same exact mixed-precision products as the scores.
         if (wave == 0) value_chain<false>(kv_s, p_s, nlds, pos, vbase(l), cur_s);
         else value_chain<true>(kv_s, p_s, nlds, pos, vbase(l), cur_s);
       }
       mark(e + 10);
       lds_barrier_p();
       if (wave == 0) {
-        // The head's four 32-value blocks quantised for the o projection:
-        // lanes 0-31 write them (block lane / 8), two whole lines.
         static_assert(HS == 128, "four blocks per head");
-        float d;
-        const uint32_t q = quantize_lane4(*reinterpret_cast<const float4*>(&cur_s[0][4 * (lane & 31)]), &d);
-        if (lane < 32) qword_store(a.tattq + 32 * hq + lane, gen(l, 2), qside(lane & 7, d), q);
-        // The output values themselves, for tracing.
-        tag_store(a.tatt + hq * HS + lane, gen(l, 2), cur_s[0][lane]);
-        tag_store(a.tatt + hq * HS + kWave + lane, gen(l, 2), cur_s[0][kWave + lane]);
+        if (!lng) {
+          // The head's four 32-value blocks quantised for the o projection:
+          // lanes 0-31 write them (block lane / 8), two whole lines.
+          float d;
+          const uint32_t q = quantize_lane4(*reinterpret_cast<const float4*>(&cur_s[0][4 * (lane & 31)]), &d);
+          if (lane < 32) qword_store(a.tattq + 32 * hq + lane, gen(l, 2), qside(lane & 7, d), q);
+          // The output values themselves, for tracing.
+          tag_store(a.tatt + hq * HS + lane, gen(l, 2), cur_s[0][lane]);
+          tag_store(a.tatt + hq * HS + kWave + lane, gen(l, 2), cur_s[0][kWave + lane]);
+        }
         if ((w >> 3) == 0) {
           // The first query head of the pair writes this position's K/V row
           // (four channels per lane).
@@ -1279,15 +1277,21 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           half4 h = {to_half(src[c]), to_half(src[c + 1]), to_half(src[c + 2]), to_half(src[c + 3])};
           *reinterpret_cast<half4*>(dst) = h;
         }
-        stamps(e + 3, e + 7, e + 4, 3);
+        if (!lng) {
+          stamps(e + 3, e + 7, e + 4, 3);
+        } else if (tl && lane == 0) {
+          // The output's publication time (e + 7) comes from the value
+          // workgroups.
+          tl[e + 3] = t_in;
+          for (int i = 0; i < 3; ++i) tl[e + 4 + i] = t_sub[i];
+        }
       }
       // Stage the next layer's K/V while the projections run.
       // The next layer's K/V staging starts ~0.9 us later, after the
       // attention-output exchange has left (measured slightly faster).
-      if (l + 1 < L) {
+      if (!lng && l + 1 < L) {
         __builtin_amdgcn_s_sleep(32);
-        if (lng) ring_prefetch(l + 1);
-        else stage_kv(l + 1);
+        stage_kv(l + 1);
       }
     }
     // lm_head input: the last layer's output with output_norm.
@@ -1331,16 +1335,20 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // layer l's o, gate/up and down and of layer l + 1's q/k/v, staged while
     // the attention runs (nothing else then reads weights), so that no
     // weight stream competes with the exchanges of the later phases.
-    auto stage_window = [&](int l) {
+    // `parts`: 1 the o slice and the next layer's q/k/v, 2 gate/up and
+    // down, 3 all.
+    auto stage_window = [&](int l, int parts) __attribute__((always_inline)) {
       const auto& Ly = LT[l];
       // The piece addresses are recomputed here each layer rather than kept
       // in registers across the loop.
       int cl = ct;
       asm volatile("" : "+v"(cl));
-      stage_slice<QW, SO>(kv_s + OO, Ly.wo, Ly.so, ro.count, cl, row_at);
-      stage_slice<W, SG>(kv_s + OG, Ly.wgu, Ly.sgu, 2 * rf.count, cl, gu_at);
-      stage_slice<FF, SD>(kv_s + OD, Ly.wd, Ly.sd, ro.count, cl, row_at);
-      if (l + 1 < L) stage_slice<W, SQ>(kv_s + OQ, LT[l + 1].wqkv, LT[l + 1].sqkv, rq.count, cl, qkv_at);
+      if (parts & 1) stage_slice<QW, SO>(kv_s + OO, Ly.wo, Ly.so, ro.count, cl, row_at);
+      if (parts & 2) {
+        stage_slice<W, SG>(kv_s + OG, Ly.wgu, Ly.sgu, 2 * rf.count, cl, gu_at);
+        stage_slice<FF, SD>(kv_s + OD, Ly.wd, Ly.sd, ro.count, cl, row_at);
+      }
+      if ((parts & 1) && l + 1 < L) stage_slice<W, SQ>(kv_s + OQ, LT[l + 1].wqkv, LT[l + 1].sqkv, rq.count, cl, qkv_at);
     };
     // Layer-0 input: a host row or the embedding of the device token
     // (QwenDecoder.Embed, Gguf.cs:340-344). Its loads go first so that they
@@ -1420,7 +1428,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // share at byte 256 r, its 16-byte piece i at slot i ^ (r & 15).
     static_assert(kLongPositions <= (kPT / 2) * NX && (kLongPositions + NX - 1) / NX * 256 <= kKvBytes,
                   "one position per lane pair, the share's K rows in the K/V area");
-    auto score_earlier = [&](int l) -> bool {
+    auto score_earlier = [&](int l, auto rows_in) __attribute__((always_inline)) -> bool {
       const auto& Ly = LT[l];
       const int j = (w >> 3) - G;
       const int t0 = pos * j / NX, t1 = pos * (j + 1) / NX;
@@ -1458,6 +1466,7 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       __builtin_amdgcn_s_waitcnt(0);  // this wave's K rows
       lds_barrier_p();
+      rows_in();
       if (t < t1) {
         uint2 kk[16];
 #pragma unroll
@@ -1492,123 +1501,390 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       return true;
     };
 
+    // Long caches, value workgroups: projection workgroup j < G HS / kValCh
+    // of XCD fx < HKV takes query head vhq = G fx + j / (HS / kValCh) and its
+    // channels [kValCh vb, +kValCh), vb = j % (HS / kValCh): the time-ordered
+    // value sums over the earlier positions (AttentionAvx.cs:173-224), one
+    // chain per channel, from the probabilities the attention workgroup
+    // publishes, then the block quantised for the o projection. Chains of
+    // different channels are independent, so spreading them over
+    // workgroups keeps the reference's order. Waves: 0 adds (one add per
+    // position and chain), 1 streams the V slice and 2 the probabilities
+    // through a ring of kValSlots blocks at the end of the K/V area (each
+    // wave waiting on its own load counter), 3 and 5-7 form the products
+    // p v of the block two ahead into a three-slot product ring (at OG,
+    // where gate/up and down are staged afterwards), 4 (sharing the adding
+    // wave's SIMD) checks the probabilities' tags.
+    constexpr int kValBlocks = HS / kValCh;
+    static_assert(HS % kValCh == 0 && G * kValBlocks <= NX, "one value workgroup per (query head, block)");
+    static_assert(OG + 3 * kValPSlot <= kValRing && (kLongPositions + NX - 1) / NX * 256 <= kValRing && OO <= OG,
+                  "value buffers clear of the o and q/k/v slices and of the score K rows");
+    // The value role's block, query head and block count, recomputed where
+    // used (opaque inputs keep them out of registers across the layer loop,
+    // whose register budget is full).
+    struct ValRole {
+      int vb, vhq, nvb;
+    };
+    auto val_role = [&]() __attribute__((always_inline)) {
+      int ww = w, pp = pos;
+      asm volatile("" : "+s"(ww), "+s"(pp));
+      const int vj = (ww >> 3) - G;
+      return ValRole{vj % kValBlocks, G * (ww & 7) + vj / kValBlocks, (pp + kValPos - 1) / kValPos};
+    };
+    using lds_char = __attribute__((address_space(3))) char;
+    auto vslot = [&](int k) { return (lds_char*)(kv_s + kValRing + (k % kValSlots) * kValSlot); };
+    // Wave 1: the V slice of block k (rows past pos - 1 repeat it, never used).
+    auto v_issue = [&](int l, int k, const ValRole& r) __attribute__((always_inline)) {
+      const char* src =
+          reinterpret_cast<const char*>(a.vcache + ((size_t)l * HKV + fx) * a.capacity * HS) + 2 * kValCh * r.vb;
+      lds_char* dst = vslot(k);
+#pragma unroll
+      for (int i = 0; i < kValVBytes / 1024; ++i) {
+        const int t = min(k * kValPos + 16 * i + (lane >> 2), pos - 1);
+        __builtin_amdgcn_global_load_lds(src + (size_t)t * (2 * HS) + 16 * (lane & 3), (lds_ptr)(dst + i * 1024), 16, 0, 0);
+      }
+    };
+    auto value_prefetch = [&](int l) __attribute__((always_inline)) {  // wave 1, once the score K rows are in LDS
+      const ValRole r = val_role();
+      for (int k = 0; k < min(kValSlots, r.nvb); ++k) v_issue(l, k, r);
+    };
+    auto value_sums = [&](int l) __attribute__((always_inline)) -> bool {
+      const ValRole r = val_role();
+      const int vb = r.vb, vhq = r.vhq, nvb = r.nvb;
+      float* vprod = reinterpret_cast<float*>(kv_s + OG);
+      // Wave 2 (and 4 on a retry): the tagged probabilities of block k.
+      auto p_issue = [&](int k) {
+        const u64* src = a.tscore + (size_t)vhq * a.score_stride + (size_t)k * kValPos;
+        if (lane < kValPos / 2) __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(vslot(k) + kValVBytes), 16, 0, 16);
+      };
+      // Block k's probabilities of positions below pos all current; stale
+      // ones (the ready pair came first) are read again.
+      auto p_settle = [&](int k) -> bool {
+        const uint32_t g = gen(l, 2);
+        for (long spin = 0;; ++spin) {
+          bool ok = true;
+          if (lane < kValPos / 2) {
+            const uint4 t = lds_read16_nodma(vslot(k) + kValVBytes + 16 * lane);
+            const int t0 = k * kValPos + 2 * lane;
+            ok = (t0 >= pos || t.y == g) && (t0 + 1 >= pos || t.w == g);
+          }
+          if (__all(ok)) return true;
+          if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(a.error))) {
+            if (lane == 0) __hip_atomic_fetch_or(a.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            return false;
+          }
+          p_issue(k);
+          __builtin_amdgcn_s_waitcnt(0);
+        }
+      };
+      // Products of block k: task (four positions, channel pair), 16 x 16
+      // per block over the 256 lanes of waves 3, 5, 6, 7; rows 2cp and
+      // 2cp + 1 of the product slot, four positions as one float4.
+      // Positions from pos on get +0, so that every block adds 64 products:
+      // acc + 0 is acc, since a sum from +0 is never -0.
+      auto produce = [&](int k) {
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        using lds_u32 = const __attribute__((address_space(3))) uint32_t;
+        using lds_u4 = const __attribute__((address_space(3))) u32x4;
+        const lds_char* vsl = vslot(k);
+        float* pr = vprod + (k % 3) * (kValPSlot / 4);
+        // The lane's offsets are recomputed each block rather than kept in
+        // registers across the loop.
+        int lp = (wave == 3 ? 0 : wave - 4) * kWave + lane;
+        asm volatile("" : "+v"(lp));
+        const int quad = lp >> 4, cp = lp & 15;
+        const u32x4 w0 = *(lds_u4*)(vsl + kValVBytes + 32 * quad);
+        const u32x4 w1 = *(lds_u4*)(vsl + kValVBytes + 32 * quad + 16);
+        uint32_t d[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) d[u] = *(lds_u32*)(vsl + (4 * quad + u) * (2 * kValCh) + 4 * cp);
+        // All six reads in flight before the first product.
+        __builtin_amdgcn_sched_barrier(0);
+        const float p[4] = {u2f(w0.x), u2f(w0.z), u2f(w1.x), u2f(w1.z)};
+        float lo[4], hi[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          lo[u] = fmul(from_half(__builtin_bit_cast(_Float16, (uint16_t)d[u])), p[u]);
+          hi[u] = fmul(from_half(__builtin_bit_cast(_Float16, (uint16_t)(d[u] >> 16))), p[u]);
+        }
+        if ((k + 1) * kValPos > pos) {
+          // The last block: +0 (all bits clear) from pos on, without branches.
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const uint32_t keep = 0u - (uint32_t)(k * kValPos + 4 * quad + u < pos);
+            lo[u] = u2f(f2u(lo[u]) & keep);
+            hi[u] = u2f(f2u(hi[u]) & keep);
+          }
+        }
+        *reinterpret_cast<float4*>(pr + (2 * cp) * kValRow + 4 * quad) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+        *reinterpret_cast<float4*>(pr + (2 * cp + 1) * kValRow + 4 * quad) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+      };
+      const bool producer = wave == 3 || wave >= 5;
+      lds_barrier_nodma();  // every wave's score K rows read: the value buffers and the q/k/v slice overlap them
+      if (ct >= 0) stage_window(l, 1);
+      u64* rdy = tag_s + 2048;  // the ready pair: p[pos]
+      u64* vcw = tag_s + 2176;  // this position's v, this block's channels
+      // Blocks in the ring; the last one whose V (and probabilities) the
+      // prologue waits for; the last one whose probabilities it waits for.
+      const int m = min(kValSlots, nvb), first = min(2, nvb - 1), pfirst = min(3, nvb - 1);
+      bool ok = true;
+      if (wave == 0) {
+        ok = poll_words<kValCh>(a.tqkv + QW + KVW + fx * HS + kValCh * vb, gen(l, 1), vcw, a.error, nullptr);
+      } else if (wave == 1) {
+        if (nvb > 0) vm_wait<4 * kValSlots>(4 * (m - 1 - first));
+      } else if (wave == 2) {
+        ok = poll_words<2>(a.tready + 2 * vhq, gen(l, 2), rdy, a.error, nullptr);
+        if (ok && nvb > 0) {
+          for (int k = 0; k < m; ++k) p_issue(k);
+          vm_wait<kValSlots>(m - 1 - pfirst);
+          for (int k = 0; ok && k <= first; ++k) ok = p_settle(k);
+        }
+      }
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      lds_barrier_nodma();
+      {
+        int all = 1;
+#pragma unroll
+        for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
+        if (!all) return false;
+      }
+      if (producer)
+        for (int k = 0; k < min(2, nvb); ++k) produce(k);
+      lds_barrier_nodma();
+      // Block j: wave 0 adds slot j % 3 (reading the next block's groups as
+      // it goes, from block j + 1's slot, formed the step before), the
+      // producers form block j + 2, waves 1 and 2 issue block j + kValSlots
+      // into block j's ring slot (its products were formed two steps ago)
+      // and wait for blocks j + 3 (V) and j + 4 (probabilities), wave 4
+      // checks block j + 3's probabilities. Each role runs its own loop, one
+      // barrier a block, so that no role's registers are live in another's.
+      float acc = 0.0f;
+      if (wave == 0) {
+        auto load_group = [&](int j, int g, float4* dst) {
+          const float* row = vprod + (j % 3) * (kValPSlot / 4) + (lane & (kValCh - 1)) * kValRow + 16 * g;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) dst[k] = *reinterpret_cast<const float4*>(row + 4 * k);
+        };
+        // The whole block in registers: group i of the next block is read
+        // as soon as group i of this one is added (stale past the last
+        // block, never added), three groups ahead of its use.
+        float4 q[4][4];
+        if (lane < kValCh)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) load_group(0, g, q[g]);
+        for (int j = 0; j < nvb; ++j) {
+          if (lane < kValCh) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                acc = fadd(acc, q[i][k].x);
+                acc = fadd(acc, q[i][k].y);
+                acc = fadd(acc, q[i][k].z);
+                acc = fadd(acc, q[i][k].w);
+              }
+              __builtin_amdgcn_sched_barrier(0);
+              load_group(j + 1, i, q[i]);
+            }
+          }
+          // Its reads in flight are of slots j and j + 1, which the
+          // producers overwrite two and three steps on.
+          lds_barrier_nodma<true>();
+        }
+      } else if (wave == 1) {
+        for (int j = 0; j < nvb; ++j) {
+          if (j + kValSlots < nvb) v_issue(l, j + kValSlots, r);
+          if (j + 3 < nvb) vm_wait<4 * kValSlots>(4 * (min(j + kValSlots, nvb - 1) - (j + 3)));
+          lds_barrier_nodma();
+        }
+      } else if (wave == 2) {
+        // Block j + 4 in LDS by the end of step j.
+        for (int j = 0; j < nvb; ++j) {
+          if (j + kValSlots < nvb) p_issue(j + kValSlots);
+          if (j + 4 < nvb) vm_wait<kValSlots>(min(j + kValSlots, nvb - 1) - (j + 4));
+          lds_barrier_nodma();
+        }
+      } else if (wave == 4) {
+        // Block j + 3's probabilities (in LDS since step j - 1) all current
+        // before the producers read them in step j + 1; stale ones are read
+        // again (with this wave's own loads).
+        for (int j = 0; j < nvb; ++j) {
+          if (ok && j + 3 < nvb) ok = p_settle(j + 3);
+          lds_barrier_nodma();
+        }
+      } else {
+        for (int j = 0; j < nvb; ++j) {
+          if (producer && j + 2 < nvb) produce(j + 2);
+          lds_barrier_nodma();
+        }
+      }
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      if (wave == 0 && lane < kValCh) {
+        // This position's term, then the block's values for quantisation.
+        const float vc = from_half(to_half(tag_value(vcw, lane)));
+        acc = fadd(acc, fmul(vc, tag_value(rdy, 0)));
+        cur_s[2][lane] = acc;
+      }
+      lds_barrier_p();
+      {
+        int all = 1;
+#pragma unroll
+        for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
+        if (!all) return false;
+      }
+      if (wave == 0) {
+        float d;
+        const uint32_t qw = quantize_lane4(*reinterpret_cast<const float4*>(&cur_s[2][4 * (lane & 7)]), &d);
+        if (lane < 8) qword_store(a.tattq + 32 * vhq + 8 * vb + lane, gen(l, 2), qside(lane, d), qw);
+        // The output values themselves, for tracing.
+        if (lane < kValCh) tag_store(a.tatt + vhq * HS + kValCh * vb + lane, gen(l, 2), cur_s[2][lane]);
+        // The attention's publication time, on its attention workgroup's
+        // timeline (the latest of its value workgroups).
+        if (a.timeline && lane == 0)
+          __hip_atomic_fetch_max(a.timeline + (size_t)(fx + 8 * (vhq - G * fx)) * kTimelineEvents + 16 * l + 1 + 7,
+                                 (unsigned long long)__builtin_amdgcn_s_memrealtime(), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return true;
+    };
+
     // Each phase: all threads quantise (or unpack) the gathered input and
     // form the block products of the LDS slice, then wave 0 sums the rows in
     // order and publishes them, and the memory waves gather
     // the next phase's input. After the q/k/v publication (and a barrier, so
     // that the stores leave ahead of the burst) the compute waves stage the
     // slices of the rest of the layer and the next layer's q/k/v.
-    for (int l = 0; l < L; ++l) {
-      const auto& Ly = LT[l];
-      const auto& Nx = LT[l + 1 < L ? l + 1 : l];
-      const int e = 16 * l + 1;
-      // ---- P1: attn_norm + qkv ----------------------------------------------
-      quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
-      if (ct >= 0 && l == 0) __builtin_amdgcn_s_waitcnt(0);  // layer 0's staged q/k/v slice
-      lds_barrier_p();
-      sub(0);
-      lds_products<NPQ, B1>(kv_s + OQ, rq.count, xq_s, xs_s, prod_s);
-      lds_barrier_p();
-      sub(1);
-      // This workgroup's residual rows of x (read in the o epilogue), while
-      // wave 0 sums the q/k/v rows; the gather area keeps x until the
-      // attention output arrives, after the next barrier.
-      if (wave == 1 && lane < ro.count) row_s[0][lane] = tag_value(tag_s, row_at(lane));
-      if (wave == 0) {
-        if (lane < rq.count) {
-          const float v = ordered_sum<B1>(prod_s, lane);
-          u64* dst = a.tqkv + qkv_row(rq.r0 + lane);
-          if (a.local_l2) tag_store_local(dst, gen(l, 1), v);
-          else tag_store(dst, gen(l, 1), v);
-        }
-        stamps(e + 0, e + 2, e + 1, 1);
-        if (tl && lane == 0) tl[e + 4] = t_sub[1];
-      }
-      lds_barrier_p();
-      if (lng && fx < HKV && !score_earlier(l)) return;
-      if (ct >= 0) stage_window(l);
-      gather_q(a.tattq, QWA, gen(l, 2));
-      if (ct >= 0) __builtin_amdgcn_s_waitcnt(0);  // the staged slices are in LDS before the barrier
-      if (!gathered()) return;
-
-      // ---- P3: o projection + residual -------------------------------------
-      unpack_qblocks<QW>(tag_s, xq_s, xs_s);
-      lds_barrier_p();
-      lds_products<NPO, Bq>(kv_s + OO, ro.count, xq_s, xs_s, prod_s);
-      lds_barrier_p();
-      if (wave == 0) {
-        if (lane < ro.count) {
-          const float v = fadd(ordered_sum<Bq>(prod_s, lane), row_s[0][lane]);
-          row_s[1][lane] = v;
-          tag_store(a.ta + row_at(lane), gen(l, 3), v);
-        }
-        stamps(e + 8, e + 9);
-      }
-      gather_norm(a.ta, gen(l, 3), [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
-      if (!gathered()) return;
-
-      // ---- P4: ffn_norm + gate/up + SwiGLU -----------------------------------
-      quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
-      lds_barrier_p();
-      sub(0);
-      lds_products<NPG, B1>(kv_s + OG, 2 * rf.count, xq_s, xs_s, prod_s);
-      lds_barrier_p();
-      if (wave == 0) {
-        // Lanes [0, n) sum the gate rows, [n, 2n) the matching up rows.
-        const int nr = rf.count;
-        const float gs = lane < 2 * nr ? ordered_sum<B1>(prod_s, lane) : 0.0f;
-        const float u = __shfl(gs, lane + nr, kWave);
-        if (lane < nr) {
-          const float silu = fdiv(gs, fadd(1.0f, exp_ref(-gs)));
-          u64* dst = a.th + persistent_xcd_row(fx, rf.r0 + lane, 64);
-          if (a.local_l2) tag_store_local(dst, gen(l, 4), fmul(silu, u));
-          else tag_store(dst, gen(l, 4), fmul(silu, u));
-        }
-        stamps(e + 10, e + 12, e + 11, 1);
-      }
-      // The pair owners quantise their blocks (read through this XCD's L2)
-      // and publish them; every projection workgroup gathers the quantised
-      // vector.
-      // The quantised ffn vector (QWH / 128 <= 8 chunks) is gathered one
-      // chunk per wave, polled whole; wave 0 (the owner's publisher) and as
-      // few others as possible take none.
-      {
-        bool ok = true;
-        if (wave == 0 && own >= 0) {
-          u64 seen = 0;
-          ok = publish_pair(a.th, a.thq, own, gen(l, 4), tag_s + kTagWords - 64, a.error, &seen);
-          if (tl && lane == 0) {
-            tl[e + 6] = seen;
-            tl[e + 7] = __builtin_amdgcn_s_memrealtime();
+    // The layer loop, instantiated for the value workgroups and for the
+    // others: the value sums' registers then do not burden the others'
+    // projection phases. False when an exchange failed.
+    auto layers = [&](auto value_role) __attribute__((always_inline)) -> bool {
+      constexpr bool VAL = decltype(value_role)::value;
+      for (int l = 0; l < L; ++l) {
+        const auto& Ly = LT[l];
+        const auto& Nx = LT[l + 1 < L ? l + 1 : l];
+        const int e = 16 * l + 1;
+        // ---- P1: attn_norm + qkv ----------------------------------------------
+        quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
+        if (ct >= 0 && l == 0) __builtin_amdgcn_s_waitcnt(0);  // layer 0's staged q/k/v slice
+        lds_barrier_p();
+        sub(0);
+        lds_products<NPQ, B1>(kv_s + OQ, rq.count, xq_s, xs_s, prod_s);
+        lds_barrier_p();
+        sub(1);
+        // This workgroup's residual rows of x (read in the o epilogue), while
+        // wave 0 sums the q/k/v rows; the gather area keeps x until the
+        // attention output arrives, after the next barrier.
+        if (wave == 1 && lane < ro.count) row_s[0][lane] = tag_value(tag_s, row_at(lane));
+        if (wave == 0) {
+          if (lane < rq.count) {
+            const float v = ordered_sum<B1>(prod_s, lane);
+            u64* dst = a.tqkv + qkv_row(rq.r0 + lane);
+            if (a.local_l2) tag_store_local(dst, gen(l, 1), v);
+            else tag_store(dst, gen(l, 1), v);
           }
+          stamps(e + 0, e + 2, e + 1, 1);
+          if (tl && lane == 0) tl[e + 4] = t_sub[1];
         }
-        if (ok)
-          ok = gather(a.thq, QWH, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gen(l, 4)), tag_s, a.error, NoPre{}, wave,
-                      kPT / kWave, NoChunk{}, nullptr, kQTagMask);
-        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
-      }
-      if (!gathered()) return;
+        lds_barrier_p();
+        if constexpr (VAL) {
+          if (!score_earlier(l, [&] {
+                if (wave == 1) value_prefetch(l);
+              }))
+            return false;
+          if (!value_sums(l)) return false;
+          if (ct >= 0) stage_window(l, 2);
+        } else {
+          if (lng && fx < HKV && !score_earlier(l, [] {})) return false;
+          if (ct >= 0) stage_window(l, 3);
+        }
+        gather_q(a.tattq, QWA, gen(l, 2));
+        if (ct >= 0) __builtin_amdgcn_s_waitcnt(0);  // the staged slices are in LDS before the barrier
+        if (!gathered()) return false;
 
-      // ---- P5: down projection + residual ------------------------------------
-      unpack_qblocks<FF>(tag_s, xq_s, xs_s);
-      lds_barrier_p();
-      sub(0);
-      lds_products<NPD, Bf>(kv_s + OD, ro.count, xq_s, xs_s, prod_s);
-      lds_barrier_p();
-      sub(1);
-      if (wave == 0) {
-        if (lane < ro.count) {
-          const float v = fadd(ordered_sum<Bf>(prod_s, lane), row_s[1][lane]);
-          tag_store(a.tx + row_at(lane), gen(l, 5), v);
+        // ---- P3: o projection + residual -------------------------------------
+        unpack_qblocks<QW>(tag_s, xq_s, xs_s);
+        lds_barrier_p();
+        lds_products<NPO, Bq>(kv_s + OO, ro.count, xq_s, xs_s, prod_s);
+        lds_barrier_p();
+        if (wave == 0) {
+          if (lane < ro.count) {
+            const float v = fadd(ordered_sum<Bq>(prod_s, lane), row_s[0][lane]);
+            row_s[1][lane] = v;
+            tag_store(a.ta + row_at(lane), gen(l, 3), v);
+          }
+          stamps(e + 8, e + 9);
         }
-        stamps(e + 13, e + 15, e + 14, 1);
-        if (tl && lane == 0) tl[e + 5] = t_sub[1];
+        gather_norm(a.ta, gen(l, 3), [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
+        if (!gathered()) return false;
+
+        // ---- P4: ffn_norm + gate/up + SwiGLU -----------------------------------
+        quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
+        lds_barrier_p();
+        sub(0);
+        lds_products<NPG, B1>(kv_s + OG, 2 * rf.count, xq_s, xs_s, prod_s);
+        lds_barrier_p();
+        if (wave == 0) {
+          // Lanes [0, n) sum the gate rows, [n, 2n) the matching up rows.
+          const int nr = rf.count;
+          const float gs = lane < 2 * nr ? ordered_sum<B1>(prod_s, lane) : 0.0f;
+          const float u = __shfl(gs, lane + nr, kWave);
+          if (lane < nr) {
+            const float silu = fdiv(gs, fadd(1.0f, exp_ref(-gs)));
+            u64* dst = a.th + persistent_xcd_row(fx, rf.r0 + lane, 64);
+            if (a.local_l2) tag_store_local(dst, gen(l, 4), fmul(silu, u));
+            else tag_store(dst, gen(l, 4), fmul(silu, u));
+          }
+          stamps(e + 10, e + 12, e + 11, 1);
+        }
+        // The pair owners quantise their blocks (read through this XCD's L2)
+        // and publish them; every projection workgroup gathers the quantised
+        // vector.
+        // The quantised ffn vector (QWH / 128 <= 8 chunks) is gathered one
+        // chunk per wave, polled whole; wave 0 (the owner's publisher) and as
+        // few others as possible take none.
+        {
+          bool ok = true;
+          if (wave == 0 && own >= 0) {
+            u64 seen = 0;
+            ok = publish_pair(a.th, a.thq, own, gen(l, 4), tag_s + kTagWords - 64, a.error, &seen);
+            if (tl && lane == 0) {
+              tl[e + 6] = seen;
+              tl[e + 7] = __builtin_amdgcn_s_memrealtime();
+            }
+          }
+          if (ok)
+            ok = gather(a.thq, QWH, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gen(l, 4)), tag_s, a.error, NoPre{}, wave,
+                        kPT / kWave, NoChunk{}, nullptr, kQTagMask);
+          if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+        }
+        if (!gathered()) return false;
+
+        // ---- P5: down projection + residual ------------------------------------
+        unpack_qblocks<FF>(tag_s, xq_s, xs_s);
+        lds_barrier_p();
+        sub(0);
+        lds_products<NPD, Bf>(kv_s + OD, ro.count, xq_s, xs_s, prod_s);
+        lds_barrier_p();
+        sub(1);
+        if (wave == 0) {
+          if (lane < ro.count) {
+            const float v = fadd(ordered_sum<Bf>(prod_s, lane), row_s[1][lane]);
+            tag_store(a.tx + row_at(lane), gen(l, 5), v);
+          }
+          stamps(e + 13, e + 15, e + 14, 1);
+          if (tl && lane == 0) tl[e + 5] = t_sub[1];
+        }
+        // Next layer's input with its attn_norm, or the lm_head input with output_norm.
+        const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
+        gather_norm(a.tx, gen(l, 5), [&] { dma(next_norm, norm_s, W * 4); });
+        if (!gathered()) return false;
       }
-      // Next layer's input with its attn_norm, or the lm_head input with output_norm.
-      const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
-      gather_norm(a.tx, gen(l, 5), [&] { dma(next_norm, norm_s, W * 4); });
-      if (!gathered()) return;
-    }
+      return true;
+    };
+    const int vj = (w >> 3) - G;
+    const bool valued = lng && fx < HKV && vj >= 0 && vj < G * kValBlocks;
+    if (valued ? !layers(std::true_type{}) : !layers(std::false_type{})) return;
   }
 
   if (a.mode == 0) {
