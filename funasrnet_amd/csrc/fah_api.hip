@@ -770,14 +770,13 @@ void init_state(fah_decoder* d, hipStream_t s) {
     // most, and by default, the positions the attention workgroups hold).
     a.long_from = fah::persistent_exact_positions();
     if (const char* lf = std::getenv("FAH_LONG_FROM")) a.long_from = std::max(0, std::min(a.long_from, std::atoi(lf)));
-    // Past kLongPersistentPositions the multi-kernel step is the faster one:
-    // its value chains run on many workgroups at once, while the persistent
-    // kernel's run on one per query head (measured, a token, persistent
-    // against the multi-kernel step over these weights: 1.42 / 1.56 ms at
-    // 2,560 cached positions, 1.61 / 1.64 at 3,072, 1.79 / 1.71 at 3,584).
+    // Every position the persistent kernel holds runs on it: with the value
+    // sums spread over the projection workgroups it is the faster step at
+    // every length it takes (measured, a token, persistent against the
+    // multi-kernel step over these weights: 1.34 / 1.79 ms at 4,096 cached
+    // positions). Past that the multi-kernel step runs.
     // FAH_PERSISTENT_POSITIONS moves the switch.
-    constexpr int kLongPersistentPositions = 3200;
-    d->persistent_positions = std::min(kLongPersistentPositions, fah::persistent_max_positions());
+    d->persistent_positions = fah::persistent_max_positions();
     if (const char* pp = std::getenv("FAH_PERSISTENT_POSITIONS"))
       d->persistent_positions = std::max(0, std::min(fah::persistent_max_positions(), std::atoi(pp)));
     a.x_in = d->x.as<float>();

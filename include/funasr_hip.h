@@ -425,7 +425,7 @@ int fah_decoder_fail_next_step(fah_decoder* decoder);
  * with roles by workgroup index (after a launch found the XCD dealing it
  * relies on broken, or with FAH_LOCAL_L2=0 in the environment at creation),
  * 0 for the per-kernel graph path (FAH_PERSISTENT=0 at creation). A
- * persistent decoder runs the steps of positions below 3200 (below 483 with
+ * persistent decoder runs the steps of positions below 5120 (below 483 with
  * every earlier K/V row held by the attention workgroups, from 483 with the
  * long-cache attention) on the persistent kernel and later steps on the
  * per-kernel graph path; FAH_PERSISTENT_POSITIONS and FAH_LONG_FROM at

@@ -93,12 +93,13 @@ def test_persistent_against_oracle_tokens(backend, oracle_lib):
 
 
 @pytest.mark.parametrize("shape,positions,persistent_positions",
-                         [("small", 4096, 5120), ("qwen3", 4096, 5120), ("qwen3", 2048, None)])
+                         [("small", 4096, None), ("qwen3", 4096, None), ("qwen3", 2048, 2052)])
 def test_long_cache_matches_graph_path(backend, oracle_lib, shape, positions, persistent_positions):
     """A cache pre-filled with F16 N(0,1) rows in every layer: the persistent
-    kernel's long-cache attention (scores on the projection workgroups, V
-    rows streamed; at 4096 positions with FAH_PERSISTENT_POSITIONS past its
-    default switch, at 2048 by default) and the per-kernel path give
+    kernel's long-cache attention (scores on the projection workgroups, the
+    value sums on value workgroups from the published probabilities; at
+    2048 positions with FAH_PERSISTENT_POSITIONS=2052, so that the greedy
+    steps cross over to the per-kernel path) and the per-kernel path give
     identical logits bits, K/V rows and tokens, and match the oracle (the
     full-size shape too, 8 greedy steps)."""
     cfg = model.small_config(layers=2) if shape == "small" else model.QWEN3_0_6B
