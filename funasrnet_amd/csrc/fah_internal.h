@@ -152,10 +152,8 @@ struct PersistentArgs {
   // tagged words (score_stride = capacity rounded up to 128), written by
   // the projection workgroups of the kv head's XCD from position long_from
   // on, then overwritten with the probabilities by the attention
-  // workgroups; tready[2 h], [2 h + 1]: head h's probabilities are all
-  // written (the first word carries p[pos]).
+  // workgroups (see tready).
   unsigned long long* tscore;
-  unsigned long long* tready;
   int score_stride;
   int long_from;
   const float* x_in;    // modes 0/1: the input row
@@ -172,6 +170,10 @@ struct PersistentArgs {
   // launch), so the q/k/v rows of kv head x are computed on XCD x and handed
   // to its attention workgroups through that XCD's L2.
   int local_l2;
+  // Long caches: tready[2 h], [2 h + 1] carry head h's generation once its
+  // probabilities are all written over its scores (the first word carries
+  // p[pos]).
+  unsigned long long* tready;
 };
 
 constexpr int kTimelineEvents = 480;

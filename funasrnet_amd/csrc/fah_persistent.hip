@@ -1303,593 +1303,582 @@ __global__ __launch_bounds__(kPT) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (!flag_s) return;
   } else {
     // ======================= projection workgroup ===============================
-    // The whole role, instantiated for the value workgroups and for the
-    // others: every value either computes lives in its own instantiation,
-    // so that the value sums' registers do not burden the others'
-    // projection phases (the kernel's register budget is full).
-    auto projection = [&](auto value_role) __attribute__((always_inline)) -> bool {
-      constexpr bool VAL = decltype(value_role)::value;
-      // g: rank among the projection workgroups (attention ones below w skipped).
-      int g = w;
-  #pragma unroll
-      for (int s8 = 0; s8 < G; ++s8) g -= min(max(w - 8 * s8, 0), HKV);
-      const Rows ro = split_rows<W, NG>(g);
-      auto row_at = [&](int r) { return ro.r0 + r; };  // o and down rows
-      // ffn rows: entries of this XCD's list (persistent_xcd_entries, 64-row
-      // block pairs), the gate/up tile's storage row, and the block pair this
-      // role quantises and publishes (the one whose entry 32 it computes), if
-      // any.
-      const int fx = w & 7;
-      const XcdEntries rf = persistent_xcd_entries(fx, (w >> 3) - (fx < HKV ? G : 0), FF, HKV, G, NB);
-      const size_t rf_store = 2 * (size_t)(fx * (FF / 8) + rf.r0);
-      int own = -1;
-      {
-        const int k = (rf.r0 + rf.count - 33) >> 6;
-        if (rf.count > 0 && k >= 0 && 64 * k + 32 >= rf.r0) own = fx + 8 * k;
+    // g: rank among the projection workgroups (attention ones below w skipped).
+    int g = w;
+#pragma unroll
+    for (int s8 = 0; s8 < G; ++s8) g -= min(max(w - 8 * s8, 0), HKV);
+    const Rows ro = split_rows<W, NG>(g);
+    auto row_at = [&](int r) { return ro.r0 + r; };  // o and down rows
+    // ffn rows: entries of this XCD's list (persistent_xcd_entries, 64-row
+    // block pairs), the gate/up tile's storage row, and the block pair this
+    // role quantises and publishes (the one whose entry 32 it computes), if
+    // any.
+    const int fx = w & 7;
+    const XcdEntries rf = persistent_xcd_entries(fx, (w >> 3) - (fx < HKV ? G : 0), FF, HKV, G, NB);
+    const size_t rf_store = 2 * (size_t)(fx * (FF / 8) + rf.r0);
+    int own = -1;
+    {
+      const int k = (rf.r0 + rf.count - 33) >> 6;
+      if (rf.count > 0 && k >= 0 && 64 * k + 32 >= rf.r0) own = fx + 8 * k;
+    }
+    // q/k/v: this XCD's kv head; none on XCDs past the kv heads, whose
+    // (unused, clamped) slice loads then read kv head 0's rows.
+    const int xk = (w & 7) < HKV ? (w & 7) : 0;
+    const Rows rq = (w & 7) < HKV ? split_rows<QL, NX>((w >> 3) - G) : Rows{0, 0};
+    auto qkv_row = [&](int r) {  // row r of kv head xk's list -> q/k/v row
+      return r < G * HS ? G * HS * xk + r
+                        : (r < (G + 1) * HS ? QW + HS * xk + (r - G * HS) : QW + KVW + HS * xk + (r - (G + 1) * HS));
+    };
+    auto qkv_at = [&](int r) { return qkv_row(rq.r0 + r); };
+    auto gu_at = [&](int r) { return (int)rf_store + r; };
+    // Compute lanes, after the q/k/v publication of layer l: the slices of
+    // layer l's o, gate/up and down and of layer l + 1's q/k/v, staged while
+    // the attention runs (nothing else then reads weights), so that no
+    // weight stream competes with the exchanges of the later phases.
+    // `parts`: 1 the o slice and the next layer's q/k/v, 2 gate/up and
+    // down, 3 all.
+    auto stage_window = [&](int l, int parts) __attribute__((always_inline)) {
+      const auto& Ly = LT[l];
+      // The piece addresses are recomputed here each layer rather than kept
+      // in registers across the loop.
+      int cl = ct;
+      asm volatile("" : "+v"(cl));
+      if (parts & 1) stage_slice<QW, SO>(kv_s + OO, Ly.wo, Ly.so, ro.count, cl, row_at);
+      if (parts & 2) {
+        stage_slice<W, SG>(kv_s + OG, Ly.wgu, Ly.sgu, 2 * rf.count, cl, gu_at);
+        stage_slice<FF, SD>(kv_s + OD, Ly.wd, Ly.sd, ro.count, cl, row_at);
       }
-      // q/k/v: this XCD's kv head; none on XCDs past the kv heads, whose
-      // (unused, clamped) slice loads then read kv head 0's rows.
-      const int xk = (w & 7) < HKV ? (w & 7) : 0;
-      const Rows rq = (w & 7) < HKV ? split_rows<QL, NX>((w >> 3) - G) : Rows{0, 0};
-      auto qkv_row = [&](int r) {  // row r of kv head xk's list -> q/k/v row
-        return r < G * HS ? G * HS * xk + r
-                          : (r < (G + 1) * HS ? QW + HS * xk + (r - G * HS) : QW + KVW + HS * xk + (r - (G + 1) * HS));
-      };
-      auto qkv_at = [&](int r) { return qkv_row(rq.r0 + r); };
-      auto gu_at = [&](int r) { return (int)rf_store + r; };
-      // Compute lanes, after the q/k/v publication of layer l: the slices of
-      // layer l's o, gate/up and down and of layer l + 1's q/k/v, staged while
-      // the attention runs (nothing else then reads weights), so that no
-      // weight stream competes with the exchanges of the later phases.
-      // `parts`: 1 the o slice and the next layer's q/k/v, 2 gate/up and
-      // down, 3 all.
-      auto stage_window = [&](int l, int parts) __attribute__((always_inline)) {
-        const auto& Ly = LT[l];
-        // The piece addresses are recomputed here each layer rather than kept
-        // in registers across the loop.
-        int cl = ct;
-        asm volatile("" : "+v"(cl));
-        if (parts & 1) stage_slice<QW, SO>(kv_s + OO, Ly.wo, Ly.so, ro.count, cl, row_at);
-        if (parts & 2) {
-          stage_slice<W, SG>(kv_s + OG, Ly.wgu, Ly.sgu, 2 * rf.count, cl, gu_at);
-          stage_slice<FF, SD>(kv_s + OD, Ly.wd, Ly.sd, ro.count, cl, row_at);
+      if ((parts & 1) && l + 1 < L) stage_slice<W, SQ>(kv_s + OQ, LT[l + 1].wqkv, LT[l + 1].sqkv, rq.count, cl, qkv_at);
+    };
+    // Layer-0 input: a host row or the embedding of the device token
+    // (QwenDecoder.Embed, Gguf.cs:340-344). Its loads go first so that they
+    // do not wait behind the weight slices.
+    constexpr int XI = W / kPT;
+    int8_t eq[XI];
+    _Float16 es[XI];
+    float xr[XI];
+    if (a.mode == 2) {
+      int token = *a.token;
+      if (token < 0 || token >= a.vocab) token = 0;
+#pragma unroll
+      for (int k = 0; k < XI; ++k) {
+        const size_t at = (size_t)token * W + tid + k * kPT;
+        eq[k] = a.embed_q[at];
+        es[k] = a.embed_s[at / 32];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < XI; ++k) xr[k] = a.x_in[tid + k * kPT];
+    }
+    if (ct >= 0) {
+      stage_slice<W, SQ>(kv_s + OQ, LT[0].wqkv, LT[0].sqkv, rq.count, ct, qkv_at);
+    } else if (wave == 0) {
+      dma(LT[0].attn_norm, norm_s, W * 4);
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+#pragma unroll
+    for (int k = 0; k < XI; ++k)
+      tag_s[tid + k * kPT] = (u64)f2u(a.mode == 2 ? fmul((float)eq[k], (float)es[k]) : xr[k]);
+    lds_barrier_p();
+    // The layer-0 input's norm partials (later inputs get theirs in the gather).
+    norm_chunk_partial<W>(tag_s, wave, red_s);
+    lds_barrier_p();
+
+    // The next phase's input. An input that is RMS-normalised (W values, one
+    // 1 KB chunk per wave) is gathered by all eight waves (wave 0 also copies
+    // the constants `pre` names), each polling its chunk whole and adding
+    // that chunk's part of the square sum as soon as it is in; the quantised
+    // attention output is gathered by the memory waves (a quarter each) while
+    // the compute waves stage weight slices.
+    auto gather_norm = [&](const u64* src, uint32_t gn, auto pre) {
+      constexpr int parts = W / 128;
+      bool ok = true;
+      if (wave < parts) {
+        ok = wave == 0 ? gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, pre, wave, parts)
+                       : gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, NoPre{}, wave, parts);
+        if (ok) norm_chunk_partial<W>(tag_s, wave, red_s);
+      } else if (lane == 0) {
+        red_s[wave] = 0.0;
+      }
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+    };
+    auto gather_q = [&](const u64* src, int count, uint32_t gn) {
+      bool ok = true;
+      if (ct < 0)
+        ok = gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gn), tag_s, a.error, NoPre{}, wave, 4, NoChunk{},
+                    nullptr, kQTagMask);
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+    };
+    auto gathered = [&] {
+      lds_barrier_p();
+      t_in = __builtin_amdgcn_s_memrealtime();
+      int all = 1;
+#pragma unroll
+      for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
+      return all != 0;
+    };
+    // Long caches, after the q/k/v publication of layer l: this workgroup's
+    // share [t0, t1) of the earlier positions of kv head fx, scored against
+    // both of its query heads (lane pair per position, the attention
+    // workgroups' arithmetic: QK-norm + RoPE of each q by one wave, then
+    // pair_score), stored as tagged words; the last share also tags the
+    // words up to the next multiple of 128, so that the attention
+    // workgroups gather whole chunks. The K rows are requested first, into
+    // the K/V area (free from P1's products until stage_window): row r of the
+    // share at byte 256 r, its 16-byte piece i at slot i ^ (r & 15).
+    static_assert(kLongPositions <= (kPT / 2) * NX && (kLongPositions + NX - 1) / NX * 256 <= kKvBytes,
+                  "one position per lane pair, the share's K rows in the K/V area");
+    auto score_earlier = [&](int l, auto rows_in) __attribute__((always_inline)) -> bool {
+      const auto& Ly = LT[l];
+      const int j = (w >> 3) - G;
+      const int t0 = pos * j / NX, t1 = pos * (j + 1) / NX;
+      const int h = tid & 1, r = tid >> 1, t = t0 + r;
+      {
+        const char* kb = reinterpret_cast<const char*>(a.kcache + ((size_t)l * HKV + fx) * a.capacity * HS) +
+                         (size_t)t0 * 256;
+        const int bytes = (t1 - t0) * 256;
+        for (int c = wave * 1024; c < bytes; c += kPT / kWave * 1024) {
+          const int b = c + 16 * lane, br = b >> 8;
+          if (b < bytes)
+            __builtin_amdgcn_global_load_lds(kb + (size_t)br * 256 + ((((b >> 4) & 15) ^ (br & 15)) << 4),
+                                             (lds_ptr)(kv_s + c), 16, 0, 0);
         }
-        if ((parts & 1) && l + 1 < L) stage_slice<W, SQ>(kv_s + OQ, LT[l + 1].wqkv, LT[l + 1].sqkv, rq.count, cl, qkv_at);
+      }
+      // q comes through this XCD's L2 (as to the attention workgroups), so
+      // it is polled at once, two reads in flight, without the cross-XCD
+      // gather delay; wave s takes query head G fx + s.
+      bool ok = true;
+      if (wave < G) {
+        if (wave == 0) {
+          dma(Ly.q_norm, norm_s, HS * 4);
+          dma(a.rope_cos + (size_t)pos * (HS / 2), norm_s + 2 * HS, HS * 2);
+          dma(a.rope_sin + (size_t)pos * (HS / 2), norm_s + 2 * HS + HS / 2, HS * 2);
+        }
+        ok = poll_words<HS>(a.tqkv + (size_t)(G * fx + wave) * HS, gen(l, 1), tag_s + wave * HS, a.error, nullptr);
+      }
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      if (!gathered()) return false;
+      if (wave < G) {
+        const float2 qn = head_norm_rope<true>(tag_value(tag_s, wave * HS + lane), tag_value(tag_s, wave * HS + HS / 2 + lane),
+                                         norm_s, norm_s + 2 * HS, a.eps);
+        cur_s[wave][lane] = qn.x;
+        cur_s[wave][HS / 2 + lane] = qn.y;
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's K rows
+      lds_barrier_p();
+      rows_in();
+      if (t < t1) {
+        uint2 kk[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) kk[i] = *reinterpret_cast<const uint2*>(kv_s + r * 256 + 8 * h + ((i ^ (r & 15)) << 4));
+#pragma unroll
+        for (int s = 0; s < G; ++s) {
+          float qr[64];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(&cur_s[s][8 * i + 4 * h]);
+            qr[4 * i] = v.x;
+            qr[4 * i + 1] = v.y;
+            qr[4 * i + 2] = v.z;
+            qr[4 * i + 3] = v.w;
+          }
+          const float sd = pair_score(kk, qr, h, a.divisor);
+          if (h == (s & 1)) {
+            u64* dst = a.tscore + (size_t)(G * fx + s) * a.score_stride + t;
+            if (a.local_l2) tag_store_local(dst, gen(l, 1), sd);
+            else tag_store(dst, gen(l, 1), sd);
+          }
+        }
+      }
+      const int pad = ((pos + 127) & ~127) - pos;
+      if (j == NX - 1 && pad > 0) {
+        for (int i = tid; i < G * pad; i += kPT) {
+          u64* dst = a.tscore + (size_t)(G * fx + i / pad) * a.score_stride + pos + i % pad;
+          if (a.local_l2) tag_store_local(dst, gen(l, 1), 0.0f);
+          else tag_store(dst, gen(l, 1), 0.0f);
+        }
+      }
+      return true;
+    };
+
+    // Long caches, value workgroups: projection workgroup j < G HS / kValCh
+    // of XCD fx < HKV takes query head vhq = G fx + j / (HS / kValCh) and its
+    // channels [kValCh vb, +kValCh), vb = j % (HS / kValCh): the time-ordered
+    // value sums over the earlier positions (AttentionAvx.cs:173-224), one
+    // chain per channel, from the probabilities the attention workgroup
+    // publishes, then the block quantised for the o projection. Chains of
+    // different channels are independent, so spreading them over
+    // workgroups keeps the reference's order. Waves: 0 adds (one add per
+    // position and chain), 1 streams the V slice and 2 the probabilities
+    // through a ring of kValSlots blocks at the end of the K/V area (each
+    // wave waiting on its own load counter), 3 and 5-7 form the products
+    // p v of the block two ahead into a three-slot product ring (at OG,
+    // where gate/up and down are staged afterwards), 4 (sharing the adding
+    // wave's SIMD) checks the probabilities' tags.
+    constexpr int kValBlocks = HS / kValCh;
+    static_assert(HS % kValCh == 0 && G * kValBlocks <= NX, "one value workgroup per (query head, block)");
+    static_assert(OG + 3 * kValPSlot <= kValRing && (kLongPositions + NX - 1) / NX * 256 <= kValRing && OO <= OG,
+                  "value buffers clear of the o and q/k/v slices and of the score K rows");
+    // The value role's block, query head and block count, recomputed where
+    // used (opaque inputs keep them out of registers across the layer loop,
+    // whose register budget is full).
+    struct ValRole {
+      int vb, vhq, nvb;
+    };
+    auto val_role = [&]() __attribute__((always_inline)) {
+      int ww = w, pp = pos;
+      asm volatile("" : "+s"(ww), "+s"(pp));
+      const int vj = (ww >> 3) - G;
+      return ValRole{vj % kValBlocks, G * (ww & 7) + vj / kValBlocks, (pp + kValPos - 1) / kValPos};
+    };
+    using lds_char = __attribute__((address_space(3))) char;
+    auto vslot = [&](int k) { return (lds_char*)(kv_s + kValRing + (k % kValSlots) * kValSlot); };
+    // Wave 1: the V slice of block k (rows past pos - 1 repeat it, never used).
+    auto v_issue = [&](int l, int k, const ValRole& r) __attribute__((always_inline)) {
+      const char* src =
+          reinterpret_cast<const char*>(a.vcache + ((size_t)l * HKV + fx) * a.capacity * HS) + 2 * kValCh * r.vb;
+      lds_char* dst = vslot(k);
+#pragma unroll
+      for (int i = 0; i < kValVBytes / 1024; ++i) {
+        const int t = min(k * kValPos + 16 * i + (lane >> 2), pos - 1);
+        __builtin_amdgcn_global_load_lds(src + (size_t)t * (2 * HS) + 16 * (lane & 3), (lds_ptr)(dst + i * 1024), 16, 0, 0);
+      }
+    };
+    auto value_prefetch = [&](int l) __attribute__((always_inline)) {  // wave 1, once the score K rows are in LDS
+      const ValRole r = val_role();
+      for (int k = 0; k < min(kValSlots, r.nvb); ++k) v_issue(l, k, r);
+    };
+    auto value_sums = [&](int l) __attribute__((always_inline)) -> bool {
+      const ValRole r = val_role();
+      const int vb = r.vb, vhq = r.vhq, nvb = r.nvb;
+      float* vprod = reinterpret_cast<float*>(kv_s + OG);
+      // Wave 2 (and 4 on a retry): the tagged probabilities of block k.
+      auto p_issue = [&](int k) {
+        const u64* src = a.tscore + (size_t)vhq * a.score_stride + (size_t)k * kValPos;
+        if (lane < kValPos / 2) __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(vslot(k) + kValVBytes), 16, 0, 16);
       };
-      // Layer-0 input: a host row or the embedding of the device token
-      // (QwenDecoder.Embed, Gguf.cs:340-344). Its loads go first so that they
-      // do not wait behind the weight slices.
-      constexpr int XI = W / kPT;
-      int8_t eq[XI];
-      _Float16 es[XI];
-      float xr[XI];
-      if (a.mode == 2) {
-        int token = *a.token;
-        if (token < 0 || token >= a.vocab) token = 0;
-  #pragma unroll
-        for (int k = 0; k < XI; ++k) {
-          const size_t at = (size_t)token * W + tid + k * kPT;
-          eq[k] = a.embed_q[at];
-          es[k] = a.embed_s[at / 32];
+      // Block k's probabilities of positions below pos all current; stale
+      // ones (the ready pair came first) are read again.
+      auto p_settle = [&](int k) -> bool {
+        const uint32_t g = gen(l, 2);
+        for (long spin = 0;; ++spin) {
+          bool ok = true;
+          if (lane < kValPos / 2) {
+            const uint4 t = lds_read16_nodma(vslot(k) + kValVBytes + 16 * lane);
+            const int t0 = k * kValPos + 2 * lane;
+            ok = (t0 >= pos || t.y == g) && (t0 + 1 >= pos || t.w == g);
+          }
+          if (__all(ok)) return true;
+          if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(a.error))) {
+            if (lane == 0) __hip_atomic_fetch_or(a.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            return false;
+          }
+          p_issue(k);
+          __builtin_amdgcn_s_waitcnt(0);
+        }
+      };
+      // Products of block k: task (four positions, channel pair), 16 x 16
+      // per block over the 256 lanes of waves 3, 5, 6, 7; rows 2cp and
+      // 2cp + 1 of the product slot, four positions as one float4.
+      // Positions from pos on get +0, so that every block adds 64 products:
+      // acc + 0 is acc, since a sum from +0 is never -0.
+      auto produce = [&](int k) {
+        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+        using lds_u32 = const __attribute__((address_space(3))) uint32_t;
+        using lds_u4 = const __attribute__((address_space(3))) u32x4;
+        const lds_char* vsl = vslot(k);
+        float* pr = vprod + (k % 3) * (kValPSlot / 4);
+        // The lane's offsets are recomputed each block rather than kept in
+        // registers across the loop.
+        int lp = (wave == 3 ? 0 : wave - 4) * kWave + lane;
+        asm volatile("" : "+v"(lp));
+        const int quad = lp >> 4, cp = lp & 15;
+        const u32x4 w0 = *(lds_u4*)(vsl + kValVBytes + 32 * quad);
+        const u32x4 w1 = *(lds_u4*)(vsl + kValVBytes + 32 * quad + 16);
+        uint32_t d[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) d[u] = *(lds_u32*)(vsl + (4 * quad + u) * (2 * kValCh) + 4 * cp);
+        // All six reads in flight before the first product.
+        __builtin_amdgcn_sched_barrier(0);
+        const float p[4] = {u2f(w0.x), u2f(w0.z), u2f(w1.x), u2f(w1.z)};
+        float lo[4], hi[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          lo[u] = fmul(from_half(__builtin_bit_cast(_Float16, (uint16_t)d[u])), p[u]);
+          hi[u] = fmul(from_half(__builtin_bit_cast(_Float16, (uint16_t)(d[u] >> 16))), p[u]);
+        }
+        if ((k + 1) * kValPos > pos) {
+          // The last block: +0 (all bits clear) from pos on, without branches.
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const uint32_t keep = 0u - (uint32_t)(k * kValPos + 4 * quad + u < pos);
+            lo[u] = u2f(f2u(lo[u]) & keep);
+            hi[u] = u2f(f2u(hi[u]) & keep);
+          }
+        }
+        *reinterpret_cast<float4*>(pr + (2 * cp) * kValRow + 4 * quad) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+        *reinterpret_cast<float4*>(pr + (2 * cp + 1) * kValRow + 4 * quad) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+      };
+      const bool producer = wave == 3 || wave >= 5;
+      lds_barrier_nodma();  // every wave's score K rows read: the value buffers and the q/k/v slice overlap them
+      if (ct >= 0) stage_window(l, 1);
+      u64* rdy = tag_s + 2048;  // the ready pair: p[pos]
+      u64* vcw = tag_s + 2176;  // this position's v, this block's channels
+      // Blocks in the ring; the last one whose V (and probabilities) the
+      // prologue waits for; the last one whose probabilities it waits for.
+      const int m = min(kValSlots, nvb), first = min(2, nvb - 1), pfirst = min(3, nvb - 1);
+      bool ok = true;
+      if (wave == 0) {
+        ok = poll_words<kValCh>(a.tqkv + QW + KVW + fx * HS + kValCh * vb, gen(l, 1), vcw, a.error, nullptr);
+      } else if (wave == 1) {
+        if (nvb > 0) vm_wait<4 * kValSlots>(4 * (m - 1 - first));
+      } else if (wave == 2) {
+        ok = poll_words<2>(a.tready + 2 * vhq, gen(l, 2), rdy, a.error, nullptr);
+        if (ok && nvb > 0) {
+          for (int k = 0; k < m; ++k) p_issue(k);
+          vm_wait<kValSlots>(m - 1 - pfirst);
+          for (int k = 0; ok && k <= first; ++k) ok = p_settle(k);
+        }
+      }
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      lds_barrier_nodma();
+      {
+        int all = 1;
+#pragma unroll
+        for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
+        if (!all) return false;
+      }
+      if (producer)
+        for (int k = 0; k < min(2, nvb); ++k) produce(k);
+      lds_barrier_nodma();
+      // Block j: wave 0 adds slot j % 3 (reading the next block's groups as
+      // it goes, from block j + 1's slot, formed the step before), the
+      // producers form block j + 2, waves 1 and 2 issue block j + kValSlots
+      // into block j's ring slot (its products were formed two steps ago)
+      // and wait for blocks j + 3 (V) and j + 4 (probabilities), wave 4
+      // checks block j + 3's probabilities. Each role runs its own loop, one
+      // barrier a block, so that no role's registers are live in another's.
+      float acc = 0.0f;
+      if (wave == 0) {
+        auto load_group = [&](int j, int g, float4* dst) {
+          const float* row = vprod + (j % 3) * (kValPSlot / 4) + (lane & (kValCh - 1)) * kValRow + 16 * g;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) dst[k] = *reinterpret_cast<const float4*>(row + 4 * k);
+        };
+        // The whole block in registers: group i of the next block is read
+        // as soon as group i of this one is added (stale past the last
+        // block, never added), three groups ahead of its use.
+        float4 q[4][4];
+        if (lane < kValCh)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) load_group(0, g, q[g]);
+        for (int j = 0; j < nvb; ++j) {
+          if (lane < kValCh) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                acc = fadd(acc, q[i][k].x);
+                acc = fadd(acc, q[i][k].y);
+                acc = fadd(acc, q[i][k].z);
+                acc = fadd(acc, q[i][k].w);
+              }
+              __builtin_amdgcn_sched_barrier(0);
+              load_group(j + 1, i, q[i]);
+            }
+          }
+          // Its reads in flight are of slots j and j + 1, which the
+          // producers overwrite two and three steps on.
+          lds_barrier_nodma<true>();
+        }
+      } else if (wave == 1) {
+        for (int j = 0; j < nvb; ++j) {
+          if (j + kValSlots < nvb) v_issue(l, j + kValSlots, r);
+          if (j + 3 < nvb) vm_wait<4 * kValSlots>(4 * (min(j + kValSlots, nvb - 1) - (j + 3)));
+          lds_barrier_nodma();
+        }
+      } else if (wave == 2) {
+        // Block j + 4 in LDS by the end of step j.
+        for (int j = 0; j < nvb; ++j) {
+          if (j + kValSlots < nvb) p_issue(j + kValSlots);
+          if (j + 4 < nvb) vm_wait<kValSlots>(min(j + kValSlots, nvb - 1) - (j + 4));
+          lds_barrier_nodma();
+        }
+      } else if (wave == 4) {
+        // Block j + 3's probabilities (in LDS since step j - 1) all current
+        // before the producers read them in step j + 1; stale ones are read
+        // again (with this wave's own loads).
+        for (int j = 0; j < nvb; ++j) {
+          if (ok && j + 3 < nvb) ok = p_settle(j + 3);
+          lds_barrier_nodma();
         }
       } else {
-  #pragma unroll
-        for (int k = 0; k < XI; ++k) xr[k] = a.x_in[tid + k * kPT];
-      }
-      if (ct >= 0) {
-        stage_slice<W, SQ>(kv_s + OQ, LT[0].wqkv, LT[0].sqkv, rq.count, ct, qkv_at);
-      } else if (wave == 0) {
-        dma(LT[0].attn_norm, norm_s, W * 4);
-        __builtin_amdgcn_s_waitcnt(0);
-      }
-  #pragma unroll
-      for (int k = 0; k < XI; ++k)
-        tag_s[tid + k * kPT] = (u64)f2u(a.mode == 2 ? fmul((float)eq[k], (float)es[k]) : xr[k]);
-      lds_barrier_p();
-      // The layer-0 input's norm partials (later inputs get theirs in the gather).
-      norm_chunk_partial<W>(tag_s, wave, red_s);
-      lds_barrier_p();
-
-      // The next phase's input. An input that is RMS-normalised (W values, one
-      // 1 KB chunk per wave) is gathered by all eight waves (wave 0 also copies
-      // the constants `pre` names), each polling its chunk whole and adding
-      // that chunk's part of the square sum as soon as it is in; the quantised
-      // attention output is gathered by the memory waves (a quarter each) while
-      // the compute waves stage weight slices.
-      auto gather_norm = [&](const u64* src, uint32_t gn, auto pre) {
-        constexpr int parts = W / 128;
-        bool ok = true;
-        if (wave < parts) {
-          ok = wave == 0 ? gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, pre, wave, parts)
-                         : gather(src, W, 0, nullptr, 0, 0, nullptr, 0, 0, gn, tag_s, a.error, NoPre{}, wave, parts);
-          if (ok) norm_chunk_partial<W>(tag_s, wave, red_s);
-        } else if (lane == 0) {
-          red_s[wave] = 0.0;
+        for (int j = 0; j < nvb; ++j) {
+          if (producer && j + 2 < nvb) produce(j + 2);
+          lds_barrier_nodma();
         }
-        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
-      };
-      auto gather_q = [&](const u64* src, int count, uint32_t gn) {
-        bool ok = true;
-        if (ct < 0)
-          ok = gather(src, count, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gn), tag_s, a.error, NoPre{}, wave, 4, NoChunk{},
-                      nullptr, kQTagMask);
-        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
-      };
-      auto gathered = [&] {
-        lds_barrier_p();
-        t_in = __builtin_amdgcn_s_memrealtime();
+      }
+      if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      if (wave == 0 && lane < kValCh) {
+        // This position's term, then the block's values for quantisation.
+        const float vc = from_half(to_half(tag_value(vcw, lane)));
+        acc = fadd(acc, fmul(vc, tag_value(rdy, 0)));
+        cur_s[2][lane] = acc;
+      }
+      lds_barrier_p();
+      {
         int all = 1;
-  #pragma unroll
+#pragma unroll
         for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
-        return all != 0;
-      };
-      // Long caches, after the q/k/v publication of layer l: this workgroup's
-      // share [t0, t1) of the earlier positions of kv head fx, scored against
-      // both of its query heads (lane pair per position, the attention
-      // workgroups' arithmetic: QK-norm + RoPE of each q by one wave, then
-      // pair_score), stored as tagged words; the last share also tags the
-      // words up to the next multiple of 128, so that the attention
-      // workgroups gather whole chunks. The K rows are requested first, into
-      // the K/V area (free from P1's products until stage_window): row r of the
-      // share at byte 256 r, its 16-byte piece i at slot i ^ (r & 15).
-      static_assert(kLongPositions <= (kPT / 2) * NX && (kLongPositions + NX - 1) / NX * 256 <= kKvBytes,
-                    "one position per lane pair, the share's K rows in the K/V area");
-      auto score_earlier = [&](int l, auto rows_in) __attribute__((always_inline)) -> bool {
-        const auto& Ly = LT[l];
-        const int j = (w >> 3) - G;
-        const int t0 = pos * j / NX, t1 = pos * (j + 1) / NX;
-        const int h = tid & 1, r = tid >> 1, t = t0 + r;
-        {
-          const char* kb = reinterpret_cast<const char*>(a.kcache + ((size_t)l * HKV + fx) * a.capacity * HS) +
-                           (size_t)t0 * 256;
-          const int bytes = (t1 - t0) * 256;
-          for (int c = wave * 1024; c < bytes; c += kPT / kWave * 1024) {
-            const int b = c + 16 * lane, br = b >> 8;
-            if (b < bytes)
-              __builtin_amdgcn_global_load_lds(kb + (size_t)br * 256 + ((((b >> 4) & 15) ^ (br & 15)) << 4),
-                                               (lds_ptr)(kv_s + c), 16, 0, 0);
-          }
-        }
-        // q comes through this XCD's L2 (as to the attention workgroups), so
-        // it is polled at once, two reads in flight, without the cross-XCD
-        // gather delay; wave s takes query head G fx + s.
-        bool ok = true;
-        if (wave < G) {
-          if (wave == 0) {
-            dma(Ly.q_norm, norm_s, HS * 4);
-            dma(a.rope_cos + (size_t)pos * (HS / 2), norm_s + 2 * HS, HS * 2);
-            dma(a.rope_sin + (size_t)pos * (HS / 2), norm_s + 2 * HS + HS / 2, HS * 2);
-          }
-          ok = poll_words<HS>(a.tqkv + (size_t)(G * fx + wave) * HS, gen(l, 1), tag_s + wave * HS, a.error, nullptr);
-        }
-        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
-        if (!gathered()) return false;
-        if (wave < G) {
-          const float2 qn = head_norm_rope<true>(tag_value(tag_s, wave * HS + lane), tag_value(tag_s, wave * HS + HS / 2 + lane),
-                                           norm_s, norm_s + 2 * HS, a.eps);
-          cur_s[wave][lane] = qn.x;
-          cur_s[wave][HS / 2 + lane] = qn.y;
-        }
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's K rows
-        lds_barrier_p();
-        rows_in();
-        if (t < t1) {
-          uint2 kk[16];
-  #pragma unroll
-          for (int i = 0; i < 16; ++i) kk[i] = *reinterpret_cast<const uint2*>(kv_s + r * 256 + 8 * h + ((i ^ (r & 15)) << 4));
-  #pragma unroll
-          for (int s = 0; s < G; ++s) {
-            float qr[64];
-  #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const float4 v = *reinterpret_cast<const float4*>(&cur_s[s][8 * i + 4 * h]);
-              qr[4 * i] = v.x;
-              qr[4 * i + 1] = v.y;
-              qr[4 * i + 2] = v.z;
-              qr[4 * i + 3] = v.w;
-            }
-            const float sd = pair_score(kk, qr, h, a.divisor);
-            if (h == (s & 1)) {
-              u64* dst = a.tscore + (size_t)(G * fx + s) * a.score_stride + t;
-              if (a.local_l2) tag_store_local(dst, gen(l, 1), sd);
-              else tag_store(dst, gen(l, 1), sd);
-            }
-          }
-        }
-        const int pad = ((pos + 127) & ~127) - pos;
-        if (j == NX - 1 && pad > 0) {
-          for (int i = tid; i < G * pad; i += kPT) {
-            u64* dst = a.tscore + (size_t)(G * fx + i / pad) * a.score_stride + pos + i % pad;
-            if (a.local_l2) tag_store_local(dst, gen(l, 1), 0.0f);
-            else tag_store(dst, gen(l, 1), 0.0f);
-          }
-        }
-        return true;
-      };
-
-      // Long caches, value workgroups: projection workgroup j < G HS / kValCh
-      // of XCD fx < HKV takes query head vhq = G fx + j / (HS / kValCh) and its
-      // channels [kValCh vb, +kValCh), vb = j % (HS / kValCh): the time-ordered
-      // value sums over the earlier positions (AttentionAvx.cs:173-224), one
-      // chain per channel, from the probabilities the attention workgroup
-      // publishes, then the block quantised for the o projection. Chains of
-      // different channels are independent, so spreading them over
-      // workgroups keeps the reference's order. Waves: 0 adds (one add per
-      // position and chain), 1 streams the V slice and 2 the probabilities
-      // through a ring of kValSlots blocks at the end of the K/V area (each
-      // wave waiting on its own load counter), 3 and 5-7 form the products
-      // p v of the block two ahead into a three-slot product ring (at OG,
-      // where gate/up and down are staged afterwards), 4 (sharing the adding
-      // wave's SIMD) checks the probabilities' tags.
-      constexpr int kValBlocks = HS / kValCh;
-      static_assert(HS % kValCh == 0 && G * kValBlocks <= NX, "one value workgroup per (query head, block)");
-      static_assert(OG + 3 * kValPSlot <= kValRing && (kLongPositions + NX - 1) / NX * 256 <= kValRing && OO <= OG,
-                    "value buffers clear of the o and q/k/v slices and of the score K rows");
-      // The value role's block, query head and block count, recomputed where
-      // used (opaque inputs keep them out of registers across the layer loop,
-      // whose register budget is full).
-      struct ValRole {
-        int vb, vhq, nvb;
-      };
-      auto val_role = [&]() __attribute__((always_inline)) {
-        int ww = w, pp = pos;
-        asm volatile("" : "+s"(ww), "+s"(pp));
-        const int vj = (ww >> 3) - G;
-        return ValRole{vj % kValBlocks, G * (ww & 7) + vj / kValBlocks, (pp + kValPos - 1) / kValPos};
-      };
-      using lds_char = __attribute__((address_space(3))) char;
-      auto vslot = [&](int k) { return (lds_char*)(kv_s + kValRing + (k % kValSlots) * kValSlot); };
-      // Wave 1: the V slice of block k (rows past pos - 1 repeat it, never used).
-      auto v_issue = [&](int l, int k, const ValRole& r) __attribute__((always_inline)) {
-        const char* src =
-            reinterpret_cast<const char*>(a.vcache + ((size_t)l * HKV + fx) * a.capacity * HS) + 2 * kValCh * r.vb;
-        lds_char* dst = vslot(k);
-  #pragma unroll
-        for (int i = 0; i < kValVBytes / 1024; ++i) {
-          const int t = min(k * kValPos + 16 * i + (lane >> 2), pos - 1);
-          __builtin_amdgcn_global_load_lds(src + (size_t)t * (2 * HS) + 16 * (lane & 3), (lds_ptr)(dst + i * 1024), 16, 0, 0);
-        }
-      };
-      auto value_prefetch = [&](int l) __attribute__((always_inline)) {  // wave 1, once the score K rows are in LDS
-        const ValRole r = val_role();
-        for (int k = 0; k < min(kValSlots, r.nvb); ++k) v_issue(l, k, r);
-      };
-      auto value_sums = [&](int l) __attribute__((always_inline)) -> bool {
-        const ValRole r = val_role();
-        const int vb = r.vb, vhq = r.vhq, nvb = r.nvb;
-        float* vprod = reinterpret_cast<float*>(kv_s + OG);
-        // Wave 2 (and 4 on a retry): the tagged probabilities of block k.
-        auto p_issue = [&](int k) {
-          const u64* src = a.tscore + (size_t)vhq * a.score_stride + (size_t)k * kValPos;
-          if (lane < kValPos / 2) __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)(vslot(k) + kValVBytes), 16, 0, 16);
-        };
-        // Block k's probabilities of positions below pos all current; stale
-        // ones (the ready pair came first) are read again.
-        auto p_settle = [&](int k) -> bool {
-          const uint32_t g = gen(l, 2);
-          for (long spin = 0;; ++spin) {
-            bool ok = true;
-            if (lane < kValPos / 2) {
-              const uint4 t = lds_read16_nodma(vslot(k) + kValVBytes + 16 * lane);
-              const int t0 = k * kValPos + 2 * lane;
-              ok = (t0 >= pos || t.y == g) && (t0 + 1 >= pos || t.w == g);
-            }
-            if (__all(ok)) return true;
-            if (spin > kSpinLimit || ((spin & 63) == 63 && error_load(a.error))) {
-              if (lane == 0) __hip_atomic_fetch_or(a.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              __builtin_amdgcn_s_waitcnt(0);
-              return false;
-            }
-            p_issue(k);
-            __builtin_amdgcn_s_waitcnt(0);
-          }
-        };
-        // Products of block k: task (four positions, channel pair), 16 x 16
-        // per block over the 256 lanes of waves 3, 5, 6, 7; rows 2cp and
-        // 2cp + 1 of the product slot, four positions as one float4.
-        // Positions from pos on get +0, so that every block adds 64 products:
-        // acc + 0 is acc, since a sum from +0 is never -0.
-        auto produce = [&](int k) {
-          typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-          using lds_u32 = const __attribute__((address_space(3))) uint32_t;
-          using lds_u4 = const __attribute__((address_space(3))) u32x4;
-          const lds_char* vsl = vslot(k);
-          float* pr = vprod + (k % 3) * (kValPSlot / 4);
-          // The lane's offsets are recomputed each block rather than kept in
-          // registers across the loop.
-          int lp = (wave == 3 ? 0 : wave - 4) * kWave + lane;
-          asm volatile("" : "+v"(lp));
-          const int quad = lp >> 4, cp = lp & 15;
-          const u32x4 w0 = *(lds_u4*)(vsl + kValVBytes + 32 * quad);
-          const u32x4 w1 = *(lds_u4*)(vsl + kValVBytes + 32 * quad + 16);
-          uint32_t d[4];
-  #pragma unroll
-          for (int u = 0; u < 4; ++u) d[u] = *(lds_u32*)(vsl + (4 * quad + u) * (2 * kValCh) + 4 * cp);
-          // All six reads in flight before the first product.
-          __builtin_amdgcn_sched_barrier(0);
-          const float p[4] = {u2f(w0.x), u2f(w0.z), u2f(w1.x), u2f(w1.z)};
-          float lo[4], hi[4];
-  #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            lo[u] = fmul(from_half(__builtin_bit_cast(_Float16, (uint16_t)d[u])), p[u]);
-            hi[u] = fmul(from_half(__builtin_bit_cast(_Float16, (uint16_t)(d[u] >> 16))), p[u]);
-          }
-          if ((k + 1) * kValPos > pos) {
-            // The last block: +0 (all bits clear) from pos on, without branches.
-  #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const uint32_t keep = 0u - (uint32_t)(k * kValPos + 4 * quad + u < pos);
-              lo[u] = u2f(f2u(lo[u]) & keep);
-              hi[u] = u2f(f2u(hi[u]) & keep);
-            }
-          }
-          *reinterpret_cast<float4*>(pr + (2 * cp) * kValRow + 4 * quad) = make_float4(lo[0], lo[1], lo[2], lo[3]);
-          *reinterpret_cast<float4*>(pr + (2 * cp + 1) * kValRow + 4 * quad) = make_float4(hi[0], hi[1], hi[2], hi[3]);
-        };
-        const bool producer = wave == 3 || wave >= 5;
-        lds_barrier_nodma();  // every wave's score K rows read: the value buffers and the q/k/v slice overlap them
-        if (ct >= 0) stage_window(l, 1);
-        u64* rdy = tag_s + 2048;  // the ready pair: p[pos]
-        u64* vcw = tag_s + 2176;  // this position's v, this block's channels
-        // Blocks in the ring; the last one whose V (and probabilities) the
-        // prologue waits for; the last one whose probabilities it waits for.
-        const int m = min(kValSlots, nvb), first = min(2, nvb - 1), pfirst = min(3, nvb - 1);
-        bool ok = true;
-        if (wave == 0) {
-          ok = poll_words<kValCh>(a.tqkv + QW + KVW + fx * HS + kValCh * vb, gen(l, 1), vcw, a.error, nullptr);
-        } else if (wave == 1) {
-          if (nvb > 0) vm_wait<4 * kValSlots>(4 * (m - 1 - first));
-        } else if (wave == 2) {
-          ok = poll_words<2>(a.tready + 2 * vhq, gen(l, 2), rdy, a.error, nullptr);
-          if (ok && nvb > 0) {
-            for (int k = 0; k < m; ++k) p_issue(k);
-            vm_wait<kValSlots>(m - 1 - pfirst);
-            for (int k = 0; ok && k <= first; ++k) ok = p_settle(k);
-          }
-        }
-        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
-        lds_barrier_nodma();
-        {
-          int all = 1;
-  #pragma unroll
-          for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
-          if (!all) return false;
-        }
-        if (producer)
-          for (int k = 0; k < min(2, nvb); ++k) produce(k);
-        lds_barrier_nodma();
-        // Block j: wave 0 adds slot j % 3 (reading the next block's groups as
-        // it goes, from block j + 1's slot, formed the step before), the
-        // producers form block j + 2, waves 1 and 2 issue block j + kValSlots
-        // into block j's ring slot (its products were formed two steps ago)
-        // and wait for blocks j + 3 (V) and j + 4 (probabilities), wave 4
-        // checks block j + 3's probabilities. Each role runs its own loop, one
-        // barrier a block, so that no role's registers are live in another's.
-        float acc = 0.0f;
-        if (wave == 0) {
-          auto load_group = [&](int j, int g, float4* dst) {
-            const float* row = vprod + (j % 3) * (kValPSlot / 4) + (lane & (kValCh - 1)) * kValRow + 16 * g;
-  #pragma unroll
-            for (int k = 0; k < 4; ++k) dst[k] = *reinterpret_cast<const float4*>(row + 4 * k);
-          };
-          // The whole block in registers: group i of the next block is read
-          // as soon as group i of this one is added (stale past the last
-          // block, never added), three groups ahead of its use.
-          float4 q[4][4];
-          if (lane < kValCh)
-  #pragma unroll
-            for (int g = 0; g < 4; ++g) load_group(0, g, q[g]);
-          for (int j = 0; j < nvb; ++j) {
-            if (lane < kValCh) {
-  #pragma unroll
-              for (int i = 0; i < 4; ++i) {
-  #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                  acc = fadd(acc, q[i][k].x);
-                  acc = fadd(acc, q[i][k].y);
-                  acc = fadd(acc, q[i][k].z);
-                  acc = fadd(acc, q[i][k].w);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                load_group(j + 1, i, q[i]);
-              }
-            }
-            // Its reads in flight are of slots j and j + 1, which the
-            // producers overwrite two and three steps on.
-            lds_barrier_nodma<true>();
-          }
-        } else if (wave == 1) {
-          for (int j = 0; j < nvb; ++j) {
-            if (j + kValSlots < nvb) v_issue(l, j + kValSlots, r);
-            if (j + 3 < nvb) vm_wait<4 * kValSlots>(4 * (min(j + kValSlots, nvb - 1) - (j + 3)));
-            lds_barrier_nodma();
-          }
-        } else if (wave == 2) {
-          // Block j + 4 in LDS by the end of step j.
-          for (int j = 0; j < nvb; ++j) {
-            if (j + kValSlots < nvb) p_issue(j + kValSlots);
-            if (j + 4 < nvb) vm_wait<kValSlots>(min(j + kValSlots, nvb - 1) - (j + 4));
-            lds_barrier_nodma();
-          }
-        } else if (wave == 4) {
-          // Block j + 3's probabilities (in LDS since step j - 1) all current
-          // before the producers read them in step j + 1; stale ones are read
-          // again (with this wave's own loads).
-          for (int j = 0; j < nvb; ++j) {
-            if (ok && j + 3 < nvb) ok = p_settle(j + 3);
-            lds_barrier_nodma();
-          }
-        } else {
-          for (int j = 0; j < nvb; ++j) {
-            if (producer && j + 2 < nvb) produce(j + 2);
-            lds_barrier_nodma();
-          }
-        }
-        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
-        if (wave == 0 && lane < kValCh) {
-          // This position's term, then the block's values for quantisation.
-          const float vc = from_half(to_half(tag_value(vcw, lane)));
-          acc = fadd(acc, fmul(vc, tag_value(rdy, 0)));
-          cur_s[2][lane] = acc;
-        }
-        lds_barrier_p();
-        {
-          int all = 1;
-  #pragma unroll
-          for (int i = 0; i < kPT / kWave; ++i) all &= okw_s[i];
-          if (!all) return false;
-        }
-        if (wave == 0) {
-          float d;
-          const uint32_t qw = quantize_lane4(*reinterpret_cast<const float4*>(&cur_s[2][4 * (lane & 7)]), &d);
-          if (lane < 8) qword_store(a.tattq + 32 * vhq + 8 * vb + lane, gen(l, 2), qside(lane, d), qw);
-          // The output values themselves, for tracing.
-          if (lane < kValCh) tag_store(a.tatt + vhq * HS + kValCh * vb + lane, gen(l, 2), cur_s[2][lane]);
-          // The attention's publication time, on its attention workgroup's
-          // timeline (the latest of its value workgroups).
-          if (a.timeline && lane == 0)
-            __hip_atomic_fetch_max(a.timeline + (size_t)(fx + 8 * (vhq - G * fx)) * kTimelineEvents + 16 * l + 1 + 7,
-                                   (unsigned long long)__builtin_amdgcn_s_memrealtime(), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        }
-        return true;
-      };
-
-      // Each phase: all threads quantise (or unpack) the gathered input and
-      // form the block products of the LDS slice, then wave 0 sums the rows in
-      // order and publishes them, and the memory waves gather
-      // the next phase's input. After the q/k/v publication (and a barrier, so
-      // that the stores leave ahead of the burst) the compute waves stage the
-      // slices of the rest of the layer and the next layer's q/k/v.
-      // The layer loop. False when an exchange failed.
-      auto layers = [&]() __attribute__((always_inline)) -> bool {
-        for (int l = 0; l < L; ++l) {
-          const auto& Ly = LT[l];
-          const auto& Nx = LT[l + 1 < L ? l + 1 : l];
-          const int e = 16 * l + 1;
-          // ---- P1: attn_norm + qkv ----------------------------------------------
-          quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
-          if (ct >= 0 && l == 0) __builtin_amdgcn_s_waitcnt(0);  // layer 0's staged q/k/v slice
-          lds_barrier_p();
-          sub(0);
-          lds_products<NPQ, B1>(kv_s + OQ, rq.count, xq_s, xs_s, prod_s);
-          lds_barrier_p();
-          sub(1);
-          // This workgroup's residual rows of x (read in the o epilogue), while
-          // wave 0 sums the q/k/v rows; the gather area keeps x until the
-          // attention output arrives, after the next barrier.
-          if (wave == 1 && lane < ro.count) row_s[0][lane] = tag_value(tag_s, row_at(lane));
-          if (wave == 0) {
-            if (lane < rq.count) {
-              const float v = ordered_sum<B1>(prod_s, lane);
-              u64* dst = a.tqkv + qkv_row(rq.r0 + lane);
-              if (a.local_l2) tag_store_local(dst, gen(l, 1), v);
-              else tag_store(dst, gen(l, 1), v);
-            }
-            stamps(e + 0, e + 2, e + 1, 1);
-            if (tl && lane == 0) tl[e + 4] = t_sub[1];
-          }
-          lds_barrier_p();
-          if constexpr (VAL) {
-            if (!score_earlier(l, [&] {
-                  if (wave == 1) value_prefetch(l);
-                }))
-              return false;
-            if (!value_sums(l)) return false;
-            if (ct >= 0) stage_window(l, 2);
-          } else {
-            if (lng && fx < HKV && !score_earlier(l, [] {})) return false;
-            if (ct >= 0) stage_window(l, 3);
-          }
-          gather_q(a.tattq, QWA, gen(l, 2));
-          if (ct >= 0) __builtin_amdgcn_s_waitcnt(0);  // the staged slices are in LDS before the barrier
-          if (!gathered()) return false;
-
-          // ---- P3: o projection + residual -------------------------------------
-          unpack_qblocks<QW>(tag_s, xq_s, xs_s);
-          lds_barrier_p();
-          lds_products<NPO, Bq>(kv_s + OO, ro.count, xq_s, xs_s, prod_s);
-          lds_barrier_p();
-          if (wave == 0) {
-            if (lane < ro.count) {
-              const float v = fadd(ordered_sum<Bq>(prod_s, lane), row_s[0][lane]);
-              row_s[1][lane] = v;
-              tag_store(a.ta + row_at(lane), gen(l, 3), v);
-            }
-            stamps(e + 8, e + 9);
-          }
-          gather_norm(a.ta, gen(l, 3), [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
-          if (!gathered()) return false;
-
-          // ---- P4: ffn_norm + gate/up + SwiGLU -----------------------------------
-          quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
-          lds_barrier_p();
-          sub(0);
-          lds_products<NPG, B1>(kv_s + OG, 2 * rf.count, xq_s, xs_s, prod_s);
-          lds_barrier_p();
-          if (wave == 0) {
-            // Lanes [0, n) sum the gate rows, [n, 2n) the matching up rows.
-            const int nr = rf.count;
-            const float gs = lane < 2 * nr ? ordered_sum<B1>(prod_s, lane) : 0.0f;
-            const float u = __shfl(gs, lane + nr, kWave);
-            if (lane < nr) {
-              const float silu = fdiv(gs, fadd(1.0f, exp_ref(-gs)));
-              u64* dst = a.th + persistent_xcd_row(fx, rf.r0 + lane, 64);
-              if (a.local_l2) tag_store_local(dst, gen(l, 4), fmul(silu, u));
-              else tag_store(dst, gen(l, 4), fmul(silu, u));
-            }
-            stamps(e + 10, e + 12, e + 11, 1);
-          }
-          // The pair owners quantise their blocks (read through this XCD's L2)
-          // and publish them; every projection workgroup gathers the quantised
-          // vector.
-          // The quantised ffn vector (QWH / 128 <= 8 chunks) is gathered one
-          // chunk per wave, polled whole; wave 0 (the owner's publisher) and as
-          // few others as possible take none.
-          {
-            bool ok = true;
-            if (wave == 0 && own >= 0) {
-              u64 seen = 0;
-              ok = publish_pair(a.th, a.thq, own, gen(l, 4), tag_s + kTagWords - 64, a.error, &seen);
-              if (tl && lane == 0) {
-                tl[e + 6] = seen;
-                tl[e + 7] = __builtin_amdgcn_s_memrealtime();
-              }
-            }
-            if (ok)
-              ok = gather(a.thq, QWH, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gen(l, 4)), tag_s, a.error, NoPre{}, wave,
-                          kPT / kWave, NoChunk{}, nullptr, kQTagMask);
-            if (lane == 0) okw_s[wave] = ok ? 1 : 0;
-          }
-          if (!gathered()) return false;
-
-          // ---- P5: down projection + residual ------------------------------------
-          unpack_qblocks<FF>(tag_s, xq_s, xs_s);
-          lds_barrier_p();
-          sub(0);
-          lds_products<NPD, Bf>(kv_s + OD, ro.count, xq_s, xs_s, prod_s);
-          lds_barrier_p();
-          sub(1);
-          if (wave == 0) {
-            if (lane < ro.count) {
-              const float v = fadd(ordered_sum<Bf>(prod_s, lane), row_s[1][lane]);
-              tag_store(a.tx + row_at(lane), gen(l, 5), v);
-            }
-            stamps(e + 13, e + 15, e + 14, 1);
-            if (tl && lane == 0) tl[e + 5] = t_sub[1];
-          }
-          // Next layer's input with its attn_norm, or the lm_head input with output_norm.
-          const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
-          gather_norm(a.tx, gen(l, 5), [&] { dma(next_norm, norm_s, W * 4); });
-          if (!gathered()) return false;
-        }
-        return true;
-      };
-      return layers();
+        if (!all) return false;
+      }
+      if (wave == 0) {
+        float d;
+        const uint32_t qw = quantize_lane4(*reinterpret_cast<const float4*>(&cur_s[2][4 * (lane & 7)]), &d);
+        if (lane < 8) qword_store(a.tattq + 32 * vhq + 8 * vb + lane, gen(l, 2), qside(lane, d), qw);
+        // The output values themselves, for tracing.
+        if (lane < kValCh) tag_store(a.tatt + vhq * HS + kValCh * vb + lane, gen(l, 2), cur_s[2][lane]);
+        // The attention's publication time, on its attention workgroup's
+        // timeline (the latest of its value workgroups).
+        if (a.timeline && lane == 0)
+          __hip_atomic_fetch_max(a.timeline + (size_t)(fx + 8 * (vhq - G * fx)) * kTimelineEvents + 16 * l + 1 + 7,
+                                 (unsigned long long)__builtin_amdgcn_s_memrealtime(), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return true;
     };
+
+    // Each phase: all threads quantise (or unpack) the gathered input and
+    // form the block products of the LDS slice, then wave 0 sums the rows in
+    // order and publishes them, and the memory waves gather
+    // the next phase's input. After the q/k/v publication (and a barrier, so
+    // that the stores leave ahead of the burst) the compute waves stage the
+    // slices of the rest of the layer and the next layer's q/k/v.
+    // Value workgroups (long caches): the time-ordered value sums between
+    // the scores and the attention-output gather.
     const int pvj = (w >> 3) - G;
-    const bool valued = lng && (w & 7) < HKV && pvj >= 0 && pvj < G * (HS / kValCh);
-    if (valued ? !projection(std::true_type{}) : !projection(std::false_type{})) return;
+    const bool valued = lng && fx < HKV && pvj >= 0 && pvj < G * kValBlocks;
+    for (int l = 0; l < L; ++l) {
+      const auto& Ly = LT[l];
+      const auto& Nx = LT[l + 1 < L ? l + 1 : l];
+      const int e = 16 * l + 1;
+      // ---- P1: attn_norm + qkv ----------------------------------------------
+      quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
+      if (ct >= 0 && l == 0) __builtin_amdgcn_s_waitcnt(0);  // layer 0's staged q/k/v slice
+      lds_barrier_p();
+      sub(0);
+      lds_products<NPQ, B1>(kv_s + OQ, rq.count, xq_s, xs_s, prod_s);
+      lds_barrier_p();
+      sub(1);
+      // This workgroup's residual rows of x (read in the o epilogue), while
+      // wave 0 sums the q/k/v rows; the gather area keeps x until the
+      // attention output arrives, after the next barrier.
+      if (wave == 1 && lane < ro.count) row_s[0][lane] = tag_value(tag_s, row_at(lane));
+      if (wave == 0) {
+        if (lane < rq.count) {
+          const float v = ordered_sum<B1>(prod_s, lane);
+          u64* dst = a.tqkv + qkv_row(rq.r0 + lane);
+          if (a.local_l2) tag_store_local(dst, gen(l, 1), v);
+          else tag_store(dst, gen(l, 1), v);
+        }
+        stamps(e + 0, e + 2, e + 1, 1);
+        if (tl && lane == 0) tl[e + 4] = t_sub[1];
+      }
+      lds_barrier_p();
+      if (valued) {
+        if (!score_earlier(l, [&] {
+              if (wave == 1) value_prefetch(l);
+            }))
+          return;
+        if (!value_sums(l)) return;
+        if (ct >= 0) stage_window(l, 2);
+      } else {
+        if (lng && fx < HKV && !score_earlier(l, [] {})) return;
+        if (ct >= 0) stage_window(l, 3);
+      }
+      gather_q(a.tattq, QWA, gen(l, 2));
+      if (ct >= 0) __builtin_amdgcn_s_waitcnt(0);  // the staged slices are in LDS before the barrier
+      if (!gathered()) return;
+
+      // ---- P3: o projection + residual -------------------------------------
+      unpack_qblocks<QW>(tag_s, xq_s, xs_s);
+      lds_barrier_p();
+      lds_products<NPO, Bq>(kv_s + OO, ro.count, xq_s, xs_s, prod_s);
+      lds_barrier_p();
+      if (wave == 0) {
+        if (lane < ro.count) {
+          const float v = fadd(ordered_sum<Bq>(prod_s, lane), row_s[0][lane]);
+          row_s[1][lane] = v;
+          tag_store(a.ta + row_at(lane), gen(l, 3), v);
+        }
+        stamps(e + 8, e + 9);
+      }
+      gather_norm(a.ta, gen(l, 3), [&] { dma(Ly.ffn_norm, norm_s, W * 4); });
+      if (!gathered()) return;
+
+      // ---- P4: ffn_norm + gate/up + SwiGLU -----------------------------------
+      quantize_norm_chunks<W>(tag_s, norm_s, a.eps, red_s, xq_s, xs_s);
+      lds_barrier_p();
+      sub(0);
+      lds_products<NPG, B1>(kv_s + OG, 2 * rf.count, xq_s, xs_s, prod_s);
+      lds_barrier_p();
+      if (wave == 0) {
+        // Lanes [0, n) sum the gate rows, [n, 2n) the matching up rows.
+        const int nr = rf.count;
+        const float gs = lane < 2 * nr ? ordered_sum<B1>(prod_s, lane) : 0.0f;
+        const float u = __shfl(gs, lane + nr, kWave);
+        if (lane < nr) {
+          const float silu = fdiv(gs, fadd(1.0f, exp_ref(-gs)));
+          u64* dst = a.th + persistent_xcd_row(fx, rf.r0 + lane, 64);
+          if (a.local_l2) tag_store_local(dst, gen(l, 4), fmul(silu, u));
+          else tag_store(dst, gen(l, 4), fmul(silu, u));
+        }
+        stamps(e + 10, e + 12, e + 11, 1);
+      }
+      // The pair owners quantise their blocks (read through this XCD's L2)
+      // and publish them; every projection workgroup gathers the quantised
+      // vector.
+      // The quantised ffn vector (QWH / 128 <= 8 chunks) is gathered one
+      // chunk per wave, polled whole; wave 0 (the owner's publisher) and as
+      // few others as possible take none.
+      {
+        bool ok = true;
+        if (wave == 0 && own >= 0) {
+          u64 seen = 0;
+          ok = publish_pair(a.th, a.thq, own, gen(l, 4), tag_s + kTagWords - 64, a.error, &seen);
+          if (tl && lane == 0) {
+            tl[e + 6] = seen;
+            tl[e + 7] = __builtin_amdgcn_s_memrealtime();
+          }
+        }
+        if (ok)
+          ok = gather(a.thq, QWH, 0, nullptr, 0, 0, nullptr, 0, 0, qtag(gen(l, 4)), tag_s, a.error, NoPre{}, wave,
+                      kPT / kWave, NoChunk{}, nullptr, kQTagMask);
+        if (lane == 0) okw_s[wave] = ok ? 1 : 0;
+      }
+      if (!gathered()) return;
+
+      // ---- P5: down projection + residual ------------------------------------
+      unpack_qblocks<FF>(tag_s, xq_s, xs_s);
+      lds_barrier_p();
+      sub(0);
+      lds_products<NPD, Bf>(kv_s + OD, ro.count, xq_s, xs_s, prod_s);
+      lds_barrier_p();
+      sub(1);
+      if (wave == 0) {
+        if (lane < ro.count) {
+          const float v = fadd(ordered_sum<Bf>(prod_s, lane), row_s[1][lane]);
+          tag_store(a.tx + row_at(lane), gen(l, 5), v);
+        }
+        stamps(e + 13, e + 15, e + 14, 1);
+        if (tl && lane == 0) tl[e + 5] = t_sub[1];
+      }
+      // Next layer's input with its attn_norm, or the lm_head input with output_norm.
+      const float* next_norm = l + 1 < L ? Nx.attn_norm : a.output_norm;
+      gather_norm(a.tx, gen(l, 5), [&] { dma(next_norm, norm_s, W * 4); });
+      if (!gathered()) return;
+    }
   }
 
   if (a.mode == 0) {
