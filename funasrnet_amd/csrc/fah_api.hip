@@ -1877,8 +1877,10 @@ int fah_decoder_create(fah_context* h, const fah_decoder_config* cfg, const fah_
     require(k.heads == 2 * k.kv_heads, "the paired GQA path needs heads == 2 * kv_heads");
     require(k.width % 32 == 0 && k.ffn % 32 == 0, "widths must be multiples of 32");
     int q_width = k.heads * k.head_size, kv_width = k.kv_heads * k.head_size;
-    int maxk = fah::gemv_max_k();
-    require(k.width <= maxk && k.ffn <= maxk && q_width <= maxk, "projection width exceeds kernel limit");
+    // The ffn width (the down projection's K) up to the GEMV's limit; the
+    // model width and q width up to 4096 (the norm, embedding and attention
+    // kernels hold rows of that width).
+    require(k.width <= 4096 && q_width <= 4096 && k.ffn <= fah::gemv_max_k(), "projection width exceeds kernel limit");
     require(k.capacity >= 1 && fah::attention_slices(k.capacity, k.head_size) != 0,
             "capacity exceeds the attention kernel's LDS budget");
     for (int l = 0; l < k.layers; ++l) {

@@ -17,7 +17,8 @@ namespace fah {
 
 constexpr int kThreads = 256;
 using lds_ptr = __attribute__((address_space(3))) void*;
-constexpr int kMaxK = 4096;
+constexpr int kMaxK = 4096;       // K held in registers in 4 chunks (the decoder's projections)
+constexpr int kMaxKLarge = 16384; // wider inputs (larger models' down projection): 16 chunks
 
 struct ScaleHalf {
   using type = _Float16;
@@ -28,12 +29,12 @@ struct ScaleFloat {
   static __device__ __forceinline__ float get(type v) { return v; }
 };
 
-constexpr int kMaxChunks = kMaxK / (4 * kThreads);  // K = chunks * 1024: 4 values per lane per chunk
-
-template <typename Scale, int IN, int OUT, int PAIRS>
+// CH: chunks of 4 * kThreads values, K <= CH * 1024.
+template <typename Scale, int IN, int OUT, int PAIRS, int CH>
 __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(GemvArgs a) {
-  __shared__ int xq_s[kMaxK / 4];
-  __shared__ float xs_s[kMaxK / 32];
+  constexpr int kMaxChunks = CH;
+  __shared__ int xq_s[kMaxChunks * kThreads];
+  __shared__ float xs_s[kMaxChunks * kThreads / 8];
   __shared__ float prod_s[kThreads * PAIRS];  // [block][row]
   __shared__ float sums_s[64];
   __shared__ double red_s[kThreads / kWave];
@@ -51,7 +52,9 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(GemvArgs a) {
   float4 xv[kMaxChunks];
   float4 nw[kMaxChunks];
   int xw[kMaxChunks];
-  float xsv = 0.0f, rv = 0.0f;
+  // Block scales of a quantised input: B = K/32 of them, two per lane past
+  // 256 blocks (K > 8192).
+  float xsv = 0.0f, xsv2 = 0.0f, rv = 0.0f;
 #pragma unroll
   for (int c = 0; c < kMaxChunks; ++c) {
     int e = c * 4 * kThreads + 4 * tid;
@@ -65,6 +68,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(GemvArgs a) {
     }
   }
   if (IN == kInputQuantized && tid < B) xsv = a.xs[(size_t)frame * B + tid];
+  if (IN == kInputQuantized && kMaxChunks > 8 && kThreads + tid < B) xsv2 = a.xs[(size_t)frame * B + kThreads + tid];
   if (OUT == kOutResidual && tid < nrows) rv = a.resid[(size_t)frame * a.out_rows + row0 + tid];
   if (OUT == kOutPlain && a.bias && tid < nrows) rv = a.bias[row0 + tid];
 
@@ -92,6 +96,7 @@ __global__ __launch_bounds__(kThreads) void q8_gemv_kernel(GemvArgs a) {
       if (e < K) xq_s[e >> 2] = xw[c];
     }
     if (tid < B) xs_s[tid] = xsv;
+    if (kMaxChunks > 8 && kThreads + tid < B) xs_s[kThreads + tid] = xsv2;
   } else {
     float inverse = 1.0f;
     if (IN == kInputNorm) {
@@ -720,17 +725,23 @@ __global__ __launch_bounds__(kThreads) void block_dots_kernel(const int8_t* x, c
 // Host-side launchers
 // ---------------------------------------------------------------------------
 
-template <typename Scale, int IN, int OUT>
-static hipError_t launch_gemv_pairs(const GemvArgs& a, int frames, int pairs_per_thread, hipStream_t s) {
+template <typename Scale, int IN, int OUT, int CH>
+static hipError_t launch_gemv_pairs_ch(const GemvArgs& a, int frames, int pairs_per_thread, hipStream_t s) {
   dim3 grid((a.rows + a.group_rows - 1) / a.group_rows, frames);
   switch (pairs_per_thread) {
-    case 1: q8_gemv_kernel<Scale, IN, OUT, 1><<<grid, kThreads, 0, s>>>(a); break;
-    case 2: q8_gemv_kernel<Scale, IN, OUT, 2><<<grid, kThreads, 0, s>>>(a); break;
-    case 3: q8_gemv_kernel<Scale, IN, OUT, 3><<<grid, kThreads, 0, s>>>(a); break;
-    case 4: q8_gemv_kernel<Scale, IN, OUT, 4><<<grid, kThreads, 0, s>>>(a); break;
+    case 1: q8_gemv_kernel<Scale, IN, OUT, 1, CH><<<grid, kThreads, 0, s>>>(a); break;
+    case 2: q8_gemv_kernel<Scale, IN, OUT, 2, CH><<<grid, kThreads, 0, s>>>(a); break;
+    case 3: q8_gemv_kernel<Scale, IN, OUT, 3, CH><<<grid, kThreads, 0, s>>>(a); break;
+    case 4: q8_gemv_kernel<Scale, IN, OUT, 4, CH><<<grid, kThreads, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <typename Scale, int IN, int OUT>
+static hipError_t launch_gemv_pairs(const GemvArgs& a, int frames, int pairs_per_thread, hipStream_t s) {
+  return a.K <= kMaxK ? launch_gemv_pairs_ch<Scale, IN, OUT, kMaxK / (4 * kThreads)>(a, frames, pairs_per_thread, s)
+                      : launch_gemv_pairs_ch<Scale, IN, OUT, kMaxKLarge / (4 * kThreads)>(a, frames, pairs_per_thread, s);
 }
 
 template <typename Scale, int IN>
@@ -754,7 +765,7 @@ static hipError_t launch_gemv_in(const GemvArgs& a, int in, int out, int frames,
   return hipErrorInvalidValue;
 }
 
-int gemv_max_k() { return kMaxK; }
+int gemv_max_k() { return kMaxKLarge; }
 
 int gemv_pairs_per_thread(int group_rows, int K) {
   int pairs = group_rows * (K >> 5);
@@ -762,7 +773,7 @@ int gemv_pairs_per_thread(int group_rows, int K) {
 }
 
 hipError_t launch_gemv(const GemvArgs& a, bool half_scales, int in, int out, int frames, hipStream_t s) {
-  if (a.K % 32 != 0 || a.K > kMaxK || a.group_rows < 1 || a.group_rows > 64 || a.rows < 1) return hipErrorInvalidValue;
+  if (a.K % 32 != 0 || a.K > kMaxKLarge || a.group_rows < 1 || a.group_rows > 64 || a.rows < 1) return hipErrorInvalidValue;
   if (a.group_rows * (a.K / 32) > 4 * kThreads) return hipErrorInvalidValue;
   if (out == kOutSwiGLU && (a.group_rows % 2 != 0 || a.rows % a.group_rows != 0)) return hipErrorInvalidValue;
   int ppt = gemv_pairs_per_thread(a.group_rows, a.K);

@@ -284,7 +284,12 @@ typedef struct fah_layer_host {
  * `capacity` positions. `output` NULL means the lm_head is tied to
  * token_embd (QwenDecoder.cs:267). There is no reference counterpart for a
  * step-level seam: the C# side probes an optional IDecoderStepBackend at the
- * top of QwenDecoder.Decode, like IAttentionComputeBackend (TensorMath.cs:619). */
+ * top of QwenDecoder.Decode, like IAttentionComputeBackend (TensorMath.cs:619).
+ * Shapes: head_size 128, heads == 2 * kv_heads, width and heads*head_size
+ * at most 4096, ffn at most 16384, all multiples of 32 (Qwen3-0.6B and
+ * Qwen3-1.7B); others return FAH_ERROR_ARGUMENT. Qwen3-0.6B's shape steps
+ * on the persistent kernel; other shapes on the multi-kernel step, with
+ * multi-row inputs decoded row by row when ffn exceeds 3072. */
 int fah_decoder_create(fah_context* context, const fah_decoder_config* config, const fah_layer_host* layers,
                        const fah_q8_host* token_embd, const fah_q8_host* output, const float* output_norm,
                        fah_decoder** out);

@@ -66,6 +66,19 @@ def test_small_decoder_matches_oracle(backend, oracle_lib):
     _run_pair(backend, oracle_lib, w, prefix, steps=12)
 
 
+def test_qwen3_1_7b_shaped_decoder_matches_oracle(backend, oracle_lib):
+    """Qwen3-1.7B's shape (width 2048, 16/8 heads, ffn 6144; two layers and
+    a 16,384-token vocabulary to keep the oracle quick): no persistent
+    instantiation, so the multi-kernel step runs (the down projection's
+    GEMV on 16 register chunks), and the prefix goes row by row (the
+    prefill GEMMs take ffn up to 3072). Bit-exact logits, K/V rows and
+    tokens against the oracle."""
+    cfg = model.DecoderConfig(width=2048, heads=16, kv_heads=8, layers=2, ffn=6144, vocab=16384)
+    w = model.synthetic(cfg, seed=17)
+    prefix = np.random.default_rng(18).standard_normal((6, cfg.width)).astype(np.float32)
+    _run_pair(backend, oracle_lib, w, prefix, steps=6, capacity=64)
+
+
 def test_small_decoder_fp32_scales(backend, oracle_lib):
     """Scales that fp16 cannot hold keep an fp32 plane on the device."""
     w = model.synthetic(model.small_config(layers=1), seed=4)

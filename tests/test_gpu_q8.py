@@ -79,7 +79,12 @@ def test_block_dots_bit_exact(backend, dev, oracle_lib, cols, rows):
     assert np.array_equal(dots.numpy().reshape(rows, -1), oracle_lib.block_dots(xq, w.quantized))
 
 
-@pytest.mark.parametrize("cols,rows", SHAPES)
+# Inputs wider than the 0.6B decoder's: Qwen3-1.7B's down projection
+# (6144 -> 2048), 8B's width of ffn (12288), the GEMV's limit (16384).
+LARGE_K = [(6144, 2048), (12288, 1024), (16384, 64)]
+
+
+@pytest.mark.parametrize("cols,rows", SHAPES + LARGE_K)
 def test_gemv_bit_exact(backend, dev, oracle_lib, cols, rows):
     rng = np.random.default_rng(cols * 7 + rows)
     w = _weights(rng, rows, cols)
@@ -130,6 +135,21 @@ def test_linear_many_equals_independent(backend, oracle_lib):
                 expected = oracle_lib.linear(x, t.quantized, t.scales).ravel()
                 assert np.array_equal(o.view(np.uint32), single.view(np.uint32))
                 assert np.array_equal(o.view(np.uint32), expected.view(np.uint32))
+
+
+@pytest.mark.parametrize("frames", [1, 3])
+def test_quantized_linear_wide_input(backend, oracle_lib, frames):
+    """The seam's Q8_0 linear at K = 6144 (past the four register chunks of
+    the decoder's widths): the oracle's quantise-then-GEMV bits."""
+    rng = np.random.default_rng(61 + frames)
+    w = _weights(rng, 2048, 6144)
+    x = rng.standard_normal((frames, 6144)).astype(np.float32)
+    out = np.zeros((frames, 2048), dtype=np.float32)
+    assert backend.try_quantized_linear(x.ravel(), frames, w, None, out.ravel())
+    for f in range(frames):
+        xq, xs = oracle_lib.quantize(x[f])
+        expected = oracle_lib.gemv_quantized(xq, xs, w.quantized, w.scales)[0]
+        assert np.array_equal(out[f].view(np.uint32), expected.view(np.uint32)), f
 
 
 def test_declines_small_and_leaves_output_untouched():
