@@ -1874,14 +1874,14 @@ int fah_decoder_create(fah_context* h, const fah_decoder_config* cfg, const fah_
             "invalid decoder dimensions");
     require(k.heads % k.kv_heads == 0, "Invalid GQA head counts");
     require(k.head_size == 128, "head_size must be 128");
-    require(k.heads == 2 * k.kv_heads, "the paired GQA path needs heads == 2 * kv_heads");
+    require(k.heads == 2 * k.kv_heads || k.heads == 4 * k.kv_heads, "GQA groups of 2 or 4 query heads per KV head");
     require(k.width % 32 == 0 && k.ffn % 32 == 0, "widths must be multiples of 32");
     int q_width = k.heads * k.head_size, kv_width = k.kv_heads * k.head_size;
     // The ffn width (the down projection's K) up to the GEMV's limit; the
     // model width and q width up to 4096 (the norm, embedding and attention
     // kernels hold rows of that width).
     require(k.width <= 4096 && q_width <= 4096 && k.ffn <= fah::gemv_max_k(), "projection width exceeds kernel limit");
-    require(k.capacity >= 1 && fah::attention_slices(k.capacity, k.head_size) != 0,
+    require(k.capacity >= 1 && fah::attention_slices(k.capacity, k.head_size, k.heads / k.kv_heads) != 0,
             "capacity exceeds the attention kernel's LDS budget");
     for (int l = 0; l < k.layers; ++l) {
       const fah_layer_host& L = layers[l];
@@ -1901,7 +1901,7 @@ int fah_decoder_create(fah_context* h, const fah_decoder_config* cfg, const fah_
     std::lock_guard<std::mutex> lock(c->gate);
     check(hipSetDevice(c->device), "hipSetDevice");
     DeviceWork work(*c);
-    check(fah::prepare_attention(k.capacity, k.head_size), "attention LDS budget");
+    check(fah::prepare_attention(k.capacity, k.head_size, k.heads / k.kv_heads), "attention LDS budget");
     auto d = std::make_unique<fah_decoder>();
     d->ctx = h->st;
     d->cfg = k;
@@ -2241,13 +2241,13 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
     d->kv_width = parent->kv_width;
     d->wt = parent->wt;
     if (d->wt->persistent_layout) d->persistent = true;
-    require(fah::attention_slices(capacity, d->cfg.head_size) != 0,
+    require(fah::attention_slices(capacity, d->cfg.head_size, d->cfg.heads / d->cfg.kv_heads) != 0,
             "capacity exceeds the attention kernel's LDS budget");
     std::lock_guard<std::mutex> lock(c->gate);
     require_live(parent);
     check(hipSetDevice(c->device), "hipSetDevice");
     DeviceWork work(*c);
-    check(fah::prepare_attention(capacity, d->cfg.head_size), "attention LDS budget");
+    check(fah::prepare_attention(capacity, d->cfg.head_size, d->cfg.heads / d->cfg.kv_heads), "attention LDS budget");
     init_state(d.get(), c->stream);
     work.release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");

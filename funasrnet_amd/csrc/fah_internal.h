@@ -285,10 +285,12 @@ hipError_t launch_unpack_q8_blocks(const uint8_t* raw, int64_t blocks, int8_t* q
 hipError_t launch_embed(const int8_t* q, const void* scales, bool half_scales, int K, int vocab, const int* token,
                         float* x, int* history, int* history_count, hipStream_t s);
 hipError_t launch_qk_prepare(const QkArgs& a, hipStream_t s);
-int attention_slices(int capacity, int head_size);
+// Value-kernel workgroups per KV head for G = `group` query heads a KV head
+// (2 or 4); 0 when the capacity exceeds its LDS budget.
+int attention_slices(int capacity, int head_size, int group);
 // Row stride (doubles) of AttnArgs::exp_t for a cache of `capacity` positions.
 inline int attention_exp_stride(int capacity) { return ((capacity + 7) / 8 + 1) & ~1; }
-hipError_t prepare_attention(int capacity, int head_size);
+hipError_t prepare_attention(int capacity, int head_size, int group);
 hipError_t launch_attention(const AttnArgs& a, int score_groups, hipStream_t s);
 hipError_t launch_advance(int* position, int frames, hipStream_t s);
 hipError_t launch_quantize(const float* x, int64_t n, int8_t* q, float* scales, hipStream_t s);

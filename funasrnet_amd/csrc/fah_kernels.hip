@@ -445,53 +445,58 @@ __device__ __forceinline__ float softmax_inverse(const double* et, int stride, c
 }
 
 // Value sums out[c] = sum over t of v[t][c] * p[t] in time order from 0f
-// (TensorMath.AttentionAvx.cs:173-224) for both query heads of one KV head
-// and a slice of kValC channels: 2 kValC chains, run by lanes of wave 0 (one
-// add per position); wave 4 copies V rows of the slice into a three-slot
-// LDS ring two blocks ahead (direct global->LDS loads) and the other six
-// waves form the products v * p of the next block into a two-slot product
-// ring, so each chain step is one add (the product's rounding is the same
-// wherever it is made). Before the first block, waves 0 and 1 form the two heads'
-// softmax denominators from the numerators by residue (staged in the
-// product ring's space when they fit). Dynamic LDS: see values_lds.
+// (TensorMath.AttentionAvx.cs:173-224) for the G query heads of one KV head
+// (G = heads / kv_heads, 2 or 4) and a slice of kValC = 32 / G channels:
+// 32 chains, run by lanes of wave 0 (one add per position); wave 4 copies V
+// rows of the slice into a three-slot LDS ring two blocks ahead (direct
+// global->LDS loads) and the other six waves form the products v * p of the
+// next block into a two-slot product ring, so each chain step is one add
+// (the product's rounding is the same wherever it is made). Before the first
+// block, waves 0..G-1 form the heads' softmax denominators from the
+// numerators by residue (staged in the product ring's space when they fit).
+// Dynamic LDS: see values_lds.
 constexpr int kValThreads = 512;
-constexpr int kValC = 16;                      // channels per workgroup
-constexpr int kValChains = 2 * kValC;          // both query heads
+constexpr int kValChains = 32;                 // chains per workgroup: G heads x 32 / G channels
 constexpr int kValBlk = 256;                   // positions per ring block
 constexpr int kValRow = kValBlk + 12;          // product ring row (floats; also the residue rows' room)
-constexpr int kValVSlot = kValBlk * kValC * 2; // V ring slot (bytes)
 constexpr int kValPSlot = kValChains * kValRow * 4;  // product ring slot (bytes)
+constexpr int val_vslot(int group) { return kValBlk * (kValChains / group) * 2; }  // V ring slot (bytes)
 
+template <int G>
 __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
+  constexpr int kValC = kValChains / G;        // channels per workgroup
+  constexpr int kValVSlot = val_vslot(G);
+  constexpr int kPieces = kValC / 8;           // 16-byte pieces of a position's V slice
+  constexpr int kQuarters = kValC / 4;         // 4-channel producer tasks per position
   extern __shared__ __attribute__((aligned(16))) float dyn_s[];
-  __shared__ float inv_s[2];
+  __shared__ float inv_s[G];
   constexpr int kWaves = kValThreads / kWave;
   const int slices = a.head_size / kValC;
   const int kh = blockIdx.x / slices, c0 = (blockIdx.x % slices) * kValC;
   const int hs = a.head_size, n = *a.position + 1, tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   const int group = a.heads / a.kv_heads;
   const int np = (n + 3) & ~3;
-  float* p_s = dyn_s;                                               // [2][np]
-  char* vring = reinterpret_cast<char*>(dyn_s + 2 * np);            // [3][kValBlk][kValC] fp16
+  float* p_s = dyn_s;                                               // [G][np]
+  char* vring = reinterpret_cast<char*>(dyn_s + G * np);            // [3][kValBlk][kValC] fp16
   float* pring = reinterpret_cast<float*>(vring + 3 * kValVSlot);   // [2][kValChains][kValRow]
   const int blocks = (n + kValBlk - 1) / kValBlk;
   const _Float16* vbase = a.vcache + (size_t)kh * a.capacity * hs + c0;
-  // V block j into ring slot j % 3: 2 pieces of 16 bytes a position, piece
-  // q of the block at byte 16 q; `first`/`step` spread the pieces over the
-  // calling waves (positions past n repeat the last one, never used).
+  // V block j into ring slot j % 3: kPieces pieces of 16 bytes a position,
+  // piece q of the block at byte 16 q; `first`/`step` spread the pieces over
+  // the calling waves (positions past n repeat the last one, never used).
   auto fill = [&](int j, int first, int step) {
     char* dst = vring + (size_t)(j % 3) * kValVSlot;
-    for (int q0 = first * 64; q0 < 2 * kValBlk; q0 += step * 64) {
-      const int q = q0 + lane, t = min(j * kValBlk + (q >> 1), n - 1);
-      __builtin_amdgcn_global_load_lds(vbase + (size_t)t * hs + 8 * (q & 1), (lds_ptr)(dst + 16 * q0), 16, 0, 0);
+    for (int q0 = first * 64; q0 < kPieces * kValBlk; q0 += step * 64) {
+      const int q = q0 + lane, t = min(j * kValBlk + q / kPieces, n - 1);
+      __builtin_amdgcn_global_load_lds(vbase + (size_t)t * hs + 8 * (q % kPieces), (lds_ptr)(dst + 16 * q0), 16, 0, 0);
     }
   };
-  // The residue rows of both heads' numerators (m doubles a row, 16-byte
+  // The residue rows of the heads' numerators (m doubles a row, 16-byte
   // pieces; row r at `rs` doubles, two more than m rounded up to 2 so that
   // the eight lanes reading a column hit different banks), in the product
   // ring's space when they fit; else read from global memory.
   const int m = (n & ~7) >> 3, rs = ((m + 1) & ~1) + 2;
-  const bool staged = (size_t)16 * rs * 8 <= (size_t)2 * kValPSlot;
+  const bool staged = (size_t)8 * G * rs * 8 <= (size_t)2 * kValPSlot;
   double* et_s = reinterpret_cast<double*>(pring);
   const double* et_g = a.exp_t + (size_t)kh * group * 8 * a.exp_stride;
   // Wave 0 runs the chains; wave 4, which shares its SIMD, only issues the
@@ -501,41 +506,43 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
   const bool producer = wave != 0 && wave != kWaves / 2;
   const int prank = wave < kWaves / 2 ? wave - 1 : wave - 2;
   // Products of block j into product slot j & 1: task = (four positions,
-  // 4-channel quarter), whose 8 product rows of four positions each are
-  // written as float4; rows [0, kValC) head 0, [kValC, 2 kValC) head 1.
-  // Positions past n are formed from the clamped V rows and garbage
-  // probabilities and never added.
-  float inv0 = 0.0f, inv1 = 0.0f;  // softmax inverses of the two heads
+  // 4-channel quarter), whose 4 G product rows of four positions each are
+  // written as float4; rows [h kValC, (h + 1) kValC) head h. Positions past
+  // n are formed from the clamped V rows and garbage probabilities and never
+  // added.
+  float inv[G];  // the heads' softmax inverses
   auto produce = [&](int j) {
     const char* vs = vring + (size_t)(j % 3) * kValVSlot;
     float* ps = pring + (size_t)(j & 1) * kValChains * kValRow;
     const int t0 = j * kValBlk, len = min(kValBlk, n - t0);
-    for (int task = prank * kWave + lane; task < 4 * ((len + 3) >> 2); task += kProducers * kWave) {
-      const int tq = 4 * (task >> 2), q = task & 3, t = t0 + tq;
+    for (int task = prank * kWave + lane; task < kQuarters * ((len + 3) >> 2); task += kProducers * kWave) {
+      const int tq = 4 * (task / kQuarters), q = task % kQuarters, t = t0 + tq;
       uint2 raw[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) raw[u] = *reinterpret_cast<const uint2*>(vs + 32 * (tq + u) + 8 * q);
+      for (int u = 0; u < 4; ++u) raw[u] = *reinterpret_cast<const uint2*>(vs + 2 * kValC * (tq + u) + 8 * q);
       // The probabilities p = e * inverse (the softmax's last step).
-      const float4 e0 = *reinterpret_cast<const float4*>(p_s + t);
-      const float4 e1 = *reinterpret_cast<const float4*>(p_s + np + t);
-      const float4 p0 = make_float4(fmul(e0.x, inv0), fmul(e0.y, inv0), fmul(e0.z, inv0), fmul(e0.w, inv0));
-      const float4 p1 = make_float4(fmul(e1.x, inv1), fmul(e1.y, inv1), fmul(e1.z, inv1), fmul(e1.w, inv1));
+      float4 p[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float4 e = *reinterpret_cast<const float4*>(p_s + h * np + t);
+        p[h] = make_float4(fmul(e.x, inv[h]), fmul(e.y, inv[h]), fmul(e.z, inv[h]), fmul(e.w, inv[h]));
+      }
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         float v[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) v[u] = from_half(reinterpret_cast<const _Float16*>(&raw[u])[k]);
-        *reinterpret_cast<float4*>(ps + (size_t)(4 * q + k) * kValRow + tq) =
-            make_float4(fmul(v[0], p0.x), fmul(v[1], p0.y), fmul(v[2], p0.z), fmul(v[3], p0.w));
-        *reinterpret_cast<float4*>(ps + (size_t)(kValC + 4 * q + k) * kValRow + tq) =
-            make_float4(fmul(v[0], p1.x), fmul(v[1], p1.y), fmul(v[2], p1.z), fmul(v[3], p1.w));
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+          *reinterpret_cast<float4*>(ps + (size_t)(h * kValC + 4 * q + k) * kValRow + tq) =
+              make_float4(fmul(v[0], p[h].x), fmul(v[1], p[h].y), fmul(v[2], p[h].z), fmul(v[3], p[h].w));
       }
     }
   };
-  // The numerators of both heads (written by attn_exp_kernel), their
+  // The numerators of the heads (written by attn_exp_kernel), their
   // residue rows and the first two V blocks, by all waves.
   {
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < G; ++h) {
       const char* src = reinterpret_cast<const char*>(a.scores + (size_t)(kh * group + h) * a.capacity);
       char* dst = reinterpret_cast<char*>(p_s + h * np);
       const int bytes = np * 4;
@@ -544,7 +551,7 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
     }
     if (staged) {
       const int rb = rs * 8;  // bytes a staged row
-      for (int r = wave; r < 16; r += kWaves) {
+      for (int r = wave; r < 8 * G; r += kWaves) {
         const char* src = reinterpret_cast<const char*>(et_g + (size_t)r * a.exp_stride);
         char* dst = reinterpret_cast<char*>(et_s) + (size_t)r * rb;
         for (int c = 0; c < m * 8; c += 1024)
@@ -556,10 +563,10 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
     __builtin_amdgcn_s_waitcnt(0);
   }
   lds_barrier();
-  // The two heads' denominators, one wave each: the exact block sums of
+  // The heads' denominators, one wave each: the exact block sums of
   // attn_exp_kernel when every block qualifies (any order of exact
   // additions is the reference's), else the residue chains.
-  if (wave < 2) {
+  if (wave < G) {
     const double* bs = a.block_sum + (size_t)(kh * group + wave) * ((a.capacity + kThreads - 1) / kThreads);
     double total = 0.0;
     for (int b = lane; b < blocks; b += kWave) total += bs[b];
@@ -571,8 +578,8 @@ __global__ __launch_bounds__(kValThreads) void attn_values_kernel(AttnArgs a) {
     if (lane == 0) inv_s[wave] = inv;
   }
   lds_barrier();
-  inv0 = inv_s[0];
-  inv1 = inv_s[1];
+#pragma unroll
+  for (int h = 0; h < G; ++h) inv[h] = inv_s[h];
   if (producer) produce(0);
   lds_barrier();
   float acc = 0.0f;
@@ -823,40 +830,40 @@ hipError_t launch_qk_prepare(const QkArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Dynamic LDS of attn_values_kernel for `capacity` positions: both heads'
-// probabilities (rounded up to 4 positions), the three-slot V ring and the
-// two-slot product ring.
-static size_t values_lds(int capacity) {
-  return (size_t)2 * ((capacity + 3) & ~3) * 4 + 3 * kValVSlot + 2 * kValPSlot;
+// Dynamic LDS of attn_values_kernel for `capacity` positions and G =
+// `group` query heads a KV head: the heads' probabilities (rounded up to 4
+// positions), the three-slot V ring and the two-slot product ring.
+static size_t values_lds(int capacity, int group) {
+  return (size_t)group * ((capacity + 3) & ~3) * 4 + 3 * val_vslot(group) + 2 * kValPSlot;
 }
 
-int attention_slices(int capacity, int head_size) {
-  if (head_size % kValC != 0 || values_lds(capacity) > 160 * 1024 - 1024) return 0;
-  return head_size / kValC;
+int attention_slices(int capacity, int head_size, int group) {
+  if (group != 2 && group != 4) return 0;
+  const int channels = kValChains / group;
+  if (head_size % channels != 0 || values_lds(capacity, group) > 160 * 1024 - 1024) return 0;
+  return head_size / channels;
 }
 
-size_t attention_lds_bytes(int capacity, int head_size) {
-  return attention_slices(capacity, head_size) ? values_lds(capacity) : 0;
+size_t attention_lds_bytes(int capacity, int head_size, int group) {
+  return attention_slices(capacity, head_size, group) ? values_lds(capacity, group) : 0;
 }
 
-hipError_t prepare_attention(int capacity, int head_size) {
-  if (!attention_lds_bytes(capacity, head_size)) return hipErrorInvalidValue;
+hipError_t prepare_attention(int capacity, int head_size, int group) {
+  if (!attention_lds_bytes(capacity, head_size, group)) return hipErrorInvalidValue;
   // The limits are per kernel, not per decoder: set the largest size any
   // capacity that attention_slices accepts can ask for, so decoders of
   // different capacities do not lower each other's limit.
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(attn_values_kernel),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+  const void* kernel = group == 2 ? reinterpret_cast<const void*>(attn_values_kernel<2>)
+                                  : reinterpret_cast<const void*>(attn_values_kernel<4>);
+  return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
 }
 
-// Scores (one lane per position) with each block's maximum, the softmax
-// numerators in place, then the denominators and the value sums. The grids
-// cover the cache's capacity: workgroups past the current position return
-// at once.
 hipError_t launch_attention(const AttnArgs& a, int /*score_groups*/, hipStream_t s) {
-  if (a.head_size != 128 || a.heads != 2 * a.kv_heads || !a.block_max || !a.exp_t ||
+  const int group = a.kv_heads > 0 ? a.heads / a.kv_heads : 0;
+  if (a.head_size != 128 || a.heads != group * a.kv_heads || !a.block_max || !a.exp_t ||
       a.exp_stride < attention_exp_stride(a.capacity))
     return hipErrorInvalidValue;
-  int slices = attention_slices(a.capacity, a.head_size);
+  const int slices = attention_slices(a.capacity, a.head_size, group);
   if (!slices) return hipErrorInvalidValue;
   const dim3 grid(a.heads, (a.capacity + kThreads - 1) / kThreads);
   attn_scores_kernel<<<grid, kThreads, 0, s>>>(a);
@@ -865,7 +872,9 @@ hipError_t launch_attention(const AttnArgs& a, int /*score_groups*/, hipStream_t
   attn_exp_kernel<<<grid, kThreads, 0, s>>>(a);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  attn_values_kernel<<<a.kv_heads * slices, kValThreads, attention_lds_bytes(a.capacity, a.head_size), s>>>(a);
+  const size_t lds = attention_lds_bytes(a.capacity, a.head_size, group);
+  if (group == 2) attn_values_kernel<2><<<a.kv_heads * slices, kValThreads, lds, s>>>(a);
+  else attn_values_kernel<4><<<a.kv_heads * slices, kValThreads, lds, s>>>(a);
   return hipGetLastError();
 }
 

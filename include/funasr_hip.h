@@ -251,7 +251,7 @@ int fah_q8_block_dots_device(fah_context* context, const int8_t* q, const fah_we
 typedef struct fah_decoder_config {
     int width;      /* qwen3.embedding_length, 1024 */
     int heads;      /* qwen3.attention.head_count, 16 */
-    int kv_heads;   /* qwen3.attention.head_count_kv, 8 (heads == 2*kv_heads) */
+    int kv_heads;   /* qwen3.attention.head_count_kv, 8 (heads == 2 or 4 * kv_heads) */
     int head_size;  /* qwen3.attention.key_length, 128 */
     int layers;     /* qwen3.block_count, 28 */
     int ffn;        /* ffn_gate rows, 3072 */
@@ -285,11 +285,12 @@ typedef struct fah_layer_host {
  * token_embd (QwenDecoder.cs:267). There is no reference counterpart for a
  * step-level seam: the C# side probes an optional IDecoderStepBackend at the
  * top of QwenDecoder.Decode, like IAttentionComputeBackend (TensorMath.cs:619).
- * Shapes: head_size 128, heads == 2 * kv_heads, width and heads*head_size
- * at most 4096, ffn at most 16384, all multiples of 32 (Qwen3-0.6B and
- * Qwen3-1.7B); others return FAH_ERROR_ARGUMENT. Qwen3-0.6B's shape steps
- * on the persistent kernel; other shapes on the multi-kernel step, with
- * multi-row inputs decoded row by row when ffn exceeds 3072. */
+ * Shapes: head_size 128, heads == 2 or 4 * kv_heads, width and
+ * heads*head_size at most 4096, ffn at most 16384, all multiples of 32
+ * (Qwen3-0.6B, 1.7B, 4B and 8B); others return FAH_ERROR_ARGUMENT.
+ * Qwen3-0.6B's shape steps on the persistent kernel; other shapes on the
+ * multi-kernel step, with multi-row inputs decoded row by row when ffn
+ * exceeds 3072 (lock-step sessions and the step batcher need ffn <= 3072). */
 int fah_decoder_create(fah_context* context, const fah_decoder_config* config, const fah_layer_host* layers,
                        const fah_q8_host* token_embd, const fah_q8_host* output, const float* output_norm,
                        fah_decoder** out);

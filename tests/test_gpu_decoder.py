@@ -79,6 +79,55 @@ def test_qwen3_1_7b_shaped_decoder_matches_oracle(backend, oracle_lib):
     _run_pair(backend, oracle_lib, w, prefix, steps=6, capacity=64)
 
 
+@pytest.mark.parametrize("name,width,ffn", [("4b", 2560, 9728), ("8b", 4096, 12288)])
+def test_qwen3_grouped_by_four_shapes_match_oracle(backend, oracle_lib, name, width, ffn):
+    """Qwen3-4B and 8B shapes (32 query heads on 8 KV heads: four a group,
+    the value kernel's 8-channel slices; two layers, a 16,384-token
+    vocabulary): bit-exact logits, K/V rows and tokens against the oracle."""
+    cfg = model.DecoderConfig(width=width, heads=32, kv_heads=8, layers=2, ffn=ffn, vocab=16384)
+    w = model.synthetic(cfg, seed=19)
+    prefix = np.random.default_rng(20).standard_normal((5, cfg.width)).astype(np.float32)
+    print(f"qwen3 {name} shape", flush=True)
+    _run_pair(backend, oracle_lib, w, prefix, steps=4, capacity=64)
+
+
+def test_grouped_by_four_long_cache_matches_oracle(backend, oracle_lib):
+    """The 4B shape after 700 cached F16 N(0,1) rows: the value kernel over
+    three 256-position blocks with four heads' denominators (exact block sums
+    or the residue chains), bit-exact against the oracle for the first step
+    and the next four greedy tokens."""
+    from funasrnet_amd.hip import HipDecoder
+    cfg = model.DecoderConfig(width=2560, heads=32, kv_heads=8, layers=2, ffn=9728, vocab=16384)
+    w = model.synthetic(cfg, seed=21)
+    positions, capacity = 700, 768
+    rng = np.random.default_rng(22)
+    kv = [(rng.standard_normal((positions, cfg.kv_width)).astype(np.float16),
+           rng.standard_normal((positions, cfg.kv_width)).astype(np.float16)) for _ in range(cfg.layers)]
+    x = rng.standard_normal((1, cfg.width)).astype(np.float32)
+    gpu = HipDecoder(backend, w, capacity=capacity)
+    ref = oracle_lib.Decoder(w, capacity=capacity)
+    try:
+        for layer, (k, v) in enumerate(kv):
+            gpu.kv_write(layer, k, v)
+            ref.set_kv(layer, k.astype(np.float32), v.astype(np.float32))
+        gpu.set_position(positions)
+        ref.set_position(positions)
+        print("qwen3 4b shape, 700 cached positions", flush=True)
+        lg = gpu.decode(x, 1)
+        lr = ref.decode(x, 1)
+        assert np.array_equal(lg.view(np.uint32), lr.view(np.uint32))
+        tokens = gpu.generate(4).tolist()
+        expected = []
+        for _ in range(4):
+            t = oracle_lib.greedy(lr)
+            expected.append(t)
+            lr = ref.decode(ref.embed([t]), 1)
+        assert tokens == expected
+    finally:
+        gpu.close()
+        ref.close()
+
+
 def test_small_decoder_fp32_scales(backend, oracle_lib):
     """Scales that fp16 cannot hold keep an fp32 plane on the device."""
     w = model.synthetic(model.small_config(layers=1), seed=4)
