@@ -30,8 +30,18 @@ public sealed unsafe class HipDecoderStep : IDecoderStep
         }
     }
 
+    /// <summary>The shapes fah_decoder_create takes (funasr_hip.h): head size 128,
+    /// 2 or 4 query heads per KV head, widths multiples of 32 with the model and
+    /// q widths at most 4096 and the ffn width at most 16384 (Qwen3-0.6B to 8B).</summary>
+    internal static bool ShapeSupported(in Native.DecoderConfig c) =>
+        c.HeadSize == 128 && c.KvHeads > 0 && (c.Heads == 2 * c.KvHeads || c.Heads == 4 * c.KvHeads) &&
+        c.Width % 32 == 0 && c.Ffn % 32 == 0 && c.Width <= 4096 && c.Heads * c.HeadSize <= 4096 && c.Ffn <= 16384;
+
     /// <summary>fah_decoder_create from the model's tensors (names and metadata of
-    /// QwenDecoder.cs:46-75); null when a tensor is not Q8_0 in row-major form.</summary>
+    /// QwenDecoder.cs:46-75); null when the shape is not one the library takes
+    /// (the reference's own decoder then runs) or a tensor is not Q8_0 in
+    /// row-major form. Step batching needs an ffn width of at most 3072; larger
+    /// models step on their own.</summary>
     internal static HipDecoderStep? Create(IntPtr context, Gguf model, int capacity, bool batching)
     {
         int layers = model.Int("qwen3.block_count", 28);
@@ -50,6 +60,11 @@ public sealed unsafe class HipDecoderStep : IDecoderStep
             RopeBase = model.Float("qwen3.rope.freq_base", 1000000),
             Capacity = capacity,
         };
+        if (!ShapeSupported(config))
+        {
+            return null;
+        }
+        batching &= config.Ffn <= 3072;
         var pins = new List<GCHandle>();
         try
         {
