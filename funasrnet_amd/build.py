@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libfunasr_hip.so")
-SOURCES = ["fah_kernels.hip", "fah_persistent.hip", "fah_prefill.hip", "fah_float.hip", "fah_api.hip"]
+SOURCES = ["fah_kernels.hip", "fah_persistent.hip", "fah_prefill.hip", "fah_sessions.hip", "fah_float.hip",
+           "fah_api.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
          "-fno-gpu-flush-denormals-to-zero", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -167,6 +167,11 @@ struct SessionBatch {
   DeviceBuffer tokens;  // the step batcher's gathered tokens, one per session
   std::vector<fah::SessionRef> host_table;  // source of the last table upload (alive until the next)
   hipGraphExec_t graph = nullptr;
+  // One-launch layers (fah_sessions.hip): its layer table, exchange words,
+  // epoch and error word, and the launch arguments.
+  bool fused = false;
+  DeviceBuffer layer_table, exchange, epoch, error;
+  fah::SessionStepArgs sargs{};
   SessionBatch() = default;
   SessionBatch(const SessionBatch&) = delete;
   SessionBatch& operator=(const SessionBatch&) = delete;
@@ -1087,7 +1092,9 @@ void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s)
   check(fah::launch_session_embed(w.embed.q.as<int8_t>(), w.embed.s.ptr, w.half_scales, c.width, c.vocab, table, S,
                                   b.x.as<float>(), s),
         "session embed");
-  for (int l = 0; l < c.layers; ++l) {
+  // One launch for every layer and the output norm (its rows land in xq/xs).
+  if (b.fused) check(fah::launch_session_step(b.sargs, s), "session step");
+  for (int l = 0; l < c.layers && !b.fused; ++l) {
     norm_quantize(b.x.as<float>(), c.width, &w.attn_norm[l]);
     gemm(w.qkv[l], qkv_rows, b.qkv.as<float>(), nullptr, fah::kGemmPlain);
     // Attention with the QK-norm, RoPE and K/V row write of each session's
@@ -1116,7 +1123,7 @@ void enqueue_sessions_step(const fah_decoder* d, SessionBatch& b, hipStream_t s)
     norm_quantize(b.h.as<float>(), c.ffn, nullptr);
     gemm(w.down[l], c.width, b.x.as<float>(), b.a.as<float>(), fah::kGemmResidual);
   }
-  norm_quantize(b.x.as<float>(), c.width, &w.output_norm);
+  if (!b.fused) norm_quantize(b.x.as<float>(), c.width, &w.output_norm);
   const int head_groups = fah::few_frame_groups(c.vocab, c.width, S, fah::kGemmGreedy);
   require(head_groups > 0, "lock-step sessions: the lm_head shape does not fit the few-frame kernel");
   gemm(head_matrix(d), c.vocab, b.logits.as<float>(), nullptr, fah::kGemmGreedy);
@@ -1154,9 +1161,134 @@ void upload_session_table(SessionBatch& b, fah_decoder* const* sessions, int cou
         "H2D session table");
 }
 
+// Whether `count` sessions of d0's weights with positions below `bound` step
+// on the one-launch layers (fah_sessions.hip): a shape it is built for, fp16
+// block scales, every position within what an attention workgroup stages,
+// and a device whose CUs hold all of its workgroups at once.
+// FAH_SESSION_STEP=0 keeps the kernel-per-projection step.
+bool session_step_fits(const fah_decoder* d0, int count, int bound) {
+  static const bool on = [] {
+    const char* v = std::getenv("FAH_SESSION_STEP");
+    return !(v && v[0] == '0');
+  }();
+  const fah_decoder_config& k = d0->cfg;
+  if (!on || !d0->wt->half_scales || bound > fah::session_step_positions() || count * k.heads > fah::session_step_groups())
+    return false;
+  if (!fah::session_step_supported(k.width, k.heads, k.kv_heads, k.head_size, k.ffn)) return false;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, d0->ctx->device) != hipSuccess) return false;
+  static const int fit1024 = fah::session_step_blocks_per_cu(1024), fit512 = fah::session_step_blocks_per_cu(512);
+  return cus >= fah::session_step_groups() && (k.width == 1024 ? fit1024 : fit512) >= 1;
+}
+
+// The one-launch step's buffers and arguments for batch b (zeroed exchange
+// words, so that no word carries a generation before it is written).
+void prepare_session_step(const fah_decoder* d0, SessionBatch& b, int count, hipStream_t s) {
+  const fah_decoder_config& k = d0->cfg;
+  const DecoderWeights& w = *d0->wt;
+  std::vector<fah::PersistentLayer> layers(k.layers);
+  for (int l = 0; l < k.layers; ++l) {
+    fah::PersistentLayer& e = layers[l];
+    e.wqkv = w.qkv[l].q.as<int8_t>();
+    e.sqkv = w.qkv[l].s.as<_Float16>();
+    e.wo = w.wo[l].q.as<int8_t>();
+    e.so = w.wo[l].s.as<_Float16>();
+    e.wgu = w.gateup[l].q.as<int8_t>();
+    e.sgu = w.gateup[l].s.as<_Float16>();
+    e.wd = w.down[l].q.as<int8_t>();
+    e.sd = w.down[l].s.as<_Float16>();
+    e.attn_norm = w.attn_norm[l].as<float>();
+    e.q_norm = w.q_norm[l].as<float>();
+    e.k_norm = w.k_norm[l].as<float>();
+    e.ffn_norm = w.ffn_norm[l].as<float>();
+  }
+  upload(b.layer_table, layers.data(), layers.size() * sizeof(fah::PersistentLayer), s);
+  const size_t qkv_rows = (size_t)d0->q_width + 2 * (size_t)d0->kv_width;
+  // Every layer has its own exchange words (the gate/up maxima excepted).
+  const size_t L = (size_t)k.layers;
+  const size_t words[8] = {L * count * k.width,       L * count * k.width / 4, L * count * qkv_rows,
+                           L * count * d0->q_width / 4, L * count * k.width,     L * count * k.width / 4,
+                           (size_t)fah::session_step_groups() * 16, L * count * k.ffn / 4};
+  size_t total = 0;
+  for (size_t n : words) total += n;
+  b.exchange.allocate(total * 8);
+  b.epoch.allocate(16);
+  b.error.allocate(16);
+  check(hipMemsetAsync(b.exchange.ptr, 0, total * 8, s), "clear exchange words");
+  check(hipMemsetAsync(b.epoch.ptr, 0, 16, s), "clear epoch");
+  check(hipMemsetAsync(b.error.ptr, 0, 16, s), "clear error word");
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  unsigned long long* at[8];
+  unsigned long long* p = b.exchange.as<unsigned long long>();
+  for (int i = 0; i < 8; ++i) {
+    at[i] = p;
+    p += words[i];
+  }
+  fah::SessionStepArgs& a = b.sargs;
+  a.layer_table = b.layer_table.as<fah::PersistentLayer>();
+  a.layers = k.layers;
+  a.width = k.width;
+  a.heads = k.heads;
+  a.kv_heads = k.kv_heads;
+  a.head_size = k.head_size;
+  a.ffn = k.ffn;
+  a.output_norm = w.output_norm.as<float>();
+  a.sessions = b.table.as<fah::SessionRef>();
+  a.S = count;
+  a.max_positions = b.max_positions;
+  a.gu_map = w.gu_map.as<int>();
+  a.gu_base = w.gu_base;
+  a.gu_extra = w.gu_extra;
+  a.eps = k.eps;
+  a.divisor = std::sqrt((float)k.head_size);
+  a.x_in = b.x.as<float>();
+  a.xq_out = b.xq.as<int8_t>();
+  a.xs_out = b.xs.as<float>();
+  a.tx = at[0];
+  a.txq = at[1];
+  a.tqkv = at[2];
+  a.tattq = at[3];
+  a.ta = at[4];
+  a.taq = at[5];
+  a.tmax = at[6];
+  a.thq = at[7];
+  a.epoch = b.epoch.as<unsigned>();
+  a.error = b.error.as<unsigned>();
+  b.fused = true;
+}
+
+// After the steps of a one-launch batch: if a bounded wait expired, move
+// the epoch past every generation the failed launches may have published,
+// clear the error word, return every session's device position to its
+// host position with an empty history, and throw. The sessions' logits are
+// not valid afterwards (decode again before the next greedy step).
+void recover_session_step(SessionBatch& b, fah_decoder* const* sessions, int count, hipStream_t s) {
+  if (!b.fused) return;
+  unsigned e = 0, epoch = 0;
+  check(hipMemcpyAsync(&e, b.error.ptr, 4, hipMemcpyDeviceToHost, s), "D2H error word");
+  check(hipMemcpyAsync(&epoch, b.epoch.ptr, 4, hipMemcpyDeviceToHost, s), "D2H epoch");
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  if (!e) return;
+  epoch += 2;
+  const unsigned zero = 0;
+  check(hipMemcpyAsync(b.epoch.ptr, &epoch, 4, hipMemcpyHostToDevice, s), "H2D epoch");
+  check(hipMemcpyAsync(b.error.ptr, &zero, 4, hipMemcpyHostToDevice, s), "H2D error word");
+  std::vector<int> positions(count);
+  for (int i = 0; i < count; ++i) {
+    positions[i] = sessions[i]->host_position;
+    check(hipMemcpyAsync(sessions[i]->position.ptr, &positions[i], 4, hipMemcpyHostToDevice, s), "H2D position");
+    check(hipMemcpyAsync(sessions[i]->history_count.ptr, &zero, 4, hipMemcpyHostToDevice, s), "H2D history count");
+    sessions[i]->have_logits = false;
+  }
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  throw DeviceError{"lock-step sessions step: an exchange timed out (workgroups not co-resident?)"};
+}
+
 // Row buffers and the captured lock-step step of `count` sessions of d0's
-// weights whose positions stay below `bound`.
-std::unique_ptr<SessionBatch> make_session_batch(const fah_decoder* d0, int count, int bound, hipStream_t s) {
+// weights whose positions stay below `bound` (on the one-launch layers when
+// `fused`).
+std::unique_ptr<SessionBatch> make_session_batch(const fah_decoder* d0, int count, int bound, hipStream_t s,
+                                                 bool fused) {
   auto b = std::make_unique<SessionBatch>();
   b->members.assign(count, nullptr);
   b->max_positions = bound;
@@ -1172,6 +1304,7 @@ std::unique_ptr<SessionBatch> make_session_batch(const fah_decoder* d0, int coun
   b->xs.allocate((size_t)count * (widest / 32) * 4);
   b->logits.allocate((size_t)count * k.vocab * 4);
   b->keys.allocate((size_t)count * std::max(1, fah::few_frame_groups(k.vocab, k.width, count, fah::kGemmGreedy)) * 8);
+  if (fused) prepare_session_step(d0, *b, count, s);
   if (use_graphs()) {
     hipGraph_t graph = nullptr;
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -2270,11 +2403,17 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
     require_live(d0);
     hipStream_t s = c->stream;
     check(hipSetDevice(c->device), "hipSetDevice");
-    DeviceWork work(*c);
+    // The one-launch step needs every CU: the device to itself until its
+    // stream drains (PersistentSection), the plain enqueue lock otherwise.
+    const bool fused = session_step_fits(d0, count, bound);
+    std::optional<PersistentSection> exclusive;
+    std::optional<DeviceWork> work;
+    if (fused) exclusive.emplace(*c);
+    else work.emplace(*c);
     std::vector<fah_decoder*> members(sessions, sessions + count);
     if (!c->batch || c->batch->members != members || c->batch->max_positions != bound) {
       c->batch.reset();
-      auto b = make_session_batch(d0, count, bound, s);
+      auto b = make_session_batch(d0, count, bound, s, fused);
       upload_session_table(*b, sessions, count, s);
       b->members = members;
       c->batch = std::move(b);
@@ -2290,8 +2429,9 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
       check(hipMemcpyAsync(tokens + (size_t)i * steps, sessions[i]->history.ptr, (size_t)steps * 4,
                            hipMemcpyDeviceToHost, s),
             "D2H tokens");
-    work.release();  // enqueued: other contexts may enqueue while this stream drains
+    if (work) work->release();  // enqueued: other contexts may enqueue while this stream drains
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    recover_session_step(b, sessions, count, s);
     for (int i = 0; i < count; ++i) sessions[i]->host_position += steps;
     return FAH_OK;
   });
@@ -2402,10 +2542,16 @@ void run_batch(fah_batcher* b, const std::vector<BatchRequest*>& reqs) {
     require_live(sessions[0]);
     hipStream_t s = c->stream;
     check(hipSetDevice(c->device), "hipSetDevice");
+    const bool fused = session_step_fits(sessions[0], count, b->max_positions);
+    auto& batch = b->by_size[count];
     {
-      DeviceWork work(*c);
-      auto& batch = b->by_size[count];
-      if (!batch) batch = make_session_batch(sessions[0], count, b->max_positions, s);
+      // The one-launch step needs the device to itself until its stream
+      // drains; the plain enqueue lock otherwise.
+      std::optional<PersistentSection> exclusive;
+      std::optional<DeviceWork> work;
+      if (fused) exclusive.emplace(*c);
+      else work.emplace(*c);
+      if (!batch) batch = make_session_batch(sessions[0], count, b->max_positions, s, fused);
       upload_session_table(*batch, sessions.data(), count, s);
       const fah::SessionRef* table = batch->table.as<fah::SessionRef>();
       batch->tokens.ensure((size_t)fah::kFewFrames * 4);
@@ -2414,6 +2560,10 @@ void run_batch(fah_batcher* b, const std::vector<BatchRequest*>& reqs) {
       else enqueue_sessions_step(sessions[0], *batch, s);
       check(fah::launch_session_batch_io(table, count, batch->tokens.as<int>(), s), "gather tokens");
       check(hipMemcpyAsync(tokens.data(), batch->tokens.ptr, (size_t)count * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
+      if (fused) {
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        recover_session_step(*batch, sessions.data(), count, s);
+      }
     }
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
     for (fah_decoder* d : sessions) d->host_position += 1;

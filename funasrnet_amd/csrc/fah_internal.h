@@ -275,6 +275,37 @@ int persistent_exact_positions();
 int persistent_threads();
 int persistent_blocks_per_cu(int width);
 
+// Lock-step sessions step in one launch (fah_sessions.hip): the decoder
+// layers of S sessions, one token each, with tagged-word exchanges between
+// the phases; the output-normalised Q8_0 rows go to xq_out/xs_out for the
+// lm_head.
+struct SessionStepArgs {
+  const PersistentLayer* layer_table;  // device array [layers]
+  int layers;
+  int width, heads, kv_heads, head_size, ffn;
+  const float* output_norm;
+  const SessionRef* sessions;  // [S]
+  int S;
+  int max_positions;  // bound on every session's position + 1
+  const int* gu_map;  // gate/up storage rows (or null: tiles of gu_base rows)
+  int gu_base, gu_extra;
+  float eps, divisor;
+  const float* x_in;  // [S][width] embeddings
+  int8_t* xq_out;     // [S][width]
+  float* xs_out;      // [S][width / 32]
+  // Exchange words: residual rows, attention-norm rows (Q8_0), q/k/v,
+  // attention output (Q8_0), o + residual, ffn-norm rows (Q8_0), gate/up
+  // half-block maxima, ffn activations (Q8_0).
+  unsigned long long *tx, *txq, *tqkv, *tattq, *ta, *taq, *tmax, *thq;
+  unsigned* epoch;
+  unsigned* error;
+};
+bool session_step_supported(int width, int heads, int kv_heads, int head_size, int ffn);
+int session_step_positions();
+int session_step_groups();
+int session_step_blocks_per_cu(int width);
+hipError_t launch_session_step(const SessionStepArgs& a, hipStream_t s);
+
 int gemv_max_k();
 int gemv_pairs_per_thread(int group_rows, int K);
 hipError_t launch_gemv(const GemvArgs& a, bool half_scales, int in, int out, int frames, hipStream_t s);

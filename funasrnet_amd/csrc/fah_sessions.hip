@@ -1,0 +1,806 @@
+// Lock-step sessions step in one launch: the decoder layers of up to 16
+// sessions, one new token each, in one grid of one workgroup per CU
+// (FunAsr.cs:122-190 runs these steps one session at a time; every session's
+// arithmetic here is that of its own decode step).
+//
+// Every workgroup owns a fixed slice of every projection's rows and computes
+// them for all sessions at once, so each weight byte is read once per step
+// for the whole batch. The phases of a layer hand their outputs over through
+// global memory as tagged words (the value and its generation in one 64-bit
+// word, written with one relaxed device-scope store), so a consumer sees data
+// and readiness in the same load and no grid barrier is needed:
+//
+//   norm      one workgroup per session row: RMSNorm + Q8_0 of the row
+//   q/k/v     all workgroups: their q/k/v rows for every session
+//   attention one workgroup per (session, query head): QK-norm, RoPE, the
+//             new K/V row, exact softmax and time-ordered value sums over
+//             the session's cache (V rows staged in LDS), Q8_0 output
+//   o         all workgroups: their o rows + the residual (kept in registers
+//             by the same workgroup, which also owns those rows of down)
+//   norm      one workgroup per session row (ffn norm)
+//   gate/up   16 pairs of gate and up rows per workgroup: SwiGLU, then the
+//             Q8_0 block of 32 ffn values, whose two halves swap their
+//             maxima so that both use the block's scale
+//   down      all workgroups: their down rows + the residual
+//
+// Quantised rows travel as Q8_0 words (four int8 codes, the block scale's
+// halves in the side bits of words 0 and 1) in word-major order: word j of
+// block b at j B + b, so that the product lanes of consecutive blocks read
+// consecutive LDS words. After the last layer the norm workgroups write the
+// output-normalised rows in Q8_0 for the lm_head. Every wait is bounded: a
+// missing generation sets the error word and the workgroup leaves, so a
+// broken launch ends.
+#include <algorithm>
+
+#include "fah_device.h"
+#include "fah_internal.h"
+
+namespace fah {
+namespace {
+
+using u64 = unsigned long long;
+using lds_ptr = __attribute__((address_space(3))) void*;
+
+constexpr int kSG = 256;                      // workgroups, all co-resident (one per CU)
+constexpr int kST = 256;                      // threads per workgroup (four waves)
+constexpr int kSLds = 160 * 1024;             // dynamic LDS per workgroup
+constexpr int kSPositions = 320;              // bound on an attention unit's position + 1
+constexpr int kVArea = kSPositions * 256;     // V rows of the unit's earlier positions
+constexpr int kSmall = kSLds - 8 * 1024;      // small attention and exchange buffers
+constexpr int kPhases = 8;                    // exchanges per layer
+constexpr long kSSpin = 1L << 21;             // bounded polls per wait (~1-2 s)
+constexpr uint32_t kQMask = 0xFFFF0000u;      // quantised words: 16-bit tags
+constexpr int kGuPairs = 16;                  // gate/up pairs per workgroup (half a block)
+
+// Small area offsets (bytes from kSmall).
+constexpr int kPOff = 0;                            // probabilities [kSPositions]
+constexpr int kQOff = kPOff + kSPositions * 4;      // q, then value sums [128]
+constexpr int kKcOff = kQOff + 512;                 // this position's K row (F16) [128]
+constexpr int kVcOff = kKcOff + 256;                // this position's V row (F16) [128]
+constexpr int kYOff = kVcOff + 256;                 // normalised q and k [2][128]
+constexpr int kTagOff = kYOff + 1024;               // q, k, v words [3][128]
+constexpr int kRedOff = kTagOff + 3 * 128 * 8;      // doubles [8]
+constexpr int kLaneOff = kRedOff + 64;              // doubles [8]
+constexpr int kChainOff = kLaneOff + 64;            // doubles [8]
+constexpr int kMaxOff = kChainOff + 64;             // floats [4]
+constexpr int kExactOff = kMaxOff + 16;             // ints [4]
+constexpr int kInvOff = kExactOff + 16;             // float
+constexpr int kOkOff = kInvOff + 16;                // ints [4]
+constexpr int kPartOff = kOkOff + 16;               // partner maxima words [16]
+static_assert(kPartOff + 128 <= 8 * 1024, "small area");
+static_assert(kTagOff % 16 == 0 && kPartOff % 16 == 0, "16-byte LDS destinations");
+
+__device__ __forceinline__ unsigned err_load(const unsigned* e) {
+  return __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void err_raise(unsigned* e) {
+  __hip_atomic_fetch_or(e, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void put_word(u64* p, uint32_t gen, uint32_t bits) {
+  __hip_atomic_store(p, ((u64)gen << 32) | (u64)bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Quantised word: 16-bit tag and 16 side bits (the block scale's halves in
+// words 0 and 1 of a block) above four int8 codes.
+__device__ __forceinline__ void put_qword(u64* p, uint32_t gen, uint32_t side, uint32_t codes) {
+  __hip_atomic_store(p, ((u64)((gen << 16) | (side & 0xFFFFu)) << 32) | (u64)codes, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t qside(int k, float d) {
+  return k == 0 ? (f2u(d) & 0xFFFFu) : (k == 1 ? f2u(d) >> 16 : 0u);
+}
+// Position of word wi (values 4 wi .. 4 wi + 3, block wi / 8) in a
+// word-major row of B blocks.
+__device__ __forceinline__ int word_major(int wi, int B) { return (wi & 7) * B + (wi >> 3); }
+__device__ __forceinline__ bool current(const uint4& t, uint32_t want, uint32_t mask) {
+  return (t.y & mask) == want && (t.w & mask) == want;
+}
+
+// One wave: tagged words src[128 first, 128 total) into tag (same offsets)
+// until all carry the generation (high words equal `want` under `mask`).
+// The last chunk's last 64 bytes are polled first (two reads in flight), so
+// that an early consumer costs one small read per round trip; then rounds
+// over the chunks not yet current. The loads are device-coherent (sc1).
+// False after the spin bound or when another workgroup reported an error.
+__device__ bool gather_words(const u64* src, u64* tag, int first, int total, uint32_t want, uint32_t mask,
+                             unsigned* error) {
+  const int lane = threadIdx.x & (kWave - 1);
+  if (total <= first) return true;
+  long spin = 0;
+  {
+    const u64* s = src + (size_t)(total - 1) * 128 + 120;
+    u64* d = tag + (size_t)(total - 1) * 128 + 120;
+    if (lane < 4) __builtin_amdgcn_global_load_lds(s + 2 * lane, (lds_ptr)d, 16, 0, 16);
+    for (;; ++spin) {
+      if (lane < 4) __builtin_amdgcn_global_load_lds(s + 2 * lane, (lds_ptr)d, 16, 0, 16);
+      __builtin_amdgcn_s_waitcnt(1 | (7 << 4) | (15 << 8));  // vmcnt <= 1: the older poll is in
+      const uint4 t = lane < 4 ? *reinterpret_cast<const uint4*>(d + 2 * lane) : make_uint4(0, want, 0, want);
+      if (__all(current(t, want, mask))) break;
+      if (spin > kSSpin || ((spin & 63) == 63 && err_load(error))) {
+        if (lane == 0) err_raise(error);
+        __builtin_amdgcn_s_waitcnt(0);
+        return false;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  const int n = total - first;
+  u64 pending = n >= 64 ? ~0ull : ((1ull << n) - 1ull);
+  for (;; ++spin) {
+    for (u64 m = pending; m; m &= m - 1) {
+      const int k = first + __builtin_ctzll(m);
+      __builtin_amdgcn_global_load_lds(src + (size_t)k * 128 + 2 * lane, (lds_ptr)(tag + (size_t)k * 128), 16, 0, 16);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    for (u64 m = pending; m; m &= m - 1) {
+      const int j = __builtin_ctzll(m);
+      const uint4 t = *reinterpret_cast<const uint4*>(tag + (size_t)(first + j) * 128 + 2 * lane);
+      if (__all(current(t, want, mask))) pending &= ~(1ull << j);
+    }
+    if (!pending) return true;
+    if (spin > kSSpin || ((spin & 63) == 63 && err_load(error))) {
+      if (lane == 0) err_raise(error);
+      return false;
+    }
+  }
+}
+
+// One wave: three 128-word chunks at a, b, c into tag[0, 384), polled whole
+// in rounds of three reads, two rounds in flight.
+__device__ bool gather3(const u64* a, const u64* b, const u64* c, u64* tag, uint32_t gen, unsigned* error) {
+  const int lane = threadIdx.x & (kWave - 1);
+  auto round = [&] {
+    __builtin_amdgcn_global_load_lds(a + 2 * lane, (lds_ptr)(tag), 16, 0, 16);
+    __builtin_amdgcn_global_load_lds(b + 2 * lane, (lds_ptr)(tag + 128), 16, 0, 16);
+    __builtin_amdgcn_global_load_lds(c + 2 * lane, (lds_ptr)(tag + 256), 16, 0, 16);
+  };
+  round();
+  for (long spin = 0;; ++spin) {
+    round();
+    __builtin_amdgcn_s_waitcnt(3 | (7 << 4) | (15 << 8));  // vmcnt <= 3: the older round is in
+    bool all = true;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) all = all && __all(current(*reinterpret_cast<const uint4*>(tag + 128 * k + 2 * lane), gen, ~0u));
+    if (all) {
+      __builtin_amdgcn_s_waitcnt(0);  // the newer round writes the same current words
+      return true;
+    }
+    if (spin > kSSpin || ((spin & 63) == 63 && err_load(error))) {
+      if (lane == 0) err_raise(error);
+      __builtin_amdgcn_s_waitcnt(0);
+      return false;
+    }
+  }
+}
+
+// One wave: 16 tagged words at src into tag, two polls in flight.
+__device__ bool gather16(const u64* src, u64* tag, uint32_t gen, unsigned* error) {
+  const int lane = threadIdx.x & (kWave - 1);
+  auto poll = [&] {
+    if (lane < 8) __builtin_amdgcn_global_load_lds(src + 2 * lane, (lds_ptr)tag, 16, 0, 16);
+  };
+  poll();
+  for (long spin = 0;; ++spin) {
+    poll();
+    __builtin_amdgcn_s_waitcnt(1 | (7 << 4) | (15 << 8));
+    const uint4 t = lane < 8 ? *reinterpret_cast<const uint4*>(tag + 2 * lane) : make_uint4(0, gen, 0, gen);
+    if (__all(current(t, gen, ~0u))) {
+      __builtin_amdgcn_s_waitcnt(0);
+      return true;
+    }
+    if (spin > kSSpin || ((spin & 63) == 63 && err_load(error))) {
+      if (lane == 0) err_raise(error);
+      __builtin_amdgcn_s_waitcnt(0);
+      return false;
+    }
+  }
+}
+
+// Whether every wave's part succeeded (two barriers, so the flags can be
+// written again by the next call).
+__device__ __forceinline__ bool all_waves(bool ok, int* ok_s) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
+  if (lane == 0) ok_s[wave] = ok ? 1 : 0;
+  lds_barrier();
+  const bool r = (ok_s[0] & ok_s[1] & ok_s[2] & ok_s[3]) != 0;
+  lds_barrier();
+  return r;
+}
+
+// A workgroup's rows of one projection (K inputs, SLOTS storage rows) for
+// every session, as q8_gemm_few_kernel forms them: lane = (row step, block)
+// keeps its rows' 32-byte weight blocks and block scales in registers; for
+// each session's quantised input block it forms the exact int32 block dot
+// (v_dot4_i32_i8 x 8) and the term ((float)dot * w_scale) * x_scale into
+// LDS; then one lane per (row, session) adds the terms in block order.
+template <int K, int SLOTS>
+struct Slice {
+  static constexpr int B = K / 32, RS = kST / B, P = (SLOTS + RS - 1) / RS, TB = B + 4, KW = K / 4;
+  uint4 w0[P], w1[P];
+  float ws[P];
+
+  template <class RowOf>
+  __device__ __forceinline__ void load(const int8_t* w, const _Float16* s, RowOf row_of) {
+    const int tid = threadIdx.x, lrow = tid / B, b = tid - lrow * B;
+    const bool active = lrow < RS;
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      // Unconditional loads (row clamped into the matrix); rows past the
+      // slice are never summed.
+      const int i = lrow + RS * k;
+      const int sr = active && i < SLOTS ? row_of(i) : 0;
+      const uint4* wp = reinterpret_cast<const uint4*>(w + (size_t)sr * K + 32 * b);
+      w0[k] = wp[0];
+      w1[k] = wp[1];
+      ws[k] = (float)s[(size_t)sr * B + b];
+    }
+  }
+
+  // stage: the sessions' quantised rows as gathered words [S][KW] in
+  // word-major order (word j of block b at j B + b, so that the lanes of
+  // consecutive blocks read consecutive words); terms: [SLOTS][S][TB] floats.
+  __device__ __forceinline__ void products(const u64* stage, int S, float* terms) const {
+    const int tid = threadIdx.x, lrow = tid / B, b = tid - lrow * B;
+    if (lrow >= RS) return;
+    // The next session's block is read while this one is formed.
+    uint2 nx[8];
+    {
+      const uint2* xp = reinterpret_cast<const uint2*>(stage + b);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) nx[j] = xp[j * B];
+    }
+    for (int f = 0; f < S; ++f) {
+      uint2 u[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) u[j] = nx[j];
+      if (f + 1 < S) {
+        const uint2* xp = reinterpret_cast<const uint2*>(stage + (size_t)(f + 1) * KW + b);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) nx[j] = xp[j * B];
+      }
+      const float xsv = u2f((u[0].y & 0xFFFFu) | ((u[1].y & 0xFFFFu) << 16));
+#pragma unroll
+      for (int k = 0; k < P; ++k) {
+        const int i = lrow + RS * k;
+        if (i < SLOTS) {
+          // Two independent chains (integer sums: exact in any order).
+          int d0 = 0, d1 = 0;
+          d0 = __builtin_amdgcn_sdot4((int)w0[k].x, (int)u[0].x, d0, false);
+          d1 = __builtin_amdgcn_sdot4((int)w1[k].x, (int)u[4].x, d1, false);
+          d0 = __builtin_amdgcn_sdot4((int)w0[k].y, (int)u[1].x, d0, false);
+          d1 = __builtin_amdgcn_sdot4((int)w1[k].y, (int)u[5].x, d1, false);
+          d0 = __builtin_amdgcn_sdot4((int)w0[k].z, (int)u[2].x, d0, false);
+          d1 = __builtin_amdgcn_sdot4((int)w1[k].z, (int)u[6].x, d1, false);
+          d0 = __builtin_amdgcn_sdot4((int)w0[k].w, (int)u[3].x, d0, false);
+          d1 = __builtin_amdgcn_sdot4((int)w1[k].w, (int)u[7].x, d1, false);
+          const int dot = d0 + d1;
+          terms[((size_t)i * S + f) * TB + b] = fmul(fmul((float)dot, ws[k]), xsv);
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ static float row_sum(const float* terms, int i, int f, int S) {
+    const float* t = terms + ((size_t)i * S + f) * TB;
+    float sum = 0.0f;
+#pragma unroll 4
+    for (int b = 0; b < B; b += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(t + b);
+      sum = fadd(sum, v.x);
+      sum = fadd(sum, v.y);
+      sum = fadd(sum, v.z);
+      sum = fadd(sum, v.w);
+    }
+    return sum;
+  }
+  static constexpr size_t stage_bytes(int S) { return (size_t)S * KW * 8; }
+};
+
+// Gathers the sessions' quantised rows ([S][KW] words) on all four waves.
+template <int KW>
+__device__ __forceinline__ bool gather_rows(const u64* src, u64* stage, int S, uint32_t gen, unsigned* error, int* ok_s) {
+  const int wave = threadIdx.x >> 6;
+  const int n = S * KW / 128;
+  const bool ok = gather_words(src, stage, wave * n / 4, (wave + 1) * n / 4, gen << 16, kQMask, error);
+  return all_waves(ok, ok_s);
+}
+
+// RMSNorm + Q8_0 of one W-value row, norm_quantize_rows_kernel's arithmetic:
+// thread t holds values 4t + 1024c; the square sum in any tree order with
+// the reference order where the mean is unsettled (rms_inverse). read(k)
+// returns value k. Each thread's 4 codes and (every 8th thread) the block
+// scale go to emit(e, codes, d).
+template <int W, class Read, class Emit>
+__device__ __forceinline__ void norm_row(Read read, const float* norm_w, float eps, double* red_s, Emit emit) {
+  constexpr int NC = (W + 1023) / 1024;
+  const int tid = threadIdx.x;
+  float4 v[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int e = c * 1024 + 4 * tid;
+    v[c] = e < W ? make_float4(read(e), read(e + 1), read(e + 2), read(e + 3)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  double sq = 0.0;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    sq += (double)v[c].x * (double)v[c].x + (double)v[c].y * (double)v[c].y;
+    sq += (double)v[c].z * (double)v[c].z + (double)v[c].w * (double)v[c].w;
+  }
+  const float inverse = rms_inverse(block_sum_double(sq, red_s), W, eps, read);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int e = c * 1024 + 4 * tid;
+    if (e < W) {
+      const float4 w = *reinterpret_cast<const float4*>(norm_w + e);
+      const float x0 = fmul(fmul(v[c].x, inverse), w.x), x1 = fmul(fmul(v[c].y, inverse), w.y);
+      const float x2 = fmul(fmul(v[c].z, inverse), w.z), x3 = fmul(fmul(v[c].w, inverse), w.w);
+      float d;
+      const int packed = quantize4(x0, x1, x2, x3, &d);
+      emit(e, packed, d);
+    }
+  }
+}
+
+template <int W, int H, int KVH, int FF>
+__global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  constexpr int HS = 128, G = H / KVH, QW = H * HS, KVW = KVH * HS, NQKV = QW + 2 * KVW;
+  constexpr int R1 = NQKV / kSG, R2 = W / kSG, NGU = FF / kGuPairs;
+  static_assert(NQKV % kSG == 0 && W % kSG == 0 && FF % 32 == 0 && NGU <= kSG && NGU % 2 == 0, "shape");
+  using QkvSlice = Slice<W, R1>;
+  using OSlice = Slice<QW, R2>;
+  using GuSlice = Slice<W, 2 * kGuPairs>;
+  using DownSlice = Slice<FF, R2>;
+  static_assert(QkvSlice::stage_bytes(16) + (size_t)R1 * 16 * QkvSlice::TB * 4 <= (size_t)(kSmall - kVArea), "q/k/v area");
+  static_assert(OSlice::stage_bytes(16) + (size_t)R2 * 16 * OSlice::TB * 4 <= (size_t)kSmall, "o area");
+  static_assert(GuSlice::stage_bytes(16) + (size_t)2 * kGuPairs * 16 * GuSlice::TB * 4 + kGuPairs * 16 * 4 <=
+                    (size_t)kSmall, "gate/up area");
+  static_assert(DownSlice::stage_bytes(16) + (size_t)R2 * 16 * DownSlice::TB * 4 <= (size_t)kSmall, "down area");
+
+  const int w = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
+  const int S = a.S, L = a.layers;
+  if (err_load(a.error)) return;
+  const uint32_t g0 = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) *
+                          (uint32_t)(kPhases * L + 1) + 1u;
+  auto gen = [&](int l, int p) { return g0 + (uint32_t)(l * kPhases + p - 1); };
+
+  char* small = lds + kSmall;
+  float* p_s = reinterpret_cast<float*>(small + kPOff);
+  float* q_s = reinterpret_cast<float*>(small + kQOff);
+  _Float16* kcur_s = reinterpret_cast<_Float16*>(small + kKcOff);
+  _Float16* vcur_s = reinterpret_cast<_Float16*>(small + kVcOff);
+  float* y_s = reinterpret_cast<float*>(small + kYOff);
+  u64* qkv_tag = reinterpret_cast<u64*>(small + kTagOff);
+  double* red_s = reinterpret_cast<double*>(small + kRedOff);
+  double* lane_s = reinterpret_cast<double*>(small + kLaneOff);
+  double* chain_s = reinterpret_cast<double*>(small + kChainOff);
+  float* tmax_s = reinterpret_cast<float*>(small + kMaxOff);
+  int* exact_s = reinterpret_cast<int*>(small + kExactOff);
+  float* inv_s = reinterpret_cast<float*>(small + kInvOff);
+  int* ok_s = reinterpret_cast<int*>(small + kOkOff);
+  u64* part_s = reinterpret_cast<u64*>(small + kPartOff);
+
+  // Roles. Norm workgroups 17 s spread the session rows over the XCDs;
+  // attention unit w is (session w / H, query head w % H).
+  const int ns = (w % 17 == 0 && w / 17 < S) ? w / 17 : -1;
+  const int us = w / H, uh = w % H, kh = uh / G;
+  const bool unit = us < S;
+  int pos = 0, cap = 0;
+  const float *rcos = nullptr, *rsin = nullptr;
+  _Float16 *kbase = nullptr, *vbase = nullptr;
+  if (unit) {
+    const SessionRef& ss = a.sessions[us];
+    pos = min(*ss.position, a.max_positions - 1);
+    cap = ss.capacity;
+    rcos = ss.rope_cos;
+    rsin = ss.rope_sin;
+    kbase = ss.kcache;
+    vbase = ss.vcache;
+  }
+  const int nv = pos, n = pos + 1;  // earlier positions read from the cache; this one is local
+  // Exchange words per layer.
+  const size_t LX = (size_t)S * W, LQ = (size_t)S * (W / 4), LQKV = (size_t)S * NQKV, LATT = (size_t)S * (QW / 4),
+               LH = (size_t)S * (FF / 4);
+
+  // Residual rows of this workgroup's o/down rows: lane t < R2 S holds
+  // (row R2 w + t / S, session t % S).
+  float xres = 0.0f, ares = 0.0f;
+  const int ri = tid / max(S, 1), rf = tid - ri * max(S, 1), rrow = R2 * w + ri;
+  const bool rlane = tid < R2 * S;
+  if (rlane) xres = a.x_in[(size_t)rf * W + rrow];
+
+  for (int l = 0; l < L; ++l) {
+    const PersistentLayer& lw = a.layer_table[l];
+    // This layer's exchange words (each layer has its own: a slow reader of
+    // one layer's words never meets the next layer's).
+    u64* const tx = a.tx + (size_t)l * LX;
+    u64* const txq = a.txq + (size_t)l * LQ;
+    u64* const tqkv = a.tqkv + (size_t)l * LQKV;
+    u64* const tattq = a.tattq + (size_t)l * LATT;
+    u64* const ta = a.ta + (size_t)l * LX;
+    u64* const taq = a.taq + (size_t)l * LQ;
+    u64* const thq = a.thq + (size_t)l * LH;
+    // ---- attention unit: this layer's earlier K rows (one a thread, in
+    // registers) and V rows (to LDS), requested at the start of the layer --
+    // by a norm workgroup once its row is published, so that its gather does
+    // not wait behind them -- and used after q/k/v.
+    const _Float16* kc = unit ? kbase + ((size_t)l * KVH + kh) * (size_t)cap * HS : nullptr;
+    const _Float16* vc = unit ? vbase + ((size_t)l * KVH + kh) * (size_t)cap * HS : nullptr;
+    uint4 k0[16];
+    auto kv_loads = [&]() __attribute__((always_inline)) {
+      const char* src = reinterpret_cast<const char*>(vc);
+      const int bytes = nv * HS * 2;
+      for (int c = wave * 1024; c < bytes; c += 4 * 1024)
+        if (c + 16 * lane < bytes) __builtin_amdgcn_global_load_lds(src + c + 16 * lane, (lds_ptr)(lds + c), 16, 0, 0);
+      if (tid < nv) {
+        const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)tid * HS);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) k0[i] = row[i];
+      }
+    };
+    if (unit && ns < 0) kv_loads();
+
+    // ---- attention norm of session row ns (norm workgroups)
+    u64* qstage = reinterpret_cast<u64*>(lds + kVArea);  // q/k/v phase: staging, then terms
+    if (ns >= 0) {
+      u64* dst = txq + (size_t)ns * (W / 4);
+      auto emit = [&](int e, int packed, float d) {
+        put_qword(dst + word_major(e / 4, W / 32), gen(l, 1), qside((e / 4) & 7, d), (uint32_t)packed);
+      };
+      if (l == 0) {
+        const float* row = a.x_in + (size_t)ns * W;
+        norm_row<W>([&](int k) { return row[k]; }, lw.attn_norm, a.eps, red_s, emit);
+      } else {
+        const bool ok = gather_words(a.tx + (size_t)(l - 1) * LX + (size_t)ns * W, qstage, wave * (W / 128) / 4, (wave + 1) * (W / 128) / 4,
+                                     gen(l - 1, 8), ~0u, a.error);
+        if (!all_waves(ok, ok_s)) return;
+        norm_row<W>([&](int k) { return u2f((uint32_t)qstage[k]); }, lw.attn_norm, a.eps, red_s, emit);
+      }
+      lds_barrier();
+      if (unit) kv_loads();
+    }
+
+    // ---- q/k/v rows R1 w .. of every session
+    {
+      QkvSlice sl;
+      sl.load(lw.wqkv, lw.sqkv, [&](int i) { return R1 * w + i; });
+      if (!gather_rows<W / 4>(txq, qstage, S, gen(l, 1), a.error, ok_s)) return;
+      float* terms = reinterpret_cast<float*>(lds + kVArea + QkvSlice::stage_bytes(S));
+      sl.products(qstage, S, terms);
+      lds_barrier();
+      for (int t = tid; t < R1 * S; t += kST) {
+        const int i = t / S, f = t - i * S;
+        put_word(tqkv + (size_t)f * NQKV + R1 * w + i, gen(l, 2), f2u(QkvSlice::row_sum(terms, i, f, S)));
+      }
+    }
+
+    // ---- attention of (session us, query head uh)
+    if (unit) {
+      bool ok = true;
+      const u64* base = tqkv + (size_t)us * NQKV;
+      if (wave == 0) ok = gather3(base + uh * HS, base + QW + kh * HS, base + QW + KVW + kh * HS, qkv_tag, gen(l, 2), a.error);
+      if (!all_waves(ok, ok_s)) return;
+      // QK-norm and RoPE of q (threads 0-127) and k (128-255), v rounded to
+      // F16 (QwenDecoder.cs:186-203, Rope.cs:14-55); the first query head of
+      // the pair writes the K/V row.
+      {
+        const int part = tid >> 7, c = tid & 127, half = HS / 2;
+        const float v = u2f((uint32_t)qkv_tag[128 * part + c]);
+        const float nw = (part == 0 ? lw.q_norm : lw.k_norm)[c];
+        const float cs = rcos[(size_t)pos * half + (c & (half - 1))];
+        const float sn = rsin[(size_t)pos * half + (c & (half - 1))];
+        const double sq = wave_sum_double((double)v * (double)v);
+        if (lane == 0) red_s[wave] = sq;
+        lds_barrier();
+        const float inverse = rms_inverse(red_s[2 * part] + red_s[2 * part + 1], HS, a.eps,
+                                          [&](int k) { return u2f((uint32_t)qkv_tag[128 * part + k]); });
+        y_s[part * 128 + c] = fmul(fmul(v, inverse), nw);
+        lds_barrier();
+        const float* y = y_s + part * 128;
+        float r;
+        if (c < half) r = fadd(fmul(y[c], cs), -fmul(y[c + half], sn));
+        else r = fadd(fmul(y[c - half], sn), fmul(y[c], cs));
+        if (part == 0) {
+          q_s[c] = r;
+          const _Float16 v16 = to_half(u2f((uint32_t)qkv_tag[256 + c]));
+          vcur_s[c] = v16;
+          if (uh % G == 0) const_cast<_Float16*>(vc)[(size_t)pos * HS + c] = v16;
+        } else {
+          const _Float16 k16 = to_half(r);
+          kcur_s[c] = k16;
+          if (uh % G == 0) const_cast<_Float16*>(kc)[(size_t)pos * HS + c] = k16;
+        }
+      }
+      lds_barrier();
+      // Scores: one position per thread, eight channel-strided accumulators
+      // and their pairwise tree (AttentionAvx.cs:74-118).
+      if (tid < nv) {
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) score8(acc, k0[i], q_s + 8 * i);
+        const float sc = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
+        p_s[tid] = fdiv(sc, a.divisor);
+      }
+      for (int s = tid < nv ? tid + kST : tid; s < n; s += kST) {
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (s < nv) {
+          const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)s * HS);
+#pragma unroll
+          for (int i0 = 0; i0 < 16; i0 += 4) {
+            uint4 kk[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kk[i] = row[i0 + i];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) score8(acc, kk[i], q_s + 8 * (i0 + i));
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) score8(acc, reinterpret_cast<const uint4*>(kcur_s)[i], q_s + 8 * i);
+        }
+        const float sc = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
+        p_s[s] = fdiv(sc, a.divisor);
+      }
+      lds_barrier();
+      // Exact softmax (SoftmaxAvx.cs:11-58): the maximum, the numerators, the
+      // double denominator -- as wave trees when every numerator is 0 or in
+      // [2^-17, 1] (then every partial sum is exact), the reference's
+      // residue chains otherwise.
+      float m = -__builtin_inff();
+      for (int s = tid; s < n; s += kST) m = nan_max_p(m, p_s[s]);
+      m = wave_max_nan(m);
+      if (lane == 0) tmax_s[wave] = m;
+      lds_barrier();
+      const float mx = nan_max_p(nan_max_p(tmax_s[0], tmax_s[1]), nan_max_p(tmax_s[2], tmax_s[3]));
+      double dpart = 0.0;
+      bool dexact = true;
+      for (int s = tid; s < n; s += kST) {
+        const float ev = exp_ref(fadd(p_s[s], -mx));
+        p_s[s] = ev;
+        dpart += (double)ev;
+        dexact = dexact && (ev == 0.0f || (ev >= 0x1p-17f && ev <= 1.0f));
+      }
+      dpart = wave_sum_double(dpart);
+      const bool wexact = __all(dexact);
+      if (lane == 0) {
+        lane_s[wave] = dpart;
+        exact_s[wave] = wexact ? 1 : 0;
+      }
+      lds_barrier();
+      float inverse;
+      if (exact_s[0] & exact_s[1] & exact_s[2] & exact_s[3]) {
+        inverse = (float)(1.0 / (((lane_s[0] + lane_s[1]) + lane_s[2]) + lane_s[3]));
+      } else {  // (every thread takes the same branch)
+        const int full = n & ~7;
+        if (tid < 8) {
+          double acc = 0.0;
+          int s = tid;
+          for (; s + 56 < full; s += 64) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = p_s[s + 8 * k];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc = acc + (double)v[k];
+          }
+          for (; s < full; s += 8) acc = acc + (double)p_s[s];
+          chain_s[tid] = acc;
+        }
+        lds_barrier();
+        if (tid == 0) {
+          double sum = ((chain_s[0] + chain_s[4]) + (chain_s[1] + chain_s[5])) + ((chain_s[2] + chain_s[6]) + (chain_s[3] + chain_s[7]));
+          for (int s = full; s < n; ++s) sum = sum + (double)p_s[s];
+          inv_s[0] = (float)(1.0 / sum);
+        }
+        lds_barrier();
+        inverse = inv_s[0];
+      }
+      for (int s = tid; s < n; s += kST) p_s[s] = fmul(p_s[s], inverse);
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's V rows are in LDS
+      lds_barrier();
+      // Time-ordered value sums, one channel per thread (AttentionAvx.cs:120-171).
+      if (tid < HS) {
+        const _Float16* v = reinterpret_cast<const _Float16*>(lds) + tid;
+        float acc = 0.0f;
+        int s = 0;
+        for (; s + 16 <= nv; s += 16) {
+          _Float16 x[16];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) x[k] = v[(s + k) * HS];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) acc = fadd(acc, mulh(p_s[s + k], x[k]));
+        }
+        for (; s < nv; ++s) acc = fadd(acc, mulh(p_s[s], v[s * HS]));
+        acc = fadd(acc, mulh(p_s[pos], vcur_s[tid]));
+        q_s[tid] = acc;
+      }
+      lds_barrier();
+      if (tid < HS / 4) {
+        const float4 v4 = *reinterpret_cast<const float4*>(q_s + 4 * tid);
+        float d;
+        const int packed = quantize4(v4.x, v4.y, v4.z, v4.w, &d);
+        put_qword(tattq + (size_t)us * (QW / 4) + word_major(uh * (HS / 4) + tid, QW / 32), gen(l, 3), qside(tid & 7, d),
+                  (uint32_t)packed);
+      }
+    }
+    lds_barrier();
+
+    // ---- o rows R2 w .. + the residual
+    {
+      OSlice sl;
+      sl.load(lw.wo, lw.so, [&](int i) { return R2 * w + i; });
+      u64* stage = reinterpret_cast<u64*>(lds);
+      if (!gather_rows<QW / 4>(tattq, stage, S, gen(l, 3), a.error, ok_s)) return;
+      float* terms = reinterpret_cast<float*>(lds + OSlice::stage_bytes(S));
+      sl.products(stage, S, terms);
+      lds_barrier();
+      if (rlane) {
+        ares = fadd(OSlice::row_sum(terms, ri, rf, S), xres);
+        put_word(ta + (size_t)rf * W + rrow, gen(l, 4), f2u(ares));
+      }
+      lds_barrier();
+    }
+
+    // ---- ffn norm of session row ns
+    if (ns >= 0) {
+      u64* stage = reinterpret_cast<u64*>(lds);
+      const bool ok = gather_words(ta + (size_t)ns * W, stage, wave * (W / 128) / 4, (wave + 1) * (W / 128) / 4,
+                                   gen(l, 4), ~0u, a.error);
+      if (!all_waves(ok, ok_s)) return;
+      u64* dst = taq + (size_t)ns * (W / 4);
+      norm_row<W>([&](int k) { return u2f((uint32_t)stage[k]); }, lw.ffn_norm, a.eps, red_s,
+                  [&](int e, int packed, float d) {
+                    put_qword(dst + word_major(e / 4, W / 32), gen(l, 5), qside((e / 4) & 7, d), (uint32_t)packed);
+                  });
+      lds_barrier();
+    }
+
+    // ---- gate/up pairs kGuPairs w ..: SwiGLU, then Q8_0 of the half block
+    if (w < NGU) {
+      const int p0 = kGuPairs * w;
+      GuSlice sl;
+      sl.load(lw.wgu, lw.sgu, [&](int i) {
+        const int p = p0 + (i < kGuPairs ? i : i - kGuPairs), kind = i < kGuPairs ? 0 : 1;
+        if (a.gu_map) return a.gu_map[2 * p + kind];
+        // Tiles of `base` (the first `extra` of them base + 1) gate rows,
+        // then the same count of up rows.
+        const int base = a.gu_base, big = a.gu_extra * (base + 1);
+        int r0, count;
+        if (p < big) {
+          r0 = p / (base + 1) * (base + 1);
+          count = base + 1;
+        } else {
+          r0 = big + (p - big) / base * base;
+          count = base;
+        }
+        return 2 * r0 + kind * count + (p - r0);
+      });
+      u64* stage = reinterpret_cast<u64*>(lds);
+      if (!gather_rows<W / 4>(taq, stage, S, gen(l, 5), a.error, ok_s)) return;
+      float* terms = reinterpret_cast<float*>(lds + GuSlice::stage_bytes(S));
+      sl.products(stage, S, terms);
+      lds_barrier();
+      float* h_s = terms + (size_t)2 * kGuPairs * S * GuSlice::TB;  // [S][kGuPairs]
+      for (int t = tid; t < kGuPairs * S; t += kST) {
+        const int i = t / S, f = t - i * S;
+        // SwiGLU (Elementwise.cs:167-196).
+        const float g = GuSlice::row_sum(terms, i, f, S), u = GuSlice::row_sum(terms, kGuPairs + i, f, S);
+        h_s[f * kGuPairs + i] = fmul(fdiv(g, fadd(1.0f, exp_ref(-g))), u);
+      }
+      lds_barrier();
+      if (wave == 0) {
+        // Half-block maxima of the absolute bit patterns, one session a lane,
+        // swapped with the workgroup holding the block's other half.
+        uint32_t mine = 0u;
+        if (lane < S) {
+#pragma unroll
+          for (int i = 0; i < kGuPairs; ++i) {
+            const uint32_t t = f2u(h_s[lane * kGuPairs + i]) & 0x7fffffffu;
+            mine = t > mine ? t : mine;
+          }
+        }
+        if (lane < 16) put_word(a.tmax + (size_t)w * 16 + lane, gen(l, 6), mine);
+        const bool ok = gather16(a.tmax + (size_t)(w ^ 1) * 16, part_s, gen(l, 6), a.error);
+        if (ok) {
+          const uint32_t other = lane < 16 ? (uint32_t)part_s[lane] : 0u;
+          const uint32_t mx = other > mine ? other : mine;
+          float inv;
+          const float d = block_scale(mx, &inv);
+          // Lane t < 4 S quantises values 4 j .. 4 j + 3 of session t / 4.
+          const int f = lane >> 2, j = lane & 3;
+          const float df = __shfl(d, f), invf = __shfl(inv, f);
+          if (f < S) {
+            const float* hv = h_s + f * kGuPairs + 4 * j;
+            const uint32_t codes = (uint32_t)(uint8_t)quantize_value(hv[0], invf) |
+                                   ((uint32_t)(uint8_t)quantize_value(hv[1], invf) << 8) |
+                                   ((uint32_t)(uint8_t)quantize_value(hv[2], invf) << 16) |
+                                   ((uint32_t)(uint8_t)quantize_value(hv[3], invf) << 24);
+            const int k = 4 * (w & 1) + j;
+            put_qword(thq + (size_t)f * (FF / 4) + k * (FF / 32) + (w >> 1), gen(l, 7), qside(k, df), codes);
+          }
+        }
+        if (lane == 0) ok_s[0] = ok ? 1 : 0;
+      }
+      lds_barrier();
+      if (!ok_s[0]) return;
+      lds_barrier();
+    }
+
+    // ---- down rows R2 w .. + the residual
+    {
+      DownSlice sl;
+      sl.load(lw.wd, lw.sd, [&](int i) { return R2 * w + i; });
+      u64* stage = reinterpret_cast<u64*>(lds);
+      if (!gather_rows<FF / 4>(thq, stage, S, gen(l, 7), a.error, ok_s)) return;
+      float* terms = reinterpret_cast<float*>(lds + DownSlice::stage_bytes(S));
+      sl.products(stage, S, terms);
+      lds_barrier();
+      if (rlane) {
+        xres = fadd(DownSlice::row_sum(terms, ri, rf, S), ares);
+        put_word(tx + (size_t)rf * W + rrow, gen(l, 8), f2u(xres));
+      }
+      lds_barrier();
+    }
+  }
+
+  // ---- output norm of session row ns, as Q8_0 rows for the lm_head
+  if (ns >= 0) {
+    u64* stage = reinterpret_cast<u64*>(lds);
+    const bool ok = gather_words(a.tx + (size_t)(L - 1) * LX + (size_t)ns * W, stage, wave * (W / 128) / 4, (wave + 1) * (W / 128) / 4,
+                                 gen(L - 1, 8), ~0u, a.error);
+    if (!all_waves(ok, ok_s)) return;
+    int8_t* xq = a.xq_out + (size_t)ns * W;
+    float* xs = a.xs_out + (size_t)ns * (W / 32);
+    norm_row<W>([&](int k) { return u2f((uint32_t)stage[k]); }, a.output_norm, a.eps, red_s, [&](int e, int packed, float d) {
+      *reinterpret_cast<int*>(xq + e) = packed;
+      if ((tid & 7) == 0) xs[e >> 5] = d;
+    });
+    // Every workgroup has read the epoch (each published its last down
+    // rows, which this gather waited for): the next launch's generations.
+    if (ns == 0 && tid == 0) *a.epoch = *a.epoch + 1;
+  }
+}
+
+template <int W, int H, int KVH, int FF>
+hipError_t launch_shape(const SessionStepArgs& a, hipStream_t s) {
+  static const hipError_t raised = hipFuncSetAttribute(reinterpret_cast<const void*>(session_step_kernel<W, H, KVH, FF>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kSLds);
+  if (raised != hipSuccess) return raised;
+  session_step_kernel<W, H, KVH, FF><<<kSG, kST, kSLds, s>>>(a);
+  return hipGetLastError();
+}
+
+template <int W, int H, int KVH, int FF>
+int blocks_per_cu() {
+  int b = 0;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(session_step_kernel<W, H, KVH, FF>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kSLds) != hipSuccess)
+    return 0;
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, session_step_kernel<W, H, KVH, FF>, kST, kSLds) == hipSuccess
+             ? b
+             : 0;
+}
+
+}  // namespace
+
+// Shapes with an instantiation: Qwen3-0.6B and the reduced Qwen3-shaped
+// decoder of the quick parity runs.
+bool session_step_supported(int width, int heads, int kv_heads, int head_size, int ffn) {
+  if (head_size != 128) return false;
+  return (width == 1024 && heads == 16 && kv_heads == 8 && ffn == 3072) ||
+         (width == 512 && heads == 4 && kv_heads == 2 && ffn == 1024);
+}
+
+int session_step_positions() { return kSPositions; }
+int session_step_groups() { return kSG; }
+
+int session_step_blocks_per_cu(int width) {
+  return width == 1024 ? blocks_per_cu<1024, 16, 8, 3072>() : blocks_per_cu<512, 4, 2, 1024>();
+}
+
+hipError_t launch_session_step(const SessionStepArgs& a, hipStream_t s) {
+  if (!session_step_supported(a.width, a.heads, a.kv_heads, a.head_size, a.ffn)) return hipErrorInvalidValue;
+  if (a.S < 1 || a.S > 16 || a.S * a.heads > kSG || a.max_positions < 1 || a.max_positions > kSPositions || a.layers < 1)
+    return hipErrorInvalidValue;
+  if (a.width == 1024) return launch_shape<1024, 16, 8, 3072>(a, s);
+  return launch_shape<512, 4, 2, 1024>(a, s);
+}
+
+}  // namespace fah
