@@ -338,7 +338,11 @@ int fah_decoder_create_session(fah_decoder* parent, int capacity, fah_decoder** 
  * takes every row's greedy token. Each session's tokens equal those of
  * fah_decoder_generate on it alone. All sessions share one weight set
  * (fah_decoder_create_session) and each must hold logits from its last
- * decode. tokens[count][steps], row i for sessions[i]. */
+ * decode. tokens[count][steps], row i for sessions[i]. Qwen3-0.6B-shaped
+ * batches whose largest capacity is at most 320 run the layers in one
+ * launch that needs every CU (the call holds the device meanwhile); if it
+ * cannot complete, the call returns FAH_ERROR_DEVICE with every session back
+ * at its starting position and without logits. */
 int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int steps, int32_t* tokens);
 
 /* Cross-context step batching (the server side of FunAsr.Transcribe,

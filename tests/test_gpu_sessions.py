@@ -36,7 +36,13 @@ def _alone(backend, w, prefix, steps, capacity):
         d.close()
 
 
-def test_sessions_match_each_session_alone(backend, oracle_lib):
+@pytest.mark.parametrize("wide", [256, 512], ids=["one_launch", "kernel_per_projection"])
+def test_sessions_match_each_session_alone(backend, oracle_lib, wide):
+    """Five sessions of the reduced shape, one of capacity `wide`: the batch's
+    position bound is the largest capacity, so 256 runs the layers in one
+    launch and 512 (past the one-launch step's 320 positions) on the kernel
+    per projection. Tokens and K/V rows equal each session decoded alone, and
+    the tokens equal the oracle's."""
     from funasrnet_amd.hip import HipDecoder
     cfg = model.small_config(layers=2)
     w = model.synthetic(cfg, seed=21)
@@ -44,11 +50,11 @@ def test_sessions_match_each_session_alone(backend, oracle_lib):
     prefixes = _prefixes(cfg, lengths, 40)
     parent = HipDecoder(backend, w, capacity=128)
     # The parent takes part too; one session has a different capacity.
-    sessions = [parent] + [parent.session(128 if i != 2 else 256) for i in range(1, len(lengths))]
+    sessions = [parent] + [parent.session(128 if i != 2 else wide) for i in range(1, len(lengths))]
     try:
         for d, p in zip(sessions, prefixes):
             d.decode(p, p.shape[0])
-        print(f"sessions small count={len(sessions)} steps={steps}", flush=True)
+        print(f"sessions small count={len(sessions)} steps={steps} wide={wide}", flush=True)
         toks = HipDecoder.generate_sessions(sessions, steps)
         assert toks.shape == (len(sessions), steps)
         for i, (d, p) in enumerate(zip(sessions, prefixes)):
