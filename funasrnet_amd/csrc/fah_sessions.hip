@@ -379,9 +379,12 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   int* ok_s = reinterpret_cast<int*>(small + kOkOff);
   u64* part_s = reinterpret_cast<u64*>(small + kPartOff);
 
-  // Roles. Norm workgroups 17 s spread the session rows over the XCDs;
-  // attention unit w is (session w / H, query head w % H).
-  const int ns = (w % 17 == 0 && w / 17 < S) ? w / 17 : -1;
+  // Roles. The norm rows of session s on workgroup 192 + s + 16 (s % 4):
+  // past the gate/up workgroups (their ffn norm does not delay a gate/up
+  // share), one XCD per session row mod 8. Attention unit w is (session
+  // w / H, query head w % H).
+  static_assert(FF / kGuPairs <= 192, "norm workgroups hold no gate/up share");
+  const int nr = w - 192, ns = (nr >= 0 && (nr & 15) + 16 * ((nr & 15) & 3) == nr && (nr & 15) < S) ? (nr & 15) : -1;
   const int us = w / H, uh = w % H, kh = uh / G;
   const bool unit = us < S;
   int pos = 0, cap = 0;
@@ -439,6 +442,13 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
     };
     if (unit && ns < 0) kv_loads();
 
+    // The q/k/v weight slice: requested now, or by a norm workgroup once its
+    // row is gathered (its polls would wait behind the loads), so that its
+    // products do not start later than the others'.
+    QkvSlice qsl;
+    auto qkv_weights = [&]() __attribute__((always_inline)) { qsl.load(lw.wqkv, lw.sqkv, [&](int i) { return R1 * w + i; }); };
+    if (ns < 0) qkv_weights();
+
     // ---- attention norm of session row ns (norm workgroups)
     u64* qstage = reinterpret_cast<u64*>(lds + kVArea);  // q/k/v phase: staging, then terms
     if (ns >= 0) {
@@ -447,12 +457,14 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
         put_qword(dst + word_major(e / 4, W / 32), gen(l, 1), qside((e / 4) & 7, d), (uint32_t)packed);
       };
       if (l == 0) {
+        qkv_weights();
         const float* row = a.x_in + (size_t)ns * W;
         norm_row<W>([&](int k) { return row[k]; }, lw.attn_norm, a.eps, red_s, emit);
       } else {
         const bool ok = gather_words(a.tx + (size_t)(l - 1) * LX + (size_t)ns * W, qstage, wave * (W / 128) / 4, (wave + 1) * (W / 128) / 4,
                                      gen(l - 1, 8), ~0u, a.error);
         if (!all_waves(ok, ok_s)) return;
+        qkv_weights();
         norm_row<W>([&](int k) { return u2f((uint32_t)qstage[k]); }, lw.attn_norm, a.eps, red_s, emit);
       }
       lds_barrier();
@@ -461,11 +473,9 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
 
     // ---- q/k/v rows R1 w .. of every session
     {
-      QkvSlice sl;
-      sl.load(lw.wqkv, lw.sqkv, [&](int i) { return R1 * w + i; });
       if (!gather_rows<W / 4>(txq, qstage, S, gen(l, 1), a.error, ok_s)) return;
       float* terms = reinterpret_cast<float*>(lds + kVArea + QkvSlice::stage_bytes(S));
-      sl.products(qstage, S, terms);
+      qsl.products(qstage, S, terms);
       lds_barrier();
       for (int t = tid; t < R1 * S; t += kST) {
         const int i = t / S, f = t - i * S;
