@@ -387,6 +387,7 @@ struct fah_decoder {
   int lm_groups = 0;
   int host_position = 0;
   bool have_logits = false;
+  bool fail_sessions = false;  // fah_decoder_fail_next_step: the next one-launch lock-step step fails too
   hipGraphExec_t graph_row = nullptr, graph_logits = nullptr, graph_step = nullptr;
   // Persistent single-launch step (one workgroup per CU), when the shape has
   // an instantiation and the device has the CUs for it.
@@ -972,6 +973,7 @@ void recover_step_error(fah_decoder* d) {
   check(hipMemcpyAsync(&e, d->error.ptr, 4, hipMemcpyDeviceToHost, s), "D2H error word");
   check(hipStreamSynchronize(s), "hipStreamSynchronize");
   if (!e) return;
+  d->fail_sessions = false;  // the preset, if any, is consumed by this step
   check(hipMemcpyAsync(&epoch, d->epoch.ptr, 4, hipMemcpyDeviceToHost, s), "D2H epoch");
   check(hipStreamSynchronize(s), "hipStreamSynchronize");
   epoch += 2;
@@ -1281,7 +1283,28 @@ void recover_session_step(SessionBatch& b, fah_decoder* const* sessions, int cou
     sessions[i]->have_logits = false;
   }
   check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  if (e & kErrorPreset) throw DeviceError{"lock-step sessions step: stopped by the host (fah_decoder_fail_next_step)"};
   throw DeviceError{"lock-step sessions step: an exchange timed out (workgroups not co-resident?)"};
+}
+
+// Before the steps of a one-launch batch: a session marked by
+// fah_decoder_fail_next_step makes the batch's next launch end at its entry
+// check (the word is set before the step is enqueued, never inside it); the
+// mark and the session's own preset are consumed.
+void preset_session_failure(SessionBatch& b, fah_decoder* const* sessions, int count, hipStream_t s) {
+  if (!b.fused) return;
+  bool any = false;
+  const unsigned preset = kErrorPreset, zero = 0;
+  for (int i = 0; i < count; ++i) {
+    fah_decoder* d = sessions[i];
+    if (!d->fail_sessions) continue;
+    any = true;
+    d->fail_sessions = false;
+    if (d->persistent) check(hipMemcpyAsync(d->error.ptr, &zero, 4, hipMemcpyHostToDevice, s), "H2D error word");
+  }
+  if (!any) return;
+  check(hipMemcpyAsync(b.error.ptr, &preset, 4, hipMemcpyHostToDevice, s), "H2D error word");
+  check(hipStreamSynchronize(s), "hipStreamSynchronize");  // (the copies read these locals)
 }
 
 // Row buffers and the captured lock-step step of `count` sessions of d0's
@@ -2357,6 +2380,7 @@ int fah_decoder_fail_next_step(fah_decoder* d) {
     const unsigned preset = kErrorPreset;
     check(hipMemcpyAsync(d->error.ptr, &preset, 4, hipMemcpyHostToDevice, d->ctx->stream), "H2D error word");
     check(hipStreamSynchronize(d->ctx->stream), "sync");
+    d->fail_sessions = true;
     return FAH_OK;
   });
 }
@@ -2421,6 +2445,7 @@ int fah_decoder_generate_sessions(fah_decoder* const* sessions, int count, int s
     SessionBatch& b = *c->batch;
     for (int i = 0; i < count; ++i)
       check(hipMemsetAsync(sessions[i]->history_count.ptr, 0, 4, s), "reset history");
+    preset_session_failure(b, sessions, count, s);
     for (int i = 0; i < steps; ++i) {
       if (b.graph) check(hipGraphLaunch(b.graph, s), "hipGraphLaunch");
       else enqueue_sessions_step(d0, b, s);
@@ -2553,6 +2578,7 @@ void run_batch(fah_batcher* b, const std::vector<BatchRequest*>& reqs) {
       else work.emplace(*c);
       if (!batch) batch = make_session_batch(sessions[0], count, b->max_positions, s, fused);
       upload_session_table(*batch, sessions.data(), count, s);
+      preset_session_failure(*batch, sessions.data(), count, s);
       const fah::SessionRef* table = batch->table.as<fah::SessionRef>();
       batch->tokens.ensure((size_t)fah::kFewFrames * 4);
       check(fah::launch_session_batch_io(table, count, nullptr, s), "reset histories");

@@ -19,10 +19,11 @@
  * to the device once at upload and are immutable afterwards. A context owns
  * one HIP stream; calls on one context are serialised by the library. Calls
  * on different contexts may be made from different threads: their work is
- * enqueued under a per-device lock, and a persistent decode step (which
- * needs every CU of the device) first waits for the work already enqueued
- * by the other contexts and keeps the device to itself until it has
- * finished, so their kernels never run beside it.
+ * enqueued under a per-device lock, and a persistent decode step or a
+ * lock-step sessions step that runs the layers in one launch (both need
+ * every CU of the device) first waits for the work already enqueued by the
+ * other contexts and keeps the device to itself until it has finished, so
+ * their kernels never run beside it.
  *
  * Lifetime: weights and decoders keep their context's state alive.
  * fah_context_destroy releases the handle (which must not be used again);
@@ -424,9 +425,13 @@ int fah_decoder_attention_time(fah_decoder* decoder, double* milliseconds, int* 
  * entry check (every workgroup exits normally) and the call reports
  * FAH_ERROR_DEVICE. The failed call restores the device state from the
  * host's (position, epoch, empty history) and drops its logits, as after an
- * exchange that timed out. FAH_DECLINED when the decoder does not run the
- * persistent step. No reference counterpart (the reference's failure path is
- * a thrown exception, Vk.cs:57-61). */
+ * exchange that timed out. If the decoder's next device step is a lock-step
+ * call that runs the layers in one launch (fah_decoder_generate_sessions or a
+ * batcher batch), that launch fails the same way instead: every session of
+ * the call returns to its starting position without logits. FAH_DECLINED
+ * when the decoder does not run the persistent step. No reference
+ * counterpart (the reference's failure path is a thrown exception,
+ * Vk.cs:57-61). */
 int fah_decoder_fail_next_step(fah_decoder* decoder);
 
 /* 2 when decode steps run as one persistent launch with XCD-local roles

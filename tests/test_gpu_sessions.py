@@ -90,6 +90,54 @@ def test_sessions_match_each_session_alone(backend, oracle_lib, wide):
         parent.close()
 
 
+def test_sessions_failed_step_recovers(backend):
+    """A one-launch lock-step call stopped by the host
+    (fah_decoder_fail_next_step on one session: the batch's error word is set
+    before the launch, so every workgroup ends at its entry check) fails with
+    the device error, leaves every session at its starting position without
+    logits, and the sessions then continue exactly as decoders that never
+    failed (FunAsr.cs:167-178 after a Decode of the last token)."""
+    from funasrnet_amd import hip
+    from funasrnet_amd.hip import HipDecoder
+    cfg = model.small_config(layers=2)
+    w = model.synthetic(cfg, seed=23)
+    lengths = [7, 12, 20]
+    prefixes = _prefixes(cfg, lengths, 60)
+    parent = HipDecoder(backend, w, capacity=96)
+    sessions = [parent] + [parent.session(96) for _ in range(len(lengths) - 1)]
+    lib = hip.load()
+    try:
+        assert all(d.persistent for d in sessions)
+        for d, p in zip(sessions, prefixes):
+            d.decode(p, p.shape[0])
+        print("sessions failure recovery", flush=True)
+        first = HipDecoder.generate_sessions(sessions, 3)
+        assert lib.fah_decoder_fail_next_step(sessions[1].handle) == hip.OK
+        with pytest.raises(RuntimeError, match="stopped by the host"):
+            HipDecoder.generate_sessions(sessions, 2)
+        for d, p in zip(sessions, prefixes):
+            assert d.position == p.shape[0] + 3
+        with pytest.raises(RuntimeError, match="no logits"):
+            HipDecoder.generate_sessions(sessions, 1)
+        for d, t in zip(sessions, first[:, -1]):
+            d.decode(d.embed([int(t)]), 1)
+        second = HipDecoder.generate_sessions(sessions, 4)
+        for i, p in enumerate(prefixes):
+            ref = HipDecoder(backend, w, capacity=96)
+            try:
+                ref.decode(p, p.shape[0])
+                a = ref.generate(3).tolist()
+                assert a == first[i].tolist(), i
+                ref.decode(ref.embed([a[-1]]), 1)
+                assert ref.generate(4).tolist() == second[i].tolist(), i
+            finally:
+                ref.close()
+    finally:
+        for d in sessions[1:]:
+            d.close()
+        parent.close()
+
+
 def test_sessions_reject_bad_batches(backend):
     from funasrnet_amd.hip import HipDecoder
     cfg = model.small_config(layers=1)
