@@ -344,17 +344,22 @@ template <int W, int H, int KVH, int FF>
 __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   constexpr int HS = 128, G = H / KVH, QW = H * HS, KVW = KVH * HS, NQKV = QW + 2 * KVW;
-  constexpr int R1 = NQKV / kSG, R2 = W / kSG, NGU = FF / kGuPairs;
+  // o and down: kOGroups groups of sessions, each workgroup R2 rows of one
+  // group (fewer sessions a workgroup: less of the exchanged vectors to read,
+  // more weight rows, which are requested before the wait).
+  constexpr int kOGroups = 4, kOSessions = 16 / kOGroups;
+  constexpr int R1 = NQKV / kSG, R2 = W * kOGroups / kSG, NGU = FF / kGuPairs;
   static_assert(NQKV % kSG == 0 && W % kSG == 0 && FF % 32 == 0 && NGU <= kSG && NGU % 2 == 0, "shape");
   using QkvSlice = Slice<W, R1>;
   using OSlice = Slice<QW, R2>;
   using GuSlice = Slice<W, 2 * kGuPairs>;
   using DownSlice = Slice<FF, R2>;
   static_assert(QkvSlice::stage_bytes(16) + (size_t)R1 * 16 * QkvSlice::TB * 4 <= (size_t)(kSmall - kVArea), "q/k/v area");
-  static_assert(OSlice::stage_bytes(16) + (size_t)R2 * 16 * OSlice::TB * 4 <= (size_t)kSmall, "o area");
+  static_assert(OSlice::stage_bytes(kOSessions) + (size_t)R2 * kOSessions * OSlice::TB * 4 <= (size_t)kSmall, "o area");
   static_assert(GuSlice::stage_bytes(16) + (size_t)2 * kGuPairs * 16 * GuSlice::TB * 4 + kGuPairs * 16 * 4 <=
                     (size_t)kSmall, "gate/up area");
-  static_assert(DownSlice::stage_bytes(16) + (size_t)R2 * 16 * DownSlice::TB * 4 <= (size_t)kSmall, "down area");
+  static_assert(DownSlice::stage_bytes(kOSessions) + (size_t)R2 * kOSessions * DownSlice::TB * 4 <= (size_t)kSmall,
+                "down area");
 
   const int w = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & (kWave - 1);
   const int S = a.S, L = a.layers;
@@ -404,11 +409,13 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   const size_t LX = (size_t)S * W, LQ = (size_t)S * (W / 4), LQKV = (size_t)S * NQKV, LATT = (size_t)S * (QW / 4),
                LH = (size_t)S * (FF / 4);
 
-  // Residual rows of this workgroup's o/down rows: lane t < R2 S holds
-  // (row R2 w + t / S, session t % S).
+  // o/down share: rows R2 (w / kOGroups) .. of sessions f0 .. f0 + Sg - 1
+  // (group w % kOGroups). Their residual: lane t < R2 Sg holds (row
+  // R2 (w / kOGroups) + t / Sg, session f0 + t % Sg).
+  const int f0 = kOSessions * (w % kOGroups), Sg = max(0, min(kOSessions, S - f0)), orow0 = R2 * (w / kOGroups);
   float xres = 0.0f, ares = 0.0f;
-  const int ri = tid / max(S, 1), rf = tid - ri * max(S, 1), rrow = R2 * w + ri;
-  const bool rlane = tid < R2 * S;
+  const int ri = tid / max(Sg, 1), rf = f0 + tid - ri * max(Sg, 1), rrow = orow0 + ri;
+  const bool rlane = tid < R2 * Sg;
   if (rlane) xres = a.x_in[(size_t)rf * W + rrow];
 
   for (int l = 0; l < L; ++l) {
@@ -632,17 +639,17 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
     }
     lds_barrier();
 
-    // ---- o rows R2 w .. + the residual
-    {
+    // ---- o rows orow0 .. of sessions f0 .. + the residual
+    if (Sg > 0) {
       OSlice sl;
-      sl.load(lw.wo, lw.so, [&](int i) { return R2 * w + i; });
+      sl.load(lw.wo, lw.so, [&](int i) { return orow0 + i; });
       u64* stage = reinterpret_cast<u64*>(lds);
-      if (!gather_rows<QW / 4>(tattq, stage, S, gen(l, 3), a.error, ok_s)) return;
-      float* terms = reinterpret_cast<float*>(lds + OSlice::stage_bytes(S));
-      sl.products(stage, S, terms);
+      if (!gather_rows<QW / 4>(tattq + (size_t)f0 * (QW / 4), stage, Sg, gen(l, 3), a.error, ok_s)) return;
+      float* terms = reinterpret_cast<float*>(lds + OSlice::stage_bytes(Sg));
+      sl.products(stage, Sg, terms);
       lds_barrier();
       if (rlane) {
-        ares = fadd(OSlice::row_sum(terms, ri, rf, S), xres);
+        ares = fadd(OSlice::row_sum(terms, ri, rf - f0, Sg), xres);
         put_word(ta + (size_t)rf * W + rrow, gen(l, 4), f2u(ares));
       }
       lds_barrier();
@@ -733,17 +740,17 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
       lds_barrier();
     }
 
-    // ---- down rows R2 w .. + the residual
-    {
+    // ---- down rows orow0 .. of sessions f0 .. + the residual
+    if (Sg > 0) {
       DownSlice sl;
-      sl.load(lw.wd, lw.sd, [&](int i) { return R2 * w + i; });
+      sl.load(lw.wd, lw.sd, [&](int i) { return orow0 + i; });
       u64* stage = reinterpret_cast<u64*>(lds);
-      if (!gather_rows<FF / 4>(thq, stage, S, gen(l, 7), a.error, ok_s)) return;
-      float* terms = reinterpret_cast<float*>(lds + DownSlice::stage_bytes(S));
-      sl.products(stage, S, terms);
+      if (!gather_rows<FF / 4>(thq + (size_t)f0 * (FF / 4), stage, Sg, gen(l, 7), a.error, ok_s)) return;
+      float* terms = reinterpret_cast<float*>(lds + DownSlice::stage_bytes(Sg));
+      sl.products(stage, Sg, terms);
       lds_barrier();
       if (rlane) {
-        xres = fadd(DownSlice::row_sum(terms, ri, rf, S), ares);
+        xres = fadd(DownSlice::row_sum(terms, ri, rf - f0, Sg), ares);
         put_word(tx + (size_t)rf * W + rrow, gen(l, 8), f2u(xres));
       }
       lds_barrier();
