@@ -50,7 +50,7 @@ constexpr int kSmall = kSLds - 8 * 1024;      // small attention and exchange bu
 constexpr int kPhases = 8;                    // exchanges per layer
 constexpr long kSSpin = 1L << 21;             // bounded polls per wait (~1-2 s)
 constexpr uint32_t kQMask = 0xFFFF0000u;      // quantised words: 16-bit tags
-constexpr int kGuPairs = 16;                  // gate/up pairs per workgroup (half a block)
+constexpr int kGuPairs = 32;                  // gate/up pairs per workgroup (one Q8_0 block)
 
 // Small area offsets (bytes from kSmall).
 constexpr int kPOff = 0;                            // probabilities [kSPositions]
@@ -348,15 +348,20 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   // group (fewer sessions a workgroup: less of the exchanged vectors to read,
   // more weight rows, which are requested before the wait).
   constexpr int kOGroups = 4, kOSessions = 16 / kOGroups;
-  constexpr int R1 = NQKV / kSG, R2 = W * kOGroups / kSG, NGU = FF / kGuPairs;
+  // q/k/v: kQGroups groups of sessions likewise; gate/up: kGuGroups groups,
+  // kGuPairs pairs (one Q8_0 block of the ffn vector) a workgroup.
+  constexpr int kQGroups = 4, kQSessions = 16 / kQGroups, kGuGroups = 2, kGuSessions = 16 / kGuGroups;
+  constexpr int R1 = NQKV * kQGroups / kSG, R2 = W * kOGroups / kSG, NGU = FF / kGuPairs * kGuGroups;
   static_assert(NQKV % kSG == 0 && W % kSG == 0 && FF % 32 == 0 && NGU <= kSG && NGU % 2 == 0, "shape");
   using QkvSlice = Slice<W, R1>;
   using OSlice = Slice<QW, R2>;
   using GuSlice = Slice<W, 2 * kGuPairs>;
   using DownSlice = Slice<FF, R2>;
-  static_assert(QkvSlice::stage_bytes(16) + (size_t)R1 * 16 * QkvSlice::TB * 4 <= (size_t)(kSmall - kVArea), "q/k/v area");
+  static_assert(QkvSlice::stage_bytes(kQSessions) + (size_t)R1 * kQSessions * QkvSlice::TB * 4 <= (size_t)(kSmall - kVArea),
+                "q/k/v area");
   static_assert(OSlice::stage_bytes(kOSessions) + (size_t)R2 * kOSessions * OSlice::TB * 4 <= (size_t)kSmall, "o area");
-  static_assert(GuSlice::stage_bytes(16) + (size_t)2 * kGuPairs * 16 * GuSlice::TB * 4 + kGuPairs * 16 * 4 <=
+  static_assert(GuSlice::stage_bytes(kGuSessions) + (size_t)2 * kGuPairs * kGuSessions * GuSlice::TB * 4 +
+                    kGuPairs * kGuSessions * 4 <=
                     (size_t)kSmall, "gate/up area");
   static_assert(DownSlice::stage_bytes(kOSessions) + (size_t)R2 * kOSessions * DownSlice::TB * 4 <= (size_t)kSmall,
                 "down area");
@@ -388,7 +393,7 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   // past the gate/up workgroups (their ffn norm does not delay a gate/up
   // share), one XCD per session row mod 8. Attention unit w is (session
   // w / H, query head w % H).
-  static_assert(FF / kGuPairs <= 192, "norm workgroups hold no gate/up share");
+  static_assert(NGU <= 192, "norm workgroups hold no gate/up share");
   const int nr = w - 192, ns = (nr >= 0 && (nr & 15) + 16 * ((nr & 15) & 3) == nr && (nr & 15) < S) ? (nr & 15) : -1;
   const int us = w / H, uh = w % H, kh = uh / G;
   const bool unit = us < S;
@@ -413,6 +418,10 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   // (group w % kOGroups). Their residual: lane t < R2 Sg holds (row
   // R2 (w / kOGroups) + t / Sg, session f0 + t % Sg).
   const int f0 = kOSessions * (w % kOGroups), Sg = max(0, min(kOSessions, S - f0)), orow0 = R2 * (w / kOGroups);
+  // q/k/v share: rows qrow0 .. of sessions qf0 .. qf0 + Sq - 1; gate/up
+  // share: pairs gp0 .. of sessions gf0 .. gf0 + Sgu - 1.
+  const int qf0 = kQSessions * (w % kQGroups), Sq = max(0, min(kQSessions, S - qf0)), qrow0 = R1 * (w / kQGroups);
+  const int gf0 = kGuSessions * (w % kGuGroups), Sgu = max(0, min(kGuSessions, S - gf0)), gp0 = kGuPairs * (w / kGuGroups);
   float xres = 0.0f, ares = 0.0f;
   const int ri = tid / max(Sg, 1), rf = f0 + tid - ri * max(Sg, 1), rrow = orow0 + ri;
   const bool rlane = tid < R2 * Sg;
@@ -453,7 +462,7 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
     // row is gathered (its polls would wait behind the loads), so that its
     // products do not start later than the others'.
     QkvSlice qsl;
-    auto qkv_weights = [&]() __attribute__((always_inline)) { qsl.load(lw.wqkv, lw.sqkv, [&](int i) { return R1 * w + i; }); };
+    auto qkv_weights = [&]() __attribute__((always_inline)) { qsl.load(lw.wqkv, lw.sqkv, [&](int i) { return qrow0 + i; }); };
     if (ns < 0) qkv_weights();
 
     // ---- attention norm of session row ns (norm workgroups)
@@ -478,15 +487,15 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
       if (unit) kv_loads();
     }
 
-    // ---- q/k/v rows R1 w .. of every session
-    {
-      if (!gather_rows<W / 4>(txq, qstage, S, gen(l, 1), a.error, ok_s)) return;
-      float* terms = reinterpret_cast<float*>(lds + kVArea + QkvSlice::stage_bytes(S));
-      qsl.products(qstage, S, terms);
+    // ---- q/k/v rows qrow0 .. of sessions qf0 ..
+    if (Sq > 0) {
+      if (!gather_rows<W / 4>(txq + (size_t)qf0 * (W / 4), qstage, Sq, gen(l, 1), a.error, ok_s)) return;
+      float* terms = reinterpret_cast<float*>(lds + kVArea + QkvSlice::stage_bytes(Sq));
+      qsl.products(qstage, Sq, terms);
       lds_barrier();
-      for (int t = tid; t < R1 * S; t += kST) {
-        const int i = t / S, f = t - i * S;
-        put_word(tqkv + (size_t)f * NQKV + R1 * w + i, gen(l, 2), f2u(QkvSlice::row_sum(terms, i, f, S)));
+      for (int t = tid; t < R1 * Sq; t += kST) {
+        const int i = t / Sq, f = t - i * Sq;
+        put_word(tqkv + (size_t)(qf0 + f) * NQKV + qrow0 + i, gen(l, 2), f2u(QkvSlice::row_sum(terms, i, f, Sq)));
       }
     }
 
@@ -669,12 +678,12 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
       lds_barrier();
     }
 
-    // ---- gate/up pairs kGuPairs w ..: SwiGLU, then Q8_0 of the half block
-    if (w < NGU) {
-      const int p0 = kGuPairs * w;
+    // ---- gate/up pairs gp0 .. (one Q8_0 block of the ffn vector) of
+    // sessions gf0 ..: SwiGLU, then the block's Q8_0 words
+    if (w < NGU && Sgu > 0) {
       GuSlice sl;
       sl.load(lw.wgu, lw.sgu, [&](int i) {
-        const int p = p0 + (i < kGuPairs ? i : i - kGuPairs), kind = i < kGuPairs ? 0 : 1;
+        const int p = gp0 + (i < kGuPairs ? i : i - kGuPairs), kind = i < kGuPairs ? 0 : 1;
         if (a.gu_map) return a.gu_map[2 * p + kind];
         // Tiles of `base` (the first `extra` of them base + 1) gate rows,
         // then the same count of up rows.
@@ -690,53 +699,26 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
         return 2 * r0 + kind * count + (p - r0);
       });
       u64* stage = reinterpret_cast<u64*>(lds);
-      if (!gather_rows<W / 4>(taq, stage, S, gen(l, 5), a.error, ok_s)) return;
-      float* terms = reinterpret_cast<float*>(lds + GuSlice::stage_bytes(S));
-      sl.products(stage, S, terms);
+      if (!gather_rows<W / 4>(taq + (size_t)gf0 * (W / 4), stage, Sgu, gen(l, 5), a.error, ok_s)) return;
+      float* terms = reinterpret_cast<float*>(lds + GuSlice::stage_bytes(Sgu));
+      sl.products(stage, Sgu, terms);
       lds_barrier();
-      float* h_s = terms + (size_t)2 * kGuPairs * S * GuSlice::TB;  // [S][kGuPairs]
-      for (int t = tid; t < kGuPairs * S; t += kST) {
-        const int i = t / S, f = t - i * S;
+      float* h_s = terms + (size_t)2 * kGuPairs * Sgu * GuSlice::TB;  // [Sgu][kGuPairs]
+      for (int t = tid; t < kGuPairs * Sgu; t += kST) {
+        const int i = t / Sgu, f = t - i * Sgu;
         // SwiGLU (Elementwise.cs:167-196).
-        const float g = GuSlice::row_sum(terms, i, f, S), u = GuSlice::row_sum(terms, kGuPairs + i, f, S);
+        const float g = GuSlice::row_sum(terms, i, f, Sgu), u = GuSlice::row_sum(terms, kGuPairs + i, f, Sgu);
         h_s[f * kGuPairs + i] = fmul(fdiv(g, fadd(1.0f, exp_ref(-g))), u);
       }
       lds_barrier();
-      if (wave == 0) {
-        // Half-block maxima of the absolute bit patterns, one session a lane,
-        // swapped with the workgroup holding the block's other half.
-        uint32_t mine = 0u;
-        if (lane < S) {
-#pragma unroll
-          for (int i = 0; i < kGuPairs; ++i) {
-            const uint32_t t = f2u(h_s[lane * kGuPairs + i]) & 0x7fffffffu;
-            mine = t > mine ? t : mine;
-          }
-        }
-        if (lane < 16) put_word(a.tmax + (size_t)w * 16 + lane, gen(l, 6), mine);
-        const bool ok = gather16(a.tmax + (size_t)(w ^ 1) * 16, part_s, gen(l, 6), a.error);
-        if (ok) {
-          const uint32_t other = lane < 16 ? (uint32_t)part_s[lane] : 0u;
-          const uint32_t mx = other > mine ? other : mine;
-          float inv;
-          const float d = block_scale(mx, &inv);
-          // Lane t < 4 S quantises values 4 j .. 4 j + 3 of session t / 4.
-          const int f = lane >> 2, j = lane & 3;
-          const float df = __shfl(d, f), invf = __shfl(inv, f);
-          if (f < S) {
-            const float* hv = h_s + f * kGuPairs + 4 * j;
-            const uint32_t codes = (uint32_t)(uint8_t)quantize_value(hv[0], invf) |
-                                   ((uint32_t)(uint8_t)quantize_value(hv[1], invf) << 8) |
-                                   ((uint32_t)(uint8_t)quantize_value(hv[2], invf) << 16) |
-                                   ((uint32_t)(uint8_t)quantize_value(hv[3], invf) << 24);
-            const int k = 4 * (w & 1) + j;
-            put_qword(thq + (size_t)f * (FF / 4) + k * (FF / 32) + (w >> 1), gen(l, 7), qside(k, df), codes);
-          }
-        }
-        if (lane == 0) ok_s[0] = ok ? 1 : 0;
+      // The block of each session: eight lanes, four values each (quantize4).
+      if (tid < 8 * Sgu) {
+        const int f = tid >> 3, j = tid & 7;
+        const float4 v4 = *reinterpret_cast<const float4*>(h_s + f * kGuPairs + 4 * j);
+        float d;
+        const int packed = quantize4(v4.x, v4.y, v4.z, v4.w, &d);
+        put_qword(thq + (size_t)(gf0 + f) * (FF / 4) + j * (FF / 32) + gp0 / 32, gen(l, 7), qside(j, d), (uint32_t)packed);
       }
-      lds_barrier();
-      if (!ok_s[0]) return;
       lds_barrier();
     }
 
