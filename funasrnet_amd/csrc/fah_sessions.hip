@@ -350,7 +350,7 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   constexpr int kOGroups = 4, kOSessions = 16 / kOGroups;
   // q/k/v: kQGroups groups of sessions likewise; gate/up: kGuGroups groups,
   // kGuPairs pairs (one Q8_0 block of the ffn vector) a workgroup.
-  constexpr int kQGroups = 4, kQSessions = 16 / kQGroups, kGuGroups = 2, kGuSessions = 16 / kGuGroups;
+  constexpr int kQGroups = 2, kQSessions = 16 / kQGroups, kGuGroups = 2, kGuSessions = 16 / kGuGroups;
   constexpr int R1 = NQKV * kQGroups / kSG, R2 = W * kOGroups / kSG, NGU = FF / kGuPairs * kGuGroups;
   static_assert(NQKV % kSG == 0 && W % kSG == 0 && FF % 32 == 0 && NGU <= kSG && NGU % 2 == 0, "shape");
   using QkvSlice = Slice<W, R1>;
