@@ -396,10 +396,13 @@ def sessions_decode(backend, weights, count: int = 16, steps: int = 128, prefix:
         step_bytes = cfg.weight_bytes_per_token() + kv
         gbs = step_bytes / (ms * 1e-3) / 1e9
         distinct = len({tuple(t) for t in toks.tolist()})
+        # The weight bytes one-token-at-a-time decoders would stream for the
+        # same tokens, per second: count x the weights per step.
+        effective = count * cfg.weight_bytes_per_token() / (ms * 1e-3) / 1e9
         result = {"sessions": count, "steps": steps, "ms_per_step": round(ms, 4),
                   "tok_s": round(count * 1000.0 / ms, 1), "bytes_per_step": int(step_bytes),
                   "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                  "distinct_token_rows": distinct}
+                  "effective_weight_gbs": round(effective, 1), "distinct_token_rows": distinct}
     finally:
         for d in sessions[1:]:
             d.close()
@@ -654,7 +657,7 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the GEMV sweep, prefill, long-cache and sessions measurements")
     ap.add_argument("--extra-only", choices=["gemv_sweep", "prefill", "long_kv", "sessions", "float_gemv_sweep",
-                                             "encoder_float", "step_batcher"],
+                                             "encoder_float", "step_batcher", "sessions_by_count"],
                     help="run one of the extra measurements alone and print its JSON (for profilers)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -676,7 +679,9 @@ def main() -> int:
         run = {"gemv_sweep": lambda: gemv_sweep(backend), "prefill": lambda: prefill_ttft(backend, weights),
                "long_kv": lambda: long_kv(backend, weights), "sessions": lambda: sessions_decode(backend, weights),
                "float_gemv_sweep": lambda: float_gemv_sweep(backend), "encoder_float": lambda: encoder_float(backend),
-               "step_batcher": lambda: step_batcher_decode(backend, weights)}
+               "step_batcher": lambda: step_batcher_decode(backend, weights),
+               "sessions_by_count": lambda: {str(n): sessions_decode(backend, weights, count=n, steps=64)
+                                             for n in (4, 8)}}
         print(json.dumps({args.extra_only: run[args.extra_only]()}), flush=True)
         backend.close()
         return 0
@@ -722,6 +727,8 @@ def main() -> int:
         extra["sessions"] = sessions_decode(backend, weights,
                                             check=None if args.no_cpu else min(16, os.cpu_count() or 1))
         oracle_tokens = extra["sessions"].get("oracle_check", {}).pop("_tokens", None)
+        extra["sessions"]["by_count"] = {str(n): sessions_decode(backend, weights, count=n, steps=64)
+                                         for n in (4, 8)}
         extra["step_batcher"] = step_batcher_decode(backend, weights, expected=oracle_tokens)
         if not args.no_cpu:
             extra["cpu_baselines"] = cpu_extra_baselines(weights, min(16, os.cpu_count() or 1))
