@@ -381,89 +381,6 @@ __device__ __forceinline__ bool gather1(const u64* src, int count, uint32_t gen,
 __device__ __forceinline__ float tag_value(const u64* tag, int i) { return u2f((uint32_t)tag[i]); }
 
 
-// Part of the time-ordered value sum of channel c = 2 * lane + HI: acc =
-// acc + p[t] * v[t][c] in order (the reference's value loop) over
-// positions [t0, t0 + count), whose V rows sit at 256 B per position from
-// `base`. The dword at byte 4 * lane of a V row holds channels 2 * lane (low
-// half) and 2 * lane + 1 (high half). Blocks of 16 positions: 8 paired
-// reads and 4 probability reads, the next block's issued before the
-// current block is added.
-template <bool HI>
-__device__ __forceinline__ void value_region(const char* base, const float* p, int t0, int count, float& acc) {
-  const int lane = threadIdx.x & (kWave - 1);
-  auto half = [](uint32_t d) { return __builtin_bit_cast(_Float16, (uint16_t)(HI ? d >> 16 : d)); };
-  // Drain earlier scalar loads: with none pending, the waits inside the
-  // block loop can count LDS reads instead of draining them all.
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  {
-    const char* vr = base + 4 * lane;
-    // The probabilities through a per-lane pointer, so that their block loads
-    // take immediate offsets from one VGPR and issue with the value loads.
-    using lds_float = __attribute__((address_space(3))) const float;
-    lds_float* pl = (lds_float*)(p + t0);
-    asm volatile("" : "+v"(pl));
-    auto one = [&](int i) { acc = fadd(acc, mulh(p[t0 + i], half(*reinterpret_cast<const uint32_t*>(vr + (size_t)i * 256)))); };
-    int i = 0;
-    for (; i < count && ((t0 + i) & 3) != 0; ++i) one(i);
-    auto fetch = [&](uint32_t* v, float4* pq, int i0) {
-#pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = *reinterpret_cast<const uint32_t*>(vr + (size_t)(i0 + k) * 256);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        typedef float f4 __attribute__((ext_vector_type(4)));
-        using lds_f4 = __attribute__((address_space(3))) const f4;
-        const f4 v = *reinterpret_cast<lds_f4*>(pl + i0 + 4 * k);
-        pq[k] = make_float4(v.x, v.y, v.z, v.w);
-      }
-    };
-    // The sixteen products first, then the in-order adds: each add then
-    // finds its product long finished instead of waiting for the mixed
-    // multiply issued just before it.
-    auto add16 = [&](const uint32_t* v, const float4* pq) {
-      float m[16];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        m[4 * k] = mulh(pq[k].x, half(v[4 * k]));
-        m[4 * k + 1] = mulh(pq[k].y, half(v[4 * k + 1]));
-        m[4 * k + 2] = mulh(pq[k].z, half(v[4 * k + 2]));
-        m[4 * k + 3] = mulh(pq[k].w, half(v[4 * k + 3]));
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int k = 0; k < 16; ++k) acc = fadd(acc, m[k]);
-    };
-    if (i + 16 <= count) {
-      uint32_t va[16], vb[16];
-      float4 pa[4], pb[4];
-      // sched_barrier keeps each block's loads ahead of the previous block's
-      // adds (the scheduler would otherwise sink them next to their use).
-      fetch(va, pa, i);
-      for (; i + 48 <= count; i += 32) {
-        fetch(vb, pb, i + 16);
-        __builtin_amdgcn_sched_barrier(0);
-        add16(va, pa);
-        __builtin_amdgcn_sched_barrier(0);
-        fetch(va, pa, i + 32);
-        __builtin_amdgcn_sched_barrier(0);
-        add16(vb, pb);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // va holds [i, i + 16); i + 16 <= count here.
-      if (i + 32 <= count) {
-        fetch(vb, pb, i + 16);
-        __builtin_amdgcn_sched_barrier(0);
-        add16(va, pa);
-        add16(vb, pb);
-        i += 32;
-      } else {
-        add16(va, pa);
-        i += 16;
-      }
-    }
-    for (; i < count; ++i) one(i);
-  }
-}
-
 // The whole value sum of channel c = 2 * lane + HI over positions [0, pos]:
 // the V rows of positions [0, nlds) staged at 256 B per position in vs, later
 // ones read from vglob (this layer and head), this position's value in

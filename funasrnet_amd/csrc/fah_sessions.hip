@@ -206,6 +206,45 @@ __device__ __forceinline__ bool all_waves(bool ok, int* ok_s) {
   return r;
 }
 
+// The score of one position whose K row (16 pieces of 8 F16 channels) is in
+// registers: the eight channel-strided accumulators and their pairwise tree
+// (AttentionAvx.cs:74-118), divided by the divisor. q is read from LDS in
+// blocks of 16 channels, the next block's reads issued before the current
+// block's products, so that a wave waits for one LDS round trip per score
+// rather than one per 8 channels.
+__device__ __forceinline__ float score_regs(const uint4* k, const float* q, float divisor) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  using lds_f4 = __attribute__((address_space(3))) const f4;
+  // No scalar loads pending: the block waits can count LDS reads alone.
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  lds_f4* ql = (lds_f4*)q;
+  asm volatile("" : "+v"(ql));
+  float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  f4 qa[4], qb[4];
+  auto fetch = [&](f4* d, int blk) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d[j] = ql[4 * blk + j];
+  };
+  auto use = [&](const f4* d, int blk) {
+    score8(acc, k[2 * blk], make_float4(d[0].x, d[0].y, d[0].z, d[0].w), make_float4(d[1].x, d[1].y, d[1].z, d[1].w));
+    score8(acc, k[2 * blk + 1], make_float4(d[2].x, d[2].y, d[2].z, d[2].w), make_float4(d[3].x, d[3].y, d[3].z, d[3].w));
+  };
+  fetch(qa, 0);
+#pragma unroll
+  for (int blk = 0; blk < 8; blk += 2) {
+    fetch(qb, blk + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    use(qa, blk);
+    __builtin_amdgcn_sched_barrier(0);
+    if (blk + 2 < 8) fetch(qa, blk + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    use(qb, blk + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const float sc = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
+  return fdiv(sc, divisor);
+}
+
 // A workgroup's rows of one projection (K inputs, SLOTS storage rows) for
 // every session, as q8_gemm_few_kernel forms them: lane = (row step, block)
 // keeps its rows' 32-byte weight blocks and block scales in registers; for
@@ -537,16 +576,16 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
         }
       }
       lds_barrier();
-      // Scores: one position per thread, eight channel-strided accumulators
-      // and their pairwise tree (AttentionAvx.cs:74-118).
-      if (tid < nv) {
-        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+      // Scores: one position per thread, its K row in registers (thread nv,
+      // this position when it is below kST, copies its row from LDS), eight
+      // channel-strided accumulators and their pairwise tree
+      // (AttentionAvx.cs:74-118); positions from kST on read their rows here.
+      if (tid == nv) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) score8(acc, k0[i], q_s + 8 * i);
-        const float sc = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
-        p_s[tid] = fdiv(sc, a.divisor);
+        for (int i = 0; i < 16; ++i) k0[i] = reinterpret_cast<const uint4*>(kcur_s)[i];
       }
-      for (int s = tid < nv ? tid + kST : tid; s < n; s += kST) {
+      if (tid < n) p_s[tid] = score_regs(k0, q_s, a.divisor);
+      for (int s = tid + kST; s < n; s += kST) {
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
         if (s < nv) {
           const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)s * HS);
@@ -621,21 +660,16 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
       for (int s = tid; s < n; s += kST) p_s[s] = fmul(p_s[s], inverse);
       __builtin_amdgcn_s_waitcnt(0);  // this wave's V rows are in LDS
       lds_barrier();
-      // Time-ordered value sums, one channel per thread (AttentionAvx.cs:120-171).
-      if (tid < HS) {
-        const _Float16* v = reinterpret_cast<const _Float16*>(lds) + tid;
+      // Time-ordered value sums (AttentionAvx.cs:120-171): channel 2 lane + w
+      // on wave w < 2, in blocks of 16 positions, the next block's LDS reads
+      // issued before the current block is added.
+      if (wave < 2) {
+        const int c = 2 * lane + wave;
         float acc = 0.0f;
-        int s = 0;
-        for (; s + 16 <= nv; s += 16) {
-          _Float16 x[16];
-#pragma unroll
-          for (int k = 0; k < 16; ++k) x[k] = v[(s + k) * HS];
-#pragma unroll
-          for (int k = 0; k < 16; ++k) acc = fadd(acc, mulh(p_s[s + k], x[k]));
-        }
-        for (; s < nv; ++s) acc = fadd(acc, mulh(p_s[s], v[s * HS]));
-        acc = fadd(acc, mulh(p_s[pos], vcur_s[tid]));
-        q_s[tid] = acc;
+        if (wave == 0) value_region<false>(lds, p_s, 0, nv, acc);
+        else value_region<true>(lds, p_s, 0, nv, acc);
+        acc = fadd(acc, mulh(p_s[pos], vcur_s[c]));
+        q_s[c] = acc;
       }
       lds_barrier();
       if (tid < HS / 4) {
