@@ -144,22 +144,21 @@ __device__ bool gather_words(const u64* src, u64* tag, int first, int total, uin
   }
 }
 
-// One wave: three 128-word chunks at a, b, c into tag[0, 384), polled whole
-// in rounds of three reads, two rounds in flight.
-__device__ bool gather3(const u64* a, const u64* b, const u64* c, u64* tag, uint32_t gen, unsigned* error) {
+// One wave: two 128-word chunks at a, b into tag[0, 256), polled whole in
+// rounds of two reads, two rounds in flight.
+__device__ bool gather2(const u64* a, const u64* b, u64* tag, uint32_t gen, unsigned* error) {
   const int lane = threadIdx.x & (kWave - 1);
   auto round = [&] {
     __builtin_amdgcn_global_load_lds(a + 2 * lane, (lds_ptr)(tag), 16, 0, 16);
     __builtin_amdgcn_global_load_lds(b + 2 * lane, (lds_ptr)(tag + 128), 16, 0, 16);
-    __builtin_amdgcn_global_load_lds(c + 2 * lane, (lds_ptr)(tag + 256), 16, 0, 16);
   };
   round();
   for (long spin = 0;; ++spin) {
     round();
-    __builtin_amdgcn_s_waitcnt(3 | (7 << 4) | (15 << 8));  // vmcnt <= 3: the older round is in
+    __builtin_amdgcn_s_waitcnt(2 | (7 << 4) | (15 << 8));  // vmcnt <= 2: the older round is in
     bool all = true;
 #pragma unroll
-    for (int k = 0; k < 3; ++k) all = all && __all(current(*reinterpret_cast<const uint4*>(tag + 128 * k + 2 * lane), gen, ~0u));
+    for (int k = 0; k < 2; ++k) all = all && __all(current(*reinterpret_cast<const uint4*>(tag + 128 * k + 2 * lane), gen, ~0u));
     if (all) {
       __builtin_amdgcn_s_waitcnt(0);  // the newer round writes the same current words
       return true;
@@ -542,11 +541,11 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
     if (unit) {
       bool ok = true;
       const u64* base = tqkv + (size_t)us * NQKV;
-      if (wave == 0) ok = gather3(base + uh * HS, base + QW + kh * HS, base + QW + KVW + kh * HS, qkv_tag, gen(l, 2), a.error);
+      if (wave == 0) ok = gather2(base + uh * HS, base + QW + kh * HS, qkv_tag, gen(l, 2), a.error);
       if (!all_waves(ok, ok_s)) return;
-      // QK-norm and RoPE of q (threads 0-127) and k (128-255), v rounded to
-      // F16 (QwenDecoder.cs:186-203, Rope.cs:14-55); the first query head of
-      // the pair writes the K/V row.
+      // QK-norm and RoPE of q (threads 0-127) and k (128-255)
+      // (QwenDecoder.cs:186-203, Rope.cs:14-55); the first query head of the
+      // pair writes the K row. The v row is gathered during the value sums.
       {
         const int part = tid >> 7, c = tid & 127, half = HS / 2;
         const float v = u2f((uint32_t)qkv_tag[128 * part + c]);
@@ -566,9 +565,6 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
         else r = fadd(fmul(y[c - half], sn), fmul(y[c], cs));
         if (part == 0) {
           q_s[c] = r;
-          const _Float16 v16 = to_half(u2f((uint32_t)qkv_tag[256 + c]));
-          vcur_s[c] = v16;
-          if (uh % G == 0) const_cast<_Float16*>(vc)[(size_t)pos * HS + c] = v16;
         } else {
           const _Float16 k16 = to_half(r);
           kcur_s[c] = k16;
@@ -662,14 +658,31 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
       lds_barrier();
       // Time-ordered value sums (AttentionAvx.cs:120-171): channel 2 lane + w
       // on wave w < 2, in blocks of 16 positions, the next block's LDS reads
-      // issued before the current block is added.
+      // issued before the current block is added. Meanwhile wave 2 gathers
+      // this position's v row (rounded to F16; QwenDecoder.cs:195-203), which
+      // the first query head of the pair writes to the cache, and which
+      // gives the last term.
+      float vacc = 0.0f;
+      bool vok = true;
+      if (wave < 2) {
+        if (wave == 0) value_region<false>(lds, p_s, 0, nv, vacc);
+        else value_region<true>(lds, p_s, 0, nv, vacc);
+      } else if (wave == 2) {
+        vok = gather_words(tqkv + (size_t)us * NQKV + QW + KVW + kh * HS, qkv_tag + 256, 0, 1, gen(l, 2), ~0u, a.error);
+        if (vok) {
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const int c = lane + 64 * k;
+            const _Float16 v16 = to_half(u2f((uint32_t)qkv_tag[256 + c]));
+            vcur_s[c] = v16;
+            if (uh % G == 0) const_cast<_Float16*>(vc)[(size_t)pos * HS + c] = v16;
+          }
+        }
+      }
+      if (!all_waves(vok, ok_s)) return;
       if (wave < 2) {
         const int c = 2 * lane + wave;
-        float acc = 0.0f;
-        if (wave == 0) value_region<false>(lds, p_s, 0, nv, acc);
-        else value_region<true>(lds, p_s, 0, nv, acc);
-        acc = fadd(acc, mulh(p_s[pos], vcur_s[c]));
-        q_s[c] = acc;
+        q_s[c] = fadd(vacc, mulh(p_s[pos], vcur_s[c]));
       }
       lds_barrier();
       if (tid < HS / 4) {
