@@ -478,8 +478,8 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
     u64* const thq = a.thq + (size_t)l * LH;
     // ---- attention unit: this layer's earlier K rows (one a thread, in
     // registers) and V rows (to LDS), requested at the start of the layer --
-    // by a norm workgroup once its row is published, so that its gather does
-    // not wait behind them -- and used after q/k/v.
+    // by a norm workgroup once it has gathered its q/k/v input, so that
+    // neither of its gathers waits behind them -- and used after q/k/v.
     const _Float16* kc = unit ? kbase + ((size_t)l * KVH + kh) * (size_t)cap * HS : nullptr;
     const _Float16* vc = unit ? vbase + ((size_t)l * KVH + kh) * (size_t)cap * HS : nullptr;
     uint4 k0[16];
@@ -522,12 +522,13 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
         norm_row<W>([&](int k) { return u2f((uint32_t)qstage[k]); }, lw.attn_norm, a.eps, red_s, emit);
       }
       lds_barrier();
-      if (unit) kv_loads();
+      if (unit && Sq == 0) kv_loads();
     }
 
     // ---- q/k/v rows qrow0 .. of sessions qf0 ..
     if (Sq > 0) {
       if (!gather_rows<W / 4>(txq + (size_t)qf0 * (W / 4), qstage, Sq, gen(l, 1), a.error, ok_s)) return;
+      if (unit && ns >= 0) kv_loads();
       float* terms = reinterpret_cast<float*>(lds + kVArea + QkvSlice::stage_bytes(Sq));
       qsl.products(qstage, Sq, terms);
       lds_barrier();
