@@ -70,6 +70,20 @@ constexpr int kPartOff = kOkOff + 16;               // partner maxima words [16]
 static_assert(kPartOff + 128 <= 8 * 1024, "small area");
 static_assert(kTagOff % 16 == 0 && kPartOff % 16 == 0, "16-byte LDS destinations");
 
+// A load through a global-address-space pointer: unlike a generic (flat)
+// load it cannot alias LDS, so it need not wait for the direct-to-LDS loads
+// in flight.
+__device__ __forceinline__ float gload(const float* p) { return *(const __attribute__((address_space(1))) float*)p; }
+__device__ __forceinline__ uint4 gload(const uint4* p) {
+  typedef unsigned int v4 __attribute__((ext_vector_type(4)));
+  const v4 v = *(const __attribute__((address_space(1))) v4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 gload(const float4* p) {
+  typedef float v4 __attribute__((ext_vector_type(4)));
+  const v4 v = *(const __attribute__((address_space(1))) v4*)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ unsigned err_load(const unsigned* e) {
   return __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -347,9 +361,25 @@ __device__ __forceinline__ bool gather_rows(const u64* src, u64* stage, int S, u
 // the reference order where the mean is unsettled (rms_inverse). read(k)
 // returns value k. Each thread's 4 codes and (every 8th thread) the block
 // scale go to emit(e, codes, d).
+template <int W>
+struct NormWeights {
+  static constexpr int NC = (W + 1023) / 1024;
+  float4 v[NC];
+  // Thread t's weights 4t + 1024c .. + 3, loaded ahead of the row's gather
+  // (a wave's loads complete in order: a load issued after the gather's
+  // weight loads would wait for them).
+  __device__ __forceinline__ void load(const float* norm_w) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int e = c * 1024 + 4 * (int)threadIdx.x;
+      v[c] = e < W ? gload(reinterpret_cast<const float4*>(norm_w + e)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  }
+};
+
 template <int W, class Read, class Emit>
-__device__ __forceinline__ void norm_row(Read read, const float* norm_w, float eps, double* red_s, Emit emit) {
-  constexpr int NC = (W + 1023) / 1024;
+__device__ __forceinline__ void norm_row(Read read, const NormWeights<W>& nwt, float eps, double* red_s, Emit emit) {
+  constexpr int NC = NormWeights<W>::NC;
   const int tid = threadIdx.x;
   float4 v[NC];
 #pragma unroll
@@ -368,7 +398,7 @@ __device__ __forceinline__ void norm_row(Read read, const float* norm_w, float e
   for (int c = 0; c < NC; ++c) {
     const int e = c * 1024 + 4 * tid;
     if (e < W) {
-      const float4 w = *reinterpret_cast<const float4*>(norm_w + e);
+      const float4 w = nwt.v[c];
       const float x0 = fmul(fmul(v[c].x, inverse), w.x), x1 = fmul(fmul(v[c].y, inverse), w.y);
       const float x2 = fmul(fmul(v[c].z, inverse), w.z), x3 = fmul(fmul(v[c].w, inverse), w.w);
       float d;
@@ -491,9 +521,18 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
       if (tid < nv) {
         const uint4* row = reinterpret_cast<const uint4*>(kc + (size_t)tid * HS);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) k0[i] = row[i];
+        for (int i = 0; i < 16; ++i) k0[i] = gload(row + i);
       }
     };
+    // The unit's QK-norm weight and RoPE factors of its channel (thread t:
+    // channel t % 128 of q (t < 128) or k), requested first.
+    float qk_nw = 0.0f, qk_cs = 0.0f, qk_sn = 0.0f;
+    if (unit) {
+      const int c = tid & (HS - 1), half = HS / 2;
+      qk_nw = gload((tid < HS ? lw.q_norm : lw.k_norm) + c);
+      qk_cs = gload(rcos + (size_t)pos * half + (c & (half - 1)));
+      qk_sn = gload(rsin + (size_t)pos * half + (c & (half - 1)));
+    }
     if (unit && ns < 0) kv_loads();
 
     // The q/k/v weight slice: requested now, or by a norm workgroup once its
@@ -506,6 +545,8 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
     // ---- attention norm of session row ns (norm workgroups)
     u64* qstage = reinterpret_cast<u64*>(lds + kVArea);  // q/k/v phase: staging, then terms
     if (ns >= 0) {
+      NormWeights<W> nwt;
+      nwt.load(lw.attn_norm);
       u64* dst = txq + (size_t)ns * (W / 4);
       auto emit = [&](int e, int packed, float d) {
         put_qword(dst + word_major(e / 4, W / 32), gen(l, 1), qside((e / 4) & 7, d), (uint32_t)packed);
@@ -513,13 +554,13 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
       if (l == 0) {
         qkv_weights();
         const float* row = a.x_in + (size_t)ns * W;
-        norm_row<W>([&](int k) { return row[k]; }, lw.attn_norm, a.eps, red_s, emit);
+        norm_row<W>([&](int k) { return row[k]; }, nwt, a.eps, red_s, emit);
       } else {
         const bool ok = gather_words(a.tx + (size_t)(l - 1) * LX + (size_t)ns * W, qstage, wave * (W / 128) / 4, (wave + 1) * (W / 128) / 4,
                                      gen(l - 1, 8), ~0u, a.error);
         if (!all_waves(ok, ok_s)) return;
         qkv_weights();
-        norm_row<W>([&](int k) { return u2f((uint32_t)qstage[k]); }, lw.attn_norm, a.eps, red_s, emit);
+        norm_row<W>([&](int k) { return u2f((uint32_t)qstage[k]); }, nwt, a.eps, red_s, emit);
       }
       lds_barrier();
       if (unit && Sq == 0) kv_loads();
@@ -550,9 +591,7 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
       {
         const int part = tid >> 7, c = tid & 127, half = HS / 2;
         const float v = u2f((uint32_t)qkv_tag[128 * part + c]);
-        const float nw = (part == 0 ? lw.q_norm : lw.k_norm)[c];
-        const float cs = rcos[(size_t)pos * half + (c & (half - 1))];
-        const float sn = rsin[(size_t)pos * half + (c & (half - 1))];
+        const float nw = qk_nw, cs = qk_cs, sn = qk_sn;
         const double sq = wave_sum_double((double)v * (double)v);
         if (lane == 0) red_s[wave] = sq;
         lds_barrier();
@@ -714,12 +753,14 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
 
     // ---- ffn norm of session row ns
     if (ns >= 0) {
+      NormWeights<W> nwt;
+      nwt.load(lw.ffn_norm);
       u64* stage = reinterpret_cast<u64*>(lds);
       const bool ok = gather_words(ta + (size_t)ns * W, stage, wave * (W / 128) / 4, (wave + 1) * (W / 128) / 4,
                                    gen(l, 4), ~0u, a.error);
       if (!all_waves(ok, ok_s)) return;
       u64* dst = taq + (size_t)ns * (W / 4);
-      norm_row<W>([&](int k) { return u2f((uint32_t)stage[k]); }, lw.ffn_norm, a.eps, red_s,
+      norm_row<W>([&](int k) { return u2f((uint32_t)stage[k]); }, nwt, a.eps, red_s,
                   [&](int e, int packed, float d) {
                     put_qword(dst + word_major(e / 4, W / 32), gen(l, 5), qside((e / 4) & 7, d), (uint32_t)packed);
                   });
@@ -789,13 +830,15 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
 
   // ---- output norm of session row ns, as Q8_0 rows for the lm_head
   if (ns >= 0) {
+    NormWeights<W> nwt;
+    nwt.load(a.output_norm);
     u64* stage = reinterpret_cast<u64*>(lds);
     const bool ok = gather_words(a.tx + (size_t)(L - 1) * LX + (size_t)ns * W, stage, wave * (W / 128) / 4, (wave + 1) * (W / 128) / 4,
                                  gen(L - 1, 8), ~0u, a.error);
     if (!all_waves(ok, ok_s)) return;
     int8_t* xq = a.xq_out + (size_t)ns * W;
     float* xs = a.xs_out + (size_t)ns * (W / 32);
-    norm_row<W>([&](int k) { return u2f((uint32_t)stage[k]); }, a.output_norm, a.eps, red_s, [&](int e, int packed, float d) {
+    norm_row<W>([&](int k) { return u2f((uint32_t)stage[k]); }, nwt, a.eps, red_s, [&](int e, int packed, float d) {
       *reinterpret_cast<int*>(xq + e) = packed;
       if ((tid & 7) == 0) xs[e >> 5] = d;
     });
