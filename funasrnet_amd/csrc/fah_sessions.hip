@@ -293,22 +293,14 @@ struct Slice {
   __device__ __forceinline__ void products(const u64* stage, int S, float* terms) const {
     const int tid = threadIdx.x, lrow = tid / B, b = tid - lrow * B;
     if (lrow >= RS) return;
-    // The next session's block is read while this one is formed.
-    uint2 nx[8];
-    {
-      const uint2* xp = reinterpret_cast<const uint2*>(stage + b);
+    // Two sessions' blocks in flight: the next one is read while this one is
+    // formed, the buffers alternating (no register copies).
+    auto fetch = [&](uint2* u, int f) {
+      const uint2* xp = reinterpret_cast<const uint2*>(stage + (size_t)f * KW + b);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) nx[j] = xp[j * B];
-    }
-    for (int f = 0; f < S; ++f) {
-      uint2 u[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) u[j] = nx[j];
-      if (f + 1 < S) {
-        const uint2* xp = reinterpret_cast<const uint2*>(stage + (size_t)(f + 1) * KW + b);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) nx[j] = xp[j * B];
-      }
+      for (int j = 0; j < 8; ++j) u[j] = xp[j * B];
+    };
+    auto form = [&](const uint2* u, int f) {
       const float xsv = u2f((u[0].y & 0xFFFFu) | ((u[1].y & 0xFFFFu) << 16));
 #pragma unroll
       for (int k = 0; k < P; ++k) {
@@ -328,7 +320,17 @@ struct Slice {
           terms[((size_t)i * S + f) * TB + b] = fmul(fmul((float)dot, ws[k]), xsv);
         }
       }
+    };
+    uint2 ua[8], ub[8];
+    fetch(ua, 0);
+    int f = 0;
+    for (; f + 2 <= S; f += 2) {
+      fetch(ub, f + 1);
+      form(ua, f);
+      if (f + 2 < S) fetch(ua, f + 2);
+      form(ub, f + 1);
     }
+    if (f < S) form(ua, f);
   }
 
   __device__ __forceinline__ static float row_sum(const float* terms, int i, int f, int S) {
