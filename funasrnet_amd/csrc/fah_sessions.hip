@@ -306,17 +306,17 @@ struct Slice {
       for (int k = 0; k < P; ++k) {
         const int i = lrow + RS * k;
         if (i < SLOTS) {
-          // Two independent chains (integer sums: exact in any order).
-          int d0 = 0, d1 = 0;
-          d0 = __builtin_amdgcn_sdot4((int)w0[k].x, (int)u[0].x, d0, false);
-          d1 = __builtin_amdgcn_sdot4((int)w1[k].x, (int)u[4].x, d1, false);
-          d0 = __builtin_amdgcn_sdot4((int)w0[k].y, (int)u[1].x, d0, false);
-          d1 = __builtin_amdgcn_sdot4((int)w1[k].y, (int)u[5].x, d1, false);
-          d0 = __builtin_amdgcn_sdot4((int)w0[k].z, (int)u[2].x, d0, false);
-          d1 = __builtin_amdgcn_sdot4((int)w1[k].z, (int)u[6].x, d1, false);
-          d0 = __builtin_amdgcn_sdot4((int)w0[k].w, (int)u[3].x, d0, false);
-          d1 = __builtin_amdgcn_sdot4((int)w1[k].w, (int)u[7].x, d1, false);
-          const int dot = d0 + d1;
+          // One chain of eight (integer sums: exact in any order; the P
+          // rows' chains interleave).
+          int dot = 0;
+          dot = __builtin_amdgcn_sdot4((int)w0[k].x, (int)u[0].x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w0[k].y, (int)u[1].x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w0[k].z, (int)u[2].x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w0[k].w, (int)u[3].x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w1[k].x, (int)u[4].x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w1[k].y, (int)u[5].x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w1[k].z, (int)u[6].x, dot, false);
+          dot = __builtin_amdgcn_sdot4((int)w1[k].w, (int)u[7].x, dot, false);
           terms[((size_t)i * S + f) * TB + b] = fmul(fmul((float)dot, ws[k]), xsv);
         }
       }
