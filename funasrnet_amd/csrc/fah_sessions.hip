@@ -258,6 +258,80 @@ __device__ __forceinline__ float score_regs(const uint4* k, const float* q, floa
   return fdiv(sc, divisor);
 }
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// One wave's 16-row tile of a projection for up to 16 sessions on the matrix
+// cores, in q8_head_mfma16_kernel's operand layout: lane (r, q) = (lane % 16,
+// lane / 16) keeps weight bytes 8q .. 8q + 7 of every block of tile row r and
+// the row's block scales; per block one v_mfma_i32_16x16x32_i8 forms the
+// exact int32 block dots of the 16 rows with 16 sessions' codes (session r
+// as operand A), and lane (r, q) adds the terms ((float)dot * w_scale) *
+// x_scale of sessions 4q .. 4q + 3 in block order -- the few-frame kernel's
+// arithmetic and order.
+template <int K>
+struct MfmaTile {
+  static constexpr int B = K / 32;
+  static constexpr int APS = 65;  // u64 per block in the packed operands (64 + 1: no bank conflicts)
+  long wv[B];
+  float wsv[B];
+
+  template <class RowOf>
+  __device__ __forceinline__ void load(const int8_t* w, const _Float16* s, RowOf row_of) {
+    const int lane = threadIdx.x & (kWave - 1), r = lane & 15, q = lane >> 4;
+    const int sr = row_of(r);
+    const int8_t* wrow = w + (size_t)sr * K + 8 * q;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      wv[b] = *(const __attribute__((address_space(1))) long*)(wrow + 32 * b);
+      wsv[b] = (float)s[(size_t)sr * B + b];
+    }
+  }
+
+  // All threads: the sessions' gathered words (stage: [S][K / 4], word j of
+  // block b at j B + b) into the packed A operands apack[b][q * 16 + r] and
+  // the session scales xs[b][16] (sessions past S: zero).
+  __device__ __forceinline__ static void pack(const u64* stage, int S, u64* apack, float* xs) {
+    const int tid = threadIdx.x, r = tid >> 4, m = tid & 15;
+    for (int b = m; b < B; b += 16) {
+      uint32_t lo[8];
+      uint32_t s01 = 0;
+      if (r < S) {
+        const u64* src = stage + (size_t)r * (K / 4) + b;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const u64 v = src[(size_t)j * B];
+          lo[j] = (uint32_t)v;
+          if (j == 0) s01 = (uint32_t)(v >> 32) & 0xFFFFu;
+          if (j == 1) s01 |= ((uint32_t)(v >> 32) & 0xFFFFu) << 16;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) lo[j] = 0u;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) apack[(size_t)b * APS + q * 16 + r] = (u64)lo[2 * q] | ((u64)lo[2 * q + 1] << 32);
+      xs[b * 16 + r] = u2f(s01);
+    }
+  }
+
+  // This wave's sums: acc[j] = row r, session 4q + j.
+  __device__ __forceinline__ void sums(const u64* apack, const float* xs, float* acc) const {
+    const int lane = threadIdx.x & (kWave - 1), q = lane >> 4;
+    const v4i zero4 = {0, 0, 0, 0};
+    acc[0] = acc[1] = acc[2] = acc[3] = 0.0f;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const long av = (long)apack[(size_t)b * APS + lane];
+      const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv[b], zero4, 0, 0, 0);
+      const float4 xv = *reinterpret_cast<const float4*>(xs + b * 16 + 4 * q);
+      acc[0] = fadd(acc[0], fmul(fmul((float)d[0], wsv[b]), xv.x));
+      acc[1] = fadd(acc[1], fmul(fmul((float)d[1], wsv[b]), xv.y));
+      acc[2] = fadd(acc[2], fmul(fmul((float)d[2], wsv[b]), xv.z));
+      acc[3] = fadd(acc[3], fmul(fmul((float)d[3], wsv[b]), xv.w));
+    }
+  }
+};
+
 // A workgroup's rows of one projection (K inputs, SLOTS storage rows) for
 // every session, as q8_gemm_few_kernel forms them: lane = (row step, block)
 // keeps its rows' 32-byte weight blocks and block scales in registers; for
@@ -425,12 +499,16 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   static_assert(NQKV % kSG == 0 && W % kSG == 0 && FF % 32 == 0 && NGU <= kSG && NGU % 2 == 0, "shape");
   using QkvSlice = Slice<W, R1>;
   using OSlice = Slice<QW, R2>;
-  using GuSlice = Slice<W, 2 * kGuPairs>;
+  using GuTile = MfmaTile<W>;
+  static_assert(2 * kGuPairs == 64, "four 16-row gate/up tiles, one a wave");
   using DownSlice = Slice<FF, R2>;
   static_assert(QkvSlice::stage_bytes(kQSessions) + (size_t)R1 * kQSessions * QkvSlice::TB * 4 <= (size_t)(kSmall - kVArea),
                 "q/k/v area");
   static_assert(OSlice::stage_bytes(kOSessions) + (size_t)R2 * kOSessions * OSlice::TB * 4 <= (size_t)kSmall, "o area");
-  static_assert(GuSlice::stage_bytes(kGuSessions) + (size_t)2 * kGuPairs * kGuSessions * GuSlice::TB * 4 +
+  // Gate/up LDS: the gathered rows, then from kGuPackOff the packed operands,
+  // session scales, sums and SwiGLU values.
+  constexpr int kGuPackOff = kGuSessions * (W / 4) * 8;
+  static_assert(kGuPackOff + (size_t)GuTile::B * GuTile::APS * 8 + GuTile::B * 16 * 4 + 2 * kGuPairs * 16 * 4 +
                     kGuPairs * kGuSessions * 4 <=
                     (size_t)kSmall, "gate/up area");
   static_assert(DownSlice::stage_bytes(kOSessions) + (size_t)R2 * kOSessions * DownSlice::TB * 4 <= (size_t)kSmall,
@@ -772,8 +850,10 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
     // ---- gate/up pairs gp0 .. (one Q8_0 block of the ffn vector) of
     // sessions gf0 ..: SwiGLU, then the block's Q8_0 words
     if (w < NGU && Sgu > 0) {
-      GuSlice sl;
-      sl.load(lw.wgu, lw.sgu, [&](int i) {
+      // Wave v: slots 16 v .. 16 v + 15 (gate rows of pairs 0-31, then up).
+      GuTile sl;
+      sl.load(lw.wgu, lw.sgu, [&](int r) {
+        const int i = 16 * wave + r;
         const int p = gp0 + (i < kGuPairs ? i : i - kGuPairs), kind = i < kGuPairs ? 0 : 1;
         if (a.gu_map) return a.gu_map[2 * p + kind];
         // Tiles of `base` (the first `extra` of them base + 1) gate rows,
@@ -791,14 +871,23 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
       });
       u64* stage = reinterpret_cast<u64*>(lds);
       if (!gather_rows<W / 4>(taq + (size_t)gf0 * (W / 4), stage, Sgu, gen(l, 5), a.error, ok_s)) return;
-      float* terms = reinterpret_cast<float*>(lds + GuSlice::stage_bytes(Sgu));
-      sl.products(stage, Sgu, terms);
+      u64* apack = reinterpret_cast<u64*>(lds + kGuPackOff);
+      float* xs_s = reinterpret_cast<float*>(lds + kGuPackOff + (size_t)GuTile::B * GuTile::APS * 8);
+      float* sum_s = xs_s + GuTile::B * 16;   // [2 kGuPairs][16]
+      float* h_s = sum_s + 2 * kGuPairs * 16;  // [Sgu][kGuPairs]
+      GuTile::pack(stage, Sgu, apack, xs_s);
       lds_barrier();
-      float* h_s = terms + (size_t)2 * kGuPairs * Sgu * GuSlice::TB;  // [Sgu][kGuPairs]
+      {
+        float acc[4];
+        sl.sums(apack, xs_s, acc);
+        const int r = lane & 15, q = lane >> 4;
+        *reinterpret_cast<float4*>(sum_s + (16 * wave + r) * 16 + 4 * q) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      }
+      lds_barrier();
       for (int t = tid; t < kGuPairs * Sgu; t += kST) {
         const int i = t / Sgu, f = t - i * Sgu;
         // SwiGLU (Elementwise.cs:167-196).
-        const float g = GuSlice::row_sum(terms, i, f, Sgu), u = GuSlice::row_sum(terms, kGuPairs + i, f, Sgu);
+        const float g = sum_s[i * 16 + f], u = sum_s[(kGuPairs + i) * 16 + f];
         h_s[f * kGuPairs + i] = fmul(fdiv(g, fadd(1.0f, exp_ref(-g))), u);
       }
       lds_barrier();
