@@ -314,20 +314,29 @@ struct MfmaTile {
     }
   }
 
-  // This wave's sums: acc[j] = row r, session 4q + j.
+  // This wave's sums: acc[j] = row r, session 4q + j. The next block's dots
+  // are issued before this block's terms are added (and its operand read
+  // before that), so the adds do not wait for the matrix core.
   __device__ __forceinline__ void sums(const u64* apack, const float* xs, float* acc) const {
     const int lane = threadIdx.x & (kWave - 1), q = lane >> 4;
     const v4i zero4 = {0, 0, 0, 0};
     acc[0] = acc[1] = acc[2] = acc[3] = 0.0f;
+    long an = (long)apack[lane];
+    v4i dc = __builtin_amdgcn_mfma_i32_16x16x32_i8(an, wv[0], zero4, 0, 0, 0);
+    if (B > 1) an = (long)apack[(size_t)APS + lane];
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-      const long av = (long)apack[(size_t)b * APS + lane];
-      const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv[b], zero4, 0, 0, 0);
+      v4i dn = dc;
+      if (b + 1 < B) dn = __builtin_amdgcn_mfma_i32_16x16x32_i8(an, wv[b + 1], zero4, 0, 0, 0);
+      if (b + 2 < B) an = (long)apack[(size_t)(b + 2) * APS + lane];
+      __builtin_amdgcn_sched_barrier(0);
       const float4 xv = *reinterpret_cast<const float4*>(xs + b * 16 + 4 * q);
-      acc[0] = fadd(acc[0], fmul(fmul((float)d[0], wsv[b]), xv.x));
-      acc[1] = fadd(acc[1], fmul(fmul((float)d[1], wsv[b]), xv.y));
-      acc[2] = fadd(acc[2], fmul(fmul((float)d[2], wsv[b]), xv.z));
-      acc[3] = fadd(acc[3], fmul(fmul((float)d[3], wsv[b]), xv.w));
+      acc[0] = fadd(acc[0], fmul(fmul((float)dc[0], wsv[b]), xv.x));
+      acc[1] = fadd(acc[1], fmul(fmul((float)dc[1], wsv[b]), xv.y));
+      acc[2] = fadd(acc[2], fmul(fmul((float)dc[2], wsv[b]), xv.z));
+      acc[3] = fadd(acc[3], fmul(fmul((float)dc[3], wsv[b]), xv.w));
+      __builtin_amdgcn_sched_barrier(0);
+      dc = dn;
     }
   }
 };
