@@ -324,13 +324,17 @@ struct MfmaTile {
     long an = (long)apack[lane];
     v4i dc = __builtin_amdgcn_mfma_i32_16x16x32_i8(an, wv[0], zero4, 0, 0, 0);
     if (B > 1) an = (long)apack[(size_t)APS + lane];
+    float4 xn = *reinterpret_cast<const float4*>(xs + 4 * q);
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       v4i dn = dc;
-      if (b + 1 < B) dn = __builtin_amdgcn_mfma_i32_16x16x32_i8(an, wv[b + 1], zero4, 0, 0, 0);
+      const float4 xv = xn;
+      if (b + 1 < B) {
+        dn = __builtin_amdgcn_mfma_i32_16x16x32_i8(an, wv[b + 1], zero4, 0, 0, 0);
+        xn = *reinterpret_cast<const float4*>(xs + (b + 1) * 16 + 4 * q);
+      }
       if (b + 2 < B) an = (long)apack[(size_t)(b + 2) * APS + lane];
       __builtin_amdgcn_sched_barrier(0);
-      const float4 xv = *reinterpret_cast<const float4*>(xs + b * 16 + 4 * q);
       acc[0] = fadd(acc[0], fmul(fmul((float)dc[0], wsv[b]), xv.x));
       acc[1] = fadd(acc[1], fmul(fmul((float)dc[1], wsv[b]), xv.y));
       acc[2] = fadd(acc[2], fmul(fmul((float)dc[2], wsv[b]), xv.z));
