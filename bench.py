@@ -475,11 +475,60 @@ def step_batcher_decode(backend, weights, count: int = 16, steps: int = 128, pre
             t.join()
         wall = max(times) - t0
         batches, rows = batcher.stats()
-        result = {"sessions": count, "steps": steps, "tok_s": round(count * steps / wall, 1),
-                  "ms_per_batch": round(wall * 1e3 / max(batches, 1), 4), "batches": batches,
-                  "mean_batch": round(rows / max(batches, 1), 2), "errors": errors}
+        python = {"tok_s": round(count * steps / wall, 1), "ms_per_batch": round(wall * 1e3 / max(batches, 1), 4),
+                  "batches": batches, "mean_batch": round(rows / max(batches, 1), 2), "errors": errors}
         if expected is not None:
-            result["oracle_check"] = compare_sessions(got, expected)
+            python["oracle_check"] = compare_sessions(got, expected)
+    finally:
+        batcher.close()
+        for d in sessions[1:]:
+            d.close()
+        parent.close()
+    native = step_batcher_native(backend, weights, count, steps, prefix, expected)
+    # The native worker threads are the reference's kind of caller (a pool's
+    # .NET threads); the Python threads' figure includes the interpreter lock.
+    result = {"sessions": count, "steps": steps, "workers": "native threads", **native,
+              "python_threads": python}
+    return result
+
+
+def step_batcher_native(backend, weights, count: int, steps: int, prefix: int, expected=None):
+    """The same sessions and steps as step_batcher_decode, each session's
+    steps issued by a native thread of funasrnet_amd/libfah_bench_workers.so
+    (fah_bench_batcher_threads) through fah_batcher_step."""
+    import ctypes
+    from funasrnet_amd import build as fab
+    from funasrnet_amd.hip import HipDecoder, HipStepBatcher, load
+
+    workers = ctypes.CDLL(fab.BENCH_WORKERS)
+    workers.fah_bench_batcher_threads.restype = ctypes.c_int
+    workers.fah_bench_batcher_threads.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
+                                                  ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int32),
+                                                  ctypes.POINTER(ctypes.c_double)]
+    cfg = weights.config
+    capacity = prefix + steps + 8
+    parent = HipDecoder(backend, weights, capacity=capacity)
+    sessions = [parent] + [parent.session() for _ in range(count - 1)]
+    batcher = HipStepBatcher(parent, max_positions=capacity, window_us=2000)
+    try:
+        for i, d in enumerate(sessions):
+            d.decode(np.random.default_rng(i + 1).standard_normal((prefix, cfg.width)).astype(np.float32), prefix)
+            batcher.join(d)
+        handles = (ctypes.c_void_p * count)(*[ctypes.cast(d.handle, ctypes.c_void_p).value for d in sessions])
+        tokens = np.zeros((count, steps), dtype=np.int32)
+        seconds = ctypes.c_double(0.0)
+        step_fn = ctypes.cast(load().fah_batcher_step, ctypes.c_void_p)
+        rc = workers.fah_bench_batcher_threads(step_fn, ctypes.cast(batcher.handle, ctypes.c_void_p), handles, count, steps,
+                                               tokens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ctypes.byref(seconds))
+        batches, rows = batcher.stats()
+        wall = max(seconds.value, 1e-9)
+        result = {"tok_s": round(count * steps / wall, 1), "ms_per_batch": round(wall * 1e3 / max(batches, 1), 4),
+                  "batches": batches, "mean_batch": round(rows / max(batches, 1), 2),
+                  "errors": [] if rc == 0 else [f"fah_batcher_step returned {rc}"]}
+        if expected is not None:
+            result["oracle_check"] = compare_sessions([list(t) for t in tokens.tolist()], expected)
+        for d in sessions:
+            batcher.leave(d)
         return result
     finally:
         batcher.close()

@@ -15,6 +15,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIBRARY = os.path.join(HERE, "libfunasr_hip.so")
+# Host-only helper of the benchmark: native worker threads that step the
+# batcher (no HIP code; built with the host compiler).
+BENCH_WORKERS = os.path.join(HERE, "libfah_bench_workers.so")
 SOURCES = ["fah_kernels.hip", "fah_persistent.hip", "fah_prefill.hip", "fah_sessions.hip", "fah_float.hip",
            "fah_api.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -45,6 +48,10 @@ def build() -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIBRARY)
+    r = subprocess.run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-pthread", os.path.join(SRC, "bench_workers.cpp"),
+                        "-o", BENCH_WORKERS], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"bench_workers.cpp failed:\n{r.stderr}")
     return LIBRARY
 
 

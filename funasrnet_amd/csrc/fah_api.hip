@@ -7,6 +7,7 @@
 #include "fah_internal.h"
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <condition_variable>
@@ -16,6 +17,7 @@
 #include <mutex>
 #include <optional>
 #include <string>
+#include <thread>
 #include <vector>
 
 namespace {
@@ -172,11 +174,15 @@ struct SessionBatch {
   bool fused = false;
   DeviceBuffer layer_table, exchange, epoch, error;
   fah::SessionStepArgs sargs{};
+  // Pinned read-back of a batcher step: the tokens, then the error word and
+  // the epoch (asynchronous copies, one synchronisation).
+  int32_t* readback = nullptr;
   SessionBatch() = default;
   SessionBatch(const SessionBatch&) = delete;
   SessionBatch& operator=(const SessionBatch&) = delete;
   ~SessionBatch() {
     if (graph) (void)hipGraphExecDestroy(graph);
+    if (readback) (void)hipHostFree(readback);
   }
 };
 
@@ -416,7 +422,9 @@ struct BatchRequest {
   int32_t token = 0;
   int status = FAH_OK;
   std::string error;
-  bool done = false;
+  // Set by the leader after every other field, as its last access: the
+  // requester may then read them without the batcher's lock and return.
+  std::atomic<bool> done{false};
 };
 
 // Cross-context step batcher: greedy steps of sessions of one weight set,
@@ -434,7 +442,8 @@ struct fah_batcher {
   // encoding, prefilling, idle between requests). The collector stops
   // waiting for them until they request a step again.
   std::vector<fah_decoder*> idle;
-  bool running = false;  // a leader is collecting or running a batch
+  std::atomic<bool> running{false};  // a leader is collecting or running a batch (written under m)
+  std::atomic<int64_t> arrivals{0};  // steps requested so far (incremented under m)
   int64_t batches_run = 0, rows_run = 0;
   // The captured step of each batch size (the session table is rewritten
   // before each launch).
@@ -1264,13 +1273,22 @@ void prepare_session_step(const fah_decoder* d0, SessionBatch& b, int count, hip
 // clear the error word, return every session's device position to its
 // host position with an empty history, and throw. The sessions' logits are
 // not valid afterwards (decode again before the next greedy step).
+void recover_session_step_read(SessionBatch& b, fah_decoder* const* sessions, int count, unsigned e, unsigned epoch,
+                               hipStream_t s);
+
 void recover_session_step(SessionBatch& b, fah_decoder* const* sessions, int count, hipStream_t s) {
   if (!b.fused) return;
   unsigned e = 0, epoch = 0;
   check(hipMemcpyAsync(&e, b.error.ptr, 4, hipMemcpyDeviceToHost, s), "D2H error word");
   check(hipMemcpyAsync(&epoch, b.epoch.ptr, 4, hipMemcpyDeviceToHost, s), "D2H epoch");
   check(hipStreamSynchronize(s), "hipStreamSynchronize");
-  if (!e) return;
+  recover_session_step_read(b, sessions, count, e, epoch, s);
+}
+
+// The same with the error word and epoch already read back (e, epoch).
+void recover_session_step_read(SessionBatch& b, fah_decoder* const* sessions, int count, unsigned e, unsigned epoch,
+                               hipStream_t s) {
+  if (!b.fused || !e) return;
   epoch += 2;
   const unsigned zero = 0;
   check(hipMemcpyAsync(b.epoch.ptr, &epoch, 4, hipMemcpyHostToDevice, s), "H2D epoch");
@@ -2585,11 +2603,20 @@ void run_batch(fah_batcher* b, const std::vector<BatchRequest*>& reqs) {
       if (batch->graph) check(hipGraphLaunch(batch->graph, s), "hipGraphLaunch");
       else enqueue_sessions_step(sessions[0], *batch, s);
       check(fah::launch_session_batch_io(table, count, batch->tokens.as<int>(), s), "gather tokens");
-      check(hipMemcpyAsync(tokens.data(), batch->tokens.ptr, (size_t)count * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
+      if (!batch->readback)
+        check(hipHostMalloc(reinterpret_cast<void**>(&batch->readback), (fah::kFewFrames + 2) * 4, hipHostMallocDefault),
+              "hipHostMalloc read-back");
+      int32_t* rb = batch->readback;
+      check(hipMemcpyAsync(rb, batch->tokens.ptr, (size_t)count * 4, hipMemcpyDeviceToHost, s), "D2H tokens");
       if (fused) {
-        check(hipStreamSynchronize(s), "hipStreamSynchronize");
-        recover_session_step(*batch, sessions.data(), count, s);
+        check(hipMemcpyAsync(rb + fah::kFewFrames, batch->error.ptr, 4, hipMemcpyDeviceToHost, s), "D2H error word");
+        check(hipMemcpyAsync(rb + fah::kFewFrames + 1, batch->epoch.ptr, 4, hipMemcpyDeviceToHost, s), "D2H epoch");
       }
+      check(hipStreamSynchronize(s), "hipStreamSynchronize");
+      std::copy(rb, rb + count, tokens.begin());
+      if (fused)
+        recover_session_step_read(*batch, sessions.data(), count, (unsigned)rb[fah::kFewFrames],
+                                  (unsigned)rb[fah::kFewFrames + 1], s);
     }
     check(hipStreamSynchronize(s), "hipStreamSynchronize");
     for (fah_decoder* d : sessions) d->host_position += 1;
@@ -2624,6 +2651,7 @@ int fah_batcher_step(fah_batcher* b, fah_decoder* session, int32_t* token) {
   for (BatchRequest* r : b->pending)
     if (r->session == session) return fail(FAH_ERROR_STATE, "the session already has a step pending");
   b->pending.push_back(&req);
+  b->arrivals.fetch_add(1, std::memory_order_release);
   b->idle.erase(std::remove(b->idle.begin(), b->idle.end(), session), b->idle.end());
   b->cv.notify_all();
   while (!req.done) {
@@ -2645,6 +2673,17 @@ int fah_batcher_step(fah_batcher* b, fah_decoder* session, int32_t* token) {
         return b->pending.size() >= (size_t)fah::kFewFrames || (expected > 0 && joined_pending >= expected);
       };
       while (!want()) {
+        // Spin a little for the next arrival before blocking (arrivals come
+        // microseconds apart when every session is stepping).
+        const int64_t seen = b->arrivals.load(std::memory_order_acquire);
+        lk.unlock();
+        const auto spin_until = std::min(deadline, std::chrono::steady_clock::now() + std::chrono::microseconds(500));
+        while (b->arrivals.load(std::memory_order_acquire) == seen && std::chrono::steady_clock::now() < spin_until)
+          std::this_thread::yield();
+        lk.lock();
+        if (want()) break;
+        if (b->arrivals.load(std::memory_order_acquire) != seen) continue;
+        if (std::chrono::steady_clock::now() >= deadline) break;
         if (b->cv.wait_until(lk, deadline) == std::cv_status::timeout) break;
       }
       const size_t n = std::min<size_t>(fah::kFewFrames, b->pending.size());
@@ -2660,18 +2699,27 @@ int fah_batcher_step(fah_batcher* b, fah_decoder* session, int32_t* token) {
       run_batch(b, batch);
       lk.lock();
       int64_t served = 0;
-      for (BatchRequest* r : batch) {
-        r->done = true;
-        served += r->status == FAH_OK;
-      }
+      for (BatchRequest* r : batch) served += r->status == FAH_OK;
       b->batches_run += served > 0;
       b->rows_run += served;
+      for (BatchRequest* r : batch) r->done.store(true, std::memory_order_release);  // (last access)
       b->running = false;
       b->cv.notify_all();
       continue;
     }
-    b->cv.wait(lk);
+    // Another thread leads: spin a little (a batch ends within a step's
+    // time; 16 blocked waiters would otherwise wake one after another
+    // through the lock), then block.
+    lk.unlock();
+    const auto spin_until = std::chrono::steady_clock::now() + std::chrono::milliseconds(3);
+    while (!req.done.load(std::memory_order_acquire) && b->running.load(std::memory_order_acquire) &&
+           std::chrono::steady_clock::now() < spin_until)
+      std::this_thread::yield();
+    if (req.done.load(std::memory_order_acquire)) break;
+    lk.lock();
+    if (!req.done.load(std::memory_order_acquire) && b->running) b->cv.wait(lk);
   }
+  if (lk.owns_lock()) lk.unlock();
   if (req.status != FAH_OK) return fail(req.status, req.error);
   *token = req.token;
   return FAH_OK;
