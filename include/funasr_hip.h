@@ -379,8 +379,10 @@ int fah_batcher_join(fah_batcher* batcher, fah_decoder* session);
 int fah_batcher_leave(fah_batcher* batcher, fah_decoder* session);
 /* One greedy step of `session` (Greedy -> Embed -> Decode(1), as
  * fah_decoder_generate(session, 1, token)), batched with the steps other
- * threads request at the same time; blocks until it has run. The session
- * must hold logits from its last decode. */
+ * threads request at the same time; blocks until it has run (a waiting
+ * thread yields in a loop for up to 3 ms, then sleeps; the collecting thread
+ * yields for up to 0.5 ms between arrivals). The session must hold logits
+ * from its last decode. */
 int fah_batcher_step(fah_batcher* batcher, fah_decoder* session, int32_t* token);
 /* Batches run and session steps served (successful steps) so far. */
 int fah_batcher_stats(fah_batcher* batcher, int64_t* batches, int64_t* rows);
