@@ -73,6 +73,9 @@ static_assert(kTagOff % 16 == 0 && kPartOff % 16 == 0, "16-byte LDS destinations
 // A load through a global-address-space pointer: unlike a generic (flat)
 // load it cannot alias LDS, so it need not wait for the direct-to-LDS loads
 // in flight.
+// A store through a global-address-space pointer: a generic (flat) store
+// might write LDS, so a workgroup barrier after it would wait for it.
+__device__ __forceinline__ void gstore(_Float16* p, _Float16 v) { *(__attribute__((address_space(1))) _Float16*)p = v; }
 __device__ __forceinline__ float gload(const float* p) { return *(const __attribute__((address_space(1))) float*)p; }
 __device__ __forceinline__ uint4 gload(const uint4* p) {
   typedef unsigned int v4 __attribute__((ext_vector_type(4)));
@@ -701,7 +704,7 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
         } else {
           const _Float16 k16 = to_half(r);
           kcur_s[c] = k16;
-          if (uh % G == 0) const_cast<_Float16*>(kc)[(size_t)pos * HS + c] = k16;
+          if (uh % G == 0) gstore(const_cast<_Float16*>(kc) + (size_t)pos * HS + c, k16);
         }
       }
       lds_barrier();
@@ -808,7 +811,7 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
             const int c = lane + 64 * k;
             const _Float16 v16 = to_half(u2f((uint32_t)qkv_tag[256 + c]));
             vcur_s[c] = v16;
-            if (uh % G == 0) const_cast<_Float16*>(vc)[(size_t)pos * HS + c] = v16;
+            if (uh % G == 0) gstore(const_cast<_Float16*>(vc) + (size_t)pos * HS + c, v16);
           }
         }
       }
