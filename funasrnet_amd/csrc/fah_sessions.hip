@@ -716,7 +716,15 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) k0[i] = reinterpret_cast<const uint4*>(kcur_s)[i];
       }
-      if (tid < n) p_s[tid] = score_regs(k0, q_s, a.divisor);
+      // Each thread also takes the maximum of its own scores (the softmax's
+      // first step, SoftmaxAvx.cs:11-58, order-free), so that one barrier
+      // serves both.
+      float m = -__builtin_inff();
+      if (tid < n) {
+        const float sc = score_regs(k0, q_s, a.divisor);
+        p_s[tid] = sc;
+        m = sc;
+      }
       for (int s = tid + kST; s < n; s += kST) {
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
         if (s < nv) {
@@ -733,16 +741,16 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) score8(acc, reinterpret_cast<const uint4*>(kcur_s)[i], q_s + 8 * i);
         }
-        const float sc = fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7])));
-        p_s[s] = fdiv(sc, a.divisor);
+        const float sc = fdiv(fadd(fadd(fadd(acc[0], acc[4]), fadd(acc[1], acc[5])), fadd(fadd(acc[2], acc[6]), fadd(acc[3], acc[7]))),
+                              a.divisor);
+        p_s[s] = sc;
+        m = nan_max_p(m, sc);
       }
-      lds_barrier();
       // Exact softmax (SoftmaxAvx.cs:11-58): the maximum, the numerators, the
       // double denominator -- as wave trees when every numerator is 0 or in
       // [2^-17, 1] (then every partial sum is exact), the reference's
-      // residue chains otherwise.
-      float m = -__builtin_inff();
-      for (int s = tid; s < n; s += kST) m = nan_max_p(m, p_s[s]);
+      // residue chains otherwise. (A thread's numerators come from its own
+      // scores; the value sums read all of them after a later barrier.)
       m = wave_max_nan(m);
       if (lane == 0) tmax_s[wave] = m;
       lds_barrier();
