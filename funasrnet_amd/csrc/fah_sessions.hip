@@ -581,11 +581,14 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   // o/down share: rows R2 (w / kOGroups) .. of sessions f0 .. f0 + Sg - 1
   // (group w % kOGroups). Their residual: lane t < R2 Sg holds (row
   // R2 (w / kOGroups) + t / Sg, session f0 + t % Sg).
-  const int f0 = kOSessions * (w % kOGroups), Sg = max(0, min(kOSessions, S - f0)), orow0 = R2 * (w / kOGroups);
+  // A batch below 16 sessions is split evenly over the groups (ceil(S /
+  // groups) sessions a group), so that every group has work.
+  const int on = (S + kOGroups - 1) / kOGroups, qn = (S + kQGroups - 1) / kQGroups, gn = (S + kGuGroups - 1) / kGuGroups;
+  const int f0 = on * (w % kOGroups), Sg = max(0, min(on, S - f0)), orow0 = R2 * (w / kOGroups);
   // q/k/v share: rows qrow0 .. of sessions qf0 .. qf0 + Sq - 1; gate/up
   // share: pairs gp0 .. of sessions gf0 .. gf0 + Sgu - 1.
-  const int qf0 = kQSessions * (w % kQGroups), Sq = max(0, min(kQSessions, S - qf0)), qrow0 = R1 * (w / kQGroups);
-  const int gf0 = kGuSessions * (w % kGuGroups), Sgu = max(0, min(kGuSessions, S - gf0)), gp0 = kGuPairs * (w / kGuGroups);
+  const int qf0 = qn * (w % kQGroups), Sq = max(0, min(qn, S - qf0)), qrow0 = R1 * (w / kQGroups);
+  const int gf0 = gn * (w % kGuGroups), Sgu = max(0, min(gn, S - gf0)), gp0 = kGuPairs * (w / kGuGroups);
   float xres = 0.0f, ares = 0.0f;
   const int ri = tid / max(Sg, 1), rf = f0 + tid - ri * max(Sg, 1), rrow = orow0 + ri;
   const bool rlane = tid < R2 * Sg;
