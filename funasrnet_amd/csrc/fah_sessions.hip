@@ -66,9 +66,8 @@ constexpr int kMaxOff = kChainOff + 64;             // floats [4]
 constexpr int kExactOff = kMaxOff + 16;             // ints [4]
 constexpr int kInvOff = kExactOff + 16;             // float
 constexpr int kOkOff = kInvOff + 16;                // ints [4]
-constexpr int kPartOff = kOkOff + 16;               // partner maxima words [16]
-static_assert(kPartOff + 128 <= 8 * 1024, "small area");
-static_assert(kTagOff % 16 == 0 && kPartOff % 16 == 0, "16-byte LDS destinations");
+static_assert(kOkOff + 16 <= 8 * 1024, "small area");
+static_assert(kTagOff % 16 == 0, "16-byte LDS destinations");
 
 // A load through a global-address-space pointer: unlike a generic (flat)
 // load it cannot alias LDS, so it need not wait for the direct-to-LDS loads
@@ -551,7 +550,6 @@ __global__ __launch_bounds__(kST) void session_step_kernel(SessionStepArgs a) {
   int* exact_s = reinterpret_cast<int*>(small + kExactOff);
   float* inv_s = reinterpret_cast<float*>(small + kInvOff);
   int* ok_s = reinterpret_cast<int*>(small + kOkOff);
-  u64* part_s = reinterpret_cast<u64*>(small + kPartOff);
 
   // Roles. The norm rows of session s on workgroup 192 + s + 16 (s % 4):
   // past the gate/up workgroups (their ffn norm does not delay a gate/up
