@@ -786,8 +786,8 @@ def main() -> int:
     baseline = None
     if not args.no_cpu:
         # The reference's default of 4 threads (FunAsr.cs:94), then every core
-        # this process may use (at most the physical cores; 16 on a GPU box's
-        # share of its host).
+        # this process may use (at most the physical cores, and at most 16:
+        # a single-GPU host's share of its cores).
         cpu = host_cpu()
         every = min(cpu["available_cpus"], cpu["physical_cores"] or cpu["available_cpus"], 16)
         runs = {}
